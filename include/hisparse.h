@@ -1,0 +1,230 @@
+/*
+ * hisparse.h -- C ABI of the gfx950 kernels behind mini-hisparse's per-step
+ * sparse decode path (libhisparse_hip.so).
+ *
+ * The reference (mini-hisparse 0.2.0) has no native code and no FFI: its
+ * swappable points are Python functions.  Each entry point below replaces one
+ * of them; the comment names the reference function (file:line under the
+ * reference checkout) whose semantics it implements.
+ *
+ * Conventions
+ *  - All pointers are device pointers unless stated otherwise; all buffers are
+ *    caller-owned; nothing is allocated persistently by the library.
+ *  - Scratch memory is a caller-provided workspace sized by the matching
+ *    hs_*_workspace_bytes query.
+ *  - `stream` is a hipStream_t (NULL = the default stream).  Every call only
+ *    enqueues work; none synchronises the host.
+ *  - Return value: HS_OK (0) or a negative status; hs_last_error() gives the
+ *    message of the calling thread's last failure.
+ *  - Device-side invalid indices (-1, out of range) are masked, not errors,
+ *    as in the reference (row_index.py:67-68, row_index.py:103).
+ */
+#ifndef HISPARSE_H
+#define HISPARSE_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define HS_VERSION 1
+
+#define HS_OK 0
+#define HS_EINVAL (-1)
+#define HS_ELAUNCH (-2)
+#define HS_EWORKSPACE (-3)
+#define HS_ERUNTIME (-4)
+
+/* KV / query element types (CacheConfig.dtype, config.py:19, :27-28) */
+#define HS_DTYPE_F32 0
+#define HS_DTYPE_F16 1
+#define HS_DTYPE_BF16 2
+
+typedef struct ihipStream_t* hs_stream_t;
+
+/* Message of the calling thread's last failed call ("" if none). */
+const char* hs_last_error(void);
+
+/* HS_VERSION of the loaded library. */
+int hs_version(void);
+
+/* LDS bytes available to one workgroup on `device` (diagnostic). */
+int hs_device_lds_bytes(int device, int64_t* bytes);
+
+/*
+ * Device alias of a pinned host allocation owned by the caller (never
+ * registered or unregistered here).
+ * Replaces: MappedHost (mini_hisparse/row_kernels.py:10-32), called from
+ * HybridKVCache.__init__ (hybrid.py:129-132).  `host_ptr` is a host pointer.
+ */
+int hs_host_alias(const void* host_ptr, void** device_ptr);
+
+/* ---------------------------------------------------------------- (1) Quest */
+
+/* Bytes of scratch hs_quest_topk needs for `batch` requests of up to `max_pages`. */
+int64_t hs_quest_workspace_bytes(int64_t batch, int64_t heads, int64_t max_pages);
+
+/*
+ * Quest page scores and per-head top-k for `batch` (<= 16) requests.
+ * Replaces: quest_selection (mini_hisparse/selection.py:80-101) up to the
+ * chosen page ids (:100).
+ *   query      [batch, heads, head_dim] float32 (exact copy of the model-dtype
+ *              query; query_is_16bit = 1 when that dtype is bf16/fp16)
+ *   minimum[b], maximum[b]  per request [pages, kv_heads, head_dim] bounds in
+ *              kv_dtype (RequestPages.minimum/maximum[layer], storage.py:193-206)
+ *   page_counts host array [batch]: ceil(length / page_size)
+ *   out_pages  [batch, heads, top] int32: the min(top, count) chosen pages of
+ *              each head, ascending; all pages when top >= count (:90-91);
+ *              the tail page and, if keep_sink && top > 1 && count > 1, page 0
+ *              are always chosen (:96-99).  Scores are float32 sums over the
+ *              channels in ascending order; ties go to the lower page.
+ * `minimum`, `maximum` and `page_counts` are host arrays of device pointers / sizes.
+ */
+int hs_quest_topk(const float* query, int64_t q_stride_b, int64_t q_stride_h,
+                  int32_t query_is_16bit, const void* const* minimum, const void* const* maximum,
+                  int32_t kv_dtype, const int64_t* page_counts, int64_t batch, int64_t heads,
+                  int64_t kv_heads, int64_t head_dim, int64_t top, int32_t keep_sink,
+                  int32_t* out_pages, int64_t out_stride_b, void* workspace,
+                  int64_t workspace_bytes, hs_stream_t stream);
+
+/*
+ * Device-side Selection -> LogicalTopK adapter for page selections.
+ * Replaces: Selection.from_pages (selection.py:43-60) followed by
+ * LogicalTopK.from_selection (row_index.py:20-31), without the host sync of
+ * selection.py:100.
+ *   pages         [batch, heads, top] from hs_quest_topk; lengths host [batch]
+ *   positions     [batch, pos_capacity] int32: ascending union of the
+ *                 selected tokens, then -1
+ *   head_columns  [batch, heads, width] int64: union column of each head's
+ *                 tokens in ascending token order, then -1
+ *   union_count   [batch] int32: union size n
+ *   entry_*       per (request, kv head) the deduplicated union columns read
+ *                 by any query head of the group, ascending, with the bit mask
+ *                 of those heads: [batch, kv_heads, entry_capacity], counts
+ *                 [batch, kv_heads]
+ *   status        int32 flag OR-ed with 1 (union over capacity) / 2 (entries
+ *                 over capacity); the caller clears it.
+ */
+int hs_build_union(const int32_t* pages, int64_t p_stride_b, int64_t top, const int64_t* lengths,
+                   int64_t page_size, int64_t batch, int64_t heads, int64_t kv_heads,
+                   int32_t* positions, int64_t pos_capacity, int64_t* head_columns, int64_t width,
+                   int32_t* union_count, int32_t* entry_columns, uint32_t* entry_masks,
+                   int64_t entry_capacity, int32_t* entry_counts, int32_t* status,
+                   hs_stream_t stream);
+
+/* ------------------------------------------------------------- (2) resolver */
+
+/*
+ * One (request, layer) resolve: the tables of LayerTables (hybrid.py:45-64)
+ * and the outputs of RowPlan (row_index.py:51-56).
+ */
+typedef struct hs_resolve_desc {
+  const void* positions;        /* [n] logical tokens, int32 or int64 */
+  int64_t n;
+  int32_t positions_i64;        /* 1 = int64 positions, 0 = int32 */
+  int32_t reserved0;
+  const int64_t* head_columns;  /* nullable [heads, width] union columns, -1 padded */
+  int64_t heads, width, hc_stride_h, hc_stride_w;
+  const int32_t* source;        /* [n_pages] host page of each logical page, -1 = none */
+  const int32_t* resident;      /* [n_pages] device block of a resident page, -1 = none */
+  int64_t n_pages;
+  const int32_t* hot;           /* [hot_blocks] device block of each hot block */
+  int64_t hot_blocks;
+  int32_t* tags;                /* [hot_rows] in/out: host row held by each hot slot, -1 = empty */
+  int64_t* lru;                 /* [hot_rows] in/out: slots, least recent first */
+  int64_t hot_rows;             /* <= 32768 (hybrid.py:34) */
+  int64_t length, page_size;    /* length <= n_pages * page_size */
+  int64_t* physical;            /* out [n], or [heads, width] contiguous when head_columns */
+  int64_t* union_physical;      /* out, nullable: [n] physical rows in input order */
+  int64_t* miss_host_rows;      /* out [n]: host rows to load, compact prefix, then -1 */
+  int64_t* miss_device_rows;    /* out [n]: matching device rows */
+  int64_t* counts;              /* out [3]: resident hits, hot hits, misses */
+  int64_t* row_stats;           /* nullable [3]: counts are added here (hybrid.py:454) */
+  void* workspace;              /* set by the library from the call's workspace */
+} hs_resolve_desc;
+
+/* Scratch bytes for one descriptor (sum them for a batch). */
+int64_t hs_resolve_workspace_bytes(int64_t n, int64_t length, int64_t n_pages, int64_t hot_rows);
+
+/*
+ * Resolve logical tokens to physical rows, mutating tags/lru in place.
+ * Replaces: resolve_rows (mini_hisparse/row_index.py:59-137); bit-exact on
+ * every output including the updated tags and LRU.  `desc` is a host pointer.
+ */
+int hs_resolve_rows(const hs_resolve_desc* desc, void* workspace, int64_t workspace_bytes,
+                    hs_stream_t stream);
+
+/* The same over `count` independent (request, layer) descriptors (host array). */
+int hs_resolve_rows_batched(const hs_resolve_desc* descs, int32_t count, void* workspace,
+                            int64_t workspace_bytes, hs_stream_t stream);
+
+/* --------------------------------------------------------------- (3) gather */
+
+/*
+ * Copy the K and V planes of each planned host row into its hot device row.
+ * Replaces: gather_rows (mini_hisparse/row_kernels.py:35-70) and the CPU loop
+ * of HybridKVCache.resolve (hybrid.py:466-472).
+ *   host_alias  device alias of the pinned host pool [host_pages, 2, P, Hkv, D]
+ *   pool        device pool [gpu_pages, 2, P, Hkv, D]
+ *   miss_*_rows [n] int64 plan from the resolver; entries < 0 are skipped
+ *   miss_count  nullable device int64: only the first *miss_count entries are read
+ *   row_bytes   Hkv * D * element size
+ */
+int hs_gather_rows(const void* host_alias, void* pool, const int64_t* miss_host_rows,
+                   const int64_t* miss_device_rows, int64_t n, const int64_t* miss_count,
+                   int64_t page_size, int64_t row_bytes, hs_stream_t stream);
+
+/* The same for `batch` (<= 16) plans in one launch; every array argument is a
+ * host array of per-request values; grid_x <= 0 picks the default grid. */
+int hs_gather_rows_batched(const void* const* host_alias, void* pool,
+                           const int64_t* const* miss_host_rows,
+                           const int64_t* const* miss_device_rows,
+                           const int64_t* const* miss_counts, const int64_t* n, int32_t batch,
+                           int64_t page_size, int64_t row_bytes, int32_t grid_x,
+                           hs_stream_t stream);
+
+/* ------------------------------------------------------------ (4) attention */
+
+/* Scratch bytes of one attention call (split-K partials). */
+int64_t hs_attend_workspace_bytes(int32_t dtype, int64_t batch, int64_t heads, int64_t kv_heads,
+                                  int64_t head_dim, int64_t max_entries);
+
+/*
+ * Physical-row GQA decode attention over per-head row lists.
+ * Replaces: attend_rows (mini_hisparse/row_kernels.py:73-135) and the torch
+ * branch of row_attention (attention.py:26-35).
+ *   query [batch, heads, head_dim] (strides in elements, head_dim contiguous)
+ *   rows  [batch, heads, width] int64 physical rows, -1 masked; r_stride_h == 0
+ *         means one list shared by every head (attention.py:19-21)
+ *   pool_rows  blocks * page_size of the pool; rows >= pool_rows are masked
+ *   out   [batch, heads, head_dim] in the pool dtype; 0 for a head with no row
+ *   max_entries for the workspace query: width (shared) or width * heads / kv_heads
+ */
+int hs_attend_rows(const void* query, int64_t q_stride_b, int64_t q_stride_h, const void* pool,
+                   int32_t dtype, int64_t page_size, int64_t kv_heads, int64_t head_dim,
+                   int64_t pool_rows, const int64_t* rows, int64_t r_stride_b, int64_t r_stride_h,
+                   int64_t r_stride_w, int64_t width, int64_t batch, int64_t heads, void* out,
+                   int64_t o_stride_b, int64_t o_stride_h, void* workspace,
+                   int64_t workspace_bytes, hs_stream_t stream);
+
+/*
+ * The same attention reading each KV head's deduplicated row set once: the
+ * entry lists of hs_build_union, with physical rows taken from the
+ * resolver's union_physical [batch, n].  Same result as hs_attend_rows over
+ * the per-head rows physical[h, j] = union_physical[head_columns[h, j]].
+ */
+int hs_attend_groups(const void* query, int64_t q_stride_b, int64_t q_stride_h, const void* pool,
+                     int32_t dtype, int64_t page_size, int64_t kv_heads, int64_t head_dim,
+                     int64_t pool_rows, const int64_t* union_physical, int64_t u_stride_b,
+                     const int32_t* entry_columns, const uint32_t* entry_masks,
+                     int64_t e_stride_b, int64_t e_stride_k, const int32_t* entry_counts,
+                     int64_t max_entries, int64_t batch, int64_t heads, void* out,
+                     int64_t o_stride_b, int64_t o_stride_h, void* workspace,
+                     int64_t workspace_bytes, hs_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* HISPARSE_H */

@@ -1,0 +1,147 @@
+"""ctypes binding of libhisparse_hip.so (declared in include/hisparse.h).
+
+The library is built in-tree by ``python -m mini_hisparse_amd.build``.  There is
+no fallback: when the library is missing every kernel call raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from ctypes import POINTER, c_char_p, c_int, c_int32, c_int64, c_void_p
+from pathlib import Path
+
+LIBRARY_PATH = Path(__file__).resolve().parent / "libhisparse_hip.so"
+
+HS_DTYPE_F32, HS_DTYPE_F16, HS_DTYPE_BF16 = 0, 1, 2
+
+
+class HipLibraryError(RuntimeError):
+    """A libhisparse_hip call failed (the message comes from hs_last_error)."""
+
+
+class ResolveDesc(ctypes.Structure):
+    """``hs_resolve_desc`` of include/hisparse.h."""
+
+    _fields_ = [
+        ("positions", c_void_p),
+        ("n", c_int64),
+        ("positions_i64", c_int32),
+        ("reserved0", c_int32),
+        ("head_columns", c_void_p),
+        ("heads", c_int64),
+        ("width", c_int64),
+        ("hc_stride_h", c_int64),
+        ("hc_stride_w", c_int64),
+        ("source", c_void_p),
+        ("resident", c_void_p),
+        ("n_pages", c_int64),
+        ("hot", c_void_p),
+        ("hot_blocks", c_int64),
+        ("tags", c_void_p),
+        ("lru", c_void_p),
+        ("hot_rows", c_int64),
+        ("length", c_int64),
+        ("page_size", c_int64),
+        ("physical", c_void_p),
+        ("union_physical", c_void_p),
+        ("miss_host_rows", c_void_p),
+        ("miss_device_rows", c_void_p),
+        ("counts", c_void_p),
+        ("row_stats", c_void_p),
+        ("workspace", c_void_p),
+    ]
+
+
+# name -> (restype, argtypes); every symbol of include/hisparse.h
+SIGNATURES = {
+    "hs_last_error": (c_char_p, []),
+    "hs_version": (c_int, []),
+    "hs_device_lds_bytes": (c_int, [c_int, POINTER(c_int64)]),
+    "hs_host_alias": (c_int, [c_void_p, POINTER(c_void_p)]),
+    "hs_quest_workspace_bytes": (c_int64, [c_int64, c_int64, c_int64]),
+    "hs_quest_topk": (
+        c_int,
+        [c_void_p, c_int64, c_int64, c_int32, POINTER(c_void_p), POINTER(c_void_p), c_int32,
+         POINTER(c_int64), c_int64, c_int64, c_int64, c_int64, c_int64, c_int32,
+         c_void_p, c_int64, c_void_p, c_int64, c_void_p],
+    ),
+    "hs_build_union": (
+        c_int,
+        [c_void_p, c_int64, c_int64, POINTER(c_int64), c_int64, c_int64, c_int64, c_int64,
+         c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_void_p, c_void_p, c_int64,
+         c_void_p, c_void_p, c_void_p],
+    ),
+    "hs_resolve_workspace_bytes": (c_int64, [c_int64, c_int64, c_int64, c_int64]),
+    "hs_resolve_rows": (c_int, [POINTER(ResolveDesc), c_void_p, c_int64, c_void_p]),
+    "hs_resolve_rows_batched": (c_int, [POINTER(ResolveDesc), c_int32, c_void_p, c_int64, c_void_p]),
+    "hs_gather_rows": (
+        c_int,
+        [c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_void_p, c_int64, c_int64, c_void_p],
+    ),
+    "hs_gather_rows_batched": (
+        c_int,
+        [POINTER(c_void_p), c_void_p, POINTER(c_void_p), POINTER(c_void_p), POINTER(c_void_p),
+         POINTER(c_int64), c_int32, c_int64, c_int64, c_int32, c_void_p],
+    ),
+    "hs_attend_workspace_bytes": (c_int64, [c_int32, c_int64, c_int64, c_int64, c_int64, c_int64]),
+    "hs_attend_rows": (
+        c_int,
+        [c_void_p, c_int64, c_int64, c_void_p, c_int32, c_int64, c_int64, c_int64, c_int64,
+         c_void_p, c_int64, c_int64, c_int64, c_int64, c_int64, c_int64,
+         c_void_p, c_int64, c_int64, c_void_p, c_int64, c_void_p],
+    ),
+    "hs_attend_groups": (
+        c_int,
+        [c_void_p, c_int64, c_int64, c_void_p, c_int32, c_int64, c_int64, c_int64, c_int64,
+         c_void_p, c_int64, c_void_p, c_void_p, c_int64, c_int64, c_void_p, c_int64,
+         c_int64, c_int64, c_void_p, c_int64, c_int64, c_void_p, c_int64, c_void_p],
+    ),
+}
+
+_LIB = None
+
+
+def load(path: Path | str | None = None):
+    """Load (once) and return the library; raises if it is absent."""
+    global _LIB
+    if _LIB is not None and path is None:
+        return _LIB
+    target = Path(path) if path is not None else LIBRARY_PATH
+    if not target.exists():
+        raise HipLibraryError(
+            f"{target} is missing: build it with `python -m mini_hisparse_amd.build` "
+            "(the HIP kernels have no fallback)"
+        )
+    lib = ctypes.CDLL(str(target))
+    for name, (restype, argtypes) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = restype
+        fn.argtypes = argtypes
+    if path is None:
+        _LIB = lib
+    return lib
+
+
+def check(status: int, what: str):
+    if status != 0:
+        message = load().hs_last_error().decode(errors="replace")
+        raise HipLibraryError(f"{what} failed ({status}): {message}")
+
+
+def dtype_code(dtype) -> int:
+    import torch
+
+    codes = {torch.float32: HS_DTYPE_F32, torch.float16: HS_DTYPE_F16, torch.bfloat16: HS_DTYPE_BF16}
+    if dtype not in codes:
+        raise ValueError("KV dtype must be float32, float16 or bfloat16")
+    return codes[dtype]
+
+
+def ptr(tensor) -> int:
+    return 0 if tensor is None else tensor.data_ptr()
+
+
+def stream_handle(device=None) -> int:
+    import torch
+
+    return torch.cuda.current_stream(device).cuda_stream

@@ -1,0 +1,601 @@
+// Physical-row paged GQA decode attention for gfx950.
+//
+// Replaces the Triton `_attend` / `attend_rows` of mini_hisparse
+// (row_kernels.py:73-135) and the torch branch of `row_attention`
+// (attention.py:26-35).  Per query head h with KV head h // g, the kernel
+// computes softmax((K_j . q) * D^-0.5) over the rows j it selects and the
+// weighted sum of V_j, accumulating in fp32; rows < 0 are masked and a head
+// with no valid row returns 0.
+//
+// Work is organised per (request, KV head): an "entry" is one physical row
+// together with the bit mask of the query heads of the group that read it.
+// Each row is therefore read from HBM once per KV head however many heads
+// selected it.  Entries come from one of three sources:
+//   ROWS   : per-head row lists [H, W] (no cross-head deduplication),
+//   SHARED : one row list read by every head of the group,
+//   GROUPS : per-KV-head deduplicated union columns + head masks, with the
+//            physical row of a column taken from the resolver's output.
+//
+// bf16 / fp16 pools use MFMA (v_mfma_f32_16x16x32_{bf16,f16}): S^T = K Q^T
+// with the group's query heads as the N dimension (padded to 16), then
+// O^T += V^T P^T with V staged through LDS.  fp32 pools (and head dims not a
+// multiple of 8) use a VALU kernel with the same entry sources.  Both write
+// split-K partials (m, l, acc) that `attend_merge_kernel` combines.
+#include <float.h>
+#include <math.h>
+
+#include "hs_common.h"
+
+namespace hs {
+
+enum { MODE_ROWS = 0, MODE_SHARED = 1, MODE_GROUPS = 2 };
+
+struct AttendArgs {
+  const void* q;
+  int64_t q_sb, q_sh;
+  const void* pool;
+  int64_t P, Hkv, D;
+  int64_t pool_rows;  // rows >= pool_rows are masked like rows < 0
+  const int64_t* rows;
+  int64_t r_sb, r_sh, r_sw, width;
+  const int64_t* uphys;
+  int64_t u_sb;
+  const int32_t* ecol;
+  const uint32_t* emask;
+  int64_t e_sb, e_sk;
+  const int32_t* ecount;
+  int64_t emax;
+  int mode;
+  int head_chunks;
+  int64_t B, Hq, g;
+  int64_t splits, chunk;
+  float scale;
+  float* part_m;  // [B, Hq, splits]
+  float* part_l;  // [B, Hq, splits]
+  float* part_o;  // [B, Hq, splits, D]
+};
+
+__device__ __forceinline__ int64_t entry_count(const AttendArgs& a, int64_t b, int64_t k) {
+  if (a.mode == MODE_ROWS) return a.g * a.width;
+  if (a.mode == MODE_SHARED) return a.width;
+  int64_t e = a.ecount[b * a.Hkv + k];
+  return e < 0 ? 0 : (e > a.emax ? a.emax : e);
+}
+
+__device__ __forceinline__ void entry_at(const AttendArgs& a, int64_t b, int64_t k, int64_t e,
+                                         int64_t& phys, uint32_t& mask) {
+  if (a.mode == MODE_ROWS) {
+    const int64_t hl = e / a.width, j = e - hl * a.width;
+    phys = a.rows[b * a.r_sb + (k * a.g + hl) * a.r_sh + j * a.r_sw];
+    mask = 1u << hl;
+  } else if (a.mode == MODE_SHARED) {
+    phys = a.rows[b * a.r_sb + e * a.r_sw];
+    mask = a.g >= 32 ? 0xffffffffu : ((1u << a.g) - 1u);
+  } else {
+    const int64_t off = b * a.e_sb + k * a.e_sk + e;
+    const int32_t col = a.ecol[off];
+    mask = a.emask[off];
+    phys = col >= 0 ? a.uphys[b * a.u_sb + col] : -1;
+  }
+  if (phys < 0 || phys >= a.pool_rows) {
+    phys = -1;
+    mask = 0;
+  }
+}
+
+// Element offset of K(row, kv) in a [blocks, 2, P, Hkv, D] pool; V is + P*Hkv*D.
+__device__ __forceinline__ int64_t k_offset(int64_t row, int64_t kv, int64_t P, int64_t Hkv, int64_t D) {
+  const uint32_t r = static_cast<uint32_t>(row);
+  const uint32_t blk = r / static_cast<uint32_t>(P);
+  const uint32_t off = r - blk * static_cast<uint32_t>(P);
+  return ((static_cast<int64_t>(blk) * 2 * P + off) * Hkv + kv) * D;
+}
+
+__device__ __forceinline__ u32x4 load16(const void* p) {
+  return *reinterpret_cast<const u32x4*>(p);
+}
+
+template <int DT>
+__device__ __forceinline__ f32x4 mfma16x16x32(u32x4 a, u32x4 b, f32x4 c) {
+  if constexpr (DT == HS_DTYPE_BF16) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  } else {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+}
+
+template <int DT>
+__device__ __forceinline__ unsigned short to_bits(float v) {
+  if constexpr (DT == HS_DTYPE_BF16) return f32_to_bf16_bits(v);
+  else return f32_to_f16_bits(v);
+}
+template <int DT>
+__device__ __forceinline__ float from_bits(unsigned short v) {
+  if constexpr (DT == HS_DTYPE_BF16) return bf16_bits_to_f32(v);
+  else return f16_bits_to_f32(v);
+}
+
+// One workgroup (4 waves) per (split, KV head x head chunk, request).
+template <int DT, int DP>
+__global__ __launch_bounds__(256) void attend_mfma_kernel(AttendArgs a) {
+  constexpr int NT = DP / 16;   // PV M-tiles over d
+  constexpr int KK = DP / 32;   // QK k-steps over d
+  constexpr int RS = DP + 8;    // LDS row stride of the V tile (elements)
+  constexpr int LPR = DP / 8;   // lanes per row for 16-byte V loads
+  constexpr int RPI = 64 / LPR; // rows per V load instruction
+  constexpr int VI = 32 / RPI;  // V load instructions per 32-row tile
+  constexpr int VS_BYTES = 4 * 32 * RS * 2;
+  constexpr int MERGE_BYTES = 4 * 16 * DP * 4;
+  constexpr int SMEM = VS_BYTES > MERGE_BYTES ? VS_BYTES : MERGE_BYTES;
+  __shared__ __attribute__((aligned(16))) unsigned char smem[SMEM];
+  __shared__ int64_t s_phys[4][32];
+  __shared__ uint32_t s_mask[4][32];
+  __shared__ float s_m[4][16], s_l[4][16];
+
+  unsigned short* vs_all = reinterpret_cast<unsigned short*>(smem);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int j = lane >> 4, c = lane & 15;
+  const int64_t split = blockIdx.x;
+  const int64_t k = blockIdx.y / a.head_chunks;
+  const int hchunk = blockIdx.y % a.head_chunks;
+  const int64_t b = blockIdx.z;
+  const int hh = 16 * hchunk + c;  // head index within the group owned by this lane
+  const int64_t D = a.D, P = a.P, Hkv = a.Hkv;
+  const unsigned short* pool = static_cast<const unsigned short*>(a.pool);
+  unsigned short* vs = vs_all + wave * 32 * RS;
+
+  // Q^T fragments: lane holds Q[head hh][d = 32kk + 8j .. +8]
+  u32x4 qf[KK];
+#pragma unroll
+  for (int kk = 0; kk < KK; ++kk) {
+    const int d0 = 32 * kk + 8 * j;
+    u32x4 v = {0u, 0u, 0u, 0u};
+    if (hh < a.g && d0 < D) {
+      const unsigned short* qp = static_cast<const unsigned short*>(a.q) + b * a.q_sb + (k * a.g + hh) * a.q_sh + d0;
+      v = load16(qp);
+    }
+    qf[kk] = v;
+  }
+
+  f32x4 acc[NT];
+#pragma unroll
+  for (int mt = 0; mt < NT; ++mt) acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m_run = -INFINITY, l_run = 0.f;
+
+  const int64_t E = entry_count(a, b, k);
+  const int64_t e0 = split * a.chunk;
+  int64_t e1 = e0 + a.chunk;
+  if (e1 > E) e1 = E;
+  const int64_t vplane = P * Hkv * D;
+  const uint32_t hbit_shift = static_cast<uint32_t>(hh);
+
+  for (int64_t base = e0 + 32 * wave; base < e1; base += 128) {
+    if (lane < 32) {
+      int64_t ph = -1;
+      uint32_t mk = 0;
+      const int64_t e = base + lane;
+      if (e < e1) entry_at(a, b, k, e, ph, mk);
+      s_phys[wave][lane] = ph;
+      s_mask[wave][lane] = mk;
+    }
+    wave_sync();
+
+    // K rows as the A operand: lane holds K[row 16rt + c][d = 32kk + 8j .. +8]
+    u32x4 kf[2][KK];
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) {
+      const int64_t ph = s_phys[wave][16 * rt + c];
+      const unsigned short* kp = pool + (ph >= 0 ? k_offset(ph, k, P, Hkv, D) : 0);
+#pragma unroll
+      for (int kk = 0; kk < KK; ++kk) {
+        const int d0 = 32 * kk + 8 * j;
+        u32x4 v = {0u, 0u, 0u, 0u};
+        if (ph >= 0 && d0 < D) v = load16(kp + d0);
+        kf[rt][kk] = v;
+      }
+    }
+    // V rows into LDS, 16 bytes per lane
+#pragma unroll
+    for (int vi = 0; vi < VI; ++vi) {
+      const int row = vi * RPI + lane / LPR;
+      const int cc = lane % LPR;
+      const int64_t ph = s_phys[wave][row];
+      u32x4 v = {0u, 0u, 0u, 0u};
+      if (ph >= 0 && 8 * cc < D) v = load16(pool + k_offset(ph, k, P, Hkv, D) + vplane + 8 * cc);
+      *reinterpret_cast<u32x4*>(vs + row * RS + 8 * cc) = v;
+    }
+
+    // S^T[row][head] = K Q^T
+    f32x4 st[2];
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) {
+      f32x4 s = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kk = 0; kk < KK; ++kk) s = mfma16x16x32<DT>(kf[rt][kk], qf[kk], s);
+      st[rt] = s;
+    }
+
+    // online softmax for head hh over rows 16rt + 4j + i
+    float sv[2][4];
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t mk = s_mask[wave][16 * rt + 4 * j + i];
+        const bool valid = hh < 32 && ((mk >> hbit_shift) & 1u);
+        const float s = valid ? st[rt][i] * a.scale : -INFINITY;
+        sv[rt][i] = s;
+        tmax = fmaxf(tmax, s);
+      }
+    }
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+    const float m_new = fmaxf(m_run, tmax);
+    const float alpha = (m_new == -INFINITY) ? 1.f : __expf(m_run - m_new);
+    unsigned short pb[8];
+    float psum = 0.f;
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float p = (sv[rt][i] == -INFINITY) ? 0.f : __expf(sv[rt][i] - m_new);
+        const unsigned short bits = to_bits<DT>(p);
+        pb[4 * rt + i] = bits;
+        psum += from_bits<DT>(bits);
+      }
+    }
+    l_run = l_run * alpha + psum;
+    m_run = m_new;
+#pragma unroll
+    for (int mt = 0; mt < NT; ++mt) acc[mt] *= alpha;
+
+    u32x4 pf;
+    pf[0] = pb[0] | (static_cast<uint32_t>(pb[1]) << 16);
+    pf[1] = pb[2] | (static_cast<uint32_t>(pb[3]) << 16);
+    pf[2] = pb[4] | (static_cast<uint32_t>(pb[5]) << 16);
+    pf[3] = pb[6] | (static_cast<uint32_t>(pb[7]) << 16);
+
+    wave_sync();  // V tile visible to every lane of the wave
+    // O^T[d][head] += V^T P^T; lane holds V[row rho(j,e)][d = 16mt + c]
+#pragma unroll
+    for (int mt = 0; mt < NT; ++mt) {
+      unsigned short vv[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int row = 16 * (e >> 2) + 4 * j + (e & 3);
+        vv[e] = vs[row * RS + 16 * mt + c];
+      }
+      u32x4 vf;
+      vf[0] = vv[0] | (static_cast<uint32_t>(vv[1]) << 16);
+      vf[1] = vv[2] | (static_cast<uint32_t>(vv[3]) << 16);
+      vf[2] = vv[4] | (static_cast<uint32_t>(vv[5]) << 16);
+      vf[3] = vv[6] | (static_cast<uint32_t>(vv[7]) << 16);
+      acc[mt] = mfma16x16x32<DT>(vf, pf, acc[mt]);
+    }
+    wave_sync();  // all reads of this tile done before the next overwrites it
+  }
+
+  // per-wave totals over the four lane groups that share a head
+  l_run += __shfl_xor(l_run, 16, 64);
+  l_run += __shfl_xor(l_run, 32, 64);
+
+  __syncthreads();
+  float* mo = reinterpret_cast<float*>(smem);  // [4][16][DP]
+  if (j == 0) {
+    s_m[wave][c] = m_run;
+    s_l[wave][c] = l_run;
+  }
+#pragma unroll
+  for (int mt = 0; mt < NT; ++mt) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) mo[(wave * 16 + c) * DP + 16 * mt + 4 * j + i] = acc[mt][i];
+  }
+  __syncthreads();
+
+  // merge the four waves and write this split's partial for each real head
+  for (int idx = threadIdx.x; idx < 16 * DP; idx += 256) {
+    const int head = idx / DP, d = idx % DP;
+    const int hl = 16 * hchunk + head;
+    if (hl >= a.g || d >= D) continue;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) M = fmaxf(M, s_m[w][head]);
+    float L = 0.f, O = 0.f;
+    if (M != -INFINITY) {
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const float f = (s_m[w][head] == -INFINITY) ? 0.f : __expf(s_m[w][head] - M);
+        L += f * s_l[w][head];
+        O += f * mo[(w * 16 + head) * DP + d];
+      }
+    }
+    const int64_t h = k * a.g + hl;
+    const int64_t pidx = (b * a.Hq + h) * a.splits + split;
+    if (d == 0) {
+      a.part_m[pidx] = M;
+      a.part_l[pidx] = L;
+    }
+    a.part_o[pidx * D + d] = O;
+  }
+}
+
+// VALU fallback: one wave per (split, query head, request); any dtype, D <= 512.
+template <int DT>
+__global__ __launch_bounds__(64) void attend_valu_kernel(AttendArgs a) {
+  constexpr int ND = 8;
+  const int lane = threadIdx.x;
+  const int64_t split = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int64_t k = h / a.g;
+  const uint32_t hl = static_cast<uint32_t>(h - k * a.g);
+  const int64_t D = a.D;
+  float q[ND], acc[ND];
+#pragma unroll
+  for (int t = 0; t < ND; ++t) {
+    const int64_t d = lane + 64 * t;
+    q[t] = d < D ? load_elem<DT>(a.q, b * a.q_sb + h * a.q_sh + d) : 0.f;
+    acc[t] = 0.f;
+  }
+  float m_run = -INFINITY, l_run = 0.f;
+  const int64_t E = entry_count(a, b, k);
+  const int64_t e0 = split * a.chunk;
+  int64_t e1 = e0 + a.chunk;
+  if (e1 > E) e1 = E;
+  const int64_t vplane = a.P * a.Hkv * D;
+  for (int64_t e = e0; e < e1; ++e) {
+    int64_t ph;
+    uint32_t mk;
+    entry_at(a, b, k, e, ph, mk);
+    if (hl >= 32 || !((mk >> hl) & 1u)) continue;
+    const int64_t base = k_offset(ph, k, a.P, a.Hkv, D);
+    float dot = 0.f;
+#pragma unroll
+    for (int t = 0; t < ND; ++t) {
+      const int64_t d = lane + 64 * t;
+      if (d < D) dot += q[t] * load_elem<DT>(a.pool, base + d);
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) dot += __shfl_xor(dot, off, 64);
+    const float s = dot * a.scale;
+    const float m_new = fmaxf(m_run, s);
+    const float alpha = (m_run == -INFINITY) ? 0.f : __expf(m_run - m_new);
+    const float p = __expf(s - m_new);
+    l_run = l_run * alpha + p;
+#pragma unroll
+    for (int t = 0; t < ND; ++t) {
+      const int64_t d = lane + 64 * t;
+      const float v = d < D ? load_elem<DT>(a.pool, base + vplane + d) : 0.f;
+      acc[t] = acc[t] * alpha + p * v;
+    }
+    m_run = m_new;
+  }
+  const int64_t pidx = (b * a.Hq + h) * a.splits + split;
+  if (lane == 0) {
+    a.part_m[pidx] = m_run;
+    a.part_l[pidx] = l_run;
+  }
+#pragma unroll
+  for (int t = 0; t < ND; ++t) {
+    const int64_t d = lane + 64 * t;
+    if (d < D) a.part_o[pidx * D + d] = acc[t];
+  }
+}
+
+// Combine split partials: out = sum_s e^(m_s-M) o_s / sum_s e^(m_s-M) l_s, 0 if empty.
+template <int DT>
+__global__ __launch_bounds__(256) void attend_merge_kernel(const float* part_m, const float* part_l,
+                                                            const float* part_o, int64_t splits,
+                                                            int64_t Hq, int64_t D, void* out,
+                                                            int64_t o_sb, int64_t o_sh) {
+  const int64_t h = blockIdx.x, b = blockIdx.y;
+  const int64_t base = (b * Hq + h) * splits;
+  float M = -INFINITY;
+  for (int64_t s = 0; s < splits; ++s) M = fmaxf(M, part_m[base + s]);
+  for (int64_t d = threadIdx.x; d < D; d += blockDim.x) {
+    float L = 0.f, O = 0.f;
+    if (M != -INFINITY) {
+      for (int64_t s = 0; s < splits; ++s) {
+        const float ms = part_m[base + s];
+        if (ms == -INFINITY) continue;
+        const float f = __expf(ms - M);
+        L += f * part_l[base + s];
+        O += f * part_o[(base + s) * D + d];
+      }
+    }
+    store_elem<DT>(out, b * o_sb + h * o_sh + d, L > 0.f ? O / L : 0.f);
+  }
+}
+
+// ---- host side ----------------------------------------------------------------
+
+static int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+struct Plan {
+  bool mfma;
+  int dp;
+  int head_chunks;
+  int64_t splits, chunk;
+};
+
+static Plan plan_attend(int dtype, int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int64_t max_entries) {
+  Plan p{};
+  const int64_t g = Hq / Hkv;
+  p.mfma = dtype != HS_DTYPE_F32 && D % 8 == 0 && D <= 256;
+  if (p.mfma) {
+    p.dp = D <= 32 ? 32 : D <= 64 ? 64 : D <= 128 ? 128 : 256;
+    p.head_chunks = static_cast<int>(ceil_div(g, 16));
+    const int64_t groups = B * Hkv * p.head_chunks;
+    int64_t splits = ceil_div(2048, groups);
+    const int64_t cap = ceil_div(max_entries, 128);
+    if (splits > cap) splits = cap;
+    if (splits < 1) splits = 1;
+    p.chunk = ceil_div(ceil_div(max_entries, splits), 32) * 32;
+    if (p.chunk < 32) p.chunk = 32;
+    p.splits = ceil_div(max_entries, p.chunk);
+    if (p.splits < 1) p.splits = 1;
+  } else {
+    p.dp = 0;
+    p.head_chunks = 1;
+    int64_t splits = ceil_div(1024, B * Hq);
+    const int64_t cap = ceil_div(max_entries, 64);
+    if (splits > cap) splits = cap;
+    if (splits < 1) splits = 1;
+    p.chunk = ceil_div(max_entries, splits);
+    if (p.chunk < 1) p.chunk = 1;
+    p.splits = ceil_div(max_entries, p.chunk);
+    if (p.splits < 1) p.splits = 1;
+  }
+  return p;
+}
+
+static int64_t workspace_for(const Plan& p, int64_t B, int64_t Hq, int64_t D) {
+  const int64_t n = B * Hq * p.splits;
+  return (2 * n + n * D) * 4 + 256;
+}
+
+template <int DT>
+static void launch_mfma(const Plan& p, const AttendArgs& a, hipStream_t s) {
+  dim3 grid(static_cast<unsigned>(p.splits), static_cast<unsigned>(a.Hkv * p.head_chunks),
+            static_cast<unsigned>(a.B));
+  switch (p.dp) {
+    case 32: hipLaunchKernelGGL((attend_mfma_kernel<DT, 32>), grid, dim3(256), 0, s, a); break;
+    case 64: hipLaunchKernelGGL((attend_mfma_kernel<DT, 64>), grid, dim3(256), 0, s, a); break;
+    case 128: hipLaunchKernelGGL((attend_mfma_kernel<DT, 128>), grid, dim3(256), 0, s, a); break;
+    default: hipLaunchKernelGGL((attend_mfma_kernel<DT, 256>), grid, dim3(256), 0, s, a); break;
+  }
+}
+
+static int run_attend(int dtype, AttendArgs a, int64_t max_entries, void* out, int64_t o_sb,
+                      int64_t o_sh, void* ws, int64_t ws_bytes, hipStream_t stream) {
+  Plan p = plan_attend(dtype, a.B, a.Hq, a.Hkv, a.D, max_entries);
+  const int64_t need = workspace_for(p, a.B, a.Hq, a.D);
+  HS_CHECK_ARG(ws != nullptr && ws_bytes >= need, "attention workspace too small: need %lld bytes",
+               static_cast<long long>(need));
+  const int64_t n = a.B * a.Hq * p.splits;
+  float* base = static_cast<float*>(ws);
+  a.part_m = base;
+  a.part_l = base + n;
+  a.part_o = base + 2 * n;
+  a.splits = p.splits;
+  a.chunk = p.chunk;
+  a.head_chunks = p.head_chunks;
+  a.scale = 1.0f / sqrtf(static_cast<float>(a.D));
+  if (p.mfma) {
+    if (dtype == HS_DTYPE_BF16) launch_mfma<HS_DTYPE_BF16>(p, a, stream);
+    else launch_mfma<HS_DTYPE_F16>(p, a, stream);
+  } else {
+    dim3 grid(static_cast<unsigned>(p.splits), static_cast<unsigned>(a.Hq), static_cast<unsigned>(a.B));
+    if (dtype == HS_DTYPE_F32) hipLaunchKernelGGL((attend_valu_kernel<HS_DTYPE_F32>), grid, dim3(64), 0, stream, a);
+    else if (dtype == HS_DTYPE_BF16) hipLaunchKernelGGL((attend_valu_kernel<HS_DTYPE_BF16>), grid, dim3(64), 0, stream, a);
+    else hipLaunchKernelGGL((attend_valu_kernel<HS_DTYPE_F16>), grid, dim3(64), 0, stream, a);
+  }
+  HS_CHECK_LAUNCH("attention");
+  dim3 mgrid(static_cast<unsigned>(a.Hq), static_cast<unsigned>(a.B));
+  const unsigned mthreads = a.D <= 64 ? 64 : (a.D <= 128 ? 128 : 256);
+  if (dtype == HS_DTYPE_F32)
+    hipLaunchKernelGGL((attend_merge_kernel<HS_DTYPE_F32>), mgrid, dim3(mthreads), 0, stream, a.part_m, a.part_l, a.part_o, p.splits, a.Hq, a.D, out, o_sb, o_sh);
+  else if (dtype == HS_DTYPE_BF16)
+    hipLaunchKernelGGL((attend_merge_kernel<HS_DTYPE_BF16>), mgrid, dim3(mthreads), 0, stream, a.part_m, a.part_l, a.part_o, p.splits, a.Hq, a.D, out, o_sb, o_sh);
+  else
+    hipLaunchKernelGGL((attend_merge_kernel<HS_DTYPE_F16>), mgrid, dim3(mthreads), 0, stream, a.part_m, a.part_l, a.part_o, p.splits, a.Hq, a.D, out, o_sb, o_sh);
+  HS_CHECK_LAUNCH("attention merge");
+  return HS_OK;
+}
+
+static int check_common(int dtype, int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int64_t P,
+                        const void* q, const void* pool, const void* out) {
+  HS_CHECK_ARG(valid_dtype(dtype), "invalid dtype code %d", dtype);
+  HS_CHECK_ARG(B >= 1 && Hq >= 1 && Hkv >= 1 && D >= 1 && P >= 1, "attention dimensions must be positive");
+  HS_CHECK_ARG(Hq % Hkv == 0, "query heads must be a multiple of KV heads");
+  HS_CHECK_ARG(Hq / Hkv <= 32, "at most 32 query heads per KV head are supported");
+  HS_CHECK_ARG(D <= 512, "head_dim above 512 is not supported");
+  HS_CHECK_ARG(q && pool && out, "null attention pointer");
+  if (dtype != HS_DTYPE_F32 && D % 8 == 0 && D <= 256)
+    HS_CHECK_ARG((reinterpret_cast<uintptr_t>(q) & 15) == 0 && (reinterpret_cast<uintptr_t>(pool) & 15) == 0,
+                 "query and pool must be 16-byte aligned");
+  return HS_OK;
+}
+
+}  // namespace hs
+
+using namespace hs;
+
+extern "C" int64_t hs_attend_workspace_bytes(int32_t dtype, int64_t batch, int64_t heads,
+                                             int64_t kv_heads, int64_t head_dim,
+                                             int64_t max_entries) {
+  if (batch < 1 || heads < 1 || kv_heads < 1 || head_dim < 1 || max_entries < 1) return 256;
+  Plan p = plan_attend(dtype, batch, heads, kv_heads, head_dim, max_entries);
+  return workspace_for(p, batch, heads, head_dim);
+}
+
+extern "C" int hs_attend_rows(const void* query, int64_t q_stride_b, int64_t q_stride_h,
+                              const void* pool, int32_t dtype, int64_t page_size,
+                              int64_t kv_heads, int64_t head_dim, int64_t pool_rows, const int64_t* rows,
+                              int64_t r_stride_b, int64_t r_stride_h, int64_t r_stride_w,
+                              int64_t width, int64_t batch, int64_t heads, void* out,
+                              int64_t o_stride_b, int64_t o_stride_h, void* workspace,
+                              int64_t workspace_bytes, hipStream_t stream) {
+  int rc = check_common(dtype, batch, heads, kv_heads, head_dim, page_size, query, pool, out);
+  if (rc) return rc;
+  HS_CHECK_ARG(rows != nullptr && width >= 1, "attention needs a nonempty row list");
+  AttendArgs a{};
+  a.q = query;
+  a.q_sb = q_stride_b;
+  a.q_sh = q_stride_h;
+  a.pool = pool;
+  a.P = page_size;
+  a.Hkv = kv_heads;
+  a.D = head_dim;
+  a.pool_rows = pool_rows;
+  a.rows = rows;
+  a.r_sb = r_stride_b;
+  a.r_sh = r_stride_h;
+  a.r_sw = r_stride_w;
+  a.width = width;
+  a.B = batch;
+  a.Hq = heads;
+  a.g = heads / kv_heads;
+  a.mode = r_stride_h == 0 ? MODE_SHARED : MODE_ROWS;
+  const int64_t max_entries = a.mode == MODE_SHARED ? width : a.g * width;
+  return run_attend(dtype, a, max_entries, out, o_stride_b, o_stride_h, workspace, workspace_bytes, stream);
+}
+
+extern "C" int hs_attend_groups(const void* query, int64_t q_stride_b, int64_t q_stride_h,
+                                const void* pool, int32_t dtype, int64_t page_size,
+                                int64_t kv_heads, int64_t head_dim, int64_t pool_rows,
+                                const int64_t* union_physical, int64_t u_stride_b,
+                                const int32_t* entry_columns, const uint32_t* entry_masks,
+                                int64_t e_stride_b, int64_t e_stride_k,
+                                const int32_t* entry_counts, int64_t max_entries,
+                                int64_t batch, int64_t heads, void* out, int64_t o_stride_b,
+                                int64_t o_stride_h, void* workspace, int64_t workspace_bytes,
+                                hipStream_t stream) {
+  int rc = check_common(dtype, batch, heads, kv_heads, head_dim, page_size, query, pool, out);
+  if (rc) return rc;
+  HS_CHECK_ARG(union_physical && entry_columns && entry_masks && entry_counts && max_entries >= 1,
+               "group attention needs union rows and entry lists");
+  AttendArgs a{};
+  a.q = query;
+  a.q_sb = q_stride_b;
+  a.q_sh = q_stride_h;
+  a.pool = pool;
+  a.P = page_size;
+  a.Hkv = kv_heads;
+  a.D = head_dim;
+  a.pool_rows = pool_rows;
+  a.uphys = union_physical;
+  a.u_sb = u_stride_b;
+  a.ecol = entry_columns;
+  a.emask = entry_masks;
+  a.e_sb = e_stride_b;
+  a.e_sk = e_stride_k;
+  a.ecount = entry_counts;
+  a.emax = max_entries;
+  a.B = batch;
+  a.Hq = heads;
+  a.g = heads / kv_heads;
+  a.mode = MODE_GROUPS;
+  return run_attend(dtype, a, max_entries, out, o_stride_b, o_stride_h, workspace, workspace_bytes, stream);
+}

@@ -1,0 +1,163 @@
+// Pinned-host -> hot-row gather for gfx950.
+//
+// Replaces the Triton `_gather` / `gather_rows` of mini_hisparse
+// (row_kernels.py:35-70) and the CPU loop of hybrid.py:466-472: for each plan
+// entry i with host row h >= 0 and device row r >= 0, copy the K plane row and
+// the V plane row (Hkv * D elements each) of host row h into device row r.
+// Both pools are [blocks, 2, P, Hkv, D]; the kernel reads the pinned host pool
+// directly through its device alias, 16 bytes per lane, many rows in flight
+// per workgroup.  It is a byte copy: the dtype only sets the row size.
+#include "hs_common.h"
+
+namespace hs {
+
+constexpr int GT = 256;
+constexpr int GMAXB = 16;
+
+struct GatherArgs {
+  const char* host[GMAXB];
+  char* pool;
+  const int64_t* hrows[GMAXB];
+  const int64_t* drows[GMAXB];
+  const int64_t* count[GMAXB];  // nullable: number of leading valid entries
+  int64_t n[GMAXB];
+  int64_t P, row_bytes;
+};
+
+template <int U>
+struct Unit;
+template <> struct Unit<16> { typedef u32x4 T; };
+template <> struct Unit<8> { typedef unsigned long long T; };
+template <> struct Unit<4> { typedef unsigned int T; };
+template <> struct Unit<2> { typedef unsigned short T; };
+
+// Each workgroup copies `per` rows per iteration; a row (K plane + V plane) is
+// 2 * row_bytes / U units of U bytes.
+template <int U>
+__global__ __launch_bounds__(GT) void gather_kernel(GatherArgs a) {
+  typedef typename Unit<U>::T T;
+  const int64_t b = blockIdx.y;
+  const int64_t units_plane = a.row_bytes / U;
+  const int64_t units_row = 2 * units_plane;
+  int64_t per = GT / units_row;
+  if (per < 1) per = 1;
+  int64_t n = a.n[b];
+  if (a.count[b]) {
+    const int64_t c = *a.count[b];
+    if (c < n) n = c;
+  }
+  const int64_t plane_stride = a.P * a.row_bytes;  // bytes between K and V planes
+  const uint32_t P32 = static_cast<uint32_t>(a.P);
+  const char* host = a.host[b];
+  const int64_t* hrows = a.hrows[b];
+  const int64_t* drows = a.drows[b];
+  if (units_row <= GT) {
+    // fixed (row slot, unit) per thread
+    const int64_t slot = threadIdx.x / units_row;
+    const int64_t w = threadIdx.x - slot * units_row;
+    const bool active = slot < per;
+    const int64_t plane = w / units_plane;
+    const int64_t inrow = plane * plane_stride + (w - plane * units_plane) * U;
+    for (int64_t first = static_cast<int64_t>(blockIdx.x) * per; first < n;
+         first += static_cast<int64_t>(gridDim.x) * per) {
+      const int64_t i = first + slot;
+      if (!active || i >= n) continue;
+      const int64_t h = hrows[i];
+      const int64_t r = drows[i];
+      if (h < 0 || r < 0) continue;
+      const uint32_t hb = static_cast<uint32_t>(h) / P32, ho = static_cast<uint32_t>(h) - hb * P32;
+      const uint32_t rb = static_cast<uint32_t>(r) / P32, ro = static_cast<uint32_t>(r) - rb * P32;
+      const int64_t src = (static_cast<int64_t>(hb) * 2 * a.P + ho) * a.row_bytes + inrow;
+      const int64_t dst = (static_cast<int64_t>(rb) * 2 * a.P + ro) * a.row_bytes + inrow;
+      *reinterpret_cast<T*>(a.pool + dst) = *reinterpret_cast<const T*>(host + src);
+    }
+  } else {
+    // a row wider than the workgroup: one row per iteration, strided units
+    for (int64_t i = blockIdx.x; i < n; i += gridDim.x) {
+      const int64_t h = hrows[i];
+      const int64_t r = drows[i];
+      if (h < 0 || r < 0) continue;
+      const uint32_t hb = static_cast<uint32_t>(h) / P32, ho = static_cast<uint32_t>(h) - hb * P32;
+      const uint32_t rb = static_cast<uint32_t>(r) / P32, ro = static_cast<uint32_t>(r) - rb * P32;
+      const int64_t sbase = (static_cast<int64_t>(hb) * 2 * a.P + ho) * a.row_bytes;
+      const int64_t dbase = (static_cast<int64_t>(rb) * 2 * a.P + ro) * a.row_bytes;
+      for (int64_t w = threadIdx.x; w < units_row; w += GT) {
+        const int64_t plane = w / units_plane;
+        const int64_t inrow = plane * plane_stride + (w - plane * units_plane) * U;
+        *reinterpret_cast<T*>(a.pool + dbase + inrow) = *reinterpret_cast<const T*>(host + sbase + inrow);
+      }
+    }
+  }
+}
+
+}  // namespace hs
+
+using namespace hs;
+
+extern "C" int hs_host_alias(const void* host_ptr, void** device_ptr) {
+  HS_CHECK_ARG(host_ptr != nullptr && device_ptr != nullptr, "null host alias argument");
+  void* dev = nullptr;
+  hipError_t e = hipHostGetDevicePointer(&dev, const_cast<void*>(host_ptr), 0);
+  if (e != hipSuccess || dev == nullptr) {
+    (void)hipGetLastError();
+    hs::set_error("cannot map pinned host allocation to the device: %s", hipGetErrorString(e));
+    return HS_ERUNTIME;
+  }
+  *device_ptr = dev;
+  return HS_OK;
+}
+
+extern "C" int hs_gather_rows_batched(const void* const* host_alias, void* pool,
+                                      const int64_t* const* miss_host_rows,
+                                      const int64_t* const* miss_device_rows,
+                                      const int64_t* const* miss_counts, const int64_t* n,
+                                      int32_t batch, int64_t page_size, int64_t row_bytes,
+                                      int32_t grid_x, hipStream_t stream) {
+  HS_CHECK_ARG(batch >= 1 && batch <= GMAXB, "gather batch must be in [1, %d]", GMAXB);
+  HS_CHECK_ARG(pool && host_alias && miss_host_rows && miss_device_rows && n, "null gather pointer");
+  HS_CHECK_ARG(page_size >= 1 && row_bytes >= 2 && row_bytes % 2 == 0, "invalid gather row shape");
+  GatherArgs a{};
+  a.pool = static_cast<char*>(pool);
+  a.P = page_size;
+  a.row_bytes = row_bytes;
+  int64_t nmax = 0;
+  uintptr_t align = reinterpret_cast<uintptr_t>(pool);
+  for (int32_t i = 0; i < batch; ++i) {
+    HS_CHECK_ARG(host_alias[i] && miss_host_rows[i] && miss_device_rows[i], "null gather plan");
+    a.host[i] = static_cast<const char*>(host_alias[i]);
+    a.hrows[i] = miss_host_rows[i];
+    a.drows[i] = miss_device_rows[i];
+    a.count[i] = miss_counts ? miss_counts[i] : nullptr;
+    a.n[i] = n[i];
+    if (n[i] > nmax) nmax = n[i];
+    align |= reinterpret_cast<uintptr_t>(host_alias[i]);
+  }
+  if (nmax == 0) return HS_OK;
+  const int64_t per_row = 2 * row_bytes;
+  int unit = 2;
+  if (row_bytes % 16 == 0 && (align & 15) == 0) unit = 16;
+  else if (row_bytes % 8 == 0 && (align & 7) == 0) unit = 8;
+  else if (row_bytes % 4 == 0 && (align & 3) == 0) unit = 4;
+  int64_t rows_per_block = (GT * unit) / per_row;
+  if (rows_per_block < 1) rows_per_block = 1;
+  int64_t gx = grid_x > 0 ? grid_x : 1024;
+  const int64_t useful = (nmax + rows_per_block - 1) / rows_per_block;
+  if (gx > useful) gx = useful;
+  dim3 grid(static_cast<unsigned>(gx), static_cast<unsigned>(batch));
+  switch (unit) {
+    case 16: hipLaunchKernelGGL(gather_kernel<16>, grid, dim3(GT), 0, stream, a); break;
+    case 8: hipLaunchKernelGGL(gather_kernel<8>, grid, dim3(GT), 0, stream, a); break;
+    case 4: hipLaunchKernelGGL(gather_kernel<4>, grid, dim3(GT), 0, stream, a); break;
+    default: hipLaunchKernelGGL(gather_kernel<2>, grid, dim3(GT), 0, stream, a); break;
+  }
+  HS_CHECK_LAUNCH("gather");
+  return HS_OK;
+}
+
+extern "C" int hs_gather_rows(const void* host_alias, void* pool, const int64_t* miss_host_rows,
+                              const int64_t* miss_device_rows, int64_t n, const int64_t* miss_count,
+                              int64_t page_size, int64_t row_bytes, hipStream_t stream) {
+  const int64_t* counts[1] = {miss_count};
+  return hs_gather_rows_batched(&host_alias, pool, &miss_host_rows, &miss_device_rows,
+                                miss_count ? counts : nullptr, &n, 1, page_size, row_bytes, 0, stream);
+}

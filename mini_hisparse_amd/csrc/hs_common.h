@@ -1,0 +1,126 @@
+// Shared definitions for the gfx950 kernels of the sparse decode path.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "hisparse.h"
+
+namespace hs {
+
+// ---- error reporting -------------------------------------------------------
+void set_error(const char* fmt, ...);
+
+#define HS_CHECK_ARG(cond, ...)                \
+  do {                                         \
+    if (!(cond)) {                             \
+      ::hs::set_error(__VA_ARGS__);            \
+      return HS_EINVAL;                        \
+    }                                          \
+  } while (0)
+
+#define HS_CHECK_LAUNCH(what)                                              \
+  do {                                                                     \
+    hipError_t _e = hipGetLastError();                                     \
+    if (_e != hipSuccess) {                                                \
+      ::hs::set_error("%s launch failed: %s", what, hipGetErrorString(_e)); \
+      return HS_ELAUNCH;                                                   \
+    }                                                                      \
+  } while (0)
+
+// ---- element types -----------------------------------------------------------
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float bf16_bits_to_f32(unsigned short b) {
+  return __uint_as_float(static_cast<unsigned int>(b) << 16);
+}
+__device__ __forceinline__ float f16_bits_to_f32(unsigned short b) {
+  _Float16 h;
+  __builtin_memcpy(&h, &b, 2);
+  return static_cast<float>(h);
+}
+// Round-to-nearest-even float -> bf16 bits (finite inputs; NaN kept quiet).
+__device__ __forceinline__ unsigned short f32_to_bf16_bits(float f) {
+  unsigned int u = __float_as_uint(f);
+  if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) return static_cast<unsigned short>((u >> 16) | 0x40);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<unsigned short>(u >> 16);
+}
+__device__ __forceinline__ unsigned short f32_to_f16_bits(float f) {
+  _Float16 h = static_cast<_Float16>(f);
+  unsigned short b;
+  __builtin_memcpy(&b, &h, 2);
+  return b;
+}
+
+// Storage element -> float for the three cache dtypes.
+template <int DT>
+__device__ __forceinline__ float load_elem(const void* base, int64_t i) {
+  if constexpr (DT == HS_DTYPE_F32) {
+    return static_cast<const float*>(base)[i];
+  } else if constexpr (DT == HS_DTYPE_BF16) {
+    return bf16_bits_to_f32(static_cast<const unsigned short*>(base)[i]);
+  } else {
+    return f16_bits_to_f32(static_cast<const unsigned short*>(base)[i]);
+  }
+}
+template <int DT>
+__device__ __forceinline__ void store_elem(void* base, int64_t i, float v) {
+  if constexpr (DT == HS_DTYPE_F32) {
+    static_cast<float*>(base)[i] = v;
+  } else if constexpr (DT == HS_DTYPE_BF16) {
+    static_cast<unsigned short*>(base)[i] = f32_to_bf16_bits(v);
+  } else {
+    static_cast<unsigned short*>(base)[i] = f32_to_f16_bits(v);
+  }
+}
+
+inline int elem_bytes(int dtype) { return dtype == HS_DTYPE_F32 ? 4 : 2; }
+inline bool valid_dtype(int dtype) {
+  return dtype == HS_DTYPE_F32 || dtype == HS_DTYPE_F16 || dtype == HS_DTYPE_BF16;
+}
+
+// ---- wave / block primitives (wave64) -----------------------------------------
+__device__ __forceinline__ void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+template <typename T>
+__device__ __forceinline__ T wave_inclusive_sum(T v) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    T o = __shfl_up(v, off, 64);
+    if (lane >= off) v += o;
+  }
+  return v;
+}
+
+// Exclusive prefix sum over a 1-D block of up to 1024 threads.  `scratch` must
+// hold 16 elements.  Returns the exclusive prefix; `total` gets the block sum.
+template <typename T>
+__device__ __forceinline__ T block_exclusive_sum(T v, T* scratch, T* total) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int waves = (blockDim.x + 63) >> 6;
+  T inc = wave_inclusive_sum(v);
+  __syncthreads();
+  if (lane == 63) scratch[wave] = inc;
+  __syncthreads();
+  T base = 0, all = 0;
+  for (int w = 0; w < waves; ++w) {
+    T s = scratch[w];
+    if (w < wave) base += s;
+    all += s;
+  }
+  *total = all;
+  __syncthreads();
+  return base + inc - v;
+}
+
+}  // namespace hs

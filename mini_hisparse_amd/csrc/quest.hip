@@ -1,0 +1,466 @@
+// Quest page scorer, per-head top-k and the device-side union builder for gfx950.
+//
+// Scorer + top-k replace `quest_selection` (selection.py:80-101): for query
+// head h with KV head h // g, page p scores
+//     s = sum_d max(q_d * lo_d, q_d * hi_d)
+// over the page's K minimum/maximum bounds; the tail page and (optionally)
+// page 0 are forced; the `top` best pages per head are kept.  The sum runs over
+// d in ascending order with one float32 rounding per step (for 16-bit inputs
+// the product is exact, so a fused multiply-add gives the same value); ties
+// go to the lower page index.  Since max(q*lo, q*hi) is q*hi for q >= 0 and
+// q*lo otherwise (hi >= lo), the kernel selects the bound before multiplying.
+//
+// The union builder replaces the host adapter Selection -> LogicalTopK
+// (row_index.py:20-31, selection.py:43-60): from the chosen pages it writes the
+// ascending union of selected tokens (padded with -1), each head's union
+// columns, and per KV head the deduplicated union columns its query heads read
+// with a bit mask of those heads (the entry lists of the group attention).
+#include "hs_common.h"
+
+namespace hs {
+
+constexpr int QMAXB = 16;       // requests per launch
+constexpr int QHEADS = 8;       // query heads per scorer thread
+constexpr int QT = 256;         // scorer / top-k threads
+constexpr int UT = 1024;        // union builder threads
+constexpr int64_t UMAXPAGES = 65536;
+
+struct QuestArgs {
+  const float* q;               // [B, Hq, D] float32 (exact copy of the query)
+  int64_t q_sb, q_sh;
+  const void* kmin[QMAXB];      // per request [pages, Hkv, D]
+  const void* kmax[QMAXB];
+  int64_t count[QMAXB];         // ceil(length / P)
+  int64_t Hq, Hkv, g, D, top;
+  int keep_sink;
+  float* scores;                // [B, Hq, cmax]
+  int64_t cmax;
+  int32_t* pages;               // [B, Hq, top]
+  int64_t p_sb;
+};
+
+template <int DT, bool FUSED>
+__global__ __launch_bounds__(QT) void quest_score_kernel(QuestArgs a) {
+#pragma clang fp contract(off)
+  extern __shared__ float sq[];  // [QHEADS][D]
+  const int64_t b = blockIdx.z;
+  const int64_t kv = blockIdx.y / ((a.g + QHEADS - 1) / QHEADS);
+  const int64_t hc = blockIdx.y % ((a.g + QHEADS - 1) / QHEADS);
+  const int64_t count = a.count[b];
+  if (a.top >= count) return;
+  const int64_t h0 = kv * a.g + hc * QHEADS;
+  int64_t nh = a.g - hc * QHEADS;
+  if (nh > QHEADS) nh = QHEADS;
+  const int64_t D = a.D;
+  for (int64_t i = threadIdx.x; i < QHEADS * D; i += QT) {
+    const int64_t hl = i / D, d = i - hl * D;
+    sq[i] = hl < nh ? a.q[b * a.q_sb + (h0 + hl) * a.q_sh + d] : 0.f;
+  }
+  __syncthreads();
+  const int64_t p = static_cast<int64_t>(blockIdx.x) * QT + threadIdx.x;
+  if (p >= count) return;
+  const int64_t row = (p * a.Hkv + kv) * D;
+  const void* lo = a.kmin[b];
+  const void* hi = a.kmax[b];
+  float acc[QHEADS];
+#pragma unroll
+  for (int hl = 0; hl < QHEADS; ++hl) acc[hl] = 0.f;
+  auto step = [&](int64_t d, float l, float u) {
+#pragma unroll
+    for (int hl = 0; hl < QHEADS; ++hl) {
+      const float qv = sq[hl * D + d];
+      const float bound = qv >= 0.f ? u : l;
+      if constexpr (FUSED) {
+        acc[hl] = __builtin_fmaf(qv, bound, acc[hl]);
+      } else {
+        const float prod = qv * bound;
+        acc[hl] = acc[hl] + prod;
+      }
+    }
+  };
+  constexpr int EPV = DT == HS_DTYPE_F32 ? 4 : 8;  // elements per 16-byte load
+  const bool vec = (D % EPV) == 0;
+  if (vec) {
+    for (int64_t d0 = 0; d0 < D; d0 += EPV) {
+      const u32x4 L = *reinterpret_cast<const u32x4*>(static_cast<const char*>(lo) + (row + d0) * (DT == HS_DTYPE_F32 ? 4 : 2));
+      const u32x4 U = *reinterpret_cast<const u32x4*>(static_cast<const char*>(hi) + (row + d0) * (DT == HS_DTYPE_F32 ? 4 : 2));
+#pragma unroll
+      for (int e = 0; e < EPV; ++e) {
+        float l, u;
+        if constexpr (DT == HS_DTYPE_F32) {
+          l = __uint_as_float(L[e]);
+          u = __uint_as_float(U[e]);
+        } else {
+          const unsigned short lb = static_cast<unsigned short>(L[e >> 1] >> (16 * (e & 1)));
+          const unsigned short ub = static_cast<unsigned short>(U[e >> 1] >> (16 * (e & 1)));
+          if constexpr (DT == HS_DTYPE_BF16) {
+            l = bf16_bits_to_f32(lb);
+            u = bf16_bits_to_f32(ub);
+          } else {
+            l = f16_bits_to_f32(lb);
+            u = f16_bits_to_f32(ub);
+          }
+        }
+        step(d0 + e, l, u);
+      }
+    }
+  } else {
+    for (int64_t d = 0; d < D; ++d) step(d, load_elem<DT>(lo, row + d), load_elem<DT>(hi, row + d));
+  }
+  for (int hl = 0; hl < nh; ++hl) a.scores[(b * a.Hq + h0 + hl) * a.cmax + p] = acc[hl];
+}
+
+__device__ __forceinline__ uint32_t score_key(float s) {
+  if (s == 0.f) s = 0.f;  // -0 and +0 compare equal
+  const uint32_t u = __float_as_uint(s);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+// One workgroup per (query head, request): radix select of the top keys, ties
+// to the lower page, pages written ascending.
+__global__ __launch_bounds__(QT) void quest_topk_kernel(QuestArgs a) {
+  __shared__ uint32_t hist[256];
+  __shared__ uint32_t s_prefix, s_mask, s_need;
+  __shared__ int64_t scan64[16];
+  const int64_t h = blockIdx.x, b = blockIdx.y;
+  const int64_t count = a.count[b];
+  int32_t* out = a.pages + b * a.p_sb + h * a.top;
+  if (a.top >= count) {
+    for (int64_t j = threadIdx.x; j < count; j += QT) out[j] = static_cast<int32_t>(j);
+    return;
+  }
+  const float* sc = a.scores + (b * a.Hq + h) * a.cmax;
+  const bool sink = a.keep_sink && a.top > 1 && count > 1;
+  auto key_of = [&](int64_t p) -> uint32_t {
+    if (p == count - 1 || (sink && p == 0)) return 0xffffffffu;
+    return score_key(sc[p]);
+  };
+  if (threadIdx.x == 0) {
+    s_prefix = 0u;
+    s_mask = 0u;
+    s_need = static_cast<uint32_t>(a.top);
+  }
+  __syncthreads();
+  for (int shift = 24; shift >= 0; shift -= 8) {
+    for (int i = threadIdx.x; i < 256; i += QT) hist[i] = 0u;
+    __syncthreads();
+    const uint32_t prefix = s_prefix, mask = s_mask;
+    for (int64_t p = threadIdx.x; p < count; p += QT) {
+      const uint32_t k = key_of(p);
+      if ((k & mask) == prefix) atomicAdd(&hist[(k >> shift) & 255u], 1u);
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      uint32_t need = s_need, above = 0u;
+      int dsel = 0;
+      for (int dg = 255; dg >= 0; --dg) {
+        if (above + hist[dg] >= need) {
+          dsel = dg;
+          break;
+        }
+        above += hist[dg];
+      }
+      s_need = need - above;
+      s_prefix = prefix | (static_cast<uint32_t>(dsel) << shift);
+      s_mask = mask | (255u << shift);
+    }
+    __syncthreads();
+  }
+  const uint32_t kth = s_prefix, need_eq = s_need;
+  // ordered compaction over contiguous page ranges
+  const int64_t per = (count + QT - 1) / QT;
+  const int64_t p0 = threadIdx.x * per;
+  int64_t p1 = p0 + per;
+  if (p1 > count) p1 = count;
+  int64_t eq = 0;
+  for (int64_t p = p0; p < p1; ++p) eq += key_of(p) == kth;
+  int64_t tot;
+  const int64_t eq_before = block_exclusive_sum<int64_t>(eq, scan64, &tot);
+  int64_t sel = 0, e = eq_before;
+  for (int64_t p = p0; p < p1; ++p) {
+    const uint32_t k = key_of(p);
+    if (k > kth) ++sel;
+    else if (k == kth && e++ < static_cast<int64_t>(need_eq)) ++sel;
+  }
+  const int64_t sel_before = block_exclusive_sum<int64_t>(sel, scan64, &tot);
+  int64_t o = sel_before;
+  e = eq_before;
+  for (int64_t p = p0; p < p1; ++p) {
+    const uint32_t k = key_of(p);
+    bool take = k > kth;
+    if (!take && k == kth) take = e++ < static_cast<int64_t>(need_eq);
+    if (take) out[o++] = static_cast<int32_t>(p);
+  }
+}
+
+struct UnionArgs {
+  const int32_t* pages;  // [B, Hq, top], first min(top, count) ascending
+  int64_t p_sb, top;
+  int64_t length[QMAXB];
+  int64_t P, Hq, Hkv, g;
+  int32_t* positions;    // [B, cap]
+  int64_t pos_cap;
+  int64_t* head_columns; // [B, Hq, width]
+  int64_t width;
+  int32_t* union_count;  // [B]
+  int32_t* ecol;         // [B, Hkv, ecap]
+  uint32_t* emask;
+  int64_t ecap;
+  int32_t* ecount;       // [B, Hkv]
+  int32_t* status;       // nonzero on overflow
+};
+
+__device__ __forceinline__ bool head_has_page(const int32_t* row, int64_t k, int32_t p) {
+  int64_t lo = 0, hi = k;
+  while (lo < hi) {
+    const int64_t mid = (lo + hi) >> 1;
+    if (row[mid] < p) lo = mid + 1;
+    else hi = mid;
+  }
+  return lo < k && row[lo] == p;
+}
+
+// blockIdx.x < Hkv: group entries of that KV head; blockIdx.x == Hkv: union
+// positions, per-head columns and the union size.
+__global__ __launch_bounds__(UT) void build_union_kernel(UnionArgs a) {
+  __shared__ uint32_t ubits[UMAXPAGES / 32];
+  __shared__ uint32_t uprefix[UMAXPAGES / 32];
+  __shared__ uint32_t gbits[UMAXPAGES / 32];
+  __shared__ uint32_t gprefix[UMAXPAGES / 32];
+  __shared__ int32_t scan32[16];
+  const int64_t b = blockIdx.y;
+  const int64_t part = blockIdx.x;
+  const int64_t L = a.length[b], P = a.P;
+  const int64_t count = (L + P - 1) / P;
+  const int64_t k = a.top < count ? a.top : count;
+  const int64_t tail_len = L - (count - 1) * P;
+  const int64_t words = (count + 31) / 32;
+  const int32_t* pg = a.pages + b * a.p_sb;
+  const bool group = part < a.Hkv;
+
+  for (int64_t i = threadIdx.x; i < words; i += UT) {
+    ubits[i] = 0u;
+    gbits[i] = 0u;
+  }
+  __syncthreads();
+  for (int64_t i = threadIdx.x; i < a.Hq * k; i += UT) {
+    const int64_t h = i / k, j = i - h * k;
+    const int32_t p = pg[h * a.top + j];
+    if (p < 0 || p >= count) continue;
+    atomicOr(&ubits[p >> 5], 1u << (p & 31));
+    if (group && h / a.g == part) atomicOr(&gbits[p >> 5], 1u << (p & 31));
+  }
+  __syncthreads();
+  // word prefix popcounts (serial per thread chunk, then block scan)
+  {
+    const int64_t per = (words + UT - 1) / UT;
+    const int64_t w0 = threadIdx.x * per;
+    int64_t w1 = w0 + per;
+    if (w1 > words) w1 = words;
+    int32_t cu = 0, cg = 0;
+    for (int64_t w = w0; w < w1; ++w) {
+      cu += __popc(ubits[w]);
+      cg += __popc(gbits[w]);
+    }
+    int32_t tu, tg;
+    int32_t bu = block_exclusive_sum<int32_t>(cu, scan32, &tu);
+    int32_t bg = block_exclusive_sum<int32_t>(cg, scan32, &tg);
+    for (int64_t w = w0; w < w1; ++w) {
+      uprefix[w] = bu;
+      gprefix[w] = bg;
+      bu += __popc(ubits[w]);
+      bg += __popc(gbits[w]);
+    }
+  }
+  __syncthreads();
+  auto rank_of = [&](const uint32_t* bits, const uint32_t* pre, int64_t p) -> int64_t {
+    const uint32_t below = (p & 31) ? (bits[p >> 5] & ((1u << (p & 31)) - 1u)) : 0u;
+    return static_cast<int64_t>(pre[p >> 5]) + __popc(below);
+  };
+
+  if (!group) {
+    const int64_t upages = rank_of(ubits, uprefix, count - 1) + 1;  // the tail page is always selected
+    const int64_t n = upages * P - (P - tail_len);
+    if (threadIdx.x == 0) {
+      a.union_count[b] = static_cast<int32_t>(n);
+      if (n > a.pos_cap) atomicOr(a.status, 1);
+    }
+    int32_t* pos = a.positions + b * a.pos_cap;
+    for (int64_t p = threadIdx.x; p < count; p += UT) {
+      if (!((ubits[p >> 5] >> (p & 31)) & 1u)) continue;
+      const int64_t base = rank_of(ubits, uprefix, p) * P;
+      const int64_t plen = p == count - 1 ? tail_len : P;
+      for (int64_t off = 0; off < plen; ++off)
+        if (base + off < a.pos_cap) pos[base + off] = static_cast<int32_t>(p * P + off);
+    }
+    for (int64_t i = n + threadIdx.x; i < a.pos_cap; i += UT) pos[i] = -1;
+    // per-head columns: head h's j-th token (its pages ascending, tail last)
+    const int64_t W = (k - 1) * P + tail_len;
+    int64_t* hc = a.head_columns + b * a.Hq * a.width;
+    for (int64_t e = threadIdx.x; e < a.Hq * a.width; e += UT) {
+      const int64_t h = e / a.width, jj = e - h * a.width;
+      int64_t col = -1;
+      if (jj < W) {
+        int64_t p, off;
+        if (jj < (k - 1) * P) {
+          p = pg[h * a.top + jj / P];
+          off = jj % P;
+        } else {
+          p = count - 1;
+          off = jj - (k - 1) * P;
+        }
+        col = rank_of(ubits, uprefix, p) * P + off;
+      }
+      hc[e] = col;
+    }
+  } else {
+    const int64_t kv = part;
+    const int64_t gpages = rank_of(gbits, gprefix, count - 1) + 1;
+    const int64_t E = gpages * P - (P - tail_len);
+    if (threadIdx.x == 0) {
+      a.ecount[b * a.Hkv + kv] = static_cast<int32_t>(E < a.ecap ? E : a.ecap);
+      if (E > a.ecap) atomicOr(a.status, 2);
+    }
+    int32_t* ec = a.ecol + (b * a.Hkv + kv) * a.ecap;
+    uint32_t* em = a.emask + (b * a.Hkv + kv) * a.ecap;
+    for (int64_t p = threadIdx.x; p < count; p += UT) {
+      if (!((gbits[p >> 5] >> (p & 31)) & 1u)) continue;
+      uint32_t mask = 0u;
+      for (int64_t hl = 0; hl < a.g; ++hl)
+        if (head_has_page(pg + (kv * a.g + hl) * a.top, k, static_cast<int32_t>(p))) mask |= 1u << hl;
+      const int64_t gbase = rank_of(gbits, gprefix, p) * P;
+      const int64_t ubase = rank_of(ubits, uprefix, p) * P;
+      const int64_t plen = p == count - 1 ? tail_len : P;
+      for (int64_t off = 0; off < plen; ++off) {
+        if (gbase + off < a.ecap) {
+          ec[gbase + off] = static_cast<int32_t>(ubase + off);
+          em[gbase + off] = mask;
+        }
+      }
+    }
+  }
+}
+
+static int64_t ceil_div(int64_t x, int64_t y) { return (x + y - 1) / y; }
+
+}  // namespace hs
+
+using namespace hs;
+
+extern "C" int64_t hs_quest_workspace_bytes(int64_t batch, int64_t heads, int64_t max_pages) {
+  if (batch < 1 || heads < 1 || max_pages < 1) return 256;
+  return ((batch * heads * max_pages * 4) + 255) & ~static_cast<int64_t>(255);
+}
+
+extern "C" int hs_quest_topk(const float* query, int64_t q_stride_b, int64_t q_stride_h,
+                             int32_t query_is_16bit, const void* const* minimum,
+                             const void* const* maximum, int32_t kv_dtype,
+                             const int64_t* page_counts, int64_t batch, int64_t heads,
+                             int64_t kv_heads, int64_t head_dim, int64_t top, int32_t keep_sink,
+                             int32_t* out_pages, int64_t out_stride_b, void* workspace,
+                             int64_t workspace_bytes, hipStream_t stream) {
+  HS_CHECK_ARG(top >= 1 && heads >= 1 && kv_heads >= 1 && heads % kv_heads == 0,
+               "invalid page budget or GQA shape");
+  HS_CHECK_ARG(batch >= 1 && batch <= QMAXB, "quest batch must be in [1, %d]", QMAXB);
+  HS_CHECK_ARG(valid_dtype(kv_dtype), "invalid dtype code %d", kv_dtype);
+  HS_CHECK_ARG(head_dim >= 1 && head_dim <= 1024, "invalid head_dim");
+  HS_CHECK_ARG(query && minimum && maximum && page_counts && out_pages, "null quest pointer");
+  QuestArgs a{};
+  a.q = query;
+  a.q_sb = q_stride_b;
+  a.q_sh = q_stride_h;
+  int64_t cmax = 1;
+  for (int64_t i = 0; i < batch; ++i) {
+    HS_CHECK_ARG(page_counts[i] >= 1, "cannot select pages of an empty history");
+    HS_CHECK_ARG(minimum[i] && maximum[i], "null bounds pointer");
+    a.kmin[i] = minimum[i];
+    a.kmax[i] = maximum[i];
+    a.count[i] = page_counts[i];
+    if (page_counts[i] > cmax) cmax = page_counts[i];
+  }
+  a.Hq = heads;
+  a.Hkv = kv_heads;
+  a.g = heads / kv_heads;
+  a.D = head_dim;
+  a.top = top;
+  a.keep_sink = keep_sink;
+  a.cmax = cmax;
+  a.pages = out_pages;
+  a.p_sb = out_stride_b;
+  const int64_t need = hs_quest_workspace_bytes(batch, heads, cmax);
+  HS_CHECK_ARG(workspace && workspace_bytes >= need, "quest workspace too small: need %lld bytes",
+               static_cast<long long>(need));
+  a.scores = static_cast<float*>(workspace);
+  bool any_scored = false;
+  for (int64_t i = 0; i < batch; ++i) any_scored |= top < page_counts[i];
+  if (any_scored) {
+    const int64_t hchunks = ceil_div(a.g, QHEADS);
+    dim3 grid(static_cast<unsigned>(ceil_div(cmax, QT)), static_cast<unsigned>(kv_heads * hchunks),
+              static_cast<unsigned>(batch));
+    const size_t lds = static_cast<size_t>(QHEADS * head_dim * 4);
+    const bool fused = query_is_16bit && kv_dtype != HS_DTYPE_F32;
+    if (kv_dtype == HS_DTYPE_BF16) {
+      if (fused) hipLaunchKernelGGL((quest_score_kernel<HS_DTYPE_BF16, true>), grid, dim3(QT), lds, stream, a);
+      else hipLaunchKernelGGL((quest_score_kernel<HS_DTYPE_BF16, false>), grid, dim3(QT), lds, stream, a);
+    } else if (kv_dtype == HS_DTYPE_F16) {
+      if (fused) hipLaunchKernelGGL((quest_score_kernel<HS_DTYPE_F16, true>), grid, dim3(QT), lds, stream, a);
+      else hipLaunchKernelGGL((quest_score_kernel<HS_DTYPE_F16, false>), grid, dim3(QT), lds, stream, a);
+    } else {
+      hipLaunchKernelGGL((quest_score_kernel<HS_DTYPE_F32, false>), grid, dim3(QT), lds, stream, a);
+    }
+    HS_CHECK_LAUNCH("quest scorer");
+  }
+  hipLaunchKernelGGL(quest_topk_kernel, dim3(static_cast<unsigned>(heads), static_cast<unsigned>(batch)),
+                     dim3(QT), 0, stream, a);
+  HS_CHECK_LAUNCH("quest top-k");
+  return HS_OK;
+}
+
+extern "C" int hs_build_union(const int32_t* pages, int64_t p_stride_b, int64_t top,
+                              const int64_t* lengths, int64_t page_size, int64_t batch,
+                              int64_t heads, int64_t kv_heads, int32_t* positions,
+                              int64_t pos_capacity, int64_t* head_columns, int64_t width,
+                              int32_t* union_count, int32_t* entry_columns,
+                              uint32_t* entry_masks, int64_t entry_capacity,
+                              int32_t* entry_counts, int32_t* status, hipStream_t stream) {
+  HS_CHECK_ARG(batch >= 1 && batch <= QMAXB, "union batch must be in [1, %d]", QMAXB);
+  HS_CHECK_ARG(top >= 1 && page_size >= 1 && heads >= 1 && kv_heads >= 1 && heads % kv_heads == 0,
+               "invalid union shape");
+  HS_CHECK_ARG(heads / kv_heads <= 32, "at most 32 query heads per KV head");
+  HS_CHECK_ARG(pages && lengths && positions && head_columns && union_count && entry_columns &&
+                   entry_masks && entry_counts && status,
+               "null union pointer");
+  HS_CHECK_ARG(pos_capacity >= 1 && entry_capacity >= 1 && width >= 1, "union capacities must be positive");
+  UnionArgs a{};
+  a.pages = pages;
+  a.p_sb = p_stride_b;
+  a.top = top;
+  for (int64_t i = 0; i < batch; ++i) {
+    HS_CHECK_ARG(lengths[i] >= 1, "cannot build a union over an empty history");
+    HS_CHECK_ARG(ceil_div(lengths[i], page_size) <= UMAXPAGES, "too many pages for the union builder");
+    const int64_t count = ceil_div(lengths[i], page_size);
+    const int64_t k = top < count ? top : count;
+    const int64_t W = (k - 1) * page_size + (lengths[i] - (count - 1) * page_size);
+    HS_CHECK_ARG(W <= width, "head column width %lld below the selection width %lld",
+                 static_cast<long long>(width), static_cast<long long>(W));
+    a.length[i] = lengths[i];
+  }
+  a.P = page_size;
+  a.Hq = heads;
+  a.Hkv = kv_heads;
+  a.g = heads / kv_heads;
+  a.positions = positions;
+  a.pos_cap = pos_capacity;
+  a.head_columns = head_columns;
+  a.width = width;
+  a.union_count = union_count;
+  a.ecol = entry_columns;
+  a.emask = entry_masks;
+  a.ecap = entry_capacity;
+  a.ecount = entry_counts;
+  a.status = status;
+  hipLaunchKernelGGL(build_union_kernel, dim3(static_cast<unsigned>(kv_heads + 1), static_cast<unsigned>(batch)),
+                     dim3(UT), 0, stream, a);
+  HS_CHECK_LAUNCH("union builder");
+  return HS_OK;
+}

@@ -1,0 +1,156 @@
+"""Row gather from pinned host memory and physical-row attention on gfx950.
+
+Replaces mini_hisparse's ``row_kernels.py`` (Triton ``_gather``/``_attend`` and
+the ctypes ``MappedHost``, row_kernels.py:10-135) with calls into
+libhisparse_hip.so.  Same function names and arguments; no Triton, no CUDA
+driver calls.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _lib
+
+
+class MappedHost:
+    """Keep a pinned host tensor alive and expose its device alias.
+
+    Like the reference (row_kernels.py:10-32) the allocation stays owned by
+    PyTorch; the alias comes from ``hs_host_alias`` and nothing is registered
+    or unregistered.
+    """
+
+    def __init__(self, tensor):
+        if not tensor.is_pinned():
+            raise ValueError("row gather requires pinned host backing")
+        device_ptr = ctypes.c_void_p()
+        status = _lib.load().hs_host_alias(tensor.data_ptr(), ctypes.byref(device_ptr))
+        if status != 0:
+            raise RuntimeError(
+                "cannot map pinned host allocation to the device: "
+                + _lib.load().hs_last_error().decode(errors="replace")
+            )
+        self.tensor, self.dtype, self.pointer = tensor, tensor.dtype, device_ptr.value
+
+    def data_ptr(self):
+        return self.pointer
+
+
+def _row_bytes(config, element_size):
+    return config.kv_heads * config.head_dim * element_size
+
+
+def gather_rows(host, pool, plan, config, *, miss_count=None):
+    """Copy every planned host row (K and V planes) into its hot device row.
+
+    ``host`` is a :class:`MappedHost`; ``plan`` a RowPlan (row_index.py:51-56).
+    ``miss_count`` (optional device int64 scalar, e.g. ``plan.counts[2:]``)
+    bounds the number of plan entries read.
+    """
+    if pool.device.type != "cuda":
+        raise ValueError("the HIP gather needs a ROCm device pool")
+    n = plan.miss_host_rows.numel()
+    if n == 0:
+        return
+    if plan.miss_host_rows.dtype != torch.int64 or plan.miss_device_rows.dtype != torch.int64:
+        raise ValueError("gather plans must be int64")
+    status = _lib.load().hs_gather_rows(
+        host.data_ptr(),
+        pool.data_ptr(),
+        plan.miss_host_rows.data_ptr(),
+        plan.miss_device_rows.data_ptr(),
+        n,
+        _lib.ptr(miss_count),
+        config.page_size,
+        _row_bytes(config, pool.element_size()),
+        _lib.stream_handle(pool.device),
+    )
+    _lib.check(status, "hs_gather_rows")
+
+
+def _attend_workspace(dtype_code, batch, heads, kv_heads, head_dim, max_entries, device):
+    size = _lib.load().hs_attend_workspace_bytes(dtype_code, batch, heads, kv_heads, head_dim, max_entries)
+    return torch.empty(size, dtype=torch.uint8, device=device), size
+
+
+def _check_query(query, pool, config):
+    if query.device.type != "cuda" or pool.device.type != "cuda":
+        raise ValueError("the HIP attention needs ROCm device tensors")
+    if query.dtype != pool.dtype:
+        query = query.to(pool.dtype)
+    return query.contiguous()
+
+
+def attend_rows(query, pool, rows, config):
+    """Attention of each query head over its physical rows (row_kernels.py:116-135).
+
+    query [Hq, D] (or [B, Hq, D]); rows [Hq, W] or [W] shared (or batched
+    [B, Hq, W] / [B, W]); returns [Hq, D] (or [B, Hq, D]) in the query dtype.
+    """
+    batched = query.ndim == 3
+    out_dtype = query.dtype
+    q = _check_query(query, pool, config)
+    if not batched:
+        q = q[None]
+        rows = rows[None]
+    batch, heads, dim = q.shape
+    if rows.dtype != torch.int64:
+        rows = rows.to(torch.int64)
+    if rows.ndim == 2:  # one row list shared by every head
+        r_sb, r_sh, r_sw = rows.stride(0), 0, rows.stride(1)
+        width = rows.shape[1]
+        max_entries = width
+    else:
+        r_sb, r_sh, r_sw = rows.stride()
+        width = rows.shape[2]
+        if r_sh == 0:
+            max_entries = width
+        else:
+            max_entries = width * (heads // config.kv_heads)
+    out = torch.empty_like(q)
+    code = _lib.dtype_code(pool.dtype)
+    workspace, ws_bytes = _attend_workspace(code, batch, heads, config.kv_heads, dim, max(1, max_entries), q.device)
+    status = _lib.load().hs_attend_rows(
+        q.data_ptr(), q.stride(0), q.stride(1),
+        pool.data_ptr(), code, config.page_size, config.kv_heads, config.head_dim,
+        pool.shape[0] * config.page_size, rows.data_ptr(), r_sb, r_sh, r_sw, width, batch, heads,
+        out.data_ptr(), out.stride(0), out.stride(1),
+        workspace.data_ptr(), ws_bytes, _lib.stream_handle(q.device),
+    )
+    _lib.check(status, "hs_attend_rows")
+    out = out if batched else out[0]
+    return out if out.dtype == out_dtype else out.to(out_dtype)
+
+
+def attend_groups(query, pool, union_physical, entries, config):
+    """Attention reading each KV head's deduplicated rows once (hs_attend_groups).
+
+    ``entries`` is a GroupEntries (or a batched one with a leading batch dim)
+    and ``union_physical`` the resolver's input-order physical rows.
+    """
+    batched = query.ndim == 3
+    out_dtype = query.dtype
+    q = _check_query(query, pool, config)
+    cols, masks, counts = entries.columns, entries.masks, entries.counts
+    up = union_physical
+    if not batched:
+        q, cols, masks, counts, up = q[None], cols[None], masks[None], counts[None], up[None]
+    batch, heads, dim = q.shape
+    out = torch.empty_like(q)
+    code = _lib.dtype_code(pool.dtype)
+    capacity = entries.capacity
+    workspace, ws_bytes = _attend_workspace(code, batch, heads, config.kv_heads, dim, capacity, q.device)
+    status = _lib.load().hs_attend_groups(
+        q.data_ptr(), q.stride(0), q.stride(1),
+        pool.data_ptr(), code, config.page_size, config.kv_heads, config.head_dim,
+        pool.shape[0] * config.page_size, up.data_ptr(), up.stride(0),
+        cols.data_ptr(), masks.data_ptr(), cols.stride(0), cols.stride(1), counts.data_ptr(), capacity,
+        batch, heads, out.data_ptr(), out.stride(0), out.stride(1),
+        workspace.data_ptr(), ws_bytes, _lib.stream_handle(q.device),
+    )
+    _lib.check(status, "hs_attend_groups")
+    out = out if batched else out[0]
+    return out if out.dtype == out_dtype else out.to(out_dtype)

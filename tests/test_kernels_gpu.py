@@ -1,0 +1,318 @@
+"""Parity of the gfx950 kernels with the CPU oracle on identical seeded inputs.
+
+Integer outputs (resolver, Quest pages, union builder, gather) must be
+bit-exact; attention must match the float64 oracle within the north-star
+tolerance (2e-2 abs / 1e-2 rel in bf16/fp16, fp32 accumulate) and the
+reference's own test tolerances (fp32: 2e-6 / 2e-5, low precision 0.004 / 0.02,
+tests/test_hybrid.py:59, :187-189).
+"""
+
+from __future__ import annotations
+
+import json
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from oracle.quest import pages_to_positions
+from oracle.union import from_selection as oracle_union, group_entries
+from tests.kernel_cases import (
+    cfg,
+    make_pool,
+    quest_bounds,
+    random_positions,
+    random_rows,
+    resolver_tables,
+)
+
+pytestmark = pytest.mark.gpu
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+
+
+def _close(actual, expected, atol, rtol):
+    actual = actual.detach().cpu().double().numpy()
+    err = np.abs(actual - expected)
+    bound = atol + rtol * np.abs(expected)
+    assert (err <= bound).all(), f"max err {err.max():.3g}, worst excess {(err - bound).max():.3g}"
+
+
+TOL = {torch.bfloat16: (2e-2, 1e-2), torch.float16: (2e-2, 1e-2), torch.float32: (2e-6, 2e-5)}
+
+
+# ----------------------------------------------------------------- attention
+@pytest.mark.parametrize(
+    "dtype,P,kv,g,D,W,blocks",
+    [
+        (torch.bfloat16, 16, 8, 8, 128, 300, 64),  # microbench head shape
+        (torch.bfloat16, 16, 4, 7, 128, 200, 40),  # Qwen2.5-7B head shape
+        (torch.bfloat16, 16, 2, 7, 64, 130, 40),   # Qwen2.5-0.5B head shape
+        (torch.float16, 7, 2, 3, 24, 45, 30),      # non-power-of-two page and head_dim
+        (torch.bfloat16, 4, 1, 2, 8, 9, 10),
+        (torch.float32, 4, 1, 2, 8, 9, 10),        # reference test shape
+        (torch.float32, 16, 2, 7, 64, 70, 20),
+        (torch.bfloat16, 16, 1, 20, 32, 40, 20),   # more than 16 heads per KV head
+    ],
+)
+def test_attend_rows_matches_oracle(gpu, dtype, P, kv, g, D, W, blocks):
+    from mini_hisparse_amd.row_kernels import attend_rows
+
+    heads = kv * g
+    pool = make_pool(blocks, P, kv, D, dtype, seed=1, outliers=True)
+    q = torch.randn(heads, D, generator=torch.Generator().manual_seed(2)).to(dtype)
+    rows = random_rows(heads, W, blocks * P, seed=3)
+    expected = oracle.row_attention_rows(q, pool, rows, P)
+    actual = attend_rows(q.to(gpu), pool.to(gpu), rows.to(gpu), cfg(P, kv, D))
+    assert actual.dtype == dtype and actual.shape == (heads, D)
+    _close(actual, expected, *TOL[dtype])
+    if dtype != torch.float32:
+        _close(actual, expected, 0.004, 0.02)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_attend_shared_rows_masks_and_empty_heads(gpu, dtype):
+    from mini_hisparse_amd.row_kernels import attend_rows
+
+    P, kv, D, heads, blocks = 16, 2, 64, 8, 12
+    pool = make_pool(blocks, P, kv, D, dtype, seed=5)
+    q = torch.randn(heads, D, generator=torch.Generator().manual_seed(6)).to(dtype)
+    shared = torch.tensor([5, -1, 17, 17, 190, -1, 3])  # duplicate rows count twice, like the reference
+    expected = oracle.row_attention_rows(q, pool, shared, P)
+    actual = attend_rows(q.to(gpu), pool.to(gpu), shared.to(gpu), cfg(P, kv, D))
+    _close(actual, expected, *TOL[dtype])
+    masked = torch.full((heads, 5), -1)
+    masked[1, 2] = 7
+    out = attend_rows(q.to(gpu), pool.to(gpu), masked.to(gpu), cfg(P, kv, D)).cpu()
+    assert torch.count_nonzero(out[0]) == 0 and torch.count_nonzero(out[2:]) == 0
+    _close(out[1:2], oracle.row_attention_rows(q, pool, masked, P)[1:2], *TOL[dtype])
+
+
+def test_attend_batched_matches_single(gpu):
+    from mini_hisparse_amd.row_kernels import attend_rows
+
+    P, kv, g, D, blocks, W = 16, 4, 7, 128, 50, 260
+    heads = kv * g
+    pool = make_pool(blocks, P, kv, D, torch.bfloat16, seed=8).to(gpu)
+    qs = torch.randn(3, heads, D, generator=torch.Generator().manual_seed(9)).to(torch.bfloat16).to(gpu)
+    rows = torch.stack([random_rows(heads, W, blocks * P, seed=10 + b) for b in range(3)]).to(gpu)
+    batched = attend_rows(qs, pool, rows, cfg(P, kv, D))
+    for b in range(3):
+        single = attend_rows(qs[b], pool, rows[b], cfg(P, kv, D))
+        torch.testing.assert_close(batched[b], single, atol=1e-2, rtol=1e-2)
+
+
+# ------------------------------------------------------------------ resolver
+def _resolve_gpu(gpu, tables, positions, length, page_size, head_columns=None):
+    from mini_hisparse_amd.row_index import LogicalTopK, resolve_rows
+
+    t = {k: torch.from_numpy(np.ascontiguousarray(v)).to(gpu) for k, v in tables.items()}
+    cols = None if head_columns is None else torch.from_numpy(head_columns).to(gpu)
+    topk = LogicalTopK(torch.from_numpy(positions).to(gpu), cols)
+    plan = resolve_rows(topk, t["source"], t["resident"], t["hot"], t["tags"], t["lru"], length, page_size)
+    return plan, t["tags"].cpu().numpy(), t["lru"].cpu().numpy()
+
+
+def _assert_plan(plan, tags, lru, expected):
+    phys, mh, md, counts, tags_after, lru_after = expected
+    np.testing.assert_array_equal(plan.physical_rows.cpu().numpy(), phys)
+    np.testing.assert_array_equal(plan.miss_host_rows.cpu().numpy(), mh)
+    np.testing.assert_array_equal(plan.miss_device_rows.cpu().numpy(), md)
+    np.testing.assert_array_equal(plan.counts.cpu().numpy(), counts)
+    np.testing.assert_array_equal(tags, tags_after)
+    np.testing.assert_array_equal(lru, lru_after)
+
+
+def test_resolver_walkthrough_known_answer(gpu):
+    with open(os.path.join(GOLDEN, "index_walkthrough.json")) as f:
+        w = json.load(f)
+    tables = dict(
+        source=np.asarray(w["source_table"], np.int32),
+        resident=np.asarray(w["resident_table"], np.int32),
+        hot=np.asarray(w["hot_block_table"], np.int32),
+        tags=np.asarray(w["tags_before"], np.int32),
+        lru=np.asarray([0, 1, 2, 3, 4, 6, 7, 5], np.int64),
+    )
+    positions = np.asarray(w["logical_tokens"], np.int64)
+    plan, tags, lru = _resolve_gpu(gpu, tables, positions, 16, w["page_size"])
+    assert plan.physical_rows.tolist() == w["physical_rows"]
+    assert plan.miss_host_rows.tolist() == w["miss_host_rows"]
+    assert plan.miss_device_rows.tolist() == w["miss_device_rows"]
+    c = w["counts"]
+    assert plan.counts.tolist() == [c["resident_hits"], c["hot_hits"], c["misses"]]
+    assert tags.tolist() == w["tags_after"]
+    expected = oracle.resolve_rows(positions, *[tables[k] for k in ("source", "resident", "hot", "tags", "lru")], 16, 4)
+    _assert_plan(plan, tags, lru, expected)
+
+
+@pytest.mark.parametrize(
+    "seed,length,P,S,n,res_frac",
+    [
+        (0, 97, 4, 64, 40, 0.5),
+        (1, 1000, 16, 512, 300, 0.3),
+        (2, 4096, 16, 2048, 1500, 0.5),
+        (3, 65536, 16, 32768, 20000, 0.5),
+        (4, 131072, 16, 32768, 27808, 0.15),
+        (5, 50, 3, 30, 30, 0.0),
+        (6, 300, 7, 128, 100, 1.0),
+    ],
+)
+def test_resolver_random_matches_oracle(gpu, seed, length, P, S, n, res_frac):
+    tables = resolver_tables(seed, length, P, S, resident_frac=res_frac)
+    positions = random_positions(seed + 100, n, length)
+    expected = oracle.resolve_rows(positions, *[tables[k] for k in ("source", "resident", "hot", "tags", "lru")], length, P)
+    plan, tags, lru = _resolve_gpu(gpu, tables, positions, length, P)
+    _assert_plan(plan, tags, lru, expected)
+    # int32 positions give the same answer
+    plan32, tags32, lru32 = _resolve_gpu(gpu, tables, positions.astype(np.int32), length, P)
+    _assert_plan(plan32, tags32, lru32, expected)
+
+
+def test_resolver_head_columns_and_multistep_trajectory(gpu):
+    from mini_hisparse_amd.row_index import LogicalTopK, resolve_rows
+
+    length, P, S = 3000, 16, 1024
+    tables = resolver_tables(11, length, P, S, resident_frac=0.4, tag_frac=0.3)
+    gpu_t = {k: torch.from_numpy(np.ascontiguousarray(v)).to(gpu) for k, v in tables.items()}
+    cpu_tags, cpu_lru = tables["tags"].copy(), tables["lru"].copy()
+    rng = np.random.default_rng(12)
+    for step in range(6):
+        heads, width = 6, 64
+        sel = [sorted(set(rng.integers(0, length, size=width).tolist())) for _ in range(heads)]
+        union, columns = oracle_union(sel)
+        expected = oracle.resolve_rows(union, tables["source"], tables["resident"], tables["hot"], cpu_tags, cpu_lru, length, P, head_columns=columns)
+        topk = LogicalTopK(torch.from_numpy(union.astype(np.int32)).to(gpu), torch.from_numpy(columns).to(gpu))
+        plan = resolve_rows(topk, gpu_t["source"], gpu_t["resident"], gpu_t["hot"], gpu_t["tags"], gpu_t["lru"], length, P)
+        _assert_plan(plan, gpu_t["tags"].cpu().numpy(), gpu_t["lru"].cpu().numpy(), expected)
+        cpu_tags, cpu_lru = expected[4], expected[5]
+
+
+def test_resolver_row_stats_accumulate(gpu):
+    from mini_hisparse_amd.row_index import LogicalTopK, resolve_rows
+
+    tables = resolver_tables(21, 500, 4, 200)
+    positions = random_positions(22, 120, 500)
+    expected = oracle.resolve_rows(positions, *[tables[k] for k in ("source", "resident", "hot", "tags", "lru")], 500, 4)
+    t = {k: torch.from_numpy(np.ascontiguousarray(v)).to(gpu) for k, v in tables.items()}
+    stats = torch.tensor([10, 20, 30], dtype=torch.int64, device=gpu)
+    resolve_rows(LogicalTopK(torch.from_numpy(positions).to(gpu)), t["source"], t["resident"], t["hot"], t["tags"], t["lru"], 500, 4, row_stats=stats)
+    assert stats.tolist() == [10 + int(expected[3][0]), 20 + int(expected[3][1]), 30 + int(expected[3][2])]
+
+
+# --------------------------------------------------------------------- Quest
+@pytest.mark.parametrize(
+    "dtype,pages,P,kv,g,D,top,sink,length",
+    [
+        (torch.bfloat16, 300, 16, 2, 4, 64, 16, True, None),
+        (torch.bfloat16, 4096, 16, 8, 8, 128, 64, True, None),  # microbench shape
+        (torch.bfloat16, 1000, 16, 4, 7, 128, 64, False, 15990),
+        (torch.float16, 77, 7, 2, 3, 24, 5, True, 535),
+        (torch.float32, 90, 4, 1, 2, 8, 7, True, 357),
+        (torch.bfloat16, 10, 16, 2, 2, 32, 12, True, 150),  # top >= count: every page
+        (torch.bfloat16, 50, 16, 2, 2, 32, 1, True, None),  # top == 1: tail only
+    ],
+)
+def test_quest_pages_match_oracle(gpu, dtype, pages, P, kv, g, D, top, sink, length):
+    from mini_hisparse_amd.selection import quest_selection
+
+    length = length or pages * P
+    lo, hi = quest_bounds(7, pages, P, kv, D, dtype, length)
+    q = torch.randn(kv * g, D, generator=torch.Generator().manual_seed(8)).to(dtype)
+    expected = oracle.quest_pages(q, lo, hi, length, P, top, keep_sink=sink)
+    sel = quest_selection(q.to(gpu), lo.to(gpu), hi.to(gpu), length, P, top, keep_sink=sink)
+    k = expected.shape[1]
+    np.testing.assert_array_equal(sel.device_pages[:, :k].cpu().numpy(), expected)
+    assert sel.positions == pages_to_positions(expected, length, P)
+
+
+def test_quest_reference_known_answer(gpu):
+    """tests/test_selection.py:33-47 of the reference: pages [0, 2], not the mean's page 1."""
+    from mini_hisparse_amd.selection import quest_selection
+
+    k = torch.tensor([[[10.0, 0.0]], [[-10.0, 0.0]], [[1.0, 0.0]], [[1.0, 0.0]], [[0.0, 0.0]]])
+    lo = torch.stack([k[0:2].amin(0), k[2:4].amin(0), k[4:5].amin(0)])
+    hi = torch.stack([k[0:2].amax(0), k[2:4].amax(0), k[4:5].amax(0)])
+    sel = quest_selection(torch.tensor([[1.0, 0.0]], device=gpu), lo.to(gpu), hi.to(gpu), 5, 2, 2, keep_sink=False)
+    assert sel.pages == [0, 2]
+
+
+# -------------------------------------------------------------- union builder
+@pytest.mark.parametrize("pages,P,kv,g,top,length", [(300, 16, 2, 4, 16, None), (77, 7, 2, 3, 5, 535), (10, 16, 2, 2, 12, 150), (4096, 16, 8, 8, 64, None)])
+def test_union_builder_matches_host_adapter(gpu, pages, P, kv, g, top, length):
+    from mini_hisparse_amd.selection import quest_selection
+
+    length = length or pages * P
+    lo, hi = quest_bounds(17, pages, P, kv, 32, torch.bfloat16, length)
+    q = torch.randn(kv * g, 32, generator=torch.Generator().manual_seed(18)).to(torch.bfloat16)
+    sel = quest_selection(q.to(gpu), lo.to(gpu), hi.to(gpu), length, P, top)
+    topk = sel.logical_topk(torch.device(gpu))
+    union, columns = oracle_union(sel.positions)
+    n = int(topk.union_count.item())
+    assert n == len(union)
+    pos = topk.positions.cpu().numpy()
+    np.testing.assert_array_equal(pos[:n], union)
+    assert (pos[n:] == -1).all()
+    hc = topk.head_columns.cpu().numpy()
+    np.testing.assert_array_equal(hc[:, : columns.shape[1]], columns)
+    assert (hc[:, columns.shape[1] :] == -1).all()
+    groups = group_entries(columns, kv)
+    counts = topk.entries.counts.cpu().numpy()
+    for k, (cols, masks) in enumerate(groups):
+        assert counts[k] == len(cols)
+        np.testing.assert_array_equal(topk.entries.columns[k, : len(cols)].cpu().numpy(), cols)
+        np.testing.assert_array_equal(topk.entries.masks[k, : len(cols)].cpu().numpy().astype(np.int64), masks)
+
+
+# --------------------------------------------------------------------- gather
+@pytest.mark.parametrize("dtype,P,kv,D", [(torch.bfloat16, 16, 8, 128), (torch.float32, 4, 1, 8), (torch.float16, 7, 2, 24), (torch.bfloat16, 16, 4, 128)])
+def test_gather_copies_planned_rows(gpu, dtype, P, kv, D):
+    from mini_hisparse_amd.row_index import RowPlan
+    from mini_hisparse_amd.row_kernels import MappedHost, gather_rows
+
+    host_blocks, dev_blocks = 40, 30
+    host = make_pool(host_blocks, P, kv, D, dtype, seed=31).pin_memory()
+    pool_cpu = make_pool(dev_blocks, P, kv, D, dtype, seed=32)
+    rng = np.random.default_rng(33)
+    m = 57
+    hrows = rng.choice(host_blocks * P, size=m, replace=False)
+    drows = rng.choice(dev_blocks * P, size=m, replace=False)
+    hplan = np.full(m + 20, -1, np.int64)
+    dplan = np.full(m + 20, -1, np.int64)
+    hplan[:m], dplan[:m] = hrows, drows
+    expected = pool_cpu.clone()
+    oracle.gather_rows(host, expected, hplan, dplan, P)
+    pool = pool_cpu.to(gpu)
+    plan = RowPlan(None, torch.from_numpy(hplan).to(gpu), torch.from_numpy(dplan).to(gpu), None)
+    gather_rows(MappedHost(host), pool, plan, cfg(P, kv, D))
+    torch.cuda.synchronize()
+    assert torch.equal(pool.cpu(), expected)
+
+
+# ---------------------------------------------- group attention = row attention
+@pytest.mark.parametrize("P,kv,g,D,pages,top", [(16, 8, 8, 128, 512, 64), (16, 4, 7, 128, 300, 32), (7, 2, 3, 24, 60, 6)])
+def test_group_attention_matches_per_head_rows(gpu, P, kv, g, D, pages, top):
+    from mini_hisparse_amd.row_index import resolve_rows
+    from mini_hisparse_amd.row_kernels import attend_groups, attend_rows
+    from mini_hisparse_amd.selection import quest_selection
+
+    length = pages * P - 3
+    heads = kv * g
+    lo, hi = quest_bounds(41, pages, P, kv, D, torch.bfloat16, length)
+    q = torch.randn(heads, D, generator=torch.Generator().manual_seed(42)).to(torch.bfloat16).to(gpu)
+    sel = quest_selection(q, lo.to(gpu), hi.to(gpu), length, P, top)
+    topk = sel.logical_topk(torch.device(gpu))
+    # every page resident at block = page, so physical rows are the logical tokens
+    resident = torch.arange(pages, dtype=torch.int32, device=gpu)
+    source = torch.arange(pages, dtype=torch.int32, device=gpu)
+    hot = torch.zeros(1, dtype=torch.int32, device=gpu)
+    tags = torch.full((P,), -1, dtype=torch.int32, device=gpu)
+    lru = torch.arange(P, dtype=torch.int64, device=gpu)
+    plan = resolve_rows(topk, source, resident, hot, tags, lru, length, P)
+    pool = make_pool(pages, P, kv, D, torch.bfloat16, seed=43, outliers=True).to(gpu)
+    c = cfg(P, kv, D)
+    by_rows = attend_rows(q, pool, plan.physical_rows, c)
+    by_groups = attend_groups(q, pool, plan.union_physical, topk.entries, c)
+    expected = oracle.row_attention_rows(q.cpu(), pool.cpu(), plan.physical_rows.cpu(), P)
+    _close(by_rows, expected, 2e-2, 1e-2)
+    _close(by_groups, expected, 2e-2, 1e-2)
