@@ -1,0 +1,382 @@
+#!/usr/bin/env python
+"""Sparse decode step benchmark on one MI355X.
+
+Workload ("microbench"): one layer, 8 KV heads x 64 query heads (GQA group 8),
+head_dim 128, page_size 16, 4096 logical pages (65,536 tokens) per request,
+batch 8, bf16.  K/V ~ N(0,1) with 2% of channels scaled x8; Quest top-64 pages
+per query head (sink and tail forced).  Of the selected union rows 50% sit in
+resident pages, 30% in hot slots and 20% miss to pinned host memory.  Inputs
+are seeded and synthetic; they live in HBM / pinned host memory before timing.
+
+A step is the whole hot path for the 8 requests: restore the hot tags/LRU to
+the step's starting state (so every step sees the same 20% misses), Quest
+scorer + top-k, device union, resolver, host->hot gather on the transfer
+stream, group attention.  `value` = decode tokens/s = batch / step time.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+from math import ceil
+
+import numpy as np
+
+METRIC = "decode tokens/s at 1 MI355X; sparse-attn HBM GB/s as % of peak"
+HBM_PEAK_GBS = 8000.0
+
+
+def parse_args():
+    p = argparse.ArgumentParser(description=__doc__)
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--batch", type=int, default=8)
+    p.add_argument("--seed", type=int, default=2024)
+    p.add_argument("--no-cpu-baseline", action="store_true", help="skip the CPU oracle leg")
+    p.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU sample work")
+    return p.parse_args()
+
+
+class Shape:
+    kv_heads = 8
+    heads = 64
+    head_dim = 128
+    page_size = 16
+    pages = 4096
+    top = 64
+    hot_rows = 32768
+    resident_frac = 0.5
+    hot_frac_of_rest = 0.6  # 30% of all union rows
+
+
+def build_workload(args, torch, device):
+    """Seeded synthetic state of the microbench in HBM and pinned host memory."""
+    from mini_hisparse_amd.batched import BatchedSparseDecode, LayerTablesView
+    from mini_hisparse_amd.config import CacheConfig
+    from mini_hisparse_amd.row_kernels import MappedHost
+
+    S = Shape
+    B, P, C, Hkv, D = args.batch, S.page_size, S.pages, S.kv_heads, S.head_dim
+    L = C * P
+    gen = torch.Generator(device=device).manual_seed(args.seed)
+    cpu_gen = torch.Generator().manual_seed(args.seed)
+    scale = torch.ones(Hkv, D)
+    outliers = max(1, round(0.02 * D))
+    for kv in range(Hkv):
+        scale[kv, torch.randperm(D, generator=cpu_gen)[:outliers]] = 8.0
+    scale = scale.to(device)
+    # KV in page layout [B, C, 2, P, Hkv, D]
+    kv_pages = torch.empty((B, C, 2, P, Hkv, D), dtype=torch.bfloat16, device=device)
+    for b in range(B):
+        x = torch.randn((C, 2, P, Hkv, D), generator=gen, device=device)
+        kv_pages[b] = (x * scale).to(torch.bfloat16)
+        del x
+    kmin = [kv_pages[b, :, 0].amin(1).contiguous() for b in range(B)]  # [C, Hkv, D]
+    kmax = [kv_pages[b, :, 0].amax(1).contiguous() for b in range(B)]
+    q = torch.randn((B, S.heads, D), generator=gen, device=device).to(torch.bfloat16)
+    host = torch.empty((B * C, 2, P, Hkv, D), dtype=torch.bfloat16, pin_memory=True)
+    host.copy_(kv_pages.view(B * C, 2, P, Hkv, D))
+    torch.cuda.synchronize()
+
+    cfg_probe = CacheConfig(gpu_pages=1, host_pages=1, page_size=P, kv_heads=Hkv, head_dim=D, device=device, dtype=torch.bfloat16)
+    dec = BatchedSparseDecode(cfg_probe, S.heads, S.top, [L] * B, device=device)
+    dec.select(q, kmin, kmax)
+    torch.cuda.synchronize()
+    positions = dec.positions.cpu().numpy()
+    union_n = dec.union_count.cpu().numpy()
+
+    HB = ceil(S.hot_rows / P)
+    plan = []
+    n_resident_blocks = 0
+    for b in range(B):
+        rng = np.random.default_rng(args.seed + 17 * b)
+        union = positions[b, : union_n[b]].astype(np.int64)
+        upages = np.unique(union // P)
+        res = set(rng.choice(upages, size=int(round(S.resident_frac * len(upages))), replace=False).tolist())
+        res.add(C - 1)  # the active tail page stays resident
+        res = sorted(res)
+        rest = union[~np.isin(union // P, res)]
+        hot_tokens = np.sort(rng.choice(rest, size=int(round(S.hot_frac_of_rest * len(rest))), replace=False))
+        plan.append((res, hot_tokens, rng))
+        n_resident_blocks += len(res)
+    blocks = n_resident_blocks + B * HB
+    pool = torch.empty((blocks, 2, P, Hkv, D), dtype=torch.bfloat16, device=device)
+    perm = np.random.default_rng(args.seed + 1).permutation(B * HB) + n_resident_blocks
+    tags_all = torch.full((B, S.hot_rows), -1, dtype=torch.int32, device=device)
+    lru_all = torch.empty((B, S.hot_rows), dtype=torch.int64, device=device)
+    tables = []
+    next_block = 0
+    stats = {"union_rows": 0, "resident_rows": 0, "hot_rows": 0, "miss_rows": 0}
+    for b, (res, hot_tokens, rng) in enumerate(plan):
+        source = torch.arange(b * C, (b + 1) * C, dtype=torch.int32, device=device)
+        resident = torch.full((C,), -1, dtype=torch.int32, device=device)
+        res_blocks = torch.arange(next_block, next_block + len(res), device=device)
+        res_idx = torch.tensor(res, device=device)
+        resident[res_idx] = res_blocks.to(torch.int32)
+        pool[res_blocks] = kv_pages[b, res_idx]
+        next_block += len(res)
+        hot = torch.from_numpy(perm[b * HB : (b + 1) * HB].astype(np.int32)).to(device)
+        slots = rng.choice(S.hot_rows, size=len(hot_tokens), replace=False)
+        host_rows = (b * C + hot_tokens // P) * P + hot_tokens % P
+        tags = np.full(S.hot_rows, -1, np.int32)
+        tags[slots] = host_rows
+        tags_all[b] = torch.from_numpy(tags).to(device)
+        lru_all[b] = torch.from_numpy(rng.permutation(S.hot_rows)).to(device)
+        slot_t = torch.from_numpy(slots).to(device)
+        phys = hot[slot_t // P].long() * P + slot_t % P
+        tok = torch.from_numpy(hot_tokens).to(device)
+        pool[phys // P, :, phys % P] = kv_pages[b, tok // P, :, tok % P]
+        tables.append(LayerTablesView(source, resident, hot, tags_all[b], lru_all[b]))
+        n = int(union_n[b])
+        n_res = int(np.isin(positions[b, :n] // P, res).sum())
+        stats["union_rows"] += n
+        stats["resident_rows"] += n_res
+        stats["hot_rows"] += len(hot_tokens)
+        stats["miss_rows"] += n - n_res - len(hot_tokens)
+    del kv_pages
+    torch.cuda.synchronize()
+    cfg = CacheConfig(gpu_pages=blocks, host_pages=B * C, page_size=P, kv_heads=Hkv, head_dim=D, device=device, dtype=torch.bfloat16)
+    dec = BatchedSparseDecode(cfg, S.heads, S.top, [L] * B, device=device)
+    return dict(
+        cfg=cfg, dec=dec, q=q, kmin=kmin, kmax=kmax, host=host, alias=MappedHost(host), pool=pool,
+        tables=tables, tags_all=tags_all, lru_all=lru_all, tags0=tags_all.clone(), lru0=lru_all.clone(),
+        stats=stats, length=L,
+    )
+
+
+def run_steps(torch, w, steps, record):
+    """`steps` decode steps; per-stage HIP events when `record`."""
+    dec, device = w["dec"], w["pool"].device
+    compute = torch.cuda.current_stream(device)
+    transfer = w.setdefault("transfer", torch.cuda.Stream(device))
+    row_stats = w.setdefault("row_stats", torch.zeros(3, dtype=torch.int64, device=device))
+    events = []
+    last = w.get("last_use")
+    out = None
+    for _ in range(steps):
+        ev = [torch.cuda.Event(enable_timing=record) for _ in range(8)]
+        w["tags_all"].copy_(w["tags0"])
+        w["lru_all"].copy_(w["lru0"])
+        ev[0].record(compute)
+        dec.select(w["q"], w["kmin"], w["kmax"])
+        ev[1].record(compute)
+        dec.resolve(w["tables"], row_stats=row_stats)
+        ev[2].record(compute)
+        transfer.wait_event(ev[2])
+        if last is not None:
+            transfer.wait_event(last)
+        ev[3].record(transfer)
+        dec.gather(w["alias"], w["pool"], transfer)
+        ev[4].record(transfer)
+        compute.wait_event(ev[4])
+        ev[5].record(compute)
+        out = dec.attend(w["q"], w["pool"])
+        ev[6].record(compute)
+        last = ev[6]
+        events.append(ev)
+    w["last_use"] = last
+    w["out"] = out
+    return events
+
+
+def stage_ms(events):
+    def avg(i, j):
+        return float(np.mean([e[i].elapsed_time(e[j]) for e in events]))
+
+    return {
+        "quest_and_union": avg(0, 1),
+        "resolve": avg(1, 2),
+        "gather": avg(3, 4),
+        "attention": avg(5, 6),
+    }
+
+
+def host_link_gbs(torch, device, nbytes=1 << 30):
+    src = torch.empty(nbytes, dtype=torch.uint8, pin_memory=True)
+    dst = torch.empty(nbytes, dtype=torch.uint8, device=device)
+    dst.copy_(src, non_blocking=True)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(3):
+        dst.copy_(src, non_blocking=True)
+    e1.record()
+    torch.cuda.synchronize()
+    return 3 * nbytes / (e0.elapsed_time(e1) * 1e-3) / 1e9
+
+
+def hbm_copy_gbs(torch, device, nbytes=1 << 30):
+    """Plain device-to-device copy of known size (also the PMC calibration kernel)."""
+    a = torch.empty(nbytes, dtype=torch.uint8, device=device)
+    b = torch.empty_like(a)
+    b.copy_(a)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(5):
+        b.copy_(a)
+    e1.record()
+    torch.cuda.synchronize()
+    return 5 * 2 * nbytes / (e0.elapsed_time(e1) * 1e-3) / 1e9
+
+
+def algorithmic_bytes(w, torch):
+    """Per-launch algorithmic bytes of each kernel (per-unit formulas x units)."""
+    S, dec = Shape, w["dec"]
+    B, e, D = dec.batch, 2, S.head_dim
+    entries = int(w["dec"].entry_counts.sum().item())
+    per_head = int((w["dec"].physical >= 0).sum().item())
+    misses = int(w["dec"].row_counts[:, 2].sum().item())
+    n_union = int(w["dec"].union_count.sum().item())
+    W = dec.width
+    attention = entries * 2 * D * e + 8 * S.heads * W * B + 2 * S.heads * D * e * B
+    attention_per_head = per_head * 2 * D * e + 8 * S.heads * W * B + 2 * S.heads * D * e * B
+    quest = B * (2 * S.pages * S.kv_heads * D * e + S.heads * D * e + S.heads * S.top * 4)
+    resolver = sum(
+        4 * n + 8 * n + 8 * S.hot_rows + 16 * S.hot_rows + 16 * n + 8 * S.heads * W + 24
+        for n in w["dec"].union_count.tolist()
+    )
+    gather = misses * 2 * S.kv_heads * D * e
+    return dict(
+        attention=attention, attention_per_head=attention_per_head, quest=quest,
+        resolver=resolver, gather=gather, entries=entries, misses=misses, union_rows=n_union,
+    )
+
+
+def cpu_baseline(torch, w, budget_s):
+    """The numpy oracle on the host cores: whole requests of the same step."""
+    import oracle
+    from oracle.quest import pages_to_positions
+
+    torch.set_num_threads(1)
+    S, dec = Shape, w["dec"]
+    P, L = S.page_size, w["length"]
+    q = w["q"].cpu()
+    pool = w["pool"].cpu()
+    host = w["host"]
+    tags0, lru0 = w["tags0"].cpu().numpy(), w["lru0"].cpu().numpy()
+    gpu_pages = dec.pages.cpu().numpy()
+    gpu_phys = dec.physical.cpu().numpy()
+    gpu_out = w["out"].float().cpu()
+    done, parity = 0, {"pages_equal": True, "physical_equal": True, "max_abs_err": 0.0}
+    t0 = time.perf_counter()
+    for b in range(dec.batch):
+        t = w["tables"][b]
+        pages = oracle.quest_pages(q[b], w["kmin"][b].cpu(), w["kmax"][b].cpu(), L, P, S.top)
+        positions = pages_to_positions(pages, L, P)
+        union, cols = oracle.from_selection(positions)
+        phys, mh, md, counts, _, _ = oracle.resolve_rows(
+            union, t.source.cpu().numpy(), t.resident.cpu().numpy(), t.hot.cpu().numpy(),
+            tags0[b], lru0[b], L, P, head_columns=cols,
+        )
+        oracle.gather_rows(host, pool, mh, md, P)
+        out = oracle.row_attention_rows(q[b], pool, phys, P)
+        done += 1
+        parity["pages_equal"] &= bool((gpu_pages[b, :, : pages.shape[1]] == pages).all())
+        parity["physical_equal"] &= bool((gpu_phys[b, :, : phys.shape[1]] == phys).all())
+        parity["max_abs_err"] = max(parity["max_abs_err"], float(np.abs(gpu_out[b].double().numpy() - out).max()))
+        if time.perf_counter() - t0 > budget_s:
+            break
+    elapsed = time.perf_counter() - t0
+    return {
+        "value": done / elapsed,
+        "unit": "tokens/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": f"{done} of {dec.batch} requests of one step (Quest scores+top-k, union, resolve, "
+        f"row gather, attention), numpy oracle, 1 thread, {elapsed:.1f} s",
+        "host": platform.processor() or platform.machine(),
+        "host_cpus": os.cpu_count(),
+    }, parity
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on exactly one GPU; --gpus above 1 is not supported "
+                          "(the decode path shards by request, see DESIGN.md)", "n_gpus": args.gpus}))
+        sys.exit(2)
+    import torch
+
+    if not torch.cuda.is_available():
+        print(json.dumps({"error": "no ROCm GPU visible"}))
+        sys.exit(1)
+    device = torch.device("cuda:0")
+    print(f"[bench] building workload (batch {args.batch})", file=sys.stderr, flush=True)
+    w = build_workload(args, torch, device)
+    run_steps(torch, w, args.warmup, record=False)
+    torch.cuda.synchronize()
+    print("[bench] timing", file=sys.stderr, flush=True)
+    t0 = time.perf_counter()
+    events = run_steps(torch, w, args.steps, record=True)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    ms_per_step = elapsed * 1e3 / args.steps
+    stages = stage_ms(events)
+    bytes_ = algorithmic_bytes(w, torch)
+    link = host_link_gbs(torch, device)
+    copy = hbm_copy_gbs(torch, device)
+    att_gbs = bytes_["attention"] / (stages["attention"] * 1e-3) / 1e9
+    kernels = {
+        "attention": {"ms": stages["attention"], "bytes": bytes_["attention"], "GBps": att_gbs,
+                      "frac_hbm_peak": att_gbs / HBM_PEAK_GBS,
+                      "per_head_bytes": bytes_["attention_per_head"]},
+        "quest_and_union": {"ms": stages["quest_and_union"], "bytes": bytes_["quest"],
+                            "GBps": bytes_["quest"] / (stages["quest_and_union"] * 1e-3) / 1e9},
+        "resolve": {"ms": stages["resolve"], "bytes": bytes_["resolver"],
+                    "GBps": bytes_["resolver"] / (stages["resolve"] * 1e-3) / 1e9},
+        "gather": {"ms": stages["gather"], "bytes": bytes_["gather"],
+                   "GBps": bytes_["gather"] / (stages["gather"] * 1e-3) / 1e9,
+                   "host_link_memcpy_GBps": link,
+                   "frac_host_link": bytes_["gather"] / (stages["gather"] * 1e-3) / 1e9 / link},
+    }
+    result = {
+        "metric": METRIC,
+        "value": args.batch / (ms_per_step * 1e-3),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded K/V ~ N(0,1), 2% channels x8; random-init tables)",
+        "config": {
+            "workload": "microbench (BASELINE configs[1]): 1 layer, 64 q / 8 kv heads, head_dim 128, "
+            "page 16, 4096 pages/request, batch 8, Quest top-64, 50% resident / 30% hot / 20% miss",
+            "global_batch": args.batch,
+            "seq_len": w["length"],
+            "parallelism": "none (1 GPU)",
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": att_gbs,
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": att_gbs / HBM_PEAK_GBS,
+            "traffic": None,
+            "kernel": "attend_mfma_kernel + attend_merge_kernel (hs_attend_groups)",
+        },
+        "kernels": kernels,
+        "rows": {**w["stats"], "misses_per_step": bytes_["misses"], "attention_entries": bytes_["entries"]},
+        "hbm_copy_GBps": copy,
+    }
+    if not args.no_cpu_baseline:
+        print("[bench] cpu baseline", file=sys.stderr, flush=True)
+        base, parity = cpu_baseline(torch, w, args.cpu_budget)
+        result["cpu_baseline"] = base
+        result["parity"] = parity
+    else:
+        result["cpu_baseline"] = None
+    print(json.dumps(result))
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,218 @@
+"""One layer of sparse decode for a batch of requests, in a fixed set of launches.
+
+The reference decodes requests one at a time (engine.py:115-128) and, per
+(request, layer), runs ~40 resolver launches, a host sync in the selector and
+a host-built union (selection.py:100, row_index.py:20-31).  Here a layer of B
+requests is:
+
+    hs_quest_topk      scorer + top-k for all B x Hq heads          (compute stream)
+    hs_build_union     unions, head columns, per-KV-head entry lists (compute stream)
+    hs_resolve_rows    one workgroup per request, row_stats fused   (compute stream)
+    hs_gather_rows     all B miss plans, host -> hot rows           (transfer stream)
+    hs_attend_groups   split-K group attention + merge              (compute stream)
+
+with the reference's event ordering (hybrid.py:443, :455-457, :473, :83-85):
+the transfer stream waits for the resolve and for the previous readers of
+the hot rows; attention waits for the gather.  Buffers are allocated once per
+shape, so a step allocates nothing and never reads back to the host.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+from math import ceil
+
+import torch
+
+from . import _lib
+from .selection import selection_width, union_bound
+
+
+@dataclass
+class LayerTablesView:
+    """The per-(request, layer) tables the resolver reads and updates (hybrid.py:45-64)."""
+
+    source: torch.Tensor  # [pages] int32
+    resident: torch.Tensor  # [pages] int32
+    hot: torch.Tensor  # [hot_blocks] int32
+    tags: torch.Tensor  # [hot_rows] int32 (updated)
+    lru: torch.Tensor  # [hot_rows] int64 (updated)
+
+
+class BatchedSparseDecode:
+    """Quest -> union -> resolve -> gather -> attention for B requests of one layer."""
+
+    def __init__(self, config, heads, top_pages, lengths, *, keep_sink=True, device="cuda"):
+        self.config = config
+        self.heads = heads
+        self.kv_heads = config.kv_heads
+        self.groups = heads // config.kv_heads
+        self.top = top_pages
+        self.keep_sink = keep_sink
+        self.device = torch.device(device)
+        self.batch = len(lengths)
+        self._shape(list(lengths))
+
+    def _shape(self, lengths):
+        P, B, dev = self.config.page_size, self.batch, self.device
+        self.lengths = lengths
+        self.counts = [ceil(l / P) for l in lengths]
+        self.capacity = max(union_bound(l, P, self.top, self.heads, self.keep_sink) for l in lengths)
+        self.entry_capacity = max(union_bound(l, P, self.top, self.groups, self.keep_sink) for l in lengths)
+        self.width = max(selection_width(l, P, self.top) for l in lengths)
+        i32, i64 = torch.int32, torch.int64
+        self.pages = torch.empty((B, self.heads, self.top), dtype=i32, device=dev)
+        self.positions = torch.empty((B, self.capacity), dtype=i32, device=dev)
+        self.head_columns = torch.empty((B, self.heads, self.width), dtype=i64, device=dev)
+        self.union_count = torch.empty(B, dtype=i32, device=dev)
+        self.entry_columns = torch.empty((B, self.kv_heads, self.entry_capacity), dtype=i32, device=dev)
+        self.entry_masks = torch.empty((B, self.kv_heads, self.entry_capacity), dtype=i32, device=dev)
+        self.entry_counts = torch.empty((B, self.kv_heads), dtype=i32, device=dev)
+        self.status = torch.zeros(1, dtype=i32, device=dev)
+        self.physical = torch.empty((B, self.heads, self.width), dtype=i64, device=dev)
+        self.union_physical = torch.empty((B, self.capacity), dtype=i64, device=dev)
+        self.miss_host = torch.empty((B, self.capacity), dtype=i64, device=dev)
+        self.miss_device = torch.empty((B, self.capacity), dtype=i64, device=dev)
+        self.row_counts = torch.empty((B, 3), dtype=i64, device=dev)
+        lib = _lib.load()
+        self.quest_ws_bytes = lib.hs_quest_workspace_bytes(B, self.heads, max(self.counts))
+        self.quest_ws = torch.empty(self.quest_ws_bytes, dtype=torch.uint8, device=dev)
+        self.resolve_ws_bytes = 0
+        self.max_tables = None
+        self.attend_ws_bytes = lib.hs_attend_workspace_bytes(
+            _lib.HS_DTYPE_BF16, B, self.heads, self.kv_heads, self.config.head_dim, self.entry_capacity
+        )
+        self.attend_ws_bytes = max(
+            self.attend_ws_bytes,
+            lib.hs_attend_workspace_bytes(_lib.HS_DTYPE_F32, B, self.heads, self.kv_heads, self.config.head_dim, self.entry_capacity),
+        )
+        self.attend_ws = torch.empty(self.attend_ws_bytes, dtype=torch.uint8, device=dev)
+        self._len_arr = (ctypes.c_int64 * B)(*lengths)
+        self._count_arr = (ctypes.c_int64 * B)(*self.counts)
+
+    def set_lengths(self, lengths):
+        if list(lengths) != self.lengths:
+            self._shape(list(lengths))
+
+    # -- stages ------------------------------------------------------------
+    def select(self, queries, minimums, maximums, stream=None):
+        """Quest scorer + top-k and the device union for all B requests."""
+        B = self.batch
+        q = queries.float().contiguous()
+        lib = _lib.load()
+        s = stream.cuda_stream if stream is not None else _lib.stream_handle(self.device)
+        lo = (ctypes.c_void_p * B)(*[t.data_ptr() for t in minimums])
+        hi = (ctypes.c_void_p * B)(*[t.data_ptr() for t in maximums])
+        _lib.check(
+            lib.hs_quest_topk(
+                q.data_ptr(), q.stride(0), q.stride(1), int(queries.dtype in (torch.bfloat16, torch.float16)),
+                lo, hi, _lib.dtype_code(minimums[0].dtype), self._count_arr, B, self.heads,
+                self.kv_heads, q.shape[2], self.top, int(self.keep_sink), self.pages.data_ptr(),
+                self.pages.stride(0), self.quest_ws.data_ptr(), self.quest_ws_bytes, s,
+            ),
+            "hs_quest_topk",
+        )
+        _lib.check(
+            lib.hs_build_union(
+                self.pages.data_ptr(), self.pages.stride(0), self.top, self._len_arr,
+                self.config.page_size, B, self.heads, self.kv_heads, self.positions.data_ptr(),
+                self.capacity, self.head_columns.data_ptr(), self.width, self.union_count.data_ptr(),
+                self.entry_columns.data_ptr(), self.entry_masks.data_ptr(), self.entry_capacity,
+                self.entry_counts.data_ptr(), self.status.data_ptr(), s,
+            ),
+            "hs_build_union",
+        )
+
+    def resolve(self, tables, row_stats=None, stream=None):
+        """One resolver launch over B (request, layer) tables; counts land in row_counts."""
+        B, P = self.batch, self.config.page_size
+        lib = _lib.load()
+        descs = (_lib.ResolveDesc * B)()
+        total = 0
+        for b, t in enumerate(tables):
+            d = descs[b]
+            d.positions = self.positions[b].data_ptr()
+            d.n = self.capacity
+            d.positions_i64 = 0
+            d.head_columns = self.head_columns[b].data_ptr()
+            d.heads, d.width = self.heads, self.width
+            d.hc_stride_h, d.hc_stride_w = self.head_columns.stride(1), 1
+            d.source, d.resident = t.source.data_ptr(), t.resident.data_ptr()
+            d.n_pages = t.source.numel()
+            d.hot, d.hot_blocks = t.hot.data_ptr(), t.hot.numel()
+            d.tags, d.lru, d.hot_rows = t.tags.data_ptr(), t.lru.data_ptr(), t.tags.numel()
+            d.length, d.page_size = self.lengths[b], P
+            d.physical = self.physical[b].data_ptr()
+            d.union_physical = self.union_physical[b].data_ptr()
+            d.miss_host_rows = self.miss_host[b].data_ptr()
+            d.miss_device_rows = self.miss_device[b].data_ptr()
+            d.counts = self.row_counts[b].data_ptr()
+            d.row_stats = _lib.ptr(row_stats)
+            total += lib.hs_resolve_workspace_bytes(self.capacity, self.lengths[b], d.n_pages, d.hot_rows)
+        if total > self.resolve_ws_bytes:
+            self.resolve_ws = torch.empty(total, dtype=torch.uint8, device=self.device)
+            self.resolve_ws_bytes = total
+        s = stream.cuda_stream if stream is not None else _lib.stream_handle(self.device)
+        _lib.check(lib.hs_resolve_rows_batched(descs, B, self.resolve_ws.data_ptr(), self.resolve_ws_bytes, s), "hs_resolve_rows_batched")
+
+    def gather(self, host_alias, pool, stream, grid_x=0):
+        """All B miss plans in one launch on `stream` (reads host memory directly)."""
+        B, cfg = self.batch, self.config
+        lib = _lib.load()
+        hosts = (ctypes.c_void_p * B)(*([host_alias.data_ptr()] * B))
+        mh = (ctypes.c_void_p * B)(*[self.miss_host[b].data_ptr() for b in range(B)])
+        md = (ctypes.c_void_p * B)(*[self.miss_device[b].data_ptr() for b in range(B)])
+        mc = (ctypes.c_void_p * B)(*[self.row_counts[b, 2:].data_ptr() for b in range(B)])
+        ns = (ctypes.c_int64 * B)(*([self.capacity] * B))
+        row_bytes = cfg.kv_heads * cfg.head_dim * pool.element_size()
+        _lib.check(
+            lib.hs_gather_rows_batched(hosts, pool.data_ptr(), mh, md, mc, ns, B, cfg.page_size, row_bytes, grid_x, stream.cuda_stream),
+            "hs_gather_rows_batched",
+        )
+
+    def attend(self, queries, pool, out=None, stream=None):
+        """Group attention over the deduplicated rows of every (request, KV head)."""
+        cfg = self.config
+        q = queries if queries.dtype == pool.dtype else queries.to(pool.dtype)
+        q = q.contiguous()
+        if out is None:
+            out = torch.empty_like(q)
+        lib = _lib.load()
+        s = stream.cuda_stream if stream is not None else _lib.stream_handle(self.device)
+        _lib.check(
+            lib.hs_attend_groups(
+                q.data_ptr(), q.stride(0), q.stride(1), pool.data_ptr(), _lib.dtype_code(pool.dtype),
+                cfg.page_size, cfg.kv_heads, cfg.head_dim, pool.shape[0] * cfg.page_size,
+                self.union_physical.data_ptr(), self.union_physical.stride(0),
+                self.entry_columns.data_ptr(), self.entry_masks.data_ptr(),
+                self.entry_columns.stride(0), self.entry_columns.stride(1), self.entry_counts.data_ptr(),
+                self.entry_capacity, self.batch, self.heads, out.data_ptr(), out.stride(0), out.stride(1),
+                self.attend_ws.data_ptr(), self.attend_ws_bytes, s,
+            ),
+            "hs_attend_groups",
+        )
+        return out
+
+    def step(self, queries, minimums, maximums, tables, pool, host_alias, transfer, *, row_stats=None, last_use=None):
+        """The whole layer; returns (out, ready_event, done_event).
+
+        ``last_use`` (optional event) is the previous reader of the hot rows;
+        the gather waits for it, as hybrid.py:457 does.
+        """
+        compute = torch.cuda.current_stream(self.device)
+        self.select(queries, minimums, maximums)
+        self.resolve(tables, row_stats=row_stats)
+        resolved = torch.cuda.Event()
+        resolved.record(compute)
+        transfer.wait_event(resolved)
+        if last_use is not None:
+            transfer.wait_event(last_use)
+        self.gather(host_alias, pool, transfer)
+        ready = torch.cuda.Event()
+        ready.record(transfer)
+        compute.wait_event(ready)
+        out = self.attend(queries, pool)
+        done = torch.cuda.Event()
+        done.record(compute)
+        return out, ready, done

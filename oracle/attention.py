@@ -37,7 +37,6 @@ def _softmax_weighted(scores, valid, values):
 def row_attention_rows(query, pool, rows, page_size):
     """query [Hq, D]; pool [blocks, 2, P, Hkv, D]; rows [Hq, W] or [W] (shared) -> [Hq, D] float64."""
     q = _f64(query)
-    pool = _f64(pool)
     rows = np.asarray(rows.cpu() if hasattr(rows, "cpu") else rows, dtype=np.int64)
     heads, dim = q.shape
     kv_heads = pool.shape[3]
@@ -46,8 +45,16 @@ def row_attention_rows(query, pool, rows, page_size):
     kv_of = np.arange(heads) // (heads // kv_heads)
     safe = np.clip(rows, 0, None)
     blocks, offsets = safe // page_size, safe % page_size
-    k = pool[blocks, 0, offsets, kv_of[:, None]]  # [Hq, W, D]
-    v = pool[blocks, 1, offsets, kv_of[:, None]]
+    if hasattr(pool, "detach"):  # gather in the storage dtype first, then widen
+        import torch
+
+        bi, oi, ki = (torch.from_numpy(np.ascontiguousarray(x)) for x in (blocks, offsets, np.broadcast_to(kv_of[:, None], blocks.shape)))
+        k = _f64(pool[bi, 0, oi, ki])  # [Hq, W, D]
+        v = _f64(pool[bi, 1, oi, ki])
+    else:
+        pool = np.asarray(pool, dtype=np.float64)
+        k = pool[blocks, 0, offsets, kv_of[:, None]]
+        v = pool[blocks, 1, offsets, kv_of[:, None]]
     scores = (k * q[:, None, :]).sum(-1) * dim**-0.5
     return _softmax_weighted(scores, rows >= 0, v)
 
