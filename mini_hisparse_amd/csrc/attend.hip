@@ -22,6 +22,7 @@
 // multiple of 8) use a VALU kernel with the same entry sources.  Both write
 // split-K partials (m, l, acc) that `attend_merge_kernel` combines.
 #include <float.h>
+#include <stdlib.h>
 #include <math.h>
 
 #include "hs_common.h"
@@ -117,7 +118,12 @@ __device__ __forceinline__ float from_bits(unsigned short v) {
   else return f16_bits_to_f32(v);
 }
 
-// One workgroup (4 waves) per (split, KV head x head chunk, request).
+// One workgroup (4 waves) per (split, KV head x head chunk, request).  The
+// split's entries (K element offset, head mask) are staged in LDS once; each
+// wave then walks tiles w, w+4, ... of 32 entries, loading the next tile's K
+// fragments and V rows into registers while the current tile computes.
+constexpr int ACH = 512;  // entries per workgroup (chunk) of the MFMA kernel
+
 template <int DT, int DP>
 __global__ __launch_bounds__(256) void attend_mfma_kernel(AttendArgs a) {
   constexpr int NT = DP / 16;   // PV M-tiles over d
@@ -130,8 +136,8 @@ __global__ __launch_bounds__(256) void attend_mfma_kernel(AttendArgs a) {
   constexpr int MERGE_BYTES = 4 * 16 * DP * 4;
   constexpr int SMEM = VS_BYTES > MERGE_BYTES ? VS_BYTES : MERGE_BYTES;
   __shared__ __attribute__((aligned(16))) unsigned char smem[SMEM];
-  __shared__ int64_t s_phys[4][32];
-  __shared__ uint32_t s_mask[4][32];
+  __shared__ int64_t s_koff[ACH];
+  __shared__ uint32_t s_mask[ACH];
   __shared__ float s_m[4][16], s_l[4][16];
 
   unsigned short* vs_all = reinterpret_cast<unsigned short*>(smem);
@@ -145,6 +151,23 @@ __global__ __launch_bounds__(256) void attend_mfma_kernel(AttendArgs a) {
   const int64_t D = a.D, P = a.P, Hkv = a.Hkv;
   const unsigned short* pool = static_cast<const unsigned short*>(a.pool);
   unsigned short* vs = vs_all + wave * 32 * RS;
+
+  const int64_t E = entry_count(a, b, k);
+  const int64_t e0 = split * a.chunk;
+  int64_t e1 = e0 + a.chunk;
+  if (e1 > E) e1 = E;
+  const int cnt = e1 > e0 ? static_cast<int>(e1 - e0) : 0;
+  for (int i = threadIdx.x; i < ACH; i += 256) {
+    int64_t koff = -1;
+    uint32_t mk = 0;
+    if (i < cnt) {
+      int64_t ph;
+      entry_at(a, b, k, e0 + i, ph, mk);
+      if (ph >= 0) koff = k_offset(ph, k, P, Hkv, D);
+    }
+    s_koff[i] = koff;
+    s_mask[i] = mk;
+  }
 
   // Q^T fragments: lane holds Q[head hh][d = 32kk + 8j .. +8]
   u32x4 qf[KK];
@@ -163,48 +186,47 @@ __global__ __launch_bounds__(256) void attend_mfma_kernel(AttendArgs a) {
 #pragma unroll
   for (int mt = 0; mt < NT; ++mt) acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
   float m_run = -INFINITY, l_run = 0.f;
-
-  const int64_t E = entry_count(a, b, k);
-  const int64_t e0 = split * a.chunk;
-  int64_t e1 = e0 + a.chunk;
-  if (e1 > E) e1 = E;
   const int64_t vplane = P * Hkv * D;
   const uint32_t hbit_shift = static_cast<uint32_t>(hh);
+  __syncthreads();
 
-  for (int64_t base = e0 + 32 * wave; base < e1; base += 128) {
-    if (lane < 32) {
-      int64_t ph = -1;
-      uint32_t mk = 0;
-      const int64_t e = base + lane;
-      if (e < e1) entry_at(a, b, k, e, ph, mk);
-      s_phys[wave][lane] = ph;
-      s_mask[wave][lane] = mk;
-    }
-    wave_sync();
-
-    // K rows as the A operand: lane holds K[row 16rt + c][d = 32kk + 8j .. +8]
-    u32x4 kf[2][KK];
+  const int ntiles = (cnt + 31) / 32;
+  // K fragments (A operand: lane holds K[row 16rt + c][d = 32kk + 8j .. +8]) and the
+  // V rows this lane stages (row vi*RPI + lane/LPR, d = 8*(lane%LPR) .. +8) of tile t
+  auto load_tile = [&](int t, u32x4 (&kf)[2][KK], u32x4 (&vr)[VI]) {
 #pragma unroll
     for (int rt = 0; rt < 2; ++rt) {
-      const int64_t ph = s_phys[wave][16 * rt + c];
-      const unsigned short* kp = pool + (ph >= 0 ? k_offset(ph, k, P, Hkv, D) : 0);
+      const int li = 32 * t + 16 * rt + c;
+      const int64_t koff = li < ACH ? s_koff[li] : -1;
 #pragma unroll
       for (int kk = 0; kk < KK; ++kk) {
         const int d0 = 32 * kk + 8 * j;
         u32x4 v = {0u, 0u, 0u, 0u};
-        if (ph >= 0 && d0 < D) v = load16(kp + d0);
+        if (koff >= 0 && d0 < D) v = load16(pool + koff + d0);
         kf[rt][kk] = v;
       }
     }
-    // V rows into LDS, 16 bytes per lane
+#pragma unroll
+    for (int vi = 0; vi < VI; ++vi) {
+      const int li = 32 * t + vi * RPI + lane / LPR;
+      const int cc = lane % LPR;
+      const int64_t koff = li < ACH ? s_koff[li] : -1;
+      u32x4 v = {0u, 0u, 0u, 0u};
+      if (koff >= 0 && 8 * cc < D) v = load16(pool + koff + vplane + 8 * cc);
+      vr[vi] = v;
+    }
+  };
+
+  u32x4 kf[2][KK], vr[VI];
+  if (wave < ntiles) load_tile(wave, kf, vr);
+  for (int t = wave; t < ntiles; t += 4) {
+    u32x4 kn[2][KK], vn[VI];
+    load_tile(t + 4 < ntiles ? t + 4 : ACH / 32, kn, vn);  // past the end: every lane masked
+    // V rows of this tile into LDS
 #pragma unroll
     for (int vi = 0; vi < VI; ++vi) {
       const int row = vi * RPI + lane / LPR;
-      const int cc = lane % LPR;
-      const int64_t ph = s_phys[wave][row];
-      u32x4 v = {0u, 0u, 0u, 0u};
-      if (ph >= 0 && 8 * cc < D) v = load16(pool + k_offset(ph, k, P, Hkv, D) + vplane + 8 * cc);
-      *reinterpret_cast<u32x4*>(vs + row * RS + 8 * cc) = v;
+      *reinterpret_cast<u32x4*>(vs + row * RS + 8 * (lane % LPR)) = vr[vi];
     }
 
     // S^T[row][head] = K Q^T
@@ -224,7 +246,7 @@ __global__ __launch_bounds__(256) void attend_mfma_kernel(AttendArgs a) {
     for (int rt = 0; rt < 2; ++rt) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const uint32_t mk = s_mask[wave][16 * rt + 4 * j + i];
+        const uint32_t mk = s_mask[32 * t + 16 * rt + 4 * j + i];
         const bool valid = hh < 32 && ((mk >> hbit_shift) & 1u);
         const float s = valid ? st[rt][i] * a.scale : -INFINITY;
         sv[rt][i] = s;
@@ -276,6 +298,12 @@ __global__ __launch_bounds__(256) void attend_mfma_kernel(AttendArgs a) {
       acc[mt] = mfma16x16x32<DT>(vf, pf, acc[mt]);
     }
     wave_sync();  // all reads of this tile done before the next overwrites it
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+      for (int kk = 0; kk < KK; ++kk) kf[rt][kk] = kn[rt][kk];
+#pragma unroll
+    for (int vi = 0; vi < VI; ++vi) vr[vi] = vn[vi];
   }
 
   // per-wave totals over the four lane groups that share a head
@@ -426,13 +454,18 @@ static Plan plan_attend(int dtype, int64_t B, int64_t Hq, int64_t Hkv, int64_t D
   if (p.mfma) {
     p.dp = D <= 32 ? 32 : D <= 64 ? 64 : D <= 128 ? 128 : 256;
     p.head_chunks = static_cast<int>(ceil_div(g, 16));
+    // entries per workgroup: enough workgroups to cover the chip ~3 times,
+    // at most ACH (the LDS entry list), at least 128
     const int64_t groups = B * Hkv * p.head_chunks;
-    int64_t splits = ceil_div(2048, groups);
-    const int64_t cap = ceil_div(max_entries, 128);
-    if (splits > cap) splits = cap;
-    if (splits < 1) splits = 1;
-    p.chunk = ceil_div(ceil_div(max_entries, splits), 32) * 32;
-    if (p.chunk < 32) p.chunk = 32;
+    int64_t chunk = ceil_div(ceil_div(groups * max_entries, 768), 32) * 32;
+    static const int64_t forced = [] {
+      const char* env = getenv("HS_ATTEND_CHUNK");
+      return env ? atoll(env) : 0;
+    }();
+    if (forced > 0) chunk = ceil_div(forced, 32) * 32;
+    if (chunk > ACH) chunk = ACH;
+    if (chunk < 128) chunk = 128;
+    p.chunk = chunk;
     p.splits = ceil_div(max_entries, p.chunk);
     if (p.splits < 1) p.splits = 1;
   } else {
