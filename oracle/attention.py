@@ -48,7 +48,7 @@ def row_attention_rows(query, pool, rows, page_size):
     if hasattr(pool, "detach"):  # gather in the storage dtype first, then widen
         import torch
 
-        bi, oi, ki = (torch.from_numpy(np.ascontiguousarray(x)) for x in (blocks, offsets, np.broadcast_to(kv_of[:, None], blocks.shape)))
+        bi, oi, ki = (torch.from_numpy(np.array(x, dtype=np.int64)) for x in (blocks, offsets, np.broadcast_to(kv_of[:, None], blocks.shape)))
         k = _f64(pool[bi, 0, oi, ki])  # [Hq, W, D]
         v = _f64(pool[bi, 1, oi, ki])
     else:

@@ -79,7 +79,7 @@ def pages_to_positions(pages, length, page_size):
     """Selection.from_pages canonicalisation (selection.py:43-60, 30-39): per head, the
     sorted token set of its pages clipped to ``length``."""
     rows = []
-    for row in np.asarray(pages).tolist():
+    for row in pages.tolist() if hasattr(pages, "tolist") else pages:
         tokens = sorted(
             {t for p in row for t in range(p * page_size, min((p + 1) * page_size, length))}
         )
