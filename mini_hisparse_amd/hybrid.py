@@ -371,7 +371,10 @@ class HybridKVCache:
             self.storage.wait(self.storage.transfer, self.allocator.slots[block].fence)
             self.allocator.bind(block, (request_id, layer, -i - 1))
         tables.blocks = blocks
-        tables.hot.copy_(torch.tensor(blocks, dtype=torch.int32, device=self.device))
+        staged = torch.tensor(blocks, dtype=torch.int32)
+        if self.storage.cuda:  # pinned staging: no host synchronisation on the decode path
+            staged = staged.pin_memory()
+        tables.hot.copy_(staged, non_blocking=self.storage.cuda)
         tables.ready = self.storage.event(self.storage.transfer)
         self.storage.stats["hot_region_allocations"] += 1
         self._unpin_clean_pages(group)
