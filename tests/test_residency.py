@@ -27,6 +27,16 @@ def make(device, pages=7, watermark=0, window=64):
     return make_cache(config, HotConfig(4, 4, resident_window_pages=window, transition_watermark=watermark))
 
 
+def spin_cycles(ms):
+    """Cycle count for torch's spin kernel that keeps a stream busy for about ``ms``."""
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    torch.cuda._sleep(1_000_000)
+    end.record()
+    end.synchronize()
+    return int(1_000_000 * ms / max(start.elapsed_time(end), 1e-3))
+
+
 def write(cache, name, count):
     k, v = [torch.randn(count, 1, 8, device=cache.device) for _ in range(2)]
     cache.write(name, 0, k, v)
@@ -231,12 +241,19 @@ def test_pending_mirror_is_not_clean_and_policy_tick_does_not_wait():
 def test_gpu_page_is_not_unpinned_before_its_d2h_event_completes():
     if not gpu_available():
         pytest.skip("no ROCm GPU")
+    # the same writes once on a scratch cache, so first-launch code loading of
+    # every kernel on this path is done before the timed stall below
+    warm = make("cuda:0", pages=8)
+    warm.reserve("w", 64, 1)
+    write(warm, "w", 12)
+    warm.transition_to_host("w", 0)
+    warm.storage.synchronize()
     cache = make("cuda:0", pages=8)
     cache.reserve("a", 64, 1)
     k, v = [torch.randn(12, 1, 8, device=cache.device) for _ in range(2)]
     cache.storage.synchronize()
     with torch.cuda.stream(cache.storage.transfer):
-        torch.cuda._sleep(100_000_000)
+        torch.cuda._sleep(spin_cycles(1000.0))  # the transfer stream stays busy for ~1 s
     cache.write("a", 0, k, v)
     page = cache.storage.pages["a", 0, 0]
     cache.transition_to_host("a", 0)
