@@ -110,6 +110,126 @@ __global__ __launch_bounds__(QT) void quest_score_kernel(QuestArgs a) {
   for (int hl = 0; hl < nh; ++hl) a.scores[(b * a.Hq + h0 + hl) * a.cmax + p] = acc[hl];
 }
 
+// LDS-tiled scorer for the common shapes.  One workgroup scores QS_PAGES pages
+// of one KV head for a chunk of up to QHEADS query heads.  The pages' lower and
+// upper bound rows (D elements each, 2 KB apart in HBM for Hkv = 8, D = 128
+// bf16) are staged in LDS with full-line loads (consecutive lanes read
+// consecutive 16-byte units, every unit of a fetched line is used); then lane
+// l of wave w scores page l for query heads 2w and 2w+1 of the chunk, reading
+// its row from LDS (row stride padded by 16 bytes: conflict-free 16-byte
+// reads) and the query values as wave-wide broadcasts.  The per-score
+// arithmetic is that of quest_score_kernel: d ascending, one float32 rounding
+// per step.
+constexpr int QS_PAGES = 64;
+constexpr int QS_UNITS = 8;                  // 16-byte units per thread per bound
+constexpr int64_t QS_MAX_ROW_BYTES = QS_UNITS * QT * 16 / QS_PAGES;  // 512
+
+__host__ __device__ constexpr int64_t qs_lds_bytes(int64_t row_bytes, int64_t D) {
+  return 2 * QS_PAGES * (row_bytes + 16) + QHEADS * D * 4;
+}
+
+template <int DT, bool FUSED>
+__global__ __launch_bounds__(QT) void quest_score_tile_kernel(QuestArgs a) {
+#pragma clang fp contract(off)
+  extern __shared__ __attribute__((aligned(16))) unsigned char qs_smem[];
+  constexpr int ESZ = DT == HS_DTYPE_F32 ? 4 : 2;
+  constexpr int EPV = 16 / ESZ;  // elements per 16-byte unit
+  const int64_t b = blockIdx.z;
+  const int64_t hchunks = (a.g + QHEADS - 1) / QHEADS;
+  const int64_t kv = blockIdx.y / hchunks, hc = blockIdx.y - kv * hchunks;
+  const int64_t count = a.count[b];
+  const int64_t p0 = static_cast<int64_t>(blockIdx.x) * QS_PAGES;
+  if (a.top >= count || p0 >= count) return;
+  const int64_t D = a.D, Hkv = a.Hkv;
+  const int64_t rb = D * ESZ, rs = rb + 16, upr = rb / 16;
+  unsigned char* tlo = qs_smem;
+  unsigned char* thi = qs_smem + QS_PAGES * rs;
+  float* sq = reinterpret_cast<float*>(qs_smem + 2 * QS_PAGES * rs);  // [QHEADS][D]
+  int64_t nh = a.g - hc * QHEADS;
+  if (nh > QHEADS) nh = QHEADS;
+  const int64_t h0 = kv * a.g + hc * QHEADS;
+  for (int64_t i = threadIdx.x; i < QHEADS * D; i += QT) {
+    const int64_t hl = i / D, d = i - hl * D;
+    sq[i] = hl < nh ? a.q[b * a.q_sb + (h0 + hl) * a.q_sh + d] : 0.f;
+  }
+  int64_t npg = count - p0;
+  if (npg > QS_PAGES) npg = QS_PAGES;
+  const char* lo = static_cast<const char*>(a.kmin[b]);
+  const char* hi = static_cast<const char*>(a.kmax[b]);
+  // 32-bit tile indexing: at most QS_PAGES * 32 units per bound
+  const uint32_t units = static_cast<uint32_t>(npg * upr), upr32 = static_cast<uint32_t>(upr);
+  const uint32_t rb32 = static_cast<uint32_t>(rb), rs32 = static_cast<uint32_t>(rs);
+  const char* lo_t = lo + (p0 * Hkv + kv) * rb;
+  const char* hi_t = hi + (p0 * Hkv + kv) * rb;
+  const uint32_t gstride = static_cast<uint32_t>(Hkv) * rb32;  // bytes between consecutive pages
+  // every thread issues all of its loads before the first LDS store; a unit
+  // past the tile reloads unit 0 (in bounds) and is not stored
+  u32x4 L[QS_UNITS], U[QS_UNITS];
+#pragma unroll
+  for (int k = 0; k < QS_UNITS; ++k) {
+    uint32_t u = threadIdx.x + static_cast<uint32_t>(k) * QT;
+    if (u >= units) u = 0;
+    const uint32_t r = u / upr32, c = u - r * upr32;
+    const uint64_t off = static_cast<uint64_t>(r) * gstride + c * 16u;
+    L[k] = *reinterpret_cast<const u32x4*>(lo_t + off);
+    U[k] = *reinterpret_cast<const u32x4*>(hi_t + off);
+  }
+#pragma unroll
+  for (int k = 0; k < QS_UNITS; ++k) {
+    const uint32_t u = threadIdx.x + static_cast<uint32_t>(k) * QT;
+    const uint32_t r = u / upr32, c = u - r * upr32;
+    if (u < units) {
+      *reinterpret_cast<u32x4*>(tlo + r * rs32 + c * 16u) = L[k];
+      *reinterpret_cast<u32x4*>(thi + r * rs32 + c * 16u) = U[k];
+    }
+  }
+  __syncthreads();
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int hA = 2 * wave, hB = 2 * wave + 1;
+  if (lane >= npg || hA >= nh) return;  // no barrier follows
+  const float* qa = sq + hA * D;
+  const float* qb = sq + hB * D;
+  const unsigned char* rlo = tlo + lane * rs;
+  const unsigned char* rhi = thi + lane * rs;
+  float accA = 0.f, accB = 0.f;
+  auto step = [&](float qv, float l, float u, float& acc) {
+    const float bound = qv >= 0.f ? u : l;
+    if constexpr (FUSED) {
+      acc = __builtin_fmaf(qv, bound, acc);
+    } else {
+      const float prod = qv * bound;
+      acc = acc + prod;
+    }
+  };
+  for (int64_t d0 = 0; d0 < D; d0 += EPV) {
+    const u32x4 Lv = *reinterpret_cast<const u32x4*>(rlo + d0 * ESZ);
+    const u32x4 Uv = *reinterpret_cast<const u32x4*>(rhi + d0 * ESZ);
+#pragma unroll
+    for (int e = 0; e < EPV; ++e) {
+      float l, u;
+      if constexpr (DT == HS_DTYPE_F32) {
+        l = __uint_as_float(Lv[e]);
+        u = __uint_as_float(Uv[e]);
+      } else {
+        const unsigned short lb = static_cast<unsigned short>(Lv[e >> 1] >> (16 * (e & 1)));
+        const unsigned short ub = static_cast<unsigned short>(Uv[e >> 1] >> (16 * (e & 1)));
+        if constexpr (DT == HS_DTYPE_BF16) {
+          l = bf16_bits_to_f32(lb);
+          u = bf16_bits_to_f32(ub);
+        } else {
+          l = f16_bits_to_f32(lb);
+          u = f16_bits_to_f32(ub);
+        }
+      }
+      step(qa[d0 + e], l, u, accA);
+      step(qb[d0 + e], l, u, accB);
+    }
+  }
+  const int64_t p = p0 + lane;
+  a.scores[(b * a.Hq + h0 + hA) * a.cmax + p] = accA;
+  if (hB < nh) a.scores[(b * a.Hq + h0 + hB) * a.cmax + p] = accB;
+}
+
 __device__ __forceinline__ uint32_t score_key(float s) {
   if (s == 0.f) s = 0.f;  // -0 and +0 compare equal
   const uint32_t u = __float_as_uint(s);
@@ -117,8 +237,14 @@ __device__ __forceinline__ uint32_t score_key(float s) {
 }
 
 // One workgroup per (query head, request): radix select of the top keys, ties
-// to the lower page, pages written ascending.
+// to the lower page, pages written ascending.  When the page keys fit
+// (`KEYS_IN_LDS`), they are computed once into LDS; the digit of each of the
+// four 8-bit passes is found by wave 0 with a suffix scan over the histogram.
+constexpr int64_t QTOPK_LDS_KEYS = 16384;
+
+template <bool KEYS_IN_LDS>
 __global__ __launch_bounds__(QT) void quest_topk_kernel(QuestArgs a) {
+  extern __shared__ uint32_t s_keys[];
   __shared__ uint32_t hist[256];
   __shared__ uint32_t s_prefix, s_mask, s_need;
   __shared__ int64_t scan64[16];
@@ -131,16 +257,23 @@ __global__ __launch_bounds__(QT) void quest_topk_kernel(QuestArgs a) {
   }
   const float* sc = a.scores + (b * a.Hq + h) * a.cmax;
   const bool sink = a.keep_sink && a.top > 1 && count > 1;
-  auto key_of = [&](int64_t p) -> uint32_t {
+  auto key_from_scores = [&](int64_t p) -> uint32_t {
     if (p == count - 1 || (sink && p == 0)) return 0xffffffffu;
     return score_key(sc[p]);
+  };
+  if constexpr (KEYS_IN_LDS) {
+    for (int64_t p = threadIdx.x; p < count; p += QT) s_keys[p] = key_from_scores(p);
+  }
+  auto key_of = [&](int64_t p) -> uint32_t {
+    if constexpr (KEYS_IN_LDS) return s_keys[p];
+    else return key_from_scores(p);
   };
   if (threadIdx.x == 0) {
     s_prefix = 0u;
     s_mask = 0u;
     s_need = static_cast<uint32_t>(a.top);
   }
-  __syncthreads();
+  const int lane = threadIdx.x & 63;
   for (int shift = 24; shift >= 0; shift -= 8) {
     for (int i = threadIdx.x; i < 256; i += QT) hist[i] = 0u;
     __syncthreads();
@@ -150,19 +283,31 @@ __global__ __launch_bounds__(QT) void quest_topk_kernel(QuestArgs a) {
       if ((k & mask) == prefix) atomicAdd(&hist[(k >> shift) & 255u], 1u);
     }
     __syncthreads();
-    if (threadIdx.x == 0) {
-      uint32_t need = s_need, above = 0u;
-      int dsel = 0;
-      for (int dg = 255; dg >= 0; --dg) {
-        if (above + hist[dg] >= need) {
-          dsel = dg;
-          break;
-        }
-        above += hist[dg];
+    if (threadIdx.x < 64) {
+      // lane l owns digits 4l .. 4l+3; keys with a digit above d number
+      // above(d) = (sum over lanes > l) + (own digits above d)
+      const uint32_t h0 = hist[4 * lane], h1 = hist[4 * lane + 1], h2 = hist[4 * lane + 2],
+                     h3 = hist[4 * lane + 3];
+      const uint32_t own = h0 + h1 + h2 + h3;
+      uint32_t suffix = own;  // inclusive suffix sum over lanes >= l
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) {
+        const uint32_t o = __shfl_down(suffix, off, 64);
+        if (lane + off < 64) suffix += o;
       }
-      s_need = need - above;
-      s_prefix = prefix | (static_cast<uint32_t>(dsel) << shift);
-      s_mask = mask | (255u << shift);
+      const uint32_t need = s_need;
+      uint32_t above = suffix - own;
+      const uint32_t hv[4] = {h0, h1, h2, h3};
+#pragma unroll
+      for (int i = 3; i >= 0; --i) {
+        if (above < need && above + hv[i] >= need) {
+          // exactly one (lane, digit) satisfies this
+          s_need = need - above;
+          s_prefix = prefix | (static_cast<uint32_t>(4 * lane + i) << shift);
+          s_mask = mask | (255u << shift);
+        }
+        above += hv[i];
+      }
     }
     __syncthreads();
   }
@@ -395,10 +540,30 @@ extern "C" int hs_quest_topk(const float* query, int64_t q_stride_b, int64_t q_s
   for (int64_t i = 0; i < batch; ++i) any_scored |= top < page_counts[i];
   if (any_scored) {
     const int64_t hchunks = ceil_div(a.g, QHEADS);
+    const bool fused = query_is_16bit && kv_dtype != HS_DTYPE_F32;
+    const int64_t epv = kv_dtype == HS_DTYPE_F32 ? 4 : 8;
+    const int64_t row_bytes = head_dim * (kv_dtype == HS_DTYPE_F32 ? 4 : 2);
+    bool aligned = true;
+    for (int64_t i = 0; i < batch; ++i)
+      aligned &= ((reinterpret_cast<uintptr_t>(minimum[i]) | reinterpret_cast<uintptr_t>(maximum[i])) & 15) == 0;
+    if (head_dim % epv == 0 && aligned && row_bytes <= QS_MAX_ROW_BYTES) {
+      dim3 grid(static_cast<unsigned>(ceil_div(cmax, QS_PAGES)), static_cast<unsigned>(kv_heads * hchunks),
+                static_cast<unsigned>(batch));
+      const size_t lds = static_cast<size_t>(qs_lds_bytes(row_bytes, head_dim));
+      if (kv_dtype == HS_DTYPE_BF16) {
+        if (fused) hipLaunchKernelGGL((quest_score_tile_kernel<HS_DTYPE_BF16, true>), grid, dim3(QT), lds, stream, a);
+        else hipLaunchKernelGGL((quest_score_tile_kernel<HS_DTYPE_BF16, false>), grid, dim3(QT), lds, stream, a);
+      } else if (kv_dtype == HS_DTYPE_F16) {
+        if (fused) hipLaunchKernelGGL((quest_score_tile_kernel<HS_DTYPE_F16, true>), grid, dim3(QT), lds, stream, a);
+        else hipLaunchKernelGGL((quest_score_tile_kernel<HS_DTYPE_F16, false>), grid, dim3(QT), lds, stream, a);
+      } else {
+        hipLaunchKernelGGL((quest_score_tile_kernel<HS_DTYPE_F32, false>), grid, dim3(QT), lds, stream, a);
+      }
+      HS_CHECK_LAUNCH("quest scorer");
+    } else {
     dim3 grid(static_cast<unsigned>(ceil_div(cmax, QT)), static_cast<unsigned>(kv_heads * hchunks),
               static_cast<unsigned>(batch));
     const size_t lds = static_cast<size_t>(QHEADS * head_dim * 4);
-    const bool fused = query_is_16bit && kv_dtype != HS_DTYPE_F32;
     if (kv_dtype == HS_DTYPE_BF16) {
       if (fused) hipLaunchKernelGGL((quest_score_kernel<HS_DTYPE_BF16, true>), grid, dim3(QT), lds, stream, a);
       else hipLaunchKernelGGL((quest_score_kernel<HS_DTYPE_BF16, false>), grid, dim3(QT), lds, stream, a);
@@ -409,9 +574,13 @@ extern "C" int hs_quest_topk(const float* query, int64_t q_stride_b, int64_t q_s
       hipLaunchKernelGGL((quest_score_kernel<HS_DTYPE_F32, false>), grid, dim3(QT), lds, stream, a);
     }
     HS_CHECK_LAUNCH("quest scorer");
+    }
   }
-  hipLaunchKernelGGL(quest_topk_kernel, dim3(static_cast<unsigned>(heads), static_cast<unsigned>(batch)),
-                     dim3(QT), 0, stream, a);
+  const dim3 tgrid(static_cast<unsigned>(heads), static_cast<unsigned>(batch));
+  if (cmax <= QTOPK_LDS_KEYS)
+    hipLaunchKernelGGL(quest_topk_kernel<true>, tgrid, dim3(QT), static_cast<size_t>(cmax * 4), stream, a);
+  else
+    hipLaunchKernelGGL(quest_topk_kernel<false>, tgrid, dim3(QT), 0, stream, a);
   HS_CHECK_LAUNCH("quest top-k");
   return HS_OK;
 }

@@ -211,6 +211,10 @@ def test_resolver_row_stats_accumulate(gpu):
         (torch.float32, 90, 4, 1, 2, 8, 7, True, 357),
         (torch.bfloat16, 10, 16, 2, 2, 32, 12, True, 150),  # top >= count: every page
         (torch.bfloat16, 50, 16, 2, 2, 32, 1, True, None),  # top == 1: tail only
+        (torch.bfloat16, 40, 16, 2, 3, 20, 6, True, None),  # D not a multiple of 8: strided scorer
+        (torch.bfloat16, 64, 16, 16, 1, 256, 8, True, None),  # query tile above the LDS limit
+        (torch.bfloat16, 120, 16, 1, 12, 64, 9, True, None),  # two head chunks per KV head
+        (torch.float16, 20000, 16, 1, 2, 32, 64, True, None),  # keys beyond the LDS key buffer
     ],
 )
 def test_quest_pages_match_oracle(gpu, dtype, pages, P, kv, g, D, top, sink, length):
