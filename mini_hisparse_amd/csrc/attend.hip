@@ -171,15 +171,15 @@ __global__ __launch_bounds__(256) void attend_mfma_kernel(AttendArgs a) {
 
   // Q^T fragments: lane holds Q[head hh][d = 32kk + 8j .. +8]
   u32x4 qf[KK];
+  {
+    const unsigned short* q0 = static_cast<const unsigned short*>(a.q) + b * a.q_sb + k * a.g * a.q_sh;
 #pragma unroll
-  for (int kk = 0; kk < KK; ++kk) {
-    const int d0 = 32 * kk + 8 * j;
-    u32x4 v = {0u, 0u, 0u, 0u};
-    if (hh < a.g && d0 < D) {
-      const unsigned short* qp = static_cast<const unsigned short*>(a.q) + b * a.q_sb + (k * a.g + hh) * a.q_sh + d0;
-      v = load16(qp);
+    for (int kk = 0; kk < KK; ++kk) {
+      const int d0 = 32 * kk + 8 * j;
+      const bool ok = hh < a.g && d0 < D;
+      const u32x4 v = load16(ok ? q0 + hh * a.q_sh + d0 : q0);
+      qf[kk] = ok ? v : u32x4{0u, 0u, 0u, 0u};
     }
-    qf[kk] = v;
   }
 
   f32x4 acc[NT];
@@ -193,27 +193,33 @@ __global__ __launch_bounds__(256) void attend_mfma_kernel(AttendArgs a) {
   const int ntiles = (cnt + 31) / 32;
   // K fragments (A operand: lane holds K[row 16rt + c][d = 32kk + 8j .. +8]) and the
   // V rows this lane stages (row vi*RPI + lane/LPR, d = 8*(lane%LPR) .. +8) of tile t
+  // Loads are unconditional so that a tile's loads stay in flight together: a
+  // masked lane reads its own query row instead (always in bounds) and its
+  // value is replaced by zero afterwards.
+  const unsigned short* qrow = static_cast<const unsigned short*>(a.q) + b * a.q_sb + k * a.g * a.q_sh;
+  const u32x4 zero4 = {0u, 0u, 0u, 0u};
   auto load_tile = [&](int t, u32x4 (&kf)[2][KK], u32x4 (&vr)[VI]) {
 #pragma unroll
     for (int rt = 0; rt < 2; ++rt) {
       const int li = 32 * t + 16 * rt + c;
-      const int64_t koff = li < ACH ? s_koff[li] : -1;
+      const int64_t koff = s_koff[li < ACH ? li : 0];
+      const bool row_ok = li < ACH && koff >= 0;
 #pragma unroll
       for (int kk = 0; kk < KK; ++kk) {
         const int d0 = 32 * kk + 8 * j;
-        u32x4 v = {0u, 0u, 0u, 0u};
-        if (koff >= 0 && d0 < D) v = load16(pool + koff + d0);
-        kf[rt][kk] = v;
+        const bool ok = row_ok && d0 < D;
+        const u32x4 v = load16(ok ? pool + koff + d0 : qrow);
+        kf[rt][kk] = ok ? v : zero4;
       }
     }
 #pragma unroll
     for (int vi = 0; vi < VI; ++vi) {
       const int li = 32 * t + vi * RPI + lane / LPR;
       const int cc = lane % LPR;
-      const int64_t koff = li < ACH ? s_koff[li] : -1;
-      u32x4 v = {0u, 0u, 0u, 0u};
-      if (koff >= 0 && 8 * cc < D) v = load16(pool + koff + vplane + 8 * cc);
-      vr[vi] = v;
+      const int64_t koff = s_koff[li < ACH ? li : 0];
+      const bool ok = li < ACH && koff >= 0 && 8 * cc < D;
+      const u32x4 v = load16(ok ? pool + koff + vplane + 8 * cc : qrow);
+      vr[vi] = ok ? v : zero4;
     }
   };
 
@@ -280,7 +286,7 @@ __global__ __launch_bounds__(256) void attend_mfma_kernel(AttendArgs a) {
     pf[2] = pb[4] | (static_cast<uint32_t>(pb[5]) << 16);
     pf[3] = pb[6] | (static_cast<uint32_t>(pb[7]) << 16);
 
-    wave_sync();  // V tile visible to every lane of the wave
+    wave_lds_sync();  // V tile visible to every lane of the wave
     // O^T[d][head] += V^T P^T; lane holds V[row rho(j,e)][d = 16mt + c]
 #pragma unroll
     for (int mt = 0; mt < NT; ++mt) {
@@ -297,7 +303,7 @@ __global__ __launch_bounds__(256) void attend_mfma_kernel(AttendArgs a) {
       vf[3] = vv[6] | (static_cast<uint32_t>(vv[7]) << 16);
       acc[mt] = mfma16x16x32<DT>(vf, pf, acc[mt]);
     }
-    wave_sync();  // all reads of this tile done before the next overwrites it
+    wave_lds_sync();  // all reads of this tile done before the next overwrites it
 #pragma unroll
     for (int rt = 0; rt < 2; ++rt)
 #pragma unroll

@@ -90,6 +90,15 @@ __device__ __forceinline__ void wave_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+// Orders one wave's LDS writes before its later LDS reads of other lanes'
+// data.  LDS executes a wave's operations in order; this waits for the wave's
+// outstanding LDS operations and stops compiler reordering, without waiting
+// for vector memory loads still in flight (a memory fence would).
+__device__ __forceinline__ void wave_lds_sync() {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_wave_barrier();
+}
+
 template <typename T>
 __device__ __forceinline__ T wave_inclusive_sum(T v) {
   const int lane = threadIdx.x & 63;

@@ -3,31 +3,48 @@
 //
 // The reference sorts the selected tokens and the hot tags and uses
 // searchsorted/argsort to find hits, protect them, pick least-recent victims
-// and reorder the LRU.  Here one 1024-thread workgroup resolves one
-// (request, layer) without sorting anything:
+// and reorder the LRU.  Nothing is sorted here.  A batch of (request, layer)
+// descriptors is resolved by four launches; the two whose work is per element
+// spread every descriptor over many workgroups, the two that need one
+// block-wide order use one workgroup per descriptor but read only bitmaps and
+// the LRU (no per-token table lookups):
 //
-//   * the selected tokens become a bitmap over [0, length) in LDS, so their
-//     ascending order is the bit order and duplicates are found by the
-//     atomicOr that sees its bit already set;
-//   * hot tags are matched through a hash of the host blocks of the selected
-//     non-resident pages (host row = source[page] * P + offset), so a tag maps
-//     back to the logical token it caches;
-//   * victims are the stable partition "unprotected then protected" of the LRU
-//     order, built with one block-wide prefix sum;
-//   * miss ranks are a prefix count of miss bits in token order;
-//   * the new LRU is the stable partition by category (untouched, filled, hit),
-//     again one block-wide prefix sum.
+//   mark    (1 WG / desc)  selected tokens become a bitmap over [0, length) in
+//                          LDS: ascending order is bit order, a duplicate input
+//                          is the atomicOr that finds its bit set (the first
+//                          input index of a duplicated token by atomicMin).
+//                          Per page with selected tokens: resident hits are
+//                          counted, host-backed non-resident tokens get a
+//                          needs-hot bit, and the page's host block is hashed to
+//                          the logical page (host row = source[page] * P + off).
+//   tags    (S/256 WGs)    each hot tag finds its logical token through the
+//                          hash; a tag whose token needs a hot row is a hit:
+//                          hit bit, the token's slot, the slot's protection bit.
+//   order   (1 WG / desc)  miss bits = needs-hot and not hit, with their
+//                          per-word prefix (miss ranks in token order) and the
+//                          counts; victims = the stable partition "unprotected,
+//                          then protected" of the LRU order; the new LRU = the
+//                          stable partition by category (untouched, filled,
+//                          hit), a slot being filled iff its victim rank is
+//                          below the miss count.  Two block-wide prefix sums.
+//   outputs (n/256 + H*W/256 WGs)  per input: its physical row (the first
+//                          occurrence of a token wins), and for a miss its plan
+//                          entry and the new tag of its victim slot; per head
+//                          column: the row of the input it names.
 //
-// Batched launches run one workgroup per descriptor.  Preconditions, as in the
-// reference: unique non-negative tags, an injective source table, and
-// length <= n_pages * page_size (checked on the host).
+// Preconditions, as in the reference: unique non-negative tags, an injective
+// source table, and length <= n_pages * page_size (checked on the host).
 #include "hs_common.h"
 
 namespace hs {
 
-constexpr int RT = 1024;      // threads per resolver workgroup
+constexpr int RT = 1024;      // threads of the single-workgroup phases
+constexpr int RW = 256;       // threads of the wide phases
 constexpr int RMAXB = 8;      // descriptors per launch
 constexpr int LRU_CHUNK = 32; // hot_rows <= 32768 = RT * LRU_CHUNK
+constexpr int MARK_BATCH = 8; // pages loaded per thread before use
+constexpr int MARK_TILE = 512;                // inputs per wave and tile (8 per lane)
+constexpr int MARK_TILE_PAD = MARK_TILE / 8 * 9;
 
 struct ResolveBatch {
   hs_resolve_desc d[RMAXB];
@@ -35,13 +52,18 @@ struct ResolveBatch {
 };
 
 struct ResolveWs {
-  uint32_t* dupbits;  // [wl]
-  int32_t* first_in;  // [length]
-  int32_t* tslot;     // [length]
-  int32_t* hkeys;     // [hcap]
-  int32_t* hvals;     // [hcap]
-  int32_t* victims;   // [hot_rows]
-  int64_t* uresult;   // [n] when the caller gives no union buffer
+  uint32_t* needbits;  // [wl] selected, host-backed, not resident
+  uint32_t* hitbits;   // [wl] needs-hot tokens with a hot tag
+  uint32_t* missbits;  // [wl] needs-hot tokens without one
+  uint32_t* dupbits;   // [wl] tokens given more than once
+  int32_t* mprefix;    // [wl] misses in the words before this one
+  uint32_t* protbits;  // [wsw] slots holding a wanted tag
+  int32_t* first_in;   // [length] first input index of a duplicated token
+  int32_t* tslot;      // [length] hot slot of a hit token
+  int32_t* hkeys;      // [hcap] host block (-1 = empty)
+  int32_t* hvals;      // [hcap] logical page of that host block
+  int32_t* victims;    // [hot_rows] slots in victim order
+  int64_t* totals;     // [4] resident hits, hot hits, misses, any duplicate
   int64_t hcap;
 };
 
@@ -54,9 +76,10 @@ __host__ __device__ inline int64_t pow2_at_least(int64_t x) {
 
 __host__ __device__ inline int64_t words_for(int64_t length) { return (length + 32) / 32; }
 
-__host__ __device__ inline int64_t ws_layout(int64_t n, int64_t length, int64_t n_pages, int64_t hot_rows, ResolveWs* w,
-                         char* base) {
+__host__ __device__ inline int64_t ws_layout(int64_t length, int64_t n_pages, int64_t hot_rows, ResolveWs* w,
+                                             char* base) {
   const int64_t wl = words_for(length);
+  const int64_t wsw = (hot_rows + 31) / 32;
   const int64_t hcap = pow2_at_least(2 * (n_pages < 1 ? 1 : n_pages));
   int64_t off = 0;
   auto take = [&](int64_t bytes) {
@@ -65,23 +88,39 @@ __host__ __device__ inline int64_t ws_layout(int64_t n, int64_t length, int64_t 
     return base ? base + at : nullptr;
   };
   char* p0 = take(wl * 4);
-  char* p1 = take(length * 4);
-  char* p2 = take(length * 4);
-  char* p3 = take(hcap * 4);
-  char* p4 = take(hcap * 4);
-  char* p5 = take(hot_rows * 4);
-  char* p6 = take(n * 8);
+  char* p1 = take(wl * 4);
+  char* p2 = take(wl * 4);
+  char* p3 = take(wl * 4);
+  char* p4 = take(wl * 4);
+  char* p5 = take(wsw * 4);
+  char* p6 = take(length * 4);
+  char* p7 = take(length * 4);
+  char* p8 = take(hcap * 4);
+  char* p9 = take(hcap * 4);
+  char* p10 = take(hot_rows * 4);
+  char* p11 = take(4 * 8);
   if (w) {
-    w->dupbits = reinterpret_cast<uint32_t*>(p0);
-    w->first_in = reinterpret_cast<int32_t*>(p1);
-    w->tslot = reinterpret_cast<int32_t*>(p2);
-    w->hkeys = reinterpret_cast<int32_t*>(p3);
-    w->hvals = reinterpret_cast<int32_t*>(p4);
-    w->victims = reinterpret_cast<int32_t*>(p5);
-    w->uresult = reinterpret_cast<int64_t*>(p6);
+    w->needbits = reinterpret_cast<uint32_t*>(p0);
+    w->hitbits = reinterpret_cast<uint32_t*>(p1);
+    w->missbits = reinterpret_cast<uint32_t*>(p2);
+    w->dupbits = reinterpret_cast<uint32_t*>(p3);
+    w->mprefix = reinterpret_cast<int32_t*>(p4);
+    w->protbits = reinterpret_cast<uint32_t*>(p5);
+    w->first_in = reinterpret_cast<int32_t*>(p6);
+    w->tslot = reinterpret_cast<int32_t*>(p7);
+    w->hkeys = reinterpret_cast<int32_t*>(p8);
+    w->hvals = reinterpret_cast<int32_t*>(p9);
+    w->victims = reinterpret_cast<int32_t*>(p10);
+    w->totals = reinterpret_cast<int64_t*>(p11);
     w->hcap = hcap;
   }
   return off;
+}
+
+__device__ __forceinline__ ResolveWs ws_of(const hs_resolve_desc& d) {
+  ResolveWs w;
+  ws_layout(d.length, d.n_pages, d.hot_rows, &w, static_cast<char*>(d.workspace));
+  return w;
 }
 
 __device__ __forceinline__ uint32_t hash32(uint32_t x) {
@@ -102,51 +141,112 @@ __device__ __forceinline__ int64_t load_pos(const hs_resolve_desc& d, int64_t i)
                          : static_cast<int64_t>(static_cast<const int32_t*>(d.positions)[i]);
 }
 
-// LDS: selbits[wl], hitbits[wl], missbits[wl], protbits[ws], insbits[ws] (u32 words)
-__global__ __launch_bounds__(RT) void resolve_kernel(ResolveBatch batch) {
+// Bits [lo, hi) of word `word` (lo, hi absolute token indices).
+__device__ __forceinline__ uint32_t range_mask(int64_t word, int64_t lo, int64_t hi) {
+  const int64_t base = word << 5;
+  const int64_t a = lo > base ? lo - base : 0;
+  const int64_t b = hi < base + 32 ? hi - base : 32;
+  if (b <= a) return 0u;
+  const uint32_t upto = b >= 32 ? 0xffffffffu : ((1u << b) - 1u);
+  return upto & ~((1u << a) - 1u);
+}
+
+// ---- mark: bitmaps, duplicates, resident count, needs-hot bits, host-block hash
+// LDS: selbits[wl], needs[wl]
+__global__ __launch_bounds__(RT) void resolve_mark_kernel(ResolveBatch batch) {
   extern __shared__ uint32_t lds[];
   __shared__ int64_t scan64[16];
-  __shared__ int32_t scan32[16];
   __shared__ int any_dup;
-
+  __shared__ int32_t mark_tile[(RT / 64) * MARK_TILE_PAD];
   const hs_resolve_desc& d = batch.d[blockIdx.x];
+  const ResolveWs w = ws_of(d);
   const int T = threadIdx.x;
   const int64_t n = d.n, L = d.length, P = d.page_size, NP = d.n_pages, S = d.hot_rows;
-  const int64_t wl = words_for(L);
-  const int64_t wsw = (S + 31) / 32;
+  const int64_t wl = words_for(L), wsw = (S + 31) / 32;
   uint32_t* selbits = lds;
-  uint32_t* hitbits = selbits + wl;
-  uint32_t* missbits = hitbits + wl;
-  uint32_t* protbits = missbits + wl;
-  uint32_t* insbits = protbits + wsw;
+  uint32_t* needs = lds + wl;
 
-  ResolveWs w;
-  ws_layout(n, L, NP, S, &w, static_cast<char*>(d.workspace));
-  int64_t* result = d.union_physical ? d.union_physical : (d.head_columns ? w.uresult : d.physical);
-
-  // P0: clear bitmaps and the page hash
-  for (int64_t i = T; i < 3 * wl + 2 * wsw; i += RT) lds[i] = 0u;
-  for (int64_t i = T; i < wl; i += RT) w.dupbits[i] = 0u;
+  for (int64_t i = T; i < 2 * wl; i += RT) lds[i] = 0u;
+  for (int64_t i = T; i < wl; i += RT) {
+    w.dupbits[i] = 0u;
+    w.hitbits[i] = 0u;
+  }
+  for (int64_t i = T; i < wsw; i += RT) w.protbits[i] = 0u;
   for (int64_t i = T; i < w.hcap; i += RT) w.hkeys[i] = -1;
   if (T == 0) any_dup = 0;
   __syncthreads();
 
-  // P1: mark the selected tokens; a bit already set means a duplicate input
-  for (int64_t i = T; i < n; i += RT) {
-    const int64_t t = load_pos(d, i);
-    if (t >= 0 && t < L) {
-      const uint32_t bit = 1u << (t & 31);
-      const uint32_t old = atomicOr(&selbits[t >> 5], bit);
-      if (old & bit) {
-        atomicOr(&w.dupbits[t >> 5], bit);
+  // selected tokens; a bit already set means a duplicate input.  Each wave
+  // loads 512 consecutive inputs (coalesced) into an LDS tile; lane l then
+  // walks inputs 8l .. 8l+7 of the tile and gathers the bits of one bitmap
+  // word in a register while consecutive tokens stay in it (selected tokens
+  // mostly arrive sorted), publishing them with one atomicOr when the word
+  // changes.  A token already in the register, or already in the word when
+  // it is published, is a duplicate; any input order gives the same bitmap
+  // and duplicate set.
+  {
+    const int lane = T & 63, wave = T >> 6;
+    int32_t* tile = mark_tile + wave * MARK_TILE_PAD;
+    int64_t cur = -1;
+    uint32_t acc = 0u, accdup = 0u;
+    auto flush = [&]() {
+      if (cur < 0) return;
+      const uint32_t old = atomicOr(&selbits[cur], acc);
+      const uint32_t dm = accdup | (old & acc);
+      if (dm) {
+        atomicOr(&w.dupbits[cur], dm);
         any_dup = 1;
       }
-    }
+    };
+    constexpr int KT = MARK_TILE / 64;
+    constexpr int64_t STEP = static_cast<int64_t>(RT / 64) * MARK_TILE;
+    // one loop per position type: a per-load type branch would serialise the loads
+    auto walk = [&](const auto* pos) {
+      int64_t nxt[KT];  // the next tile's inputs, loaded while this one is walked
+      auto load_tile = [&](int64_t base) {  // unconditional loads (clamped index), then masked
+#pragma unroll
+        for (int k = 0; k < KT; ++k) {
+          const int64_t i = base + k * 64 + lane;
+          const int64_t v = static_cast<int64_t>(pos[i < n ? i : n - 1]);
+          nxt[k] = i < n ? v : -1;
+        }
+      };
+      load_tile(static_cast<int64_t>(wave) * MARK_TILE);
+      for (int64_t base = static_cast<int64_t>(wave) * MARK_TILE; base < n; base += STEP) {
+#pragma unroll
+        for (int k = 0; k < KT; ++k) {
+          const int p = k * 64 + lane;  // tile position; stored with a stride-9 row per lane
+          const int64_t t = nxt[k];
+          tile[9 * (p >> 3) + (p & 7)] = (t >= 0 && t < L) ? static_cast<int32_t>(t) : -1;
+        }
+        load_tile(base + STEP);
+        wave_lds_sync();
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          const int32_t t = tile[9 * lane + k];
+          if (t < 0) continue;
+          const int64_t word = t >> 5;
+          const uint32_t bit = 1u << (t & 31);
+          if (word != cur) {
+            flush();
+            cur = word;
+            acc = accdup = 0u;
+          }
+          accdup |= acc & bit;
+          acc |= bit;
+        }
+        wave_lds_sync();
+      }
+    };
+    if (d.positions_i64) walk(static_cast<const int64_t*>(d.positions));
+    else walk(static_cast<const int32_t*>(d.positions));
+    flush();
   }
   __syncthreads();
 
-  // P1b: first input index of each duplicated token (row_index.py:121-126)
-  if (any_dup) {
+  // first input index of each duplicated token (row_index.py:121-126)
+  const bool dups = any_dup != 0;
+  if (dups) {
     for (int64_t i = T; i < n; i += RT) {
       const int64_t t = load_pos(d, i);
       if (t >= 0 && t < L && bit_of(w.dupbits, t)) w.first_in[t] = static_cast<int32_t>(n);
@@ -156,250 +256,303 @@ __global__ __launch_bounds__(RT) void resolve_kernel(ResolveBatch batch) {
       const int64_t t = load_pos(d, i);
       if (t >= 0 && t < L && bit_of(w.dupbits, t)) atomicMin(&w.first_in[t], static_cast<int32_t>(i));
     }
-    __syncthreads();
   }
 
-  // P2: hash host block -> logical page for selected, host-backed, non-resident pages
+  // per page with selected tokens: resident hits, needs-hot bits, hash host block -> page
   const uint32_t hmask = static_cast<uint32_t>(w.hcap - 1);
-  for (int64_t p = T; p < NP; p += RT) {
-    const int64_t lo = p * P;
-    if (lo >= L) continue;
-    int64_t hi = lo + P;
-    if (hi > L) hi = L;
-    bool any = false;
-    for (int64_t t = lo; t < hi && !any;) {
-      const int64_t word = t >> 5;
-      const int64_t wend = (word + 1) << 5;
-      const int64_t stop = wend < hi ? wend : hi;
-      uint32_t m = selbits[word];
-      const int sh0 = static_cast<int>(t & 31);
-      const int cnt = static_cast<int>(stop - t);
-      m >>= sh0;
-      if (cnt < 32) m &= (1u << cnt) - 1u;
-      any = m != 0u;
-      t = stop;
-    }
-    if (!any) continue;
-    const int32_t src = d.source[p];
-    if (src < 0 || d.resident[p] >= 0) continue;
-    uint32_t h = hash32(static_cast<uint32_t>(src)) & hmask;
-    while (true) {
-      const int32_t prev = atomicCAS(&w.hkeys[h], -1, src);
-      if (prev == -1) {
-        w.hvals[h] = static_cast<int32_t>(p);
-        break;
-      }
-      if (prev == src) break;  // non-injective source table: first page wins
-      h = (h + 1) & hmask;
-    }
-  }
-  __syncthreads();
-
-  // P3: hot tag lookup and protection (row_index.py:84-90)
-  for (int64_t s = T; s < S; s += RT) {
-    const int32_t tag = d.tags[s];
-    if (tag < 0) continue;
-    const int32_t hp = static_cast<int32_t>(tag / P);
-    const int64_t off = tag - static_cast<int64_t>(hp) * P;
-    uint32_t h = hash32(static_cast<uint32_t>(hp)) & hmask;
-    int32_t page = -1;
-    while (true) {
-      const int32_t key = w.hkeys[h];
-      if (key == -1) break;
-      if (key == hp) {
-        page = w.hvals[h];
-        break;
-      }
-      h = (h + 1) & hmask;
-    }
-    if (page < 0) continue;
-    const int64_t t = static_cast<int64_t>(page) * P + off;
-    if (t >= L || !bit_of(selbits, t)) continue;
-    atomicOr(&hitbits[t >> 5], 1u << (t & 31));
-    w.tslot[t] = static_cast<int32_t>(s);
-    atomicOr(&protbits[s >> 5], 1u << (s & 31));
-  }
-  __syncthreads();
-
-  // P4: victims = unprotected slots in LRU order, then protected ones (row_index.py:94-95)
-  {
-    const int64_t j0 = static_cast<int64_t>(T) * LRU_CHUNK;
-    int32_t slot[LRU_CHUNK];
-    int32_t unprot = 0;
+  int64_t c_res = 0;
+  for (int64_t base = T; base < NP; base += static_cast<int64_t>(RT) * MARK_BATCH) {
+    int32_t src[MARK_BATCH], res[MARK_BATCH];
 #pragma unroll
-    for (int q = 0; q < LRU_CHUNK; ++q) {
-      const int64_t jj = j0 + q;
-      slot[q] = jj < S ? static_cast<int32_t>(d.lru[jj]) : -1;
-      if (jj < S && !bit_of(protbits, slot[q])) ++unprot;
+    for (int k = 0; k < MARK_BATCH; ++k) {
+      const int64_t p = base + static_cast<int64_t>(k) * RT;
+      const bool in = p < NP && p * P < L;
+      const int64_t pc = in ? p : 0;  // unconditional loads, masked afterwards
+      const int32_t sv = d.source[pc], rv = d.resident[pc];
+      src[k] = in ? sv : -1;
+      res[k] = in ? rv : -1;
     }
-    int32_t total_unprot;
-    const int32_t ubase = block_exclusive_sum<int32_t>(unprot, scan32, &total_unprot);
-    int32_t u = ubase;
 #pragma unroll
-    for (int q = 0; q < LRU_CHUNK; ++q) {
-      const int64_t jj = j0 + q;
-      if (jj >= S) break;
-      if (!bit_of(protbits, slot[q])) {
-        w.victims[u++] = slot[q];
-      } else {
-        const int64_t pr = jj - (u);  // protected slots before position jj
-        w.victims[total_unprot + pr] = slot[q];
+    for (int k = 0; k < MARK_BATCH; ++k) {
+      const int64_t p = base + static_cast<int64_t>(k) * RT;
+      if (src[k] < 0) continue;  // also pages past the history
+      const int64_t lo = p * P;
+      const int64_t hi = lo + P < L ? lo + P : L;
+      bool any = false;
+      for (int64_t wd = lo >> 5; wd <= (hi - 1) >> 5; ++wd) {
+        const uint32_t m = selbits[wd] & range_mask(wd, lo, hi);
+        if (!m) continue;
+        any = true;
+        if (res[k] >= 0) c_res += __popc(m);
+        else atomicOr(&needs[wd], m);
+      }
+      if (!any || res[k] >= 0) continue;
+      uint32_t h = hash32(static_cast<uint32_t>(src[k])) & hmask;
+      while (true) {
+        const int32_t prev = atomicCAS(&w.hkeys[h], -1, src[k]);
+        if (prev == -1) {
+          w.hvals[h] = static_cast<int32_t>(p);
+          break;
+        }
+        if (prev == src[k]) break;  // non-injective source table: first page wins
+        h = (h + 1) & hmask;
       }
     }
   }
-  __syncthreads();
+  int64_t tot_res;
+  block_exclusive_sum<int64_t>(c_res, scan64, &tot_res);  // synchronises the block
+  for (int64_t i = T; i < wl; i += RT) w.needbits[i] = needs[i];
+  if (T == 0) {
+    w.totals[0] = tot_res;
+    w.totals[3] = dups ? 1 : 0;
+  }
+}
 
-  // P5a: classify the selected tokens in ascending order (row_index.py:72-80, 96)
+// ---- tags: hot tag lookup and protection (row_index.py:84-90)
+__global__ __launch_bounds__(RW) void resolve_tags_kernel(ResolveBatch batch) {
+  const hs_resolve_desc& d = batch.d[blockIdx.y];
+  const int64_t s = static_cast<int64_t>(blockIdx.x) * RW + threadIdx.x;
+  if (s >= d.hot_rows) return;
+  const int32_t tag = d.tags[s];
+  if (tag < 0) return;
+  const ResolveWs w = ws_of(d);
+  const int64_t P = d.page_size;
+  const int32_t hp = static_cast<int32_t>(tag / P);
+  const int64_t off = tag - static_cast<int64_t>(hp) * P;
+  const uint32_t hmask = static_cast<uint32_t>(w.hcap - 1);
+  uint32_t h = hash32(static_cast<uint32_t>(hp)) & hmask;
+  int32_t page = -1;
+  while (true) {
+    const int32_t key = w.hkeys[h];
+    if (key == -1) break;
+    if (key == hp) {
+      page = w.hvals[h];
+      break;
+    }
+    h = (h + 1) & hmask;
+  }
+  if (page < 0) return;
+  const int64_t t = static_cast<int64_t>(page) * P + off;
+  if (t >= d.length || !bit_of(w.needbits, t)) return;
+  atomicOr(&w.hitbits[t >> 5], 1u << (t & 31));
+  w.tslot[t] = static_cast<int32_t>(s);
+  atomicOr(&w.protbits[s >> 5], 1u << (s & 31));
+}
+
+// ---- order: miss ranks, counts, victims, LRU reorder (row_index.py:94-96, 112-113)
+// LDS: protbits[wsw]
+__global__ __launch_bounds__(RT) void resolve_order_kernel(ResolveBatch batch) {
+  extern __shared__ uint32_t prot[];
+  __shared__ int64_t scan64[16];
+  __shared__ int32_t scan32[16];
+  __shared__ int32_t rcnt[LRU_CHUNK * (RT / 64)], rbase[LRU_CHUNK * (RT / 64)];
+  __shared__ uint64_t ccnt[LRU_CHUNK * (RT / 64)];
+  const hs_resolve_desc& d = batch.d[blockIdx.x];
+  const ResolveWs w = ws_of(d);
+  const int T = threadIdx.x;
+  const int64_t L = d.length, S = d.hot_rows;
+  const int64_t wl = words_for(L), wsw = (S + 31) / 32;
+  for (int64_t i = T; i < wsw; i += RT) prot[i] = w.protbits[i];
+
+  // miss bits in token order and their per-word exclusive prefix
   const int64_t wpt = (wl + RT - 1) / RT;
   const int64_t w0 = static_cast<int64_t>(T) * wpt;
   int64_t w1 = w0 + wpt;
   if (w1 > wl) w1 = wl;
-  int64_t c_res = 0, c_hit = 0, c_miss = 0;
+  int64_t c_hit = 0, c_miss = 0;
   for (int64_t wd = w0; wd < w1; ++wd) {
-    uint32_t m = selbits[wd];
-    uint32_t miss_word = 0u;
-    while (m) {
-      const int b = __builtin_ctz(m);
-      m &= m - 1u;
-      const int64_t t = (wd << 5) + b;
-      const int64_t page = t / P;
-      const int32_t src = d.source[page];
-      if (src < 0) continue;
-      if (d.resident[page] >= 0) {
-        ++c_res;
-      } else if ((hitbits[wd] >> b) & 1u) {
-        ++c_hit;
-      } else {
-        ++c_miss;
-        miss_word |= 1u << b;
-      }
-    }
-    missbits[wd] = miss_word;
+    const uint32_t need = w.needbits[wd], hit = w.hitbits[wd];
+    const uint32_t miss = need & ~hit;
+    w.missbits[wd] = miss;
+    c_hit += __popc(hit);
+    c_miss += __popc(miss);
   }
-  int64_t tot_res, tot_hit, tot_miss;
-  block_exclusive_sum<int64_t>(c_res, scan64, &tot_res);
+  int64_t tot_hit, tot_miss;
   block_exclusive_sum<int64_t>(c_hit, scan64, &tot_hit);
-  const int64_t mbase = block_exclusive_sum<int64_t>(c_miss, scan64, &tot_miss);
+  int64_t r = block_exclusive_sum<int64_t>(c_miss, scan64, &tot_miss);
+  for (int64_t wd = w0; wd < w1; ++wd) {
+    w.mprefix[wd] = static_cast<int32_t>(r);
+    r += __popc(w.needbits[wd] & ~w.hitbits[wd]);
+  }
 
-  // P5b: assign victims to misses in token order; tags, miss plan (row_index.py:96-120)
-  {
-    int64_t r = mbase;
-    for (int64_t wd = w0; wd < w1; ++wd) {
-      uint32_t m = missbits[wd];
-      while (m) {
-        const int b = __builtin_ctz(m);
-        m &= m - 1u;
-        const int64_t t = (wd << 5) + b;
-        const int64_t page = t / P;
-        const int64_t off = t - page * P;
-        const int64_t host = static_cast<int64_t>(d.source[page]) * P + off;
-        const int64_t vi = r < S - 1 ? r : S - 1;
-        const int32_t slot = w.victims[vi];
-        w.tslot[t] = slot;
-        const int64_t hb = slot / P;
-        const int64_t hphys = static_cast<int64_t>(d.hot[hb]) * P + (slot - hb * P);
-        d.miss_host_rows[r] = host;
-        d.miss_device_rows[r] = hphys;
-        if (r < S - 1 || r == tot_miss - 1) {
-          d.tags[slot] = static_cast<int32_t>(host);
-          atomicOr(&insbits[slot >> 5], 1u << (slot & 31));
-        }
-        ++r;
-      }
-    }
-    for (int64_t i = tot_miss + T; i < n; i += RT) {
-      d.miss_host_rows[i] = -1;
-      d.miss_device_rows[i] = -1;
-    }
+  // victims: unprotected slots in LRU order, then protected ones; a slot is
+  // filled iff its victim rank is below the miss count.  LRU entry
+  // jj = q * RT + T (row q, thread T): loads and stores of a row are
+  // coalesced.  Ranks inside a wave come from ballots (mbcnt); the counts of
+  // every (row, wave) are scanned in row-major order, which is LRU order.
+  const int lane = T & 63, wave = T >> 6;
+  constexpr int NW = RT / 64;
+  const int32_t S32 = static_cast<int32_t>(S);
+  const int32_t tm = static_cast<int32_t>(tot_miss);
+  // slots are < 32768: the low 32-bit word of each int64 LRU entry holds it
+  const int32_t* lru_lo = reinterpret_cast<const int32_t*>(d.lru);
+  int32_t slot[LRU_CHUNK];
+#pragma unroll
+  for (int q = 0; q < LRU_CHUNK; ++q) {
+    const int32_t jj = q * RT + T;
+    const int32_t v = lru_lo[2 * (jj < S32 ? jj : 0)];  // unconditional load, masked afterwards
+    slot[q] = jj < S32 ? v : -1;
+  }
+  __syncthreads();  // protection bits in LDS
+  auto below = [&](uint64_t m) -> int32_t {
+    return static_cast<int32_t>(__builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m >> 32),
+                                                          __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m), 0u)));
+  };
+  uint32_t protmask = 0u;  // bit q: entry of row q is protected
+#pragma unroll
+  for (int q = 0; q < LRU_CHUNK; ++q) {
+    const int32_t jj = q * RT + T;
+    const bool pr = jj < S32 && bit_of(prot, slot[q]);
+    protmask |= static_cast<uint32_t>(pr) << q;
+    const uint64_t up = __ballot(jj < S32 && !pr);
+    if (lane == 0) rcnt[q * NW + wave] = static_cast<int32_t>(__popcll(up));
   }
   __syncthreads();
-
-  // P6: LRU stable reorder by category 0 untouched, 1 filled, 2 hit (3 both) (row_index.py:112-113)
+  int32_t total_unprot;
   {
-    const int64_t j0 = static_cast<int64_t>(T) * LRU_CHUNK;
-    int32_t slot[LRU_CHUNK];
-    uint64_t packed = 0;  // four 16-bit category counters
-#pragma unroll
-    for (int q = 0; q < LRU_CHUNK; ++q) {
-      const int64_t jj = j0 + q;
-      slot[q] = jj < S ? static_cast<int32_t>(d.lru[jj]) : -1;
-      if (jj < S) {
-        const int cat = static_cast<int>(bit_of(insbits, slot[q])) + 2 * static_cast<int>(bit_of(protbits, slot[q]));
-        packed += static_cast<uint64_t>(1) << (16 * cat);
-      }
-    }
-    uint64_t totals;
-    const uint64_t before = block_exclusive_sum<uint64_t>(packed, reinterpret_cast<uint64_t*>(scan64), &totals);
-    int64_t pos[4];
-    int64_t catbase = 0;
-#pragma unroll
-    for (int cat = 0; cat < 4; ++cat) {
-      pos[cat] = catbase + static_cast<int64_t>((before >> (16 * cat)) & 0xffffu);
-      catbase += static_cast<int64_t>((totals >> (16 * cat)) & 0xffffu);
-    }
-    // every thread has read its LRU chunk (block scan above synchronises)
-#pragma unroll
-    for (int q = 0; q < LRU_CHUNK; ++q) {
-      const int64_t jj = j0 + q;
-      if (jj >= S) break;
-      const int cat = static_cast<int>(bit_of(insbits, slot[q])) + 2 * static_cast<int>(bit_of(protbits, slot[q]));
-      d.lru[pos[cat]++] = slot[q];
-    }
+    const int32_t v = T < LRU_CHUNK * NW ? rcnt[T] : 0;
+    const int32_t ex = block_exclusive_sum<int32_t>(v, scan32, &total_unprot);
+    if (T < LRU_CHUNK * NW) rbase[T] = ex;
   }
-
-  // P7: physical row per input, first occurrence of each token wins (row_index.py:96-103, 121-126)
-  for (int64_t i = T; i < n; i += RT) {
-    const int64_t t = load_pos(d, i);
-    int64_t r = -1;
-    if (t >= 0 && t < L) {
-      bool keep = true;
-      if (any_dup && bit_of(w.dupbits, t)) keep = w.first_in[t] == static_cast<int32_t>(i);
-      if (keep) {
-        const int64_t page = t / P;
-        const int64_t off = t - page * P;
-        if (d.source[page] >= 0) {
-          const int32_t res = d.resident[page];
-          if (res >= 0) {
-            r = static_cast<int64_t>(res) * P + off;
-          } else {
-            const int32_t slot = w.tslot[t];
-            const int64_t hb = slot / P;
-            r = static_cast<int64_t>(d.hot[hb]) * P + (slot - hb * P);
-          }
-        }
-      }
-    }
-    result[i] = r;
+  __syncthreads();
+  uint64_t catbits = 0u;  // two bits per row: filled, protected
+#pragma unroll
+  for (int q = 0; q < LRU_CHUNK; ++q) {
+    const int32_t jj = q * RT + T;
+    const bool in = jj < S32;
+    const bool pr = (protmask >> q) & 1u;
+    const uint64_t up = __ballot(in && !pr);
+    const int32_t ubefore = rbase[q * NW + wave] + below(up);  // unprotected entries before jj
+    const int32_t rank = pr ? total_unprot + (jj - ubefore) : ubefore;
+    const int cat = static_cast<int>(rank < tm) + 2 * static_cast<int>(pr);
+    if (in) w.victims[rank] = slot[q];
+    catbits |= static_cast<uint64_t>(cat) << (2 * q);
+    uint64_t packed = 0;
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+      packed |= static_cast<uint64_t>(__popcll(__ballot(in && cat == c))) << (16 * c);
+    if (lane == 0) ccnt[q * NW + wave] = packed;
   }
-  if (d.head_columns) {
-    __syncthreads();
-    // P8: per-head remap (row_index.py:127-131)
-    const int64_t total = d.heads * d.width;
-    for (int64_t e = T; e < total; e += RT) {
-      const int64_t h = e / d.width, jj = e - h * d.width;
-      const int64_t col = d.head_columns[h * d.hc_stride_h + jj * d.hc_stride_w];
-      d.physical[e] = (col >= 0 && col < n) ? result[col] : -1;
-    }
-  } else if (d.physical != result) {
-    for (int64_t i = T; i < n; i += RT) d.physical[i] = result[i];
+  __syncthreads();
+  uint64_t ctotal;
+  {
+    const uint64_t v = T < LRU_CHUNK * NW ? ccnt[T] : 0;
+    const uint64_t ex = block_exclusive_sum<uint64_t>(v, reinterpret_cast<uint64_t*>(scan64), &ctotal);
+    if (T < LRU_CHUNK * NW) ccnt[T] = ex;
   }
-
-  // counts (row_index.py:136), optionally accumulated into the cache's row_stats
+  __syncthreads();
+  const auto field = [](uint64_t v, int c) { return static_cast<int32_t>((v >> (16 * c)) & 0xffffu); };
+  const int32_t start1 = field(ctotal, 0);
+  const int32_t start2 = start1 + field(ctotal, 1);
+  const int32_t start3 = start2 + field(ctotal, 2);
+  // every thread has read its LRU entries (the barriers above)
+#pragma unroll
+  for (int q = 0; q < LRU_CHUNK; ++q) {
+    const int32_t jj = q * RT + T;
+    const bool in = jj < S32;
+    const int cat = static_cast<int>((catbits >> (2 * q)) & 3u);
+    const uint64_t base = ccnt[q * NW + wave];
+    int32_t at = 0;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const uint64_t m = __ballot(in && cat == c);
+      if (cat == c) at = (c == 0 ? 0 : c == 1 ? start1 : c == 2 ? start2 : start3) + field(base, c) + below(m);
+    }
+    if (in) d.lru[at] = slot[q];
+  }
   if (T == 0) {
-    d.counts[0] = tot_res;
-    d.counts[1] = tot_hit;
-    d.counts[2] = tot_miss;
-    if (d.row_stats) {
-      atomicAdd(reinterpret_cast<unsigned long long*>(&d.row_stats[0]), static_cast<unsigned long long>(tot_res));
-      atomicAdd(reinterpret_cast<unsigned long long*>(&d.row_stats[1]), static_cast<unsigned long long>(tot_hit));
-      atomicAdd(reinterpret_cast<unsigned long long*>(&d.row_stats[2]), static_cast<unsigned long long>(tot_miss));
-    }
+    w.totals[1] = tot_hit;
+    w.totals[2] = tot_miss;
   }
 }
 
-static int64_t lds_bytes_for(int64_t length, int64_t hot_rows) {
-  return (3 * words_for(length) + 2 * ((hot_rows + 31) / 32)) * 4;
+// Physical row of input i (-1 when invalid, a later duplicate, or host-less).
+// For a miss, `miss_rank` gets its rank, `slot` its victim slot and `host` its
+// host row; otherwise miss_rank = -1.
+__device__ __forceinline__ int64_t row_of_input(const hs_resolve_desc& d, const ResolveWs& w, bool dups,
+                                                int64_t i, int64_t& miss_rank, int32_t& slot,
+                                                int64_t& host) {
+  miss_rank = -1;
+  const int64_t t = load_pos(d, i);
+  const int64_t L = d.length, P = d.page_size, S = d.hot_rows;
+  if (t < 0 || t >= L) return -1;
+  if (dups && bit_of(w.dupbits, t) && w.first_in[t] != static_cast<int32_t>(i)) return -1;
+  const int64_t page = t / P;
+  const int64_t off = t - page * P;
+  const int32_t src = d.source[page];
+  if (src < 0) return -1;
+  const int32_t res = d.resident[page];
+  if (res >= 0) return static_cast<int64_t>(res) * P + off;
+  const int64_t word = t >> 5;
+  const uint32_t bit = 1u << (t & 31);
+  if (w.hitbits[word] & bit) {
+    slot = w.tslot[t];
+  } else {
+    miss_rank = w.mprefix[word] + __popc(w.missbits[word] & (bit - 1u));
+    slot = w.victims[miss_rank < S - 1 ? miss_rank : S - 1];
+    host = static_cast<int64_t>(src) * P + off;
+  }
+  if (slot < 0 || slot >= S) {  // only with an LRU that is not a permutation of the slots
+    host = -1;
+    return -1;
+  }
+  const int64_t hb = slot / P;
+  return static_cast<int64_t>(d.hot[hb]) * P + (slot - hb * P);
 }
+
+// ---- outputs: rows per input and per head column, miss plan, new tags, counts
+__global__ __launch_bounds__(RW) void resolve_outputs_kernel(ResolveBatch batch) {
+  const hs_resolve_desc& d = batch.d[blockIdx.y];
+  const ResolveWs w = ws_of(d);
+  const int64_t n = d.n, S = d.hot_rows;
+  const int64_t e = static_cast<int64_t>(blockIdx.x) * RW + threadIdx.x;
+  const int64_t tot_miss = w.totals[2];
+  const bool dups = w.totals[3] != 0;
+  if (e < n) {
+    int64_t rank, host = -1;
+    int32_t slot = -1;
+    const int64_t r = row_of_input(d, w, dups, e, rank, slot, host);
+    if (d.union_physical) d.union_physical[e] = r;
+    if (!d.head_columns && d.physical != d.union_physical) d.physical[e] = r;
+    if (rank >= 0) {
+      d.miss_host_rows[rank] = host;
+      d.miss_device_rows[rank] = r;
+      if (r >= 0 && (rank < S - 1 || rank == tot_miss - 1)) d.tags[slot] = static_cast<int32_t>(host);
+    }
+    if (e >= tot_miss) {
+      d.miss_host_rows[e] = -1;
+      d.miss_device_rows[e] = -1;
+    }
+    if (e == 0) {
+      const int64_t c0 = w.totals[0], c1 = w.totals[1];
+      d.counts[0] = c0;
+      d.counts[1] = c1;
+      d.counts[2] = tot_miss;
+      if (d.row_stats) {
+        atomicAdd(reinterpret_cast<unsigned long long*>(&d.row_stats[0]), static_cast<unsigned long long>(c0));
+        atomicAdd(reinterpret_cast<unsigned long long*>(&d.row_stats[1]), static_cast<unsigned long long>(c1));
+        atomicAdd(reinterpret_cast<unsigned long long*>(&d.row_stats[2]), static_cast<unsigned long long>(tot_miss));
+      }
+    }
+    return;
+  }
+  if (!d.head_columns) return;
+  // per-head remap (row_index.py:127-131)
+  const int64_t k = e - n;
+  if (k >= d.heads * d.width) return;
+  const int64_t h = k / d.width, jj = k - h * d.width;
+  const int64_t col = d.head_columns[h * d.hc_stride_h + jj * d.hc_stride_w];
+  int64_t r = -1;
+  if (col >= 0 && col < n) {
+    int64_t rank, host;
+    int32_t slot;
+    r = row_of_input(d, w, dups, col, rank, slot, host);
+  }
+  d.physical[k] = r;
+}
+
+static int64_t mark_lds_bytes(int64_t length) { return 2 * words_for(length) * 4; }
+static int64_t order_lds_bytes(int64_t hot_rows) { return (hot_rows + 31) / 32 * 4; }
 
 constexpr int64_t kMaxResolverLds = 150 * 1024;
 
@@ -414,11 +567,13 @@ static int validate_desc(const hs_resolve_desc& d) {
   HS_CHECK_ARG(d.hot_rows >= 1 && d.hot_rows <= RT * LRU_CHUNK, "hot_rows must be in [1, 32768]");
   HS_CHECK_ARG(d.hot_blocks * d.page_size >= d.hot_rows, "hot block table does not cover hot_rows");
   HS_CHECK_ARG(d.length < (static_cast<int64_t>(1) << 31), "length too large");
-  HS_CHECK_ARG(lds_bytes_for(d.length, d.hot_rows) <= kMaxResolverLds,
+  HS_CHECK_ARG(mark_lds_bytes(d.length) <= kMaxResolverLds,
                "length %lld too large for the LDS token bitmaps", static_cast<long long>(d.length));
   if (d.head_columns) HS_CHECK_ARG(d.heads >= 1 && d.width >= 1, "head columns must be a nonempty matrix");
   return HS_OK;
 }
+
+static int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 }  // namespace hs
 
@@ -426,10 +581,10 @@ using namespace hs;
 
 extern "C" int64_t hs_resolve_workspace_bytes(int64_t n, int64_t length, int64_t n_pages,
                                               int64_t hot_rows) {
-  if (n < 1) n = 1;
+  (void)n;
   if (length < 1) length = 1;
   if (hot_rows < 1) hot_rows = 1;
-  return ws_layout(n, length, n_pages, hot_rows, nullptr, nullptr);
+  return ws_layout(length, n_pages, hot_rows, nullptr, nullptr);
 }
 
 extern "C" int hs_resolve_rows_batched(const hs_resolve_desc* descs, int32_t count, void* workspace,
@@ -443,27 +598,40 @@ extern "C" int hs_resolve_rows_batched(const hs_resolve_desc* descs, int32_t cou
   }
   HS_CHECK_ARG(workspace != nullptr && workspace_bytes >= need,
                "resolver workspace too small: need %lld bytes", static_cast<long long>(need));
+  static bool attr_set = false;
+  if (!attr_set) {
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(resolve_mark_kernel),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kMaxResolverLds));
+    (void)hipGetLastError();
+    attr_set = true;
+  }
   char* ws = static_cast<char*>(workspace);
   for (int32_t start = 0; start < count; start += RMAXB) {
     ResolveBatch batch{};
     batch.count = count - start < RMAXB ? count - start : RMAXB;
-    int64_t lds = 0;
+    int64_t mark_lds = 0, order_lds = 0, max_s = 0, max_out = 0;
     for (int i = 0; i < batch.count; ++i) {
-      batch.d[i] = descs[start + i];
-      batch.d[i].workspace = ws;
-      ws += hs_resolve_workspace_bytes(batch.d[i].n, batch.d[i].length, batch.d[i].n_pages, batch.d[i].hot_rows);
-      const int64_t l = lds_bytes_for(batch.d[i].length, batch.d[i].hot_rows);
-      if (l > lds) lds = l;
+      hs_resolve_desc& d = batch.d[i];
+      d = descs[start + i];
+      d.workspace = ws;
+      ws += hs_resolve_workspace_bytes(d.n, d.length, d.n_pages, d.hot_rows);
+      if (mark_lds_bytes(d.length) > mark_lds) mark_lds = mark_lds_bytes(d.length);
+      if (order_lds_bytes(d.hot_rows) > order_lds) order_lds = order_lds_bytes(d.hot_rows);
+      if (d.hot_rows > max_s) max_s = d.hot_rows;
+      const int64_t outs = d.n + (d.head_columns ? d.heads * d.width : 0);
+      if (outs > max_out) max_out = outs;
     }
-    static bool attr_set = false;
-    if (!attr_set) {
-      (void)hipFuncSetAttribute(reinterpret_cast<const void*>(resolve_kernel),
-                          hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kMaxResolverLds));
-      (void)hipGetLastError();
-      attr_set = true;
-    }
-    hipLaunchKernelGGL(resolve_kernel, dim3(batch.count), dim3(RT), static_cast<size_t>(lds), stream, batch);
-    HS_CHECK_LAUNCH("resolver");
+    const unsigned nb = static_cast<unsigned>(batch.count);
+    hipLaunchKernelGGL(resolve_mark_kernel, dim3(nb), dim3(RT), static_cast<size_t>(mark_lds), stream, batch);
+    HS_CHECK_LAUNCH("resolver mark");
+    hipLaunchKernelGGL(resolve_tags_kernel, dim3(static_cast<unsigned>(ceil_div(max_s, RW)), nb), dim3(RW), 0,
+                       stream, batch);
+    HS_CHECK_LAUNCH("resolver tags");
+    hipLaunchKernelGGL(resolve_order_kernel, dim3(nb), dim3(RT), static_cast<size_t>(order_lds), stream, batch);
+    HS_CHECK_LAUNCH("resolver order");
+    hipLaunchKernelGGL(resolve_outputs_kernel, dim3(static_cast<unsigned>(ceil_div(max_out, RW)), nb), dim3(RW),
+                       0, stream, batch);
+    HS_CHECK_LAUNCH("resolver outputs");
   }
   return HS_OK;
 }
