@@ -119,26 +119,95 @@ __device__ __forceinline__ float from_bits(unsigned short v) {
 }
 
 // One workgroup (4 waves) per (split, KV head x head chunk, request).  The
-// split's entries (K element offset, head mask) are staged in LDS once; each
-// wave then walks tiles w, w+4, ... of 32 entries, loading the next tile's K
-// fragments and V rows into registers while the current tile computes.
-constexpr int ACH = 512;  // entries per workgroup (chunk) of the MFMA kernel
+// split's entries (K element offset, head mask) are staged in LDS once with
+// two batched rounds of loads (entry lists, then physical rows); each wave
+// then walks tiles w, w+4, ... of 32 entries with two register buffers used in
+// turn: the loads of tile t+4 are in flight while tile t computes, and no
+// buffer is copied (a copy would make the compiler wait for the loads).
+constexpr int ACH = 2048;        // entries per workgroup (chunk) of the MFMA kernel
 
-template <int DT, int DP>
-__global__ __launch_bounds__(256) void attend_mfma_kernel(AttendArgs a) {
+// Waves per workgroup of the MFMA kernel: 8 (4 for head_dim 256, whose V tiles
+// and wave-merge buffer would not fit in LDS).
+__host__ __device__ constexpr int attend_waves(int DP) { return DP <= 128 ? 8 : 4; }
+
+// Physical row and head mask of entries e0 + i, i = threadIdx.x + s * NTH < cnt
+// (rows outside the pool are masked); every load is issued before any use.
+template <int MODE, int NTH, int SPT>
+__device__ __forceinline__ void stage_entries(const AttendArgs& a, int64_t b, int64_t k, int64_t e0, int cnt,
+                                              int64_t (&ph)[SPT], uint32_t (&mk)[SPT]) {
+  if constexpr (MODE == MODE_GROUPS) {
+    int32_t col[SPT];
+    const int64_t base = b * a.e_sb + k * a.e_sk + e0;
+#pragma unroll
+    for (int s = 0; s < SPT; ++s) {
+      const int i = threadIdx.x + s * NTH;
+      const int ic = i < cnt ? i : 0;
+      col[s] = a.ecol[base + ic];
+      mk[s] = a.emask[base + ic];
+    }
+#pragma unroll
+    for (int s = 0; s < SPT; ++s) {
+      const int i = threadIdx.x + s * NTH;
+      const bool ok = i < cnt && col[s] >= 0;
+      const int64_t pv = a.uphys[b * a.u_sb + (ok ? col[s] : 0)];
+      ph[s] = ok ? pv : -1;
+    }
+  } else if constexpr (MODE == MODE_ROWS) {
+#pragma unroll
+    for (int s = 0; s < SPT; ++s) {
+      const int i = threadIdx.x + s * NTH;
+      const int64_t e = e0 + (i < cnt ? i : 0);
+      const int64_t hl = e / a.width, j = e - hl * a.width;
+      const int64_t pv = a.rows[b * a.r_sb + (k * a.g + hl) * a.r_sh + j * a.r_sw];
+      ph[s] = i < cnt ? pv : -1;
+      mk[s] = 1u << hl;
+    }
+  } else {
+    const uint32_t all = a.g >= 32 ? 0xffffffffu : ((1u << a.g) - 1u);
+#pragma unroll
+    for (int s = 0; s < SPT; ++s) {
+      const int i = threadIdx.x + s * NTH;
+      const int64_t pv = a.rows[b * a.r_sb + (e0 + (i < cnt ? i : 0)) * a.r_sw];
+      ph[s] = i < cnt ? pv : -1;
+      mk[s] = all;
+    }
+  }
+#pragma unroll
+  for (int s = 0; s < SPT; ++s)
+    if (ph[s] < 0 || ph[s] >= a.pool_rows) {
+      ph[s] = -1;
+      mk[s] = 0u;
+    }
+}
+
+template <int MODE>
+__device__ __forceinline__ int64_t entry_total(const AttendArgs& a, int64_t b, int64_t k) {
+  if constexpr (MODE == MODE_ROWS) return a.g * a.width;
+  else if constexpr (MODE == MODE_SHARED) return a.width;
+  else {
+    const int64_t e = a.ecount[b * a.Hkv + k];
+    return e < 0 ? 0 : (e > a.emax ? a.emax : e);
+  }
+}
+
+template <int DT, int DP, int MODE>
+__global__ __launch_bounds__(64 * attend_waves(DP)) void attend_mfma_kernel(AttendArgs a) {
+  constexpr int AW = attend_waves(DP);
+  constexpr int NTH = 64 * AW;
+  constexpr int SPT = ACH / NTH;  // entries staged per thread
   constexpr int NT = DP / 16;   // PV M-tiles over d
   constexpr int KK = DP / 32;   // QK k-steps over d
   constexpr int RS = DP + 8;    // LDS row stride of the V tile (elements)
   constexpr int LPR = DP / 8;   // lanes per row for 16-byte V loads
   constexpr int RPI = 64 / LPR; // rows per V load instruction
   constexpr int VI = 32 / RPI;  // V load instructions per 32-row tile
-  constexpr int VS_BYTES = 4 * 32 * RS * 2;
-  constexpr int MERGE_BYTES = 4 * 16 * DP * 4;
+  constexpr int VS_BYTES = AW * 32 * RS * 2;
+  constexpr int MERGE_BYTES = AW * 16 * DP * 4;
   constexpr int SMEM = VS_BYTES > MERGE_BYTES ? VS_BYTES : MERGE_BYTES;
   __shared__ __attribute__((aligned(16))) unsigned char smem[SMEM];
   __shared__ int64_t s_koff[ACH];
   __shared__ uint32_t s_mask[ACH];
-  __shared__ float s_m[4][16], s_l[4][16];
+  __shared__ float s_m[AW][16], s_l[AW][16];
 
   unsigned short* vs_all = reinterpret_cast<unsigned short*>(smem);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -152,32 +221,46 @@ __global__ __launch_bounds__(256) void attend_mfma_kernel(AttendArgs a) {
   const unsigned short* pool = static_cast<const unsigned short*>(a.pool);
   unsigned short* vs = vs_all + wave * 32 * RS;
 
-  const int64_t E = entry_count(a, b, k);
+  const int64_t E = entry_total<MODE>(a, b, k);
   const int64_t e0 = split * a.chunk;
   int64_t e1 = e0 + a.chunk;
   if (e1 > E) e1 = E;
   const int cnt = e1 > e0 ? static_cast<int>(e1 - e0) : 0;
-  for (int i = threadIdx.x; i < ACH; i += 256) {
-    int64_t koff = -1;
-    uint32_t mk = 0;
-    if (i < cnt) {
-      int64_t ph;
-      entry_at(a, b, k, e0 + i, ph, mk);
-      if (ph >= 0) koff = k_offset(ph, k, P, Hkv, D);
+  if (cnt == 0) {  // empty split: a partial that the merge ignores
+    for (int idx = threadIdx.x; idx < 16 * DP; idx += NTH) {
+      const int head = idx / DP, d = idx % DP;
+      const int hl = 16 * hchunk + head;
+      if (hl >= a.g || d >= D) continue;
+      const int64_t pidx = (b * a.Hq + k * a.g + hl) * a.splits + split;
+      if (d == 0) {
+        a.part_m[pidx] = -INFINITY;
+        a.part_l[pidx] = 0.f;
+      }
+      a.part_o[pidx * D + d] = 0.f;
     }
-    s_koff[i] = koff;
-    s_mask[i] = mk;
+    return;
+  }
+  {
+    int64_t ph[SPT];
+    uint32_t mk[SPT];
+    stage_entries<MODE, NTH, SPT>(a, b, k, e0, cnt, ph, mk);
+#pragma unroll
+    for (int s = 0; s < SPT; ++s) {
+      const int i = threadIdx.x + s * NTH;
+      s_koff[i] = ph[s] >= 0 ? k_offset(ph[s], k, P, Hkv, D) : -1;
+      s_mask[i] = mk[s];
+    }
   }
 
   // Q^T fragments: lane holds Q[head hh][d = 32kk + 8j .. +8]
   u32x4 qf[KK];
+  const unsigned short* qrow = static_cast<const unsigned short*>(a.q) + b * a.q_sb + k * a.g * a.q_sh;
   {
-    const unsigned short* q0 = static_cast<const unsigned short*>(a.q) + b * a.q_sb + k * a.g * a.q_sh;
 #pragma unroll
     for (int kk = 0; kk < KK; ++kk) {
       const int d0 = 32 * kk + 8 * j;
       const bool ok = hh < a.g && d0 < D;
-      const u32x4 v = load16(ok ? q0 + hh * a.q_sh + d0 : q0);
+      const u32x4 v = load16(ok ? qrow + hh * a.q_sh + d0 : qrow);
       qf[kk] = ok ? v : u32x4{0u, 0u, 0u, 0u};
     }
   }
@@ -192,24 +275,23 @@ __global__ __launch_bounds__(256) void attend_mfma_kernel(AttendArgs a) {
 
   const int ntiles = (cnt + 31) / 32;
   // K fragments (A operand: lane holds K[row 16rt + c][d = 32kk + 8j .. +8]) and the
-  // V rows this lane stages (row vi*RPI + lane/LPR, d = 8*(lane%LPR) .. +8) of tile t
-  // Loads are unconditional so that a tile's loads stay in flight together: a
-  // masked lane reads its own query row instead (always in bounds) and its
-  // value is replaced by zero afterwards.
-  const unsigned short* qrow = static_cast<const unsigned short*>(a.q) + b * a.q_sb + k * a.g * a.q_sh;
-  const u32x4 zero4 = {0u, 0u, 0u, 0u};
+  // V rows this lane stages (row vi*RPI + lane/LPR, d = 8*(lane%LPR) .. +8) of tile t.
+  // Loads are unconditional and their results are used as loaded, so that the
+  // loads of a tile stay in flight until the tile is processed: a masked lane
+  // reads its own query row instead (in bounds, finite).  That data never
+  // reaches the output: a masked entry's score is -inf (probability 0, so its
+  // V contributes 0), K columns at d >= D meet zero Q fragments, and output
+  // columns d >= D are not written.
   auto load_tile = [&](int t, u32x4 (&kf)[2][KK], u32x4 (&vr)[VI]) {
 #pragma unroll
     for (int rt = 0; rt < 2; ++rt) {
       const int li = 32 * t + 16 * rt + c;
       const int64_t koff = s_koff[li < ACH ? li : 0];
-      const bool row_ok = li < ACH && koff >= 0;
+      const bool row_ok = li < cnt && koff >= 0;
 #pragma unroll
       for (int kk = 0; kk < KK; ++kk) {
         const int d0 = 32 * kk + 8 * j;
-        const bool ok = row_ok && d0 < D;
-        const u32x4 v = load16(ok ? pool + koff + d0 : qrow);
-        kf[rt][kk] = ok ? v : zero4;
+        kf[rt][kk] = load16(row_ok && d0 < D ? pool + koff + d0 : qrow);
       }
     }
 #pragma unroll
@@ -217,17 +299,12 @@ __global__ __launch_bounds__(256) void attend_mfma_kernel(AttendArgs a) {
       const int li = 32 * t + vi * RPI + lane / LPR;
       const int cc = lane % LPR;
       const int64_t koff = s_koff[li < ACH ? li : 0];
-      const bool ok = li < ACH && koff >= 0 && 8 * cc < D;
-      const u32x4 v = load16(ok ? pool + koff + vplane + 8 * cc : qrow);
-      vr[vi] = ok ? v : zero4;
+      const bool ok = li < cnt && koff >= 0 && 8 * cc < D;
+      vr[vi] = load16(ok ? pool + koff + vplane + 8 * cc : qrow);
     }
   };
 
-  u32x4 kf[2][KK], vr[VI];
-  if (wave < ntiles) load_tile(wave, kf, vr);
-  for (int t = wave; t < ntiles; t += 4) {
-    u32x4 kn[2][KK], vn[VI];
-    load_tile(t + 4 < ntiles ? t + 4 : ACH / 32, kn, vn);  // past the end: every lane masked
+  auto process = [&](int t, const u32x4 (&kf)[2][KK], const u32x4 (&vr)[VI]) {
     // V rows of this tile into LDS
 #pragma unroll
     for (int vi = 0; vi < VI; ++vi) {
@@ -239,10 +316,10 @@ __global__ __launch_bounds__(256) void attend_mfma_kernel(AttendArgs a) {
     f32x4 st[2];
 #pragma unroll
     for (int rt = 0; rt < 2; ++rt) {
-      f32x4 s = {0.f, 0.f, 0.f, 0.f};
+      f32x4 sacc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int kk = 0; kk < KK; ++kk) s = mfma16x16x32<DT>(kf[rt][kk], qf[kk], s);
-      st[rt] = s;
+      for (int kk = 0; kk < KK; ++kk) sacc = mfma16x16x32<DT>(kf[rt][kk], qf[kk], sacc);
+      st[rt] = sacc;
     }
 
     // online softmax for head hh over rows 16rt + 4j + i
@@ -252,11 +329,11 @@ __global__ __launch_bounds__(256) void attend_mfma_kernel(AttendArgs a) {
     for (int rt = 0; rt < 2; ++rt) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const uint32_t mk = s_mask[32 * t + 16 * rt + 4 * j + i];
-        const bool valid = hh < 32 && ((mk >> hbit_shift) & 1u);
-        const float s = valid ? st[rt][i] * a.scale : -INFINITY;
-        sv[rt][i] = s;
-        tmax = fmaxf(tmax, s);
+        const uint32_t mkv = s_mask[32 * t + 16 * rt + 4 * j + i];
+        const bool valid = hh < 32 && ((mkv >> hbit_shift) & 1u);
+        const float sc = valid ? st[rt][i] * a.scale : -INFINITY;
+        sv[rt][i] = sc;
+        tmax = fmaxf(tmax, sc);
       }
     }
     tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
@@ -269,8 +346,8 @@ __global__ __launch_bounds__(256) void attend_mfma_kernel(AttendArgs a) {
     for (int rt = 0; rt < 2; ++rt) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float p = (sv[rt][i] == -INFINITY) ? 0.f : __expf(sv[rt][i] - m_new);
-        const unsigned short bits = to_bits<DT>(p);
+        const float pr = (sv[rt][i] == -INFINITY) ? 0.f : __expf(sv[rt][i] - m_new);
+        const unsigned short bits = to_bits<DT>(pr);
         pb[4 * rt + i] = bits;
         psum += from_bits<DT>(bits);
       }
@@ -304,12 +381,26 @@ __global__ __launch_bounds__(256) void attend_mfma_kernel(AttendArgs a) {
       acc[mt] = mfma16x16x32<DT>(vf, pf, acc[mt]);
     }
     wave_lds_sync();  // all reads of this tile done before the next overwrites it
-#pragma unroll
-    for (int rt = 0; rt < 2; ++rt)
-#pragma unroll
-      for (int kk = 0; kk < KK; ++kk) kf[rt][kk] = kn[rt][kk];
-#pragma unroll
-    for (int vi = 0; vi < VI; ++vi) vr[vi] = vn[vi];
+  };
+
+  u32x4 kA[2][KK], vA[VI], kB[2][KK], vB[VI];
+  int t = wave;
+  if (t < ntiles) {  // uniform per wave
+    load_tile(t, kA, vA);
+    // the scheduling barriers keep each prefetch ahead of the wait for the
+    // tile before it (the scheduler would otherwise sink the loads below it)
+    while (true) {
+      load_tile(t + AW, kB, vB);  // past the end: every lane masked
+      __builtin_amdgcn_sched_barrier(0);
+      process(t, kA, vA);
+      t += AW;
+      if (t >= ntiles) break;
+      load_tile(t + AW, kA, vA);
+      __builtin_amdgcn_sched_barrier(0);
+      process(t, kB, vB);
+      t += AW;
+      if (t >= ntiles) break;
+    }
   }
 
   // per-wave totals over the four lane groups that share a head
@@ -317,7 +408,7 @@ __global__ __launch_bounds__(256) void attend_mfma_kernel(AttendArgs a) {
   l_run += __shfl_xor(l_run, 32, 64);
 
   __syncthreads();
-  float* mo = reinterpret_cast<float*>(smem);  // [4][16][DP]
+  float* mo = reinterpret_cast<float*>(smem);  // [AW][16][DP]
   if (j == 0) {
     s_m[wave][c] = m_run;
     s_l[wave][c] = l_run;
@@ -329,18 +420,18 @@ __global__ __launch_bounds__(256) void attend_mfma_kernel(AttendArgs a) {
   }
   __syncthreads();
 
-  // merge the four waves and write this split's partial for each real head
-  for (int idx = threadIdx.x; idx < 16 * DP; idx += 256) {
+  // merge the waves and write this split's partial for each real head
+  for (int idx = threadIdx.x; idx < 16 * DP; idx += NTH) {
     const int head = idx / DP, d = idx % DP;
     const int hl = 16 * hchunk + head;
     if (hl >= a.g || d >= D) continue;
     float M = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < 4; ++w) M = fmaxf(M, s_m[w][head]);
+    for (int w = 0; w < AW; ++w) M = fmaxf(M, s_m[w][head]);
     float L = 0.f, O = 0.f;
     if (M != -INFINITY) {
 #pragma unroll
-      for (int w = 0; w < 4; ++w) {
+      for (int w = 0; w < AW; ++w) {
         const float f = (s_m[w][head] == -INFINITY) ? 0.f : __expf(s_m[w][head] - M);
         L += f * s_l[w][head];
         O += f * mo[(w * 16 + head) * DP + d];
@@ -460,10 +551,10 @@ static Plan plan_attend(int dtype, int64_t B, int64_t Hq, int64_t Hkv, int64_t D
   if (p.mfma) {
     p.dp = D <= 32 ? 32 : D <= 64 ? 64 : D <= 128 ? 128 : 256;
     p.head_chunks = static_cast<int>(ceil_div(g, 16));
-    // entries per workgroup: enough workgroups to cover the chip ~3 times,
-    // at most ACH (the LDS entry list), at least 128
+    // entries per workgroup: about one (8-wave) workgroup per CU for the
+    // largest entry lists, at most ACH (the LDS entry list), at least 128
     const int64_t groups = B * Hkv * p.head_chunks;
-    int64_t chunk = ceil_div(ceil_div(groups * max_entries, 768), 32) * 32;
+    int64_t chunk = ceil_div(ceil_div(groups * max_entries, 256), 32) * 32;
     static const int64_t forced = [] {
       const char* env = getenv("HS_ATTEND_CHUNK");
       return env ? atoll(env) : 0;
@@ -494,16 +585,23 @@ static int64_t workspace_for(const Plan& p, int64_t B, int64_t Hq, int64_t D) {
   return (2 * n + n * D) * 4 + 256;
 }
 
-template <int DT>
-static void launch_mfma(const Plan& p, const AttendArgs& a, hipStream_t s) {
+template <int DT, int MODE>
+static void launch_mfma_mode(const Plan& p, const AttendArgs& a, hipStream_t s) {
   dim3 grid(static_cast<unsigned>(p.splits), static_cast<unsigned>(a.Hkv * p.head_chunks),
             static_cast<unsigned>(a.B));
   switch (p.dp) {
-    case 32: hipLaunchKernelGGL((attend_mfma_kernel<DT, 32>), grid, dim3(256), 0, s, a); break;
-    case 64: hipLaunchKernelGGL((attend_mfma_kernel<DT, 64>), grid, dim3(256), 0, s, a); break;
-    case 128: hipLaunchKernelGGL((attend_mfma_kernel<DT, 128>), grid, dim3(256), 0, s, a); break;
-    default: hipLaunchKernelGGL((attend_mfma_kernel<DT, 256>), grid, dim3(256), 0, s, a); break;
+    case 32: hipLaunchKernelGGL((attend_mfma_kernel<DT, 32, MODE>), grid, dim3(64 * attend_waves(32)), 0, s, a); break;
+    case 64: hipLaunchKernelGGL((attend_mfma_kernel<DT, 64, MODE>), grid, dim3(64 * attend_waves(64)), 0, s, a); break;
+    case 128: hipLaunchKernelGGL((attend_mfma_kernel<DT, 128, MODE>), grid, dim3(64 * attend_waves(128)), 0, s, a); break;
+    default: hipLaunchKernelGGL((attend_mfma_kernel<DT, 256, MODE>), grid, dim3(64 * attend_waves(256)), 0, s, a); break;
   }
+}
+
+template <int DT>
+static void launch_mfma(const Plan& p, const AttendArgs& a, hipStream_t s) {
+  if (a.mode == MODE_GROUPS) launch_mfma_mode<DT, MODE_GROUPS>(p, a, s);
+  else if (a.mode == MODE_SHARED) launch_mfma_mode<DT, MODE_SHARED>(p, a, s);
+  else launch_mfma_mode<DT, MODE_ROWS>(p, a, s);
 }
 
 static int run_attend(int dtype, AttendArgs a, int64_t max_entries, void* out, int64_t o_sb,

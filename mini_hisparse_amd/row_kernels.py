@@ -71,9 +71,19 @@ def gather_rows(host, pool, plan, config, *, miss_count=None):
     _lib.check(status, "hs_gather_rows")
 
 
+# Attention workspaces, one per (device, stream), grown on demand.  Launches on
+# one stream run in order, so the calls of a stream can share its workspace.
+_ATTEND_WS = {}
+
+
 def _attend_workspace(dtype_code, batch, heads, kv_heads, head_dim, max_entries, device):
     size = _lib.load().hs_attend_workspace_bytes(dtype_code, batch, heads, kv_heads, head_dim, max_entries)
-    return torch.empty(size, dtype=torch.uint8, device=device), size
+    key = (device, torch.cuda.current_stream(device).cuda_stream)
+    ws = _ATTEND_WS.get(key)
+    if ws is None or ws.numel() < size:
+        ws = torch.empty(max(size, 1 << 16), dtype=torch.uint8, device=device)
+        _ATTEND_WS[key] = ws
+    return ws, ws.numel()
 
 
 def _check_query(query, pool, config):
