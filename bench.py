@@ -39,6 +39,9 @@ def parse_args():
     p.add_argument("--seed", type=int, default=2024)
     p.add_argument("--no-cpu-baseline", action="store_true", help="skip the CPU oracle leg")
     p.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU sample work")
+    p.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                   help="summarise two rocprofv3 --pmc runs of this script (FETCH_SIZE, WRITE_SIZE) "
+                        "into profiles/microbench_pmc.txt and exit")
     return p.parse_args()
 
 
@@ -295,8 +298,82 @@ def cpu_baseline(torch, w, budget_s):
     }, parity
 
 
+PMC_SUMMARY = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "microbench_pmc.txt")
+ROOFLINE_KERNELS = ("attend_mfma_kernel", "attend_merge_kernel")
+CALIBRATION_BYTES = 1 << 30  # hbm_copy_gbs: a plain device-to-device copy of 1 GiB
+
+
+def summarize_pmc(fetch_dir, write_dir, out_path=PMC_SUMMARY):
+    """Per-dispatch FETCH_SIZE / WRITE_SIZE of each hs:: kernel, scaled by what the
+    same counters read for the 1 GiB device copy this script makes."""
+    import csv
+    import glob
+    from collections import defaultdict
+
+    def load(d, counter):
+        (path,) = glob.glob(os.path.join(d, "*counter_collection.csv"))
+        rows = {}
+        for r in csv.DictReader(open(path)):
+            if r["Counter_Name"] == counter:
+                rows[int(r["Dispatch_Id"])] = (r["Kernel_Name"], float(r["Counter_Value"]))
+        return rows
+
+    fetch, write = load(fetch_dir, "FETCH_SIZE"), load(write_dir, "WRITE_SIZE")
+    kib = CALIBRATION_BYTES / 1024
+    calib = [i for i, (name, v) in write.items() if "copyBuffer" in name and abs(v - kib) < 0.01 * kib
+             and i in fetch and abs(fetch[i][1] - kib) < 0.6 * kib]
+    if not calib:
+        raise SystemExit("no 1 GiB device copy found in the counter runs")
+    fetch_scale = kib / float(np.mean([fetch[i][1] for i in calib]))
+    write_scale = kib / float(np.mean([write[i][1] for i in calib]))
+    per = defaultdict(lambda: [[], []])
+    for i, (name, v) in fetch.items():
+        if "hs::" in name:
+            per[name.split("(")[0].replace("void ", "")][0].append(v)
+    for i, (name, v) in write.items():
+        if "hs::" in name:
+            per[name.split("(")[0].replace("void ", "")][1].append(v)
+    lines = [
+        "# rocprofv3 --pmc summary: microbench step (BASELINE configs[1]), batch 8, bf16",
+        "# FETCH_SIZE and WRITE_SIZE (KiB per dispatch) from two runs of",
+        "#   rocprofv3 --pmc FETCH_SIZE -f csv -d <dir> -o bench -- python bench.py --steps 3 --warmup 1 --no-cpu-baseline",
+        "#   rocprofv3 --pmc WRITE_SIZE -f csv -d <dir> -o bench -- python bench.py --steps 3 --warmup 1 --no-cpu-baseline",
+        "# summarised by: python bench.py --summarize-pmc <fetch dir> <write dir>",
+        f"# calibration: the 1 GiB device-to-device copy of hbm_copy_gbs ({len(calib)} dispatches) reads "
+        f"FETCH_SIZE x{fetch_scale:.3f}, WRITE_SIZE x{write_scale:.3f} of its true bytes",
+        f"calibration fetch_scale {fetch_scale:.4f} write_scale {write_scale:.4f}",
+        "# kernel  dispatches  fetch_bytes_per_dispatch  write_bytes_per_dispatch  (scaled)",
+    ]
+    for name in sorted(per):
+        f, w = per[name]
+        fb = float(np.mean(f)) * 1024 * fetch_scale if f else 0.0
+        wb = float(np.mean(w)) * 1024 * write_scale if w else 0.0
+        lines.append(f"kernel {name.replace('hs::', '').replace(' ', '')} {len(f)} {fb:.0f} {wb:.0f}")
+    with open(out_path, "w") as fh:
+        fh.write("\n".join(lines) + "\n")
+    print("\n".join(lines))
+
+
+def pmc_traffic(kernels=ROOFLINE_KERNELS, path=PMC_SUMMARY):
+    """HBM bytes per launch of `kernels` (sum) from the committed counter summary, or None."""
+    if not os.path.exists(path):
+        return None
+    total, found = 0.0, set()
+    for line in open(path):
+        parts = line.split()
+        if len(parts) == 5 and parts[0] == "kernel":
+            for k in kernels:
+                if parts[1].startswith(k):
+                    total += float(parts[3]) + float(parts[4])
+                    found.add(k)
+    return total if found == set(kernels) else None
+
+
 def main():
     args = parse_args()
+    if args.summarize_pmc:
+        summarize_pmc(*args.summarize_pmc)
+        return
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on exactly one GPU; --gpus above 1 is not supported "
                           "(the decode path shards by request, see DESIGN.md)", "n_gpus": args.gpus}))
@@ -361,7 +438,7 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": att_gbs / HBM_PEAK_GBS,
-            "traffic": None,
+            "traffic": pmc_traffic(),
             "kernel": "attend_mfma_kernel + attend_merge_kernel (hs_attend_groups)",
         },
         "kernels": kernels,
