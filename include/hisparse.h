@@ -184,6 +184,34 @@ int hs_gather_rows_batched(const void* const* host_alias, void* pool,
                            int64_t page_size, int64_t row_bytes, int32_t grid_x,
                            hs_stream_t stream);
 
+/* ------------------------------------------------------- append (producer) */
+
+/*
+ * Append one token's K and V rows for each of `batch` (<= 32) (request, layer)
+ * pairs: the decode-step producer of the Quest bounds.
+ * Replaces: the single-token case of HostStore.append
+ * (mini_hisparse/storage.py:246-319): the new rows go to their pool row; the
+ * tail page's minimum/maximum [kv_heads, head_dim] take the element-wise
+ * min/max with the new K row exactly as torch.minimum/torch.maximum compute
+ * it on the device (a NaN operand is returned, the existing bound first;
+ * 16-bit types: old < new ? old : new, so equal zeros give the new one;
+ * float32: -0 below +0); the rows are mirrored into the pinned host pool through
+ * its device alias (the reference queues a device-to-host copy).  The page
+ * mean-K summary (selector "mean" only) is not produced here.
+ *   k, v          [batch, kv_heads, head_dim], pool dtype, kv_stride_b elements between pairs
+ *   pool          [gpu_pages, 2, P, Hkv, D]; pool_rows = gpu_pages * P
+ *   device_rows   host array [batch]: pool row (block * P + offset) of the new token
+ *   host_alias    host array [batch] of device aliases of pinned host pools (nullable
+ *                 when host_rows is NULL); host_rows host array [batch], < 0 skips the
+ *                 mirror; host_pool_rows bounds every host row
+ *   minimum, maximum  host arrays [batch] of device pointers to the tail page's bounds
+ */
+int hs_append_rows(const void* k, const void* v, int64_t kv_stride_b, void* pool, int64_t pool_rows,
+                   int32_t dtype, int64_t page_size, int64_t kv_heads, int64_t head_dim,
+                   const int64_t* device_rows, const void* const* host_alias, const int64_t* host_rows,
+                   int64_t host_pool_rows, void* const* minimum, void* const* maximum, int32_t batch,
+                   hs_stream_t stream);
+
 /* ------------------------------------------------------------ (4) attention */
 
 /* Scratch bytes of one attention call (split-K partials). */

@@ -83,6 +83,12 @@ SIGNATURES = {
         [POINTER(c_void_p), c_void_p, POINTER(c_void_p), POINTER(c_void_p), POINTER(c_void_p),
          POINTER(c_int64), c_int32, c_int64, c_int64, c_int32, c_void_p],
     ),
+    "hs_append_rows": (
+        c_int,
+        [c_void_p, c_void_p, c_int64, c_void_p, c_int64, c_int32, c_int64, c_int64, c_int64,
+         POINTER(c_int64), POINTER(c_void_p), POINTER(c_int64), c_int64, POINTER(c_void_p),
+         POINTER(c_void_p), c_int32, c_void_p],
+    ),
     "hs_attend_workspace_bytes": (c_int64, [c_int32, c_int64, c_int64, c_int64, c_int64, c_int64]),
     "hs_attend_rows": (
         c_int,

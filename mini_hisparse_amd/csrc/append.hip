@@ -1,0 +1,145 @@
+// One-token append of the decode step for gfx950: the producer of the Quest
+// bounds that the page scorer reads.
+//
+// Replaces the single-token case of HostStore.append (storage.py:246-319) for
+// a batch of (request, layer) pairs: the new K and V rows go to their pool
+// row; the tail page's minimum/maximum take the element-wise min/max with the
+// new K row as torch.minimum/torch.maximum compute it on this device (a NaN
+// operand is returned, the existing bound first; 16-bit types otherwise return
+// old < new ? old : new, so an equal compare -- +0 vs -0 included -- returns
+// the new element; float32 is IEEE minimum/maximum with -0 below +0); and the
+// rows are mirrored
+// into the pinned host pool through its device alias (the reference queues a
+// device-to-host copy on the transfer stream instead).  One workgroup per
+// pair, 16-byte units.
+#include "hs_common.h"
+
+namespace hs {
+
+constexpr int AT = 256;
+constexpr int AMAXB = 32;
+
+struct AppendArgs {
+  const char* k;
+  const char* v;
+  int64_t kv_sb;  // bytes between requests in k and v
+  char* pool;
+  char* host[AMAXB];
+  int64_t dev_row[AMAXB], host_row[AMAXB];
+  char* kmin[AMAXB];
+  char* kmax[AMAXB];
+  int64_t P, row_bytes;
+};
+
+template <int DT>
+__device__ __forceinline__ float from_storage(unsigned short bits) {
+  if constexpr (DT == HS_DTYPE_BF16) return bf16_bits_to_f32(bits);
+  else return f16_bits_to_f32(bits);
+}
+
+template <int DT>
+__device__ __forceinline__ void bound_update(const unsigned short* newv, unsigned short* lo, unsigned short* hi,
+                                             int n) {
+  for (int e = 0; e < n; ++e) {
+    const float x = from_storage<DT>(newv[e]);
+    const float a = from_storage<DT>(lo[e]);
+    const float b = from_storage<DT>(hi[e]);
+    if (!(a != a) && (x != x || !(a < x))) lo[e] = newv[e];
+    if (!(b != b) && (x != x || !(b > x))) hi[e] = newv[e];
+  }
+}
+
+template <int DT>
+__global__ __launch_bounds__(AT) void append_kernel(AppendArgs a) {
+  const int b = blockIdx.x;
+  const int64_t units = a.row_bytes / 16;
+  const uint32_t P32 = static_cast<uint32_t>(a.P);
+  const int64_t dr = a.dev_row[b], hr = a.host_row[b];
+  const uint32_t db = static_cast<uint32_t>(dr) / P32, dof = static_cast<uint32_t>(dr) - db * P32;
+  const int64_t dk = (static_cast<int64_t>(db) * 2 * a.P + dof) * a.row_bytes;  // K row; V row + P * row_bytes
+  const int64_t plane = a.P * a.row_bytes;
+  int64_t hk = -1;
+  if (hr >= 0) {
+    const uint32_t hb = static_cast<uint32_t>(hr) / P32, hof = static_cast<uint32_t>(hr) - hb * P32;
+    hk = (static_cast<int64_t>(hb) * 2 * a.P + hof) * a.row_bytes;
+  }
+  const char* ksrc = a.k + b * a.kv_sb;
+  const char* vsrc = a.v + b * a.kv_sb;
+  for (int64_t u = threadIdx.x; u < units; u += AT) {
+    const u32x4 kx = *reinterpret_cast<const u32x4*>(ksrc + u * 16);
+    const u32x4 vx = *reinterpret_cast<const u32x4*>(vsrc + u * 16);
+    *reinterpret_cast<u32x4*>(a.pool + dk + u * 16) = kx;
+    *reinterpret_cast<u32x4*>(a.pool + dk + plane + u * 16) = vx;
+    if (hk >= 0) {
+      *reinterpret_cast<u32x4*>(a.host[b] + hk + u * 16) = kx;
+      *reinterpret_cast<u32x4*>(a.host[b] + hk + plane + u * 16) = vx;
+    }
+    if constexpr (DT == HS_DTYPE_F32) {
+      float* lo = reinterpret_cast<float*>(a.kmin[b] + u * 16);
+      float* hi = reinterpret_cast<float*>(a.kmax[b] + u * 16);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float x = __uint_as_float(kx[e]);
+        const float a = lo[e], b = hi[e];
+        const bool zero_tie = x == 0.f && a == 0.f;  // both zeros: -0 is the smaller
+        if (!(a != a) && (x != x || x < a || (zero_tie && signbit(x) && !signbit(a)))) lo[e] = x;
+        const bool zero_tie_hi = x == 0.f && b == 0.f;
+        if (!(b != b) && (x != x || x > b || (zero_tie_hi && !signbit(x) && signbit(b)))) hi[e] = x;
+      }
+    } else {
+      unsigned short nv[8];
+      __builtin_memcpy(nv, &kx, 16);
+      bound_update<DT>(nv, reinterpret_cast<unsigned short*>(a.kmin[b] + u * 16),
+                       reinterpret_cast<unsigned short*>(a.kmax[b] + u * 16), 8);
+    }
+  }
+}
+
+}  // namespace hs
+
+using namespace hs;
+
+extern "C" int hs_append_rows(const void* k, const void* v, int64_t kv_stride_b, void* pool, int64_t pool_rows,
+                              int32_t dtype, int64_t page_size, int64_t kv_heads, int64_t head_dim,
+                              const int64_t* device_rows, const void* const* host_alias,
+                              const int64_t* host_rows, int64_t host_pool_rows, void* const* minimum,
+                              void* const* maximum, int32_t batch, hipStream_t stream) {
+  HS_CHECK_ARG(batch >= 1 && batch <= AMAXB, "append batch must be in [1, %d]", AMAXB);
+  HS_CHECK_ARG(valid_dtype(dtype), "invalid dtype code %d", dtype);
+  HS_CHECK_ARG(k && v && pool && device_rows && minimum && maximum, "null append pointer");
+  HS_CHECK_ARG(page_size >= 1 && kv_heads >= 1 && head_dim >= 1, "invalid append shape");
+  const int64_t esz = elem_bytes(dtype);
+  const int64_t row_bytes = kv_heads * head_dim * esz;
+  HS_CHECK_ARG(row_bytes % 16 == 0, "kv_heads * head_dim * element size must be a multiple of 16 bytes");
+  uintptr_t align = reinterpret_cast<uintptr_t>(k) | reinterpret_cast<uintptr_t>(v) |
+                    reinterpret_cast<uintptr_t>(pool) | static_cast<uintptr_t>(kv_stride_b * esz);
+  AppendArgs a{};
+  a.k = static_cast<const char*>(k);
+  a.v = static_cast<const char*>(v);
+  a.kv_sb = kv_stride_b * esz;
+  a.pool = static_cast<char*>(pool);
+  a.P = page_size;
+  a.row_bytes = row_bytes;
+  for (int32_t i = 0; i < batch; ++i) {
+    HS_CHECK_ARG(device_rows[i] >= 0 && device_rows[i] < pool_rows, "append device row %lld outside the pool",
+                 static_cast<long long>(device_rows[i]));
+    HS_CHECK_ARG(!host_rows || host_rows[i] < host_pool_rows, "append host row %lld outside the host pool",
+                 static_cast<long long>(host_rows[i]));
+    HS_CHECK_ARG(minimum[i] && maximum[i], "null bounds pointer");
+    a.dev_row[i] = device_rows[i];
+    a.host_row[i] = host_rows ? host_rows[i] : -1;
+    a.host[i] = host_alias ? static_cast<char*>(const_cast<void*>(host_alias[i])) : nullptr;
+    HS_CHECK_ARG(a.host_row[i] < 0 || a.host[i], "a host row needs a host alias");
+    a.kmin[i] = static_cast<char*>(minimum[i]);
+    a.kmax[i] = static_cast<char*>(maximum[i]);
+    align |= reinterpret_cast<uintptr_t>(a.kmin[i]) | reinterpret_cast<uintptr_t>(a.kmax[i]) |
+             reinterpret_cast<uintptr_t>(a.host[i]);
+  }
+  HS_CHECK_ARG((align & 15) == 0, "append buffers must be 16-byte aligned");
+  const dim3 grid(static_cast<unsigned>(batch));
+  if (dtype == HS_DTYPE_BF16) hipLaunchKernelGGL(append_kernel<HS_DTYPE_BF16>, grid, dim3(AT), 0, stream, a);
+  else if (dtype == HS_DTYPE_F16) hipLaunchKernelGGL(append_kernel<HS_DTYPE_F16>, grid, dim3(AT), 0, stream, a);
+  else hipLaunchKernelGGL(append_kernel<HS_DTYPE_F32>, grid, dim3(AT), 0, stream, a);
+  HS_CHECK_LAUNCH("append");
+  return HS_OK;
+}

@@ -71,6 +71,33 @@ def gather_rows(host, pool, plan, config, *, miss_count=None):
     _lib.check(status, "hs_gather_rows")
 
 
+def append_rows(k, v, pool, device_rows, minimums, maximums, config, *, host=None, host_rows=None, stream=None):
+    """One token's K/V for each of B (request, layer) pairs (storage.py:246-319, one row).
+
+    ``k``/``v`` [B, Hkv, D] in the pool dtype; ``device_rows`` / ``host_rows``
+    Python ints (pool row / host row, ``-1`` skips the mirror); ``minimums`` /
+    ``maximums`` the tail pages' ``[Hkv, D]`` bound tensors; ``host`` a
+    :class:`MappedHost` of the pinned host pool.
+    """
+    batch = k.shape[0]
+    if k.shape != v.shape or k.dim() != 3 or k.dtype != pool.dtype or not (k.is_contiguous() and v.is_contiguous()):
+        raise ValueError("append needs contiguous [B, Hkv, D] K/V in the pool dtype")
+    if not (len(device_rows) == len(minimums) == len(maximums) == batch):
+        raise ValueError("one device row and one pair of bounds per appended token")
+    i64, vp = ctypes.c_int64 * batch, ctypes.c_void_p * batch
+    hrows = None if host_rows is None else i64(*host_rows)
+    alias = None if host is None else vp(*([host.data_ptr()] * batch))
+    host_pool_rows = 0 if host is None else host.tensor.shape[0] * config.page_size
+    s = stream.cuda_stream if stream is not None else _lib.stream_handle(pool.device)
+    status = _lib.load().hs_append_rows(
+        k.data_ptr(), v.data_ptr(), k.stride(0), pool.data_ptr(), pool.shape[0] * config.page_size,
+        _lib.dtype_code(pool.dtype), config.page_size, config.kv_heads, config.head_dim,
+        i64(*device_rows), alias, hrows, host_pool_rows,
+        vp(*[t.data_ptr() for t in minimums]), vp(*[t.data_ptr() for t in maximums]), batch, s,
+    )
+    _lib.check(status, "hs_append_rows")
+
+
 # Attention workspaces, one per (device, stream), grown on demand.  Launches on
 # one stream run in order, so the calls of a stream can share its workspace.
 _ATTEND_WS = {}

@@ -16,6 +16,8 @@ checkout):
                    canonicalisation (``selection.py:18-64``)
 * ``union``     -- ``LogicalTopK.from_selection`` (``row_index.py:20-31``)
 * ``gather``    -- the CPU row gather loop (``mini_hisparse/hybrid.py:466-472``)
+* ``append``    -- the single-token append: pool rows, Quest bounds, host
+                   mirror (``mini_hisparse/storage.py:246-319``)
 * ``attention`` -- the torch row attention (``mini_hisparse/attention.py:26-35``),
                    ``dense_attention`` (``selection.py:158-163``) and
                    ``selection_oracle`` (``selection.py:104-126``)
@@ -34,10 +36,15 @@ Pinning (what each function is checked against, besides the GPU):
   tiny inputs, and the special cases (``top >= count``, forced pages).
 * union     -- reference-generated vectors and an independent formulation.
 * gather    -- byte equality of copied rows with the host rows.
+* append    -- known answers of torch's NaN / signed-zero rule, equality with
+  ``numpy.minimum``/``maximum`` where that rule and numpy's agree (no NaN, no
+  equal zeros), a page filled row by row equals its exact column extrema, and
+  (on the GPU) equality with ``torch.minimum``/``torch.maximum`` themselves.
 * attention -- a scalar textbook softmax in float64 on small inputs, and the
   special cases (all masked -> 0, one row -> V, equal scores -> mean of V).
 """
 
+from .append import append_rows, bound_max, bound_min, takes_new_max, takes_new_min
 from .attention import attend_rows, dense_attention, row_attention_rows, selection_oracle
 from .gather import gather_rows
 from .quest import quest_pages, quest_scores, quest_selection_positions
@@ -45,7 +52,12 @@ from .resolver import resolve_rows
 from .union import from_selection
 
 __all__ = [
+    "append_rows",
     "attend_rows",
+    "bound_max",
+    "bound_min",
+    "takes_new_max",
+    "takes_new_min",
     "dense_attention",
     "from_selection",
     "gather_rows",

@@ -320,3 +320,92 @@ def test_group_attention_matches_per_head_rows(gpu, P, kv, g, D, pages, top):
     expected = oracle.row_attention_rows(q.cpu(), pool.cpu(), plan.physical_rows.cpu(), P)
     _close(by_rows, expected, 2e-2, 1e-2)
     _close(by_groups, expected, 2e-2, 1e-2)
+
+
+# --------------------------------------------------------------------- append
+def _bits(t):
+    return t.view(torch.int16 if t.element_size() == 2 else torch.int32).cpu().numpy()
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+def test_append_rows_match_oracle_and_torch_bounds(gpu, dtype):
+    from mini_hisparse_amd.config import CacheConfig
+    from mini_hisparse_amd.row_kernels import MappedHost, append_rows
+
+    P, Hkv, D, B = 16, 4, 64, 5
+    cfg = CacheConfig(gpu_pages=12, host_pages=20, page_size=P, kv_heads=Hkv, head_dim=D, device=gpu, dtype=dtype)
+    g = torch.Generator().manual_seed(21)
+    pool = torch.randn(12, 2, P, Hkv, D, generator=g).to(dtype)
+    host = torch.randn(20, 2, P, Hkv, D, generator=g).to(dtype).pin_memory()
+    k = torch.randn(B, Hkv, D, generator=g).to(dtype)
+    v = torch.randn(B, Hkv, D, generator=g).to(dtype)
+    lo = torch.randn(B, Hkv, D, generator=g).to(dtype)
+    hi = lo + torch.rand(B, Hkv, D, generator=g).to(dtype)
+    # NaNs and equal signed zeros on both sides
+    k[0, 0, :4] = float("nan")
+    lo[1, 0, :4] = float("nan")
+    hi[1, 1, :4] = float("nan")
+    k[2, 0, :8] = -0.0
+    lo[2, 0, :8] = 0.0
+    hi[2, 0, :8] = 0.0
+    k[3, 1, :8] = 0.0
+    lo[3, 1, :8] = -0.0
+    hi[3, 1, :8] = -0.0
+    device_rows, host_rows = [0 * P + 3, 5 * P + 15, 7 * P, 11 * P + 8, 2 * P + 1], [19 * P + 2, -1, 4 * P + 9, 0, 13 * P]
+    # expected in bit space: rows are copied; a bound keeps its bits or takes the new
+    # element's bits where the oracle's torch.minimum/maximum rule picks the new one
+    exp_pool, exp_host = _bits(pool).copy(), _bits(host).copy()
+    kb, vb, lob, hib = _bits(k), _bits(v), _bits(lo).copy(), _bits(hi).copy()
+    for b in range(B):
+        db, do = divmod(device_rows[b], P)
+        exp_pool[db, 0, do], exp_pool[db, 1, do] = kb[b], vb[b]
+        if host_rows[b] >= 0:
+            hb, ho = divmod(host_rows[b], P)
+            exp_host[hb, 0, ho], exp_host[hb, 1, ho] = kb[b], vb[b]
+        kf, bits = k[b].float().numpy(), 8 * k.element_size()
+        lob[b] = np.where(oracle.takes_new_min(lo[b].float().numpy(), kf, bits), kb[b], lob[b])
+        hib[b] = np.where(oracle.takes_new_max(hi[b].float().numpy(), kf, bits), kb[b], hib[b])
+    torch_lo, torch_hi = torch.minimum(lo.to(gpu), k.to(gpu)), torch.maximum(hi.to(gpu), k.to(gpu))
+    dpool, dlo, dhi = pool.to(gpu), lo.to(gpu), hi.to(gpu)
+    append_rows(k.to(gpu), v.to(gpu), dpool, device_rows, list(dlo), list(dhi), cfg, host=MappedHost(host), host_rows=host_rows)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(_bits(dpool), exp_pool)
+    np.testing.assert_array_equal(_bits(host), exp_host)
+    np.testing.assert_array_equal(_bits(dlo), lob)
+    np.testing.assert_array_equal(_bits(dhi), hib)
+    # the reference's own device ops, bit for bit (NaN payloads and zero signs included)
+    np.testing.assert_array_equal(_bits(dlo), _bits(torch_lo))
+    np.testing.assert_array_equal(_bits(dhi), _bits(torch_hi))
+
+
+def test_append_fills_a_page_to_its_extrema(gpu):
+    from mini_hisparse_amd.config import CacheConfig
+    from mini_hisparse_amd.row_kernels import append_rows
+
+    P, Hkv, D = 16, 8, 128
+    cfg = CacheConfig(gpu_pages=4, host_pages=4, page_size=P, kv_heads=Hkv, head_dim=D, device=gpu, dtype=torch.bfloat16)
+    keys = torch.randn(P, Hkv, D, device=gpu).to(torch.bfloat16)
+    vals = torch.randn(P, Hkv, D, device=gpu).to(torch.bfloat16)
+    pool = torch.zeros(4, 2, P, Hkv, D, dtype=torch.bfloat16, device=gpu)
+    lo = torch.full((Hkv, D), float("inf"), dtype=torch.bfloat16, device=gpu)
+    hi = torch.full((Hkv, D), float("-inf"), dtype=torch.bfloat16, device=gpu)
+    for t in range(P):
+        append_rows(keys[t : t + 1].contiguous(), vals[t : t + 1].contiguous(), pool, [3 * P + t], [lo], [hi], cfg)
+    torch.testing.assert_close(lo, keys.amin(0), rtol=0, atol=0)
+    torch.testing.assert_close(hi, keys.amax(0), rtol=0, atol=0)
+    torch.testing.assert_close(pool[3, 0], keys, rtol=0, atol=0)
+    torch.testing.assert_close(pool[3, 1], vals, rtol=0, atol=0)
+    assert not pool[:3].any()
+
+
+def test_append_rejects_rows_outside_the_pool(gpu):
+    from mini_hisparse_amd._lib import HipLibraryError
+    from mini_hisparse_amd.config import CacheConfig
+    from mini_hisparse_amd.row_kernels import append_rows
+
+    cfg = CacheConfig(gpu_pages=2, host_pages=2, page_size=16, kv_heads=2, head_dim=64, device=gpu, dtype=torch.bfloat16)
+    pool = torch.zeros(2, 2, 16, 2, 64, dtype=torch.bfloat16, device=gpu)
+    kv = torch.zeros(1, 2, 64, dtype=torch.bfloat16, device=gpu)
+    bound = torch.zeros(2, 64, dtype=torch.bfloat16, device=gpu)
+    with pytest.raises(HipLibraryError, match="outside the pool"):
+        append_rows(kv, kv, pool, [32], [bound], [bound], cfg)

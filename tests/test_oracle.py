@@ -332,3 +332,49 @@ def test_gather_copies_exactly_the_planned_rows():
     np.testing.assert_array_equal(pool[0, :, 0], host[1, :, 1])
     np.testing.assert_array_equal(pool[4, :, 3], host[4, :, 1])
     assert np.count_nonzero(pool) == 2 * 2 * 2 * 3  # nothing else written
+
+
+# --------------------------------------------------------------------- append
+def test_append_bound_rule_known_answers():
+    """torch.minimum/maximum on the device, as measured on MI355X: a NaN wins (the
+    existing bound first); 16-bit ties (+0 vs -0 included) return the new element;
+    float32 orders -0 below +0."""
+    nan, inf = np.nan, np.inf
+    old = np.array([1.0, nan, 2.0, 0.0, -0.0, 3.0, inf, -inf], np.float32)
+    new = np.array([0.5, 1.0, nan, -0.0, 0.0, 3.0, 1.0, -2.0], np.float32)
+    lo16, hi16 = oracle.bound_min(old, new, 16), oracle.bound_max(old, new, 16)
+    lo32, hi32 = oracle.bound_min(old, new, 32), oracle.bound_max(old, new, 32)
+    for lo, hi in ((lo16, hi16), (lo32, hi32)):
+        np.testing.assert_array_equal(lo[[0, 5, 6, 7]], [0.5, 3.0, 1.0, -inf])
+        np.testing.assert_array_equal(hi[[0, 5, 6, 7]], [1.0, 3.0, inf, -2.0])
+        assert np.isnan(lo[1]) and np.isnan(lo[2]) and np.isnan(hi[1]) and np.isnan(hi[2])
+    # equal zeros: 16-bit takes the new element, float32 takes -0 (min) / +0 (max)
+    assert list(np.signbit(lo16[3:5])) == [True, False] and list(np.signbit(hi16[3:5])) == [True, False]
+    assert list(np.signbit(lo32[3:5])) == [True, True] and list(np.signbit(hi32[3:5])) == [False, False]
+
+
+def test_append_bound_rule_is_numpy_min_max_without_nan_or_zero_ties():
+    rng = np.random.default_rng(3)
+    old, new = rng.standard_normal((2, 4096)).astype(np.float32)
+    for bits in (16, 32):
+        np.testing.assert_array_equal(oracle.bound_min(old, new, bits), np.minimum(old, new))
+        np.testing.assert_array_equal(oracle.bound_max(old, new, bits), np.maximum(old, new))
+
+
+def test_append_fills_a_page_to_its_column_extrema_and_writes_rows():
+    rng = np.random.default_rng(4)
+    P, Hkv, D = 8, 2, 16
+    keys = rng.standard_normal((P, Hkv, D)).astype(np.float32)
+    vals = rng.standard_normal((P, Hkv, D)).astype(np.float32)
+    pool = np.zeros((3, 2, P, Hkv, D), np.float32)
+    host = np.zeros((5, 2, P, Hkv, D), np.float32)
+    lo = np.full((Hkv, D), np.inf, np.float32)
+    hi = np.full((Hkv, D), -np.inf, np.float32)
+    for t in range(P):  # device block 2, host block 4, one row per step
+        oracle.append_rows(pool, host, keys[t : t + 1], vals[t : t + 1], [2 * P + t], [4 * P + t], [lo], [hi], P)
+    np.testing.assert_array_equal(lo, keys.min(0))
+    np.testing.assert_array_equal(hi, keys.max(0))
+    np.testing.assert_array_equal(pool[2, 0], keys)
+    np.testing.assert_array_equal(pool[2, 1], vals)
+    np.testing.assert_array_equal(host[4], pool[2])
+    assert not pool[:2].any() and not host[:4].any()
