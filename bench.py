@@ -33,9 +33,16 @@ HBM_PEAK_GBS = 8000.0
 def parse_args():
     p = argparse.ArgumentParser(description=__doc__)
     p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--workload", default="microbench",
+                   choices=["microbench", "qwen2.5-0.5b", "qwen2.5-7b"],
+                   help="microbench = BASELINE configs[1] (default); the Qwen shapes run the "
+                        "layer-major batched engine end to end (configs[2], configs[3])")
     p.add_argument("--steps", type=int, default=20)
     p.add_argument("--warmup", type=int, default=5)
-    p.add_argument("--batch", type=int, default=8)
+    p.add_argument("--batch", type=int, default=None, help="requests (default: the workload's)")
+    p.add_argument("--host-budget-gib", type=float, default=60.0,
+                   help="pinned host memory for the model workloads' histories; the batch is cut to "
+                        "what fits (the GPU boxes here pin at most 64 GiB)")
     p.add_argument("--seed", type=int, default=2024)
     p.add_argument("--no-cpu-baseline", action="store_true", help="skip the CPU oracle leg")
     p.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU sample work")
@@ -369,6 +376,178 @@ def pmc_traffic(kernels=ROOFLINE_KERNELS, path=PMC_SUMMARY):
     return total if found == set(kernels) else None
 
 
+def model_cpu_baseline(torch, engine, wl, budget_s):
+    """The reference CPU path, extrapolated: one (request, layer) sparse path with the numpy
+    oracle (Quest, union, resolver, the per-row host gather loop, attention over the
+    selected tokens) and one layer of dense math plus the LM head in torch on the host
+    cores; per step = layers x batch sparse paths + layers dense layers + LM head."""
+    import oracle
+    from oracle.quest import pages_to_positions
+
+    st = engine.state
+    cores = os.cpu_count() or 1
+    torch.set_num_threads(cores)
+    P, Hkv, D, L, B, C = wl.page_size, wl.kv_heads, wl.head_dim, wl.layers, wl.batch, st.pages
+    length = st.lengths[0]
+    count = ceil(length / P)
+    gen = torch.Generator().manual_seed(5)
+    q = torch.randn(wl.heads, D, generator=gen).to(wl.dtype)
+    lo, hi = st.minimum[0, 0, :count].cpu(), st.maximum[0, 0, :count].cpu()
+    t = st.tables[0][0]
+    tables = [x.cpu().numpy() for x in (t.source, t.resident, t.hot, t.tags, t.lru)]
+    host = st.host[0].view(B, C, 2, P, Hkv, D)[0]
+    t0 = time.perf_counter()
+    pages = oracle.quest_pages(q, lo, hi, length, P, wl.top_pages)
+    positions = pages_to_positions(pages, length, P)
+    union, cols = oracle.from_selection(positions)
+    phys, mh, md, counts, _, _ = oracle.resolve_rows(union, *tables, length, P, head_columns=cols)
+    staging = np.empty((max(1, int(counts[2])), 2, Hkv, D), dtype=np.float32)
+    for i, hrow in enumerate(mh[: int(counts[2])].tolist()):  # the CPU gather loop, one row at a time
+        hb, ho = divmod(hrow - int(tables[0][0]) * P, P)
+        staging[i] = host[hb, :, ho].float().numpy()
+    kv = host[:count].float()
+    keys = kv[:, 0].reshape(count * P, Hkv, D)[:length]
+    vals = kv[:, 1].reshape(count * P, Hkv, D)[:length]
+    oracle.selection_oracle(q, keys, vals, positions)
+    sparse_s = time.perf_counter() - t0
+    layer = engine.model.model.layers[0]
+    weights = {n: p.detach().float().cpu() for n, p in layer.named_parameters()}
+    x = torch.randn(B, wl.hidden, generator=gen)
+    t0 = time.perf_counter()
+    for _ in range(2):
+        hq = torch.nn.functional.linear(x, weights["self_attn.q_proj.weight"], weights["self_attn.q_proj.bias"])
+        hk = torch.nn.functional.linear(x, weights["self_attn.k_proj.weight"], weights["self_attn.k_proj.bias"])
+        hv = torch.nn.functional.linear(x, weights["self_attn.v_proj.weight"], weights["self_attn.v_proj.bias"])
+        y = x + torch.nn.functional.linear(hq, weights["self_attn.o_proj.weight"])
+        g = torch.nn.functional.linear(y, weights["mlp.gate_proj.weight"])
+        u = torch.nn.functional.linear(y, weights["mlp.up_proj.weight"])
+        y = y + torch.nn.functional.linear(torch.nn.functional.silu(g) * u, weights["mlp.down_proj.weight"])
+    dense_s = (time.perf_counter() - t0) / 2
+    head = engine.model.lm_head.weight.detach()[: wl.vocab // 8].float().cpu()
+    t0 = time.perf_counter()
+    torch.nn.functional.linear(x, head)
+    head_s = (time.perf_counter() - t0) * 8
+    step_s = L * B * sparse_s + L * dense_s + head_s
+    return {
+        "value": B / step_s,
+        "unit": "tokens/s",
+        "cores": cores,
+        "kind": "port",
+        "sample": f"extrapolated: one (request, layer) sparse path (numpy oracle: Quest over {count} pages, "
+        f"union, resolver, {int(counts[2])}-row host gather loop, attention; {sparse_s:.2f} s, 1 thread) "
+        f"x {L * B} + one dense layer for {B} tokens ({dense_s:.2f} s, torch fp32, {cores} threads) x {L} "
+        f"+ LM head ({head_s:.2f} s) = {step_s:.1f} s per step",
+        "host_cpus": cores,
+    }
+
+
+def run_model_workload(args, torch, device):
+    """End-to-end decode of a Qwen-shape random-init model with the layer-major engine."""
+    from dataclasses import replace
+
+    from mini_hisparse_amd.batched_engine import (
+        WORKLOADS, BatchedDecodeEngine, build_state, host_bytes_per_request, random_model,
+    )
+
+    wl = WORKLOADS[args.workload]
+    configured = wl.batch
+    if args.batch is not None:
+        wl = replace(wl, batch=args.batch)
+    per_request = host_bytes_per_request(wl)
+    fits = int(args.host_budget_gib * 2**30 // per_request)
+    if fits < 1:
+        raise SystemExit("one request's history exceeds the pinned host budget")
+    if wl.batch > fits:
+        print(f"[bench] batch {wl.batch} needs {wl.batch * per_request / 2**30:.0f} GiB pinned; "
+              f"running batch {fits}", file=sys.stderr, flush=True)
+        wl = replace(wl, batch=fits)
+    if args.warmup + args.steps + 1 > wl.steps:
+        raise SystemExit(f"warmup + steps + 1 profiled step must fit the workload's {wl.steps} decode steps")
+    t0 = time.perf_counter()
+    print(f"[bench] {wl.name}: model + synthetic history (batch {wl.batch}, {wl.context} tokens)", file=sys.stderr, flush=True)
+    model = random_model(wl, device, seed=args.seed)
+    state = build_state(wl, device, seed=args.seed)
+    engine = BatchedDecodeEngine(model, state, wl.top_pages)
+    setup_s = time.perf_counter() - t0
+    gen = torch.Generator(device=device).manual_seed(args.seed)
+    tokens = torch.randint(0, wl.vocab, (wl.batch,), generator=gen, device=device)
+    for _ in range(args.warmup):
+        tokens = engine.step(tokens)
+    torch.cuda.synchronize()
+    print("[bench] timing", file=sys.stderr, flush=True)
+    stats0 = state.row_stats.clone()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        tokens = engine.step(tokens)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    ms_per_step = elapsed * 1e3 / args.steps
+    rows = ((state.row_stats - stats0).double() / args.steps).tolist()
+    timer = []
+    engine.step(tokens, timer=timer)  # profiled step, outside the timed region
+    torch.cuda.synchronize()
+    stage_ms = {}
+    for _, marks, _, _ in timer:
+        for stage, (start, end) in marks.items():
+            stage_ms[stage] = stage_ms.get(stage, 0.0) + start.elapsed_time(end)
+    entries = sum(int(e) for _, _, e, _ in timer)
+    misses = sum(int(m) for _, _, _, m in timer)
+    e, D, Hq, B, L = 2, wl.head_dim, wl.heads, wl.batch, wl.layers
+    W = engine.dec.width
+    att_bytes = entries * 2 * D * e + L * (8 * Hq * W * B + 2 * Hq * D * e * B)
+    att_gbs = att_bytes / (stage_ms["attend"] * 1e-3) / 1e9
+    row_bytes = 2 * wl.kv_heads * D * e
+    gather_bytes = misses * row_bytes
+    link = host_link_gbs(torch, device)
+    result = {
+        "metric": METRIC,
+        "value": wl.batch * args.steps / elapsed,
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": f"synthetic: random-init {wl.name} weights; {wl.context}-token K/V histories (N(0,1), 2% "
+        "channels x8) written directly instead of a prefill; greedy decode from random tokens",
+        "config": {
+            "workload": f"{wl.name} end to end (layer-major batched engine): {wl.layers} layers, hidden "
+            f"{wl.hidden}, {wl.heads} q / {wl.kv_heads} kv heads, head_dim {wl.head_dim}, FFN {wl.ffn}, "
+            f"batch {wl.batch}, {wl.context}-token histories, Quest top-{wl.top_pages} pages, "
+            f"{wl.resident_fraction:.0%} of pages resident, hot_rows {wl.hot_rows}"
+            + (f"; batch cut from {configured}: {configured} histories need "
+               f"{configured * per_request / 2**30:.0f} GiB of pinned host memory, the box pins at most "
+               f"64 GiB (budget {args.host_budget_gib:g} GiB)" if wl.batch < configured else ""),
+            "global_batch": wl.batch,
+            "seq_len": wl.context,
+            "parallelism": "none (1 GPU)",
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": att_gbs,
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": att_gbs / HBM_PEAK_GBS,
+            "traffic": None,
+            "kernel": "attend_mfma_kernel + attend_merge_kernel, summed over the layers of one profiled step",
+        },
+        "stages_ms_per_step": stage_ms,
+        "rows_per_step": {"resident_hits": rows[0], "hot_hits": rows[1], "misses": rows[2]},
+        "gather": {"bytes_per_step": gather_bytes, "GBps": gather_bytes / (stage_ms["gather"] * 1e-3) / 1e9,
+                   "host_link_memcpy_GBps": link},
+        "setup_s": setup_s,
+    }
+    if not args.no_cpu_baseline:
+        print("[bench] cpu baseline (extrapolated)", file=sys.stderr, flush=True)
+        result["cpu_baseline"] = model_cpu_baseline(torch, engine, wl, args.cpu_budget)
+    else:
+        result["cpu_baseline"] = None
+    print(json.dumps(result))
+
+
 def main():
     args = parse_args()
     if args.summarize_pmc:
@@ -384,6 +563,11 @@ def main():
         print(json.dumps({"error": "no ROCm GPU visible"}))
         sys.exit(1)
     device = torch.device("cuda:0")
+    if args.workload != "microbench":
+        run_model_workload(args, torch, device)
+        return
+    if args.batch is None:
+        args.batch = 8
     print(f"[bench] building workload (batch {args.batch})", file=sys.stderr, flush=True)
     w = build_workload(args, torch, device)
     run_steps(torch, w, args.warmup, record=False)

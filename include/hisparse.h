@@ -53,6 +53,16 @@ int hs_version(void);
 int hs_device_lds_bytes(int device, int64_t* bytes);
 
 /*
+ * Exact-size pinned host allocation for a caller-owned host pool (freed with
+ * hs_host_free).  No counterpart in the reference, which pins its host pool
+ * with torch (storage.py:112-114); PyTorch's pinned allocator rounds every
+ * request up to a power of two, which halves the usable pinned memory for
+ * pools just above one.  `host_ptr` receives a host pointer.
+ */
+int hs_host_alloc(int64_t bytes, void** host_ptr);
+int hs_host_free(void* host_ptr);
+
+/*
  * Device alias of a pinned host allocation owned by the caller (never
  * registered or unregistered here).
  * Replaces: MappedHost (mini_hisparse/row_kernels.py:10-32), called from

@@ -58,6 +58,8 @@ SIGNATURES = {
     "hs_version": (c_int, []),
     "hs_device_lds_bytes": (c_int, [c_int, POINTER(c_int64)]),
     "hs_host_alias": (c_int, [c_void_p, POINTER(c_void_p)]),
+    "hs_host_alloc": (c_int, [c_int64, POINTER(c_void_p)]),
+    "hs_host_free": (c_int, [c_void_p]),
     "hs_quest_workspace_bytes": (c_int64, [c_int64, c_int64, c_int64]),
     "hs_quest_topk": (
         c_int,

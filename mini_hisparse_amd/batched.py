@@ -26,7 +26,7 @@ from math import ceil
 import torch
 
 from . import _lib
-from .selection import selection_width, union_bound
+from .selection import union_bound
 
 
 @dataclass
@@ -43,7 +43,9 @@ class LayerTablesView:
 class BatchedSparseDecode:
     """Quest -> union -> resolve -> gather -> attention for B requests of one layer."""
 
-    def __init__(self, config, heads, top_pages, lengths, *, keep_sink=True, device="cuda"):
+    def __init__(self, config, heads, top_pages, lengths, *, keep_sink=True, device="cuda", capacity_lengths=None):
+        """``capacity_lengths`` (default ``lengths``) sizes every buffer, so that later
+        ``set_lengths`` calls up to those lengths (a decode run) allocate nothing."""
         self.config = config
         self.heads = heads
         self.kv_heads = config.kv_heads
@@ -52,15 +54,18 @@ class BatchedSparseDecode:
         self.keep_sink = keep_sink
         self.device = torch.device(device)
         self.batch = len(lengths)
-        self._shape(list(lengths))
+        self._shape(list(lengths), list(capacity_lengths or lengths))
 
-    def _shape(self, lengths):
+    def _shape(self, lengths, capacity_lengths):
         P, B, dev = self.config.page_size, self.batch, self.device
+        caps = [max(c, l) for c, l in zip(capacity_lengths, lengths)]
+        self.capacity_lengths = caps
         self.lengths = lengths
         self.counts = [ceil(l / P) for l in lengths]
-        self.capacity = max(union_bound(l, P, self.top, self.heads, self.keep_sink) for l in lengths)
-        self.entry_capacity = max(union_bound(l, P, self.top, self.groups, self.keep_sink) for l in lengths)
-        self.width = max(selection_width(l, P, self.top) for l in lengths)
+        # union sizes grow with the length, and a head's width is at most top pages
+        self.capacity = max(union_bound(l, P, self.top, self.heads, self.keep_sink) for l in caps)
+        self.entry_capacity = max(union_bound(l, P, self.top, self.groups, self.keep_sink) for l in caps)
+        self.width = max(min(self.top * P, l) for l in caps)
         i32, i64 = torch.int32, torch.int64
         self.pages = torch.empty((B, self.heads, self.top), dtype=i32, device=dev)
         self.positions = torch.empty((B, self.capacity), dtype=i32, device=dev)
@@ -76,7 +81,7 @@ class BatchedSparseDecode:
         self.miss_device = torch.empty((B, self.capacity), dtype=i64, device=dev)
         self.row_counts = torch.empty((B, 3), dtype=i64, device=dev)
         lib = _lib.load()
-        self.quest_ws_bytes = lib.hs_quest_workspace_bytes(B, self.heads, max(self.counts))
+        self.quest_ws_bytes = lib.hs_quest_workspace_bytes(B, self.heads, max(ceil(l / P) for l in caps))
         self.quest_ws = torch.empty(self.quest_ws_bytes, dtype=torch.uint8, device=dev)
         self.resolve_ws_bytes = 0
         self.max_tables = None
@@ -92,8 +97,17 @@ class BatchedSparseDecode:
         self._count_arr = (ctypes.c_int64 * B)(*self.counts)
 
     def set_lengths(self, lengths):
-        if list(lengths) != self.lengths:
-            self._shape(list(lengths))
+        lengths = list(lengths)
+        if lengths == self.lengths:
+            return
+        if any(l > c for l, c in zip(lengths, self.capacity_lengths)):
+            self._shape(lengths, lengths)  # beyond the reserved sizes: new buffers
+            return
+        self.lengths = lengths
+        self.counts = [ceil(l / self.config.page_size) for l in lengths]
+        for b in range(self.batch):
+            self._len_arr[b] = lengths[b]
+            self._count_arr[b] = self.counts[b]
 
     # -- stages ------------------------------------------------------------
     def select(self, queries, minimums, maximums, stream=None):

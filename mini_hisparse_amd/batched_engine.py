@@ -1,0 +1,381 @@
+"""Layer-major batched sparse decode: B requests per launch, every layer of a step.
+
+The reference decodes one request at a time, and inside a request one layer
+at a time (engine.py:115-128, model.py:199-225), with a Python control plane
+that keeps one object per page (hybrid.py, storage.py).  At the Qwen2.5-7B
+shape with 16 requests of 128k tokens that is 3.67 M pages and 448
+(request, layer) pairs per step.  This engine keeps the same per-(request,
+layer) state -- the host page of every logical page, the resident block of the
+resident ones, the hot region (blocks, tags, LRU) and the Quest bounds -- as
+stacked device tensors, and runs a decode step layer by layer over all B
+requests:
+
+    dense   RMSNorm, q/k/v projections, rotary embedding          (PyTorch-ROCm)
+    append  hs_append_rows: tail rows, Quest bounds, host mirror   (HIP)
+    select  hs_quest_topk + hs_build_union                         (HIP)
+    resolve hs_resolve_rows_batched, row statistics fused          (HIP, compute stream)
+    gather  hs_gather_rows_batched, host -> hot rows               (HIP, transfer stream)
+    attend  hs_attend_groups                                       (HIP)
+    dense   o_proj, residual, MLP                                  (PyTorch-ROCm)
+
+and the next tokens (greedy) stay on the device: a step never reads back to
+the host.  The per-(request, layer) semantics are the reference's: the new
+token is appended before selection, Quest picks pages over bounds that include
+it, the resolver is bit-exact ``resolve_rows`` and attention covers the
+selected tokens.  What differs is the residency policy: resident pages are a
+fixed subset chosen when the history is built (plus every tail page), instead
+of the reference's adaptive policy (hybrid.py:204-392); hot rows follow the
+resolver's LRU exactly.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+from math import ceil
+
+import torch
+from torch.nn import functional as F
+
+from . import _lib
+from .batched import BatchedSparseDecode, LayerTablesView
+from .config import CacheConfig
+from .model import MiniModel, ModelConfig
+from .row_kernels import MappedHost, pinned_empty
+
+
+@dataclass(frozen=True)
+class DecodeWorkload:
+    """A decode configuration: model shape, batch, history, selection and residency."""
+
+    name: str
+    layers: int
+    hidden: int
+    heads: int
+    kv_heads: int
+    head_dim: int
+    ffn: int
+    vocab: int
+    batch: int
+    context: int
+    steps: int
+    top_pages: int
+    resident_fraction: float
+    hot_rows: int
+    page_size: int = 16
+    dtype: torch.dtype = torch.bfloat16
+
+    def model_config(self):
+        return ModelConfig(
+            vocab_size=self.vocab, hidden_size=self.hidden, intermediate_size=self.ffn,
+            num_hidden_layers=self.layers, num_attention_heads=self.heads,
+            num_key_value_heads=self.kv_heads,
+        )
+
+
+# BASELINE configs[2] and configs[3] (hot rows: 2U for the 0.5B shape; the
+# reference's cap of 32768 for the 7B shape, hybrid.py:34)
+WORKLOADS = {
+    "qwen2.5-0.5b": DecodeWorkload(
+        "qwen2.5-0.5b", layers=24, hidden=896, heads=14, kv_heads=2, head_dim=64, ffn=4864,
+        vocab=151936, batch=4, context=32768, steps=128, top_pages=32, resident_fraction=0.25,
+        hot_rows=13504,
+    ),
+    "qwen2.5-7b": DecodeWorkload(
+        "qwen2.5-7b", layers=28, hidden=3584, heads=28, kv_heads=4, head_dim=128, ffn=18944,
+        vocab=152064, batch=16, context=131072, steps=256, top_pages=64, resident_fraction=0.15,
+        hot_rows=32768,
+    ),
+}
+
+
+def rotary_at(tensor, positions, theta):
+    """Rotary embedding of [B, heads, head_dim] at one position per row; the same
+    arithmetic as the model's prefill/decode rotary (model.py)."""
+    dim = tensor.shape[-1]
+    inv = theta ** (-torch.arange(0, dim, 2, device=tensor.device).float() / dim)
+    angles = positions.float()[:, None] * inv[None, :]
+    angles = torch.cat((angles, angles), -1)[:, None, :]
+    cosine, sine = angles.cos().to(tensor.dtype), angles.sin().to(tensor.dtype)
+    first, second = tensor.chunk(2, -1)
+    return tensor * cosine + torch.cat((-second, first), -1) * sine
+
+
+class SparseKVState:
+    """Per-(layer, request) KV state as stacked tensors.
+
+    host      per layer a pinned [B * C, 2, P, Hkv, D] pool (one allocation per layer:
+              pinned allocations are size-limited); logical page p of (l, b) lives
+              in host block b * C + p of layer l's pool (the ``source`` table)
+    pool      device [blocks, 2, P, Hkv, D]: resident pages, hot regions, spare
+              blocks for the tail pages the decode opens
+    source    int32 [L, B, C]    resident int32 [L, B, C] (-1 = host only)
+    hot       int32 [L, B, S/P]  tags int32 [L, B, S]  lru int64 [L, B, S]
+    minimum / maximum  [L, B, C, Hkv, D] Quest bounds (+inf / -inf when empty)
+    """
+
+    def __init__(self, layers, batch, max_tokens, config: CacheConfig, hot_rows, resident_pages, spare_blocks):
+        P, Hkv, D, dev = config.page_size, config.kv_heads, config.head_dim, torch.device(config.device)
+        self.layers, self.batch, self.config, self.device = layers, batch, config, dev
+        self.pages = ceil(max_tokens / P)
+        self.hot_rows = hot_rows
+        C, L, B = self.pages, layers, batch
+        hot_blocks = ceil(hot_rows / P)
+        self.blocks = resident_pages + L * B * hot_blocks + spare_blocks
+        self.pool = torch.empty((self.blocks, 2, P, Hkv, D), dtype=config.dtype, device=dev)
+        self.host = [pinned_empty((B * C, 2, P, Hkv, D), config.dtype) for _ in range(L)]
+        self.alias = [MappedHost(h) for h in self.host]
+        self.source = torch.arange(B * C, dtype=torch.int32, device=dev).view(1, B, C).repeat(L, 1, 1)
+        self.resident = torch.full((L, B, C), -1, dtype=torch.int32, device=dev)
+        self.first_hot = resident_pages  # resident blocks are [0, first_hot)
+        self.hot = (torch.arange(L * B * hot_blocks, dtype=torch.int32, device=dev) + self.first_hot).view(L, B, hot_blocks)
+        self.tags = torch.full((L, B, hot_rows), -1, dtype=torch.int32, device=dev)
+        self.lru = torch.arange(hot_rows, dtype=torch.int64, device=dev).repeat(L * B).view(L, B, hot_rows)
+        self.minimum = torch.full((L, B, C, Hkv, D), float("inf"), dtype=config.dtype, device=dev)
+        self.maximum = torch.full((L, B, C, Hkv, D), float("-inf"), dtype=config.dtype, device=dev)
+        self.next_resident = 0
+        self.next_spare = resident_pages + L * B * hot_blocks
+        self.lengths = [0] * B
+        self.tail_block = [[-1] * B for _ in range(L)]  # device block of each (l, b) tail page
+        self.tables = [
+            [LayerTablesView(self.source[l, b], self.resident[l, b], self.hot[l, b], self.tags[l, b], self.lru[l, b])
+             for b in range(B)]
+            for l in range(L)
+        ]
+        self.bounds = [([self.minimum[l, b] for b in range(B)], [self.maximum[l, b] for b in range(B)]) for l in range(L)]
+        self.row_stats = torch.zeros(3, dtype=torch.int64, device=dev)
+
+    # -- history -------------------------------------------------------------
+    @torch.inference_mode()
+    def build_history(self, length, resident_fraction, seed=0, outlier_fraction=0.02, outlier_scale=8.0):
+        """Synthetic history of `length` tokens for every (layer, request): K, V ~ N(0, 1)
+        with a seeded 2% of channels per KV head scaled x8, written to the host pool;
+        exact Quest bounds per page; a seeded `resident_fraction` of each (l, b)'s pages
+        plus its tail page copied into resident blocks."""
+        cfg, L, B, C, dev = self.config, self.layers, self.batch, self.pages, self.device
+        P, Hkv, D = cfg.page_size, cfg.kv_heads, cfg.head_dim
+        used = ceil(length / P)
+        tail_valid = length - (used - 1) * P
+        gen = torch.Generator(device=dev).manual_seed(seed)
+        cpu_gen = torch.Generator().manual_seed(seed)
+        for l in range(L):
+            host = self.host[l].view(B, C, 2, P, Hkv, D)
+            scale = torch.ones(B, 1, 1, Hkv, D)
+            n_out = max(1, round(outlier_fraction * D))
+            for b in range(B):
+                for kv in range(Hkv):
+                    scale[b, 0, 0, kv, torch.randperm(D, generator=cpu_gen)[:n_out]] = outlier_scale
+            scale = scale.to(dev)
+            kv_pages = torch.empty((B, used, 2, P, Hkv, D), dtype=cfg.dtype, device=dev)
+            for b in range(B):  # one request at a time bounds the float32 scratch
+                x = torch.randn((used, 2, P, Hkv, D), generator=gen, device=dev)
+                kv_pages[b] = (x * scale[b]).to(cfg.dtype)
+                del x
+            kv_pages[:, -1, :, tail_valid:] = 0  # rows past the history
+            keys = kv_pages[:, :, 0]
+            self.minimum[l, :, :used] = keys.amin(2)
+            self.maximum[l, :, :used] = keys.amax(2)
+            self.minimum[l, :, used - 1] = keys[:, -1, :tail_valid].amin(1)
+            self.maximum[l, :, used - 1] = keys[:, -1, :tail_valid].amax(1)
+            host[:, :used].copy_(kv_pages)
+            rng = torch.Generator().manual_seed(seed * 1000003 + l)
+            for b in range(B):
+                chosen = torch.randperm(used - 1, generator=rng)[: round(resident_fraction * used)]
+                pages = torch.cat((chosen, torch.tensor([used - 1]))).unique()
+                if self.next_resident + len(pages) > self.first_hot:
+                    raise ValueError("resident pages exceed the reserved resident blocks")
+                blocks = torch.arange(self.next_resident, self.next_resident + len(pages), dtype=torch.int32)
+                self.next_resident += len(pages)
+                self.resident[l, b, pages.to(dev)] = blocks.to(dev)
+                self.pool[blocks.long().to(dev)] = kv_pages[b, pages.to(dev)]
+                self.tail_block[l][b] = int(blocks[-1])
+            del kv_pages, keys
+        torch.cuda.synchronize(dev)
+        self.lengths = [length] * B
+
+    # -- decode-step bookkeeping ---------------------------------------------------
+    def open_tail_pages(self, positions):
+        """Give every (l, b) whose next token starts a page a resident tail block."""
+        P, L = self.config.page_size, self.layers
+        starts = [b for b, pos in enumerate(positions) if pos % P == 0]
+        if not starts:
+            return
+        if self.next_spare + L * len(starts) > self.blocks:
+            raise RuntimeError("no spare device blocks left for new tail pages")
+        ls, bs, ps, blocks = [], [], [], []
+        for l in range(L):
+            for b in starts:
+                blk = self.next_spare
+                self.next_spare += 1
+                self.tail_block[l][b] = blk
+                ls.append(l), bs.append(b), ps.append(positions[b] // P), blocks.append(blk)
+        index = (torch.tensor(ls), torch.tensor(bs), torch.tensor(ps))
+        self.resident[tuple(i.to(self.device) for i in index)] = torch.tensor(blocks, dtype=torch.int32).to(self.device)
+
+    def append_args(self, layer, positions):
+        """ctypes arrays of one layer's hs_append_rows call."""
+        P, B, C = self.config.page_size, self.batch, self.pages
+        Hkv, D = self.config.kv_heads, self.config.head_dim
+        esz = self.minimum.element_size()
+        page_elems = Hkv * D
+        dev_rows = (ctypes.c_int64 * B)()
+        host_rows = (ctypes.c_int64 * B)()
+        lo = (ctypes.c_void_p * B)()
+        hi = (ctypes.c_void_p * B)()
+        base_lo, base_hi = self.minimum.data_ptr(), self.maximum.data_ptr()
+        for b, pos in enumerate(positions):
+            page, off = divmod(pos, P)
+            dev_rows[b] = self.tail_block[layer][b] * P + off
+            host_rows[b] = (b * C + page) * P + off
+            at = ((layer * B + b) * C + page) * page_elems * esz
+            lo[b], hi[b] = base_lo + at, base_hi + at
+        return dev_rows, host_rows, lo, hi
+
+
+class BatchedDecodeEngine:
+    """Greedy decode of B requests, layer-major, over a :class:`SparseKVState`."""
+
+    def __init__(self, model: MiniModel, state: SparseKVState, top_pages, *, max_tokens=None, keep_sink=True):
+        cfg = model.config
+        if (cfg.num_key_value_heads, cfg.head_dim) != (state.config.kv_heads, state.config.head_dim):
+            raise ValueError("model/cache head dimensions differ")
+        if model.dtype != state.config.dtype:
+            raise ValueError("model/cache dtype differ")
+        self.model, self.state = model, state
+        self.device = state.device
+        caps = [max_tokens or state.pages * state.config.page_size] * state.batch
+        self.dec = BatchedSparseDecode(
+            state.config, cfg.num_attention_heads, top_pages, [max(1, l) for l in state.lengths],
+            keep_sink=keep_sink, device=self.device, capacity_lengths=caps,
+        )
+        if state.hot_rows < self.dec.capacity:
+            # the resolver's precondition (row_index.py:41-42, hybrid.py:34): every
+            # selected row must fit the hot region, or misses would share victim slots
+            raise ValueError(
+                f"hot_rows {state.hot_rows} below the union bound {self.dec.capacity} of "
+                f"{cfg.num_attention_heads} heads x {top_pages} pages"
+            )
+        self.transfer = torch.cuda.Stream(self.device)
+        self._host_alias = [(ctypes.c_void_p * state.batch)(*([a.data_ptr()] * state.batch)) for a in state.alias]
+        self.positions = torch.tensor(state.lengths, dtype=torch.int64, device=self.device)
+
+    def _append(self, layer, k, v, positions):
+        st, cfg = self.state, self.state.config
+        dev_rows, host_rows, lo, hi = st.append_args(layer, positions)
+        _lib.check(
+            _lib.load().hs_append_rows(
+                k.data_ptr(), v.data_ptr(), k.stride(0), st.pool.data_ptr(), st.blocks * cfg.page_size,
+                _lib.dtype_code(cfg.dtype), cfg.page_size, cfg.kv_heads, cfg.head_dim,
+                dev_rows, self._host_alias[layer], host_rows, st.host[layer].shape[0] * cfg.page_size, lo, hi,
+                st.batch, _lib.stream_handle(self.device),
+            ),
+            "hs_append_rows",
+        )
+
+    @torch.inference_mode()
+    def step(self, tokens, observer=None, timer=None):
+        """One decode step for all B requests: `tokens` [B] int64 (device) -> next tokens.
+
+        ``timer`` (optional list) receives, per layer, the stage events
+        ``(layer, {stage: (start, end)}, entries)`` with ``entries`` the layer's
+        attention entry total (device tensor) -- for profiling, not for timed runs.
+        """
+        model, st, dec = self.model, self.state, self.dec
+        cfg = model.config
+        B, Hq, Hkv, D = st.batch, cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
+        positions = list(st.lengths)
+        st.open_tail_pages(positions)
+        dec.set_lengths([p + 1 for p in positions])
+        compute = torch.cuda.current_stream(self.device)
+        x = model.model.embed_tokens(tokens)
+
+        def mark(stream):
+            if timer is None:
+                return None
+            event = torch.cuda.Event(enable_timing=True)
+            event.record(stream)
+            return event
+
+        for index, layer in enumerate(model.model.layers):
+            attn = layer.self_attn
+            marks = {"dense_in": [mark(compute)]}
+            h = layer.input_layernorm(x)
+            q = F.linear(h, attn.q_proj.weight, attn.q_proj.bias).view(B, Hq, D)
+            k = F.linear(h, attn.k_proj.weight, attn.k_proj.bias).view(B, Hkv, D)
+            v = F.linear(h, attn.v_proj.weight, attn.v_proj.bias).view(B, Hkv, D).contiguous()
+            q = rotary_at(q, self.positions, cfg.rope_theta)
+            k = rotary_at(k, self.positions, cfg.rope_theta).contiguous()
+            marks["dense_in"].append(mark(compute))
+            marks["append"] = [mark(compute)]
+            self._append(index, k, v, positions)
+            lo, hi = st.bounds[index]
+            marks["append"].append(mark(compute))
+            marks["select"] = [marks["append"][1]]
+            dec.select(q, lo, hi)
+            marks["select"].append(mark(compute))
+            marks["resolve"] = [marks["select"][1]]
+            dec.resolve(st.tables[index], row_stats=st.row_stats)
+            marks["resolve"].append(mark(compute))
+            resolved = torch.cuda.Event()
+            resolved.record(compute)
+            self.transfer.wait_event(resolved)
+            marks["gather"] = [mark(self.transfer)]
+            dec.gather(st.alias[index], st.pool, self.transfer)
+            marks["gather"].append(mark(self.transfer))
+            ready = torch.cuda.Event()
+            ready.record(self.transfer)
+            compute.wait_event(ready)
+            marks["attend"] = [mark(compute)]
+            out = dec.attend(q, st.pool)
+            marks["attend"].append(mark(compute))
+            if observer is not None:
+                observer(index, q, k, v, out)
+            marks["dense_out"] = [marks["attend"][1]]
+            x = x + F.linear(out.reshape(B, Hq * D), attn.o_proj.weight)
+            x = x + layer.mlp(layer.post_attention_layernorm(x))
+            marks["dense_out"].append(mark(compute))
+            if timer is not None:
+                timer.append((index, marks, dec.entry_counts.sum(), dec.row_counts[:, 2].sum()))
+        logits = model.lm_head(model.model.norm(x)).float()
+        st.lengths = [p + 1 for p in positions]
+        self.positions += 1
+        return logits.argmax(-1)
+
+
+def random_model(workload: DecodeWorkload, device, seed=0):
+    """Random-init model of the workload's shape, built directly on the device in its dtype."""
+    torch.manual_seed(seed)
+    with torch.device(device):
+        previous = torch.get_default_dtype()
+        torch.set_default_dtype(workload.dtype)
+        try:
+            model = MiniModel(workload.model_config())
+        finally:
+            torch.set_default_dtype(previous)
+    return model.eval()
+
+
+def host_bytes_per_request(workload: DecodeWorkload, context=None, steps=None):
+    """Pinned host bytes of one request's history (every layer, room for the decode)."""
+    context = workload.context if context is None else context
+    steps = workload.steps if steps is None else steps
+    pages = ceil((context + steps) / workload.page_size)
+    element = torch.empty((), dtype=workload.dtype).element_size()
+    return workload.layers * pages * 2 * workload.page_size * workload.kv_heads * workload.head_dim * element
+
+
+def build_state(workload: DecodeWorkload, device, seed=0, context=None, steps=None):
+    """State sized for `context` history tokens plus `steps` decoded ones, history built."""
+    context = workload.context if context is None else context
+    steps = workload.steps if steps is None else steps
+    P = workload.page_size
+    cfg = CacheConfig(
+        gpu_pages=1, host_pages=1, page_size=P, kv_heads=workload.kv_heads, head_dim=workload.head_dim,
+        device=str(device), dtype=workload.dtype,
+    )
+    used = ceil(context / P)
+    resident = workload.layers * workload.batch * (round(workload.resident_fraction * used) + 1)
+    spare = workload.layers * workload.batch * (ceil(steps / P) + 1)
+    state = SparseKVState(workload.layers, workload.batch, context + steps, cfg, workload.hot_rows, resident, spare)
+    state.build_history(context, workload.resident_fraction, seed=seed)
+    return state

@@ -39,6 +39,23 @@ class MappedHost:
         return self.pointer
 
 
+def pinned_empty(shape, dtype):
+    """A pinned host tensor of exactly ``shape`` (``hs_host_alloc``), freed when the last
+    tensor viewing it is gone.  PyTorch's pinned allocator rounds a request up to a power
+    of two, so a pool just above one would pin twice its size."""
+    import math
+    import weakref
+
+    nbytes = math.prod(shape) * torch.empty((), dtype=dtype).element_size()
+    pointer = ctypes.c_void_p()
+    lib = _lib.load()
+    _lib.check(lib.hs_host_alloc(nbytes, ctypes.byref(pointer)), "hs_host_alloc")
+    buffer = (ctypes.c_byte * nbytes).from_address(pointer.value)
+    # the buffer object lives as long as any tensor storage over it
+    weakref.finalize(buffer, lib.hs_host_free, pointer.value)
+    return torch.frombuffer(buffer, dtype=torch.uint8).view(dtype).view(shape)
+
+
 def _row_bytes(config, element_size):
     return config.kv_heads * config.head_dim * element_size
 

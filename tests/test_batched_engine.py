@@ -1,0 +1,87 @@
+"""Layer-major batched engine: every layer of a decode step against the oracle.
+
+For each step and layer, the engine's own query is re-scored by the oracle
+over the Quest bounds of the full history read back from the host pool (which
+holds the mirrored appended rows), and its attention output is compared with
+the oracle's sparse attention over the selected tokens."""
+
+from math import ceil
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from oracle.quest import pages_to_positions
+from tests.conftest import gpu_available
+
+
+def tiny(**overrides):
+    """Small workload; the hot region holds twice the union bound (the reference's default
+    hot_rows = 2U, cli.py:141-151)."""
+    from mini_hisparse_amd.batched_engine import DecodeWorkload
+    from mini_hisparse_amd.selection import union_bound
+
+    values = dict(name="tiny", layers=2, hidden=256, heads=8, kv_heads=2, head_dim=32, ffn=512, vocab=300,
+                  batch=3, context=40 * 16 - 1, steps=24, top_pages=6, resident_fraction=0.3)
+    values.update(overrides)
+    end = values["context"] + values["steps"]
+    values.setdefault("hot_rows", 2 * union_bound(end, 16, values["top_pages"], values["heads"]))
+    return DecodeWorkload(**values)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("overrides", [{}, {"heads": 16, "kv_heads": 2, "head_dim": 64, "hidden": 1024}])
+def test_batched_engine_layers_match_oracle(gpu, overrides):
+    from mini_hisparse_amd.batched_engine import BatchedDecodeEngine, build_state, random_model
+
+    wl = tiny(**overrides)
+    model = random_model(wl, gpu, seed=1)
+    state = build_state(wl, gpu, seed=2)
+    engine = BatchedDecodeEngine(model, state, wl.top_pages)
+    L, B, C, P = wl.layers, wl.batch, state.pages, wl.page_size
+    Hkv, D = wl.kv_heads, wl.head_dim
+    records = []
+    tokens = torch.tensor([1, 2, 3], device=gpu)
+    unions = 0
+    for step in range(3):  # positions 639 (last row of a page), 640 (opens a page), 641
+        records.clear()
+        tokens = engine.step(
+            tokens,
+            lambda l, q, k, v, out: records.append(
+                (l, q.clone(), out.clone(), engine.dec.pages.clone(), engine.dec.union_count.clone())
+            ),
+        )
+        torch.cuda.synchronize()
+        length = state.lengths[0]
+        count = ceil(length / P)
+        assert len(records) == L
+        for l, q, out, layer_pages, union_count in records:
+            for b in range(B):
+                kv = state.host[l].view(B, C, 2, P, Hkv, D)[b, :count].float()  # [count, 2, P, Hkv, D]
+                keys = kv[:, 0].reshape(count * P, Hkv, D)[:length]
+                vals = kv[:, 1].reshape(count * P, Hkv, D)[:length]
+                # bounds of the state = exact extrema of the history (append + mirror)
+                lo = torch.stack([keys[p * P : (p + 1) * P].amin(0) for p in range(count)])
+                hi = torch.stack([keys[p * P : (p + 1) * P].amax(0) for p in range(count)])
+                torch.testing.assert_close(state.minimum[l, b, :count].float().cpu(), lo, rtol=0, atol=0)
+                torch.testing.assert_close(state.maximum[l, b, :count].float().cpu(), hi, rtol=0, atol=0)
+                pages = oracle.quest_pages(q[b].cpu(), lo, hi, length, P, wl.top_pages)
+                np.testing.assert_array_equal(layer_pages[b, :, : pages.shape[1]].cpu().numpy(), pages)
+                positions = pages_to_positions(pages, length, P)
+                expected = oracle.selection_oracle(q[b].cpu(), keys, vals, positions)
+                got = out[b].float().cpu().double().numpy()
+                assert np.all(np.abs(got - expected) <= 2e-2 + 1e-2 * np.abs(expected)), np.abs(got - expected).max()
+                unions += int(union_count[b])
+    stats = state.row_stats.tolist()
+    assert sum(stats) == unions  # every selected row was a resident hit, a hot hit or a miss
+    assert stats[2] > 0 and stats[0] > 0 and stats[1] > 0
+
+
+@pytest.mark.gpu
+def test_batched_engine_rejects_a_hot_region_below_the_union_bound(gpu):
+    from mini_hisparse_amd.batched_engine import BatchedDecodeEngine, build_state, random_model
+
+    wl = tiny(hot_rows=128)
+    with pytest.raises(ValueError, match="below the union bound"):
+        BatchedDecodeEngine(random_model(wl, gpu), build_state(wl, gpu), wl.top_pages)
