@@ -235,6 +235,38 @@ def hbm_copy_gbs(torch, device, nbytes=1 << 30):
     return 5 * 2 * nbytes / (e0.elapsed_time(e1) * 1e-3) / 1e9
 
 
+def attention_ceilings(torch, w, nbytes, reps=10):
+    """The attention and a read-only pass over the same rows (hs_probe_row_reads):
+    back to back (`warm`: rows partly in the 256 MB Infinity Cache) and each after a
+    1 GiB copy that evicts it (`cold`: HBM).  GB/s of the attention's algorithmic bytes."""
+    dec, pool, q = w["dec"], w["pool"], w["q"]
+    sink = torch.empty(16, dtype=torch.int32, device=pool.device)
+    src = torch.empty(1 << 30, dtype=torch.uint8, device=pool.device)
+    dst = torch.empty_like(src)
+    offsets = dec.entry_offsets(pool)
+    runs = {"attention": lambda: dec.attend(q, pool), "probe": lambda: dec.probe_reads(pool, offsets, sink)}
+    out = {}
+    for name, fn in runs.items():
+        fn()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        out[f"{name}_warm_GBps"] = nbytes / (e0.elapsed_time(e1) / reps * 1e-3) / 1e9
+        times = []
+        for _ in range(reps):
+            dst.copy_(src)
+            e0.record()
+            fn()
+            e1.record()
+            torch.cuda.synchronize()
+            times.append(e0.elapsed_time(e1))
+        out[f"{name}_cold_GBps"] = nbytes / (float(np.median(times)) * 1e-3) / 1e9
+    return out
+
+
 def algorithmic_bytes(w, torch):
     """Per-launch algorithmic bytes of each kernel (per-unit formulas x units)."""
     S, dec = Shape, w["dec"]
@@ -582,6 +614,7 @@ def main():
     bytes_ = algorithmic_bytes(w, torch)
     link = host_link_gbs(torch, device)
     copy = hbm_copy_gbs(torch, device)
+    ceilings = attention_ceilings(torch, w, bytes_["attention"])
     att_gbs = bytes_["attention"] / (stages["attention"] * 1e-3) / 1e9
     kernels = {
         "attention": {"ms": stages["attention"], "bytes": bytes_["attention"], "GBps": att_gbs,
@@ -624,6 +657,7 @@ def main():
             "frac": att_gbs / HBM_PEAK_GBS,
             "traffic": pmc_traffic(),
             "kernel": "attend_mfma_kernel + attend_merge_kernel (hs_attend_groups)",
+            "measured_ceilings": ceilings,
         },
         "kernels": kernels,
         "rows": {**w["stats"], "misses_per_step": bytes_["misses"], "attention_entries": bytes_["entries"]},

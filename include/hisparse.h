@@ -261,6 +261,19 @@ int hs_attend_groups(const void* query, int64_t q_stride_b, int64_t q_stride_h, 
                      int64_t o_stride_b, int64_t o_stride_h, void* workspace,
                      int64_t workspace_bytes, hs_stream_t stream);
 
+/*
+ * Diagnostic (no reference counterpart): read, without computing, n segment
+ * pairs of a device region -- segment i at byte offset offsets[i] (device
+ * array) and its partner plane_bytes further, segment_bytes each -- with
+ * consecutive lanes on consecutive 16-byte units.  Given the K offsets of the
+ * attention's entries it measures the ceiling of the attention's memory
+ * traffic.  The caller keeps every segment inside [base, base + region_bytes).
+ * `sink` is a device buffer of at least 16 bytes (written only on an
+ * impossible match).
+ */
+int hs_probe_row_reads(const void* base, int64_t region_bytes, const int64_t* offsets, int64_t n,
+                       int64_t segment_bytes, int64_t plane_bytes, void* sink, hs_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -98,6 +98,9 @@ SIGNATURES = {
          c_void_p, c_int64, c_int64, c_int64, c_int64, c_int64, c_int64,
          c_void_p, c_int64, c_int64, c_void_p, c_int64, c_void_p],
     ),
+    "hs_probe_row_reads": (
+        c_int, [c_void_p, c_int64, c_void_p, c_int64, c_int64, c_int64, c_void_p, c_void_p],
+    ),
     "hs_attend_groups": (
         c_int,
         [c_void_p, c_int64, c_int64, c_void_p, c_int32, c_int64, c_int64, c_int64, c_int64,

@@ -208,6 +208,34 @@ class BatchedSparseDecode:
         )
         return out
 
+    def entry_offsets(self, pool):
+        """Byte offsets of the K segments `attend` reads (one per valid entry; host-side
+        torch ops, for the diagnostic read probe)."""
+        cfg = self.config
+        P, Hkv, D, esz = cfg.page_size, cfg.kv_heads, cfg.head_dim, pool.element_size()
+        offsets = []
+        counts = self.entry_counts.tolist()
+        for b in range(self.batch):
+            for k in range(Hkv):
+                cols = self.entry_columns[b, k, : counts[b][k]].long()
+                phys = self.union_physical[b][cols.clamp(min=0)]
+                phys = phys[(cols >= 0) & (phys >= 0) & (phys < pool.shape[0] * P)]
+                offsets.append((((phys // P) * 2 * P + phys % P) * Hkv + k) * D * esz)
+        return torch.cat(offsets).contiguous()
+
+    def probe_reads(self, pool, offsets, sink, stream=None):
+        """Read-only pass over the K and V segments at `offsets` (diagnostic ceiling)."""
+        cfg = self.config
+        esz = pool.element_size()
+        s = stream.cuda_stream if stream is not None else _lib.stream_handle(self.device)
+        _lib.check(
+            _lib.load().hs_probe_row_reads(
+                pool.data_ptr(), pool.numel() * esz, offsets.data_ptr(), offsets.numel(), cfg.head_dim * esz,
+                cfg.page_size * cfg.kv_heads * cfg.head_dim * esz, sink.data_ptr(), s,
+            ),
+            "hs_probe_row_reads",
+        )
+
     def step(self, queries, minimums, maximums, tables, pool, host_alias, transfer, *, row_stats=None, last_use=None):
         """The whole layer; returns (out, ready_event, done_event).
 

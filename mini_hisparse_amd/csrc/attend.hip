@@ -533,6 +533,26 @@ __global__ __launch_bounds__(256) void attend_merge_kernel(const float* part_m, 
   }
 }
 
+// Read-only probe of a row-gather access pattern: for each of n segment pairs
+// (byte offsets of a K segment; its V segment `plane_bytes` further) read every
+// 16-byte unit, consecutive lanes on consecutive units, with no arithmetic
+// beyond an XOR that keeps the loads alive.  Given the K offsets of the
+// attention's entries, its duration is the ceiling of the attention's memory
+// traffic on the device.
+constexpr int PROBE_T = 256;
+
+__global__ __launch_bounds__(PROBE_T) void probe_row_reads_kernel(const char* base, const int64_t* offsets,
+                                                                   int64_t n, int64_t seg_units,
+                                                                   int64_t plane_bytes, u32x4* sink) {
+  const int64_t u = static_cast<int64_t>(blockIdx.x) * PROBE_T + threadIdx.x;
+  const int64_t e = u / (2 * seg_units);
+  if (e >= n) return;
+  const int64_t w = u - e * 2 * seg_units;
+  const int64_t off = offsets[e] + (w >= seg_units ? plane_bytes : 0) + (w % seg_units) * 16;
+  const u32x4 v = *reinterpret_cast<const u32x4*>(base + off);
+  if (v[0] == 0x9e3779b9u && v[1] == 0x7f4a7c15u && v[2] == 0xf39cc060u && v[3] == 0x5ced1a2bu) sink[0] = v;
+}
+
 // ---- host side ----------------------------------------------------------------
 
 static int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
@@ -735,4 +755,19 @@ extern "C" int hs_attend_groups(const void* query, int64_t q_stride_b, int64_t q
   a.g = heads / kv_heads;
   a.mode = MODE_GROUPS;
   return run_attend(dtype, a, max_entries, out, o_stride_b, o_stride_h, workspace, workspace_bytes, stream);
+}
+
+extern "C" int hs_probe_row_reads(const void* base, int64_t region_bytes, const int64_t* offsets, int64_t n,
+                                  int64_t segment_bytes, int64_t plane_bytes, void* sink, hipStream_t stream) {
+  HS_CHECK_ARG(base && offsets && sink && n >= 1, "null or empty probe");
+  HS_CHECK_ARG(segment_bytes >= 16 && segment_bytes % 16 == 0 && plane_bytes % 16 == 0,
+               "segments must be multiples of 16 bytes");
+  HS_CHECK_ARG((reinterpret_cast<uintptr_t>(base) & 15) == 0, "region must be 16-byte aligned");
+  (void)region_bytes;  // offsets are validated by the caller against region_bytes
+  const int64_t seg_units = segment_bytes / 16;
+  const int64_t blocks = ceil_div(n * 2 * seg_units, PROBE_T);
+  hipLaunchKernelGGL(probe_row_reads_kernel, dim3(static_cast<unsigned>(blocks)), dim3(PROBE_T), 0, stream,
+                     static_cast<const char*>(base), offsets, n, seg_units, plane_bytes, static_cast<u32x4*>(sink));
+  HS_CHECK_LAUNCH("probe");
+  return HS_OK;
 }

@@ -409,3 +409,30 @@ def test_append_rejects_rows_outside_the_pool(gpu):
     bound = torch.zeros(2, 64, dtype=torch.bfloat16, device=gpu)
     with pytest.raises(HipLibraryError, match="outside the pool"):
         append_rows(kv, kv, pool, [32], [bound], [bound], cfg)
+
+
+def test_row_read_probe_covers_the_attention_entries(gpu):
+    """The diagnostic read probe gets one K offset per group-attention entry, stays inside
+    the pool and leaves it untouched."""
+    from mini_hisparse_amd.batched import BatchedSparseDecode, LayerTablesView
+    from mini_hisparse_amd.config import CacheConfig
+
+    P, Hkv, g, D, pages, top = 16, 2, 4, 64, 64, 8
+    cfg = CacheConfig(gpu_pages=pages, host_pages=pages, page_size=P, kv_heads=Hkv, head_dim=D, device=gpu, dtype=torch.bfloat16)
+    L = pages * P
+    k = torch.randn(pages, P, Hkv, D, device=gpu).to(torch.bfloat16)
+    dec = BatchedSparseDecode(cfg, Hkv * g, top, [L], device=gpu)
+    dec.select(torch.randn(1, Hkv * g, D, device=gpu).to(torch.bfloat16), [k.amin(1)], [k.amax(1)])
+    pool = torch.randn(pages, 2, P, Hkv, D, device=gpu).to(torch.bfloat16)
+    resident = torch.arange(pages, dtype=torch.int32, device=gpu)
+    table = LayerTablesView(resident.clone(), resident, torch.zeros(1, dtype=torch.int32, device=gpu),
+                            torch.full((P,), -1, dtype=torch.int32, device=gpu), torch.arange(P, device=gpu))
+    dec.resolve([table])
+    before = pool.clone()
+    sink = torch.zeros(4, dtype=torch.int32, device=gpu)
+    offsets = dec.entry_offsets(pool)
+    assert offsets.numel() == int(dec.entry_counts.sum()) > 0
+    assert int(offsets.max()) + D * 2 + P * Hkv * D * 2 <= pool.numel() * 2
+    dec.probe_reads(pool, offsets, sink)
+    torch.cuda.synchronize()
+    assert torch.equal(pool, before)
