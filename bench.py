@@ -44,6 +44,10 @@ def parse_args():
                    help="pinned host memory for the model workloads' histories; the batch is cut to "
                         "what fits (the GPU boxes here pin at most 64 GiB)")
     p.add_argument("--seed", type=int, default=2024)
+    p.add_argument("--parts", type=int, default=1,
+                   help="request groups of the microbench step: group g gathers while g+1 resolves "
+                        "and g-1 attends (1 = no overlap; on MI355X the host reads of a running "
+                        "gather stall concurrent HBM kernels, so overlap does not pay)")
     p.add_argument("--no-cpu-baseline", action="store_true", help="skip the CPU oracle leg")
     p.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU sample work")
     p.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
@@ -66,7 +70,7 @@ class Shape:
 
 def build_workload(args, torch, device):
     """Seeded synthetic state of the microbench in HBM and pinned host memory."""
-    from mini_hisparse_amd.batched import BatchedSparseDecode, LayerTablesView
+    from mini_hisparse_amd.batched import BatchedSparseDecode, LayerTablesView, PipelinedSparseDecode
     from mini_hisparse_amd.config import CacheConfig
     from mini_hisparse_amd.row_kernels import MappedHost
 
@@ -152,8 +156,9 @@ def build_workload(args, torch, device):
     torch.cuda.synchronize()
     cfg = CacheConfig(gpu_pages=blocks, host_pages=B * C, page_size=P, kv_heads=Hkv, head_dim=D, device=device, dtype=torch.bfloat16)
     dec = BatchedSparseDecode(cfg, S.heads, S.top, [L] * B, device=device)
+    pipe = PipelinedSparseDecode(cfg, S.heads, S.top, [L] * B, parts=args.parts, device=device)
     return dict(
-        cfg=cfg, dec=dec, q=q, kmin=kmin, kmax=kmax, host=host, alias=MappedHost(host), pool=pool,
+        cfg=cfg, dec=dec, pipe=pipe, q=q, kmin=kmin, kmax=kmax, host=host, alias=MappedHost(host), pool=pool,
         tables=tables, tags_all=tags_all, lru_all=lru_all, tags0=tags_all.clone(), lru0=lru_all.clone(),
         stats=stats, length=L,
     )
@@ -192,6 +197,23 @@ def run_steps(torch, w, steps, record):
     w["last_use"] = last
     w["out"] = out
     return events
+
+
+def run_pipelined(torch, w, steps):
+    """`steps` decode steps of the whole batch as overlapped request groups."""
+    pipe, device = w["pipe"], w["pool"].device
+    transfer = w.setdefault("transfer", torch.cuda.Stream(device))
+    row_stats = w.setdefault("row_stats", torch.zeros(3, dtype=torch.int64, device=device))
+    out = w.get("pipe_out")
+    for _ in range(steps):
+        w["tags_all"].copy_(w["tags0"])
+        w["lru_all"].copy_(w["lru0"])
+        out, done = pipe.step(w["q"], w["kmin"], w["kmax"], w["tables"], w["pool"], w["alias"], transfer,
+                              row_stats=row_stats, out=out)
+        # the next step restores the hot tables only after this step's readers
+        transfer.wait_event(done)
+    w["pipe_out"] = out
+    return out
 
 
 def stage_ms(events):
@@ -602,15 +624,22 @@ def main():
         args.batch = 8
     print(f"[bench] building workload (batch {args.batch})", file=sys.stderr, flush=True)
     w = build_workload(args, torch, device)
-    run_steps(torch, w, args.warmup, record=False)
+    run_pipelined(torch, w, args.warmup)
     torch.cuda.synchronize()
     print("[bench] timing", file=sys.stderr, flush=True)
     t0 = time.perf_counter()
-    events = run_steps(torch, w, args.steps, record=True)
+    run_pipelined(torch, w, args.steps)
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     ms_per_step = elapsed * 1e3 / args.steps
+    # per-stage times, the roofline and the CPU parity check from the same step run
+    # without the overlap (every stage of the whole batch timed on its own stream)
+    run_steps(torch, w, 2, record=False)
+    events = run_steps(torch, w, args.steps, record=True)
+    torch.cuda.synchronize()
     stages = stage_ms(events)
+    sequential_ms = float(np.mean([e[0].elapsed_time(e[6]) for e in events]))
+    diff = (w["pipe_out"].float() - w["out"].float()).abs().max().item()
     bytes_ = algorithmic_bytes(w, torch)
     link = host_link_gbs(torch, device)
     copy = hbm_copy_gbs(torch, device)
@@ -644,7 +673,8 @@ def main():
         "data": "synthetic (seeded K/V ~ N(0,1), 2% channels x8; random-init tables)",
         "config": {
             "workload": "microbench (BASELINE configs[1]): 1 layer, 64 q / 8 kv heads, head_dim 128, "
-            "page 16, 4096 pages/request, batch 8, Quest top-64, 50% resident / 30% hot / 20% miss",
+            f"page 16, 4096 pages/request, batch {args.batch}, Quest top-64, 50% resident / 30% hot / 20% miss; "
+            f"{args.parts} request groups overlapped",
             "global_batch": args.batch,
             "seq_len": w["length"],
             "parallelism": "none (1 GPU)",
@@ -661,6 +691,8 @@ def main():
         },
         "kernels": kernels,
         "rows": {**w["stats"], "misses_per_step": bytes_["misses"], "attention_entries": bytes_["entries"]},
+        "step_without_overlap_ms": sequential_ms,
+        "overlapped_vs_sequential_max_abs_diff": diff,
         "hbm_copy_GBps": copy,
     }
     if not args.no_cpu_baseline:

@@ -258,3 +258,56 @@ class BatchedSparseDecode:
         done = torch.cuda.Event()
         done.record(compute)
         return out, ready, done
+
+
+class PipelinedSparseDecode:
+    """The same layer for B requests as contiguous request groups, overlapped.
+
+    Group g's gather (transfer stream) starts as soon as g is resolved, while
+    the compute stream selects and resolves group g+1; group g's attention runs
+    while later groups gather.  Each group is a :class:`BatchedSparseDecode`
+    with its own buffers; per group the stream and event order is that of
+    ``BatchedSparseDecode.step``.
+    """
+
+    def __init__(self, config, heads, top_pages, lengths, *, parts=2, keep_sink=True, device="cuda",
+                 capacity_lengths=None):
+        lengths = list(lengths)
+        caps = list(capacity_lengths or lengths)
+        parts = max(1, min(parts, len(lengths)))
+        bounds = [round(i * len(lengths) / parts) for i in range(parts + 1)]
+        self.slices = [slice(bounds[i], bounds[i + 1]) for i in range(parts)]
+        self.parts = [
+            BatchedSparseDecode(config, heads, top_pages, lengths[s], keep_sink=keep_sink, device=device,
+                                capacity_lengths=caps[s])
+            for s in self.slices
+        ]
+        self.batch = len(lengths)
+        self.device = torch.device(device)
+
+    def set_lengths(self, lengths):
+        for s, part in zip(self.slices, self.parts):
+            part.set_lengths(list(lengths)[s])
+
+    def step(self, queries, minimums, maximums, tables, pool, host_alias, transfer, *, row_stats=None, out=None):
+        """The whole layer for all groups; returns (out [B, Hq, D], done_event)."""
+        compute = torch.cuda.current_stream(self.device)
+        if out is None:
+            out = torch.empty_like(queries if queries.dtype == pool.dtype else queries.to(pool.dtype))
+        ready = []
+        for s, part in zip(self.slices, self.parts):
+            part.select(queries[s], minimums[s], maximums[s])
+            part.resolve(tables[s], row_stats=row_stats)
+            resolved = torch.cuda.Event()
+            resolved.record(compute)
+            transfer.wait_event(resolved)
+            part.gather(host_alias, pool, transfer)
+            event = torch.cuda.Event()
+            event.record(transfer)
+            ready.append(event)
+        for s, part, event in zip(self.slices, self.parts, ready):
+            compute.wait_event(event)
+            part.attend(queries[s], pool, out=out[s])
+        done = torch.cuda.Event()
+        done.record(compute)
+        return out, done

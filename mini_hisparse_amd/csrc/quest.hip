@@ -15,6 +15,8 @@
 // ascending union of selected tokens (padded with -1), each head's union
 // columns, and per KV head the deduplicated union columns its query heads read
 // with a bit mask of those heads (the entry lists of the group attention).
+#include <algorithm>
+
 #include "hs_common.h"
 
 namespace hs {
@@ -353,6 +355,7 @@ struct UnionArgs {
   int64_t ecap;
   int32_t* ecount;       // [B, Hkv]
   int32_t* status;       // nonzero on overflow
+  int64_t words;         // bitmap words of the longest history
 };
 
 __device__ __forceinline__ bool head_has_page(const int32_t* row, int64_t k, int32_t p) {
@@ -365,13 +368,22 @@ __device__ __forceinline__ bool head_has_page(const int32_t* row, int64_t k, int
   return lo < k && row[lo] == p;
 }
 
-// blockIdx.x < Hkv: group entries of that KV head; blockIdx.x == Hkv: union
-// positions, per-head columns and the union size.
+// Workgroup roles per request (blockIdx.y): blockIdx.x < Hkv builds the group
+// entries of that KV head; == Hkv the union positions and size; Hkv + 1 + h
+// the union columns of query head h.  Every role rebuilds the selected-page
+// bitmap and its word prefix popcounts in LDS (a few hundred bits), so the
+// roles run side by side.  A group entry's head mask comes from an LDS array
+// indexed by the page's rank among the group's pages.
+constexpr int64_t UMAXMASK = 4096;  // group pages (g * top) with an LDS mask slot
+
+// Dynamic LDS: four bitmaps of `a.words` words (longest history of the batch).
 __global__ __launch_bounds__(UT) void build_union_kernel(UnionArgs a) {
-  __shared__ uint32_t ubits[UMAXPAGES / 32];
-  __shared__ uint32_t uprefix[UMAXPAGES / 32];
-  __shared__ uint32_t gbits[UMAXPAGES / 32];
-  __shared__ uint32_t gprefix[UMAXPAGES / 32];
+  extern __shared__ uint32_t union_lds[];
+  uint32_t* ubits = union_lds;
+  uint32_t* uprefix = ubits + a.words;
+  uint32_t* gbits = uprefix + a.words;
+  uint32_t* gprefix = gbits + a.words;
+  __shared__ uint32_t gmask[UMAXMASK];
   __shared__ int32_t scan32[16];
   const int64_t b = blockIdx.y;
   const int64_t part = blockIdx.x;
@@ -382,11 +394,14 @@ __global__ __launch_bounds__(UT) void build_union_kernel(UnionArgs a) {
   const int64_t words = (count + 31) / 32;
   const int32_t* pg = a.pages + b * a.p_sb;
   const bool group = part < a.Hkv;
+  const bool masks_in_lds = a.g * k <= UMAXMASK;
 
   for (int64_t i = threadIdx.x; i < words; i += UT) {
     ubits[i] = 0u;
     gbits[i] = 0u;
   }
+  if (group && masks_in_lds)
+    for (int64_t i = threadIdx.x; i < a.g * k; i += UT) gmask[i] = 0u;
   __syncthreads();
   for (int64_t i = threadIdx.x; i < a.Hq * k; i += UT) {
     const int64_t h = i / k, j = i - h * k;
@@ -423,7 +438,7 @@ __global__ __launch_bounds__(UT) void build_union_kernel(UnionArgs a) {
     return static_cast<int64_t>(pre[p >> 5]) + __popc(below);
   };
 
-  if (!group) {
+  if (part == a.Hkv) {
     const int64_t upages = rank_of(ubits, uprefix, count - 1) + 1;  // the tail page is always selected
     const int64_t n = upages * P - (P - tail_len);
     if (threadIdx.x == 0) {
@@ -439,11 +454,12 @@ __global__ __launch_bounds__(UT) void build_union_kernel(UnionArgs a) {
         if (base + off < a.pos_cap) pos[base + off] = static_cast<int32_t>(p * P + off);
     }
     for (int64_t i = n + threadIdx.x; i < a.pos_cap; i += UT) pos[i] = -1;
-    // per-head columns: head h's j-th token (its pages ascending, tail last)
+  } else if (part > a.Hkv) {
+    // union columns of head h: its j-th token (its pages ascending, tail last)
+    const int64_t h = part - a.Hkv - 1;
     const int64_t W = (k - 1) * P + tail_len;
-    int64_t* hc = a.head_columns + b * a.Hq * a.width;
-    for (int64_t e = threadIdx.x; e < a.Hq * a.width; e += UT) {
-      const int64_t h = e / a.width, jj = e - h * a.width;
+    int64_t* hc = a.head_columns + (b * a.Hq + h) * a.width;
+    for (int64_t jj = threadIdx.x; jj < a.width; jj += UT) {
       int64_t col = -1;
       if (jj < W) {
         int64_t p, off;
@@ -456,7 +472,7 @@ __global__ __launch_bounds__(UT) void build_union_kernel(UnionArgs a) {
         }
         col = rank_of(ubits, uprefix, p) * P + off;
       }
-      hc[e] = col;
+      hc[jj] = col;
     }
   } else {
     const int64_t kv = part;
@@ -466,14 +482,29 @@ __global__ __launch_bounds__(UT) void build_union_kernel(UnionArgs a) {
       a.ecount[b * a.Hkv + kv] = static_cast<int32_t>(E < a.ecap ? E : a.ecap);
       if (E > a.ecap) atomicOr(a.status, 2);
     }
+    if (masks_in_lds) {
+      // head bits of each group page, indexed by the page's rank in the group
+      for (int64_t i = threadIdx.x; i < a.g * k; i += UT) {
+        const int64_t hl = i / k, j = i - hl * k;
+        const int32_t p = pg[(kv * a.g + hl) * a.top + j];
+        if (p < 0 || p >= count) continue;
+        atomicOr(&gmask[rank_of(gbits, gprefix, p)], 1u << hl);
+      }
+      __syncthreads();
+    }
     int32_t* ec = a.ecol + (b * a.Hkv + kv) * a.ecap;
     uint32_t* em = a.emask + (b * a.Hkv + kv) * a.ecap;
     for (int64_t p = threadIdx.x; p < count; p += UT) {
       if (!((gbits[p >> 5] >> (p & 31)) & 1u)) continue;
+      const int64_t grank = rank_of(gbits, gprefix, p);
       uint32_t mask = 0u;
-      for (int64_t hl = 0; hl < a.g; ++hl)
-        if (head_has_page(pg + (kv * a.g + hl) * a.top, k, static_cast<int32_t>(p))) mask |= 1u << hl;
-      const int64_t gbase = rank_of(gbits, gprefix, p) * P;
+      if (masks_in_lds) {
+        mask = gmask[grank];
+      } else {
+        for (int64_t hl = 0; hl < a.g; ++hl)
+          if (head_has_page(pg + (kv * a.g + hl) * a.top, k, static_cast<int32_t>(p))) mask |= 1u << hl;
+      }
+      const int64_t gbase = grank * P;
       const int64_t ubase = rank_of(ubits, uprefix, p) * P;
       const int64_t plen = p == count - 1 ? tail_len : P;
       for (int64_t off = 0; off < plen; ++off) {
@@ -628,8 +659,11 @@ extern "C" int hs_build_union(const int32_t* pages, int64_t p_stride_b, int64_t 
   a.ecap = entry_capacity;
   a.ecount = entry_counts;
   a.status = status;
-  hipLaunchKernelGGL(build_union_kernel, dim3(static_cast<unsigned>(kv_heads + 1), static_cast<unsigned>(batch)),
-                     dim3(UT), 0, stream, a);
+  int64_t max_count = 1;
+  for (int64_t i = 0; i < batch; ++i) max_count = std::max(max_count, ceil_div(lengths[i], page_size));
+  a.words = (max_count + 31) / 32;
+  hipLaunchKernelGGL(build_union_kernel, dim3(static_cast<unsigned>(kv_heads + 1 + heads), static_cast<unsigned>(batch)),
+                     dim3(UT), static_cast<size_t>(4 * a.words * 4), stream, a);
   HS_CHECK_LAUNCH("union builder");
   return HS_OK;
 }
