@@ -34,9 +34,9 @@ def parse_args():
     p = argparse.ArgumentParser(description=__doc__)
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--workload", default="microbench",
-                   choices=["microbench", "qwen2.5-0.5b", "qwen2.5-7b"],
+                   choices=["microbench", "qwen2.5-0.5b", "qwen2.5-7b", "qwen2.5-32b-stress"],
                    help="microbench = BASELINE configs[1] (default); the Qwen shapes run the "
-                        "layer-major batched engine end to end (configs[2], configs[3])")
+                        "layer-major batched engine end to end (configs[2], configs[3], configs[4])")
     p.add_argument("--steps", type=int, default=20)
     p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--batch", type=int, default=None, help="requests (default: the workload's)")
@@ -451,7 +451,14 @@ def model_cpu_baseline(torch, engine, wl, budget_s):
     tables = [x.cpu().numpy() for x in (t.source, t.resident, t.hot, t.tags, t.lru)]
     host = st.host[0].view(B, C, 2, P, Hkv, D)[0]
     t0 = time.perf_counter()
-    pages = oracle.quest_pages(q, lo, hi, length, P, wl.top_pages)
+    if wl.selector == "uniform":  # the tail page and top - 1 uniform others, for every head
+        rng = np.random.default_rng(5)
+        drawn = np.sort(np.append(rng.choice(count - 1, size=wl.top_pages - 1, replace=False), count - 1))
+        pages = np.repeat(drawn[None, :], wl.heads, axis=0)
+        selection = f"{wl.top_pages} uniform pages of {count}"
+    else:
+        pages = oracle.quest_pages(q, lo, hi, length, P, wl.top_pages)
+        selection = f"Quest over {count} pages"
     positions = pages_to_positions(pages, length, P)
     union, cols = oracle.from_selection(positions)
     phys, mh, md, counts, _, _ = oracle.resolve_rows(union, *tables, length, P, head_columns=cols)
@@ -487,7 +494,7 @@ def model_cpu_baseline(torch, engine, wl, budget_s):
         "unit": "tokens/s",
         "cores": cores,
         "kind": "port",
-        "sample": f"extrapolated: one (request, layer) sparse path (numpy oracle: Quest over {count} pages, "
+        "sample": f"extrapolated: one (request, layer) sparse path (numpy oracle: {selection}, "
         f"union, resolver, {int(counts[2])}-row host gather loop, attention; {sparse_s:.2f} s, 1 thread) "
         f"x {L * B} + one dense layer for {B} tokens ({dense_s:.2f} s, torch fp32, {cores} threads) x {L} "
         f"+ LM head ({head_s:.2f} s) = {step_s:.1f} s per step",
@@ -521,7 +528,7 @@ def run_model_workload(args, torch, device):
     print(f"[bench] {wl.name}: model + synthetic history (batch {wl.batch}, {wl.context} tokens)", file=sys.stderr, flush=True)
     model = random_model(wl, device, seed=args.seed)
     state = build_state(wl, device, seed=args.seed)
-    engine = BatchedDecodeEngine(model, state, wl.top_pages)
+    engine = BatchedDecodeEngine(model, state, wl.top_pages, selector=wl.selector, seed=args.seed)
     setup_s = time.perf_counter() - t0
     gen = torch.Generator(device=device).manual_seed(args.seed)
     tokens = torch.randint(0, wl.vocab, (wl.batch,), generator=gen, device=device)
@@ -570,8 +577,10 @@ def run_model_workload(args, torch, device):
         "config": {
             "workload": f"{wl.name} end to end (layer-major batched engine): {wl.layers} layers, hidden "
             f"{wl.hidden}, {wl.heads} q / {wl.kv_heads} kv heads, head_dim {wl.head_dim}, FFN {wl.ffn}, "
-            f"batch {wl.batch}, {wl.context}-token histories, Quest top-{wl.top_pages} pages, "
-            f"{wl.resident_fraction:.0%} of pages resident, hot_rows {wl.hot_rows}"
+            f"batch {wl.batch}, {wl.context}-token histories, "
+            + (f"Quest top-{wl.top_pages} pages, " if wl.selector == "quest" else
+               f"{wl.top_pages} pages resampled uniformly each step (tail page forced), shared by every head, ")
+            + f"{wl.resident_fraction:.0%} of pages resident, hot_rows {wl.hot_rows}"
             + (f"; batch cut from {configured}: {configured} histories need "
                f"{configured * per_request / 2**30:.0f} GiB of pinned host memory, the box pins at most "
                f"64 GiB (budget {args.host_budget_gib:g} GiB)" if wl.batch < configured else ""),

@@ -43,15 +43,19 @@ class LayerTablesView:
 class BatchedSparseDecode:
     """Quest -> union -> resolve -> gather -> attention for B requests of one layer."""
 
-    def __init__(self, config, heads, top_pages, lengths, *, keep_sink=True, device="cuda", capacity_lengths=None):
+    def __init__(self, config, heads, top_pages, lengths, *, keep_sink=True, device="cuda", capacity_lengths=None,
+                 shared_selection=False):
         """``capacity_lengths`` (default ``lengths``) sizes every buffer, so that later
-        ``set_lengths`` calls up to those lengths (a decode run) allocate nothing."""
+        ``set_lengths`` calls up to those lengths (a decode run) allocate nothing.
+        ``shared_selection``: every head of a request selects the same pages
+        (:meth:`select_pages`), so the union is one head's selection."""
         self.config = config
         self.heads = heads
         self.kv_heads = config.kv_heads
         self.groups = heads // config.kv_heads
         self.top = top_pages
         self.keep_sink = keep_sink
+        self.shared_selection = shared_selection
         self.device = torch.device(device)
         self.batch = len(lengths)
         self._shape(list(lengths), list(capacity_lengths or lengths))
@@ -63,8 +67,10 @@ class BatchedSparseDecode:
         self.lengths = lengths
         self.counts = [ceil(l / P) for l in lengths]
         # union sizes grow with the length, and a head's width is at most top pages
-        self.capacity = max(union_bound(l, P, self.top, self.heads, self.keep_sink) for l in caps)
-        self.entry_capacity = max(union_bound(l, P, self.top, self.groups, self.keep_sink) for l in caps)
+        union_heads = 1 if self.shared_selection else self.heads
+        group_heads = 1 if self.shared_selection else self.groups
+        self.capacity = max(union_bound(l, P, self.top, union_heads, self.keep_sink) for l in caps)
+        self.entry_capacity = max(union_bound(l, P, self.top, group_heads, self.keep_sink) for l in caps)
         self.width = max(min(self.top * P, l) for l in caps)
         i32, i64 = torch.int32, torch.int64
         self.pages = torch.empty((B, self.heads, self.top), dtype=i32, device=dev)
@@ -112,6 +118,8 @@ class BatchedSparseDecode:
     # -- stages ------------------------------------------------------------
     def select(self, queries, minimums, maximums, stream=None):
         """Quest scorer + top-k and the device union for all B requests."""
+        if self.shared_selection:
+            raise RuntimeError("a shared-selection decoder takes its pages from select_pages")
         B = self.batch
         q = queries.float().contiguous()
         lib = _lib.load()
@@ -127,10 +135,23 @@ class BatchedSparseDecode:
             ),
             "hs_quest_topk",
         )
+        self._build_union(s)
+
+    def select_pages(self, pages, stream=None):
+        """A selection given as pages: ``pages`` [B, top] int32 on the device, ascending
+        and distinct, min(top, count) of them per request, read by every head."""
+        if pages.shape != (self.batch, self.top) or pages.dtype != torch.int32:
+            raise ValueError(f"pages must be int32 [{self.batch}, {self.top}]")
+        s = stream.cuda_stream if stream is not None else _lib.stream_handle(self.device)
+        self.pages.copy_(pages[:, None, :].expand(self.batch, self.heads, self.top))
+        self._build_union(s)
+
+    def _build_union(self, s):
+        lib = _lib.load()
         _lib.check(
             lib.hs_build_union(
                 self.pages.data_ptr(), self.pages.stride(0), self.top, self._len_arr,
-                self.config.page_size, B, self.heads, self.kv_heads, self.positions.data_ptr(),
+                self.config.page_size, self.batch, self.heads, self.kv_heads, self.positions.data_ptr(),
                 self.capacity, self.head_columns.data_ptr(), self.width, self.union_count.data_ptr(),
                 self.entry_columns.data_ptr(), self.entry_masks.data_ptr(), self.entry_capacity,
                 self.entry_counts.data_ptr(), self.status.data_ptr(), s,

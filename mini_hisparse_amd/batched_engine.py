@@ -13,6 +13,8 @@ requests:
     dense   RMSNorm, q/k/v projections, rotary embedding          (PyTorch-ROCm)
     append  hs_append_rows: tail rows, Quest bounds, host mirror   (HIP)
     select  hs_quest_topk + hs_build_union                         (HIP)
+            (or pages resampled uniformly per step, shared by all heads,
+            + hs_build_union: the miss-heavy stress shape)
     resolve hs_resolve_rows_batched, row statistics fused          (HIP, compute stream)
     gather  hs_gather_rows_batched, host -> hot rows               (HIP, transfer stream)
     attend  hs_attend_groups                                       (HIP)
@@ -64,6 +66,7 @@ class DecodeWorkload:
     hot_rows: int
     page_size: int = 16
     dtype: torch.dtype = torch.bfloat16
+    selector: str = "quest"  # "quest", or "uniform": pages resampled every step, shared by all heads
 
     def model_config(self):
         return ModelConfig(
@@ -73,8 +76,10 @@ class DecodeWorkload:
         )
 
 
-# BASELINE configs[2] and configs[3] (hot rows: 2U for the 0.5B shape; the
-# reference's cap of 32768 for the 7B shape, hybrid.py:34)
+# BASELINE configs[2], configs[3] and configs[4] (hot rows: 2U for the 0.5B shape;
+# the reference's cap of 32768 for the 7B shape, hybrid.py:34; 2U of one shared
+# 64-page selection for the 32B stress shape, whose 40% resident pages and
+# uniformly resampled selection make about 60% of the selected rows miss)
 WORKLOADS = {
     "qwen2.5-0.5b": DecodeWorkload(
         "qwen2.5-0.5b", layers=24, hidden=896, heads=14, kv_heads=2, head_dim=64, ffn=4864,
@@ -86,7 +91,32 @@ WORKLOADS = {
         vocab=152064, batch=16, context=131072, steps=256, top_pages=64, resident_fraction=0.15,
         hot_rows=32768,
     ),
+    "qwen2.5-32b-stress": DecodeWorkload(
+        "qwen2.5-32b-stress", layers=64, hidden=5120, heads=40, kv_heads=8, head_dim=128, ffn=27648,
+        vocab=152064, batch=32, context=65536, steps=128, top_pages=64, resident_fraction=0.4,
+        hot_rows=2048, selector="uniform",
+    ),
 }
+
+
+def uniform_pages(lengths, page_size, top_pages, layers, generator, device):
+    """Per (layer, request) the tail page plus ``top_pages - 1`` other pages drawn
+    uniformly without replacement: int32 [layers, B, top_pages], ascending.  A
+    request with at most ``top_pages`` pages selects all of them (the first
+    ``count`` entries; the rest are never read)."""
+    B = len(lengths)
+    counts = [ceil(length / page_size) for length in lengths]
+    span = max(max(counts) - 1, top_pages - 1, 1)
+    keys = torch.rand((layers, B, span), generator=generator, device=device)
+    for b, count in enumerate(counts):
+        keys[:, b, max(count - 1, 0):] = -1.0  # the tail page and pages past the history
+    drawn = keys.topk(top_pages - 1, dim=-1).indices.to(torch.int32) if top_pages > 1 else keys[..., :0].int()
+    tails = torch.tensor([count - 1 for count in counts], dtype=torch.int32, device=device)
+    pages = torch.cat((drawn, tails.view(1, B, 1).expand(layers, B, 1)), -1).sort(-1).values
+    for b, count in enumerate(counts):
+        if count <= top_pages:
+            pages[:, b, :count] = torch.arange(count, dtype=torch.int32, device=device)
+    return pages
 
 
 def rotary_at(tensor, positions, theta):
@@ -235,7 +265,12 @@ class SparseKVState:
 class BatchedDecodeEngine:
     """Greedy decode of B requests, layer-major, over a :class:`SparseKVState`."""
 
-    def __init__(self, model: MiniModel, state: SparseKVState, top_pages, *, max_tokens=None, keep_sink=True):
+    def __init__(self, model: MiniModel, state: SparseKVState, top_pages, *, max_tokens=None, keep_sink=True,
+                 selector="quest", seed=0):
+        """``selector``: "quest" (per-head Quest pages over the bounds) or "uniform"
+        (:func:`uniform_pages`, shared by every head, resampled each step)."""
+        if selector not in ("quest", "uniform"):
+            raise ValueError(f"unknown selector {selector!r}")
         cfg = model.config
         if (cfg.num_key_value_heads, cfg.head_dim) != (state.config.kv_heads, state.config.head_dim):
             raise ValueError("model/cache head dimensions differ")
@@ -247,7 +282,10 @@ class BatchedDecodeEngine:
         self.dec = BatchedSparseDecode(
             state.config, cfg.num_attention_heads, top_pages, [max(1, l) for l in state.lengths],
             keep_sink=keep_sink, device=self.device, capacity_lengths=caps,
+            shared_selection=selector == "uniform",
         )
+        self.selector = selector
+        self._sampler = torch.Generator(device=self.device).manual_seed(seed)
         if state.hot_rows < self.dec.capacity:
             # the resolver's precondition (row_index.py:41-42, hybrid.py:34): every
             # selected row must fit the hot region, or misses would share victim slots
@@ -286,6 +324,10 @@ class BatchedDecodeEngine:
         positions = list(st.lengths)
         st.open_tail_pages(positions)
         dec.set_lengths([p + 1 for p in positions])
+        sampled = None
+        if self.selector == "uniform":
+            sampled = uniform_pages([p + 1 for p in positions], st.config.page_size, dec.top, st.layers,
+                                    self._sampler, self.device)
         compute = torch.cuda.current_stream(self.device)
         x = model.model.embed_tokens(tokens)
 
@@ -311,7 +353,10 @@ class BatchedDecodeEngine:
             lo, hi = st.bounds[index]
             marks["append"].append(mark(compute))
             marks["select"] = [marks["append"][1]]
-            dec.select(q, lo, hi)
+            if sampled is None:
+                dec.select(q, lo, hi)
+            else:
+                dec.select_pages(sampled[index])
             marks["select"].append(mark(compute))
             marks["resolve"] = [marks["select"][1]]
             dec.resolve(st.tables[index], row_stats=st.row_stats)

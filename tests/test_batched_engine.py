@@ -85,3 +85,76 @@ def test_batched_engine_rejects_a_hot_region_below_the_union_bound(gpu):
     wl = tiny(hot_rows=128)
     with pytest.raises(ValueError, match="below the union bound"):
         BatchedDecodeEngine(random_model(wl, gpu), build_state(wl, gpu), wl.top_pages)
+
+
+def test_uniform_pages_draws_distinct_pages_with_the_tail():
+    from mini_hisparse_amd.batched_engine import uniform_pages
+
+    gen = torch.Generator().manual_seed(3)
+    lengths = [40 * 16 - 1, 40 * 16 + 1, 5 * 16, 16 * 1000 + 7]
+    pages = uniform_pages(lengths, 16, 6, 4, gen, "cpu")
+    assert pages.shape == (4, 4, 6) and pages.dtype == torch.int32
+    counts = [ceil(length / 16) for length in lengths]
+    seen = set()
+    for layer in range(4):
+        for b, count in enumerate(counts):
+            row = pages[layer, b, : min(6, count)].tolist()
+            if count <= 6:
+                assert row == list(range(count))
+                continue
+            assert row == sorted(set(row)) and row[-1] == count - 1 and 0 <= row[0]
+            seen.update(row[:-1])
+    # the draws cover the history (not a fixed subset): 4 layers x 3 requests x 5 draws
+    assert len(seen) > 30
+    again = uniform_pages(lengths, 16, 6, 4, torch.Generator().manual_seed(3), "cpu")
+    assert torch.equal(pages, again)
+
+
+@pytest.mark.gpu
+def test_batched_engine_uniform_selection_matches_oracle(gpu):
+    """The miss-heavy stress path: pages resampled every step and shared by every head,
+    then union, resolver, gather and attention as for Quest selections."""
+    from mini_hisparse_amd.batched_engine import BatchedDecodeEngine, build_state, random_model
+    from mini_hisparse_amd.selection import union_bound
+
+    wl = tiny(selector="uniform", hot_rows=2 * union_bound(40 * 16 + 23, 16, 6, 1), resident_fraction=0.4)
+    model = random_model(wl, gpu, seed=1)
+    state = build_state(wl, gpu, seed=2)
+    engine = BatchedDecodeEngine(model, state, wl.top_pages, selector="uniform", seed=4)
+    assert engine.dec.capacity == 6 * 16  # one head's selection bounds the union
+    L, B, C, P = wl.layers, wl.batch, state.pages, wl.page_size
+    Hkv, D = wl.kv_heads, wl.head_dim
+    records = []
+    tokens = torch.tensor([1, 2, 3], device=gpu)
+    unions, drawn = 0, set()
+    for step in range(3):
+        records.clear()
+        tokens = engine.step(
+            tokens,
+            lambda l, q, k, v, out: records.append(
+                (l, q.clone(), out.clone(), engine.dec.pages.clone(), engine.dec.union_count.clone())
+            ),
+        )
+        torch.cuda.synchronize()
+        length = state.lengths[0]
+        count = ceil(length / P)
+        for l, q, out, layer_pages, union_count in records:
+            for b in range(B):
+                pages = layer_pages[b].cpu().numpy()
+                assert (pages == pages[0]).all()  # every head reads the same pages
+                row = pages[0].tolist()
+                assert row == sorted(set(row)) and row[-1] == count - 1
+                drawn.update((l, b, p) for p in row[:-1])
+                kv = state.host[l].view(B, C, 2, P, Hkv, D)[b, :count].float()
+                keys = kv[:, 0].reshape(count * P, Hkv, D)[:length]
+                vals = kv[:, 1].reshape(count * P, Hkv, D)[:length]
+                positions = pages_to_positions(pages, length, P)
+                assert int(union_count[b]) == len(positions[0])
+                expected = oracle.selection_oracle(q[b].cpu(), keys, vals, positions)
+                got = out[b].float().cpu().double().numpy()
+                assert np.all(np.abs(got - expected) <= 2e-2 + 1e-2 * np.abs(expected)), np.abs(got - expected).max()
+                unions += int(union_count[b])
+    stats = state.row_stats.tolist()
+    assert sum(stats) == unions
+    assert stats[2] > stats[1]  # resampling every step: misses outnumber hot hits
+    assert len(drawn) >= 8 * L * B  # fresh draws each step (5 per step; about 13 distinct expected)
