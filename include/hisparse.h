@@ -274,6 +274,31 @@ int hs_attend_groups(const void* query, int64_t q_stride_b, int64_t q_stride_h, 
 int hs_probe_row_reads(const void* base, int64_t region_bytes, const int64_t* offsets, int64_t n,
                        int64_t segment_bytes, int64_t plane_bytes, void* sink, hs_stream_t stream);
 
+/*
+ * Dense-layer helpers of the batched decode engine.  They replace the
+ * elementwise PyTorch ops of one decoder layer's decode step (the Qwen2 layer
+ * of MiniModel.decode, model.py:183-226: RMSNorm model.py:53-57 in this build,
+ * rotary, SiLU MLP) for B rows, around projections that stay PyTorch GEMMs.
+ * Rounding follows those ops (each op's result rounded to `dtype`).
+ *
+ * hs_add_rms_norm: per row, when `delta` is non-null x_out = x + delta (x_out
+ *   may alias x); then y = RMSNorm(x_out or x) * weight.  rows <= 65535.
+ * hs_rotary_split: `qkv` rows hold the q|k|v projection output (heads,
+ *   kv_heads, kv_heads head vectors of head_dim); writes rotated q [rows, heads,
+ *   head_dim], rotated k and copied v [rows, kv_heads, head_dim] at the row's
+ *   position positions[row] (device int64) with base `theta`.
+ * hs_silu_mul: out[row, j] = silu(g[row, j]) * u[row, j] where a gate_up row
+ *   holds g (width) then u (width).
+ */
+int hs_add_rms_norm(const void* x, const void* delta, void* x_out, void* y, const void* weight, int64_t rows,
+                    int64_t width, int64_t x_stride, int64_t y_stride, float eps, int32_t dtype,
+                    hs_stream_t stream);
+int hs_rotary_split(const void* qkv, int64_t qkv_stride, void* q, void* k, void* v, const int64_t* positions,
+                    int64_t rows, int64_t heads, int64_t kv_heads, int64_t head_dim, float theta, int32_t dtype,
+                    hs_stream_t stream);
+int hs_silu_mul(const void* gate_up, int64_t gu_stride, void* out, int64_t out_stride, int64_t rows,
+                int64_t width, int32_t dtype, hs_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

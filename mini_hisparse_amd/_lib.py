@@ -7,7 +7,7 @@ no fallback: when the library is missing every kernel call raises.
 from __future__ import annotations
 
 import ctypes
-from ctypes import POINTER, c_char_p, c_int, c_int32, c_int64, c_void_p
+from ctypes import POINTER, c_char_p, c_float, c_int, c_int32, c_int64, c_void_p
 from pathlib import Path
 
 LIBRARY_PATH = Path(__file__).resolve().parent / "libhisparse_hip.so"
@@ -101,6 +101,17 @@ SIGNATURES = {
     "hs_probe_row_reads": (
         c_int, [c_void_p, c_int64, c_void_p, c_int64, c_int64, c_int64, c_void_p, c_void_p],
     ),
+    "hs_add_rms_norm": (
+        c_int,
+        [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int64, c_float,
+         c_int32, c_void_p],
+    ),
+    "hs_rotary_split": (
+        c_int,
+        [c_void_p, c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int64,
+         c_float, c_int32, c_void_p],
+    ),
+    "hs_silu_mul": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_int64, c_int64, c_int32, c_void_p]),
     "hs_attend_groups": (
         c_int,
         [c_void_p, c_int64, c_int64, c_void_p, c_int32, c_int64, c_int64, c_int64, c_int64,

@@ -10,7 +10,7 @@ resident ones, the hot region (blocks, tags, LRU) and the Quest bounds -- as
 stacked device tensors, and runs a decode step layer by layer over all B
 requests:
 
-    dense   RMSNorm, q/k/v projections, rotary embedding          (PyTorch-ROCm)
+    dense   RMSNorm, q|k|v projection, rotary + split              (HIP, one PyTorch GEMM)
     append  hs_append_rows: tail rows, Quest bounds, host mirror   (HIP)
     select  hs_quest_topk + hs_build_union                         (HIP)
             (or pages resampled uniformly per step, shared by all heads,
@@ -18,7 +18,7 @@ requests:
     resolve hs_resolve_rows_batched, row statistics fused          (HIP, compute stream)
     gather  hs_gather_rows_batched, host -> hot rows               (HIP, transfer stream)
     attend  hs_attend_groups                                       (HIP)
-    dense   o_proj, residual, MLP                                  (PyTorch-ROCm)
+    dense   o_proj, residual + RMSNorm, gate|up, SiLU, down        (three PyTorch GEMMs, HIP)
 
 and the next tokens (greedy) stay on the device: a step never reads back to
 the host.  The per-(request, layer) semantics are the reference's: the new
@@ -41,6 +41,7 @@ from torch.nn import functional as F
 
 from . import _lib
 from .batched import BatchedSparseDecode, LayerTablesView
+from .dense import add_rms_norm, rotary_split, silu_mul
 from .config import CacheConfig
 from .model import MiniModel, ModelConfig
 from .row_kernels import MappedHost, pinned_empty
@@ -294,8 +295,31 @@ class BatchedDecodeEngine:
                 f"{cfg.num_attention_heads} heads x {top_pages} pages"
             )
         self.transfer = torch.cuda.Stream(self.device)
+        self._pack_projections()
         self._host_alias = [(ctypes.c_void_p * state.batch)(*([a.data_ptr()] * state.batch)) for a in state.alias]
         self.positions = torch.tensor(state.lengths, dtype=torch.int64, device=self.device)
+
+    @torch.no_grad()
+    def _pack_projections(self):
+        """One weight (and bias) per layer for q|k|v and for gate|up, so each is one GEMM;
+        the model's own parameters become views of the packed tensors (no copy kept)."""
+        self._packed = []
+        for layer in self.model.model.layers:
+            attn, mlp = layer.self_attn, layer.mlp
+            parts = (attn.q_proj, attn.k_proj, attn.v_proj)
+            qkv_w = torch.cat([m.weight for m in parts], 0)
+            qkv_b = torch.cat([m.bias for m in parts], 0)
+            start = 0
+            for m in parts:
+                rows = m.weight.shape[0]
+                m.weight.data = qkv_w[start : start + rows]
+                m.bias.data = qkv_b[start : start + rows]
+                start += rows
+            ffn = mlp.gate_proj.weight.shape[0]
+            gate_up = torch.cat((mlp.gate_proj.weight, mlp.up_proj.weight), 0)
+            mlp.gate_proj.weight.data = gate_up[:ffn]
+            mlp.up_proj.weight.data = gate_up[ffn:]
+            self._packed.append((qkv_w, qkv_b, gate_up))
 
     def _append(self, layer, k, v, positions):
         st, cfg = self.state, self.state.config
@@ -329,7 +353,9 @@ class BatchedDecodeEngine:
             sampled = uniform_pages([p + 1 for p in positions], st.config.page_size, dec.top, st.layers,
                                     self._sampler, self.device)
         compute = torch.cuda.current_stream(self.device)
+        eps = cfg.rms_norm_eps
         x = model.model.embed_tokens(tokens)
+        delta = None  # the previous layer's MLP output, added to x by the next norm
 
         def mark(stream):
             if timer is None:
@@ -340,13 +366,10 @@ class BatchedDecodeEngine:
 
         for index, layer in enumerate(model.model.layers):
             attn = layer.self_attn
+            qkv_w, qkv_b, gate_up_w = self._packed[index]
             marks = {"dense_in": [mark(compute)]}
-            h = layer.input_layernorm(x)
-            q = F.linear(h, attn.q_proj.weight, attn.q_proj.bias).view(B, Hq, D)
-            k = F.linear(h, attn.k_proj.weight, attn.k_proj.bias).view(B, Hkv, D)
-            v = F.linear(h, attn.v_proj.weight, attn.v_proj.bias).view(B, Hkv, D).contiguous()
-            q = rotary_at(q, self.positions, cfg.rope_theta)
-            k = rotary_at(k, self.positions, cfg.rope_theta).contiguous()
+            h = add_rms_norm(x, delta, layer.input_layernorm.weight, eps)
+            q, k, v = rotary_split(F.linear(h, qkv_w, qkv_b), self.positions, Hq, Hkv, D, cfg.rope_theta)
             marks["dense_in"].append(mark(compute))
             marks["append"] = [mark(compute)]
             self._append(index, k, v, positions)
@@ -376,12 +399,13 @@ class BatchedDecodeEngine:
             if observer is not None:
                 observer(index, q, k, v, out)
             marks["dense_out"] = [marks["attend"][1]]
-            x = x + F.linear(out.reshape(B, Hq * D), attn.o_proj.weight)
-            x = x + layer.mlp(layer.post_attention_layernorm(x))
+            h = add_rms_norm(x, F.linear(out.reshape(B, Hq * D), attn.o_proj.weight),
+                             layer.post_attention_layernorm.weight, eps)
+            delta = F.linear(silu_mul(F.linear(h, gate_up_w)), layer.mlp.down_proj.weight)
             marks["dense_out"].append(mark(compute))
             if timer is not None:
                 timer.append((index, marks, dec.entry_counts.sum(), dec.row_counts[:, 2].sum()))
-        logits = model.lm_head(model.model.norm(x)).float()
+        logits = model.lm_head(add_rms_norm(x, delta, model.model.norm.weight, eps))
         st.lengths = [p + 1 for p in positions]
         self.positions += 1
         return logits.argmax(-1)

@@ -1,0 +1,81 @@
+"""Fused elementwise stages of a decoder layer's decode step (HIP kernels).
+
+Wrappers of ``hs_add_rms_norm``, ``hs_rotary_split`` and ``hs_silu_mul``: the
+RMSNorm (with the residual add before it), the rotary embedding of q and k
+(with the split of a packed q|k|v projection) and the SiLU gate of the MLP
+(over a packed gate|up projection) of the Qwen2 layer that ``MiniModel``
+implements (model.py:53-57 RMSNorm, the rotary and MLP of this package's
+``model.py``; the reference's model.py:183-226).  One launch each for B rows.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+
+
+def _stream(tensor):
+    return _lib.stream_handle(tensor.device)
+
+
+def add_rms_norm(x, delta, weight, eps, out=None):
+    """RMSNorm of ``x`` [rows, width] (of ``x + delta`` when ``delta`` is given, and then
+    ``x`` is updated in place to the sum).  Returns the normalised rows."""
+    if x.dim() != 2 or x.stride(1) != 1:
+        raise ValueError("x must be [rows, width] with unit inner stride")
+    if delta is not None and (delta.shape != x.shape or delta.stride() != x.stride() or delta.dtype != x.dtype):
+        raise ValueError("delta must match x in shape, strides and dtype")
+    if weight.shape != (x.shape[1],) or weight.dtype != x.dtype:
+        raise ValueError("weight must be [width] in the dtype of x")
+    y = torch.empty_like(x) if out is None else out
+    _lib.check(
+        _lib.load().hs_add_rms_norm(
+            x.data_ptr(), _lib.ptr(delta), x.data_ptr() if delta is not None else None, y.data_ptr(),
+            weight.data_ptr(), x.shape[0], x.shape[1], x.stride(0), y.stride(0), float(eps),
+            _lib.dtype_code(x.dtype), _stream(x),
+        ),
+        "hs_add_rms_norm",
+    )
+    return y
+
+
+def rotary_split(qkv, positions, heads, kv_heads, head_dim, theta, out=None):
+    """Split a packed projection ``qkv`` [rows, (heads + 2 kv_heads) head_dim] into q
+    [rows, heads, head_dim], k and v [rows, kv_heads, head_dim], with q and k rotated
+    at ``positions`` [rows] (int64, device)."""
+    rows = qkv.shape[0]
+    if qkv.dim() != 2 or qkv.stride(1) != 1 or qkv.shape[1] != (heads + 2 * kv_heads) * head_dim:
+        raise ValueError("qkv must be [rows, (heads + 2 kv_heads) head_dim] with unit inner stride")
+    if positions.dtype != torch.int64 or positions.shape != (rows,) or positions.device != qkv.device:
+        raise ValueError("positions must be int64 [rows] on the device of qkv")
+    if out is None:
+        q = torch.empty((rows, heads, head_dim), dtype=qkv.dtype, device=qkv.device)
+        k = torch.empty((rows, kv_heads, head_dim), dtype=qkv.dtype, device=qkv.device)
+        v = torch.empty_like(k)
+    else:
+        q, k, v = out
+    _lib.check(
+        _lib.load().hs_rotary_split(
+            qkv.data_ptr(), qkv.stride(0), q.data_ptr(), k.data_ptr(), v.data_ptr(), positions.data_ptr(), rows,
+            heads, kv_heads, head_dim, float(theta), _lib.dtype_code(qkv.dtype), _stream(qkv),
+        ),
+        "hs_rotary_split",
+    )
+    return q, k, v
+
+
+def silu_mul(gate_up, out=None):
+    """silu(gate) * up of a packed ``gate_up`` [rows, 2 width] -> [rows, width]."""
+    if gate_up.dim() != 2 or gate_up.stride(1) != 1 or gate_up.shape[1] % 2:
+        raise ValueError("gate_up must be [rows, 2 width] with unit inner stride")
+    rows, width = gate_up.shape[0], gate_up.shape[1] // 2
+    y = torch.empty((rows, width), dtype=gate_up.dtype, device=gate_up.device) if out is None else out
+    _lib.check(
+        _lib.load().hs_silu_mul(
+            gate_up.data_ptr(), gate_up.stride(0), y.data_ptr(), y.stride(0), rows, width,
+            _lib.dtype_code(gate_up.dtype), _stream(gate_up),
+        ),
+        "hs_silu_mul",
+    )
+    return y

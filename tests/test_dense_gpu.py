@@ -1,0 +1,85 @@
+"""Fused dense-layer kernels of the batched engine against the PyTorch ops they replace
+(the model's RMSNorm, the engine's PyTorch rotary, F.silu) and fp32 references."""
+
+import pytest
+import torch
+from torch.nn import functional as F
+
+from mini_hisparse_amd.batched_engine import rotary_at
+from mini_hisparse_amd.dense import add_rms_norm, rotary_split, silu_mul
+from mini_hisparse_amd.model import RMSNorm
+
+BF16_ULP = 2.0**-7  # relative spacing of bfloat16 values in [1, 2)
+
+
+def test_wrappers_check_shapes_without_a_gpu():
+    x = torch.zeros(4, 8, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="weight"):
+        add_rms_norm(x, None, torch.ones(7, dtype=torch.bfloat16), 1e-6)
+    with pytest.raises(ValueError, match="delta"):
+        add_rms_norm(x, torch.zeros(4, 7, dtype=torch.bfloat16), torch.ones(8, dtype=torch.bfloat16), 1e-6)
+    with pytest.raises(ValueError, match="qkv"):
+        rotary_split(torch.zeros(2, 10, dtype=torch.bfloat16), torch.zeros(2, dtype=torch.int64), 1, 1, 4, 1e4)
+    with pytest.raises(ValueError, match="gate_up"):
+        silu_mul(torch.zeros(2, 5, dtype=torch.bfloat16))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("rows,width", [(1, 896), (8, 3584), (3, 5120), (5, 100)])
+def test_add_rms_norm_matches_the_model_norm(gpu, dtype, rows, width):
+    gen = torch.Generator(device=gpu).manual_seed(rows * 7 + width)
+    x = (torch.randn(rows, width, generator=gen, device=gpu) * 3).to(dtype)
+    delta = torch.randn(rows, width, generator=gen, device=gpu).to(dtype)
+    norm = RMSNorm(width, 1e-6).to(device=gpu, dtype=dtype)
+    with torch.no_grad():
+        norm.weight.copy_((torch.rand(width, generator=gen, device=gpu) + 0.5).to(dtype))
+        summed = x + delta  # PyTorch's residual add in the model dtype
+        expected = norm(summed)
+        exact = (summed.double() * torch.rsqrt(summed.double().square().mean(-1, keepdim=True) + 1e-6)) * norm.weight.double()
+    got_plain = add_rms_norm(summed.clone(), None, norm.weight, 1e-6)
+    inplace = x.clone()
+    got = add_rms_norm(inplace, delta, norm.weight, 1e-6)
+    torch.testing.assert_close(inplace, summed, rtol=0, atol=0)  # the residual add is exact
+    tol = dict(rtol=2 * BF16_ULP if dtype != torch.float32 else 1e-5, atol=1e-5)
+    torch.testing.assert_close(got, expected, **tol)
+    torch.testing.assert_close(got_plain, got, rtol=0, atol=0)
+    torch.testing.assert_close(got.double(), exact, rtol=2 * BF16_ULP if dtype != torch.float32 else 1e-5, atol=1e-5)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("heads,kv_heads,head_dim", [(28, 4, 128), (14, 2, 64), (40, 8, 128), (4, 2, 32)])
+def test_rotary_split_matches_the_pytorch_rotary(gpu, heads, kv_heads, head_dim):
+    rows = 5
+    gen = torch.Generator(device=gpu).manual_seed(heads)
+    qkv = torch.randn(rows, (heads + 2 * kv_heads) * head_dim, generator=gen, device=gpu).to(torch.bfloat16)
+    positions = torch.tensor([0, 1, 639, 65536, 131071], dtype=torch.int64, device=gpu)
+    q, k, v = rotary_split(qkv, positions, heads, kv_heads, head_dim, 1e6)
+    parts = qkv.view(rows, heads + 2 * kv_heads, head_dim)
+    ref_q = rotary_at(parts[:, :heads], positions, 1e6)
+    ref_k = rotary_at(parts[:, heads : heads + kv_heads], positions, 1e6)
+    torch.testing.assert_close(v, parts[:, heads + kv_heads :], rtol=0, atol=0)
+    # same rounding sequence; cos/sin/pow of the device may differ from PyTorch's by an ulp
+    torch.testing.assert_close(q, ref_q, rtol=2 * BF16_ULP, atol=2 * BF16_ULP)
+    torch.testing.assert_close(k, ref_k, rtol=2 * BF16_ULP, atol=2 * BF16_ULP)
+    # fp32 rotation: the bf16 result is within a few roundings of it
+    half = head_dim // 2
+    inv = 1e6 ** (-torch.arange(0, head_dim, 2, device=gpu, dtype=torch.float64) / head_dim)
+    ang = positions.double()[:, None] * inv[None, :]
+    t = parts[:, :heads].double()
+    a, b = t[..., :half], t[..., half:]
+    c, s = ang.cos()[:, None, :], ang.sin()[:, None, :]
+    exact = torch.cat((a * c - b * s, b * c + a * s), -1)
+    assert (q.double() - exact).abs().max().item() < 0.05
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("rows,width", [(1, 4864), (8, 18944), (3, 27648), (2, 33)])
+def test_silu_mul_matches_pytorch(gpu, rows, width):
+    gen = torch.Generator(device=gpu).manual_seed(width)
+    gate_up = (torch.randn(rows, 2 * width, generator=gen, device=gpu) * 4).to(torch.bfloat16)
+    got = silu_mul(gate_up)
+    gate, up = gate_up[:, :width], gate_up[:, width:]
+    torch.testing.assert_close(got, F.silu(gate) * up, rtol=2 * BF16_ULP, atol=1e-6)
+    exact = gate.double() * torch.sigmoid(gate.double()) * up.double()
+    torch.testing.assert_close(got.double(), exact, rtol=2 * BF16_ULP, atol=1e-6)
