@@ -598,6 +598,7 @@ def run_model_workload(args, torch, device):
             "kernel": "attend_mfma_kernel + attend_merge_kernel, summed over the layers of one profiled step",
         },
         "stages_ms_per_step": stage_ms,
+        "projections_on_hs_skinny_gemm": engine.projection_kernel,
         "rows_per_step": {"resident_hits": rows[0], "hot_hits": rows[1], "misses": rows[2]},
         "gather": {"bytes_per_step": gather_bytes, "GBps": gather_bytes / (stage_ms["gather"] * 1e-3) / 1e9,
                    "host_link_memcpy_GBps": link},

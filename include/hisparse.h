@@ -299,6 +299,20 @@ int hs_rotary_split(const void* qkv, int64_t qkv_stride, void* q, void* k, void*
 int hs_silu_mul(const void* gate_up, int64_t gu_stride, void* out, int64_t out_stride, int64_t rows,
                 int64_t width, int32_t dtype, hs_stream_t stream);
 
+/*
+ * Decode projection of the batched engine: out[rows, n] = x[rows, k] . W[n, k]^T
+ * (+ bias[n]) for 1 <= rows <= 16, bf16 or f16, fp32 accumulation; replaces
+ * the PyTorch GEMMs of the decode step's projections (model.py:183-226) for
+ * these skinny shapes.  k % 32 == 0, x rows 16-byte aligned (x_stride % 8 == 0),
+ * W contiguous [n, k].  Tall-k shapes are split over k: the workspace
+ * (hs_skinny_gemm_workspace_bytes) then holds fp32 partials that a second
+ * launch sums in a fixed order, so results are deterministic.
+ */
+int64_t hs_skinny_gemm_workspace_bytes(int64_t rows, int64_t n, int64_t k);
+int hs_skinny_gemm(const void* x, int64_t x_stride, const void* weight, int64_t n, int64_t k, const void* bias,
+                   void* out, int64_t out_stride, int64_t rows, int32_t dtype, void* workspace,
+                   int64_t workspace_bytes, hs_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

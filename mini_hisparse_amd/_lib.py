@@ -112,6 +112,12 @@ SIGNATURES = {
          c_float, c_int32, c_void_p],
     ),
     "hs_silu_mul": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_int64, c_int64, c_int32, c_void_p]),
+    "hs_skinny_gemm_workspace_bytes": (c_int64, [c_int64, c_int64, c_int64]),
+    "hs_skinny_gemm": (
+        c_int,
+        [c_void_p, c_int64, c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_int64, c_int64, c_int32, c_void_p,
+         c_int64, c_void_p],
+    ),
     "hs_attend_groups": (
         c_int,
         [c_void_p, c_int64, c_int64, c_void_p, c_int32, c_int64, c_int64, c_int64, c_int64,

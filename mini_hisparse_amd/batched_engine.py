@@ -10,7 +10,7 @@ resident ones, the hot region (blocks, tags, LRU) and the Quest bounds -- as
 stacked device tensors, and runs a decode step layer by layer over all B
 requests:
 
-    dense   RMSNorm, q|k|v projection, rotary + split              (HIP, one PyTorch GEMM)
+    dense   RMSNorm, q|k|v projection, rotary + split              (HIP)
     append  hs_append_rows: tail rows, Quest bounds, host mirror   (HIP)
     select  hs_quest_topk + hs_build_union                         (HIP)
             (or pages resampled uniformly per step, shared by all heads,
@@ -18,7 +18,7 @@ requests:
     resolve hs_resolve_rows_batched, row statistics fused          (HIP, compute stream)
     gather  hs_gather_rows_batched, host -> hot rows               (HIP, transfer stream)
     attend  hs_attend_groups                                       (HIP)
-    dense   o_proj, residual + RMSNorm, gate|up, SiLU, down        (three PyTorch GEMMs, HIP)
+    dense   o_proj, residual + RMSNorm, gate|up, SiLU, down        (HIP)
 
 and the next tokens (greedy) stay on the device: a step never reads back to
 the host.  The per-(request, layer) semantics are the reference's: the new
@@ -41,7 +41,7 @@ from torch.nn import functional as F
 
 from . import _lib
 from .batched import BatchedSparseDecode, LayerTablesView
-from .dense import add_rms_norm, rotary_split, silu_mul
+from .dense import add_rms_norm, linear, linear_supported, rotary_split, silu_mul
 from .config import CacheConfig
 from .model import MiniModel, ModelConfig
 from .row_kernels import MappedHost, pinned_empty
@@ -296,6 +296,7 @@ class BatchedDecodeEngine:
             )
         self.transfer = torch.cuda.Stream(self.device)
         self._pack_projections()
+        self._choose_projections()
         self._host_alias = [(ctypes.c_void_p * state.batch)(*([a.data_ptr()] * state.batch)) for a in state.alias]
         self.positions = torch.tensor(state.lengths, dtype=torch.int64, device=self.device)
 
@@ -320,6 +321,44 @@ class BatchedDecodeEngine:
             mlp.gate_proj.weight.data = gate_up[:ffn]
             mlp.up_proj.weight.data = gate_up[ffn:]
             self._packed.append((qkv_w, qkv_b, gate_up))
+
+    @torch.no_grad()
+    def _choose_projections(self):
+        """Per projection, the faster of the skinny-GEMM kernel (hs_skinny_gemm) and
+        PyTorch's GEMM at this batch, timed over the layers' own weights (each call
+        reads another layer's weight from HBM, as in a step).  The kernel wins the
+        small and tall-K shapes; PyTorch's GEMM can win the widest ones."""
+        B, dev, dt = self.state.batch, self.device, self.model.dtype
+        layers = self.model.model.layers
+        groups = {
+            "qkv": [(w, b) for w, b, _ in self._packed],
+            "o_proj": [(layer.self_attn.o_proj.weight, None) for layer in layers],
+            "gate_up": [(gate_up, None) for _, _, gate_up in self._packed],
+            "down": [(layer.mlp.down_proj.weight, None) for layer in layers],
+            "lm_head": [(self.model.lm_head.weight, None)] * 4,
+        }
+        self.projection_kernel = {}
+        for name, weights in groups.items():
+            x = torch.full((B, weights[0][0].shape[1]), 0.01, dtype=dt, device=dev)
+            if not linear_supported(x, weights[0][0]):
+                self.projection_kernel[name] = False
+                continue
+            elapsed = {}
+            for label, fn in (("kernel", linear), ("torch", F.linear)):
+                fn(x, *weights[0])
+                start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                start.record()
+                for w, b in weights:
+                    fn(x, w, b)
+                end.record()
+                end.synchronize()
+                elapsed[label] = start.elapsed_time(end)
+            self.projection_kernel[name] = elapsed["kernel"] <= elapsed["torch"]
+
+    def _project(self, name, x, weight, bias=None):
+        if self.projection_kernel[name]:
+            return linear(x, weight, bias)
+        return F.linear(x, weight, bias)
 
     def _append(self, layer, k, v, positions):
         st, cfg = self.state, self.state.config
@@ -369,7 +408,8 @@ class BatchedDecodeEngine:
             qkv_w, qkv_b, gate_up_w = self._packed[index]
             marks = {"dense_in": [mark(compute)]}
             h = add_rms_norm(x, delta, layer.input_layernorm.weight, eps)
-            q, k, v = rotary_split(F.linear(h, qkv_w, qkv_b), self.positions, Hq, Hkv, D, cfg.rope_theta)
+            q, k, v = rotary_split(self._project("qkv", h, qkv_w, qkv_b), self.positions, Hq, Hkv, D,
+                                   cfg.rope_theta)
             marks["dense_in"].append(mark(compute))
             marks["append"] = [mark(compute)]
             self._append(index, k, v, positions)
@@ -399,13 +439,13 @@ class BatchedDecodeEngine:
             if observer is not None:
                 observer(index, q, k, v, out)
             marks["dense_out"] = [marks["attend"][1]]
-            h = add_rms_norm(x, F.linear(out.reshape(B, Hq * D), attn.o_proj.weight),
+            h = add_rms_norm(x, self._project("o_proj", out.reshape(B, Hq * D), attn.o_proj.weight),
                              layer.post_attention_layernorm.weight, eps)
-            delta = F.linear(silu_mul(F.linear(h, gate_up_w)), layer.mlp.down_proj.weight)
+            delta = self._project("down", silu_mul(self._project("gate_up", h, gate_up_w)), layer.mlp.down_proj.weight)
             marks["dense_out"].append(mark(compute))
             if timer is not None:
                 timer.append((index, marks, dec.entry_counts.sum(), dec.row_counts[:, 2].sum()))
-        logits = model.lm_head(add_rms_norm(x, delta, model.model.norm.weight, eps))
+        logits = self._project("lm_head", add_rms_norm(x, delta, model.model.norm.weight, eps), model.lm_head.weight)
         st.lengths = [p + 1 for p in positions]
         self.positions += 1
         return logits.argmax(-1)

@@ -1,0 +1,236 @@
+// Decode projections for gfx950: y[M, N] = x[M, K] . W[N, K]^T (+ bias) with M <= 16.
+//
+// In a decode step every projection of the batched engine multiplies a few
+// token rows by a large weight, so the weight read is the whole cost: the
+// kernel is an HBM stream of W.  Tiles are v_mfma_f32_16x16x32_{bf16,f16} with
+// 16 weight rows as the MFMA's M dimension and the (padded) token rows as its
+// N dimension, so the MFMA's output tile is 16 weight rows x 16 tokens.
+//
+// A workgroup (4 waves) owns 16 or 32 weight rows and one K slice; wave w
+// takes k-steps (of 32) in groups of GU consecutive steps, round-robin over
+// the waves, so within a round the four waves read GU * 4 * 64 contiguous
+// bytes of every row.  Per round a lane issues all of its loads (4 * GU
+// weight fragments, GU token fragments) before the first MFMA.  The waves'
+// partial tiles are summed in LDS.  With one K slice the workgroup adds the
+// bias and writes y; with several (split-K, for tall-K shapes that would
+// otherwise give too few workgroups) it writes fp32 partials and
+// gemm_finalize_kernel sums them in slice order (deterministic), adds the
+// bias and rounds.
+#include <math.h>
+#include <stdlib.h>
+
+#include "hs_common.h"
+
+namespace hs {
+
+constexpr int GM_T = 256;  // threads per workgroup
+
+template <int DT>
+__device__ __forceinline__ f32x4 gemm_mfma(u32x4 a, u32x4 b, f32x4 c) {
+  if constexpr (DT == HS_DTYPE_BF16) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
+                                                   0, 0, 0);
+  } else {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0,
+                                                  0, 0);
+  }
+}
+
+struct GemmArgs {
+  const unsigned short* x;
+  int64_t x_stride;
+  const unsigned short* w;
+  int64_t K, N, M;
+  const unsigned short* bias;  // nullable
+  void* out;
+  int64_t out_stride;
+  float* part;  // [splits, M, N] when splits > 1
+  int64_t splits, slice_steps;
+};
+
+// GM_TILES row tiles of 16 per workgroup, shared by the 4 waves, which split
+// the slice's k-steps in rounds of GU.  (Measured on MI355X: splitting rows
+// over the waves instead, or double-buffering the rounds in registers, is
+// slower at every decode shape of the Qwen2.5 0.5B/7B/32B projections.)
+template <int DT, int GM_TILES, int GU>
+__global__ __launch_bounds__(GM_T) void skinny_gemm_kernel(GemmArgs a) {
+  constexpr int GM_ROWS = 16 * GM_TILES;  // weight rows per workgroup
+  __shared__ float red[4][GM_ROWS][17];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int c = lane & 15, j = lane >> 4;
+  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * GM_ROWS;
+  const int64_t split = blockIdx.y;
+  const int64_t steps = a.K / 32;
+  const int64_t s0 = split * a.slice_steps;
+  int64_t s1 = s0 + a.slice_steps;
+  if (s1 > steps) s1 = steps;
+  // lane (c, j): weight rows n0 + 16t + c, token row c, k offset 8j within a step
+  const unsigned short* wrow[GM_TILES];
+#pragma unroll
+  for (int t = 0; t < GM_TILES; ++t) {
+    int64_t n = n0 + 16 * t + c;
+    if (n >= a.N) n = a.N - 1;  // rows past N read the last row; their outputs are dropped
+    wrow[t] = a.w + n * a.K + 8 * j;
+  }
+  const unsigned short* xrow = a.x + (c < a.M ? c : a.M - 1) * a.x_stride + 8 * j;
+  f32x4 acc[GM_TILES];
+#pragma unroll
+  for (int t = 0; t < GM_TILES; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int64_t base = s0 + static_cast<int64_t>(wave) * GU; base < s1; base += 4 * GU) {
+    // every load of the round before the first MFMA; steps past the slice
+    // reload its last step (in bounds) and are skipped
+    u32x4 wf[GU][GM_TILES], xf[GU];
+#pragma unroll
+    for (int u = 0; u < GU; ++u) {
+      int64_t s = base + u;
+      if (s >= s1) s = s1 - 1;
+      const int64_t k = 32 * s;
+#pragma unroll
+      for (int t = 0; t < GM_TILES; ++t) wf[u][t] = *reinterpret_cast<const u32x4*>(wrow[t] + k);
+      xf[u] = *reinterpret_cast<const u32x4*>(xrow + k);
+    }
+#pragma unroll
+    for (int u = 0; u < GU; ++u) {
+      if (base + u < s1) {  // uniform per wave
+#pragma unroll
+        for (int t = 0; t < GM_TILES; ++t) acc[t] = gemm_mfma<DT>(wf[u][t], xf[u], acc[t]);
+      }
+    }
+  }
+  // lane holds C[row 16t + 4j + i][token c]; the waves' partials summed in wave order
+#pragma unroll
+  for (int t = 0; t < GM_TILES; ++t)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) red[wave][16 * t + 4 * j + i][c] = acc[t][i];
+  __syncthreads();
+  for (int idx = threadIdx.x; idx < GM_ROWS * 16; idx += GM_T) {
+    const int r = idx >> 4, m = idx & 15;
+    const int64_t n = n0 + r;
+    if (m >= a.M || n >= a.N) continue;
+    const float v = red[0][r][m] + red[1][r][m] + red[2][r][m] + red[3][r][m];
+    if (a.splits > 1) {
+      a.part[(split * a.M + m) * a.N + n] = v;
+    } else {
+      const float b = a.bias != nullptr ? load_elem<DT>(a.bias, n) : 0.f;
+      store_elem<DT>(a.out, m * a.out_stride + n, v + b);
+    }
+  }
+}
+
+template <int DT>
+__global__ __launch_bounds__(GM_T) void gemm_finalize_kernel(const float* part, int64_t splits, int64_t M, int64_t N,
+                                                             const unsigned short* bias, void* out,
+                                                             int64_t out_stride) {
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * GM_T + threadIdx.x;
+  if (idx >= M * N) return;
+  const int64_t m = idx / N, n = idx - m * N;
+  float v = 0.f;
+  for (int64_t s = 0; s < splits; ++s) v += part[(s * M + m) * N + n];
+  if (bias != nullptr) v += load_elem<DT>(bias, n);
+  store_elem<DT>(out, m * out_stride + n, v);
+}
+
+struct GemmPlan {
+  int tiles, gu;
+  int64_t blocks, splits, slice_steps;
+};
+
+static int64_t gemm_ceil(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+static int64_t env_or(const char* name, int64_t fallback) {
+  const char* env = getenv(name);
+  return env ? atoll(env) : fallback;
+}
+
+// 16-row workgroups up to 1024 of them, else 32-row; rounds of 8 k-steps
+// (the best of 1/2/4 tiles x 2/4/8 steps measured over the Qwen2.5 decode
+// shapes).  Enough K slices for about two workgroups per CU, each slice
+// keeping at least two rounds per wave.  HS_GEMM_TILES / HS_GEMM_GU /
+// HS_GEMM_SPLITS override the choice (read once).
+static GemmPlan plan_gemm(int64_t N, int64_t K) {
+  static const int64_t f_tiles = env_or("HS_GEMM_TILES", 0), f_gu = env_or("HS_GEMM_GU", 0),
+                       f_splits = env_or("HS_GEMM_SPLITS", 0);
+  GemmPlan p{};
+  p.tiles = gemm_ceil(N, 16) <= 1024 ? 1 : 2;
+  if (f_tiles == 1 || f_tiles == 2 || f_tiles == 4) p.tiles = static_cast<int>(f_tiles);
+  p.gu = f_gu == 4 ? 4 : 8;
+  p.blocks = gemm_ceil(N, 16 * p.tiles);
+  const int64_t steps = K / 32;
+  int64_t splits = f_splits > 0 ? f_splits : gemm_ceil(512, p.blocks);
+  const int64_t most = steps / (2 * 4 * p.gu);
+  if (splits > most) splits = most;
+  if (splits < 1) splits = 1;
+  p.slice_steps = gemm_ceil(steps, splits);
+  p.splits = gemm_ceil(steps, p.slice_steps);
+  return p;
+}
+
+template <int DT, int TILES>
+static void launch_gemm_tiles(const GemmPlan& p, dim3 grid, const GemmArgs& a, hipStream_t s) {
+  if (p.gu == 4) hipLaunchKernelGGL((skinny_gemm_kernel<DT, TILES, 4>), grid, dim3(GM_T), 0, s, a);
+  else hipLaunchKernelGGL((skinny_gemm_kernel<DT, TILES, 8>), grid, dim3(GM_T), 0, s, a);
+}
+
+template <int DT>
+static void launch_gemm(const GemmPlan& p, dim3 grid, const GemmArgs& a, hipStream_t s) {
+  if (p.tiles == 1) launch_gemm_tiles<DT, 1>(p, grid, a, s);
+  else if (p.tiles == 2) launch_gemm_tiles<DT, 2>(p, grid, a, s);
+  else launch_gemm_tiles<DT, 4>(p, grid, a, s);
+}
+
+}  // namespace hs
+
+using namespace hs;
+
+extern "C" int64_t hs_skinny_gemm_workspace_bytes(int64_t rows, int64_t n, int64_t k) {
+  if (rows < 1 || n < 1 || k < 32) return 256;
+  const GemmPlan p = plan_gemm(n, k);
+  return p.splits > 1 ? p.splits * rows * n * 4 + 256 : 256;
+}
+
+extern "C" int hs_skinny_gemm(const void* x, int64_t x_stride, const void* weight, int64_t n, int64_t k,
+                              const void* bias, void* out, int64_t out_stride, int64_t rows, int32_t dtype,
+                              void* workspace, int64_t workspace_bytes, hipStream_t stream) {
+  HS_CHECK_ARG(dtype == HS_DTYPE_BF16 || dtype == HS_DTYPE_F16, "the decode GEMM takes bf16 or f16");
+  HS_CHECK_ARG(rows >= 1 && rows <= 16, "the decode GEMM takes 1 to 16 rows");
+  HS_CHECK_ARG(n >= 1 && k >= 32 && k % 32 == 0, "K must be a positive multiple of 32");
+  HS_CHECK_ARG(x_stride >= k && x_stride % 8 == 0 && out_stride >= n, "invalid row strides");
+  HS_CHECK_ARG(x && weight && out, "null GEMM pointer");
+  HS_CHECK_ARG((reinterpret_cast<uintptr_t>(x) & 15) == 0 && (reinterpret_cast<uintptr_t>(weight) & 15) == 0,
+               "x and weight must be 16-byte aligned");
+  const GemmPlan p = plan_gemm(n, k);
+  HS_CHECK_ARG(p.blocks <= 0x7fffffff && p.splits <= 65535, "GEMM too large");
+  GemmArgs a{};
+  a.x = static_cast<const unsigned short*>(x);
+  a.x_stride = x_stride;
+  a.w = static_cast<const unsigned short*>(weight);
+  a.K = k;
+  a.N = n;
+  a.M = rows;
+  a.bias = static_cast<const unsigned short*>(bias);
+  a.out = out;
+  a.out_stride = out_stride;
+  a.splits = p.splits;
+  a.slice_steps = p.slice_steps;
+  if (p.splits > 1) {
+    const int64_t need = p.splits * rows * n * 4;
+    HS_CHECK_ARG(workspace != nullptr && workspace_bytes >= need, "GEMM workspace too small: need %lld bytes",
+                 static_cast<long long>(need));
+    a.part = static_cast<float*>(workspace);
+  }
+  const dim3 grid(static_cast<unsigned>(p.blocks), static_cast<unsigned>(p.splits));
+  if (dtype == HS_DTYPE_BF16) launch_gemm<HS_DTYPE_BF16>(p, grid, a, stream);
+  else launch_gemm<HS_DTYPE_F16>(p, grid, a, stream);
+  HS_CHECK_LAUNCH("skinny GEMM");
+  if (p.splits > 1) {
+    const unsigned blocks = static_cast<unsigned>(gemm_ceil(rows * n, GM_T));
+    if (dtype == HS_DTYPE_BF16)
+      hipLaunchKernelGGL((gemm_finalize_kernel<HS_DTYPE_BF16>), dim3(blocks), dim3(GM_T), 0, stream, a.part, p.splits,
+                         rows, n, a.bias, out, out_stride);
+    else
+      hipLaunchKernelGGL((gemm_finalize_kernel<HS_DTYPE_F16>), dim3(blocks), dim3(GM_T), 0, stream, a.part, p.splits,
+                         rows, n, a.bias, out, out_stride);
+    HS_CHECK_LAUNCH("skinny GEMM finalize");
+  }
+  return HS_OK;
+}

@@ -1,6 +1,9 @@
-"""Fused elementwise stages of a decoder layer's decode step (HIP kernels).
+"""Dense stages of a decoder layer's decode step (HIP kernels).
 
-Wrappers of ``hs_add_rms_norm``, ``hs_rotary_split`` and ``hs_silu_mul``: the
+``linear`` wraps ``hs_skinny_gemm``, the projection of up to 16 token rows
+(an HBM stream of the weight on MFMA tiles).  ``add_rms_norm``,
+``rotary_split`` and ``silu_mul`` wrap ``hs_add_rms_norm``,
+``hs_rotary_split`` and ``hs_silu_mul``: the
 RMSNorm (with the residual add before it), the rotary embedding of q and k
 (with the split of a packed q|k|v projection) and the SiLU gate of the MLP
 (over a packed gate|up projection) of the Qwen2 layer that ``MiniModel``
@@ -17,6 +20,51 @@ from . import _lib
 
 def _stream(tensor):
     return _lib.stream_handle(tensor.device)
+
+
+_WORKSPACE = {}
+
+
+def _workspace(device, stream, nbytes):
+    key = (device, stream)
+    ws = _WORKSPACE.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=device)
+        _WORKSPACE[key] = ws
+    return ws
+
+
+def linear_supported(x, weight):
+    """Shapes ``linear`` takes: 1-16 rows, K a multiple of 32, bf16/f16, 16-byte aligned rows."""
+    return (
+        x.dim() == 2 and weight.dim() == 2 and 1 <= x.shape[0] <= 16 and x.shape[1] == weight.shape[1]
+        and x.shape[1] % 32 == 0 and x.dtype == weight.dtype and x.dtype in (torch.bfloat16, torch.float16)
+        and x.stride(1) == 1 and x.stride(0) % 8 == 0 and weight.is_contiguous()
+        and x.data_ptr() % 16 == 0 and weight.data_ptr() % 16 == 0
+    )
+
+
+def linear(x, weight, bias=None, out=None):
+    """``x @ weight.T + bias`` for ``x`` [rows <= 16, K] (F.linear's arguments)."""
+    if not linear_supported(x, weight):
+        raise ValueError("linear takes 1-16 rows of a bf16/f16 x with K a multiple of 32 and a contiguous weight")
+    if bias is not None and (bias.shape != (weight.shape[0],) or bias.dtype != x.dtype or not bias.is_contiguous()):
+        raise ValueError("bias must be [N] contiguous in the dtype of x")
+    rows, k = x.shape
+    n = weight.shape[0]
+    y = torch.empty((rows, n), dtype=x.dtype, device=x.device) if out is None else out
+    lib = _lib.load()
+    stream = _stream(x)
+    nbytes = lib.hs_skinny_gemm_workspace_bytes(rows, n, k)
+    ws = _workspace(x.device, stream, nbytes)
+    _lib.check(
+        lib.hs_skinny_gemm(
+            x.data_ptr(), x.stride(0), weight.data_ptr(), n, k, _lib.ptr(bias), y.data_ptr(), y.stride(0), rows,
+            _lib.dtype_code(x.dtype), ws.data_ptr(), ws.numel(), stream,
+        ),
+        "hs_skinny_gemm",
+    )
+    return y
 
 
 def add_rms_norm(x, delta, weight, eps, out=None):

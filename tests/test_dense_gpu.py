@@ -83,3 +83,38 @@ def test_silu_mul_matches_pytorch(gpu, rows, width):
     torch.testing.assert_close(got, F.silu(gate) * up, rtol=2 * BF16_ULP, atol=1e-6)
     exact = gate.double() * torch.sigmoid(gate.double()) * up.double()
     torch.testing.assert_close(got.double(), exact, rtol=2 * BF16_ULP, atol=1e-6)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("rows", [1, 3, 8, 16])
+@pytest.mark.parametrize("n,k,bias", [(4608, 3584, True), (3584, 18944, False), (300, 256, True), (64, 32, False),
+                                      (1000, 27648, False)])
+def test_linear_matches_an_fp32_reference(gpu, dtype, rows, n, k, bias):
+    from mini_hisparse_amd.dense import linear
+
+    gen = torch.Generator(device=gpu).manual_seed(rows + n + k)
+    x = torch.randn(rows, k, generator=gen, device=gpu).to(dtype)
+    w = (torch.randn(n, k, generator=gen, device=gpu) / k**0.5).to(dtype)
+    b = torch.randn(n, generator=gen, device=gpu).to(dtype) if bias else None
+    got = linear(x, w, b)
+    ref = x.float() @ w.float().T + (b.float() if bias else 0)
+    scale = ref.abs().max().item()
+    err = (got.float() - ref).abs()
+    assert (err <= 2 * BF16_ULP * ref.abs() + 2e-3 * scale).all(), err.max().item()
+    assert torch.equal(linear(x, w, b), got)  # split-K partials are summed in a fixed order
+
+
+@pytest.mark.gpu
+def test_linear_reads_strided_rows_and_rejects_unsupported_shapes(gpu):
+    from mini_hisparse_amd.dense import linear
+
+    gen = torch.Generator(device=gpu).manual_seed(9)
+    wide = torch.randn(4, 512, generator=gen, device=gpu).to(torch.bfloat16)
+    x = wide[:, :256]  # row stride 512
+    w = torch.randn(96, 256, generator=gen, device=gpu).to(torch.bfloat16)
+    torch.testing.assert_close(linear(x, w).float(), x.float() @ w.float().T, rtol=2 * BF16_ULP, atol=0.05)
+    with pytest.raises(ValueError):
+        linear(torch.zeros(17, 256, dtype=torch.bfloat16, device=gpu), w)
+    with pytest.raises(ValueError):
+        linear(torch.zeros(2, 100, dtype=torch.bfloat16, device=gpu), torch.zeros(8, 100, dtype=torch.bfloat16, device=gpu))
