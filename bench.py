@@ -655,14 +655,26 @@ def main():
     copy = hbm_copy_gbs(torch, device)
     ceilings = attention_ceilings(torch, w, bytes_["attention"])
     att_gbs = bytes_["attention"] / (stages["attention"] * 1e-3) / 1e9
+    def hbm_line(stage, nbytes, pmc_kernels, **extra):
+        """A stage's algorithmic-byte rate and, from the committed counter summary, the HBM
+        bytes its kernels move per launch and the rate those give (the counter evidence)."""
+        ms = stages[stage]
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        traffic = pmc_traffic(pmc_kernels)
+        line = {"ms": ms, "bytes": nbytes, "GBps": gbs, "frac_hbm_peak": gbs / HBM_PEAK_GBS,
+                "hbm_traffic_bytes": traffic,
+                "hbm_traffic_GBps": None if traffic is None else traffic / (ms * 1e-3) / 1e9,
+                "kernels": list(pmc_kernels)}
+        line.update(extra)
+        return line
+
     kernels = {
-        "attention": {"ms": stages["attention"], "bytes": bytes_["attention"], "GBps": att_gbs,
-                      "frac_hbm_peak": att_gbs / HBM_PEAK_GBS,
-                      "per_head_bytes": bytes_["attention_per_head"]},
-        "quest_and_union": {"ms": stages["quest_and_union"], "bytes": bytes_["quest"],
-                            "GBps": bytes_["quest"] / (stages["quest_and_union"] * 1e-3) / 1e9},
-        "resolve": {"ms": stages["resolve"], "bytes": bytes_["resolver"],
-                    "GBps": bytes_["resolver"] / (stages["resolve"] * 1e-3) / 1e9},
+        "attention": hbm_line("attention", bytes_["attention"], ROOFLINE_KERNELS,
+                              per_head_bytes=bytes_["attention_per_head"]),
+        "quest_and_union": hbm_line("quest_and_union", bytes_["quest"],
+                                    ("quest_score_tile_kernel", "quest_topk_kernel", "build_union_kernel")),
+        "resolve": hbm_line("resolve", bytes_["resolver"], ("resolve_mark_kernel", "resolve_tags_kernel",
+                                                            "resolve_order_kernel", "resolve_outputs_kernel")),
         "gather": {"ms": stages["gather"], "bytes": bytes_["gather"],
                    "GBps": bytes_["gather"] / (stages["gather"] * 1e-3) / 1e9,
                    "host_link_memcpy_GBps": link,

@@ -101,6 +101,17 @@ class BatchedSparseDecode:
         self.attend_ws = torch.empty(self.attend_ws_bytes, dtype=torch.uint8, device=dev)
         self._len_arr = (ctypes.c_int64 * B)(*lengths)
         self._count_arr = (ctypes.c_int64 * B)(*self.counts)
+        # ctypes arguments built once per buffer set and per table / bound / host set
+        # (only the lengths change between decode steps)
+        self._descs = {}
+        self._bounds = {}
+        self._hosts = {}
+        self._miss_args = (
+            (ctypes.c_void_p * B)(*[self.miss_host[b].data_ptr() for b in range(B)]),
+            (ctypes.c_void_p * B)(*[self.miss_device[b].data_ptr() for b in range(B)]),
+            (ctypes.c_void_p * B)(*[self.row_counts[b, 2:].data_ptr() for b in range(B)]),
+            (ctypes.c_int64 * B)(*([self.capacity] * B)),
+        )
 
     def set_lengths(self, lengths):
         lengths = list(lengths)
@@ -124,8 +135,13 @@ class BatchedSparseDecode:
         q = queries.float().contiguous()
         lib = _lib.load()
         s = stream.cuda_stream if stream is not None else _lib.stream_handle(self.device)
-        lo = (ctypes.c_void_p * B)(*[t.data_ptr() for t in minimums])
-        hi = (ctypes.c_void_p * B)(*[t.data_ptr() for t in maximums])
+        key = tuple(map(id, minimums)) + tuple(map(id, maximums))
+        hit = self._bounds.get(key)
+        if hit is None or not all(a is b for a, b in zip(hit[0], (*minimums, *maximums))):
+            hit = ((*minimums, *maximums), (ctypes.c_void_p * B)(*[t.data_ptr() for t in minimums]),
+                   (ctypes.c_void_p * B)(*[t.data_ptr() for t in maximums]))
+            self._bounds[key] = hit
+        _, lo, hi = hit
         _lib.check(
             lib.hs_quest_topk(
                 q.data_ptr(), q.stride(0), q.stride(1), int(queries.dtype in (torch.bfloat16, torch.float16)),
@@ -159,8 +175,13 @@ class BatchedSparseDecode:
             "hs_build_union",
         )
 
-    def resolve(self, tables, row_stats=None, stream=None):
-        """One resolver launch over B (request, layer) tables; counts land in row_counts."""
+    def _resolve_descs(self, tables):
+        """Resolver descriptors of one set of B tables, built once: the workspace is sized
+        for the capacity lengths, and `resolve` refreshes the lengths per call."""
+        key = tuple(map(id, tables))
+        hit = self._descs.get(key)
+        if hit is not None and all(a is b for a, b in zip(hit[0], tables)):
+            return hit[1]
         B, P = self.batch, self.config.page_size
         lib = _lib.load()
         descs = (_lib.ResolveDesc * B)()
@@ -183,23 +204,37 @@ class BatchedSparseDecode:
             d.miss_host_rows = self.miss_host[b].data_ptr()
             d.miss_device_rows = self.miss_device[b].data_ptr()
             d.counts = self.row_counts[b].data_ptr()
-            d.row_stats = _lib.ptr(row_stats)
-            total += lib.hs_resolve_workspace_bytes(self.capacity, self.lengths[b], d.n_pages, d.hot_rows)
+            total += lib.hs_resolve_workspace_bytes(self.capacity, self.capacity_lengths[b], d.n_pages, d.hot_rows)
         if total > self.resolve_ws_bytes:
             self.resolve_ws = torch.empty(total, dtype=torch.uint8, device=self.device)
             self.resolve_ws_bytes = total
+        self._descs[key] = (tuple(tables), descs)
+        return descs
+
+    def resolve(self, tables, row_stats=None, stream=None):
+        """One resolver launch over B (request, layer) tables; counts land in row_counts."""
+        if len(tables) != self.batch:
+            raise ValueError(f"expected {self.batch} tables")
+        descs = self._resolve_descs(tables)
+        stats = _lib.ptr(row_stats)
+        for b in range(self.batch):
+            descs[b].length = self.lengths[b]
+            descs[b].row_stats = stats
         s = stream.cuda_stream if stream is not None else _lib.stream_handle(self.device)
-        _lib.check(lib.hs_resolve_rows_batched(descs, B, self.resolve_ws.data_ptr(), self.resolve_ws_bytes, s), "hs_resolve_rows_batched")
+        _lib.check(
+            _lib.load().hs_resolve_rows_batched(descs, self.batch, self.resolve_ws.data_ptr(), self.resolve_ws_bytes, s),
+            "hs_resolve_rows_batched",
+        )
 
     def gather(self, host_alias, pool, stream, grid_x=0):
         """All B miss plans in one launch on `stream` (reads host memory directly)."""
         B, cfg = self.batch, self.config
         lib = _lib.load()
-        hosts = (ctypes.c_void_p * B)(*([host_alias.data_ptr()] * B))
-        mh = (ctypes.c_void_p * B)(*[self.miss_host[b].data_ptr() for b in range(B)])
-        md = (ctypes.c_void_p * B)(*[self.miss_device[b].data_ptr() for b in range(B)])
-        mc = (ctypes.c_void_p * B)(*[self.row_counts[b, 2:].data_ptr() for b in range(B)])
-        ns = (ctypes.c_int64 * B)(*([self.capacity] * B))
+        alias = host_alias.data_ptr()
+        hosts = self._hosts.get(alias)
+        if hosts is None:
+            hosts = self._hosts[alias] = (ctypes.c_void_p * B)(*([alias] * B))
+        mh, md, mc, ns = self._miss_args
         row_bytes = cfg.kv_heads * cfg.head_dim * pool.element_size()
         _lib.check(
             lib.hs_gather_rows_batched(hosts, pool.data_ptr(), mh, md, mc, ns, B, cfg.page_size, row_bytes, grid_x, stream.cuda_stream),

@@ -299,6 +299,8 @@ class BatchedDecodeEngine:
         self._choose_projections()
         self._host_alias = [(ctypes.c_void_p * state.batch)(*([a.data_ptr()] * state.batch)) for a in state.alias]
         self.positions = torch.tensor(state.lengths, dtype=torch.int64, device=self.device)
+        # per layer: resolved (compute -> transfer) and gathered (transfer -> compute)
+        self._handoff = [(torch.cuda.Event(), torch.cuda.Event()) for _ in range(state.layers)]
 
     @torch.no_grad()
     def _pack_projections(self):
@@ -424,13 +426,12 @@ class BatchedDecodeEngine:
             marks["resolve"] = [marks["select"][1]]
             dec.resolve(st.tables[index], row_stats=st.row_stats)
             marks["resolve"].append(mark(compute))
-            resolved = torch.cuda.Event()
+            resolved, ready = self._handoff[index]
             resolved.record(compute)
             self.transfer.wait_event(resolved)
             marks["gather"] = [mark(self.transfer)]
             dec.gather(st.alias[index], st.pool, self.transfer)
             marks["gather"].append(mark(self.transfer))
-            ready = torch.cuda.Event()
             ready.record(self.transfer)
             compute.wait_event(ready)
             marks["attend"] = [mark(compute)]

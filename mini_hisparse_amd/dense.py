@@ -23,6 +23,7 @@ def _stream(tensor):
 
 
 _WORKSPACE = {}
+_GEMM_WS_BYTES = {}
 
 
 def _workspace(device, stream, nbytes):
@@ -55,7 +56,9 @@ def linear(x, weight, bias=None, out=None):
     y = torch.empty((rows, n), dtype=x.dtype, device=x.device) if out is None else out
     lib = _lib.load()
     stream = _stream(x)
-    nbytes = lib.hs_skinny_gemm_workspace_bytes(rows, n, k)
+    nbytes = _GEMM_WS_BYTES.get((rows, n, k))
+    if nbytes is None:
+        nbytes = _GEMM_WS_BYTES[(rows, n, k)] = lib.hs_skinny_gemm_workspace_bytes(rows, n, k)
     ws = _workspace(x.device, stream, nbytes)
     _lib.check(
         lib.hs_skinny_gemm(
