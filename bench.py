@@ -258,34 +258,51 @@ def hbm_copy_gbs(torch, device, nbytes=1 << 30):
 
 
 def attention_ceilings(torch, w, nbytes, reps=10):
-    """The attention and a read-only pass over the same rows (hs_probe_row_reads):
-    back to back (`warm`: rows partly in the 256 MB Infinity Cache) and each after a
-    1 GiB copy that evicts it (`cold`: HBM).  GB/s of the attention's algorithmic bytes."""
+    """The attention, a read-only pass over the same row segments (hs_probe_row_reads) and a
+    contiguous read of as many bytes, in GB/s of the attention's algorithmic bytes:
+    `warm` back to back (rows partly in the 256 MB Infinity Cache); `cold` after reading 1 GiB
+    of other data (clean caches: HBM); `cold_dirty` after a 1 GiB copy, whose dirty lines the
+    reads must write back (the state after the step's gather has written its rows)."""
+    from mini_hisparse_amd import _lib
+
     dec, pool, q = w["dec"], w["pool"], w["q"]
-    sink = torch.empty(16, dtype=torch.int32, device=pool.device)
-    src = torch.empty(1 << 30, dtype=torch.uint8, device=pool.device)
+    dev = pool.device
+    sink = torch.empty(16, dtype=torch.int32, device=dev)
+    src = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
     dst = torch.empty_like(src)
     offsets = dec.entry_offsets(pool)
-    runs = {"attention": lambda: dec.attend(q, pool), "probe": lambda: dec.probe_reads(pool, offsets, sink)}
+    n = nbytes // 512
+    stream_buf = torch.empty(n * 512, dtype=torch.uint8, device=dev)
+    stream_offsets = torch.arange(n, dtype=torch.int64, device=dev) * 512
+
+    def stream_read():
+        _lib.check(_lib.load().hs_probe_row_reads(
+            stream_buf.data_ptr(), stream_buf.numel(), stream_offsets.data_ptr(), n, 256, 256, sink.data_ptr(),
+            torch.cuda.current_stream(dev).cuda_stream), "hs_probe_row_reads")
+
+    flushes = {"cold": lambda: src.view(torch.int64).sum(), "cold_dirty": lambda: dst.copy_(src)}
+    runs = {"attention": lambda: dec.attend(q, pool), "probe": lambda: dec.probe_reads(pool, offsets, sink),
+            "stream_read": stream_read}
     out = {}
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     for name, fn in runs.items():
         fn()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record()
         for _ in range(reps):
             fn()
         e1.record()
         torch.cuda.synchronize()
         out[f"{name}_warm_GBps"] = nbytes / (e0.elapsed_time(e1) / reps * 1e-3) / 1e9
-        times = []
-        for _ in range(reps):
-            dst.copy_(src)
-            e0.record()
-            fn()
-            e1.record()
-            torch.cuda.synchronize()
-            times.append(e0.elapsed_time(e1))
-        out[f"{name}_cold_GBps"] = nbytes / (float(np.median(times)) * 1e-3) / 1e9
+        for label, flush in flushes.items():
+            times = []
+            for _ in range(reps):
+                flush()
+                e0.record()
+                fn()
+                e1.record()
+                torch.cuda.synchronize()
+                times.append(e0.elapsed_time(e1))
+            out[f"{name}_{label}_GBps"] = nbytes / (float(np.median(times)) * 1e-3) / 1e9
     return out
 
 

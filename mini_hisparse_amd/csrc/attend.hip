@@ -536,21 +536,37 @@ __global__ __launch_bounds__(256) void attend_merge_kernel(const float* part_m, 
 // Read-only probe of a row-gather access pattern: for each of n segment pairs
 // (byte offsets of a K segment; its V segment `plane_bytes` further) read every
 // 16-byte unit, consecutive lanes on consecutive units, with no arithmetic
-// beyond an XOR that keeps the loads alive.  Given the K offsets of the
+// beyond an XOR that keeps the loads alive; a fixed grid strides over the units
+// with eight loads in flight per thread.  Given the K offsets of the
 // attention's entries, its duration is the ceiling of the attention's memory
 // traffic on the device.
 constexpr int PROBE_T = 256;
 
+constexpr int PROBE_U = 8;       // loads in flight per thread
+constexpr int PROBE_BLOCKS = 2048;
+
 __global__ __launch_bounds__(PROBE_T) void probe_row_reads_kernel(const char* base, const int64_t* offsets,
                                                                    int64_t n, int64_t seg_units,
                                                                    int64_t plane_bytes, u32x4* sink) {
-  const int64_t u = static_cast<int64_t>(blockIdx.x) * PROBE_T + threadIdx.x;
-  const int64_t e = u / (2 * seg_units);
-  if (e >= n) return;
-  const int64_t w = u - e * 2 * seg_units;
-  const int64_t off = offsets[e] + (w >= seg_units ? plane_bytes : 0) + (w % seg_units) * 16;
-  const u32x4 v = *reinterpret_cast<const u32x4*>(base + off);
-  if (v[0] == 0x9e3779b9u && v[1] == 0x7f4a7c15u && v[2] == 0xf39cc060u && v[3] == 0x5ced1a2bu) sink[0] = v;
+  // grid-stride over the 16-byte units, PROBE_U loads issued before any is used
+  const int64_t total = n * 2 * seg_units;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * PROBE_T;
+  u32x4 acc = {0u, 0u, 0u, 0u};
+  for (int64_t u0 = static_cast<int64_t>(blockIdx.x) * PROBE_T + threadIdx.x; u0 < total; u0 += PROBE_U * stride) {
+    u32x4 v[PROBE_U];
+#pragma unroll
+    for (int k = 0; k < PROBE_U; ++k) {
+      int64_t u = u0 + k * stride;
+      if (u >= total) u = u0;  // in bounds (a repeat of this thread's first unit)
+      const int64_t e = u / (2 * seg_units);
+      const int64_t w = u - e * 2 * seg_units;
+      const int64_t off = offsets[e] + (w >= seg_units ? plane_bytes : 0) + (w % seg_units) * 16;
+      v[k] = *reinterpret_cast<const u32x4*>(base + off);
+    }
+#pragma unroll
+    for (int k = 0; k < PROBE_U; ++k) acc ^= v[k];
+  }
+  if (acc[0] == 0x9e3779b9u && acc[1] == 0x7f4a7c15u && acc[2] == 0xf39cc060u && acc[3] == 0x5ced1a2bu) sink[0] = acc;
 }
 
 // ---- host side ----------------------------------------------------------------
@@ -765,7 +781,8 @@ extern "C" int hs_probe_row_reads(const void* base, int64_t region_bytes, const 
   HS_CHECK_ARG((reinterpret_cast<uintptr_t>(base) & 15) == 0, "region must be 16-byte aligned");
   (void)region_bytes;  // offsets are validated by the caller against region_bytes
   const int64_t seg_units = segment_bytes / 16;
-  const int64_t blocks = ceil_div(n * 2 * seg_units, PROBE_T);
+  int64_t blocks = ceil_div(n * 2 * seg_units, PROBE_T * PROBE_U);
+  if (blocks > PROBE_BLOCKS) blocks = PROBE_BLOCKS;
   hipLaunchKernelGGL(probe_row_reads_kernel, dim3(static_cast<unsigned>(blocks)), dim3(PROBE_T), 0, stream,
                      static_cast<const char*>(base), offsets, n, seg_units, plane_bytes, static_cast<u32x4*>(sink));
   HS_CHECK_LAUNCH("probe");
