@@ -48,6 +48,9 @@ def parse_args():
                    help="request groups of the microbench step: group g gathers while g+1 resolves "
                         "and g-1 attends (1 = no overlap; on MI355X the host reads of a running "
                         "gather stall concurrent HBM kernels, so overlap does not pay)")
+    p.add_argument("--transfer-stream", action="store_true",
+                   help="gather on a separate stream ordered by events (the reference's arrangement); "
+                        "by default a single request group runs every stage on the compute stream")
     p.add_argument("--no-cpu-baseline", action="store_true", help="skip the CPU oracle leg")
     p.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU sample work")
     p.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
@@ -202,7 +205,7 @@ def run_steps(torch, w, steps, record):
 def run_pipelined(torch, w, steps):
     """`steps` decode steps of the whole batch as overlapped request groups."""
     pipe, device = w["pipe"], w["pool"].device
-    transfer = w.setdefault("transfer", torch.cuda.Stream(device))
+    transfer = w.setdefault("transfer", torch.cuda.Stream(device)) if w["use_transfer_stream"] else None
     row_stats = w.setdefault("row_stats", torch.zeros(3, dtype=torch.int64, device=device))
     out = w.get("pipe_out")
     for _ in range(steps):
@@ -210,8 +213,9 @@ def run_pipelined(torch, w, steps):
         w["lru_all"].copy_(w["lru0"])
         out, done = pipe.step(w["q"], w["kmin"], w["kmax"], w["tables"], w["pool"], w["alias"], transfer,
                               row_stats=row_stats, out=out)
-        # the next step restores the hot tables only after this step's readers
-        transfer.wait_event(done)
+        if transfer is not None:
+            # the next step restores the hot tables only after this step's readers
+            transfer.wait_event(done)
     w["pipe_out"] = out
     return out
 
@@ -651,6 +655,7 @@ def main():
         args.batch = 8
     print(f"[bench] building workload (batch {args.batch})", file=sys.stderr, flush=True)
     w = build_workload(args, torch, device)
+    w["use_transfer_stream"] = args.transfer_stream or args.parts > 1
     run_pipelined(torch, w, args.warmup)
     torch.cuda.synchronize()
     print("[bench] timing", file=sys.stderr, flush=True)
@@ -713,7 +718,9 @@ def main():
         "config": {
             "workload": "microbench (BASELINE configs[1]): 1 layer, 64 q / 8 kv heads, head_dim 128, "
             f"page 16, 4096 pages/request, batch {args.batch}, Quest top-64, 50% resident / 30% hot / 20% miss; "
-            f"{args.parts} request groups overlapped",
+            + (f"{args.parts} request groups overlapped" if args.parts > 1 else
+               "gather on a transfer stream ordered by events" if args.transfer_stream else
+               "every stage on one stream"),
             "global_batch": args.batch,
             "seq_len": w["length"],
             "parallelism": "none (1 GPU)",

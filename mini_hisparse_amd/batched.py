@@ -346,24 +346,32 @@ class PipelinedSparseDecode:
             part.set_lengths(list(lengths)[s])
 
     def step(self, queries, minimums, maximums, tables, pool, host_alias, transfer, *, row_stats=None, out=None):
-        """The whole layer for all groups; returns (out [B, Hq, D], done_event)."""
+        """The whole layer for all groups; returns (out [B, Hq, D], done_event).  With
+        ``transfer`` None every stage runs on the compute stream (no hand-offs, no overlap)."""
         compute = torch.cuda.current_stream(self.device)
         if out is None:
             out = torch.empty_like(queries if queries.dtype == pool.dtype else queries.to(pool.dtype))
-        ready = []
-        for s, part in zip(self.slices, self.parts):
-            part.select(queries[s], minimums[s], maximums[s])
-            part.resolve(tables[s], row_stats=row_stats)
-            resolved = torch.cuda.Event()
-            resolved.record(compute)
-            transfer.wait_event(resolved)
-            part.gather(host_alias, pool, transfer)
-            event = torch.cuda.Event()
-            event.record(transfer)
-            ready.append(event)
-        for s, part, event in zip(self.slices, self.parts, ready):
-            compute.wait_event(event)
-            part.attend(queries[s], pool, out=out[s])
+        if transfer is None:
+            for s, part in zip(self.slices, self.parts):
+                part.select(queries[s], minimums[s], maximums[s])
+                part.resolve(tables[s], row_stats=row_stats)
+                part.gather(host_alias, pool, compute)
+                part.attend(queries[s], pool, out=out[s])
+        else:
+            ready = []
+            for s, part in zip(self.slices, self.parts):
+                part.select(queries[s], minimums[s], maximums[s])
+                part.resolve(tables[s], row_stats=row_stats)
+                resolved = torch.cuda.Event()
+                resolved.record(compute)
+                transfer.wait_event(resolved)
+                part.gather(host_alias, pool, transfer)
+                event = torch.cuda.Event()
+                event.record(transfer)
+                ready.append(event)
+            for s, part, event in zip(self.slices, self.parts, ready):
+                compute.wait_event(event)
+                part.attend(queries[s], pool, out=out[s])
         done = torch.cuda.Event()
         done.record(compute)
         return out, done

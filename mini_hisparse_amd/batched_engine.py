@@ -267,9 +267,20 @@ class BatchedDecodeEngine:
     """Greedy decode of B requests, layer-major, over a :class:`SparseKVState`."""
 
     def __init__(self, model: MiniModel, state: SparseKVState, top_pages, *, max_tokens=None, keep_sink=True,
-                 selector="quest", seed=0):
+                 selector="quest", seed=0, graphs=False, projections="auto", transfer_stream=False):
         """``selector``: "quest" (per-head Quest pages over the bounds) or "uniform"
-        (:func:`uniform_pages`, shared by every head, resampled each step)."""
+        (:func:`uniform_pages`, shared by every head, resampled each step).  ``graphs``:
+        replay the dense part of each layer boundary as a HIP graph (when every per-layer
+        projection runs on hs_skinny_gemm; captured after the first step): it cuts the host
+        time of a boundary from ~80 to ~22 us, which pays only where the host, not the GPU,
+        paces the step.  ``projections``: "auto" (timed choice per projection), "kernel"
+        (hs_skinny_gemm wherever it applies) or "torch".  ``transfer_stream``: gather on a
+        separate stream ordered by events (the reference's arrangement, hybrid.py:443-477);
+        the default gathers on the compute stream, because overlap does not pay on MI355X
+        (host reads slow the kernels beside them) and each cross-stream hand-off costs
+        ~20 us of GPU time."""
+        if projections not in ("auto", "kernel", "torch"):
+            raise ValueError(f"unknown projections {projections!r}")
         if selector not in ("quest", "uniform"):
             raise ValueError(f"unknown selector {selector!r}")
         cfg = model.config
@@ -294,14 +305,84 @@ class BatchedDecodeEngine:
                 f"hot_rows {state.hot_rows} below the union bound {self.dec.capacity} of "
                 f"{cfg.num_attention_heads} heads x {top_pages} pages"
             )
-        self.transfer = torch.cuda.Stream(self.device)
+        self.transfer = torch.cuda.Stream(self.device) if transfer_stream else None
         self._pack_projections()
-        self._choose_projections()
+        self._choose_projections(projections)
         self._host_alias = [(ctypes.c_void_p * state.batch)(*([a.data_ptr()] * state.batch)) for a in state.alias]
         self.positions = torch.tensor(state.lengths, dtype=torch.int64, device=self.device)
         # per layer: resolved (compute -> transfer) and gathered (transfer -> compute)
         self._handoff = [(torch.cuda.Event(), torch.cuda.Event()) for _ in range(state.layers)]
+        self._static_buffers()
+        self.use_graphs = graphs and all(self.projection_kernel[n] for n in ("qkv", "o_proj", "gate_up", "down"))
+        self._graphs = None
 
+    def _static_buffers(self):
+        """Fixed buffers of the dense stages, so that their launches can be replayed."""
+        cfg, B, dev, dt = self.model.config, self.state.batch, self.device, self.model.dtype
+        Hq, Hkv, D = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
+        new = lambda *shape: torch.empty(shape, dtype=dt, device=dev)
+        self._x, self._h, self._o, self._delta = (new(B, cfg.hidden_size) for _ in range(4))
+        self._qkv = new(B, (Hq + 2 * Hkv) * D)
+        self._q, self._k, self._v = new(B, Hq, D), new(B, Hkv, D), new(B, Hkv, D)
+        self._attn_out = new(B, Hq, D)
+        self._gate_up = new(B, 2 * cfg.intermediate_size)
+        self._act = new(B, cfg.intermediate_size)
+
+    # -- dense stages (the same launches eagerly and inside the graphs) ---------
+    def _dense_in(self, index, first):
+        """Residual add of the previous MLP + input RMSNorm, q|k|v, rotary + split."""
+        cfg = self.model.config
+        layer = self.model.model.layers[index]
+        qkv_w, qkv_b, _ = self._packed[index]
+        h = add_rms_norm(self._x, None if first else self._delta, layer.input_layernorm.weight, cfg.rms_norm_eps,
+                         out=self._h)
+        rotary_split(self._project("qkv", h, qkv_w, qkv_b, out=self._qkv), self.positions,
+                     cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim, cfg.rope_theta,
+                     out=(self._q, self._k, self._v))
+
+    def _dense_out(self, index):
+        """o_proj + residual + post-attention RMSNorm, gate|up, SiLU gate, down (-> delta)."""
+        cfg = self.model.config
+        layer = self.model.model.layers[index]
+        B = self.state.batch
+        _, _, gate_up_w = self._packed[index]
+        o = self._project("o_proj", self._attn_out.view(B, -1), layer.self_attn.o_proj.weight, out=self._o)
+        h = add_rms_norm(self._x, o, layer.post_attention_layernorm.weight, cfg.rms_norm_eps, out=self._h)
+        act = silu_mul(self._project("gate_up", h, gate_up_w, out=self._gate_up), out=self._act)
+        self._project("down", act, layer.mlp.down_proj.weight, out=self._delta)
+
+    def _boundary(self, index):
+        """Dense launches between the sparse stages of layer index - 1 and index
+        (index = layers: after the last layer)."""
+        L = len(self.model.model.layers)
+        if index > 0:
+            self._dense_out(index - 1)
+        if index < L:
+            self._dense_in(index, first=index == 0)
+
+    @torch.no_grad()
+    def _capture(self):
+        """One HIP graph per layer boundary, captured on a side stream (after an eager pass
+        of the same launches there, so that every kernel and workspace exists)."""
+        L = len(self.model.model.layers)
+        stream = torch.cuda.Stream(self.device)
+        stream.wait_stream(torch.cuda.current_stream(self.device))
+        saved = [t.clone() for t in (self._x, self._delta)]
+        with torch.cuda.stream(stream):
+            for index in range(L + 1):
+                self._boundary(index)
+        stream.synchronize()
+        pool = torch.cuda.graph_pool_handle()
+        graphs = []
+        for index in range(L + 1):
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph, pool=pool, stream=stream):
+                self._boundary(index)
+            graphs.append(graph)
+        torch.cuda.current_stream(self.device).wait_stream(stream)
+        self._x.copy_(saved[0])
+        self._delta.copy_(saved[1])
+        self._graphs = graphs
     @torch.no_grad()
     def _pack_projections(self):
         """One weight (and bias) per layer for q|k|v and for gate|up, so each is one GEMM;
@@ -325,7 +406,7 @@ class BatchedDecodeEngine:
             self._packed.append((qkv_w, qkv_b, gate_up))
 
     @torch.no_grad()
-    def _choose_projections(self):
+    def _choose_projections(self, mode="auto"):
         """Per projection, the faster of the skinny-GEMM kernel (hs_skinny_gemm) and
         PyTorch's GEMM at this batch, timed over the layers' own weights (each call
         reads another layer's weight from HBM, as in a step).  The kernel wins the
@@ -342,8 +423,8 @@ class BatchedDecodeEngine:
         self.projection_kernel = {}
         for name, weights in groups.items():
             x = torch.full((B, weights[0][0].shape[1]), 0.01, dtype=dt, device=dev)
-            if not linear_supported(x, weights[0][0]):
-                self.projection_kernel[name] = False
+            if not linear_supported(x, weights[0][0]) or mode != "auto":
+                self.projection_kernel[name] = mode == "kernel" and linear_supported(x, weights[0][0])
                 continue
             elapsed = {}
             for label, fn in (("kernel", linear), ("torch", F.linear)):
@@ -357,10 +438,14 @@ class BatchedDecodeEngine:
                 elapsed[label] = start.elapsed_time(end)
             self.projection_kernel[name] = elapsed["kernel"] <= elapsed["torch"]
 
-    def _project(self, name, x, weight, bias=None):
+    def _project(self, name, x, weight, bias=None, out=None):
         if self.projection_kernel[name]:
-            return linear(x, weight, bias)
-        return F.linear(x, weight, bias)
+            return linear(x, weight, bias, out=out)
+        y = F.linear(x, weight, bias)
+        if out is None:
+            return y
+        out.copy_(y)
+        return out
 
     def _append(self, layer, k, v, positions):
         st, cfg = self.state, self.state.config
@@ -385,7 +470,6 @@ class BatchedDecodeEngine:
         """
         model, st, dec = self.model, self.state, self.dec
         cfg = model.config
-        B, Hq, Hkv, D = st.batch, cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
         positions = list(st.lengths)
         st.open_tail_pages(positions)
         dec.set_lengths([p + 1 for p in positions])
@@ -394,9 +478,9 @@ class BatchedDecodeEngine:
             sampled = uniform_pages([p + 1 for p in positions], st.config.page_size, dec.top, st.layers,
                                     self._sampler, self.device)
         compute = torch.cuda.current_stream(self.device)
-        eps = cfg.rms_norm_eps
-        x = model.model.embed_tokens(tokens)
-        delta = None  # the previous layer's MLP output, added to x by the next norm
+        L = st.layers
+        self._x.copy_(model.model.embed_tokens(tokens))
+        graphs = self._graphs
 
         def mark(stream):
             if timer is None:
@@ -405,15 +489,18 @@ class BatchedDecodeEngine:
             event.record(stream)
             return event
 
-        for index, layer in enumerate(model.model.layers):
-            attn = layer.self_attn
-            qkv_w, qkv_b, gate_up_w = self._packed[index]
-            marks = {"dense_in": [mark(compute)]}
-            h = add_rms_norm(x, delta, layer.input_layernorm.weight, eps)
-            q, k, v = rotary_split(self._project("qkv", h, qkv_w, qkv_b), self.positions, Hq, Hkv, D,
-                                   cfg.rope_theta)
-            marks["dense_in"].append(mark(compute))
-            marks["append"] = [mark(compute)]
+        def boundary(index):
+            if graphs is not None:
+                graphs[index].replay()
+            else:
+                self._boundary(index)
+
+        q, k, v = self._q, self._k, self._v
+        for index in range(L):
+            marks = {"dense": [mark(compute)]}
+            boundary(index)
+            marks["dense"].append(mark(compute))
+            marks["append"] = [marks["dense"][1]]
             self._append(index, k, v, positions)
             lo, hi = st.bounds[index]
             marks["append"].append(mark(compute))
@@ -426,30 +513,38 @@ class BatchedDecodeEngine:
             marks["resolve"] = [marks["select"][1]]
             dec.resolve(st.tables[index], row_stats=st.row_stats)
             marks["resolve"].append(mark(compute))
-            resolved, ready = self._handoff[index]
-            resolved.record(compute)
-            self.transfer.wait_event(resolved)
-            marks["gather"] = [mark(self.transfer)]
-            dec.gather(st.alias[index], st.pool, self.transfer)
-            marks["gather"].append(mark(self.transfer))
-            ready.record(self.transfer)
-            compute.wait_event(ready)
+            transfer = self.transfer if self.transfer is not None else compute
+            if transfer is not compute:
+                resolved, ready = self._handoff[index]
+                resolved.record(compute)
+                transfer.wait_event(resolved)
+            marks["gather"] = [mark(transfer)]
+            dec.gather(st.alias[index], st.pool, transfer)
+            marks["gather"].append(mark(transfer))
+            if transfer is not compute:
+                ready.record(transfer)
+                compute.wait_event(ready)
             marks["attend"] = [mark(compute)]
-            out = dec.attend(q, st.pool)
+            out = dec.attend(q, st.pool, out=self._attn_out)
             marks["attend"].append(mark(compute))
             if observer is not None:
                 observer(index, q, k, v, out)
-            marks["dense_out"] = [marks["attend"][1]]
-            h = add_rms_norm(x, self._project("o_proj", out.reshape(B, Hq * D), attn.o_proj.weight),
-                             layer.post_attention_layernorm.weight, eps)
-            delta = self._project("down", silu_mul(self._project("gate_up", h, gate_up_w)), layer.mlp.down_proj.weight)
-            marks["dense_out"].append(mark(compute))
+            if index == L - 1:  # the last layer's o_proj and MLP
+                marks["dense_last"] = [marks["attend"][1]]
+                boundary(L)
+                marks["dense_last"].append(mark(compute))
             if timer is not None:
                 timer.append((index, marks, dec.entry_counts.sum(), dec.row_counts[:, 2].sum()))
-        logits = self._project("lm_head", add_rms_norm(x, delta, model.model.norm.weight, eps), model.lm_head.weight)
+        logits = self._project(
+            "lm_head", add_rms_norm(self._x, self._delta, model.model.norm.weight, cfg.rms_norm_eps),
+            model.lm_head.weight,
+        )
+        tokens = logits.argmax(-1)
         st.lengths = [p + 1 for p in positions]
         self.positions += 1
-        return logits.argmax(-1)
+        if self.use_graphs and self._graphs is None:
+            self._capture()
+        return tokens
 
 
 def random_model(workload: DecodeWorkload, device, seed=0):

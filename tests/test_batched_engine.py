@@ -31,14 +31,17 @@ def tiny(**overrides):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("overrides", [{}, {"heads": 16, "kv_heads": 2, "head_dim": 64, "hidden": 1024}])
-def test_batched_engine_layers_match_oracle(gpu, overrides):
+@pytest.mark.parametrize(
+    "overrides,transfer_stream",
+    [({}, False), ({}, True), ({"heads": 16, "kv_heads": 2, "head_dim": 64, "hidden": 1024}, False)],
+)
+def test_batched_engine_layers_match_oracle(gpu, overrides, transfer_stream):
     from mini_hisparse_amd.batched_engine import BatchedDecodeEngine, build_state, random_model
 
     wl = tiny(**overrides)
     model = random_model(wl, gpu, seed=1)
     state = build_state(wl, gpu, seed=2)
-    engine = BatchedDecodeEngine(model, state, wl.top_pages)
+    engine = BatchedDecodeEngine(model, state, wl.top_pages, transfer_stream=transfer_stream)
     L, B, C, P = wl.layers, wl.batch, state.pages, wl.page_size
     Hkv, D = wl.kv_heads, wl.head_dim
     records = []
@@ -158,3 +161,35 @@ def test_batched_engine_uniform_selection_matches_oracle(gpu):
     assert sum(stats) == unions
     assert stats[2] > stats[1]  # resampling every step: misses outnumber hot hits
     assert len(drawn) >= 8 * L * B  # fresh draws each step (5 per step; about 13 distinct expected)
+
+
+@pytest.mark.gpu
+def test_graph_replayed_dense_layers_match_eager_launches(gpu):
+    """The dense launches replayed from HIP graphs give bit-identical tokens and attention
+    outputs to the same launches made eagerly, step after step (the sparse stages run
+    eagerly in between)."""
+    from mini_hisparse_amd.batched_engine import BatchedDecodeEngine, build_state, random_model
+
+    wl = tiny()
+    runs = []
+    for graphs in (False, True):
+        model = random_model(wl, gpu, seed=1)
+        state = build_state(wl, gpu, seed=2)
+        engine = BatchedDecodeEngine(model, state, wl.top_pages, graphs=graphs, projections="kernel")
+        assert engine.use_graphs == graphs
+        outs, toks = [], []
+        tokens = torch.tensor([1, 2, 3], device=gpu)
+        for step in range(5):  # step 0 eager; the graphs are captured after it and replayed from step 1
+            tokens = engine.step(tokens, lambda l, q, k, v, out: outs.append((q.clone(), out.clone())))
+            toks.append(tokens.clone())
+        torch.cuda.synchronize()
+        if graphs:
+            assert engine._graphs is not None and len(engine._graphs) == wl.layers + 1
+        runs.append((outs, toks, state.row_stats.clone()))
+    (eo, et, es), (go, gt, gs) = runs
+    assert len(eo) == len(go) == 5 * wl.layers
+    for (q0, o0), (q1, o1) in zip(eo, go):
+        assert torch.equal(q0, q1) and torch.equal(o0, o1)
+    for t0, t1 in zip(et, gt):
+        assert torch.equal(t0, t1)
+    assert torch.equal(es, gs)
