@@ -35,6 +35,19 @@ def _workspace(device, stream, nbytes):
     return ws
 
 
+def _check_out(out, shape, like, what):
+    """An ``out`` buffer the kernels may write: the expected shape and dtype, on the
+    device of ``like``, rows of unit inner stride."""
+    if out is None:
+        return
+    if tuple(out.shape) != tuple(shape) or out.dtype != like.dtype or out.device != like.device:
+        raise ValueError(f"{what}: out must be {tuple(shape)} {like.dtype} on {like.device}")
+    if out.stride(-1) != 1 or (out.dim() == 2 and out.stride(0) < out.shape[1]):
+        raise ValueError(f"{what}: out rows must have unit inner stride")
+    if out.dim() == 3 and not out.is_contiguous():
+        raise ValueError(f"{what}: out must be contiguous")
+
+
 def linear_supported(x, weight):
     """Shapes ``linear`` takes: 1-16 rows, K a multiple of 32, bf16/f16, 16-byte aligned rows."""
     return (
@@ -53,6 +66,7 @@ def linear(x, weight, bias=None, out=None):
         raise ValueError("bias must be [N] contiguous in the dtype of x")
     rows, k = x.shape
     n = weight.shape[0]
+    _check_out(out, (rows, n), x, "linear")
     y = torch.empty((rows, n), dtype=x.dtype, device=x.device) if out is None else out
     lib = _lib.load()
     stream = _stream(x)
@@ -79,6 +93,7 @@ def add_rms_norm(x, delta, weight, eps, out=None):
         raise ValueError("delta must match x in shape, strides and dtype")
     if weight.shape != (x.shape[1],) or weight.dtype != x.dtype:
         raise ValueError("weight must be [width] in the dtype of x")
+    _check_out(out, x.shape, x, "add_rms_norm")
     y = torch.empty_like(x) if out is None else out
     _lib.check(
         _lib.load().hs_add_rms_norm(
@@ -106,6 +121,9 @@ def rotary_split(qkv, positions, heads, kv_heads, head_dim, theta, out=None):
         v = torch.empty_like(k)
     else:
         q, k, v = out
+        _check_out(q, (rows, heads, head_dim), qkv, "rotary_split q")
+        _check_out(k, (rows, kv_heads, head_dim), qkv, "rotary_split k")
+        _check_out(v, (rows, kv_heads, head_dim), qkv, "rotary_split v")
     _lib.check(
         _lib.load().hs_rotary_split(
             qkv.data_ptr(), qkv.stride(0), q.data_ptr(), k.data_ptr(), v.data_ptr(), positions.data_ptr(), rows,
@@ -121,6 +139,7 @@ def silu_mul(gate_up, out=None):
     if gate_up.dim() != 2 or gate_up.stride(1) != 1 or gate_up.shape[1] % 2:
         raise ValueError("gate_up must be [rows, 2 width] with unit inner stride")
     rows, width = gate_up.shape[0], gate_up.shape[1] // 2
+    _check_out(out, (rows, width), gate_up, "silu_mul")
     y = torch.empty((rows, width), dtype=gate_up.dtype, device=gate_up.device) if out is None else out
     _lib.check(
         _lib.load().hs_silu_mul(

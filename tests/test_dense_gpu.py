@@ -22,6 +22,19 @@ def test_wrappers_check_shapes_without_a_gpu():
         rotary_split(torch.zeros(2, 10, dtype=torch.bfloat16), torch.zeros(2, dtype=torch.int64), 1, 1, 4, 1e4)
     with pytest.raises(ValueError, match="gate_up"):
         silu_mul(torch.zeros(2, 5, dtype=torch.bfloat16))
+    # an out buffer of the wrong shape, dtype or layout is refused before any launch
+    with pytest.raises(ValueError, match="out"):
+        add_rms_norm(x, None, torch.ones(8, dtype=torch.bfloat16), 1e-6, out=torch.empty(4, 7, dtype=torch.bfloat16))
+    with pytest.raises(ValueError, match="out"):
+        silu_mul(torch.zeros(2, 8, dtype=torch.bfloat16), out=torch.empty(2, 4, dtype=torch.float32))
+    with pytest.raises(ValueError, match="out"):
+        rotary_split(torch.zeros(2, 16, dtype=torch.bfloat16), torch.zeros(2, dtype=torch.int64), 2, 1, 4, 1e4,
+                     out=(torch.empty(2, 2, 4, dtype=torch.bfloat16), torch.empty(2, 1, 4, dtype=torch.bfloat16),
+                          torch.empty(2, 2, 4, dtype=torch.bfloat16)))
+    from mini_hisparse_amd.dense import linear
+    with pytest.raises(ValueError, match="out"):
+        linear(torch.zeros(2, 32, dtype=torch.bfloat16), torch.zeros(8, 32, dtype=torch.bfloat16),
+               out=torch.empty(2, 9, dtype=torch.bfloat16))
 
 
 @pytest.mark.gpu
