@@ -293,8 +293,47 @@ def test_gather_copies_planned_rows(gpu, dtype, P, kv, D):
     assert torch.equal(pool.cpu(), expected)
 
 
+def test_gather_full_size_rows_equal_host_rows(gpu):
+    """BASELINE configs[1] scale (one request: 4096 host pages of 4 KB rows, ~8k misses): every
+    planned device row holds its host row afterwards and no other device row changes."""
+    from mini_hisparse_amd.row_index import RowPlan
+    from mini_hisparse_amd.row_kernels import MappedHost, gather_rows
+
+    P, kv, D = 16, 8, 128
+    host_blocks, dev_blocks, m = 4096, 1024, 8000
+    gen = torch.Generator(device=gpu).manual_seed(5)
+    host_dev = torch.randn((host_blocks, 2, P, kv, D), generator=gen, device=gpu).to(torch.bfloat16)
+    host = torch.empty(host_dev.shape, dtype=torch.bfloat16, pin_memory=True)
+    host.copy_(host_dev)
+    pool = torch.randn((dev_blocks, 2, P, kv, D), generator=gen, device=gpu).to(torch.bfloat16)
+    before = pool.clone()
+    rng = np.random.default_rng(6)
+    hrows = torch.from_numpy(rng.choice(host_blocks * P, size=m, replace=False)).to(gpu)
+    drows = torch.from_numpy(rng.choice(dev_blocks * P, size=m, replace=False)).to(gpu)
+    pad = torch.full((100,), -1, dtype=torch.int64, device=gpu)
+    plan = RowPlan(None, torch.cat((hrows, pad)), torch.cat((drows, pad)), None)
+    gather_rows(MappedHost(host), pool, plan, cfg(P, kv, D))
+    torch.cuda.synchronize()
+    got = pool[drows // P, :, drows % P]
+    want = host_dev[hrows // P, :, hrows % P]
+    assert torch.equal(got, want)
+    untouched = torch.ones(dev_blocks * P, dtype=torch.bool, device=gpu)
+    untouched[drows] = False
+    rows = torch.nonzero(untouched).flatten()
+    assert torch.equal(pool[rows // P, :, rows % P], before[rows // P, :, rows % P])
+
+
 # ---------------------------------------------- group attention = row attention
-@pytest.mark.parametrize("P,kv,g,D,pages,top", [(16, 8, 8, 128, 512, 64), (16, 4, 7, 128, 300, 32), (7, 2, 3, 24, 60, 6)])
+@pytest.mark.parametrize(
+    "P,kv,g,D,pages,top",
+    [
+        (16, 8, 8, 128, 512, 64),
+        (16, 4, 7, 128, 300, 32),
+        (7, 2, 3, 24, 60, 6),
+        (16, 8, 8, 128, 4096, 64),  # BASELINE configs[1]: one request of the microbench
+        (16, 4, 7, 128, 8192, 64),  # BASELINE configs[3]: one (request, layer) of the 7B shape at 128k
+    ],
+)
 def test_group_attention_matches_per_head_rows(gpu, P, kv, g, D, pages, top):
     from mini_hisparse_amd.row_index import resolve_rows
     from mini_hisparse_amd.row_kernels import attend_groups, attend_rows
