@@ -206,6 +206,7 @@ def test_resolver_row_stats_accumulate(gpu):
     [
         (torch.bfloat16, 300, 16, 2, 4, 64, 16, True, None),
         (torch.bfloat16, 4096, 16, 8, 8, 128, 64, True, None),  # microbench shape
+        (torch.bfloat16, 8193, 16, 4, 7, 128, 64, True, 131073),  # 7B shape at 128k (+1 decoded token)
         (torch.bfloat16, 1000, 16, 4, 7, 128, 64, False, 15990),
         (torch.float16, 77, 7, 2, 3, 24, 5, True, 535),
         (torch.float32, 90, 4, 1, 2, 8, 7, True, 357),
