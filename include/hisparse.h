@@ -79,8 +79,8 @@ int64_t hs_quest_workspace_bytes(int64_t batch, int64_t heads, int64_t max_pages
  * Quest page scores and per-head top-k for `batch` (<= 16) requests.
  * Replaces: quest_selection (mini_hisparse/selection.py:80-101) up to the
  * chosen page ids (:100).
- *   query      [batch, heads, head_dim] float32 (exact copy of the model-dtype
- *              query; query_is_16bit = 1 when that dtype is bf16/fp16)
+ *   query      [batch, heads, head_dim] in query_dtype (HS_DTYPE_*: the model
+ *              dtype; widened to float32 exactly, as the reference's .float())
  *   minimum[b], maximum[b]  per request [pages, kv_heads, head_dim] bounds in
  *              kv_dtype (RequestPages.minimum/maximum[layer], storage.py:193-206)
  *   page_counts host array [batch]: ceil(length / page_size)
@@ -91,8 +91,8 @@ int64_t hs_quest_workspace_bytes(int64_t batch, int64_t heads, int64_t max_pages
  *              channels in ascending order; ties go to the lower page.
  * `minimum`, `maximum` and `page_counts` are host arrays of device pointers / sizes.
  */
-int hs_quest_topk(const float* query, int64_t q_stride_b, int64_t q_stride_h,
-                  int32_t query_is_16bit, const void* const* minimum, const void* const* maximum,
+int hs_quest_topk(const void* query, int64_t q_stride_b, int64_t q_stride_h,
+                  int32_t query_dtype, const void* const* minimum, const void* const* maximum,
                   int32_t kv_dtype, const int64_t* page_counts, int64_t batch, int64_t heads,
                   int64_t kv_heads, int64_t head_dim, int64_t top, int32_t keep_sink,
                   int32_t* out_pages, int64_t out_stride_b, void* workspace,

@@ -132,7 +132,9 @@ class BatchedSparseDecode:
         if self.shared_selection:
             raise RuntimeError("a shared-selection decoder takes its pages from select_pages")
         B = self.batch
-        q = queries.float().contiguous()
+        q = queries if queries.dtype in (torch.float32, torch.bfloat16, torch.float16) else queries.float()
+        if q.stride(-1) != 1:  # read by the kernel in its dtype
+            q = q.contiguous()
         lib = _lib.load()
         s = stream.cuda_stream if stream is not None else _lib.stream_handle(self.device)
         key = tuple(map(id, minimums)) + tuple(map(id, maximums))
@@ -144,7 +146,7 @@ class BatchedSparseDecode:
         _, lo, hi = hit
         _lib.check(
             lib.hs_quest_topk(
-                q.data_ptr(), q.stride(0), q.stride(1), int(queries.dtype in (torch.bfloat16, torch.float16)),
+                q.data_ptr(), q.stride(0), q.stride(1), _lib.dtype_code(q.dtype),
                 lo, hi, _lib.dtype_code(minimums[0].dtype), self._count_arr, B, self.heads,
                 self.kv_heads, q.shape[2], self.top, int(self.keep_sink), self.pages.data_ptr(),
                 self.pages.stride(0), self.quest_ws.data_ptr(), self.quest_ws_bytes, s,

@@ -28,7 +28,8 @@ constexpr int UT = 1024;        // union builder threads
 constexpr int64_t UMAXPAGES = 65536;
 
 struct QuestArgs {
-  const float* q;               // [B, Hq, D] float32 (exact copy of the query)
+  const void* q;                // [B, Hq, D] in q_dtype (f32, bf16 or f16)
+  int q_dtype;
   int64_t q_sb, q_sh;
   const void* kmin[QMAXB];      // per request [pages, Hkv, D]
   const void* kmax[QMAXB];
@@ -40,6 +41,13 @@ struct QuestArgs {
   int32_t* pages;               // [B, Hq, top]
   int64_t p_sb;
 };
+
+// Query element i widened to fp32 (exact for every query dtype).
+__device__ __forceinline__ float query_value(const QuestArgs& a, int64_t i) {
+  if (a.q_dtype == HS_DTYPE_BF16) return load_elem<HS_DTYPE_BF16>(a.q, i);
+  if (a.q_dtype == HS_DTYPE_F16) return load_elem<HS_DTYPE_F16>(a.q, i);
+  return load_elem<HS_DTYPE_F32>(a.q, i);
+}
 
 template <int DT, bool FUSED>
 __global__ __launch_bounds__(QT) void quest_score_kernel(QuestArgs a) {
@@ -56,7 +64,7 @@ __global__ __launch_bounds__(QT) void quest_score_kernel(QuestArgs a) {
   const int64_t D = a.D;
   for (int64_t i = threadIdx.x; i < QHEADS * D; i += QT) {
     const int64_t hl = i / D, d = i - hl * D;
-    sq[i] = hl < nh ? a.q[b * a.q_sb + (h0 + hl) * a.q_sh + d] : 0.f;
+    sq[i] = hl < nh ? query_value(a, b * a.q_sb + (h0 + hl) * a.q_sh + d) : 0.f;
   }
   __syncthreads();
   const int64_t p = static_cast<int64_t>(blockIdx.x) * QT + threadIdx.x;
@@ -152,7 +160,7 @@ __global__ __launch_bounds__(QT) void quest_score_tile_kernel(QuestArgs a) {
   const int64_t h0 = kv * a.g + hc * QHEADS;
   for (int64_t i = threadIdx.x; i < QHEADS * D; i += QT) {
     const int64_t hl = i / D, d = i - hl * D;
-    sq[i] = hl < nh ? a.q[b * a.q_sb + (h0 + hl) * a.q_sh + d] : 0.f;
+    sq[i] = hl < nh ? query_value(a, b * a.q_sb + (h0 + hl) * a.q_sh + d) : 0.f;
   }
   int64_t npg = count - p0;
   if (npg > QS_PAGES) npg = QS_PAGES;
@@ -528,8 +536,8 @@ extern "C" int64_t hs_quest_workspace_bytes(int64_t batch, int64_t heads, int64_
   return ((batch * heads * max_pages * 4) + 255) & ~static_cast<int64_t>(255);
 }
 
-extern "C" int hs_quest_topk(const float* query, int64_t q_stride_b, int64_t q_stride_h,
-                             int32_t query_is_16bit, const void* const* minimum,
+extern "C" int hs_quest_topk(const void* query, int64_t q_stride_b, int64_t q_stride_h,
+                             int32_t query_dtype, const void* const* minimum,
                              const void* const* maximum, int32_t kv_dtype,
                              const int64_t* page_counts, int64_t batch, int64_t heads,
                              int64_t kv_heads, int64_t head_dim, int64_t top, int32_t keep_sink,
@@ -539,10 +547,12 @@ extern "C" int hs_quest_topk(const float* query, int64_t q_stride_b, int64_t q_s
                "invalid page budget or GQA shape");
   HS_CHECK_ARG(batch >= 1 && batch <= QMAXB, "quest batch must be in [1, %d]", QMAXB);
   HS_CHECK_ARG(valid_dtype(kv_dtype), "invalid dtype code %d", kv_dtype);
+  HS_CHECK_ARG(valid_dtype(query_dtype), "invalid query dtype code %d", query_dtype);
   HS_CHECK_ARG(head_dim >= 1 && head_dim <= 1024, "invalid head_dim");
   HS_CHECK_ARG(query && minimum && maximum && page_counts && out_pages, "null quest pointer");
   QuestArgs a{};
   a.q = query;
+  a.q_dtype = query_dtype;
   a.q_sb = q_stride_b;
   a.q_sh = q_stride_h;
   int64_t cmax = 1;
@@ -571,7 +581,9 @@ extern "C" int hs_quest_topk(const float* query, int64_t q_stride_b, int64_t q_s
   for (int64_t i = 0; i < batch; ++i) any_scored |= top < page_counts[i];
   if (any_scored) {
     const int64_t hchunks = ceil_div(a.g, QHEADS);
-    const bool fused = query_is_16bit && kv_dtype != HS_DTYPE_F32;
+    // 16-bit queries times 16-bit bounds: every product is exact in fp32, so an FMA
+    // rounds like the reference's product-then-sum
+    const bool fused = query_dtype != HS_DTYPE_F32 && kv_dtype != HS_DTYPE_F32;
     const int64_t epv = kv_dtype == HS_DTYPE_F32 ? 4 : 8;
     const int64_t row_bytes = head_dim * (kv_dtype == HS_DTYPE_F32 ? 4 : 2);
     bool aligned = true;

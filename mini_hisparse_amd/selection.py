@@ -193,7 +193,10 @@ def quest_topk(queries, minimums, maximums, lengths, page_size, top_pages, keep_
     if top_pages < 1 or heads % kv_heads:
         raise ValueError("invalid page budget or GQA shape")
     device = queries.device
-    q = queries.float().contiguous()
+    # read by the kernel in the model dtype (widened exactly, like the reference's .float())
+    q = queries if queries.dtype in (torch.float32, torch.bfloat16, torch.float16) else queries.float()
+    if q.stride(-1) != 1:
+        q = q.contiguous()
     counts = [ceil(length / page_size) for length in lengths]
     if any(c < 1 for c in counts):
         raise ValueError("cannot select pages of an empty history")
@@ -208,8 +211,7 @@ def quest_topk(queries, minimums, maximums, lengths, page_size, top_pages, keep_
     hi_ptrs = (ctypes_void_p_array(batch))(*[t.data_ptr() for t in maximums])
     count_arr = (_c_int64_array(batch))(*counts)
     status = lib.hs_quest_topk(
-        q.data_ptr(), q.stride(0), q.stride(1),
-        int(queries.dtype in (torch.bfloat16, torch.float16)),
+        q.data_ptr(), q.stride(0), q.stride(1), _lib.dtype_code(q.dtype),
         lo_ptrs, hi_ptrs, _lib.dtype_code(minimums[0].dtype), count_arr,
         batch, heads, kv_heads, dim, top_pages, int(bool(keep_sink)),
         pages.data_ptr(), pages.stride(0), workspace.data_ptr(), ws_bytes,
