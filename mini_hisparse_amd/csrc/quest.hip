@@ -365,6 +365,8 @@ struct UnionArgs {
   int32_t* ecount;       // [B, Hkv]
   int32_t* status;       // nonzero on overflow
   int64_t words;         // bitmap words of the longest history
+  int64_t maxcount;      // pages of the longest history
+  int use_map;           // rank -> page map in LDS (maxcount <= UMAPPAGES)
 };
 
 __device__ __forceinline__ bool head_has_page(const int32_t* row, int64_t k, int32_t p) {
@@ -384,14 +386,19 @@ __device__ __forceinline__ bool head_has_page(const int32_t* row, int64_t k, int
 // roles run side by side.  A group entry's head mask comes from an LDS array
 // indexed by the page's rank among the group's pages.
 constexpr int64_t UMAXMASK = 4096;  // group pages (g * top) with an LDS mask slot
+constexpr int64_t UMAPPAGES = 24576;  // longest history (pages) with an LDS rank -> page map
 
-// Dynamic LDS: four bitmaps of `a.words` words (longest history of the batch).
+// Dynamic LDS: four bitmaps of `a.words` words and a rank -> page map of
+// `a.maxcount` entries (longest history of the batch).  The positions and the
+// entry lists are written one output element per thread through that map, so
+// consecutive lanes store consecutive elements.
 __global__ __launch_bounds__(UT) void build_union_kernel(UnionArgs a) {
   extern __shared__ uint32_t union_lds[];
   uint32_t* ubits = union_lds;
   uint32_t* uprefix = ubits + a.words;
   uint32_t* gbits = uprefix + a.words;
   uint32_t* gprefix = gbits + a.words;
+  int32_t* rank_page = reinterpret_cast<int32_t*>(gprefix + a.words);  // [maxcount]
   __shared__ uint32_t gmask[UMAXMASK];
   __shared__ int32_t scan32[16];
   const int64_t b = blockIdx.y;
@@ -455,14 +462,24 @@ __global__ __launch_bounds__(UT) void build_union_kernel(UnionArgs a) {
       if (n > a.pos_cap) atomicOr(a.status, 1);
     }
     int32_t* pos = a.positions + b * a.pos_cap;
-    for (int64_t p = threadIdx.x; p < count; p += UT) {
-      if (!((ubits[p >> 5] >> (p & 31)) & 1u)) continue;
-      const int64_t base = rank_of(ubits, uprefix, p) * P;
-      const int64_t plen = p == count - 1 ? tail_len : P;
-      for (int64_t off = 0; off < plen; ++off)
-        if (base + off < a.pos_cap) pos[base + off] = static_cast<int32_t>(p * P + off);
+    const int64_t nw = n < a.pos_cap ? n : a.pos_cap;
+    if (a.use_map) {
+      for (int64_t p = threadIdx.x; p < count; p += UT)
+        if ((ubits[p >> 5] >> (p & 31)) & 1u) rank_page[rank_of(ubits, uprefix, p)] = static_cast<int32_t>(p);
+      __syncthreads();
+      // position i: token i % P of the (i / P)-th union page (the tail page is the last)
+      for (int64_t i = threadIdx.x; i < nw; i += UT)
+        pos[i] = static_cast<int32_t>(static_cast<int64_t>(rank_page[i / P]) * P + i % P);
+    } else {
+      for (int64_t p = threadIdx.x; p < count; p += UT) {
+        if (!((ubits[p >> 5] >> (p & 31)) & 1u)) continue;
+        const int64_t base = rank_of(ubits, uprefix, p) * P;
+        const int64_t plen = p == count - 1 ? tail_len : P;
+        for (int64_t off = 0; off < plen; ++off)
+          if (base + off < a.pos_cap) pos[base + off] = static_cast<int32_t>(p * P + off);
+      }
     }
-    for (int64_t i = n + threadIdx.x; i < a.pos_cap; i += UT) pos[i] = -1;
+    for (int64_t i = nw + threadIdx.x; i < a.pos_cap; i += UT) pos[i] = -1;
   } else if (part > a.Hkv) {
     // union columns of head h: its j-th token (its pages ascending, tail last)
     const int64_t h = part - a.Hkv - 1;
@@ -503,6 +520,20 @@ __global__ __launch_bounds__(UT) void build_union_kernel(UnionArgs a) {
     }
     int32_t* ec = a.ecol + (b * a.Hkv + kv) * a.ecap;
     uint32_t* em = a.emask + (b * a.Hkv + kv) * a.ecap;
+    if (masks_in_lds && a.use_map) {
+      for (int64_t p = threadIdx.x; p < count; p += UT)
+        if ((gbits[p >> 5] >> (p & 31)) & 1u) rank_page[rank_of(gbits, gprefix, p)] = static_cast<int32_t>(p);
+      __syncthreads();
+      // entry i: token i % P of the (i / P)-th group page, its union column and head mask
+      const int64_t ew = E < a.ecap ? E : a.ecap;
+      for (int64_t i = threadIdx.x; i < ew; i += UT) {
+        const int64_t r = i / P;
+        const int32_t p = rank_page[r];
+        ec[i] = static_cast<int32_t>(rank_of(ubits, uprefix, p) * P + i % P);
+        em[i] = gmask[r];
+      }
+      return;
+    }
     for (int64_t p = threadIdx.x; p < count; p += UT) {
       if (!((gbits[p >> 5] >> (p & 31)) & 1u)) continue;
       const int64_t grank = rank_of(gbits, gprefix, p);
@@ -688,8 +719,18 @@ extern "C" int hs_build_union(const int32_t* pages, int64_t p_stride_b, int64_t 
   int64_t max_count = 1;
   for (int64_t i = 0; i < batch; ++i) max_count = std::max(max_count, ceil_div(lengths[i], page_size));
   a.words = (max_count + 31) / 32;
+  a.maxcount = max_count;
+  a.use_map = max_count <= UMAPPAGES;
+  const size_t lds = static_cast<size_t>((4 * a.words + (a.use_map ? max_count : 0)) * 4);
+  static bool lds_attr = false;
+  if (!lds_attr) {  // up to 4 * 768 + 24576 words of dynamic LDS
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(build_union_kernel),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, 128 * 1024);
+    (void)hipGetLastError();
+    lds_attr = true;
+  }
   hipLaunchKernelGGL(build_union_kernel, dim3(static_cast<unsigned>(kv_heads + 1 + heads), static_cast<unsigned>(batch)),
-                     dim3(UT), static_cast<size_t>(4 * a.words * 4), stream, a);
+                     dim3(UT), lds, stream, a);
   HS_CHECK_LAUNCH("union builder");
   return HS_OK;
 }

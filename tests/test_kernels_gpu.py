@@ -243,7 +243,17 @@ def test_quest_reference_known_answer(gpu):
 
 
 # -------------------------------------------------------------- union builder
-@pytest.mark.parametrize("pages,P,kv,g,top,length", [(300, 16, 2, 4, 16, None), (77, 7, 2, 3, 5, 535), (10, 16, 2, 2, 12, 150), (4096, 16, 8, 8, 64, None)])
+@pytest.mark.parametrize(
+    "pages,P,kv,g,top,length",
+    [
+        (300, 16, 2, 4, 16, None),
+        (77, 7, 2, 3, 5, 535),
+        (10, 16, 2, 2, 12, 150),
+        (4096, 16, 8, 8, 64, None),
+        (2000, 16, 1, 8, 600, None),  # a group selects > 4096 pages: head masks by binary search
+        (30000, 16, 2, 2, 8, None),  # history beyond the LDS rank -> page map: per-page writes
+    ],
+)
 def test_union_builder_matches_host_adapter(gpu, pages, P, kv, g, top, length):
     from mini_hisparse_amd.selection import quest_selection
 
