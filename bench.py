@@ -53,6 +53,9 @@ def parse_args():
                         "by default a single request group runs every stage on the compute stream")
     p.add_argument("--no-cpu-baseline", action="store_true", help="skip the CPU oracle leg")
     p.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU sample work")
+    p.add_argument("--attention-sweep", action="store_true",
+                   help="print the group attention's duration against its work (fixed cost and "
+                        "incremental rate of both schedules) as a markdown table and exit")
     p.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                    help="summarise two rocprofv3 --pmc runs of this script (FETCH_SIZE, WRITE_SIZE) "
                         "into profiles/microbench_pmc.txt and exit")
@@ -308,6 +311,85 @@ def attention_ceilings(torch, w, nbytes, reps=10):
                 times.append(e0.elapsed_time(e1))
             out[f"{name}_{label}_GBps"] = nbytes / (float(np.median(times)) * 1e-3) / 1e9
     return out
+
+
+def attention_sweep(torch, device, reps=8):
+    """Duration of hs_attend_groups against its work at the microbench head shape (B=8,
+    8 KV heads of 8 query heads, head_dim 128, bf16): every group reads the same number of
+    entries (random pages of a 1.5 GB pool), from 32 to 6144 per group; split and balanced
+    schedules (HS_ATTEND_SCHED); warm (back to back) and cold (after reading 1 GiB of other
+    data).  A long kernel runs before each timed launch so the host is ahead of the GPU and
+    the events time the GPU only.  Fits duration = fixed + bytes / rate over the points of
+    >= 1536 entries per group.  Prints a markdown table."""
+    import os
+
+    from mini_hisparse_amd.row_index import GroupEntries
+    from mini_hisparse_amd.row_kernels import attend_groups
+
+    P, Hkv, g, D, B, blocks, cap = 16, 8, 8, 128, 8, 24000, 8192
+    cfg = type("Cfg", (), dict(page_size=P, kv_heads=Hkv, head_dim=D))
+    gen = torch.Generator(device=device).manual_seed(5)
+    pool = torch.randn((blocks, 2, P, Hkv, D), generator=gen, device=device).to(torch.bfloat16)
+    q = torch.randn((B, Hkv * g, D), generator=gen, device=device).to(torch.bfloat16)
+    other = torch.empty(1 << 30, dtype=torch.uint8, device=device)
+    rng = np.random.default_rng(5)
+    counts_list = (32, 128, 512, 1024, 1536, 3072, 6144)
+    union = np.empty((B, cap), np.int64)
+    for b in range(B):
+        pages = np.sort(rng.choice(blocks, cap // P, replace=False))
+        union[b] = (pages[:, None] * P + np.arange(P)[None, :]).reshape(-1)
+    union_t = torch.from_numpy(union).to(device)
+    cols = torch.arange(cap, dtype=torch.int32, device=device).expand(B, Hkv, cap).contiguous()
+    masks = torch.from_numpy(rng.integers(1, 1 << g, size=(B, Hkv, cap)).astype(np.int32)).to(device)
+    results = {}
+    saved = os.environ.get("HS_ATTEND_SCHED")
+    try:
+        for schedule, env in (("split", "0"), ("balanced", "1")):
+            os.environ["HS_ATTEND_SCHED"] = env
+            for c in counts_list:
+                counts = torch.full((B, Hkv), c, dtype=torch.int32, device=device)
+                entries = GroupEntries(cols, masks, counts, cap)
+                run = lambda: attend_groups(q, pool, union_t, entries, cfg)
+                run()
+                for state in ("warm", "cold"):
+                    times = []
+                    for _ in range(reps):
+                        if state == "cold":
+                            other.view(torch.int64).sum()
+                        else:
+                            run()
+                        torch.cuda._sleep(1_000_000)  # keeps the GPU busy while the host enqueues
+                        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                        e0.record()
+                        run()
+                        e1.record()
+                        torch.cuda.synchronize()
+                        times.append(e0.elapsed_time(e1) * 1e3)
+                    results[(schedule, c, state)] = float(np.median(times))
+    finally:
+        if saved is None:
+            os.environ.pop("HS_ATTEND_SCHED", None)
+        else:
+            os.environ["HS_ATTEND_SCHED"] = saved
+    mb = {c: B * Hkv * c * 512 / 1e6 for c in counts_list}
+    lines = ["| entries / group | MB | split warm µs | split cold µs | balanced warm µs | balanced cold µs |",
+             "|---|---|---|---|---|---|"]
+    for c in counts_list:
+        r = [results[(s, c, st)] for s in ("split", "balanced") for st in ("warm", "cold")]
+        lines.append(f"| {c} | {mb[c]:.1f} | " + " | ".join(f"{t:.1f}" for t in r) + " |")
+    # The balanced schedule spreads any total over every workgroup, so its duration is
+    # linear in the bytes; the split schedule's chunks are sized for the capacity (8192
+    # entries), which leaves workgroups empty below it, so no line fits it.
+    lines.append("")
+    lines.append("| balanced schedule, fit over >= 1536 entries / group | fixed µs | incremental rate TB/s |")
+    lines.append("|---|---|---|")
+    big = [c for c in counts_list if c >= 1536]
+    for st in ("warm", "cold"):
+        x = np.array([mb[c] for c in big])
+        y = np.array([results[("balanced", c, st)] for c in big])
+        slope, fixed = np.polyfit(x, y, 1)
+        lines.append(f"| {st} | {fixed:.1f} | {1.0 / slope:.2f} |")
+    print("\n".join(lines))
 
 
 def algorithmic_bytes(w, torch):
@@ -652,6 +734,9 @@ def main():
         print(json.dumps({"error": "no ROCm GPU visible"}))
         sys.exit(1)
     device = torch.device("cuda:0")
+    if args.attention_sweep:
+        attention_sweep(torch, device)
+        return
     if args.workload != "microbench":
         run_model_workload(args, torch, device)
         return

@@ -51,9 +51,10 @@ struct AttendArgs {
   int64_t B, Hq, g;
   int64_t splits, chunk;
   float scale;
-  float* part_m;  // [B, Hq, splits]
-  float* part_l;  // [B, Hq, splits]
-  float* part_o;  // [B, Hq, splits, D]
+  float* part_m;  // [B, Hq, splits], or [slots, 16] when scheduled
+  float* part_l;  // like part_m
+  float* part_o;  // [B, Hq, splits, D], or [slots, 16, D] when scheduled
+  int32_t* sched; // T(0 .. B * Hkv) of the scheduled group kernel
 };
 
 __device__ __forceinline__ int64_t entry_count(const AttendArgs& a, int64_t b, int64_t k) {
@@ -118,12 +119,14 @@ __device__ __forceinline__ float from_bits(unsigned short v) {
   else return f16_bits_to_f32(v);
 }
 
-// One workgroup (4 waves) per (split, KV head x head chunk, request).  The
-// split's entries (K element offset, head mask) are staged in LDS once with
-// two batched rounds of loads (entry lists, then physical rows); each wave
-// then walks tiles w, w+4, ... of 32 entries with two register buffers used in
-// turn: the loads of tile t+4 are in flight while tile t computes, and no
-// buffer is copied (a copy would make the compiler wait for the loads).
+// One workgroup (8 waves; 4 for head_dim 256) per (split, KV head x head chunk,
+// request), or per slot of the balanced schedule below.  The split's entries
+// (K element offset, head mask) are staged in LDS once with two batched rounds
+// of loads (entry columns with the group's count and the query, then physical
+// rows); each wave then walks tiles w, w+8, ... of 32 entries with two register
+// buffers used in turn: the loads of tile t+8 are in flight while tile t
+// computes, and no buffer is copied (a copy would make the compiler wait for
+// the loads).
 constexpr int ACH = 2048;        // entries per workgroup (chunk) of the MFMA kernel
 
 // Waves per workgroup of the MFMA kernel: 8 (4 for head_dim 256, whose V tiles
@@ -190,7 +193,106 @@ __device__ __forceinline__ int64_t entry_total(const AttendArgs& a, int64_t b, i
   }
 }
 
-template <int DT, int DP, int MODE>
+// ---- balanced schedule of the group attention ----------------------------------
+// The entry lists of the (request, KV head) groups differ in length and their
+// lengths live on the device.  Rather than splitting every group for the
+// longest possible list (which leaves the splits of short lists nearly empty
+// while the others run full), every workgroup of the scheduled kernel derives
+// the same schedule from the entry counts: the smallest chunk ch (a multiple of
+// 32, at least ATT_MIN_CHUNK, at most ACH) for which cutting each group's head
+// chunk into s_i = ceil(c_i / ch) workgroups needs at most ATT_SLOTS
+// workgroups, i.e. one round on a 256-CU gfx950 (the kernel's LDS admits one
+// workgroup per CU).  Group i's workgroups are T(i) + hc * s_i + j (head chunk
+// hc, j < s_i), each with an even share of the group's entries rounded up to
+// 32.  The workgroup index is the slot of its split-K partial; T is written to
+// the workspace for the merge.
+constexpr int ATT_SLOTS = 256;
+constexpr int ATT_MIN_CHUNK = 128;
+constexpr int64_t ATT_MAX_GROUPS = 4096;
+
+struct Assignment {
+  int32_t group;  // b * Hkv + k, or -1: this workgroup has no work
+  int32_t hc, e0, cnt;
+};
+
+__device__ __forceinline__ int32_t wave_total(int32_t v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+// c: the groups' clamped entry counts in LDS.  Every lane of the calling wave
+// takes part; `table` (or null) receives T(0..ngroups).
+__device__ Assignment balanced_assignment(const int32_t* c, int32_t ngroups, int32_t hcs, int32_t w,
+                                          int32_t* table) {
+  const int lane = threadIdx.x & 63;
+  const int32_t per = (ngroups + 63) / 64;
+  const int32_t i0 = lane * per < ngroups ? lane * per : ngroups;
+  const int32_t i1 = i0 + per < ngroups ? i0 + per : ngroups;
+  int32_t e = 0;
+  for (int32_t i = i0; i < i1; ++i) e += c[i];
+  e = wave_total(e);
+  auto workgroups = [&](int32_t ch) {
+    int32_t s = 0;
+    for (int32_t i = i0; i < i1; ++i) s += (c[i] + ch - 1) / ch;
+    return wave_total(s) * hcs;
+  };
+  int32_t lo = (hcs * e + ATT_SLOTS - 1) / ATT_SLOTS;
+  if (lo < ATT_MIN_CHUNK) lo = ATT_MIN_CHUNK;
+  int32_t mlo = (lo + 31) / 32, mhi = ACH / 32;
+  if (mlo >= mhi || workgroups(ACH) > ATT_SLOTS) {
+    mlo = mhi;  // one round is not possible: chunks of ACH over several rounds
+  } else {
+    while (mlo < mhi) {  // smallest m with workgroups(32 m) <= ATT_SLOTS (true at mhi)
+      const int32_t mid = (mlo + mhi) / 2;
+      if (workgroups(32 * mid) <= ATT_SLOTS) mhi = mid;
+      else mlo = mid + 1;
+    }
+  }
+  const int32_t ch = 32 * mlo;
+  int32_t mine = 0;
+  for (int32_t i = i0; i < i1; ++i) mine += hcs * ((c[i] + ch - 1) / ch);
+  const int32_t incl = wave_inclusive_sum(mine), excl = incl - mine;
+  if (table) {
+    int32_t t = excl;
+    for (int32_t i = i0; i < i1; ++i) {
+      table[i] = t;
+      t += hcs * ((c[i] + ch - 1) / ch);
+    }
+    if (lane == 63) table[ngroups] = incl;
+  }
+  const bool owner = excl <= w && w < incl;
+  const uint64_t owners = __ballot(owner);
+  Assignment r{-1, 0, 0, 0};
+  if (owners == 0) return r;
+  const int src = __ffsll(static_cast<unsigned long long>(owners)) - 1;
+  int32_t gi = 0, gl = 0;
+  if (owner) {
+    int32_t t = excl;
+    for (int32_t i = i0; i < i1; ++i) {
+      const int32_t n = hcs * ((c[i] + ch - 1) / ch);
+      if (w < t + n) {
+        gi = i;
+        gl = w - t;
+        break;
+      }
+      t += n;
+    }
+  }
+  gi = __shfl(gi, src, 64);
+  gl = __shfl(gl, src, 64);
+  const int32_t ci = c[gi];
+  const int32_t s = (ci + ch - 1) / ch;
+  const int32_t hc = gl / s, j = gl - hc * s;
+  const int32_t chunk = ((ci + s - 1) / s + 31) / 32 * 32;  // <= ch, and (s - 1) * chunk < ci
+  r.group = gi;
+  r.hc = hc;
+  r.e0 = j * chunk;
+  r.cnt = ci - r.e0 < chunk ? ci - r.e0 : chunk;
+  return r;
+}
+
+template <int DT, int DP, int MODE, bool SCHED>
 __global__ __launch_bounds__(64 * attend_waves(DP)) void attend_mfma_kernel(AttendArgs a) {
   constexpr int AW = attend_waves(DP);
   constexpr int NTH = 64 * AW;
@@ -213,56 +315,98 @@ __global__ __launch_bounds__(64 * attend_waves(DP)) void attend_mfma_kernel(Atte
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int j = lane >> 4, c = lane & 15;
   const int64_t split = blockIdx.x;
-  const int64_t k = blockIdx.y / a.head_chunks;
-  const int hchunk = blockIdx.y % a.head_chunks;
-  const int64_t b = blockIdx.z;
+  int64_t k, b, e0;
+  int hchunk, cnt;
+  if constexpr (SCHED) {
+    // group entry counts in the (not yet used) V-tile buffer, then the schedule
+    int32_t* s_cnt = reinterpret_cast<int32_t*>(smem);
+    const int32_t ng = static_cast<int32_t>(a.B * a.Hkv);
+    for (int32_t i = threadIdx.x; i < ng; i += NTH) {
+      const int64_t e = a.ecount[i];
+      s_cnt[i] = static_cast<int32_t>(e < 0 ? 0 : (e > a.emax ? a.emax : e));
+    }
+    __syncthreads();
+    const Assignment asg = balanced_assignment(s_cnt, ng, a.head_chunks, static_cast<int32_t>(blockIdx.x),
+                                               blockIdx.x == 0 && wave == 0 ? a.sched : nullptr);
+    if (asg.group < 0) return;  // the same for every wave: no barrier is left waiting
+    b = asg.group / a.Hkv;
+    k = asg.group - b * a.Hkv;
+    hchunk = asg.hc;
+    e0 = asg.e0;
+    cnt = asg.cnt;
+  } else {
+    k = blockIdx.y / a.head_chunks;
+    hchunk = blockIdx.y % a.head_chunks;
+    b = blockIdx.z;
+    e0 = split * a.chunk;
+    cnt = 0;  // set below, once the group's entry count is known
+  }
+  // split-K partial of head `hl` of the group (16 * hchunk <= hl < 16 * hchunk + 16)
+  auto partial_index = [&](int hl) -> int64_t {
+    if constexpr (SCHED) return static_cast<int64_t>(blockIdx.x) * 16 + (hl - 16 * hchunk);
+    else return (b * a.Hq + k * a.g + hl) * a.splits + split;
+  };
   const int hh = 16 * hchunk + c;  // head index within the group owned by this lane
   const int64_t D = a.D, P = a.P, Hkv = a.Hkv;
   const unsigned short* pool = static_cast<const unsigned short*>(a.pool);
   unsigned short* vs = vs_all + wave * 32 * RS;
 
-  const int64_t E = entry_total<MODE>(a, b, k);
-  const int64_t e0 = split * a.chunk;
-  int64_t e1 = e0 + a.chunk;
-  if (e1 > E) e1 = E;
-  const int cnt = e1 > e0 ? static_cast<int>(e1 - e0) : 0;
-  if (cnt == 0) {  // empty split: a partial that the merge ignores
-    for (int idx = threadIdx.x; idx < 16 * DP; idx += NTH) {
-      const int head = idx / DP, d = idx % DP;
-      const int hl = 16 * hchunk + head;
-      if (hl >= a.g || d >= D) continue;
-      const int64_t pidx = (b * a.Hq + k * a.g + hl) * a.splits + split;
-      if (d == 0) {
-        a.part_m[pidx] = -INFINITY;
-        a.part_l[pidx] = 0.f;
-      }
-      a.part_o[pidx * D + d] = 0.f;
-    }
-    return;
+  // Q^T fragments (lane holds Q[head hh][d = 32kk + 8j .. +8]): they depend only
+  // on (b, k, hchunk), so their loads go out with the first entry loads.
+  u32x4 qf[KK];
+  const unsigned short* qrow = static_cast<const unsigned short*>(a.q) + b * a.q_sb + k * a.g * a.q_sh;
+#pragma unroll
+  for (int kk = 0; kk < KK; ++kk) {
+    const int d0 = 32 * kk + 8 * j;
+    const bool ok = hh < a.g && d0 < D;
+    const u32x4 v = load16(ok ? qrow + hh * a.q_sh + d0 : qrow);
+    qf[kk] = ok ? v : u32x4{0u, 0u, 0u, 0u};
   }
-  {
-    int64_t ph[SPT];
-    uint32_t mk[SPT];
-    stage_entries<MODE, NTH, SPT>(a, b, k, e0, cnt, ph, mk);
+
+  int64_t ph[SPT];
+  uint32_t mk[SPT];
+  if constexpr (MODE == MODE_GROUPS && !SCHED) {
+    // The split's entry columns and masks are loaded together with the group's
+    // entry count (one round of loads instead of two): every split starts below
+    // emax, so entries e0 .. e0 + min(chunk, emax - e0) - 1 are in bounds.
+    int32_t col[SPT];
+    const int64_t lim = a.emax - e0 < a.chunk ? a.emax - e0 : a.chunk;
+    const int64_t base = b * a.e_sb + k * a.e_sk + e0;
 #pragma unroll
     for (int s = 0; s < SPT; ++s) {
       const int i = threadIdx.x + s * NTH;
-      s_koff[i] = ph[s] >= 0 ? k_offset(ph[s], k, P, Hkv, D) : -1;
-      s_mask[i] = mk[s];
+      const int64_t ic = i < lim ? i : 0;
+      col[s] = a.ecol[base + ic];
+      mk[s] = a.emask[base + ic];
     }
-  }
-
-  // Q^T fragments: lane holds Q[head hh][d = 32kk + 8j .. +8]
-  u32x4 qf[KK];
-  const unsigned short* qrow = static_cast<const unsigned short*>(a.q) + b * a.q_sb + k * a.g * a.q_sh;
-  {
+    const int64_t E = entry_total<MODE>(a, b, k);
+    cnt = E > e0 ? static_cast<int>(E - e0 < a.chunk ? E - e0 : a.chunk) : 0;
+    // no branch on cnt here: a conditional block would let the compiler sink the
+    // column loads below the wait for the count
 #pragma unroll
-    for (int kk = 0; kk < KK; ++kk) {
-      const int d0 = 32 * kk + 8 * j;
-      const bool ok = hh < a.g && d0 < D;
-      const u32x4 v = load16(ok ? qrow + hh * a.q_sh + d0 : qrow);
-      qf[kk] = ok ? v : u32x4{0u, 0u, 0u, 0u};
+    for (int s = 0; s < SPT; ++s) {
+      const int i = threadIdx.x + s * NTH;
+      const bool ok = i < cnt && col[s] >= 0;
+      const int64_t pv = a.uphys[b * a.u_sb + (ok ? col[s] : 0)];
+      ph[s] = ok && pv >= 0 && pv < a.pool_rows ? pv : -1;
+      if (ph[s] < 0) mk[s] = 0u;
     }
+  } else if constexpr (!SCHED) {
+    const int64_t E = entry_total<MODE>(a, b, k);
+    cnt = E > e0 ? static_cast<int>(E - e0 < a.chunk ? E - e0 : a.chunk) : 0;
+    stage_entries<MODE, NTH, SPT>(a, b, k, e0, cnt, ph, mk);
+  } else {
+    stage_entries<MODE, NTH, SPT>(a, b, k, e0, cnt, ph, mk);
+  }
+  // An empty split (cnt == 0, split schedule only) runs no tile and writes the
+  // partial m = -inf, l = 0, o = 0 that the merge skips.  It takes the common
+  // path on purpose: an early exit here would let the compiler sink every
+  // other load of the prologue below the wait for the entry count.
+#pragma unroll
+  for (int s = 0; s < SPT; ++s) {
+    const int i = threadIdx.x + s * NTH;
+    s_koff[i] = ph[s] >= 0 ? k_offset(ph[s], k, P, Hkv, D) : -1;
+    s_mask[i] = mk[s];
   }
 
   f32x4 acc[NT];
@@ -437,8 +581,7 @@ __global__ __launch_bounds__(64 * attend_waves(DP)) void attend_mfma_kernel(Atte
         O += f * mo[(w * 16 + head) * DP + d];
       }
     }
-    const int64_t h = k * a.g + hl;
-    const int64_t pidx = (b * a.Hq + h) * a.splits + split;
+    const int64_t pidx = partial_index(hl);
     if (d == 0) {
       a.part_m[pidx] = M;
       a.part_l[pidx] = L;
@@ -509,25 +652,63 @@ __global__ __launch_bounds__(64) void attend_valu_kernel(AttendArgs a) {
 }
 
 // Combine split partials: out = sum_s e^(m_s-M) o_s / sum_s e^(m_s-M) l_s, 0 if empty.
+// Split schedule: head h's partials are (b * Hq + h) * splits + s.  Scheduled
+// group kernel (table != null): head hl of KV head k's group owns the slots
+// T(i) + (hl / 16) * n + s, s < n = (T(i + 1) - T(i)) / head_chunks, i = b * Hkv + k,
+// and its partial in slot t is t * 16 + hl % 16.
 template <int DT>
 __global__ __launch_bounds__(256) void attend_merge_kernel(const float* part_m, const float* part_l,
                                                             const float* part_o, int64_t splits,
-                                                            int64_t Hq, int64_t D, void* out,
-                                                            int64_t o_sb, int64_t o_sh) {
+                                                            const int32_t* table, int64_t Hkv, int64_t g,
+                                                            int64_t head_chunks, int64_t Hq, int64_t D,
+                                                            void* out, int64_t o_sb, int64_t o_sh) {
   const int64_t h = blockIdx.x, b = blockIdx.y;
-  const int64_t base = (b * Hq + h) * splits;
-  float M = -INFINITY;
-  for (int64_t s = 0; s < splits; ++s) M = fmaxf(M, part_m[base + s]);
+  int64_t base, stride, n;
+  if (table) {
+    const int64_t k = h / g, hl = h - k * g, i = b * Hkv + k;
+    const int64_t t0 = table[i];
+    n = (table[i + 1] - t0) / head_chunks;
+    base = (t0 + (hl / 16) * n) * 16 + hl % 16;
+    stride = 16;
+  } else {
+    base = (b * Hq + h) * splits;
+    stride = 1;
+    n = splits;
+  }
+  // Partials are read MS at a time, every load issued before any is used (one
+  // round of loads per MS splits); chunks after the first rescale the running
+  // sums, so for n <= MS the arithmetic is a plain max, then sums in split order.
+  constexpr int MS = 16;
   for (int64_t d = threadIdx.x; d < D; d += blockDim.x) {
-    float L = 0.f, O = 0.f;
-    if (M != -INFINITY) {
-      for (int64_t s = 0; s < splits; ++s) {
-        const float ms = part_m[base + s];
-        if (ms == -INFINITY) continue;
-        const float f = __expf(ms - M);
-        L += f * part_l[base + s];
-        O += f * part_o[(base + s) * D + d];
+    float M = -INFINITY, L = 0.f, O = 0.f;
+    for (int64_t s0 = 0; s0 < n; s0 += MS) {
+      float ms[MS], ls[MS], os[MS];
+#pragma unroll
+      for (int u = 0; u < MS; ++u) {
+        const bool ok = s0 + u < n;
+        const int64_t pi = base + (ok ? s0 + u : s0) * stride;  // s0 < n: in bounds
+        const float mv = part_m[pi], lv = part_l[pi], ov = part_o[pi * D + d];
+        ms[u] = ok ? mv : -INFINITY;
+        ls[u] = lv;
+        os[u] = ov;
       }
+      float Mc = M;
+#pragma unroll
+      for (int u = 0; u < MS; ++u) Mc = fmaxf(Mc, ms[u]);
+      if (Mc == -INFINITY) continue;
+      if (M != -INFINITY && M != Mc) {
+        const float r = __expf(M - Mc);
+        L *= r;
+        O *= r;
+      }
+#pragma unroll
+      for (int u = 0; u < MS; ++u) {
+        if (ms[u] == -INFINITY) continue;
+        const float f = __expf(ms[u] - Mc);
+        L += f * ls[u];
+        O += f * os[u];
+      }
+      M = Mc;
     }
     store_elem<DT>(out, b * o_sb + h * o_sh + d, L > 0.f ? O / L : 0.f);
   }
@@ -578,6 +759,8 @@ struct Plan {
   int dp;
   int head_chunks;
   int64_t splits, chunk;
+  bool sched;    // the group attention may use the balanced schedule
+  int64_t grid;  // its workgroups (slots)
 };
 
 static Plan plan_attend(int dtype, int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int64_t max_entries) {
@@ -601,6 +784,12 @@ static Plan plan_attend(int dtype, int64_t B, int64_t Hq, int64_t Hkv, int64_t D
     p.chunk = chunk;
     p.splits = ceil_div(max_entries, p.chunk);
     if (p.splits < 1) p.splits = 1;
+    // the scheduled group kernel is possible: counts held as int32, the count
+    // table fits the V-tile buffer
+    const int64_t ng = B * Hkv;
+    p.sched = ng <= ATT_MAX_GROUPS && ng * p.head_chunks * max_entries < (int64_t{1} << 31);
+    const int64_t rounds = ng * p.head_chunks * ceil_div(max_entries, ACH);
+    p.grid = rounds > ATT_SLOTS ? rounds : ATT_SLOTS;
   } else {
     p.dp = 0;
     p.head_chunks = 1;
@@ -616,41 +805,61 @@ static Plan plan_attend(int dtype, int64_t B, int64_t Hq, int64_t Hkv, int64_t D
   return p;
 }
 
-static int64_t workspace_for(const Plan& p, int64_t B, int64_t Hq, int64_t D) {
+// Bytes of the partials [n] m, [n] l, [n, D] o (+ the slot table when scheduled).
+static int64_t workspace_split(const Plan& p, int64_t B, int64_t Hq, int64_t D) {
   const int64_t n = B * Hq * p.splits;
   return (2 * n + n * D) * 4 + 256;
 }
+static int64_t workspace_sched(const Plan& p, int64_t B, int64_t Hkv, int64_t D) {
+  const int64_t n = p.grid * 16;
+  return (2 * n + n * D) * 4 + (B * Hkv + 1) * 4 + 256;
+}
+// Either schedule may run on a workspace sized by hs_attend_workspace_bytes.
+static int64_t workspace_for(const Plan& p, int64_t B, int64_t Hq, int64_t Hkv, int64_t D) {
+  const int64_t split = workspace_split(p, B, Hq, D);
+  const int64_t sched = p.sched ? workspace_sched(p, B, Hkv, D) : 0;
+  return split > sched ? split : sched;
+}
 
-template <int DT, int MODE>
+template <int DT, int MODE, bool SCHED>
 static void launch_mfma_mode(const Plan& p, const AttendArgs& a, hipStream_t s) {
   dim3 grid(static_cast<unsigned>(p.splits), static_cast<unsigned>(a.Hkv * p.head_chunks),
             static_cast<unsigned>(a.B));
+  if (SCHED) grid = dim3(static_cast<unsigned>(p.grid));
   switch (p.dp) {
-    case 32: hipLaunchKernelGGL((attend_mfma_kernel<DT, 32, MODE>), grid, dim3(64 * attend_waves(32)), 0, s, a); break;
-    case 64: hipLaunchKernelGGL((attend_mfma_kernel<DT, 64, MODE>), grid, dim3(64 * attend_waves(64)), 0, s, a); break;
-    case 128: hipLaunchKernelGGL((attend_mfma_kernel<DT, 128, MODE>), grid, dim3(64 * attend_waves(128)), 0, s, a); break;
-    default: hipLaunchKernelGGL((attend_mfma_kernel<DT, 256, MODE>), grid, dim3(64 * attend_waves(256)), 0, s, a); break;
+    case 32: hipLaunchKernelGGL((attend_mfma_kernel<DT, 32, MODE, SCHED>), grid, dim3(64 * attend_waves(32)), 0, s, a); break;
+    case 64: hipLaunchKernelGGL((attend_mfma_kernel<DT, 64, MODE, SCHED>), grid, dim3(64 * attend_waves(64)), 0, s, a); break;
+    case 128: hipLaunchKernelGGL((attend_mfma_kernel<DT, 128, MODE, SCHED>), grid, dim3(64 * attend_waves(128)), 0, s, a); break;
+    default: hipLaunchKernelGGL((attend_mfma_kernel<DT, 256, MODE, SCHED>), grid, dim3(64 * attend_waves(256)), 0, s, a); break;
   }
 }
 
 template <int DT>
 static void launch_mfma(const Plan& p, const AttendArgs& a, hipStream_t s) {
-  if (a.mode == MODE_GROUPS) launch_mfma_mode<DT, MODE_GROUPS>(p, a, s);
-  else if (a.mode == MODE_SHARED) launch_mfma_mode<DT, MODE_SHARED>(p, a, s);
-  else launch_mfma_mode<DT, MODE_ROWS>(p, a, s);
+  if (a.mode == MODE_GROUPS && a.sched) launch_mfma_mode<DT, MODE_GROUPS, true>(p, a, s);
+  else if (a.mode == MODE_GROUPS) launch_mfma_mode<DT, MODE_GROUPS, false>(p, a, s);
+  else if (a.mode == MODE_SHARED) launch_mfma_mode<DT, MODE_SHARED, false>(p, a, s);
+  else launch_mfma_mode<DT, MODE_ROWS, false>(p, a, s);
 }
 
 static int run_attend(int dtype, AttendArgs a, int64_t max_entries, void* out, int64_t o_sb,
                       int64_t o_sh, void* ws, int64_t ws_bytes, hipStream_t stream) {
   Plan p = plan_attend(dtype, a.B, a.Hq, a.Hkv, a.D, max_entries);
-  const int64_t need = workspace_for(p, a.B, a.Hq, a.D);
+  // The split schedule is the default: its first loads (entry count, columns,
+  // query) go out in one round, which the balanced schedule cannot do (it needs
+  // every count first).  HS_ATTEND_SCHED=1 selects the balanced schedule, which
+  // pays off when the entry lists are much shorter than max_entries.
+  const char* sched_env = getenv("HS_ATTEND_SCHED");
+  const bool sched = p.mfma && p.sched && a.mode == MODE_GROUPS && sched_env && atoi(sched_env) == 1;
+  const int64_t need = sched ? workspace_sched(p, a.B, a.Hkv, a.D) : workspace_split(p, a.B, a.Hq, a.D);
   HS_CHECK_ARG(ws != nullptr && ws_bytes >= need, "attention workspace too small: need %lld bytes",
                static_cast<long long>(need));
-  const int64_t n = a.B * a.Hq * p.splits;
+  const int64_t n = sched ? p.grid * 16 : a.B * a.Hq * p.splits;
   float* base = static_cast<float*>(ws);
   a.part_m = base;
   a.part_l = base + n;
   a.part_o = base + 2 * n;
+  a.sched = sched ? reinterpret_cast<int32_t*>(base + 2 * n + n * a.D) : nullptr;
   a.splits = p.splits;
   a.chunk = p.chunk;
   a.head_chunks = p.head_chunks;
@@ -667,12 +876,16 @@ static int run_attend(int dtype, AttendArgs a, int64_t max_entries, void* out, i
   HS_CHECK_LAUNCH("attention");
   dim3 mgrid(static_cast<unsigned>(a.Hq), static_cast<unsigned>(a.B));
   const unsigned mthreads = a.D <= 64 ? 64 : (a.D <= 128 ? 128 : 256);
+  const int64_t hcs = a.head_chunks;
   if (dtype == HS_DTYPE_F32)
-    hipLaunchKernelGGL((attend_merge_kernel<HS_DTYPE_F32>), mgrid, dim3(mthreads), 0, stream, a.part_m, a.part_l, a.part_o, p.splits, a.Hq, a.D, out, o_sb, o_sh);
+    hipLaunchKernelGGL((attend_merge_kernel<HS_DTYPE_F32>), mgrid, dim3(mthreads), 0, stream, a.part_m, a.part_l,
+                       a.part_o, p.splits, a.sched, a.Hkv, a.g, hcs, a.Hq, a.D, out, o_sb, o_sh);
   else if (dtype == HS_DTYPE_BF16)
-    hipLaunchKernelGGL((attend_merge_kernel<HS_DTYPE_BF16>), mgrid, dim3(mthreads), 0, stream, a.part_m, a.part_l, a.part_o, p.splits, a.Hq, a.D, out, o_sb, o_sh);
+    hipLaunchKernelGGL((attend_merge_kernel<HS_DTYPE_BF16>), mgrid, dim3(mthreads), 0, stream, a.part_m, a.part_l,
+                       a.part_o, p.splits, a.sched, a.Hkv, a.g, hcs, a.Hq, a.D, out, o_sb, o_sh);
   else
-    hipLaunchKernelGGL((attend_merge_kernel<HS_DTYPE_F16>), mgrid, dim3(mthreads), 0, stream, a.part_m, a.part_l, a.part_o, p.splits, a.Hq, a.D, out, o_sb, o_sh);
+    hipLaunchKernelGGL((attend_merge_kernel<HS_DTYPE_F16>), mgrid, dim3(mthreads), 0, stream, a.part_m, a.part_l,
+                       a.part_o, p.splits, a.sched, a.Hkv, a.g, hcs, a.Hq, a.D, out, o_sb, o_sh);
   HS_CHECK_LAUNCH("attention merge");
   return HS_OK;
 }
@@ -700,7 +913,7 @@ extern "C" int64_t hs_attend_workspace_bytes(int32_t dtype, int64_t batch, int64
                                              int64_t max_entries) {
   if (batch < 1 || heads < 1 || kv_heads < 1 || head_dim < 1 || max_entries < 1) return 256;
   Plan p = plan_attend(dtype, batch, heads, kv_heads, head_dim, max_entries);
-  return workspace_for(p, batch, heads, head_dim);
+  return workspace_for(p, batch, heads, kv_heads, head_dim);
 }
 
 extern "C" int hs_attend_rows(const void* query, int64_t q_stride_b, int64_t q_stride_h,

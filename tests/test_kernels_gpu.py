@@ -372,6 +372,80 @@ def test_group_attention_matches_per_head_rows(gpu, P, kv, g, D, pages, top):
     _close(by_groups, expected, 2e-2, 1e-2)
 
 
+def _group_rows_oracle(union_physical, cols, masks, counts, capacity, kv, g):
+    """Per-head physical row lists [B, Hq, W] (-1 padded) that the entry lists
+    encode: head kv*g + i reads entry e < clamp(count, 0, capacity) when bit i of
+    its mask is set and its column is valid."""
+    B = counts.shape[0]
+    n = np.clip(counts, 0, capacity)
+    lists = [[[] for _ in range(kv * g)] for _ in range(B)]
+    for b in range(B):
+        for k in range(kv):
+            c = cols[b, k, : n[b, k]]
+            m = masks[b, k, : n[b, k]].astype(np.uint32)
+            ok = c >= 0
+            phys = np.where(ok, union_physical[b, np.clip(c, 0, None)], -1)
+            for i in range(g):
+                sel = ok & ((m >> np.uint32(i)) & 1).astype(bool)
+                lists[b][k * g + i] = phys[sel]
+    W = max(1, max(len(r) for req in lists for r in req))
+    rows = np.full((B, kv * g, W), -1, np.int64)
+    for b in range(B):
+        for h, r in enumerate(lists[b]):
+            rows[b, h, : len(r)] = r
+    return rows
+
+
+@pytest.mark.parametrize(
+    "name,B,kv,g,D,capacity,counts",
+    [
+        # ragged lists: empty, one entry, around the 32-entry tile and the chunk sizes,
+        # above the capacity (clamped) and negative (empty)
+        ("ragged", 5, 3, 5, 128, 5000,
+         [0, 1, 31, 32, 33, 127, 128, 129, 500, 2047, 2048, 2049, 5007, -3, 3000]),
+        ("two-head-chunks", 3, 2, 20, 64, 3000, [2999, 17, 1500, 0, 2200, 800]),
+        ("several-rounds", 40, 8, 2, 32, 2100, None),  # > 256 workgroups of ACH entries
+        ("all-empty", 2, 4, 8, 128, 64, [0] * 8),
+        ("many-groups", 520, 8, 1, 32, 40, None),  # > 4096 groups: always the split schedule
+    ],
+)
+@pytest.mark.parametrize("schedule", ["split", "balanced"])
+def test_group_attention_schedule_matches_oracle(gpu, monkeypatch, schedule, name, B, kv, g, D, capacity, counts):
+    """hs_attend_groups over synthetic entry lists of very different lengths, with
+    the default split schedule and the device-derived balanced one (HS_ATTEND_SCHED=1,
+    read per call), each with its merge, against the per-head oracle."""
+    monkeypatch.setenv("HS_ATTEND_SCHED", "1" if schedule == "balanced" else "0")
+    from mini_hisparse_amd.row_index import GroupEntries
+    from mini_hisparse_amd.row_kernels import attend_groups
+
+    P, blocks, U = 16, 96, 700
+    rng = np.random.default_rng(B * 1000 + g)
+    if counts is None:
+        low = 1500 if name == "several-rounds" else 0
+        counts = rng.integers(low, capacity + 1, size=B * kv)
+    counts = np.asarray(counts, np.int64).reshape(B, kv)
+    union_physical = rng.integers(0, blocks * P, size=(B, U))
+    union_physical[rng.random((B, U)) < 0.05] = -1
+    cols = rng.integers(0, U, size=(B, kv, capacity)).astype(np.int32)
+    cols[rng.random(cols.shape) < 0.03] = -1
+    masks = rng.integers(0, 1 << g, size=(B, kv, capacity)).astype(np.int64)
+    masks[rng.random(masks.shape) < 0.02] = 0
+    masks = masks.astype(np.uint32).view(np.int32)
+    pool = make_pool(blocks, P, kv, D, torch.bfloat16, seed=B + g, outliers=True)
+    q = torch.randn(B, kv * g, D, generator=torch.Generator().manual_seed(g)).to(torch.bfloat16)
+    entries = GroupEntries(
+        torch.from_numpy(cols).to(gpu), torch.from_numpy(masks).to(gpu),
+        torch.from_numpy(counts.astype(np.int32)).to(gpu), capacity,
+    )
+    got = attend_groups(q.to(gpu), pool.to(gpu), torch.from_numpy(union_physical).to(gpu), entries, cfg(P, kv, D))
+    rows = _group_rows_oracle(union_physical, cols, masks.view(np.uint32), counts, capacity, kv, g)
+    for b in range(B):
+        expected = oracle.row_attention_rows(q[b], pool, rows[b], P)
+        _close(got[b], expected, 2e-2, 1e-2)
+    if name == "all-empty":
+        assert not got.any()
+
+
 # --------------------------------------------------------------------- append
 def _bits(t):
     return t.view(torch.int16 if t.element_size() == 2 else torch.int32).cpu().numpy()
