@@ -262,6 +262,25 @@ int hs_attend_groups(const void* query, int64_t q_stride_b, int64_t q_stride_h, 
                      int64_t workspace_bytes, hs_stream_t stream);
 
 /*
+ * Page-window attention of the paged cache: replaces the Triton
+ * `_attention_window` / `triton_chunk` of the reference's optional page layout
+ * (reference/kernels.py:12-97), called per window by `paged_attention`
+ * (reference/attention.py:42-128).  One request; page i of the window sits in
+ * device slot slots[i] of the [blocks, 2, P, Hkv, D] pool with lengths[i]
+ * valid tokens; mask (null = every valid token) is a [heads, n_pages, P] byte
+ * array, nonzero where the head reads the token.  Writes the unnormalised fp32
+ * state per query head: out_m[h] = max score (-inf when the head reads no
+ * token), out_l[h] = sum exp(s - m), out_acc[h, :] = sum exp(s - m) V, with
+ * s = (K . q) * head_dim^-0.5, for the caller to merge windows.  Workspace:
+ * hs_attend_workspace_bytes(dtype, 1, heads, kv_heads, head_dim, n_pages * P).
+ */
+int hs_attend_window(const void* query, int64_t q_stride_h, const void* pool, int32_t dtype,
+                     int64_t page_size, int64_t kv_heads, int64_t head_dim, int64_t pool_rows,
+                     const int32_t* slots, const int32_t* lengths, int64_t n_pages,
+                     const uint8_t* mask, int64_t heads, float* out_m, float* out_l, float* out_acc,
+                     void* workspace, int64_t workspace_bytes, hs_stream_t stream);
+
+/*
  * Diagnostic (no reference counterpart): read, without computing, n segment
  * pairs of a device region -- segment i at byte offset offsets[i] (device
  * array) and its partner plane_bytes further, segment_bytes each -- with

@@ -124,6 +124,12 @@ SIGNATURES = {
          c_void_p, c_int64, c_void_p, c_void_p, c_int64, c_int64, c_void_p, c_int64,
          c_int64, c_int64, c_void_p, c_int64, c_int64, c_void_p, c_int64, c_void_p],
     ),
+    "hs_attend_window": (
+        c_int,
+        [c_void_p, c_int64, c_void_p, c_int32, c_int64, c_int64, c_int64, c_int64,
+         c_void_p, c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_void_p, c_void_p,
+         c_void_p, c_int64, c_void_p],
+    ),
 }
 
 _LIB = None

@@ -48,6 +48,11 @@ def build_parser():
         command.add_argument("--top-k", type=_top_k, default=None, help="page count, or all (default)")
         command.add_argument("--max-new-tokens", type=int, default=12)
         command.add_argument("--selector", choices=["quest", "mean"], default="quest")
+        command.add_argument("--cache-layout", choices=["hybrid", "pages"], default="hybrid")
+        command.add_argument("--chunk-pages", type=int, default=2, help="pages layout only")
+        command.add_argument("--no-overlap", action="store_true", help="pages layout only")
+        command.add_argument("--eviction-policy", choices=["legacy", "lru", "fair_lru"], default="fair_lru",
+                             help="pages layout only; hybrid uses request/layer-local row LRU")
         if name == "generate":
             command.add_argument("--model", required=True, help="local Qwen2/2.5 directory")
             command.add_argument("--prompt", default="Explain how a KV cache works.")
@@ -92,17 +97,7 @@ def run(args, parser=None, ops=None):
             for i in range(args.requests)
         ]
     cfg = model.config
-    heads = cfg.num_attention_heads if args.selector == "quest" else 1
-    bound = union_rows_bound(max(map(len, prompts)), args.max_new_tokens, args.top_k, heads, args.page_size)
-    hot = HotConfig(
-        bound if args.max_union_rows is None else args.max_union_rows,
-        args.hot_rows,
-        resident_window_pages=args.resident_window_pages,
-        transition_watermark=args.hot_watermark,
-    )
-    gpu_pages = args.gpu_pages if args.gpu_pages is not None else hot.admission_blocks(args.page_size, cfg.num_hidden_layers)
-    cache_cfg = CacheConfig(
-        gpu_pages=gpu_pages,
+    common = dict(
         host_pages=args.host_pages,
         page_size=args.page_size,
         kv_heads=cfg.num_key_value_heads,
@@ -111,7 +106,28 @@ def run(args, parser=None, ops=None):
         dtype=dtype,
         index_budget_bytes=args.index_budget_mib * 1024 * 1024,
     )
-    cache = HybridKVCache(cache_cfg, hot, ops=ops)
+    if args.cache_layout == "pages":  # whole-page windows (cli.py:155-165)
+        from .paged import PagedConfig, PagedKVCache
+
+        paged_cfg = PagedConfig(
+            gpu_pages=args.gpu_pages if args.gpu_pages is not None else 8,
+            chunk_pages=args.chunk_pages,
+            overlap=not args.no_overlap,
+            eviction_policy=args.eviction_policy,
+            **common,
+        )
+        cache = PagedKVCache(paged_cfg, ops=ops)
+    else:
+        heads = cfg.num_attention_heads if args.selector == "quest" else 1
+        bound = union_rows_bound(max(map(len, prompts)), args.max_new_tokens, args.top_k, heads, args.page_size)
+        hot = HotConfig(
+            bound if args.max_union_rows is None else args.max_union_rows,
+            args.hot_rows,
+            resident_window_pages=args.resident_window_pages,
+            transition_watermark=args.hot_watermark,
+        )
+        gpu_pages = args.gpu_pages if args.gpu_pages is not None else hot.admission_blocks(args.page_size, cfg.num_hidden_layers)
+        cache = HybridKVCache(CacheConfig(gpu_pages=gpu_pages, **common), hot, ops=ops)
     engine = Engine(model, cache, args.top_k, args.backend, tokenizer.eos_token_id if tokenizer else None,
                     selector=args.selector)
     for i, prompt in enumerate(prompts):

@@ -15,6 +15,10 @@
 //   SHARED : one row list read by every head of the group,
 //   GROUPS : per-KV-head deduplicated union columns + head masks, with the
 //            physical row of a column taken from the resolver's output.
+//   WINDOW : the tokens of a window of whole pages (device slot, valid length,
+//            optional per-head token mask): the page-window attention of the
+//            reference's paged cache (reference/kernels.py:12-68), which returns
+//            the unnormalised state (m, l, acc) per head for merging windows.
 //
 // bf16 / fp16 pools use MFMA (v_mfma_f32_16x16x32_{bf16,f16}): S^T = K Q^T
 // with the group's query heads as the N dimension (padded to 16), then
@@ -29,7 +33,7 @@
 
 namespace hs {
 
-enum { MODE_ROWS = 0, MODE_SHARED = 1, MODE_GROUPS = 2 };
+enum { MODE_ROWS = 0, MODE_SHARED = 1, MODE_GROUPS = 2, MODE_WINDOW = 3 };
 
 struct AttendArgs {
   const void* q;
@@ -55,11 +59,33 @@ struct AttendArgs {
   float* part_l;  // like part_m
   float* part_o;  // [B, Hq, splits, D], or [slots, 16, D] when scheduled
   int32_t* sched; // T(0 .. B * Hkv) of the scheduled group kernel
+  const int32_t* wslots;       // WINDOW: device slot of each page [wn]
+  const int32_t* wlens;        // WINDOW: valid tokens of each page [wn]
+  const unsigned char* wmask;  // WINDOW: [Hq, wn, P] token mask, or null (every token)
+  int64_t wn;
 };
+
+// Head mask of token t of window page i for KV head k: bit hl set when query
+// head k * g + hl reads it.
+__device__ __forceinline__ uint32_t window_mask(const AttendArgs& a, int64_t k, int64_t i, int64_t t) {
+  const uint32_t all = a.g >= 32 ? 0xffffffffu : ((1u << a.g) - 1u);
+  if (!a.wmask) return all;
+  uint32_t m = 0u;
+  for (int64_t hl = 0; hl < a.g; ++hl)
+    m |= static_cast<uint32_t>(a.wmask[((k * a.g + hl) * a.wn + i) * a.P + t] != 0) << hl;
+  return m;
+}
+
+// Physical row of token t of window page i (-1 past the page's valid tokens).
+__device__ __forceinline__ int64_t window_row(const AttendArgs& a, int64_t i, int64_t t) {
+  const int64_t len = a.wlens[i];
+  return t < len ? static_cast<int64_t>(a.wslots[i]) * a.P + t : -1;
+}
 
 __device__ __forceinline__ int64_t entry_count(const AttendArgs& a, int64_t b, int64_t k) {
   if (a.mode == MODE_ROWS) return a.g * a.width;
   if (a.mode == MODE_SHARED) return a.width;
+  if (a.mode == MODE_WINDOW) return a.wn * a.P;
   int64_t e = a.ecount[b * a.Hkv + k];
   return e < 0 ? 0 : (e > a.emax ? a.emax : e);
 }
@@ -73,6 +99,10 @@ __device__ __forceinline__ void entry_at(const AttendArgs& a, int64_t b, int64_t
   } else if (a.mode == MODE_SHARED) {
     phys = a.rows[b * a.r_sb + e * a.r_sw];
     mask = a.g >= 32 ? 0xffffffffu : ((1u << a.g) - 1u);
+  } else if (a.mode == MODE_WINDOW) {
+    const int64_t i = e / a.P, t = e - i * a.P;
+    phys = window_row(a, i, t);
+    mask = window_mask(a, k, i, t);
   } else {
     const int64_t off = b * a.e_sb + k * a.e_sk + e;
     const int32_t col = a.ecol[off];
@@ -165,6 +195,16 @@ __device__ __forceinline__ void stage_entries(const AttendArgs& a, int64_t b, in
       ph[s] = i < cnt ? pv : -1;
       mk[s] = 1u << hl;
     }
+  } else if constexpr (MODE == MODE_WINDOW) {
+#pragma unroll
+    for (int s = 0; s < SPT; ++s) {
+      const int i = threadIdx.x + s * NTH;
+      const int64_t e = e0 + (i < cnt ? i : 0);
+      const int64_t pi = e / a.P, t = e - pi * a.P;
+      const int64_t pv = window_row(a, pi, t);
+      ph[s] = i < cnt ? pv : -1;
+      mk[s] = window_mask(a, k, pi, t);
+    }
   } else {
     const uint32_t all = a.g >= 32 ? 0xffffffffu : ((1u << a.g) - 1u);
 #pragma unroll
@@ -187,6 +227,7 @@ template <int MODE>
 __device__ __forceinline__ int64_t entry_total(const AttendArgs& a, int64_t b, int64_t k) {
   if constexpr (MODE == MODE_ROWS) return a.g * a.width;
   else if constexpr (MODE == MODE_SHARED) return a.width;
+  else if constexpr (MODE == MODE_WINDOW) return a.wn * a.P;
   else {
     const int64_t e = a.ecount[b * a.Hkv + k];
     return e < 0 ? 0 : (e > a.emax ? a.emax : e);
@@ -661,7 +702,8 @@ __global__ __launch_bounds__(256) void attend_merge_kernel(const float* part_m, 
                                                             const float* part_o, int64_t splits,
                                                             const int32_t* table, int64_t Hkv, int64_t g,
                                                             int64_t head_chunks, int64_t Hq, int64_t D,
-                                                            void* out, int64_t o_sb, int64_t o_sh) {
+                                                            void* out, int64_t o_sb, int64_t o_sh,
+                                                            float* st_m, float* st_l, float* st_o) {
   const int64_t h = blockIdx.x, b = blockIdx.y;
   int64_t base, stride, n;
   if (table) {
@@ -710,7 +752,15 @@ __global__ __launch_bounds__(256) void attend_merge_kernel(const float* part_m, 
       }
       M = Mc;
     }
-    store_elem<DT>(out, b * o_sb + h * o_sh + d, L > 0.f ? O / L : 0.f);
+    if (st_m) {  // the unnormalised state (m, l, acc) of the head, fp32
+      if (d == 0) {
+        st_m[b * Hq + h] = M;
+        st_l[b * Hq + h] = L;
+      }
+      st_o[(b * Hq + h) * D + d] = O;
+    } else {
+      store_elem<DT>(out, b * o_sb + h * o_sh + d, L > 0.f ? O / L : 0.f);
+    }
   }
 }
 
@@ -839,11 +889,15 @@ static void launch_mfma(const Plan& p, const AttendArgs& a, hipStream_t s) {
   if (a.mode == MODE_GROUPS && a.sched) launch_mfma_mode<DT, MODE_GROUPS, true>(p, a, s);
   else if (a.mode == MODE_GROUPS) launch_mfma_mode<DT, MODE_GROUPS, false>(p, a, s);
   else if (a.mode == MODE_SHARED) launch_mfma_mode<DT, MODE_SHARED, false>(p, a, s);
+  else if (a.mode == MODE_WINDOW) launch_mfma_mode<DT, MODE_WINDOW, false>(p, a, s);
   else launch_mfma_mode<DT, MODE_ROWS, false>(p, a, s);
 }
 
+// out (o_sb, o_sh) receives the normalised output in the pool dtype; when st_m is
+// given, st_m/st_l [B, Hq] and st_o [B, Hq, D] receive the fp32 state instead.
 static int run_attend(int dtype, AttendArgs a, int64_t max_entries, void* out, int64_t o_sb,
-                      int64_t o_sh, void* ws, int64_t ws_bytes, hipStream_t stream) {
+                      int64_t o_sh, void* ws, int64_t ws_bytes, hipStream_t stream,
+                      float* st_m = nullptr, float* st_l = nullptr, float* st_o = nullptr) {
   Plan p = plan_attend(dtype, a.B, a.Hq, a.Hkv, a.D, max_entries);
   // The split schedule is the default: its first loads (entry count, columns,
   // query) go out in one round, which the balanced schedule cannot do (it needs
@@ -879,13 +933,16 @@ static int run_attend(int dtype, AttendArgs a, int64_t max_entries, void* out, i
   const int64_t hcs = a.head_chunks;
   if (dtype == HS_DTYPE_F32)
     hipLaunchKernelGGL((attend_merge_kernel<HS_DTYPE_F32>), mgrid, dim3(mthreads), 0, stream, a.part_m, a.part_l,
-                       a.part_o, p.splits, a.sched, a.Hkv, a.g, hcs, a.Hq, a.D, out, o_sb, o_sh);
+                       a.part_o, p.splits, a.sched, a.Hkv, a.g, hcs, a.Hq, a.D, out, o_sb, o_sh,
+                       st_m, st_l, st_o);
   else if (dtype == HS_DTYPE_BF16)
     hipLaunchKernelGGL((attend_merge_kernel<HS_DTYPE_BF16>), mgrid, dim3(mthreads), 0, stream, a.part_m, a.part_l,
-                       a.part_o, p.splits, a.sched, a.Hkv, a.g, hcs, a.Hq, a.D, out, o_sb, o_sh);
+                       a.part_o, p.splits, a.sched, a.Hkv, a.g, hcs, a.Hq, a.D, out, o_sb, o_sh,
+                       st_m, st_l, st_o);
   else
     hipLaunchKernelGGL((attend_merge_kernel<HS_DTYPE_F16>), mgrid, dim3(mthreads), 0, stream, a.part_m, a.part_l,
-                       a.part_o, p.splits, a.sched, a.Hkv, a.g, hcs, a.Hq, a.D, out, o_sb, o_sh);
+                       a.part_o, p.splits, a.sched, a.Hkv, a.g, hcs, a.Hq, a.D, out, o_sb, o_sh,
+                       st_m, st_l, st_o);
   HS_CHECK_LAUNCH("attention merge");
   return HS_OK;
 }
@@ -984,6 +1041,37 @@ extern "C" int hs_attend_groups(const void* query, int64_t q_stride_b, int64_t q
   a.g = heads / kv_heads;
   a.mode = MODE_GROUPS;
   return run_attend(dtype, a, max_entries, out, o_stride_b, o_stride_h, workspace, workspace_bytes, stream);
+}
+
+extern "C" int hs_attend_window(const void* query, int64_t q_stride_h, const void* pool, int32_t dtype,
+                                int64_t page_size, int64_t kv_heads, int64_t head_dim, int64_t pool_rows,
+                                const int32_t* slots, const int32_t* lengths, int64_t n_pages,
+                                const uint8_t* mask, int64_t heads, float* out_m, float* out_l,
+                                float* out_acc, void* workspace, int64_t workspace_bytes,
+                                hipStream_t stream) {
+  int rc = check_common(dtype, 1, heads, kv_heads, head_dim, page_size, query, pool, out_m);
+  if (rc) return rc;
+  HS_CHECK_ARG(out_l != nullptr && out_acc != nullptr, "null window attention output");
+  HS_CHECK_ARG(slots && lengths && n_pages >= 1, "a window needs at least one page");
+  AttendArgs a{};
+  a.q = query;
+  a.q_sb = 0;
+  a.q_sh = q_stride_h;
+  a.pool = pool;
+  a.P = page_size;
+  a.Hkv = kv_heads;
+  a.D = head_dim;
+  a.pool_rows = pool_rows;
+  a.wslots = slots;
+  a.wlens = lengths;
+  a.wmask = mask;
+  a.wn = n_pages;
+  a.B = 1;
+  a.Hq = heads;
+  a.g = heads / kv_heads;
+  a.mode = MODE_WINDOW;
+  return run_attend(dtype, a, n_pages * page_size, nullptr, 0, 0, workspace, workspace_bytes, stream, out_m,
+                    out_l, out_acc);
 }
 
 extern "C" int hs_probe_row_reads(const void* base, int64_t region_bytes, const int64_t* offsets, int64_t n,

@@ -1,7 +1,7 @@
 """Kernel backend of the cache: the gfx950 HIP library, and nothing else.
 
-``HybridKVCache`` and ``MiniModel.decode`` call their kernels through an ops
-object.  The product has exactly one, :class:`HipOps`; a cache on a non-ROCm
+``HybridKVCache``, ``PagedKVCache`` and ``MiniModel.decode`` call their kernels
+through an ops object.  The product has exactly one, :class:`HipOps`; a cache on a non-ROCm
 device must be given an explicit ops object (the CPU restatement used by the
 test-suite lives outside this package) and otherwise fails at construction.
 """
@@ -12,7 +12,7 @@ import torch
 
 from . import _lib
 from .row_index import resolve_rows
-from .row_kernels import MappedHost, attend_groups, attend_rows, gather_rows
+from .row_kernels import MappedHost, attend_groups, attend_rows, attend_window, gather_rows
 from .selection import quest_selection
 
 
@@ -39,6 +39,10 @@ class HipOps:
             return attend_groups(query, pool, plan.union_physical, topk.entries, config)
         rows = plan.physical_rows
         return attend_rows(query, pool, rows, config)
+
+    def attend_window(self, query, pool, slots, lengths, mask, config):
+        """Unnormalised (m, l, acc) of one page window of the paged layout."""
+        return attend_window(query, pool, slots, lengths, mask, config)
 
     def quest_selection(self, query, minimum, maximum, length, page_size, top_pages, keep_sink=True):
         return quest_selection(query, minimum, maximum, length, page_size, top_pages, keep_sink)

@@ -208,3 +208,37 @@ def attend_groups(query, pool, union_physical, entries, config):
     _lib.check(status, "hs_attend_groups")
     out = out if batched else out[0]
     return out if out.dtype == out_dtype else out.to(out_dtype)
+
+
+def attend_window(query, pool, slots, lengths, mask, config):
+    """Unnormalised attention state of one window of whole pages (hs_attend_window).
+
+    Replaces ``triton_chunk`` / ``_attention_window`` of the reference's paged
+    layout (reference/kernels.py:12-97).  query [Hq, D]; slots / lengths [N]
+    int32 device tensors (device slot and valid tokens of each page); mask
+    [Hq, N, P] bool or None.  Returns fp32 (m [Hq], l [Hq], acc [Hq, D]).
+    """
+    q = _check_query(query, pool, config)
+    if q.ndim != 2 or q.shape[1] != config.head_dim or q.shape[0] % config.kv_heads:
+        raise ValueError("expected [query_heads, head_dim], query_heads divisible by KV heads")
+    heads, dim = q.shape
+    n = slots.numel()
+    if n < 1 or lengths.numel() != n or slots.dtype != torch.int32 or lengths.dtype != torch.int32:
+        raise ValueError("a window needs matching int32 slot and length vectors")
+    if mask is not None:
+        if mask.shape != (heads, n, config.page_size) or mask.dtype != torch.bool:
+            raise ValueError("the window mask must be bool [query_heads, pages, page_size]")
+        mask = mask.contiguous()
+    m = torch.empty(heads, dtype=torch.float32, device=q.device)
+    l = torch.empty_like(m)
+    acc = torch.empty((heads, dim), dtype=torch.float32, device=q.device)
+    code = _lib.dtype_code(pool.dtype)
+    workspace, ws_bytes = _attend_workspace(code, 1, heads, config.kv_heads, dim, n * config.page_size, q.device)
+    status = _lib.load().hs_attend_window(
+        q.data_ptr(), q.stride(0), pool.data_ptr(), code, config.page_size, config.kv_heads, config.head_dim,
+        pool.shape[0] * config.page_size, slots.contiguous().data_ptr(), lengths.contiguous().data_ptr(), n,
+        None if mask is None else mask.data_ptr(), heads, m.data_ptr(), l.data_ptr(), acc.data_ptr(),
+        workspace.data_ptr(), ws_bytes, _lib.stream_handle(q.device),
+    )
+    _lib.check(status, "hs_attend_window")
+    return m, l, acc

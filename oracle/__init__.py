@@ -19,8 +19,9 @@ checkout):
 * ``append``    -- the single-token append: pool rows, Quest bounds, host
                    mirror (``mini_hisparse/storage.py:246-319``)
 * ``attention`` -- the torch row attention (``mini_hisparse/attention.py:26-35``),
-                   ``dense_attention`` (``selection.py:158-163``) and
-                   ``selection_oracle`` (``selection.py:104-126``)
+                   ``dense_attention`` (``selection.py:158-163``),
+                   ``selection_oracle`` (``selection.py:104-126``) and the
+                   paged layout's window state (``reference/kernels.py:12-68``)
 * ``ops``       -- a CPU kernel backend with the same call signatures as the
                    product's HIP backend, used by CPU tests of the host
                    control plane (and by nothing else).
@@ -41,11 +42,14 @@ Pinning (what each function is checked against, besides the GPU):
   equal zeros), a page filled row by row equals its exact column extrema, and
   (on the GPU) equality with ``torch.minimum``/``torch.maximum`` themselves.
 * attention -- a scalar textbook softmax in float64 on small inputs, and the
-  special cases (all masked -> 0, one row -> V, equal scores -> mean of V).
+  special cases (all masked -> 0, one row -> V, equal scores -> mean of V);
+  window states merged across windows (the merge rule of
+  ``reference/attention.py:11-18``) equal dense attention over the union of
+  their tokens, and a head that reads nothing has (-inf, 0, 0).
 """
 
 from .append import append_rows, bound_max, bound_min, takes_new_max, takes_new_min
-from .attention import attend_rows, dense_attention, row_attention_rows, selection_oracle
+from .attention import attend_rows, dense_attention, row_attention_rows, selection_oracle, window_state
 from .gather import gather_rows
 from .quest import quest_pages, quest_scores, quest_selection_positions
 from .resolver import resolve_rows
@@ -67,4 +71,5 @@ __all__ = [
     "resolve_rows",
     "row_attention_rows",
     "selection_oracle",
+    "window_state",
 ]

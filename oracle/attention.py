@@ -5,6 +5,10 @@
   ``_attend`` (``row_kernels.py:90-113``): query head h reads KV head
   ``h // (Hq / Hkv)``; rows ``< 0`` are masked; ``s = (K . q) * D**-0.5``;
   softmax over the unmasked rows; output 0 when every row is masked.
+* ``window_state`` restates the page-window kernel of the reference's paged
+  layout (``reference/kernels.py:12-68``, and ``_torch_chunk`` of
+  ``reference/attention.py:21-37``): the unnormalised state (m, l, acc) of
+  each head over the valid, unmasked tokens of a window of whole pages.
 * ``dense_attention`` restates ``selection.py:158-163``.
 * ``selection_oracle`` restates the sparse output of ``selection.py:104-126``.
 
@@ -57,6 +61,48 @@ def row_attention_rows(query, pool, rows, page_size):
         v = pool[blocks, 1, offsets, kv_of[:, None]]
     scores = (k * q[:, None, :]).sum(-1) * dim**-0.5
     return _softmax_weighted(scores, rows >= 0, v)
+
+
+def window_state(query, pool, slots, lengths, mask, page_size):
+    """One window of whole pages (reference/kernels.py:12-68).
+
+    query [Hq, D]; pool [blocks, 2, P, Hkv, D]; page i of the window is device
+    slot ``slots[i]`` with ``lengths[i]`` valid tokens; ``mask`` [Hq, N, P]
+    bool or None (every valid token).  Returns float64 (m [Hq], l [Hq],
+    acc [Hq, D]): m = the largest valid score (-inf if none), l = sum of
+    exp(s - m), acc = sum of exp(s - m) V (both 0 when the head reads nothing),
+    with s = (K . q) * D**-0.5.
+    """
+    slots = np.asarray(slots.cpu() if hasattr(slots, "cpu") else slots, dtype=np.int64)
+    lengths = np.asarray(lengths.cpu() if hasattr(lengths, "cpu") else lengths, dtype=np.int64)
+    q = _f64(query)
+    heads, dim = q.shape
+    kv_heads = pool.shape[3]
+    t = np.arange(page_size)
+    rows = np.where(t[None, :] < lengths[:, None], slots[:, None] * page_size + t[None, :], -1).reshape(-1)
+    valid = np.broadcast_to(rows >= 0, (heads, rows.size))
+    if mask is not None:
+        m = np.asarray(mask.cpu() if hasattr(mask, "cpu") else mask, dtype=bool).reshape(heads, -1)
+        valid = valid & m
+    kv_of = np.arange(heads) // (heads // kv_heads)
+    safe = np.clip(rows, 0, None)
+    blocks, offsets = safe // page_size, safe % page_size
+    if hasattr(pool, "detach"):
+        import torch
+
+        bi = torch.from_numpy(np.broadcast_to(blocks[None, :], valid.shape).copy())
+        oi = torch.from_numpy(np.broadcast_to(offsets[None, :], valid.shape).copy())
+        ki = torch.from_numpy(np.broadcast_to(kv_of[:, None], valid.shape).copy())
+        k, v = _f64(pool[bi, 0, oi, ki]), _f64(pool[bi, 1, oi, ki])  # [Hq, N*P, D]
+    else:
+        pool = np.asarray(pool, dtype=np.float64)
+        k = pool[blocks[None, :], 0, offsets[None, :], kv_of[:, None]]
+        v = pool[blocks[None, :], 1, offsets[None, :], kv_of[:, None]]
+    scores = np.where(valid, (k * q[:, None, :]).sum(-1) * dim**-0.5, -np.inf)
+    top = scores.max(axis=1)
+    shift = np.where(np.isfinite(top), top, 0.0)
+    w = np.where(valid, np.exp(scores - shift[:, None]), 0.0)
+    return top, w.sum(axis=1), (w[..., None] * v).sum(axis=1)
 
 
 def attend_rows(query, pool, rows, page_size):

@@ -43,6 +43,10 @@ class CpuOracleOps:
         out = oracle.row_attention_rows(query, pool, plan.physical_rows, config.page_size)
         return torch.from_numpy(out).to(query.dtype)
 
+    def attend_window(self, query, pool, slots, lengths, mask, config):
+        m, l, acc = oracle.window_state(query, pool, slots, lengths, mask, config.page_size)
+        return tuple(torch.from_numpy(x).to(torch.float32) for x in (m, l, acc))
+
     def quest_selection(self, query, minimum, maximum, length, page_size, top_pages, keep_sink=True):
         positions = quest_selection_positions(query, minimum, maximum, length, page_size, top_pages, keep_sink)
         return Selection(positions, length, page_size, "quest")
@@ -54,3 +58,11 @@ def make_cache(config, hot):
 
     ops = CpuOracleOps() if torch.device(config.device).type == "cpu" else None
     return HybridKVCache(config, hot, ops=ops)
+
+
+def make_paged(config):
+    """PagedKVCache with the HIP backend on ROCm devices, the CPU oracle otherwise."""
+    from mini_hisparse_amd.paged import PagedKVCache
+
+    ops = CpuOracleOps() if torch.device(config.device).type == "cpu" else None
+    return PagedKVCache(config, ops=ops)

@@ -12,6 +12,9 @@ records, as small JSON fixtures next to this script:
   margin per head;
 * demo_outputs.json          -- the reference CLI ``demo`` (CPU, fp32):
   generated tokens, row statistics and counters for a few settings.
+* paged_demo_outputs.json    -- the same CLI with the optional page layout
+  (``--cache-layout pages``, reference/cache.py): tokens, counters and page
+  locations under each eviction policy, with and without window overlap.
 
 These are the functions no reference test or closed form pins.  The fixtures
 are data; nothing under tests/ or the product reads the reference at run time.
@@ -140,18 +143,44 @@ def demo_outputs(reference_cli):
     return results
 
 
+def paged_demo_outputs(reference_cli):
+    base = ["demo", "--device", "cpu", "--cache-layout", "pages", "--prompt-tokens", "70", "--requests", "2",
+            "--max-new-tokens", "6"]
+    settings = [
+        base + ["--top-k", "3", "--gpu-pages", "6"],  # fair_lru, overlapping windows of 2 pages
+        base + ["--top-k", "3", "--gpu-pages", "6", "--eviction-policy", "lru", "--no-overlap"],
+        base + ["--top-k", "4", "--gpu-pages", "5", "--eviction-policy", "legacy", "--chunk-pages", "3"],
+        base + ["--gpu-pages", "4"],  # every page, windows under pressure
+    ]
+    results = []
+    for argv in settings:
+        sys.argv = ["mini-hisparse", *argv]
+        out = io.StringIO()
+        with contextlib.redirect_stdout(out):
+            reference_cli.main()
+        report = json.loads(out.getvalue())
+        results.append({"argv": argv, "outputs": report["outputs"], "requests": report["requests"],
+                        "stats": report["stats"], "locations": report["locations"],
+                        "final_timeline": report["timeline"][-1]})
+    return results
+
+
 def main():
     reference = sys.argv[1] if len(sys.argv) > 1 else "/root/reference"
+    only = set(sys.argv[2:])  # optional fixture names: write only these
     sys.path.insert(0, reference)
     torch.set_num_threads(1)
     from mini_hisparse import cli, row_index, selection  # the reference package
 
-    save_quest(quest_selections(selection), os.path.join(HERE, "quest_selections.npz"))
-    print("quest_selections.npz", os.path.getsize(os.path.join(HERE, "quest_selections.npz")), "bytes")
-    fixtures = {
-        "resolver_trajectories.json": resolver_trajectories(row_index),
-        "demo_outputs.json": demo_outputs(cli),
+    if not only or "quest_selections.npz" in only:
+        save_quest(quest_selections(selection), os.path.join(HERE, "quest_selections.npz"))
+        print("quest_selections.npz", os.path.getsize(os.path.join(HERE, "quest_selections.npz")), "bytes")
+    makers = {
+        "resolver_trajectories.json": lambda: resolver_trajectories(row_index),
+        "demo_outputs.json": lambda: demo_outputs(cli),
+        "paged_demo_outputs.json": lambda: paged_demo_outputs(cli),
     }
+    fixtures = {name: make() for name, make in makers.items() if not only or name in only}
     for name, data in fixtures.items():
         with open(os.path.join(HERE, name), "w") as f:
             json.dump({"generated_by": "tests/golden/make_golden.py from mini-hisparse 0.2.0 (CPU)", "cases": data}, f)

@@ -25,7 +25,7 @@ def declared_functions():
 def test_header_declares_the_expected_entry_points():
     names = declared_functions()
     for required in ("hs_quest_topk", "hs_build_union", "hs_resolve_rows", "hs_resolve_rows_batched",
-                     "hs_gather_rows", "hs_gather_rows_batched", "hs_attend_rows", "hs_attend_groups",
+                     "hs_gather_rows", "hs_gather_rows_batched", "hs_attend_rows", "hs_attend_groups", "hs_attend_window",
                      "hs_host_alias", "hs_last_error"):
         assert required in names
 

@@ -52,3 +52,39 @@ def test_demo_matches_reference_on_gpu(case):
     expected = case["row_stats"]
     total = expected["resident_hits"] + expected["hot_hits"] + expected["misses"]
     assert rows["resident_hits"] + rows["hot_hits"] + rows["misses"] == total
+
+
+PAGED = os.path.join(os.path.dirname(__file__), "golden", "paged_demo_outputs.json")
+with open(PAGED) as f:
+    PAGED_CASES = json.load(f)["cases"]
+PAGED_IDS = [" ".join(c["argv"][9:]) for c in PAGED_CASES]
+
+
+@pytest.mark.parametrize("case", PAGED_CASES, ids=PAGED_IDS)
+def test_paged_demo_matches_reference_on_cpu(case):
+    """The page layout end to end (eviction policy, window overlap, chunk width): tokens,
+    every counter (misses, evictions, hits, windows, bytes) and the final page locations."""
+    torch.set_num_threads(1)
+    report = run(_args(case["argv"], "cpu"), ops=CpuOracleOps())
+    assert report["outputs"] == case["outputs"]
+    assert report["requests"] == case["requests"]
+    assert report["stats"] == case["stats"]
+    assert report["locations"] == case["locations"]
+    assert report["timeline"][-1] == case["final_timeline"]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("case", PAGED_CASES, ids=PAGED_IDS)
+def test_paged_demo_matches_reference_on_gpu(case):
+    """On the GPU (hs_attend_window) the placement decisions are host logic, so the
+    counters that follow them match too; only the reclamation of retired host slots
+    follows the device's event timing."""
+    if not gpu_available():
+        pytest.skip("no ROCm GPU")
+    report = run(_args(case["argv"], "cuda:0"))
+    assert report["outputs"] == case["outputs"]
+    assert report["requests"] == case["requests"]
+    timing = {"reclaimed_requests"}
+    assert {k: v for k, v in report["stats"].items() if k not in timing} == {
+        k: v for k, v in case["stats"].items() if k not in timing
+    }

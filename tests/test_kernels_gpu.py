@@ -446,6 +446,48 @@ def test_group_attention_schedule_matches_oracle(gpu, monkeypatch, schedule, nam
         assert not got.any()
 
 
+# ------------------------------------------------------- page-window attention
+@pytest.mark.parametrize(
+    "dtype,P,kv,g,D,n_pages,masked",
+    [
+        (torch.bfloat16, 16, 8, 8, 128, 4, True),   # microbench head shape
+        (torch.bfloat16, 16, 4, 7, 128, 64, False),  # Qwen2.5-7B head shape, a wide window
+        (torch.float16, 7, 2, 3, 24, 5, True),      # non-power-of-two page and head_dim
+        (torch.bfloat16, 16, 1, 20, 32, 3, True),   # more than 16 heads per KV head
+        (torch.float32, 4, 2, 2, 8, 2, True),       # reference test shape (VALU kernel)
+        (torch.float32, 16, 2, 7, 64, 9, False),
+    ],
+)
+def test_attend_window_matches_oracle(gpu, dtype, P, kv, g, D, n_pages, masked):
+    from mini_hisparse_amd.row_kernels import attend_window
+
+    heads, blocks = kv * g, 3 * n_pages + 2
+    pool = make_pool(blocks, P, kv, D, dtype, seed=n_pages, outliers=True)
+    q = torch.randn(heads, D, generator=torch.Generator().manual_seed(D)).to(dtype)
+    gen = torch.Generator().manual_seed(P * 7 + g)
+    slots = torch.randperm(blocks, generator=gen)[:n_pages].to(torch.int32)
+    lengths = torch.full((n_pages,), P, dtype=torch.int32)
+    lengths[-1] = max(1, P // 3)  # a partial tail page
+    mask = None
+    if masked:
+        mask = torch.rand((heads, n_pages, P), generator=gen) < 0.5
+        mask[0] = False  # a head that reads nothing: (-inf, 0, 0)
+    m, l, acc = attend_window(q.to(gpu), pool.to(gpu), slots.to(gpu), lengths.to(gpu),
+                              None if mask is None else mask.to(gpu), cfg(P, kv, D))
+    em, el, eacc = oracle.window_state(q, pool, slots, lengths, mask, P)
+    got_m, got_l, got_acc = (x.cpu().double().numpy() for x in (m, l, acc))
+    reads = np.isfinite(em)
+    assert (np.isfinite(got_m) == reads).all()
+    assert (got_l[~reads] == 0).all() and (got_acc[~reads] == 0).all()
+    # the state's scale is free (exp(s - m)); compare the normalised output and m
+    atol, rtol = TOL[dtype]
+    np.testing.assert_allclose(got_m[reads], em[reads], rtol=1e-3 if dtype != torch.float32 else 1e-6, atol=1e-3)
+    out = got_acc[reads] / got_l[reads][:, None]
+    want = eacc[reads] / el[reads][:, None]
+    err = np.abs(out - want)
+    assert (err <= atol + rtol * np.abs(want)).all(), err.max()
+
+
 # --------------------------------------------------------------------- append
 def _bits(t):
     return t.view(torch.int16 if t.element_size() == 2 else torch.int32).cpu().numpy()

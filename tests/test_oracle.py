@@ -323,6 +323,49 @@ def test_attention_special_cases():
     np.testing.assert_allclose(dense, sparse)
 
 
+def _merge_states(a, b):
+    """The window merge of reference/attention.py:11-18 (float64)."""
+    (m1, l1, a1), (m2, l2, a2) = a, b
+    m = np.maximum(m1, m2)
+    w1 = np.where(np.isfinite(m1), np.exp(np.where(np.isfinite(m1), m1 - m, 0.0)), 0.0)
+    w2 = np.where(np.isfinite(m2), np.exp(np.where(np.isfinite(m2), m2 - m, 0.0)), 0.0)
+    return m, w1 * l1 + w2 * l2, w1[:, None] * a1 + w2[:, None] * a2
+
+
+def test_window_states_merge_to_scalar_softmax_over_their_tokens():
+    """Windows of whole pages (partial tail page, per-head token masks, a head that
+    reads nothing in one window): merged states give the textbook softmax of each
+    head over exactly the tokens it reads; a head that reads nothing has (-inf, 0, 0)."""
+    rng = np.random.default_rng(8)
+    P, kv, D, blocks, heads = 4, 2, 6, 7, 4
+    pool = rng.standard_normal((blocks, 2, P, kv, D))
+    q = rng.standard_normal((heads, D))
+    windows = [([5, 1], [4, 4]), ([3], [2])]  # (slots, valid lengths): page 3 is a partial tail
+    masks = [rng.random((heads, 2, P)) < 0.6, np.zeros((heads, 1, P), bool)]
+    masks[1][0] = True  # head 0 reads the tail window; heads 1-3 read nothing there
+    masks[0][3] = False  # head 3 reads nothing in the first window either
+    states = [oracle.window_state(q, pool, s, n, m, P) for (s, n), m in zip(windows, masks)]
+    m, l, acc = _merge_states(*states)
+    g = heads // kv
+    for h in range(heads):
+        rows = [slot * P + t for (slots, lens), mk in zip(windows, masks)
+                for i, (slot, n) in enumerate(zip(slots, lens)) for t in range(n) if mk[h, i, t]]
+        if not rows:
+            assert m[h] == -np.inf and l[h] == 0 and (acc[h] == 0).all()
+            continue
+        keys = [[pool[r // P, 0, r % P, h // g] for r in rows]]
+        values = [[pool[r // P, 1, r % P, h // g] for r in rows]]
+        want = scalar_attention(q[h : h + 1], keys, values, np.ones((1, len(rows)), bool))[0]
+        np.testing.assert_allclose(acc[h] / l[h], want, rtol=1e-12, atol=1e-12)
+        scores = [np.dot(k, q[h]) * D**-0.5 for k in keys[0]]
+        assert m[h] == pytest.approx(max(scores), rel=1e-12, abs=1e-12)
+    # no mask: every valid token, i.e. dense attention over the window's tokens
+    m0, l0, a0 = oracle.window_state(q, pool, [2, 6], [4, 3], None, P)
+    k = np.concatenate([pool[2, 0, :4], pool[6, 0, :3]])
+    v = np.concatenate([pool[2, 1, :4], pool[6, 1, :3]])
+    np.testing.assert_allclose(a0 / l0[:, None], oracle.dense_attention(q, k, v), rtol=1e-12, atol=1e-12)
+
+
 # ------------------------------------------------------------------ gather
 def test_gather_copies_exactly_the_planned_rows():
     rng = np.random.default_rng(7)
