@@ -1,4 +1,5 @@
-"""Command line: ``demo`` (tiny random decoder) and ``generate`` (local Qwen2 checkpoint).
+"""Command line: ``demo`` (tiny random decoder), ``generate`` (local Qwen2 checkpoint) and
+``bench`` (KV microbenchmark of the page layout).
 
 Flags and the JSON report follow the reference CLI (cli.py:24-214).  The
 kernels run on the ROCm device; ``--backend`` accepts ``auto`` or ``hip``.
@@ -31,7 +32,7 @@ def _top_k(value):
 def build_parser():
     parser = argparse.ArgumentParser(description="Mini-HiSparse on MI355X: decode through partial KV residency")
     sub = parser.add_subparsers(dest="command", required=True)
-    for name in ("demo", "generate"):
+    for name in ("demo", "generate", "bench"):
         command = sub.add_parser(name)
         command.add_argument("--device", default="cuda:0")
         command.add_argument("--gpu-pages", type=int)
@@ -41,6 +42,15 @@ def build_parser():
         command.add_argument("--dtype", choices=["float32", "float16", "bfloat16"], default="float32")
         command.add_argument("--output", type=Path)
         command.add_argument("--index-budget-mib", type=int, default=64)
+        command.add_argument("--chunk-pages", type=int, default=2, help="pages layout only")
+        command.add_argument("--eviction-policy", choices=["legacy", "lru", "fair_lru"], default="fair_lru",
+                             help="pages layout only; hybrid uses request/layer-local row LRU")
+        if name == "bench":  # experiments/benchmark.py of the reference, on the page layout
+            command.add_argument("--tokens", type=int, default=1024)
+            command.add_argument("--steps", type=int, default=20)
+            command.add_argument("--requests", type=int, default=3)
+            command.add_argument("--selected-pages", type=int, default=8)
+            continue
         command.add_argument("--max-union-rows", type=int)
         command.add_argument("--hot-rows", type=int)
         command.add_argument("--resident-window-pages", type=int, default=64)
@@ -49,10 +59,7 @@ def build_parser():
         command.add_argument("--max-new-tokens", type=int, default=12)
         command.add_argument("--selector", choices=["quest", "mean"], default="quest")
         command.add_argument("--cache-layout", choices=["hybrid", "pages"], default="hybrid")
-        command.add_argument("--chunk-pages", type=int, default=2, help="pages layout only")
         command.add_argument("--no-overlap", action="store_true", help="pages layout only")
-        command.add_argument("--eviction-policy", choices=["legacy", "lru", "fair_lru"], default="fair_lru",
-                             help="pages layout only; hybrid uses request/layer-local row LRU")
         if name == "generate":
             command.add_argument("--model", required=True, help="local Qwen2/2.5 directory")
             command.add_argument("--prompt", default="Explain how a KV cache works.")
@@ -75,6 +82,21 @@ def union_rows_bound(prompt_length, max_new_tokens, top_k, heads, page_size):
 def run(args, parser=None, ops=None):
     torch.manual_seed(42)
     dtype = getattr(torch, args.dtype)
+    if args.command == "bench":
+        from .layout_bench import benchmark
+        from .paged import PagedConfig
+
+        config = PagedConfig(
+            gpu_pages=args.gpu_pages if args.gpu_pages is not None else 8,
+            host_pages=args.host_pages,
+            page_size=args.page_size,
+            device=args.device,
+            dtype=dtype,
+            index_budget_bytes=args.index_budget_mib * 1024 * 1024,
+            chunk_pages=args.chunk_pages,
+            eviction_policy=args.eviction_policy,
+        )
+        return benchmark(config, args.tokens, args.steps, args.requests, args.selected_pages, args.backend, ops=ops)
     tokenizer = None
     if args.command == "generate":
         from transformers import AutoTokenizer

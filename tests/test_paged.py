@@ -394,3 +394,55 @@ def test_exact_tokens_head_masks_and_empty_windows(device, budget):
     got = paged_attention(q, cache, "r", 0, selection=selection)
     torch.testing.assert_close(got, expected.to(got.dtype), rtol=2e-5, atol=2e-6)
     cache.assert_invariants()
+
+
+# ------------------------------------------------------- CLI bench (page layout)
+def _bench(device, ops=None):
+    from mini_hisparse_amd.cli import build_parser, run
+
+    args = build_parser().parse_args(["bench", "--device", device, "--tokens", "200", "--steps", "3",
+                                      "--requests", "2", "--selected-pages", "5", "--gpu-pages", "4"])
+    return run(args, ops=ops)
+
+
+def test_layout_bench_on_cpu():
+    """The CLI bench (experiments/benchmark.py): three arrangements, checked after timing."""
+    from tests.cpu_ops import CpuOracleOps
+
+    report = _bench("cpu", CpuOracleOps())
+    modes = [r["mode"] for r in report["results"]]
+    assert modes == ["resident", "pressured_serial", "pressured_overlap"]
+    resident, serial, overlap = report["results"]
+    assert "misses" not in resident["stats"] and serial["stats"]["misses"] > 0
+    assert overlap["stats"]["prefetch_windows"] > 0 and "prefetch_windows" not in serial["stats"]
+    assert max(r["max_abs_error"] for r in report["results"]) < 1e-5
+
+
+@pytest.mark.gpu
+def test_layout_bench_on_gpu(gpu):
+    report = _bench(gpu)
+    assert report["workload"]["gpu"]
+    assert [r["mode"] for r in report["results"]] == ["resident", "pressured_serial", "pressured_overlap"]
+    assert max(r["max_abs_error"] for r in report["results"]) < 3e-5
+
+
+@pytest.mark.parametrize("policy", ["fair_lru", "legacy"])
+def test_layout_bench_counters_match_the_reference(policy):
+    """The CLI bench at its default settings (1024 tokens, 20 steps, 3 requests, 8 pages,
+    8 slots): every cache counter of every arrangement equals the reference's
+    (tests/golden/layout_bench_counters.json, reference CPU path)."""
+    import json
+    import os
+
+    from mini_hisparse_amd.cli import build_parser, run
+    from tests.cpu_ops import CpuOracleOps
+
+    with open(os.path.join(os.path.dirname(__file__), "golden", "layout_bench_counters.json")) as f:
+        case = next(c for c in json.load(f)["cases"] if c["eviction_policy"] == policy)
+    torch.set_num_threads(1)
+    args = build_parser().parse_args(["bench", "--device", "cpu", "--eviction-policy", policy])
+    report = run(args, ops=CpuOracleOps())
+    for got, want in zip(report["results"], case["results"]):
+        assert got["mode"] == want["mode"]
+        assert got["stats"] == want["stats"]
+        assert got["budget_pages"] == want["budget_pages"]
