@@ -240,8 +240,9 @@ class SparseKVState:
                 self.next_spare += 1
                 self.tail_block[l][b] = blk
                 ls.append(l), bs.append(b), ps.append(positions[b] // P), blocks.append(blk)
-        index = (torch.tensor(ls), torch.tensor(bs), torch.tensor(ps))
-        self.resident[tuple(i.to(self.device) for i in index)] = torch.tensor(blocks, dtype=torch.int32).to(self.device)
+        # one pinned upload, queued on the current stream (no host synchronisation)
+        rows = torch.tensor([ls, bs, ps, blocks], dtype=torch.int64, pin_memory=True).to(self.device, non_blocking=True)
+        self.resident[rows[0], rows[1], rows[2]] = rows[3].to(torch.int32)
 
     def append_args(self, layer, positions):
         """ctypes arrays of one layer's hs_append_rows call."""

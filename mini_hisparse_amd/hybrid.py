@@ -229,7 +229,9 @@ class HybridKVCache:
     def _prepare_append(self, page):
         self._writing_key = page.key
         tables = self.tables[page.key[:2]]
-        tables.source[page.key[2]] = page.host_slot
+        # table entries are set with fill kernels on the compute stream: assigning a
+        # Python int to a device element is a synchronising copy on ROCm PyTorch
+        tables.source[page.key[2]].fill_(page.host_slot)
         if page.valid_tokens:
             if page.slot is None:
                 raise RuntimeError("active append tail lost its resident lease")
@@ -245,10 +247,10 @@ class HybridKVCache:
 
     def _bind(self, page, slot, location):
         self.storage.bind(page, slot, location)
-        self.tables[page.key[:2]].resident[page.key[2]] = slot
+        self.tables[page.key[:2]].resident[page.key[2]].fill_(slot)
 
     def _detach(self, page):
-        self.tables[page.key[:2]].resident[page.key[2]] = -1
+        self.tables[page.key[:2]].resident[page.key[2]].fill_(-1)
         self.storage.detach(page)
 
     def _tail_of(self, group):

@@ -28,13 +28,22 @@ def make(device, pages=7, watermark=0, window=64):
 
 
 def spin_cycles(ms):
-    """Cycle count for torch's spin kernel that keeps a stream busy for about ``ms``."""
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record()
-    torch.cuda._sleep(1_000_000)
-    end.record()
-    end.synchronize()
-    return int(1_000_000 * ms / max(start.elapsed_time(end), 1e-3))
+    """Cycle count for torch's spin kernel that keeps a stream busy for at least ``ms``.
+
+    The spin counts shader clock cycles, whose rate follows the GPU's clock state:
+    the fastest of three calibration spins sets the count, so that a later spin at a
+    higher clock than during calibration still lasts ``ms``.
+    """
+    fastest = None
+    for _ in range(3):
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        torch.cuda._sleep(10_000_000)
+        end.record()
+        end.synchronize()
+        elapsed = max(start.elapsed_time(end), 1e-3)
+        fastest = elapsed if fastest is None else min(fastest, elapsed)
+    return int(10_000_000 * ms / fastest)
 
 
 def write(cache, name, count):
