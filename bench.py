@@ -8,6 +8,11 @@ per query head (sink and tail forced).  Of the selected union rows 50% sit in
 resident pages, 30% in hot slots and 20% miss to pinned host memory.  Inputs
 are seeded and synthetic; they live in HBM / pinned host memory before timing.
 
+Workload "qwen2.5-7b-layer": the same one-layer step at the north_star shape --
+Qwen2.5-7B heads (28 q / 4 kv, head_dim 128), 8192 pages (131,072 tokens) per
+request, batch 16 -- whose attention target north_star states (>= 60% of HBM
+peak); the end-to-end 7B workload runs batch 8 (pinned host memory).
+
 A step is the whole hot path for the 8 requests: restore the hot tags/LRU to
 the step's starting state (so every step sees the same 20% misses), Quest
 scorer + top-k, device union, resolver, host->hot gather on the transfer
@@ -22,6 +27,7 @@ import os
 import platform
 import sys
 import time
+from dataclasses import dataclass
 from math import ceil
 
 import numpy as np
@@ -34,8 +40,9 @@ def parse_args():
     p = argparse.ArgumentParser(description=__doc__)
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--workload", default="microbench",
-                   choices=["microbench", "qwen2.5-0.5b", "qwen2.5-7b", "qwen2.5-32b-stress"],
-                   help="microbench = BASELINE configs[1] (default); the Qwen shapes run the "
+                   choices=["microbench", "qwen2.5-7b-layer", "qwen2.5-0.5b", "qwen2.5-7b", "qwen2.5-32b-stress"],
+                   help="microbench = BASELINE configs[1] (default); qwen2.5-7b-layer = the same one-layer "
+                        "step at the north_star shape (7B heads, 128k histories, batch 16); the Qwen shapes run the "
                         "layer-major batched engine end to end (configs[2], configs[3], configs[4])")
     p.add_argument("--steps", type=int, default=20)
     p.add_argument("--warmup", type=int, default=5)
@@ -64,16 +71,32 @@ def parse_args():
     return p.parse_args()
 
 
+@dataclass(frozen=True)
 class Shape:
-    kv_heads = 8
-    heads = 64
-    head_dim = 128
-    page_size = 16
-    pages = 4096
-    top = 64
-    hot_rows = 32768
-    resident_frac = 0.5
-    hot_frac_of_rest = 0.6  # 30% of all union rows
+    """One layer of synthetic sparse-decode state (the microbench machinery)."""
+
+    label: str
+    batch: int
+    kv_heads: int
+    heads: int
+    pages: int  # logical pages per request
+    head_dim: int = 128
+    page_size: int = 16
+    top: int = 64
+    hot_rows: int = 32768
+    resident_frac: float = 0.5
+    hot_frac_of_rest: float = 0.6  # 30% of all union rows
+
+
+SHAPES = {
+    # BASELINE configs[1]
+    "microbench": Shape("microbench (BASELINE configs[1]): 1 layer, 64 q / 8 kv heads, head_dim 128, page 16, "
+                        "4096 pages/request", batch=8, kv_heads=8, heads=64, pages=4096),
+    # one layer of the north_star shape: Qwen2.5-7B heads, 128k-token histories, batch 16
+    "qwen2.5-7b-layer": Shape("one layer of the Qwen2.5-7B shape (BASELINE configs[3] / north_star): 28 q / 4 kv "
+                              "heads, head_dim 128, page 16, 8192 pages/request (131,072 tokens)",
+                              batch=16, kv_heads=4, heads=28, pages=8192),
+}
 
 
 def build_workload(args, torch, device):
@@ -82,7 +105,7 @@ def build_workload(args, torch, device):
     from mini_hisparse_amd.config import CacheConfig
     from mini_hisparse_amd.row_kernels import MappedHost
 
-    S = Shape
+    S = SHAPES[args.workload]
     B, P, C, Hkv, D = args.batch, S.page_size, S.pages, S.kv_heads, S.head_dim
     L = C * P
     gen = torch.Generator(device=device).manual_seed(args.seed)
@@ -168,7 +191,7 @@ def build_workload(args, torch, device):
     return dict(
         cfg=cfg, dec=dec, pipe=pipe, q=q, kmin=kmin, kmax=kmax, host=host, alias=MappedHost(host), pool=pool,
         tables=tables, tags_all=tags_all, lru_all=lru_all, tags0=tags_all.clone(), lru0=lru_all.clone(),
-        stats=stats, length=L,
+        stats=stats, length=L, shape=S,
     )
 
 
@@ -226,8 +249,11 @@ def run_pipelined(torch, w, steps):
 
 
 def stage_ms(events):
+    """Per-stage milliseconds: the median over the recorded steps, so that a one-off host
+    stall (the GPU idles inside one stage's event pair until the host launches) does not
+    move it."""
     def avg(i, j):
-        return float(np.mean([e[i].elapsed_time(e[j]) for e in events]))
+        return float(np.median([e[i].elapsed_time(e[j]) for e in events]))
 
     return {
         "quest_and_union": avg(0, 1),
@@ -396,7 +422,7 @@ def attention_sweep(torch, device, reps=8):
 
 def algorithmic_bytes(w, torch):
     """Per-launch algorithmic bytes of each kernel (per-unit formulas x units)."""
-    S, dec = Shape, w["dec"]
+    S, dec = w["shape"], w["dec"]
     B, e, D = dec.batch, 2, S.head_dim
     entries = int(w["dec"].entry_counts.sum().item())
     per_head = int((w["dec"].physical >= 0).sum().item())
@@ -423,7 +449,7 @@ def cpu_baseline(torch, w, budget_s):
     from oracle.quest import pages_to_positions
 
     torch.set_num_threads(1)
-    S, dec = Shape, w["dec"]
+    S, dec = w["shape"], w["dec"]
     P, L = S.page_size, w["length"]
     q = w["q"].cpu()
     pool = w["pool"].cpu()
@@ -740,11 +766,12 @@ def main():
     if args.attention_sweep:
         attention_sweep(torch, device)
         return
-    if args.workload != "microbench":
+    if args.workload not in SHAPES:
         run_model_workload(args, torch, device)
         return
+    shape = SHAPES[args.workload]
     if args.batch is None:
-        args.batch = 8
+        args.batch = shape.batch
     print(f"[bench] building workload (batch {args.batch})", file=sys.stderr, flush=True)
     w = build_workload(args, torch, device)
     w["use_transfer_stream"] = args.transfer_stream or args.parts > 1
@@ -769,12 +796,15 @@ def main():
     copy = hbm_copy_gbs(torch, device)
     ceilings = attention_ceilings(torch, w, bytes_["attention"])
     att_gbs = bytes_["attention"] / (stages["attention"] * 1e-3) / 1e9
+    # the committed counter summary was taken on the default microbench run
+    counters_apply = args.workload == "microbench" and args.batch == shape.batch
+
     def hbm_line(stage, nbytes, pmc_kernels, **extra):
         """A stage's algorithmic-byte rate and, from the committed counter summary, the HBM
         bytes its kernels move per launch and the rate those give (the counter evidence)."""
         ms = stages[stage]
         gbs = nbytes / (ms * 1e-3) / 1e9
-        traffic = pmc_traffic(pmc_kernels)
+        traffic = pmc_traffic(pmc_kernels) if counters_apply else None
         line = {"ms": ms, "bytes": nbytes, "GBps": gbs, "frac_hbm_peak": gbs / HBM_PEAK_GBS,
                 "hbm_traffic_bytes": traffic,
                 "hbm_traffic_GBps": None if traffic is None else traffic / (ms * 1e-3) / 1e9,
@@ -808,8 +838,8 @@ def main():
         "dtype": "bf16",
         "data": "synthetic (seeded K/V ~ N(0,1), 2% channels x8; random-init tables)",
         "config": {
-            "workload": "microbench (BASELINE configs[1]): 1 layer, 64 q / 8 kv heads, head_dim 128, "
-            f"page 16, 4096 pages/request, batch {args.batch}, Quest top-64, 50% resident / 30% hot / 20% miss; "
+            "workload": f"{shape.label}, batch {args.batch}, Quest top-{shape.top}, "
+            "50% resident / 30% hot / 20% miss; "
             + (f"{args.parts} request groups overlapped" if args.parts > 1 else
                "gather on a transfer stream ordered by events" if args.transfer_stream else
                "every stage on one stream"),
@@ -823,7 +853,7 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": att_gbs / HBM_PEAK_GBS,
-            "traffic": pmc_traffic(),
+            "traffic": pmc_traffic() if counters_apply else None,
             "kernel": "attend_mfma_kernel + attend_merge_kernel (hs_attend_groups)",
             "measured_ceilings": ceilings,
         },
