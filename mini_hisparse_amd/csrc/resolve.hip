@@ -40,7 +40,7 @@ namespace hs {
 
 constexpr int RT = 1024;      // threads of the single-workgroup phases
 constexpr int RW = 256;       // threads of the wide phases
-constexpr int RMAXB = 8;      // descriptors per launch
+constexpr int RMAXB = 16;     // descriptors per launch (passed by value: 16 x 200 bytes)
 constexpr int LRU_CHUNK = 32; // hot_rows <= 32768 = RT * LRU_CHUNK
 constexpr int MARK_BATCH = 8; // pages loaded per thread before use
 constexpr int MARK_TILE = 512;                // inputs per wave and tile (8 per lane)
@@ -50,6 +50,7 @@ struct ResolveBatch {
   hs_resolve_desc d[RMAXB];
   int count;
 };
+static_assert(sizeof(ResolveBatch) <= 4096, "resolver descriptors must fit the 4 KB kernel-argument block");
 
 struct ResolveWs {
   uint32_t* needbits;  // [wl] selected, host-backed, not resident

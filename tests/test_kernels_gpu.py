@@ -169,6 +169,53 @@ def test_resolver_random_matches_oracle(gpu, seed, length, P, S, n, res_frac):
     _assert_plan(plan32, tags32, lru32, expected)
 
 
+def test_resolver_batched_descriptors_match_oracle(gpu):
+    """hs_resolve_rows_batched over 17 (request, layer) descriptors of different sizes: one
+    launch of 16 descriptors and one of 1; every output of every request equals the oracle."""
+    import ctypes
+
+    from mini_hisparse_amd import _lib
+
+    lib = _lib.load()
+    cases = []
+    for i in range(17):
+        length, P, S, n = [(1000, 16, 512, 300), (4096, 16, 2048, 1500), (97, 4, 64, 40), (300, 7, 128, 100)][i % 4]
+        tables = resolver_tables(50 + i, length, P, S, resident_frac=0.1 * (i % 6))
+        positions = random_positions(150 + i, n, length)
+        cases.append((length, P, tables, positions))
+    descs = (_lib.ResolveDesc * len(cases))()
+    keep, total = [], 0
+    for d, (length, P, tables, positions) in zip(descs, cases):
+        t = {k: torch.from_numpy(np.ascontiguousarray(v)).to(gpu) for k, v in tables.items()}
+        pos = torch.from_numpy(positions).to(gpu)
+        n = pos.numel()
+        out = {name: torch.empty(n, dtype=torch.int64, device=gpu) for name in ("phys", "uphys", "mh", "md")}
+        out["counts"] = torch.empty(3, dtype=torch.int64, device=gpu)
+        d.positions, d.n, d.positions_i64 = pos.data_ptr(), n, 1
+        d.source, d.resident, d.n_pages = t["source"].data_ptr(), t["resident"].data_ptr(), t["source"].numel()
+        d.hot, d.hot_blocks = t["hot"].data_ptr(), t["hot"].numel()
+        d.tags, d.lru, d.hot_rows = t["tags"].data_ptr(), t["lru"].data_ptr(), t["tags"].numel()
+        d.length, d.page_size = length, P
+        d.physical, d.union_physical = out["phys"].data_ptr(), out["uphys"].data_ptr()
+        d.miss_host_rows, d.miss_device_rows = out["mh"].data_ptr(), out["md"].data_ptr()
+        d.counts = out["counts"].data_ptr()
+        total += lib.hs_resolve_workspace_bytes(n, length, d.n_pages, d.hot_rows)
+        keep.append((t, pos, out))
+    ws = torch.empty(total, dtype=torch.uint8, device=gpu)
+    _lib.check(lib.hs_resolve_rows_batched(descs, len(cases), ws.data_ptr(), total,
+                                           _lib.stream_handle(torch.device(gpu))), "hs_resolve_rows_batched")
+    torch.cuda.synchronize()
+    for (length, P, tables, positions), (t, _, out) in zip(cases, keep):
+        phys, mh, md, counts, tags_after, lru_after = oracle.resolve_rows(
+            positions, *[tables[k] for k in ("source", "resident", "hot", "tags", "lru")], length, P)
+        np.testing.assert_array_equal(out["phys"].cpu().numpy(), phys)
+        np.testing.assert_array_equal(out["mh"].cpu().numpy(), mh)
+        np.testing.assert_array_equal(out["md"].cpu().numpy(), md)
+        np.testing.assert_array_equal(out["counts"].cpu().numpy(), counts)
+        np.testing.assert_array_equal(t["tags"].cpu().numpy(), tags_after)
+        np.testing.assert_array_equal(t["lru"].cpu().numpy(), lru_after)
+
+
 def test_resolver_head_columns_and_multistep_trajectory(gpu):
     from mini_hisparse_amd.row_index import LogicalTopK, resolve_rows
 
