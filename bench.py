@@ -58,6 +58,10 @@ def parse_args():
     p.add_argument("--transfer-stream", action="store_true",
                    help="gather on a separate stream ordered by events (the reference's arrangement); "
                         "by default a single request group runs every stage on the compute stream")
+    p.add_argument("--no-prefetch", action="store_true",
+                   help="uniform-selector model workloads: run select, resolve and gather in layer order "
+                        "on the compute stream instead of prefetching every layer's at step start on a "
+                        "transfer stream (overlapping the dense layers)")
     p.add_argument("--graphs", action="store_true",
                    help="model workloads: replay each dense layer boundary as a captured HIP graph")
     p.add_argument("--no-cpu-baseline", action="store_true", help="skip the CPU oracle leg")
@@ -663,7 +667,8 @@ def run_model_workload(args, torch, device):
     print(f"[bench] {wl.name}: model + synthetic history (batch {wl.batch}, {wl.context} tokens)", file=sys.stderr, flush=True)
     model = random_model(wl, device, seed=args.seed)
     state = build_state(wl, device, seed=args.seed)
-    engine = BatchedDecodeEngine(model, state, wl.top_pages, selector=wl.selector, seed=args.seed, graphs=args.graphs)
+    engine = BatchedDecodeEngine(model, state, wl.top_pages, selector=wl.selector, seed=args.seed, graphs=args.graphs,
+                                 prefetch=not args.no_prefetch and wl.selector == "uniform")
     setup_s = time.perf_counter() - t0
     gen = torch.Generator(device=device).manual_seed(args.seed)
     tokens = torch.randint(0, wl.vocab, (wl.batch,), generator=gen, device=device)
@@ -717,6 +722,8 @@ def run_model_workload(args, torch, device):
                f"{wl.top_pages} pages resampled uniformly each step (tail page forced), shared by every head, ")
             + f"{wl.resident_fraction:.0%} of pages resident, hot_rows {wl.hot_rows}"
             + ("; dense layer boundaries replayed as HIP graphs" if engine.use_graphs else "")
+            + ("; every layer's select/resolve/gather prefetched on a transfer stream at step start "
+               "(stage times of those overlap the dense layers)" if engine.prefetch else "")
             + (f"; batch cut from {configured}: {configured} histories need "
                f"{configured * per_request / 2**30:.0f} GiB of pinned host memory, the box pins at most "
                f"64 GiB (budget {args.host_budget_gib:g} GiB)" if wl.batch < configured else ""),

@@ -44,11 +44,15 @@ class BatchedSparseDecode:
     """Quest -> union -> resolve -> gather -> attention for B requests of one layer."""
 
     def __init__(self, config, heads, top_pages, lengths, *, keep_sink=True, device="cuda", capacity_lengths=None,
-                 shared_selection=False):
+                 shared_selection=False, workspaces_from=None):
         """``capacity_lengths`` (default ``lengths``) sizes every buffer, so that later
         ``set_lengths`` calls up to those lengths (a decode run) allocate nothing.
         ``shared_selection``: every head of a request selects the same pages
-        (:meth:`select_pages`), so the union is one head's selection."""
+        (:meth:`select_pages`), so the union is one head's selection.
+        ``workspaces_from``: a decoder of the same shape whose scorer and attention
+        workspaces this one reuses (decoders whose ``select`` and ``attend`` calls run
+        one after another on one stream, e.g. one decoder per layer)."""
+        self._workspaces_from = workspaces_from
         self.config = config
         self.heads = heads
         self.kv_heads = config.kv_heads
@@ -88,7 +92,6 @@ class BatchedSparseDecode:
         self.row_counts = torch.empty((B, 3), dtype=i64, device=dev)
         lib = _lib.load()
         self.quest_ws_bytes = lib.hs_quest_workspace_bytes(B, self.heads, max(ceil(l / P) for l in caps))
-        self.quest_ws = torch.empty(self.quest_ws_bytes, dtype=torch.uint8, device=dev)
         self.resolve_ws_bytes = 0
         self.max_tables = None
         self.attend_ws_bytes = lib.hs_attend_workspace_bytes(
@@ -98,7 +101,13 @@ class BatchedSparseDecode:
             self.attend_ws_bytes,
             lib.hs_attend_workspace_bytes(_lib.HS_DTYPE_F32, B, self.heads, self.kv_heads, self.config.head_dim, self.entry_capacity),
         )
-        self.attend_ws = torch.empty(self.attend_ws_bytes, dtype=torch.uint8, device=dev)
+        donor = self._workspaces_from
+        if donor is not None and donor.quest_ws_bytes >= self.quest_ws_bytes and donor.attend_ws_bytes >= self.attend_ws_bytes:
+            self.quest_ws, self.quest_ws_bytes = donor.quest_ws, donor.quest_ws_bytes
+            self.attend_ws, self.attend_ws_bytes = donor.attend_ws, donor.attend_ws_bytes
+        else:
+            self.quest_ws = torch.empty(self.quest_ws_bytes, dtype=torch.uint8, device=dev)
+            self.attend_ws = torch.empty(self.attend_ws_bytes, dtype=torch.uint8, device=dev)
         self._len_arr = (ctypes.c_int64 * B)(*lengths)
         self._count_arr = (ctypes.c_int64 * B)(*self.counts)
         # ctypes arguments built once per buffer set and per table / bound / host set

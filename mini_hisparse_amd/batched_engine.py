@@ -267,8 +267,16 @@ class SparseKVState:
 class BatchedDecodeEngine:
     """Greedy decode of B requests, layer-major, over a :class:`SparseKVState`."""
 
+    PREFETCH_AHEAD = 4  # layers the prefetched transfers are issued ahead of the compute
+    # workgroups of a prefetched gather (all requests together): enough host reads in
+    # flight for the link while it overlaps the dense layers, few enough that its waiting
+    # waves leave the projections most CUs (32B stress shape, batch 3: 48 -> 22.5 ms per
+    # step, 96 -> 24.4, the unbounded ~430 -> 26.2)
+    PREFETCH_GATHER_WORKGROUPS = 48
+
     def __init__(self, model: MiniModel, state: SparseKVState, top_pages, *, max_tokens=None, keep_sink=True,
-                 selector="quest", seed=0, graphs=False, projections="auto", transfer_stream=False):
+                 selector="quest", seed=0, graphs=False, projections="auto", transfer_stream=False,
+                 prefetch=None):
         """``selector``: "quest" (per-head Quest pages over the bounds) or "uniform"
         (:func:`uniform_pages`, shared by every head, resampled each step).  ``graphs``:
         replay the dense part of each layer boundary as a HIP graph (when every per-layer
@@ -279,7 +287,15 @@ class BatchedDecodeEngine:
         separate stream ordered by events (the reference's arrangement, hybrid.py:443-477);
         the default gathers on the compute stream, because overlap does not pay on MI355X
         (host reads slow the kernels beside them) and each cross-stream hand-off costs
-        ~20 us of GPU time."""
+        ~20 us of GPU time.  ``prefetch`` (uniform selector only, on by default there): select, resolve and
+        gather every layer at the start of the step on a transfer stream, one decoder
+        (buffer set) per layer, so that the host reads overlap the dense layers; layer
+        l's attention waits for layer l's gather only, and the step's first transfer
+        waits for the previous step's last attention (the last reader of the hot rows)."""
+        if prefetch is None:
+            prefetch = selector == "uniform"
+        if prefetch and selector != "uniform":
+            raise ValueError("prefetch needs the uniform selector (Quest pages depend on the layer's query)")
         if projections not in ("auto", "kernel", "torch"):
             raise ValueError(f"unknown projections {projections!r}")
         if selector not in ("quest", "uniform"):
@@ -292,11 +308,14 @@ class BatchedDecodeEngine:
         self.model, self.state = model, state
         self.device = state.device
         caps = [max_tokens or state.pages * state.config.page_size] * state.batch
-        self.dec = BatchedSparseDecode(
+        decoder = lambda donor=None: BatchedSparseDecode(
             state.config, cfg.num_attention_heads, top_pages, [max(1, l) for l in state.lengths],
             keep_sink=keep_sink, device=self.device, capacity_lengths=caps,
-            shared_selection=selector == "uniform",
+            shared_selection=selector == "uniform", workspaces_from=donor,
         )
+        self.dec = decoder()
+        self.prefetch = prefetch
+        self.decs = [self.dec] + [decoder(self.dec) for _ in range(state.layers - 1)] if prefetch else None
         self.selector = selector
         self._sampler = torch.Generator(device=self.device).manual_seed(seed)
         if state.hot_rows < self.dec.capacity:
@@ -306,16 +325,41 @@ class BatchedDecodeEngine:
                 f"hot_rows {state.hot_rows} below the union bound {self.dec.capacity} of "
                 f"{cfg.num_attention_heads} heads x {top_pages} pages"
             )
-        self.transfer = torch.cuda.Stream(self.device) if transfer_stream else None
+        self.transfer = torch.cuda.Stream(self.device) if transfer_stream or prefetch else None
         self._pack_projections()
         self._choose_projections(projections)
         self._host_alias = [(ctypes.c_void_p * state.batch)(*([a.data_ptr()] * state.batch)) for a in state.alias]
         self.positions = torch.tensor(state.lengths, dtype=torch.int64, device=self.device)
         # per layer: resolved (compute -> transfer) and gathered (transfer -> compute)
         self._handoff = [(torch.cuda.Event(), torch.cuda.Event()) for _ in range(state.layers)]
+        self._step_start = torch.cuda.Event()
         self._static_buffers()
         self.use_graphs = graphs and all(self.projection_kernel[n] for n in ("qkv", "o_proj", "gate_up", "down"))
         self._graphs = None
+
+    def decoder(self, layer):
+        """The decoder (selection, resolver and attention buffers) that serves `layer`."""
+        return self.decs[layer] if self.decs is not None else self.dec
+
+    def _prefetch(self, index, sampled, transfer, mark):
+        """Layer `index`'s select, resolve and gather on `transfer`; returns its stage
+        marks.  The transfer stream was ordered (at step start) after everything then
+        queued on the compute stream: the step's tail-page table updates and page draws,
+        and the previous step's attention, the last reader of the hot rows the gathers
+        overwrite.  Layers are issued in order, a few ahead of the compute stream's."""
+        st, dec = self.state, self.decs[index]
+        with torch.cuda.stream(transfer):
+            m = {"select": [mark(transfer)]}
+            dec.select_pages(sampled[index])
+            m["select"].append(mark(transfer))
+            m["resolve"] = [m["select"][1]]
+            dec.resolve(st.tables[index], row_stats=st.row_stats)
+            m["resolve"].append(mark(transfer))
+            m["gather"] = [m["resolve"][1]]
+            dec.gather(st.alias[index], st.pool, transfer, grid_x=ceil(self.PREFETCH_GATHER_WORKGROUPS / st.batch))
+            m["gather"].append(mark(transfer))
+            self._handoff[index][1].record(transfer)
+        return m
 
     def _static_buffers(self):
         """Fixed buffers of the dense stages, so that their launches can be replayed."""
@@ -473,15 +517,14 @@ class BatchedDecodeEngine:
         cfg = model.config
         positions = list(st.lengths)
         st.open_tail_pages(positions)
-        dec.set_lengths([p + 1 for p in positions])
+        for d in self.decs or (dec,):
+            d.set_lengths([p + 1 for p in positions])
         sampled = None
         if self.selector == "uniform":
             sampled = uniform_pages([p + 1 for p in positions], st.config.page_size, dec.top, st.layers,
                                     self._sampler, self.device)
         compute = torch.cuda.current_stream(self.device)
         L = st.layers
-        self._x.copy_(model.model.embed_tokens(tokens))
-        graphs = self._graphs
 
         def mark(stream):
             if timer is None:
@@ -489,6 +532,17 @@ class BatchedDecodeEngine:
             event = torch.cuda.Event(enable_timing=True)
             event.record(stream)
             return event
+
+        prefetched = None
+        if self.prefetch:
+            self._step_start.record(compute)
+            self.transfer.wait_event(self._step_start)
+            sampled.record_stream(self.transfer)
+            # issued PREFETCH_AHEAD layers ahead of the compute stream, so that neither
+            # stream waits for the host to issue the other's launches
+            prefetched = [self._prefetch(i, sampled, self.transfer, mark) for i in range(min(L, self.PREFETCH_AHEAD))]
+        self._x.copy_(model.model.embed_tokens(tokens))
+        graphs = self._graphs
 
         def boundary(index):
             if graphs is not None:
@@ -498,6 +552,8 @@ class BatchedDecodeEngine:
 
         q, k, v = self._q, self._k, self._v
         for index in range(L):
+            if prefetched is not None and index + self.PREFETCH_AHEAD < L:
+                prefetched.append(self._prefetch(index + self.PREFETCH_AHEAD, sampled, self.transfer, mark))
             marks = {"dense": [mark(compute)]}
             boundary(index)
             marks["dense"].append(mark(compute))
@@ -505,26 +561,31 @@ class BatchedDecodeEngine:
             self._append(index, k, v, positions)
             lo, hi = st.bounds[index]
             marks["append"].append(mark(compute))
-            marks["select"] = [marks["append"][1]]
-            if sampled is None:
-                dec.select(q, lo, hi)
+            if prefetched is not None:
+                dec = self.decs[index]
+                marks.update(prefetched[index])
+                compute.wait_event(self._handoff[index][1])
             else:
-                dec.select_pages(sampled[index])
-            marks["select"].append(mark(compute))
-            marks["resolve"] = [marks["select"][1]]
-            dec.resolve(st.tables[index], row_stats=st.row_stats)
-            marks["resolve"].append(mark(compute))
-            transfer = self.transfer if self.transfer is not None else compute
-            if transfer is not compute:
-                resolved, ready = self._handoff[index]
-                resolved.record(compute)
-                transfer.wait_event(resolved)
-            marks["gather"] = [mark(transfer)]
-            dec.gather(st.alias[index], st.pool, transfer)
-            marks["gather"].append(mark(transfer))
-            if transfer is not compute:
-                ready.record(transfer)
-                compute.wait_event(ready)
+                marks["select"] = [marks["append"][1]]
+                if sampled is None:
+                    dec.select(q, lo, hi)
+                else:
+                    dec.select_pages(sampled[index])
+                marks["select"].append(mark(compute))
+                marks["resolve"] = [marks["select"][1]]
+                dec.resolve(st.tables[index], row_stats=st.row_stats)
+                marks["resolve"].append(mark(compute))
+                transfer = self.transfer if self.transfer is not None else compute
+                if transfer is not compute:
+                    resolved, ready = self._handoff[index]
+                    resolved.record(compute)
+                    transfer.wait_event(resolved)
+                marks["gather"] = [mark(transfer)]
+                dec.gather(st.alias[index], st.pool, transfer)
+                marks["gather"].append(mark(transfer))
+                if transfer is not compute:
+                    ready.record(transfer)
+                    compute.wait_event(ready)
             marks["attend"] = [mark(compute)]
             out = dec.attend(q, st.pool, out=self._attn_out)
             marks["attend"].append(mark(compute))

@@ -52,7 +52,7 @@ def test_batched_engine_layers_match_oracle(gpu, overrides, transfer_stream):
         tokens = engine.step(
             tokens,
             lambda l, q, k, v, out: records.append(
-                (l, q.clone(), out.clone(), engine.dec.pages.clone(), engine.dec.union_count.clone())
+                (l, q.clone(), out.clone(), engine.decoder(l).pages.clone(), engine.decoder(l).union_count.clone())
             ),
         )
         torch.cuda.synchronize()
@@ -114,17 +114,23 @@ def test_uniform_pages_draws_distinct_pages_with_the_tail():
 
 
 @pytest.mark.gpu
-def test_batched_engine_uniform_selection_matches_oracle(gpu):
+@pytest.mark.parametrize("prefetch", [False, True])
+def test_batched_engine_uniform_selection_matches_oracle(gpu, prefetch):
     """The miss-heavy stress path: pages resampled every step and shared by every head,
-    then union, resolver, gather and attention as for Quest selections."""
+    then union, resolver, gather and attention as for Quest selections.  With
+    ``prefetch`` every layer's select, resolve and gather run at step start on the
+    transfer stream (one decoder per layer), overlapping the dense layers."""
     from mini_hisparse_amd.batched_engine import BatchedDecodeEngine, build_state, random_model
     from mini_hisparse_amd.selection import union_bound
 
     wl = tiny(selector="uniform", hot_rows=2 * union_bound(40 * 16 + 23, 16, 6, 1), resident_fraction=0.4)
     model = random_model(wl, gpu, seed=1)
     state = build_state(wl, gpu, seed=2)
-    engine = BatchedDecodeEngine(model, state, wl.top_pages, selector="uniform", seed=4)
+    engine = BatchedDecodeEngine(model, state, wl.top_pages, selector="uniform", seed=4, prefetch=prefetch)
     assert engine.dec.capacity == 6 * 16  # one head's selection bounds the union
+    if prefetch:
+        assert len({id(engine.decoder(l)) for l in range(wl.layers)}) == wl.layers
+        assert all(engine.decoder(l).attend_ws is engine.dec.attend_ws for l in range(wl.layers))
     L, B, C, P = wl.layers, wl.batch, state.pages, wl.page_size
     Hkv, D = wl.kv_heads, wl.head_dim
     records = []
@@ -135,7 +141,7 @@ def test_batched_engine_uniform_selection_matches_oracle(gpu):
         tokens = engine.step(
             tokens,
             lambda l, q, k, v, out: records.append(
-                (l, q.clone(), out.clone(), engine.dec.pages.clone(), engine.dec.union_count.clone())
+                (l, q.clone(), out.clone(), engine.decoder(l).pages.clone(), engine.decoder(l).union_count.clone())
             ),
         )
         torch.cuda.synchronize()
@@ -161,6 +167,42 @@ def test_batched_engine_uniform_selection_matches_oracle(gpu):
     assert sum(stats) == unions
     assert stats[2] > stats[1]  # resampling every step: misses outnumber hot hits
     assert len(drawn) >= 8 * L * B  # fresh draws each step (5 per step; about 13 distinct expected)
+
+
+@pytest.mark.gpu
+def test_prefetched_uniform_steps_equal_in_order_steps(gpu):
+    """Prefetching every layer's select/resolve/gather at step start changes only the
+    launch order across streams: tokens, attention outputs, the resolver's row
+    statistics and every hot region's tags and LRU equal the in-order engine's bit for bit."""
+    from mini_hisparse_amd.batched_engine import BatchedDecodeEngine, build_state, random_model
+    from mini_hisparse_amd.selection import union_bound
+
+    wl = tiny(selector="uniform", hot_rows=2 * union_bound(40 * 16 + 23, 16, 6, 1), resident_fraction=0.4)
+    runs = []
+    for prefetch in (False, True):
+        model = random_model(wl, gpu, seed=1)
+        state = build_state(wl, gpu, seed=2)
+        engine = BatchedDecodeEngine(model, state, wl.top_pages, selector="uniform", seed=4, prefetch=prefetch)
+        outs, toks = [], []
+        tokens = torch.tensor([1, 2, 3], device=gpu)
+        for step in range(4):
+            tokens = engine.step(tokens, lambda l, q, k, v, out: outs.append(out.clone()))
+            toks.append(tokens.clone())
+        torch.cuda.synchronize()
+        runs.append((outs, toks, state.row_stats.clone(), (state.tags.clone(), state.lru.clone())))
+    (eo, et, es, etab), (po, pt, ps, ptab) = runs
+    assert len(eo) == len(po) == 4 * wl.layers
+    assert all(torch.equal(a, b) for a, b in zip(eo, po))
+    assert all(torch.equal(a, b) for a, b in zip(et, pt))
+    assert torch.equal(es, ps)
+    assert torch.equal(etab[0], ptab[0]) and torch.equal(etab[1], ptab[1])
+
+
+def test_prefetch_needs_the_uniform_selector():
+    from mini_hisparse_amd.batched_engine import BatchedDecodeEngine
+
+    with pytest.raises(ValueError, match="uniform"):
+        BatchedDecodeEngine(None, None, 4, prefetch=True)
 
 
 @pytest.mark.gpu
