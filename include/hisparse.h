@@ -76,7 +76,8 @@ int hs_host_alias(const void* host_ptr, void** device_ptr);
 int64_t hs_quest_workspace_bytes(int64_t batch, int64_t heads, int64_t max_pages);
 
 /*
- * Quest page scores and per-head top-k for `batch` (<= 16) requests.
+ * Quest page scores and per-head top-k for `batch` requests (launched in
+ * chunks of at most 16, in order on `stream`).
  * Replaces: quest_selection (mini_hisparse/selection.py:80-101) up to the
  * chosen page ids (:100).
  *   query      [batch, heads, head_dim] in query_dtype (HS_DTYPE_*: the model
@@ -115,6 +116,7 @@ int hs_quest_topk(const void* query, int64_t q_stride_b, int64_t q_stride_h,
  *                 [batch, kv_heads]
  *   status        int32 flag OR-ed with 1 (union over capacity) / 2 (entries
  *                 over capacity); the caller clears it.
+ * Any batch size: launched in chunks of at most 16 requests, in order on `stream`.
  */
 int hs_build_union(const int32_t* pages, int64_t p_stride_b, int64_t top, const int64_t* lengths,
                    int64_t page_size, int64_t batch, int64_t heads, int64_t kv_heads,
@@ -185,8 +187,9 @@ int hs_gather_rows(const void* host_alias, void* pool, const int64_t* miss_host_
                    const int64_t* miss_device_rows, int64_t n, const int64_t* miss_count,
                    int64_t page_size, int64_t row_bytes, hs_stream_t stream);
 
-/* The same for `batch` (<= 16) plans in one launch; every array argument is a
- * host array of per-request values; grid_x <= 0 picks the default grid. */
+/* The same for `batch` plans, one launch per chunk of at most 16; every array
+ * argument is a host array of per-request values; grid_x (workgroups per plan)
+ * <= 0 picks the default grid. */
 int hs_gather_rows_batched(const void* const* host_alias, void* pool,
                            const int64_t* const* miss_host_rows,
                            const int64_t* const* miss_device_rows,
@@ -197,7 +200,7 @@ int hs_gather_rows_batched(const void* const* host_alias, void* pool,
 /* ------------------------------------------------------- append (producer) */
 
 /*
- * Append one token's K and V rows for each of `batch` (<= 32) (request, layer)
+ * Append one token's K and V rows for each of `batch` (request, layer)
  * pairs: the decode-step producer of the Quest bounds.
  * Replaces: the single-token case of HostStore.append
  * (mini_hisparse/storage.py:246-319): the new rows go to their pool row; the
@@ -215,6 +218,7 @@ int hs_gather_rows_batched(const void* const* host_alias, void* pool,
  *                 when host_rows is NULL); host_rows host array [batch], < 0 skips the
  *                 mirror; host_pool_rows bounds every host row
  *   minimum, maximum  host arrays [batch] of device pointers to the tail page's bounds
+ * Any batch size: launched in chunks of at most 32 pairs, in order on `stream`.
  */
 int hs_append_rows(const void* k, const void* v, int64_t kv_stride_b, void* pool, int64_t pool_rows,
                    int32_t dtype, int64_t page_size, int64_t kv_heads, int64_t head_dim,

@@ -99,11 +99,13 @@ __global__ __launch_bounds__(AT) void append_kernel(AppendArgs a) {
 
 using namespace hs;
 
-extern "C" int hs_append_rows(const void* k, const void* v, int64_t kv_stride_b, void* pool, int64_t pool_rows,
-                              int32_t dtype, int64_t page_size, int64_t kv_heads, int64_t head_dim,
-                              const int64_t* device_rows, const void* const* host_alias,
-                              const int64_t* host_rows, int64_t host_pool_rows, void* const* minimum,
-                              void* const* maximum, int32_t batch, hipStream_t stream) {
+// At most AMAXB rows (their pointers travel in the kernel arguments);
+// hs_append_rows cuts larger batches into such chunks.
+static int append_chunk(const void* k, const void* v, int64_t kv_stride_b, void* pool, int64_t pool_rows,
+                        int32_t dtype, int64_t page_size, int64_t kv_heads, int64_t head_dim,
+                        const int64_t* device_rows, const void* const* host_alias, const int64_t* host_rows,
+                        int64_t host_pool_rows, void* const* minimum, void* const* maximum, int32_t batch,
+                        hipStream_t stream) {
   HS_CHECK_ARG(batch >= 1 && batch <= AMAXB, "append batch must be in [1, %d]", AMAXB);
   HS_CHECK_ARG(valid_dtype(dtype), "invalid dtype code %d", dtype);
   HS_CHECK_ARG(k && v && pool && device_rows && minimum && maximum, "null append pointer");
@@ -141,5 +143,33 @@ extern "C" int hs_append_rows(const void* k, const void* v, int64_t kv_stride_b,
   else if (dtype == HS_DTYPE_F16) hipLaunchKernelGGL(append_kernel<HS_DTYPE_F16>, grid, dim3(AT), 0, stream, a);
   else hipLaunchKernelGGL(append_kernel<HS_DTYPE_F32>, grid, dim3(AT), 0, stream, a);
   HS_CHECK_LAUNCH("append");
+  return HS_OK;
+}
+
+extern "C" int hs_append_rows(const void* k, const void* v, int64_t kv_stride_b, void* pool, int64_t pool_rows,
+                              int32_t dtype, int64_t page_size, int64_t kv_heads, int64_t head_dim,
+                              const int64_t* device_rows, const void* const* host_alias,
+                              const int64_t* host_rows, int64_t host_pool_rows, void* const* minimum,
+                              void* const* maximum, int32_t batch, hipStream_t stream) {
+  HS_CHECK_ARG(batch >= 1, "append batch must be positive");
+  HS_CHECK_ARG(valid_dtype(dtype), "invalid dtype code %d", dtype);
+  HS_CHECK_ARG(k && v && pool && device_rows && minimum && maximum, "null append pointer");
+  for (int32_t i = 0; i < batch; ++i) {  // every row, before the first launch
+    HS_CHECK_ARG(device_rows[i] >= 0 && device_rows[i] < pool_rows, "append device row %lld outside the pool",
+                 static_cast<long long>(device_rows[i]));
+    HS_CHECK_ARG(!host_rows || host_rows[i] < host_pool_rows, "append host row %lld outside the host pool",
+                 static_cast<long long>(host_rows[i]));
+    HS_CHECK_ARG(minimum[i] && maximum[i], "null bounds pointer");
+    HS_CHECK_ARG(!host_rows || host_rows[i] < 0 || (host_alias && host_alias[i]), "a host row needs a host alias");
+  }
+  const int64_t step = kv_stride_b * elem_bytes(dtype);
+  for (int32_t s0 = 0; s0 < batch; s0 += AMAXB) {
+    const int32_t c = batch - s0 < AMAXB ? batch - s0 : AMAXB;
+    const int rc = append_chunk(static_cast<const char*>(k) + s0 * step, static_cast<const char*>(v) + s0 * step,
+                                kv_stride_b, pool, pool_rows, dtype, page_size, kv_heads, head_dim, device_rows + s0,
+                                host_alias ? host_alias + s0 : nullptr, host_rows ? host_rows + s0 : nullptr,
+                                host_pool_rows, minimum + s0, maximum + s0, c, stream);
+    if (rc != HS_OK) return rc;
+  }
   return HS_OK;
 }

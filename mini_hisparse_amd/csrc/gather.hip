@@ -128,12 +128,12 @@ extern "C" int hs_host_alias(const void* host_ptr, void** device_ptr) {
   return HS_OK;
 }
 
-extern "C" int hs_gather_rows_batched(const void* const* host_alias, void* pool,
-                                      const int64_t* const* miss_host_rows,
-                                      const int64_t* const* miss_device_rows,
-                                      const int64_t* const* miss_counts, const int64_t* n,
-                                      int32_t batch, int64_t page_size, int64_t row_bytes,
-                                      int32_t grid_x, hipStream_t stream) {
+// At most GMAXB plans (their pointers travel in the kernel arguments);
+// hs_gather_rows_batched cuts larger batches into such chunks.
+static int gather_chunk(const void* const* host_alias, void* pool, const int64_t* const* miss_host_rows,
+                        const int64_t* const* miss_device_rows, const int64_t* const* miss_counts,
+                        const int64_t* n, int32_t batch, int64_t page_size, int64_t row_bytes, int32_t grid_x,
+                        hipStream_t stream) {
   HS_CHECK_ARG(batch >= 1 && batch <= GMAXB, "gather batch must be in [1, %d]", GMAXB);
   HS_CHECK_ARG(pool && host_alias && miss_host_rows && miss_device_rows && n, "null gather pointer");
   HS_CHECK_ARG(page_size >= 1 && row_bytes >= 2 && row_bytes % 2 == 0, "invalid gather row shape");
@@ -196,6 +196,26 @@ extern "C" int hs_gather_rows_batched(const void* const* host_alias, void* pool,
     }
   }
   HS_CHECK_LAUNCH("gather");
+  return HS_OK;
+}
+
+extern "C" int hs_gather_rows_batched(const void* const* host_alias, void* pool,
+                                      const int64_t* const* miss_host_rows,
+                                      const int64_t* const* miss_device_rows,
+                                      const int64_t* const* miss_counts, const int64_t* n,
+                                      int32_t batch, int64_t page_size, int64_t row_bytes,
+                                      int32_t grid_x, hipStream_t stream) {
+  HS_CHECK_ARG(batch >= 1, "gather batch must be positive");
+  HS_CHECK_ARG(host_alias && miss_host_rows && miss_device_rows && n, "null gather pointer");
+  for (int32_t i = 0; i < batch; ++i)  // every plan, before the first launch
+    HS_CHECK_ARG(host_alias[i] && miss_host_rows[i] && miss_device_rows[i], "null gather plan");
+  for (int32_t s0 = 0; s0 < batch; s0 += GMAXB) {
+    const int32_t c = batch - s0 < GMAXB ? batch - s0 : GMAXB;
+    const int rc = gather_chunk(host_alias + s0, pool, miss_host_rows + s0, miss_device_rows + s0,
+                                miss_counts ? miss_counts + s0 : nullptr, n + s0, c, page_size, row_bytes,
+                                grid_x, stream);
+    if (rc != HS_OK) return rc;
+  }
   return HS_OK;
 }
 

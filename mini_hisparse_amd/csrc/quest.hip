@@ -568,13 +568,15 @@ extern "C" int64_t hs_quest_workspace_bytes(int64_t batch, int64_t heads, int64_
   return ((batch * heads * max_pages * 4) + 255) & ~static_cast<int64_t>(255);
 }
 
-extern "C" int hs_quest_topk(const void* query, int64_t q_stride_b, int64_t q_stride_h,
-                             int32_t query_dtype, const void* const* minimum,
-                             const void* const* maximum, int32_t kv_dtype,
-                             const int64_t* page_counts, int64_t batch, int64_t heads,
-                             int64_t kv_heads, int64_t head_dim, int64_t top, int32_t keep_sink,
-                             int32_t* out_pages, int64_t out_stride_b, void* workspace,
-                             int64_t workspace_bytes, hipStream_t stream) {
+// At most QMAXB requests (their bounds pointers and page counts travel in the
+// kernel arguments); hs_quest_topk cuts larger batches into such chunks.
+static int quest_topk_chunk(const void* query, int64_t q_stride_b, int64_t q_stride_h,
+                            int32_t query_dtype, const void* const* minimum,
+                            const void* const* maximum, int32_t kv_dtype,
+                            const int64_t* page_counts, int64_t batch, int64_t heads,
+                            int64_t kv_heads, int64_t head_dim, int64_t top, int32_t keep_sink,
+                            int32_t* out_pages, int64_t out_stride_b, void* workspace,
+                            int64_t workspace_bytes, hipStream_t stream) {
   HS_CHECK_ARG(top >= 1 && heads >= 1 && kv_heads >= 1 && heads % kv_heads == 0,
                "invalid page budget or GQA shape");
   HS_CHECK_ARG(batch >= 1 && batch <= QMAXB, "quest batch must be in [1, %d]", QMAXB);
@@ -673,13 +675,15 @@ extern "C" int hs_quest_topk(const void* query, int64_t q_stride_b, int64_t q_st
   return HS_OK;
 }
 
-extern "C" int hs_build_union(const int32_t* pages, int64_t p_stride_b, int64_t top,
-                              const int64_t* lengths, int64_t page_size, int64_t batch,
-                              int64_t heads, int64_t kv_heads, int32_t* positions,
-                              int64_t pos_capacity, int64_t* head_columns, int64_t width,
-                              int32_t* union_count, int32_t* entry_columns,
-                              uint32_t* entry_masks, int64_t entry_capacity,
-                              int32_t* entry_counts, int32_t* status, hipStream_t stream) {
+// At most QMAXB requests (their lengths travel in the kernel arguments);
+// hs_build_union cuts larger batches into such chunks.
+static int build_union_chunk(const int32_t* pages, int64_t p_stride_b, int64_t top,
+                             const int64_t* lengths, int64_t page_size, int64_t batch,
+                             int64_t heads, int64_t kv_heads, int32_t* positions,
+                             int64_t pos_capacity, int64_t* head_columns, int64_t width,
+                             int32_t* union_count, int32_t* entry_columns,
+                             uint32_t* entry_masks, int64_t entry_capacity,
+                             int32_t* entry_counts, int32_t* status, hipStream_t stream) {
   HS_CHECK_ARG(batch >= 1 && batch <= QMAXB, "union batch must be in [1, %d]", QMAXB);
   HS_CHECK_ARG(top >= 1 && page_size >= 1 && heads >= 1 && kv_heads >= 1 && heads % kv_heads == 0,
                "invalid union shape");
@@ -732,5 +736,65 @@ extern "C" int hs_build_union(const int32_t* pages, int64_t p_stride_b, int64_t 
   hipLaunchKernelGGL(build_union_kernel, dim3(static_cast<unsigned>(kv_heads + 1 + heads), static_cast<unsigned>(batch)),
                      dim3(UT), lds, stream, a);
   HS_CHECK_LAUNCH("union builder");
+  return HS_OK;
+}
+
+extern "C" int hs_quest_topk(const void* query, int64_t q_stride_b, int64_t q_stride_h,
+                             int32_t query_dtype, const void* const* minimum,
+                             const void* const* maximum, int32_t kv_dtype,
+                             const int64_t* page_counts, int64_t batch, int64_t heads,
+                             int64_t kv_heads, int64_t head_dim, int64_t top, int32_t keep_sink,
+                             int32_t* out_pages, int64_t out_stride_b, void* workspace,
+                             int64_t workspace_bytes, hipStream_t stream) {
+  HS_CHECK_ARG(batch >= 1, "quest batch must be positive");
+  HS_CHECK_ARG(valid_dtype(query_dtype), "invalid query dtype code %d", query_dtype);
+  HS_CHECK_ARG(query && minimum && maximum && page_counts && out_pages, "null quest pointer");
+  // every request is checked before the first launch, so an invalid one launches nothing
+  for (int64_t i = 0; i < batch; ++i) {
+    HS_CHECK_ARG(page_counts[i] >= 1, "cannot select pages of an empty history");
+    HS_CHECK_ARG(minimum[i] && maximum[i], "null bounds pointer");
+  }
+  const int64_t qbytes = query_dtype == HS_DTYPE_F32 ? 4 : 2;
+  // chunks run in stream order and each reuses the workspace, which holds the
+  // scores of at most the whole batch
+  for (int64_t s0 = 0; s0 < batch; s0 += QMAXB) {
+    const int64_t n = batch - s0 < QMAXB ? batch - s0 : QMAXB;
+    const int rc = quest_topk_chunk(static_cast<const char*>(query) + s0 * q_stride_b * qbytes, q_stride_b,
+                                    q_stride_h, query_dtype, minimum + s0, maximum + s0, kv_dtype,
+                                    page_counts + s0, n, heads, kv_heads, head_dim, top, keep_sink,
+                                    out_pages + s0 * out_stride_b, out_stride_b, workspace, workspace_bytes,
+                                    stream);
+    if (rc != HS_OK) return rc;
+  }
+  return HS_OK;
+}
+
+extern "C" int hs_build_union(const int32_t* pages, int64_t p_stride_b, int64_t top,
+                              const int64_t* lengths, int64_t page_size, int64_t batch,
+                              int64_t heads, int64_t kv_heads, int32_t* positions,
+                              int64_t pos_capacity, int64_t* head_columns, int64_t width,
+                              int32_t* union_count, int32_t* entry_columns,
+                              uint32_t* entry_masks, int64_t entry_capacity,
+                              int32_t* entry_counts, int32_t* status, hipStream_t stream) {
+  HS_CHECK_ARG(batch >= 1, "union batch must be positive");
+  HS_CHECK_ARG(top >= 1 && page_size >= 1 && lengths, "invalid union shape");
+  for (int64_t i = 0; i < batch; ++i) {  // every request, before the first launch
+    HS_CHECK_ARG(lengths[i] >= 1, "cannot build a union over an empty history");
+    HS_CHECK_ARG(ceil_div(lengths[i], page_size) <= UMAXPAGES, "too many pages for the union builder");
+    const int64_t count = ceil_div(lengths[i], page_size);
+    const int64_t k = top < count ? top : count;
+    const int64_t W = (k - 1) * page_size + (lengths[i] - (count - 1) * page_size);
+    HS_CHECK_ARG(W <= width, "head column width %lld below the selection width %lld",
+                 static_cast<long long>(width), static_cast<long long>(W));
+  }
+  for (int64_t s0 = 0; s0 < batch; s0 += QMAXB) {
+    const int64_t n = batch - s0 < QMAXB ? batch - s0 : QMAXB;
+    const int rc = build_union_chunk(
+        pages + s0 * p_stride_b, p_stride_b, top, lengths + s0, page_size, n, heads, kv_heads,
+        positions + s0 * pos_capacity, pos_capacity, head_columns + s0 * heads * width, width, union_count + s0,
+        entry_columns + s0 * kv_heads * entry_capacity, entry_masks + s0 * kv_heads * entry_capacity,
+        entry_capacity, entry_counts + s0 * kv_heads, status, stream);
+    if (rc != HS_OK) return rc;
+  }
   return HS_OK;
 }

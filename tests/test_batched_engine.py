@@ -33,7 +33,14 @@ def tiny(**overrides):
 @pytest.mark.gpu
 @pytest.mark.parametrize(
     "overrides,transfer_stream",
-    [({}, False), ({}, True), ({"heads": 16, "kv_heads": 2, "head_dim": 64, "hidden": 1024}, False)],
+    [
+        ({}, False),
+        ({}, True),
+        ({"heads": 16, "kv_heads": 2, "head_dim": 64, "hidden": 1024}, False),
+        # more requests than one launch of the scorer, union builder, resolver and gather
+        # (16) or of the append (32) takes: each entry point runs them in chunks
+        ({"batch": 34}, False),
+    ],
 )
 def test_batched_engine_layers_match_oracle(gpu, overrides, transfer_stream):
     from mini_hisparse_amd.batched_engine import BatchedDecodeEngine, build_state, random_model
@@ -45,7 +52,7 @@ def test_batched_engine_layers_match_oracle(gpu, overrides, transfer_stream):
     L, B, C, P = wl.layers, wl.batch, state.pages, wl.page_size
     Hkv, D = wl.kv_heads, wl.head_dim
     records = []
-    tokens = torch.tensor([1, 2, 3], device=gpu)
+    tokens = torch.arange(1, B + 1, device=gpu)
     unions = 0
     for step in range(3):  # positions 639 (last row of a page), 640 (opens a page), 641
         records.clear()
