@@ -581,12 +581,19 @@ def cpu_baseline_all_cores(torch, w, max_workers=16):
     }
 
 
-PMC_SUMMARY = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "microbench_pmc.txt")
+PROFILES = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles")
+PMC_SUMMARY = os.path.join(PROFILES, "microbench_pmc.txt")
+# counter summaries per single-layer workload (the step the bench line times)
+PMC_SUMMARIES = {
+    "microbench": (PMC_SUMMARY, "microbench step (BASELINE configs[1]), batch 8, bf16"),
+    "qwen2.5-7b-layer": (os.path.join(PROFILES, "qwen2.5-7b_layer_pmc.txt"),
+                         "one layer of the north_star step (Qwen2.5-7B heads, 128k histories), batch 16, bf16"),
+}
 ROOFLINE_KERNELS = ("attend_mfma_kernel", "attend_merge_kernel")
 CALIBRATION_BYTES = 1 << 30  # hbm_copy_gbs: a plain device-to-device copy of 1 GiB
 
 
-def summarize_pmc(fetch_dir, write_dir, out_path=PMC_SUMMARY):
+def summarize_pmc(fetch_dir, write_dir, workload="microbench"):
     """Per-dispatch FETCH_SIZE / WRITE_SIZE of each hs:: kernel, scaled by what the
     same counters read for the 1 GiB device copy this script makes."""
     import csv
@@ -616,12 +623,14 @@ def summarize_pmc(fetch_dir, write_dir, out_path=PMC_SUMMARY):
     for i, (name, v) in write.items():
         if "hs::" in name:
             per[name.split("(")[0].replace("void ", "")][1].append(v)
+    out_path, title = PMC_SUMMARIES[workload]
+    flag = "" if workload == "microbench" else f" --workload {workload}"
     lines = [
-        "# rocprofv3 --pmc summary: microbench step (BASELINE configs[1]), batch 8, bf16",
+        f"# rocprofv3 --pmc summary: {title}",
         "# FETCH_SIZE and WRITE_SIZE (KiB per dispatch) from two runs of",
-        "#   rocprofv3 --pmc FETCH_SIZE -f csv -d <dir> -o bench -- python bench.py --steps 3 --warmup 1 --no-cpu-baseline",
-        "#   rocprofv3 --pmc WRITE_SIZE -f csv -d <dir> -o bench -- python bench.py --steps 3 --warmup 1 --no-cpu-baseline",
-        "# summarised by: python bench.py --summarize-pmc <fetch dir> <write dir>",
+        f"#   rocprofv3 --pmc FETCH_SIZE -f csv -d <dir> -o bench -- python bench.py{flag} --steps 3 --warmup 1 --no-cpu-baseline",
+        f"#   rocprofv3 --pmc WRITE_SIZE -f csv -d <dir> -o bench -- python bench.py{flag} --steps 3 --warmup 1 --no-cpu-baseline",
+        f"# summarised by: python bench.py{flag} --summarize-pmc <fetch dir> <write dir>",
         f"# calibration: the 1 GiB device-to-device copy of hbm_copy_gbs ({len(calib)} dispatches) reads "
         f"FETCH_SIZE x{fetch_scale:.3f}, WRITE_SIZE x{write_scale:.3f} of its true bytes",
         f"calibration fetch_scale {fetch_scale:.4f} write_scale {write_scale:.4f}",
@@ -841,7 +850,9 @@ def run_model_workload(args, torch, device):
 def main():
     args = parse_args()
     if args.summarize_pmc:
-        summarize_pmc(*args.summarize_pmc)
+        if args.workload not in PMC_SUMMARIES:
+            raise SystemExit(f"counter summaries are kept for {sorted(PMC_SUMMARIES)}")
+        summarize_pmc(*args.summarize_pmc, workload=args.workload)
         return
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on exactly one GPU; --gpus above 1 is not supported "
@@ -887,14 +898,16 @@ def main():
     ceilings = attention_ceilings(torch, w, bytes_["attention"])
     att_gbs = bytes_["attention"] / (stages["attention"] * 1e-3) / 1e9
     # the committed counter summary was taken on the default microbench run
-    counters_apply = args.workload == "microbench" and args.batch == shape.batch
+    # the committed counter summary of this workload, when its shape is the one profiled
+    pmc_path = PMC_SUMMARIES[args.workload][0] if args.workload in PMC_SUMMARIES else None
+    counters_apply = pmc_path is not None and args.batch == shape.batch
 
     def hbm_line(stage, nbytes, pmc_kernels, **extra):
         """A stage's algorithmic-byte rate and, from the committed counter summary, the HBM
         bytes its kernels move per launch and the rate those give (the counter evidence)."""
         ms = stages[stage]
         gbs = nbytes / (ms * 1e-3) / 1e9
-        traffic = pmc_traffic(pmc_kernels) if counters_apply else None
+        traffic = pmc_traffic(pmc_kernels, pmc_path) if counters_apply else None
         line = {"ms": ms, "bytes": nbytes, "GBps": gbs, "frac_hbm_peak": gbs / HBM_PEAK_GBS,
                 "hbm_traffic_bytes": traffic,
                 "hbm_traffic_GBps": None if traffic is None else traffic / (ms * 1e-3) / 1e9,
@@ -943,7 +956,7 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": att_gbs / HBM_PEAK_GBS,
-            "traffic": pmc_traffic() if counters_apply else None,
+            "traffic": pmc_traffic(ROOFLINE_KERNELS, pmc_path) if counters_apply else None,
             "kernel": "attend_mfma_kernel + attend_merge_kernel (hs_attend_groups)",
             "measured_ceilings": ceilings,
         },
