@@ -273,7 +273,22 @@ __global__ __launch_bounds__(TT) void quest_topk_kernel(QuestArgs a) {
     return score_key(sc[p]);
   };
   if constexpr (KEYS_IN_LDS) {
-    for (int64_t p = threadIdx.x; p < count; p += TT) s_keys[p] = key_from_scores(p);
+    // TL scores per thread per round, every load issued before the first key is
+    // stored (a load-then-store loop waits out one load latency per score)
+    constexpr int TL = 8;
+    for (int64_t p0 = threadIdx.x; p0 < count; p0 += static_cast<int64_t>(TT) * TL) {
+      float v[TL];
+#pragma unroll
+      for (int u = 0; u < TL; ++u) {
+        const int64_t p = p0 + static_cast<int64_t>(u) * TT;
+        v[u] = sc[p < count ? p : p0];  // p0 < count: in bounds
+      }
+#pragma unroll
+      for (int u = 0; u < TL; ++u) {
+        const int64_t p = p0 + static_cast<int64_t>(u) * TT;
+        if (p < count) s_keys[p] = (p == count - 1 || (sink && p == 0)) ? 0xffffffffu : score_key(v[u]);
+      }
+    }
   }
   auto key_of = [&](int64_t p) -> uint32_t {
     if constexpr (KEYS_IN_LDS) return s_keys[p];
@@ -289,9 +304,27 @@ __global__ __launch_bounds__(TT) void quest_topk_kernel(QuestArgs a) {
     for (int i = threadIdx.x; i < 256; i += TT) hist[i] = 0u;
     __syncthreads();
     const uint32_t prefix = s_prefix, mask = s_mask;
-    for (int64_t p = threadIdx.x; p < count; p += TT) {
-      const uint32_t k = key_of(p);
-      if ((k & mask) == prefix) atomicAdd(&hist[(k >> shift) & 255u], 1u);
+    for (int64_t p0 = threadIdx.x - lane; p0 < count; p0 += TT) {  // wave-uniform trip count
+      const int64_t p = p0 + lane;
+      const uint32_t k = p < count ? key_of(p) : 0u;
+      const uint32_t digit = (k >> shift) & 255u;
+      bool pending = p < count && (k & mask) == prefix;
+      // Scores of one magnitude share their top digits, so most lanes of a wave
+      // would add to one bin (an LDS atomic conflicting 64 ways).  Twice, the
+      // lanes holding the first pending lane's digit add their count in one
+      // atomic; the lanes left add their own.
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+        const uint64_t live = __ballot(pending);
+        if (live == 0) break;
+        const int leader = __ffsll(static_cast<unsigned long long>(live)) - 1;
+        const uint32_t ld = __shfl(digit, leader, 64);
+        const bool same = pending && digit == ld;
+        const uint64_t group = __ballot(same);
+        if (lane == leader) atomicAdd(&hist[ld], static_cast<uint32_t>(__popcll(group)));
+        pending = pending && !same;
+      }
+      if (pending) atomicAdd(&hist[digit], 1u);
     }
     __syncthreads();
     if (threadIdx.x < 64) {
