@@ -336,6 +336,20 @@ int hs_skinny_gemm(const void* x, int64_t x_stride, const void* weight, int64_t 
                    void* out, int64_t out_stride, int64_t rows, int32_t dtype, void* workspace,
                    int64_t workspace_bytes, hs_stream_t stream);
 
+/*
+ * The same projection with W packed once, tile-major: weight_tiles holds
+ * ceil(n/16) * (k/32) blocks of 16 rows x 32 k-values, block (t, s) =
+ * W[16t .. 16t+15][32s .. 32s+31] row-major, blocks ordered by t then s, rows
+ * past n zero (ceil(n/16) * 16 * k elements in all).  Each wave then reads
+ * 1 KB of consecutive bytes per load instead of 16 rows a row stride apart
+ * (measured 10-20% faster on the Qwen2.5 decode projections).  Same
+ * arithmetic and order as hs_skinny_gemm: the outputs are bit-identical.  No
+ * reference counterpart (a weight format of the batched engine).
+ */
+int hs_skinny_gemm_tiled(const void* x, int64_t x_stride, const void* weight_tiles, int64_t n, int64_t k,
+                         const void* bias, void* out, int64_t out_stride, int64_t rows, int32_t dtype,
+                         void* workspace, int64_t workspace_bytes, hs_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -41,7 +41,7 @@ from torch.nn import functional as F
 
 from . import _lib
 from .batched import BatchedSparseDecode, LayerTablesView
-from .dense import add_rms_norm, linear, linear_supported, rotary_split, silu_mul
+from .dense import add_rms_norm, linear_supported, linear_tiled, rotary_split, silu_mul, tile_weight
 from .config import CacheConfig
 from .model import MiniModel, ModelConfig
 from .row_kernels import MappedHost, pinned_empty
@@ -452,10 +452,11 @@ class BatchedDecodeEngine:
 
     @torch.no_grad()
     def _choose_projections(self, mode="auto"):
-        """Per projection, the faster of the skinny-GEMM kernel (hs_skinny_gemm) and
-        PyTorch's GEMM at this batch, timed over the layers' own weights (each call
-        reads another layer's weight from HBM, as in a step).  The kernel wins the
-        small and tall-K shapes; PyTorch's GEMM can win the widest ones."""
+        """Per projection, the faster of the skinny-GEMM kernel on tile-major weights
+        (hs_skinny_gemm_tiled) and PyTorch's GEMM at this batch, timed over the layers'
+        own weights (each call reads another layer's weight from HBM, as in a step).
+        Each projection the kernel serves keeps a tile-major copy of its weights
+        (the model's row-major parameters stay as they are)."""
         B, dev, dt = self.state.batch, self.device, self.model.dtype
         layers = self.model.model.layers
         groups = {
@@ -466,26 +467,38 @@ class BatchedDecodeEngine:
             "lm_head": [(self.model.lm_head.weight, None)] * 4,
         }
         self.projection_kernel = {}
+        self._tiles = {}  # data_ptr of a row-major weight -> its tile-major copy
         for name, weights in groups.items():
             x = torch.full((B, weights[0][0].shape[1]), 0.01, dtype=dt, device=dev)
-            if not linear_supported(x, weights[0][0]) or mode != "auto":
-                self.projection_kernel[name] = mode == "kernel" and linear_supported(x, weights[0][0])
+            if not linear_supported(x, weights[0][0]):
+                self.projection_kernel[name] = False
                 continue
-            elapsed = {}
-            for label, fn in (("kernel", linear), ("torch", F.linear)):
-                fn(x, *weights[0])
-                start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-                start.record()
-                for w, b in weights:
-                    fn(x, w, b)
-                end.record()
-                end.synchronize()
-                elapsed[label] = start.elapsed_time(end)
-            self.projection_kernel[name] = elapsed["kernel"] <= elapsed["torch"]
+            for w, _ in weights:
+                if w.data_ptr() not in self._tiles:
+                    self._tiles[w.data_ptr()] = tile_weight(w)
+            if mode != "auto":
+                chosen = mode == "kernel"
+            else:
+                kernel = lambda x, w, b: linear_tiled(x, self._tiles[w.data_ptr()], w.shape[0], b)
+                elapsed = {}
+                for label, fn in (("kernel", kernel), ("torch", F.linear)):
+                    fn(x, *weights[0])
+                    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                    start.record()
+                    for w, b in weights:
+                        fn(x, w, b)
+                    end.record()
+                    end.synchronize()
+                    elapsed[label] = start.elapsed_time(end)
+                chosen = elapsed["kernel"] <= elapsed["torch"]
+            self.projection_kernel[name] = chosen
+            if not chosen:
+                for w, _ in weights:
+                    self._tiles.pop(w.data_ptr(), None)
 
     def _project(self, name, x, weight, bias=None, out=None):
         if self.projection_kernel[name]:
-            return linear(x, weight, bias, out=out)
+            return linear_tiled(x, self._tiles[weight.data_ptr()], weight.shape[0], bias, out=out)
         y = F.linear(x, weight, bias)
         if out is None:
             return y

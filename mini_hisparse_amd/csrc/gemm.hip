@@ -52,7 +52,11 @@ struct GemmArgs {
 // the slice's k-steps in rounds of GU.  (Measured on MI355X: splitting rows
 // over the waves instead, or double-buffering the rounds in registers, is
 // slower at every decode shape of the Qwen2.5 0.5B/7B/32B projections.)
-template <int DT, int GM_TILES, int GU>
+// TILED: W is stored tile-major, [ceil(N/16)][K/32][16][32] (each 16-row x 32-k
+// block of MFMA A fragments contiguous, rows past N zero-padded), so one wave's
+// load of a block reads 1 KB of consecutive bytes instead of 16 rows x 64 bytes
+// a row stride apart.
+template <int DT, int GM_TILES, int GU, bool TILED>
 __global__ __launch_bounds__(GM_T) void skinny_gemm_kernel(GemmArgs a) {
   constexpr int GM_ROWS = 16 * GM_TILES;  // weight rows per workgroup
   __shared__ float red[4][GM_ROWS][17];
@@ -68,9 +72,16 @@ __global__ __launch_bounds__(GM_T) void skinny_gemm_kernel(GemmArgs a) {
   const unsigned short* wrow[GM_TILES];
 #pragma unroll
   for (int t = 0; t < GM_TILES; ++t) {
-    int64_t n = n0 + 16 * t + c;
-    if (n >= a.N) n = a.N - 1;  // rows past N read the last row; their outputs are dropped
-    wrow[t] = a.w + n * a.K + 8 * j;
+    if constexpr (TILED) {
+      const int64_t tiles = (a.N + 15) / 16;
+      int64_t nt = n0 / 16 + t;
+      if (nt >= tiles) nt = tiles - 1;  // tiles past N read the last one; their outputs are dropped
+      wrow[t] = a.w + nt * steps * 512 + c * 32 + 8 * j;
+    } else {
+      int64_t n = n0 + 16 * t + c;
+      if (n >= a.N) n = a.N - 1;  // rows past N read the last row; their outputs are dropped
+      wrow[t] = a.w + n * a.K + 8 * j;
+    }
   }
   const unsigned short* xrow = a.x + (c < a.M ? c : a.M - 1) * a.x_stride + 8 * j;
   f32x4 acc[GM_TILES];
@@ -84,9 +95,10 @@ __global__ __launch_bounds__(GM_T) void skinny_gemm_kernel(GemmArgs a) {
     for (int u = 0; u < GU; ++u) {
       int64_t s = base + u;
       if (s >= s1) s = s1 - 1;
-      const int64_t k = 32 * s;
+      const int64_t k = 32 * s;                   // x is row-major
+      const int64_t wk = TILED ? 512 * s : k;      // a 16 x 32 block per k-step when tiled
 #pragma unroll
-      for (int t = 0; t < GM_TILES; ++t) wf[u][t] = *reinterpret_cast<const u32x4*>(wrow[t] + k);
+      for (int t = 0; t < GM_TILES; ++t) wf[u][t] = *reinterpret_cast<const u32x4*>(wrow[t] + wk);
       xf[u] = *reinterpret_cast<const u32x4*>(xrow + k);
     }
 #pragma unroll
@@ -165,17 +177,17 @@ static GemmPlan plan_gemm(int64_t N, int64_t K) {
   return p;
 }
 
-template <int DT, int TILES>
+template <int DT, int TILES, bool TILED>
 static void launch_gemm_tiles(const GemmPlan& p, dim3 grid, const GemmArgs& a, hipStream_t s) {
-  if (p.gu == 4) hipLaunchKernelGGL((skinny_gemm_kernel<DT, TILES, 4>), grid, dim3(GM_T), 0, s, a);
-  else hipLaunchKernelGGL((skinny_gemm_kernel<DT, TILES, 8>), grid, dim3(GM_T), 0, s, a);
+  if (p.gu == 4) hipLaunchKernelGGL((skinny_gemm_kernel<DT, TILES, 4, TILED>), grid, dim3(GM_T), 0, s, a);
+  else hipLaunchKernelGGL((skinny_gemm_kernel<DT, TILES, 8, TILED>), grid, dim3(GM_T), 0, s, a);
 }
 
-template <int DT>
+template <int DT, bool TILED>
 static void launch_gemm(const GemmPlan& p, dim3 grid, const GemmArgs& a, hipStream_t s) {
-  if (p.tiles == 1) launch_gemm_tiles<DT, 1>(p, grid, a, s);
-  else if (p.tiles == 2) launch_gemm_tiles<DT, 2>(p, grid, a, s);
-  else launch_gemm_tiles<DT, 4>(p, grid, a, s);
+  if (p.tiles == 1) launch_gemm_tiles<DT, 1, TILED>(p, grid, a, s);
+  else if (p.tiles == 2) launch_gemm_tiles<DT, 2, TILED>(p, grid, a, s);
+  else launch_gemm_tiles<DT, 4, TILED>(p, grid, a, s);
 }
 
 }  // namespace hs
@@ -188,9 +200,9 @@ extern "C" int64_t hs_skinny_gemm_workspace_bytes(int64_t rows, int64_t n, int64
   return p.splits > 1 ? p.splits * rows * n * 4 + 256 : 256;
 }
 
-extern "C" int hs_skinny_gemm(const void* x, int64_t x_stride, const void* weight, int64_t n, int64_t k,
-                              const void* bias, void* out, int64_t out_stride, int64_t rows, int32_t dtype,
-                              void* workspace, int64_t workspace_bytes, hipStream_t stream) {
+static int run_gemm(const void* x, int64_t x_stride, const void* weight, int64_t n, int64_t k, const void* bias,
+                    void* out, int64_t out_stride, int64_t rows, int32_t dtype, void* workspace,
+                    int64_t workspace_bytes, hipStream_t stream, bool tiled) {
   HS_CHECK_ARG(dtype == HS_DTYPE_BF16 || dtype == HS_DTYPE_F16, "the decode GEMM takes bf16 or f16");
   HS_CHECK_ARG(rows >= 1 && rows <= 16, "the decode GEMM takes 1 to 16 rows");
   HS_CHECK_ARG(n >= 1 && k >= 32 && k % 32 == 0, "K must be a positive multiple of 32");
@@ -219,8 +231,13 @@ extern "C" int hs_skinny_gemm(const void* x, int64_t x_stride, const void* weigh
     a.part = static_cast<float*>(workspace);
   }
   const dim3 grid(static_cast<unsigned>(p.blocks), static_cast<unsigned>(p.splits));
-  if (dtype == HS_DTYPE_BF16) launch_gemm<HS_DTYPE_BF16>(p, grid, a, stream);
-  else launch_gemm<HS_DTYPE_F16>(p, grid, a, stream);
+  if (dtype == HS_DTYPE_BF16) {
+    if (tiled) launch_gemm<HS_DTYPE_BF16, true>(p, grid, a, stream);
+    else launch_gemm<HS_DTYPE_BF16, false>(p, grid, a, stream);
+  } else {
+    if (tiled) launch_gemm<HS_DTYPE_F16, true>(p, grid, a, stream);
+    else launch_gemm<HS_DTYPE_F16, false>(p, grid, a, stream);
+  }
   HS_CHECK_LAUNCH("skinny GEMM");
   if (p.splits > 1) {
     const unsigned blocks = static_cast<unsigned>(gemm_ceil(rows * n, GM_T));
@@ -233,4 +250,18 @@ extern "C" int hs_skinny_gemm(const void* x, int64_t x_stride, const void* weigh
     HS_CHECK_LAUNCH("skinny GEMM finalize");
   }
   return HS_OK;
+}
+
+extern "C" int hs_skinny_gemm(const void* x, int64_t x_stride, const void* weight, int64_t n, int64_t k,
+                              const void* bias, void* out, int64_t out_stride, int64_t rows, int32_t dtype,
+                              void* workspace, int64_t workspace_bytes, hipStream_t stream) {
+  return run_gemm(x, x_stride, weight, n, k, bias, out, out_stride, rows, dtype, workspace, workspace_bytes, stream,
+                  false);
+}
+
+extern "C" int hs_skinny_gemm_tiled(const void* x, int64_t x_stride, const void* weight_tiles, int64_t n, int64_t k,
+                                    const void* bias, void* out, int64_t out_stride, int64_t rows, int32_t dtype,
+                                    void* workspace, int64_t workspace_bytes, hipStream_t stream) {
+  return run_gemm(x, x_stride, weight_tiles, n, k, bias, out, out_stride, rows, dtype, workspace, workspace_bytes,
+                  stream, true);
 }

@@ -84,6 +84,49 @@ def linear(x, weight, bias=None, out=None):
     return y
 
 
+def tile_weight(weight):
+    """``weight`` [N, K] packed tile-major for :func:`linear_tiled`: ceil(N/16) x K/32 blocks
+    of 16 rows x 32 k-values (block (t, s) = weight[16t:16t+16, 32s:32s+32]), rows past N zero."""
+    if weight.dim() != 2 or weight.shape[1] % 32 != 0 or weight.dtype not in (torch.bfloat16, torch.float16):
+        raise ValueError("tile_weight takes a bf16/f16 [N, K] weight with K a multiple of 32")
+    n, k = weight.shape
+    rows = -(-n // 16) * 16
+    padded = weight if rows == n else torch.cat((weight, weight.new_zeros(rows - n, k)), 0)
+    return padded.reshape(rows // 16, 16, k // 32, 32).transpose(1, 2).contiguous()
+
+
+def linear_tiled(x, tiles, n, bias=None, out=None):
+    """:func:`linear` with the weight as :func:`tile_weight` packed it (``n`` its rows):
+    the same arithmetic in the same order, so the same bits."""
+    k = x.shape[1] if x.dim() == 2 else -1
+    if not (
+        x.dim() == 2 and 1 <= x.shape[0] <= 16 and k % 32 == 0 and k > 0 and n >= 1
+        and x.dtype in (torch.bfloat16, torch.float16) and x.stride(1) == 1 and x.stride(0) % 8 == 0
+        and x.data_ptr() % 16 == 0 and tiles.dim() == 4 and tiles.shape == (-(-n // 16), k // 32, 16, 32)
+        and tiles.is_contiguous() and tiles.dtype == x.dtype and tiles.data_ptr() % 16 == 0
+    ):
+        raise ValueError("linear_tiled takes 1-16 rows of a bf16/f16 x (K a multiple of 32) and tile_weight's packing")
+    if bias is not None and (bias.shape != (n,) or bias.dtype != x.dtype or not bias.is_contiguous()):
+        raise ValueError("bias must be [N] contiguous in the dtype of x")
+    rows = x.shape[0]
+    _check_out(out, (rows, n), x, "linear_tiled")
+    y = torch.empty((rows, n), dtype=x.dtype, device=x.device) if out is None else out
+    lib = _lib.load()
+    stream = _stream(x)
+    nbytes = _GEMM_WS_BYTES.get((rows, n, k))
+    if nbytes is None:
+        nbytes = _GEMM_WS_BYTES[(rows, n, k)] = lib.hs_skinny_gemm_workspace_bytes(rows, n, k)
+    ws = _workspace(x.device, stream, nbytes)
+    _lib.check(
+        lib.hs_skinny_gemm_tiled(
+            x.data_ptr(), x.stride(0), tiles.data_ptr(), n, k, _lib.ptr(bias), y.data_ptr(), y.stride(0), rows,
+            _lib.dtype_code(x.dtype), ws.data_ptr(), ws.numel(), stream,
+        ),
+        "hs_skinny_gemm_tiled",
+    )
+    return y
+
+
 def add_rms_norm(x, delta, weight, eps, out=None):
     """RMSNorm of ``x`` [rows, width] (of ``x + delta`` when ``delta`` is given, and then
     ``x`` is updated in place to the sum).  Returns the normalised rows."""

@@ -116,6 +116,28 @@ def test_linear_matches_an_fp32_reference(gpu, dtype, rows, n, k, bias):
     err = (got.float() - ref).abs()
     assert (err <= 2 * BF16_ULP * ref.abs() + 2e-3 * scale).all(), err.max().item()
     assert torch.equal(linear(x, w, b), got)  # split-K partials are summed in a fixed order
+    from mini_hisparse_amd.dense import linear_tiled, tile_weight
+
+    # the tile-major weight (rows padded to 16) gives the same bits
+    assert torch.equal(linear_tiled(x, tile_weight(w), n, b), got)
+
+
+def test_tile_weight_packs_16_by_32_blocks():
+    from mini_hisparse_amd.dense import linear_tiled, tile_weight
+
+    w = torch.randn(37, 64).to(torch.bfloat16)
+    t = tile_weight(w)
+    assert t.shape == (3, 2, 16, 32) and t.is_contiguous()
+    for tile in range(3):
+        for step in range(2):
+            block = t[tile, step]
+            rows = w[16 * tile : 16 * tile + 16, 32 * step : 32 * step + 32]
+            assert torch.equal(block[: rows.shape[0]], rows)
+            assert not block[rows.shape[0] :].any()  # rows past N are zero
+    with pytest.raises(ValueError):
+        tile_weight(torch.zeros(8, 40, dtype=torch.bfloat16))
+    with pytest.raises(ValueError):  # a row-major weight is not a tile packing
+        linear_tiled(torch.zeros(2, 64, dtype=torch.bfloat16), w, 37)
 
 
 @pytest.mark.gpu
