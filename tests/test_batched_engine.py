@@ -177,10 +177,12 @@ def test_batched_engine_uniform_selection_matches_oracle(gpu, prefetch):
 
 
 @pytest.mark.gpu
-def test_prefetched_uniform_steps_equal_in_order_steps(gpu):
+@pytest.mark.parametrize("graphs", [False, True])
+def test_prefetched_uniform_steps_equal_in_order_steps(gpu, graphs):
     """Prefetching every layer's select/resolve/gather at step start changes only the
     launch order across streams: tokens, attention outputs, the resolver's row
-    statistics and every hot region's tags and LRU equal the in-order engine's bit for bit."""
+    statistics and every hot region's tags and LRU equal the in-order engine's bit for bit
+    (also with the dense layer boundaries replayed from HIP graphs between the waits)."""
     from mini_hisparse_amd.batched_engine import BatchedDecodeEngine, build_state, random_model
     from mini_hisparse_amd.selection import union_bound
 
@@ -189,10 +191,12 @@ def test_prefetched_uniform_steps_equal_in_order_steps(gpu):
     for prefetch in (False, True):
         model = random_model(wl, gpu, seed=1)
         state = build_state(wl, gpu, seed=2)
-        engine = BatchedDecodeEngine(model, state, wl.top_pages, selector="uniform", seed=4, prefetch=prefetch)
+        engine = BatchedDecodeEngine(model, state, wl.top_pages, selector="uniform", seed=4, prefetch=prefetch,
+                                     graphs=graphs, projections="kernel" if graphs else "auto")
+        assert engine.use_graphs == graphs
         outs, toks = [], []
         tokens = torch.tensor([1, 2, 3], device=gpu)
-        for step in range(4):
+        for step in range(4):  # with graphs: step 0 eager, captured after it, replayed from step 1
             tokens = engine.step(tokens, lambda l, q, k, v, out: outs.append(out.clone()))
             toks.append(tokens.clone())
         torch.cuda.synchronize()
