@@ -350,6 +350,20 @@ int hs_skinny_gemm_tiled(const void* x, int64_t x_stride, const void* weight_til
                          const void* bias, void* out, int64_t out_stride, int64_t rows, int32_t dtype,
                          void* workspace, int64_t workspace_bytes, hs_stream_t stream);
 
+/*
+ * The MLP's gate and up projections with the SiLU gate applied on the way out:
+ * out[rows, ffn] = silu(x . Wg^T) * (x . Wu^T), each projection rounded to the
+ * dtype, then SiLU rounded, then the product -- the arithmetic of
+ * hs_skinny_gemm_tiled on the packed gate|up weight followed by hs_silu_mul,
+ * with the same bits.  gate_up_tiles: 2 * ceil(ffn/16) blocks-of-tiles in
+ * hs_skinny_gemm_tiled's format, the gate's tile i at position 2i and the up
+ * projection's tile i at 2i + 1 (rows past ffn zero).  No workspace (one K
+ * slice).  No reference counterpart (replaces two launches of the batched
+ * engine's MLP, model.py:183-226).
+ */
+int hs_skinny_gemm_swiglu_tiled(const void* x, int64_t x_stride, const void* gate_up_tiles, int64_t ffn, int64_t k,
+                                void* out, int64_t out_stride, int64_t rows, int32_t dtype, hs_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -118,6 +118,9 @@ SIGNATURES = {
         [c_void_p, c_int64, c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_int64, c_int64, c_int32, c_void_p,
          c_int64, c_void_p],
     ),
+    "hs_skinny_gemm_swiglu_tiled": (
+        c_int, [c_void_p, c_int64, c_void_p, c_int64, c_int64, c_void_p, c_int64, c_int64, c_int32, c_void_p],
+    ),
     "hs_skinny_gemm_tiled": (
         c_int,
         [c_void_p, c_int64, c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_int64, c_int64, c_int32, c_void_p,

@@ -41,7 +41,10 @@ from torch.nn import functional as F
 
 from . import _lib
 from .batched import BatchedSparseDecode, LayerTablesView
-from .dense import add_rms_norm, linear_supported, linear_tiled, rotary_split, silu_mul, tile_weight
+from .dense import (
+    add_rms_norm, linear_supported, linear_swiglu_tiled, linear_tiled, rotary_split, silu_mul, tile_gate_up,
+    tile_weight,
+)
 from .config import CacheConfig
 from .model import MiniModel, ModelConfig
 from .row_kernels import MappedHost, pinned_empty
@@ -393,7 +396,10 @@ class BatchedDecodeEngine:
         _, _, gate_up_w = self._packed[index]
         o = self._project("o_proj", self._attn_out.view(B, -1), layer.self_attn.o_proj.weight, out=self._o)
         h = add_rms_norm(self._x, o, layer.post_attention_layernorm.weight, cfg.rms_norm_eps, out=self._h)
-        act = silu_mul(self._project("gate_up", h, gate_up_w, out=self._gate_up), out=self._act)
+        if self.projection_kernel["gate_up"]:  # gate|up and the SiLU gate in one launch
+            act = linear_swiglu_tiled(h, self._tiles[gate_up_w.data_ptr()], cfg.intermediate_size, out=self._act)
+        else:
+            act = silu_mul(self._project("gate_up", h, gate_up_w, out=self._gate_up), out=self._act)
         self._project("down", act, layer.mlp.down_proj.weight, out=self._delta)
 
     def _boundary(self, index):
@@ -495,6 +501,10 @@ class BatchedDecodeEngine:
             if not chosen:
                 for w, _ in weights:
                     self._tiles.pop(w.data_ptr(), None)
+            elif name == "gate_up":  # the fused SiLU launch reads gate and up tiles interleaved
+                ffn = self.model.config.intermediate_size
+                for w, _ in weights:
+                    self._tiles[w.data_ptr()] = tile_gate_up(w, ffn)
 
     def _project(self, name, x, weight, bias=None, out=None):
         if self.projection_kernel[name]:

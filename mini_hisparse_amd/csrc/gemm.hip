@@ -46,7 +46,14 @@ struct GemmArgs {
   int64_t out_stride;
   float* part;  // [splits, M, N] when splits > 1
   int64_t splits, slice_steps;
+  int64_t F;  // SWIGLU: output features (N = 2 * 16 * ceil(F / 16) interleaved weight rows)
 };
+
+template <int DT>
+__device__ __forceinline__ float gemm_round(float v) {
+  if constexpr (DT == HS_DTYPE_BF16) return bf16_bits_to_f32(f32_to_bf16_bits(v));
+  else return f16_bits_to_f32(f32_to_f16_bits(v));
+}
 
 // GM_TILES row tiles of 16 per workgroup, shared by the 4 waves, which split
 // the slice's k-steps in rounds of GU.  (Measured on MI355X: splitting rows
@@ -56,7 +63,12 @@ struct GemmArgs {
 // block of MFMA A fragments contiguous, rows past N zero-padded), so one wave's
 // load of a block reads 1 KB of consecutive bytes instead of 16 rows x 64 bytes
 // a row stride apart.
-template <int DT, int GM_TILES, int GU, bool TILED>
+// SWIGLU (with TILED and two tiles per workgroup): the weight interleaves the
+// gate and up projections tile by tile (tile 2i = gate rows 16i.., 2i+1 = up rows
+// 16i..), and the workgroup writes silu(gate) * up for its 16 features with the
+// arithmetic of the separate path: each projection rounded to the dtype, then
+// SiLU rounded, then the product (hs_silu_mul).
+template <int DT, int GM_TILES, int GU, bool TILED, bool SWIGLU = false>
 __global__ __launch_bounds__(GM_T) void skinny_gemm_kernel(GemmArgs a) {
   constexpr int GM_ROWS = 16 * GM_TILES;  // weight rows per workgroup
   __shared__ float red[4][GM_ROWS][17];
@@ -115,6 +127,20 @@ __global__ __launch_bounds__(GM_T) void skinny_gemm_kernel(GemmArgs a) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) red[wave][16 * t + 4 * j + i][c] = acc[t][i];
   __syncthreads();
+  if constexpr (SWIGLU) {
+    static_assert(TILED && GM_TILES == 2, "the fused gate/up product takes a gate tile and an up tile");
+    for (int idx = threadIdx.x; idx < 16 * 16; idx += GM_T) {
+      const int r = idx >> 4, m = idx & 15;
+      const int64_t f = static_cast<int64_t>(blockIdx.x) * 16 + r;
+      if (m >= a.M || f >= a.F) continue;
+      const float g = gemm_round<DT>((red[0][r][m] + red[1][r][m] + red[2][r][m] + red[3][r][m]) + 0.f);
+      const float u =
+          gemm_round<DT>((red[0][16 + r][m] + red[1][16 + r][m] + red[2][16 + r][m] + red[3][16 + r][m]) + 0.f);
+      const float act = gemm_round<DT>(g / (1.f + expf(-g)));
+      store_elem<DT>(a.out, m * a.out_stride + f, act * u);
+    }
+    return;
+  }
   for (int idx = threadIdx.x; idx < GM_ROWS * 16; idx += GM_T) {
     const int r = idx >> 4, m = idx & 15;
     const int64_t n = n0 + r;
@@ -264,4 +290,37 @@ extern "C" int hs_skinny_gemm_tiled(const void* x, int64_t x_stride, const void*
                                     void* workspace, int64_t workspace_bytes, hipStream_t stream) {
   return run_gemm(x, x_stride, weight_tiles, n, k, bias, out, out_stride, rows, dtype, workspace, workspace_bytes,
                   stream, true);
+}
+
+extern "C" int hs_skinny_gemm_swiglu_tiled(const void* x, int64_t x_stride, const void* gate_up_tiles, int64_t ffn,
+                                           int64_t k, void* out, int64_t out_stride, int64_t rows, int32_t dtype,
+                                           hipStream_t stream) {
+  HS_CHECK_ARG(dtype == HS_DTYPE_BF16 || dtype == HS_DTYPE_F16, "the decode GEMM takes bf16 or f16");
+  HS_CHECK_ARG(rows >= 1 && rows <= 16, "the decode GEMM takes 1 to 16 rows");
+  HS_CHECK_ARG(ffn >= 1 && k >= 32 && k % 32 == 0, "K must be a positive multiple of 32");
+  HS_CHECK_ARG(x_stride >= k && x_stride % 8 == 0 && out_stride >= ffn, "invalid row strides");
+  HS_CHECK_ARG(x && gate_up_tiles && out, "null GEMM pointer");
+  HS_CHECK_ARG((reinterpret_cast<uintptr_t>(x) & 15) == 0 && (reinterpret_cast<uintptr_t>(gate_up_tiles) & 15) == 0,
+               "x and weight must be 16-byte aligned");
+  const int64_t blocks = gemm_ceil(ffn, 16);
+  HS_CHECK_ARG(blocks <= 0x7fffffff, "GEMM too large");
+  GemmArgs a{};
+  a.x = static_cast<const unsigned short*>(x);
+  a.x_stride = x_stride;
+  a.w = static_cast<const unsigned short*>(gate_up_tiles);
+  a.K = k;
+  a.N = 2 * 16 * blocks;  // interleaved weight rows, padded
+  a.M = rows;
+  a.out = out;
+  a.out_stride = out_stride;
+  a.splits = 1;  // one K slice: the workgroup sees whole sums before the product
+  a.slice_steps = k / 32;
+  a.F = ffn;
+  const dim3 grid(static_cast<unsigned>(blocks));
+  if (dtype == HS_DTYPE_BF16)
+    hipLaunchKernelGGL((skinny_gemm_kernel<HS_DTYPE_BF16, 2, 8, true, true>), grid, dim3(GM_T), 0, stream, a);
+  else
+    hipLaunchKernelGGL((skinny_gemm_kernel<HS_DTYPE_F16, 2, 8, true, true>), grid, dim3(GM_T), 0, stream, a);
+  HS_CHECK_LAUNCH("skinny GEMM swiglu");
+  return HS_OK;
 }

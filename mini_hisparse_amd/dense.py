@@ -127,6 +127,40 @@ def linear_tiled(x, tiles, n, bias=None, out=None):
     return y
 
 
+def tile_gate_up(gate_up, ffn):
+    """The packed gate|up weight [2 * ffn, K] for :func:`linear_swiglu_tiled`: the gate's
+    and the up projection's :func:`tile_weight` tiles interleaved (gate tile i at 2i)."""
+    if gate_up.dim() != 2 or gate_up.shape[0] != 2 * ffn:
+        raise ValueError("gate_up must be [2 * ffn, K]")
+    gate, up = tile_weight(gate_up[:ffn]), tile_weight(gate_up[ffn:])
+    return torch.stack((gate, up), 1).reshape(2 * gate.shape[0], *gate.shape[1:]).contiguous()
+
+
+def linear_swiglu_tiled(x, tiles, ffn, out=None):
+    """``silu(x @ gate.T) * (x @ up.T)`` from :func:`tile_gate_up`'s packing: the bits of
+    :func:`linear_tiled` on the packed weight followed by :func:`silu_mul`, in one launch."""
+    k = x.shape[1] if x.dim() == 2 else -1
+    if not (
+        x.dim() == 2 and 1 <= x.shape[0] <= 16 and k % 32 == 0 and k > 0 and ffn >= 1
+        and x.dtype in (torch.bfloat16, torch.float16) and x.stride(1) == 1 and x.stride(0) % 8 == 0
+        and x.data_ptr() % 16 == 0 and tiles.dim() == 4 and tiles.shape == (2 * -(-ffn // 16), k // 32, 16, 32)
+        and tiles.is_contiguous() and tiles.dtype == x.dtype and tiles.data_ptr() % 16 == 0
+    ):
+        raise ValueError("linear_swiglu_tiled takes 1-16 rows of a bf16/f16 x (K a multiple of 32) and "
+                         "tile_gate_up's packing")
+    rows = x.shape[0]
+    _check_out(out, (rows, ffn), x, "linear_swiglu_tiled")
+    y = torch.empty((rows, ffn), dtype=x.dtype, device=x.device) if out is None else out
+    _lib.check(
+        _lib.load().hs_skinny_gemm_swiglu_tiled(
+            x.data_ptr(), x.stride(0), tiles.data_ptr(), ffn, k, y.data_ptr(), y.stride(0), rows,
+            _lib.dtype_code(x.dtype), _stream(x),
+        ),
+        "hs_skinny_gemm_swiglu_tiled",
+    )
+    return y
+
+
 def add_rms_norm(x, delta, weight, eps, out=None):
     """RMSNorm of ``x`` [rows, width] (of ``x + delta`` when ``delta`` is given, and then
     ``x`` is updated in place to the sum).  Returns the normalised rows."""

@@ -122,6 +122,35 @@ def test_linear_matches_an_fp32_reference(gpu, dtype, rows, n, k, bias):
     assert torch.equal(linear_tiled(x, tile_weight(w), n, b), got)
 
 
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("rows", [1, 3, 16])
+@pytest.mark.parametrize("ffn,k", [(4864, 896), (18944, 3584), (37, 64), (1000, 256)])
+def test_swiglu_gemm_equals_gemm_then_silu_mul(gpu, dtype, rows, ffn, k):
+    """One launch of gate|up with the SiLU gate gives the bits of the tiled GEMM on the packed
+    weight followed by hs_silu_mul (ffn not a multiple of 16 included)."""
+    from mini_hisparse_amd.dense import linear_swiglu_tiled, linear_tiled, silu_mul, tile_gate_up, tile_weight
+
+    gen = torch.Generator(device=gpu).manual_seed(rows + ffn + k)
+    x = torch.randn(rows, k, generator=gen, device=gpu).to(dtype)
+    w = (torch.randn(2 * ffn, k, generator=gen, device=gpu) / k**0.5).to(dtype)
+    want = silu_mul(linear_tiled(x, tile_weight(w), 2 * ffn))
+    got = linear_swiglu_tiled(x, tile_gate_up(w, ffn), ffn)
+    assert torch.equal(got, want)
+    ref = torch.nn.functional.silu(x.float() @ w[:ffn].float().T) * (x.float() @ w[ffn:].float().T)
+    assert ((got.float() - ref).abs() <= 0.02 + 0.02 * ref.abs()).all()
+
+
+def test_tile_gate_up_interleaves_the_two_projections():
+    from mini_hisparse_amd.dense import tile_gate_up, tile_weight
+
+    w = torch.randn(2 * 20, 32).to(torch.bfloat16)
+    t = tile_gate_up(w, 20)
+    gate, up = tile_weight(w[:20]), tile_weight(w[20:])
+    assert t.shape == (4, 1, 16, 32)
+    assert torch.equal(t[0], gate[0]) and torch.equal(t[1], up[0]) and torch.equal(t[2], gate[1]) and torch.equal(t[3], up[1])
+
+
 def test_tile_weight_packs_16_by_32_blocks():
     from mini_hisparse_amd.dense import linear_tiled, tile_weight
 
