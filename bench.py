@@ -1,22 +1,33 @@
 #!/usr/bin/env python
-"""Sparse decode step benchmark on one MI355X.
+"""Sparse decode benchmark on one MI355X.
 
-Workload ("microbench"): one layer, 8 KV heads x 64 query heads (GQA group 8),
-head_dim 128, page_size 16, 4096 logical pages (65,536 tokens) per request,
-batch 8, bf16.  K/V ~ N(0,1) with 2% of channels scaled x8; Quest top-64 pages
-per query head (sink and tail forced).  Of the selected union rows 50% sit in
-resident pages, 30% in hot slots and 20% miss to pinned host memory.  Inputs
-are seeded and synthetic; they live in HBM / pinned host memory before timing.
+Default workload ("qwen2.5-7b", BASELINE configs[3], the north_star shape): greedy
+decode of a random-init Qwen2.5-7B-shape model (28 layers, hidden 3584, 28 q / 4 kv
+heads, head_dim 128, FFN 18944, bf16) with the layer-major batched engine over
+131,072-token K/V histories, Quest top-64 pages per query head, 15% of pages
+resident, hot_rows 32768.  A step is one decode step of every request through all
+28 layers: dense layers, append (rows, Quest bounds, host mirror), Quest scorer +
+top-k, device union, resolver, pinned-host -> hot-row gather, group attention.
+`value` = decode tokens/s = batch x steps / wall time of the timed steps.  The
+batch is cut to what the box's pinned host memory holds (16 histories need 112 GiB;
+the GPU boxes here pin at most 64 GiB), and the line says so.  `roofline` is the
+group attention kernel (hs_attend_groups) over the timed steps: algorithmic bytes
+of every launch / its duration from HIP events on the compute stream.
 
-Workload "qwen2.5-7b-layer": the same one-layer step at the north_star shape --
-Qwen2.5-7B heads (28 q / 4 kv, head_dim 128), 8192 pages (131,072 tokens) per
-request, batch 16 -- whose attention target north_star states (>= 60% of HBM
-peak); the end-to-end 7B workload runs batch 8 (pinned host memory).
+The default run also carries the isolated kernel microbench
+as the key "microbench" (--no-microbench skips it).  Workload "microbench": one
+layer, 8 KV heads x 64 query heads (GQA group 8), head_dim 128, page_size 16, 4096
+logical pages (65,536 tokens) per request, batch 8, bf16; K/V ~ N(0,1) with 2% of
+channels scaled x8; Quest top-64 pages per query head (sink and tail forced); of
+the selected union rows 50% sit in resident pages, 30% in hot slots and 20% miss
+to pinned host memory.  A microbench step restores the hot tags/LRU to the step's
+starting state (so every step sees the same 20% misses) and runs Quest, union,
+resolver, gather and group attention for the 8 requests.
 
-A step is the whole hot path for the 8 requests: restore the hot tags/LRU to
-the step's starting state (so every step sees the same 20% misses), Quest
-scorer + top-k, device union, resolver, host->hot gather on the transfer
-stream, group attention.  `value` = decode tokens/s = batch / step time.
+Workload "qwen2.5-7b-layer": the microbench step at the north_star layer shape
+(28 q / 4 kv heads, 8192 pages per request, batch 16).  "qwen2.5-0.5b" and
+"qwen2.5-32b-stress" run BASELINE configs[2] and configs[4] end to end.
+Inputs are seeded and synthetic; they live in HBM / pinned host memory before timing.
 """
 
 from __future__ import annotations
@@ -39,11 +50,14 @@ HBM_PEAK_GBS = 8000.0
 def parse_args():
     p = argparse.ArgumentParser(description=__doc__)
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--workload", default="microbench",
+    p.add_argument("--workload", default="qwen2.5-7b",
                    choices=["microbench", "qwen2.5-7b-layer", "qwen2.5-0.5b", "qwen2.5-7b", "qwen2.5-32b-stress"],
-                   help="microbench = BASELINE configs[1] (default); qwen2.5-7b-layer = the same one-layer "
-                        "step at the north_star shape (7B heads, 128k histories, batch 16); the Qwen shapes run the "
-                        "layer-major batched engine end to end (configs[2], configs[3], configs[4])")
+                   help="qwen2.5-7b = BASELINE configs[3] end to end (default, the north_star shape); "
+                        "microbench = configs[1]; qwen2.5-7b-layer = the microbench step at the north_star "
+                        "layer shape (7B heads, 128k histories, batch 16); qwen2.5-0.5b and qwen2.5-32b-stress "
+                        "run configs[2] and configs[4] end to end")
+    p.add_argument("--no-microbench", action="store_true",
+                   help="default workload: skip the configs[1] microbench figures carried as extra keys")
     p.add_argument("--steps", type=int, default=20)
     p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--batch", type=int, default=None, help="requests (default: the workload's)")
@@ -586,9 +600,13 @@ PMC_SUMMARY = os.path.join(PROFILES, "microbench_pmc.txt")
 # counter summaries per single-layer workload (the step the bench line times)
 PMC_SUMMARIES = {
     "microbench": (PMC_SUMMARY, "microbench step (BASELINE configs[1]), batch 8, bf16"),
+    "qwen2.5-7b": (os.path.join(PROFILES, "qwen2.5-7b_e2e_pmc.txt"),
+                   "Qwen2.5-7B-shape end-to-end decode (BASELINE configs[3]), batch 8, bf16"),
     "qwen2.5-7b-layer": (os.path.join(PROFILES, "qwen2.5-7b_layer_pmc.txt"),
                          "one layer of the north_star step (Qwen2.5-7B heads, 128k histories), batch 16, bf16"),
 }
+# the batch each counter summary was taken at (the traffic applies to that batch only)
+PMC_BATCH = {"microbench": 8, "qwen2.5-7b": 8, "qwen2.5-7b-layer": 16}
 ROOFLINE_KERNELS = ("attend_mfma_kernel", "attend_merge_kernel")
 CALIBRATION_BYTES = 1 << 30  # hbm_copy_gbs: a plain device-to-device copy of 1 GiB
 
@@ -624,7 +642,7 @@ def summarize_pmc(fetch_dir, write_dir, workload="microbench"):
         if "hs::" in name:
             per[name.split("(")[0].replace("void ", "")][1].append(v)
     out_path, title = PMC_SUMMARIES[workload]
-    flag = "" if workload == "microbench" else f" --workload {workload}"
+    flag = f" --workload {workload}" + (" --no-microbench" if workload == "qwen2.5-7b" else "")
     lines = [
         f"# rocprofv3 --pmc summary: {title}",
         "# FETCH_SIZE and WRITE_SIZE (KiB per dispatch) from two runs of",
@@ -733,6 +751,39 @@ def model_cpu_baseline(torch, engine, wl, budget_s):
     }
 
 
+class AttendProbe:
+    """HIP events around every attention launch of the timed steps, on the compute stream
+    the launch runs on, and a device copy of each launch's entry counts (the rows each
+    (request, KV head) reads), from which the launch's algorithmic bytes follow.  Events
+    and the count buffer are allocated before the timed region."""
+
+    def __init__(self, torch, device, launches, batch, kv_heads):
+        self.torch = torch
+        self.start = [torch.cuda.Event(enable_timing=True) for _ in range(launches)]
+        self.end = [torch.cuda.Event(enable_timing=True) for _ in range(launches)]
+        self.counts = torch.zeros((launches, batch * kv_heads), dtype=torch.int32, device=device)
+        self.widths = []
+        self.i = 0
+
+    def before_attend(self, layer, stream, dec):
+        self.start[self.i].record(stream)
+
+    def after_attend(self, layer, stream, dec):
+        self.end[self.i].record(stream)
+        self.counts[self.i].copy_(dec.entry_counts.view(-1))
+        self.widths.append(dec.width)
+        self.i += 1
+
+    def totals(self, bytes_of):
+        """(total ms, total algorithmic bytes, launches); ``bytes_of(entries, width)`` gives
+        one launch's bytes."""
+        n = self.i
+        ms = sum(self.start[i].elapsed_time(self.end[i]) for i in range(n))
+        entries = self.counts[:n].sum(1).tolist()
+        nbytes = sum(bytes_of(e, w) for e, w in zip(entries, self.widths))
+        return ms, nbytes, n
+
+
 def run_model_workload(args, torch, device):
     """End-to-end decode of a Qwen-shape random-init model with the layer-major engine."""
     from dataclasses import replace
@@ -769,9 +820,11 @@ def run_model_workload(args, torch, device):
     torch.cuda.synchronize()
     print("[bench] timing", file=sys.stderr, flush=True)
     stats0 = state.row_stats.clone()
+    probe = AttendProbe(torch, device, args.steps * wl.layers, wl.batch, wl.kv_heads)
+    torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
-        tokens = engine.step(tokens)
+        tokens = engine.step(tokens, probe=probe)
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     ms_per_step = elapsed * 1e3 / args.steps
@@ -783,15 +836,21 @@ def run_model_workload(args, torch, device):
     for _, marks, _, _ in timer:
         for stage, (start, end) in marks.items():
             stage_ms[stage] = stage_ms.get(stage, 0.0) + start.elapsed_time(end)
-    entries = sum(int(e) for _, _, e, _ in timer)
     misses = sum(int(m) for _, _, _, m in timer)
     e, D, Hq, B, L = 2, wl.head_dim, wl.heads, wl.batch, wl.layers
-    W = engine.dec.width
-    att_bytes = entries * 2 * D * e + L * (8 * Hq * W * B + 2 * Hq * D * e * B)
-    att_gbs = att_bytes / (stage_ms["attend"] * 1e-3) / 1e9
+
+    def launch_bytes(entries, width):
+        # union-deduplicated K/V rows + the per-head row lists + queries and outputs
+        return entries * 2 * D * e + 8 * Hq * width * B + 2 * Hq * D * e * B
+
+    att_ms, att_bytes, launches = probe.totals(launch_bytes)
+    att_gbs = att_bytes / (att_ms * 1e-3) / 1e9
+    pmc_path = PMC_SUMMARIES.get(args.workload, (None,))[0]
+    traffic = pmc_traffic(ROOFLINE_KERNELS, pmc_path) if pmc_path and wl.batch == PMC_BATCH.get(args.workload) else None
     row_bytes = 2 * wl.kv_heads * D * e
     gather_bytes = misses * row_bytes
     link = host_link_gbs(torch, device)
+    copy = hbm_copy_gbs(torch, device)  # also the counter runs' calibration kernel
     result = {
         "metric": METRIC,
         "value": wl.batch * args.steps / elapsed,
@@ -829,22 +888,27 @@ def run_model_workload(args, torch, device):
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": att_gbs / HBM_PEAK_GBS,
-            "traffic": None,
-            "kernel": "attend_mfma_kernel + attend_merge_kernel, summed over the layers of one profiled step",
+            "traffic": traffic,
+            "kernel": "attend_mfma_kernel + attend_merge_kernel (hs_attend_groups), every layer of the timed steps",
+            "launches": launches,
+            "bytes_per_launch": att_bytes / launches,
+            "us_per_launch": att_ms * 1e3 / launches,
         },
         "stages_ms_per_step": stage_ms,
         "projections_on_hs_skinny_gemm": engine.projection_kernel,
         "rows_per_step": {"resident_hits": rows[0], "hot_hits": rows[1], "misses": rows[2]},
         "gather": {"bytes_per_step": gather_bytes, "GBps": gather_bytes / (stage_ms["gather"] * 1e-3) / 1e9,
-                   "host_link_memcpy_GBps": link},
+                   "host_link_memcpy_GBps": link,
+                   "frac_host_link": gather_bytes / (stage_ms["gather"] * 1e-3) / 1e9 / link},
         "setup_s": setup_s,
+        "hbm_copy_GBps": copy,
     }
     if not args.no_cpu_baseline:
         print("[bench] cpu baseline (extrapolated)", file=sys.stderr, flush=True)
         result["cpu_baseline"] = model_cpu_baseline(torch, engine, wl, args.cpu_budget)
     else:
         result["cpu_baseline"] = None
-    print(json.dumps(result))
+    return result
 
 
 def main():
@@ -868,8 +932,24 @@ def main():
         attention_sweep(torch, device)
         return
     if args.workload not in SHAPES:
-        run_model_workload(args, torch, device)
+        result = run_model_workload(args, torch, device)
+        if args.workload == "qwen2.5-7b" and not args.no_microbench:
+            import gc
+
+            gc.collect()  # frees the 7B histories' pinned memory before the microbench pins its own
+            torch.cuda.empty_cache()
+            mb_args = argparse.Namespace(**vars(args))
+            mb_args.workload, mb_args.batch = "microbench", None
+            mb = run_microbench(mb_args, torch, device)
+            result["microbench"] = {k: mb[k] for k in ("value", "unit", "ms_per_step", "config", "roofline",
+                                                       "kernels", "rows", "cpu_baseline", "parity") if k in mb}
+        print(json.dumps(result))
         return
+    print(json.dumps(run_microbench(args, torch, device)))
+
+
+def run_microbench(args, torch, device):
+    """The isolated kernel microbench (configs[1], or the same step at the 7B layer shape)."""
     shape = SHAPES[args.workload]
     if args.batch is None:
         args.batch = shape.batch
@@ -978,7 +1058,7 @@ def main():
         result["parity"] = parity
     else:
         result["cpu_baseline"] = None
-    print(json.dumps(result))
+    return result
 
 
 if __name__ == "__main__":

@@ -28,6 +28,10 @@
 extern "C" {
 #endif
 
+/* The library is built with hidden visibility; everything declared here is its
+ * exported API. */
+#pragma GCC visibility push(default)
+
 #define HS_VERSION 1
 
 #define HS_OK 0
@@ -181,19 +185,25 @@ int hs_resolve_rows_batched(const hs_resolve_desc* descs, int32_t count, void* w
  *   pool        device pool [gpu_pages, 2, P, Hkv, D]
  *   miss_*_rows [n] int64 plan from the resolver; entries < 0 are skipped
  *   miss_count  nullable device int64: only the first *miss_count entries are read
+ *   host_pool_rows  host_pages * P; pool_rows  gpu_pages * P: an entry whose host
+ *               row or device row is at or past its pool's rows is skipped like a
+ *               -1 entry (the reference masks only -1, row_kernels.py:50-55)
  *   row_bytes   Hkv * D * element size
  */
 int hs_gather_rows(const void* host_alias, void* pool, const int64_t* miss_host_rows,
                    const int64_t* miss_device_rows, int64_t n, const int64_t* miss_count,
-                   int64_t page_size, int64_t row_bytes, hs_stream_t stream);
+                   int64_t host_pool_rows, int64_t pool_rows, int64_t page_size,
+                   int64_t row_bytes, hs_stream_t stream);
 
 /* The same for `batch` plans, one launch per chunk of at most 16; every array
- * argument is a host array of per-request values; grid_x (workgroups per plan)
- * <= 0 picks the default grid. */
+ * argument is a host array of per-request values (host_pool_rows included: each
+ * plan may read its own host pool); grid_x (workgroups per plan) <= 0 picks the
+ * default grid. */
 int hs_gather_rows_batched(const void* const* host_alias, void* pool,
                            const int64_t* const* miss_host_rows,
                            const int64_t* const* miss_device_rows,
-                           const int64_t* const* miss_counts, const int64_t* n, int32_t batch,
+                           const int64_t* const* miss_counts, const int64_t* n,
+                           const int64_t* host_pool_rows, int64_t pool_rows, int32_t batch,
                            int64_t page_size, int64_t row_bytes, int32_t grid_x,
                            hs_stream_t stream);
 
@@ -363,6 +373,8 @@ int hs_skinny_gemm_tiled(const void* x, int64_t x_stride, const void* weight_til
  */
 int hs_skinny_gemm_swiglu_tiled(const void* x, int64_t x_stride, const void* gate_up_tiles, int64_t ffn, int64_t k,
                                 void* out, int64_t out_stride, int64_t rows, int32_t dtype, hs_stream_t stream);
+
+#pragma GCC visibility pop
 
 #ifdef __cplusplus
 }

@@ -78,12 +78,13 @@ SIGNATURES = {
     "hs_resolve_rows_batched": (c_int, [POINTER(ResolveDesc), c_int32, c_void_p, c_int64, c_void_p]),
     "hs_gather_rows": (
         c_int,
-        [c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_void_p, c_int64, c_int64, c_void_p],
+        [c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_void_p, c_int64, c_int64, c_int64, c_int64,
+         c_void_p],
     ),
     "hs_gather_rows_batched": (
         c_int,
         [POINTER(c_void_p), c_void_p, POINTER(c_void_p), POINTER(c_void_p), POINTER(c_void_p),
-         POINTER(c_int64), c_int32, c_int64, c_int64, c_int32, c_void_p],
+         POINTER(c_int64), POINTER(c_int64), c_int64, c_int32, c_int64, c_int64, c_int32, c_void_p],
     ),
     "hs_append_rows": (
         c_int,

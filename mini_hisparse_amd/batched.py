@@ -244,11 +244,16 @@ class BatchedSparseDecode:
         alias = host_alias.data_ptr()
         hosts = self._hosts.get(alias)
         if hosts is None:
-            hosts = self._hosts[alias] = (ctypes.c_void_p * B)(*([alias] * B))
+            host_rows = host_alias.tensor.shape[0] * cfg.page_size
+            hosts = self._hosts[alias] = (
+                (ctypes.c_void_p * B)(*([alias] * B)), (ctypes.c_int64 * B)(*([host_rows] * B)),
+            )
         mh, md, mc, ns = self._miss_args
         row_bytes = cfg.kv_heads * cfg.head_dim * pool.element_size()
         _lib.check(
-            lib.hs_gather_rows_batched(hosts, pool.data_ptr(), mh, md, mc, ns, B, cfg.page_size, row_bytes, grid_x, stream.cuda_stream),
+            lib.hs_gather_rows_batched(hosts[0], pool.data_ptr(), mh, md, mc, ns, hosts[1],
+                                       pool.shape[0] * cfg.page_size, B, cfg.page_size, row_bytes, grid_x,
+                                       stream.cuda_stream),
             "hs_gather_rows_batched",
         )
 

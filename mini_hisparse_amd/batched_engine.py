@@ -529,12 +529,16 @@ class BatchedDecodeEngine:
         )
 
     @torch.inference_mode()
-    def step(self, tokens, observer=None, timer=None):
+    def step(self, tokens, observer=None, timer=None, probe=None):
         """One decode step for all B requests: `tokens` [B] int64 (device) -> next tokens.
 
         ``timer`` (optional list) receives, per layer, the stage events
         ``(layer, {stage: (start, end)}, entries)`` with ``entries`` the layer's
         attention entry total (device tensor) -- for profiling, not for timed runs.
+        ``probe`` (optional) is called as ``probe.before_attend(layer, stream, decoder)``
+        and ``probe.after_attend(layer, stream, decoder)`` around each layer's attention
+        launch on the stream it runs on (light enough for timed runs: events and a copy of
+        the decoder's entry counts).
         """
         model, st, dec = self.model, self.state, self.dec
         cfg = model.config
@@ -610,7 +614,11 @@ class BatchedDecodeEngine:
                     ready.record(transfer)
                     compute.wait_event(ready)
             marks["attend"] = [mark(compute)]
+            if probe is not None:
+                probe.before_attend(index, compute, dec)
             out = dec.attend(q, st.pool, out=self._attn_out)
+            if probe is not None:
+                probe.after_attend(index, compute, dec)
             marks["attend"].append(mark(compute))
             if observer is not None:
                 observer(index, q, k, v, out)

@@ -26,6 +26,11 @@ FLAGS = [
     "-O3",
     "-std=c++17",
     "-fPIC",
+    # only the extern "C" API of include/hisparse.h is exported (the header sets default
+    # visibility on it): kernel handles, device variables and hs:: helpers stay private, so
+    # two copies of the library in one process cannot bind each other's symbols
+    "-fvisibility=hidden",
+    "-fvisibility-inlines-hidden",
     "-Wall",
     "-Wno-unused-function",
     "-Wno-unused-variable",
@@ -65,7 +70,13 @@ def build(verbose: bool = True) -> Path:
             if log.strip():
                 print(f"[{src.name}]\n{log}", file=sys.stderr)
     tmp = LIBRARY.with_suffix(".so.tmp")
-    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
+    # the dynamic symbol table holds the hs_* C API only: kernel handles of
+    # non-template kernels and the per-file offload ids keep default visibility
+    # under -fvisibility=hidden, so a version script makes them local
+    exports = out_dir / "exports.map"
+    exports.write_text("{\n  global: hs_*;\n  local: *;\n};\n")
+    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", f"-Wl,--version-script={exports}",
+           "-o", str(tmp), *map(str, objs)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode:
         raise RuntimeError(f"link failed:\n{proc.stderr}")

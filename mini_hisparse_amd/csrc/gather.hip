@@ -6,7 +6,10 @@
 // the V plane row (Hkv * D elements each) of host row h into device row r.
 // Both pools are [blocks, 2, P, Hkv, D]; the kernel reads the pinned host pool
 // directly through its device alias, 16 bytes per lane, many rows in flight
-// per workgroup.  It is a byte copy: the dtype only sets the row size.
+// per workgroup.  It is a byte copy: the dtype only sets the row size.  A plan
+// entry whose host row is past the host pool or whose device row is past the
+// device pool is skipped like a -1 entry, so a corrupt plan cannot read or
+// write outside the two allocations.
 #include <stdlib.h>
 
 #include "hs_common.h"
@@ -23,6 +26,8 @@ struct GatherArgs {
   const int64_t* drows[GMAXB];
   const int64_t* count[GMAXB];  // nullable: number of leading valid entries
   int64_t n[GMAXB];
+  int64_t host_rows[GMAXB];     // rows of each plan's host pool
+  int64_t pool_rows;            // rows of the device pool
   int64_t P, row_bytes;
 };
 
@@ -63,6 +68,8 @@ __global__ __launch_bounds__(GT) void gather_kernel(GatherArgs a) {
   const char* host = a.host[b];
   const int64_t* hrows = a.hrows[b];
   const int64_t* drows = a.drows[b];
+  const uint64_t hlimit = static_cast<uint64_t>(a.host_rows[b]);
+  const uint64_t dlimit = static_cast<uint64_t>(a.pool_rows);
   if (units_row <= GT) {
     // fixed (row slot, unit) per thread
     const int64_t slot = threadIdx.x / units_row;
@@ -81,7 +88,8 @@ __global__ __launch_bounds__(GT) void gather_kernel(GatherArgs a) {
         if (!active || i >= n) continue;
         const int64_t h = hrows[i];
         const int64_t r = drows[i];
-        if (h < 0 || r < 0) continue;
+        // one unsigned compare rejects both -1 and rows past the pool
+        if (static_cast<uint64_t>(h) >= hlimit || static_cast<uint64_t>(r) >= dlimit) continue;
         const uint32_t hb = static_cast<uint32_t>(h) / P32, ho = static_cast<uint32_t>(h) - hb * P32;
         const uint32_t rb = static_cast<uint32_t>(r) / P32, ro = static_cast<uint32_t>(r) - rb * P32;
         const int64_t src = (static_cast<int64_t>(hb) * 2 * a.P + ho) * a.row_bytes + inrow;
@@ -97,7 +105,7 @@ __global__ __launch_bounds__(GT) void gather_kernel(GatherArgs a) {
     for (int64_t i = blockIdx.x; i < n; i += gridDim.x) {
       const int64_t h = hrows[i];
       const int64_t r = drows[i];
-      if (h < 0 || r < 0) continue;
+      if (static_cast<uint64_t>(h) >= hlimit || static_cast<uint64_t>(r) >= dlimit) continue;
       const uint32_t hb = static_cast<uint32_t>(h) / P32, ho = static_cast<uint32_t>(h) - hb * P32;
       const uint32_t rb = static_cast<uint32_t>(r) / P32, ro = static_cast<uint32_t>(r) - rb * P32;
       const int64_t sbase = (static_cast<int64_t>(hb) * 2 * a.P + ho) * a.row_bytes;
@@ -132,13 +140,16 @@ extern "C" int hs_host_alias(const void* host_ptr, void** device_ptr) {
 // hs_gather_rows_batched cuts larger batches into such chunks.
 static int gather_chunk(const void* const* host_alias, void* pool, const int64_t* const* miss_host_rows,
                         const int64_t* const* miss_device_rows, const int64_t* const* miss_counts,
-                        const int64_t* n, int32_t batch, int64_t page_size, int64_t row_bytes, int32_t grid_x,
-                        hipStream_t stream) {
+                        const int64_t* n, const int64_t* host_pool_rows, int64_t pool_rows, int32_t batch,
+                        int64_t page_size, int64_t row_bytes, int32_t grid_x, hipStream_t stream) {
   HS_CHECK_ARG(batch >= 1 && batch <= GMAXB, "gather batch must be in [1, %d]", GMAXB);
-  HS_CHECK_ARG(pool && host_alias && miss_host_rows && miss_device_rows && n, "null gather pointer");
+  HS_CHECK_ARG(pool && host_alias && miss_host_rows && miss_device_rows && n && host_pool_rows,
+               "null gather pointer");
   HS_CHECK_ARG(page_size >= 1 && row_bytes >= 2 && row_bytes % 2 == 0, "invalid gather row shape");
+  HS_CHECK_ARG(pool_rows >= 0 && pool_rows % page_size == 0, "device pool rows must be whole pages");
   GatherArgs a{};
   a.pool = static_cast<char*>(pool);
+  a.pool_rows = pool_rows;
   a.P = page_size;
   a.row_bytes = row_bytes;
   int64_t nmax = 0;
@@ -150,6 +161,9 @@ static int gather_chunk(const void* const* host_alias, void* pool, const int64_t
     a.drows[i] = miss_device_rows[i];
     a.count[i] = miss_counts ? miss_counts[i] : nullptr;
     a.n[i] = n[i];
+    HS_CHECK_ARG(host_pool_rows[i] >= 0 && host_pool_rows[i] % page_size == 0,
+                 "host pool rows must be whole pages");
+    a.host_rows[i] = host_pool_rows[i];
     if (n[i] > nmax) nmax = n[i];
     align |= reinterpret_cast<uintptr_t>(host_alias[i]);
   }
@@ -203,17 +217,24 @@ extern "C" int hs_gather_rows_batched(const void* const* host_alias, void* pool,
                                       const int64_t* const* miss_host_rows,
                                       const int64_t* const* miss_device_rows,
                                       const int64_t* const* miss_counts, const int64_t* n,
+                                      const int64_t* host_pool_rows, int64_t pool_rows,
                                       int32_t batch, int64_t page_size, int64_t row_bytes,
                                       int32_t grid_x, hipStream_t stream) {
   HS_CHECK_ARG(batch >= 1, "gather batch must be positive");
-  HS_CHECK_ARG(host_alias && miss_host_rows && miss_device_rows && n, "null gather pointer");
-  for (int32_t i = 0; i < batch; ++i)  // every plan, before the first launch
+  HS_CHECK_ARG(host_alias && miss_host_rows && miss_device_rows && n && host_pool_rows,
+               "null gather pointer");
+  HS_CHECK_ARG(page_size >= 1, "invalid gather page size");
+  HS_CHECK_ARG(pool_rows >= 0 && pool_rows % page_size == 0, "device pool rows must be whole pages");
+  for (int32_t i = 0; i < batch; ++i) {  // every plan, before the first launch
     HS_CHECK_ARG(host_alias[i] && miss_host_rows[i] && miss_device_rows[i], "null gather plan");
+    HS_CHECK_ARG(host_pool_rows[i] >= 0 && host_pool_rows[i] % page_size == 0,
+                 "host pool rows must be whole pages");
+  }
   for (int32_t s0 = 0; s0 < batch; s0 += GMAXB) {
     const int32_t c = batch - s0 < GMAXB ? batch - s0 : GMAXB;
     const int rc = gather_chunk(host_alias + s0, pool, miss_host_rows + s0, miss_device_rows + s0,
-                                miss_counts ? miss_counts + s0 : nullptr, n + s0, c, page_size, row_bytes,
-                                grid_x, stream);
+                                miss_counts ? miss_counts + s0 : nullptr, n + s0, host_pool_rows + s0,
+                                pool_rows, c, page_size, row_bytes, grid_x, stream);
     if (rc != HS_OK) return rc;
   }
   return HS_OK;
@@ -221,8 +242,10 @@ extern "C" int hs_gather_rows_batched(const void* const* host_alias, void* pool,
 
 extern "C" int hs_gather_rows(const void* host_alias, void* pool, const int64_t* miss_host_rows,
                               const int64_t* miss_device_rows, int64_t n, const int64_t* miss_count,
-                              int64_t page_size, int64_t row_bytes, hipStream_t stream) {
+                              int64_t host_pool_rows, int64_t pool_rows, int64_t page_size,
+                              int64_t row_bytes, hipStream_t stream) {
   const int64_t* counts[1] = {miss_count};
   return hs_gather_rows_batched(&host_alias, pool, &miss_host_rows, &miss_device_rows,
-                                miss_count ? counts : nullptr, &n, 1, page_size, row_bytes, 0, stream);
+                                miss_count ? counts : nullptr, &n, &host_pool_rows, pool_rows, 1,
+                                page_size, row_bytes, 0, stream);
 }

@@ -81,6 +81,8 @@ def gather_rows(host, pool, plan, config, *, miss_count=None):
         plan.miss_device_rows.data_ptr(),
         n,
         _lib.ptr(miss_count),
+        host.tensor.shape[0] * config.page_size,
+        pool.shape[0] * config.page_size,
         config.page_size,
         _row_bytes(config, pool.element_size()),
         _lib.stream_handle(pool.device),

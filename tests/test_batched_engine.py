@@ -30,22 +30,15 @@ def tiny(**overrides):
     return DecodeWorkload(**values)
 
 
-@pytest.mark.gpu
-@pytest.mark.parametrize(
-    "overrides,transfer_stream",
-    [
-        ({}, False),
-        ({}, True),
-        ({"heads": 16, "kv_heads": 2, "head_dim": 64, "hidden": 1024}, False),
-        # more requests than one launch of the scorer, union builder, resolver and gather
-        # (16) or of the append (32) takes: each entry point runs them in chunks
-        ({"batch": 34}, False),
-    ],
-)
-def test_batched_engine_layers_match_oracle(gpu, overrides, transfer_stream):
+def _engine_layers_match_oracle(gpu, wl, transfer_stream=False, steps=3):
+    """Run `steps` decode steps and check every layer of every request against the oracle:
+    the state's bounds are the exact extrema of the history read back from the host pool,
+    the Quest pages equal the oracle's over those bounds, and the attention output is the
+    oracle's sparse attention over the selected tokens."""
     from mini_hisparse_amd.batched_engine import BatchedDecodeEngine, build_state, random_model
 
-    wl = tiny(**overrides)
+    print(f"[case] {wl.name}: L={wl.layers} hidden={wl.hidden} heads={wl.heads}/{wl.kv_heads} "
+          f"D={wl.head_dim} ffn={wl.ffn} batch={wl.batch} context={wl.context}", flush=True)
     model = random_model(wl, gpu, seed=1)
     state = build_state(wl, gpu, seed=2)
     engine = BatchedDecodeEngine(model, state, wl.top_pages, transfer_stream=transfer_stream)
@@ -54,7 +47,7 @@ def test_batched_engine_layers_match_oracle(gpu, overrides, transfer_stream):
     records = []
     tokens = torch.arange(1, B + 1, device=gpu)
     unions = 0
-    for step in range(3):  # positions 639 (last row of a page), 640 (opens a page), 641
+    for step in range(steps):
         records.clear()
         tokens = engine.step(
             tokens,
@@ -85,7 +78,56 @@ def test_batched_engine_layers_match_oracle(gpu, overrides, transfer_stream):
                 unions += int(union_count[b])
     stats = state.row_stats.tolist()
     assert sum(stats) == unions  # every selected row was a resident hit, a hot hit or a miss
+    return stats
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize(
+    "overrides,transfer_stream",
+    [
+        ({}, False),
+        ({}, True),
+        ({"heads": 16, "kv_heads": 2, "head_dim": 64, "hidden": 1024}, False),
+        # more requests than one launch of the scorer, union builder, resolver and gather
+        # (16) or of the append (32) takes: each entry point runs them in chunks
+        ({"batch": 34}, False),
+    ],
+)
+def test_batched_engine_layers_match_oracle(gpu, overrides, transfer_stream):
+    stats = _engine_layers_match_oracle(gpu, tiny(**overrides), transfer_stream)
     assert stats[2] > 0 and stats[0] > 0 and stats[1] > 0
+
+
+def geometry(name, **overrides):
+    """The real layer geometry of a BASELINE model workload (hidden, heads, head_dim,
+    FFN, vocab, page budget, residency, hot rows) with two layers and the given batch
+    and context, for oracle checks of whole engine steps."""
+    from dataclasses import replace
+
+    from mini_hisparse_amd.batched_engine import WORKLOADS
+    from mini_hisparse_amd.selection import union_bound
+
+    wl = replace(WORKLOADS[name], layers=2, steps=8, **overrides)
+    bound = union_bound(wl.context + wl.steps, wl.page_size, wl.top_pages,
+                        1 if wl.selector == "uniform" else wl.heads)
+    return replace(wl, hot_rows=min(wl.hot_rows, 32768, max(2 * bound, bound)))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize(
+    "name,overrides",
+    [
+        # BASELINE configs[3] (north_star): hidden 3584, 28 q / 4 kv heads, head_dim 128,
+        # FFN 18944, vocab 152064, top-64 pages, 15% resident; 4k-token histories
+        ("qwen2.5-7b", {"batch": 4, "context": 4096 - 1}),
+        # BASELINE configs[2]: hidden 896, 14 q / 2 kv heads, head_dim 64, FFN 4864,
+        # vocab 151936, top-32 pages, 25% resident; the full 32k-token histories
+        ("qwen2.5-0.5b", {"batch": 4, "context": 32768 - 1}),
+    ],
+)
+def test_engine_at_model_geometry_matches_oracle(gpu, name, overrides):
+    stats = _engine_layers_match_oracle(gpu, geometry(name, **overrides))
+    assert stats[0] > 0 and stats[2] > 0
 
 
 @pytest.mark.gpu
@@ -120,30 +162,28 @@ def test_uniform_pages_draws_distinct_pages_with_the_tail():
     assert torch.equal(pages, again)
 
 
-@pytest.mark.gpu
-@pytest.mark.parametrize("prefetch", [False, True])
-def test_batched_engine_uniform_selection_matches_oracle(gpu, prefetch):
+def _uniform_engine_matches_oracle(gpu, wl, prefetch, steps=3):
     """The miss-heavy stress path: pages resampled every step and shared by every head,
     then union, resolver, gather and attention as for Quest selections.  With
     ``prefetch`` every layer's select, resolve and gather run at step start on the
     transfer stream (one decoder per layer), overlapping the dense layers."""
     from mini_hisparse_amd.batched_engine import BatchedDecodeEngine, build_state, random_model
-    from mini_hisparse_amd.selection import union_bound
 
-    wl = tiny(selector="uniform", hot_rows=2 * union_bound(40 * 16 + 23, 16, 6, 1), resident_fraction=0.4)
+    print(f"[case] {wl.name} uniform: L={wl.layers} hidden={wl.hidden} heads={wl.heads}/{wl.kv_heads} "
+          f"batch={wl.batch} context={wl.context} prefetch={prefetch}", flush=True)
     model = random_model(wl, gpu, seed=1)
     state = build_state(wl, gpu, seed=2)
     engine = BatchedDecodeEngine(model, state, wl.top_pages, selector="uniform", seed=4, prefetch=prefetch)
-    assert engine.dec.capacity == 6 * 16  # one head's selection bounds the union
+    assert engine.dec.capacity == wl.top_pages * wl.page_size  # one head's selection bounds the union
     if prefetch:
         assert len({id(engine.decoder(l)) for l in range(wl.layers)}) == wl.layers
         assert all(engine.decoder(l).attend_ws is engine.dec.attend_ws for l in range(wl.layers))
     L, B, C, P = wl.layers, wl.batch, state.pages, wl.page_size
     Hkv, D = wl.kv_heads, wl.head_dim
     records = []
-    tokens = torch.tensor([1, 2, 3], device=gpu)
+    tokens = torch.arange(1, B + 1, device=gpu)
     unions, drawn = 0, set()
-    for step in range(3):
+    for step in range(steps):
         records.clear()
         tokens = engine.step(
             tokens,
@@ -173,7 +213,28 @@ def test_batched_engine_uniform_selection_matches_oracle(gpu, prefetch):
     stats = state.row_stats.tolist()
     assert sum(stats) == unions
     assert stats[2] > stats[1]  # resampling every step: misses outnumber hot hits
-    assert len(drawn) >= 8 * L * B  # fresh draws each step (5 per step; about 13 distinct expected)
+    return stats, drawn
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("prefetch", [False, True])
+def test_batched_engine_uniform_selection_matches_oracle(gpu, prefetch):
+    from mini_hisparse_amd.selection import union_bound
+
+    wl = tiny(selector="uniform", hot_rows=2 * union_bound(40 * 16 + 23, 16, 6, 1), resident_fraction=0.4)
+    _, drawn = _uniform_engine_matches_oracle(gpu, wl, prefetch)
+    # fresh draws each step (5 per step; about 13 distinct expected per (layer, request))
+    assert len(drawn) >= 8 * wl.layers * wl.batch
+
+
+@pytest.mark.gpu
+def test_engine_at_stress_geometry_matches_oracle(gpu):
+    """BASELINE configs[4]'s layer geometry (hidden 5120, 40 q / 8 kv heads, head_dim 128,
+    FFN 27648, vocab 152064, 64 uniformly resampled pages shared by every head, 40%
+    resident, hot_rows 2048) with two layers, batch 2 and 8k-token histories, prefetched
+    as the bench runs it: about 60% of the selected rows miss."""
+    stats, _ = _uniform_engine_matches_oracle(gpu, geometry("qwen2.5-32b-stress", batch=2, context=8192), True)
+    assert stats[2] > 0.4 * sum(stats)
 
 
 @pytest.mark.gpu

@@ -377,6 +377,27 @@ def test_gather_copies_exactly_the_planned_rows():
     assert np.count_nonzero(pool) == 2 * 2 * 2 * 3  # nothing else written
 
 
+def test_bounded_gather_skips_rows_past_either_pool():
+    """The HIP gather's range rule: an entry whose host row is past the host pool
+    (6 pages x 4 = 24 rows) or whose device row is past the device pool (5 x 4 = 20)
+    is skipped like -1; every in-range entry is copied as the reference copies it."""
+    rng = np.random.default_rng(8)
+    host = rng.standard_normal((6, 2, 4, 2, 3))
+    plan_h = [5, 24, 23, 2, 9, 0]
+    plan_d = [0, 1, 20, 19, 2, 3]
+    pool = np.zeros((5, 2, 4, 2, 3))
+    oracle.gather_rows(host, pool, plan_h, plan_d, 4, bounded=True)
+    expected = np.zeros_like(pool)
+    for h, d in ((5, 0), (2, 19), (9, 2), (0, 3)):  # (24, 1) and (23, 20) are out of range
+        expected[d // 4, :, d % 4] = host[h // 4, :, h % 4]
+    np.testing.assert_array_equal(pool, expected)
+    # on a plan inside both pools the bounded rule is the reference's rule
+    a, b = np.zeros_like(pool), np.zeros_like(pool)
+    oracle.gather_rows(host, a, [5, -1, 23, 7], [0, 3, 19, -1], 4)
+    oracle.gather_rows(host, b, [5, -1, 23, 7], [0, 3, 19, -1], 4, bounded=True)
+    np.testing.assert_array_equal(a, b)
+
+
 # --------------------------------------------------------------------- append
 def test_append_bound_rule_known_answers():
     """torch.minimum/maximum on the device, as measured on MI355X: a NaN wins (the
