@@ -83,6 +83,9 @@ def parse_args():
     p.add_argument("--attention-sweep", action="store_true",
                    help="print the group attention's duration against its work (fixed cost and "
                         "incremental rate of both schedules) as a markdown table and exit")
+    p.add_argument("--summarize-trace", metavar="TRACE_DIR",
+                   help="summarise a rocprofv3 --kernel-trace run of this script (same --workload, --steps, "
+                        "--warmup) over its timed steps into profiles/ and exit")
     p.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                    help="summarise two rocprofv3 --pmc runs of this script (FETCH_SIZE, WRITE_SIZE) "
                         "into profiles/microbench_pmc.txt and exit")
@@ -664,6 +667,71 @@ def summarize_pmc(fetch_dir, write_dir, workload="microbench"):
     print("\n".join(lines))
 
 
+TRACE_SUMMARIES = {
+    "qwen2.5-7b": os.path.join(PROFILES, "qwen2.5-7b_e2e_kernel_trace.md"),
+}
+
+
+def summarize_trace(trace_dir, args):
+    """Per-kernel dispatches and durations over the timed steps of a model workload's
+    kernel trace.  Every decode step ends with the greedy argmax over the logits, so the
+    timed region runs from the kernel after the warmup-th argmax to the (warmup +
+    steps)-th argmax; it must hold layers x steps attention launches."""
+    import csv
+    import glob
+    from collections import defaultdict
+
+    from mini_hisparse_amd.batched_engine import WORKLOADS
+
+    wl = WORKLOADS[args.workload]
+    (path,) = glob.glob(os.path.join(trace_dir, "*kernel_trace.csv"))
+    rows = sorted(csv.DictReader(open(path)), key=lambda r: int(r["Start_Timestamp"]))
+    ends = [i for i, r in enumerate(rows) if "ArgMaxOps" in r["Kernel_Name"]]
+    L = wl.layers
+    if len(ends) < args.warmup + args.steps:
+        raise SystemExit(f"trace holds {len(ends)} decode steps, warmup + steps need {args.warmup + args.steps}")
+    start = ends[args.warmup - 1] + 1 if args.warmup else 0
+    window = rows[start : ends[args.warmup + args.steps - 1] + 1]
+    launches = sum("attend_mfma_kernel" in r["Kernel_Name"] for r in window)
+    if launches != L * args.steps:
+        raise SystemExit(f"the timed region holds {launches} attention launches, expected {L * args.steps}")
+    agg = defaultdict(lambda: [0, 0])
+    for r in window:
+        name = r["Kernel_Name"].split("(")[0].replace("void ", "")
+        agg[name][0] += 1
+        agg[name][1] += int(r["End_Timestamp"]) - int(r["Start_Timestamp"])
+    span_ms = (int(window[-1]["End_Timestamp"]) - int(window[0]["Start_Timestamp"])) / 1e6
+    cmd = f"rocprofv3 --kernel-trace --stats -f csv -d <dir> -o bench -- python3 bench.py --workload {args.workload} " \
+          f"--no-microbench --no-cpu-baseline --steps {args.steps} --warmup {args.warmup}"
+    att = [agg[k] for k in agg if k.startswith("hs::attend_mfma_kernel")]
+    mrg = [agg[k] for k in agg if k.startswith("hs::attend_merge_kernel")]
+    att_us = sum(d for _, d in att) / max(1, sum(c for c, _ in att)) / 1e3
+    mrg_us = sum(d for _, d in mrg) / max(1, sum(c for c, _ in mrg)) / 1e3
+    lines = [
+        f"# Kernel trace: {wl.name} end to end, timed steps only",
+        "",
+        f"Command: `{cmd}`",
+        f"Summarised by: `python bench.py --workload {args.workload} --steps {args.steps} --warmup {args.warmup} "
+        "--summarize-trace <dir>`",
+        "",
+        f"Timed region: {args.steps} steps x {L} layers, {len(window)} dispatches over {span_ms:.1f} ms "
+        f"({span_ms / args.steps:.2f} ms per step under the profiler).",
+        f"Attention (`hs_attend_groups`) per launch: attend_mfma_kernel {att_us:.2f} us + attend_merge_kernel "
+        f"{mrg_us:.2f} us = {att_us + mrg_us:.2f} us (the bench line's HIP events around the call also hold the "
+        "dispatch gap between the two kernels).",
+        "",
+        "| kernel | dispatches | total ms | avg us | ms per step |",
+        "|---|---|---|---|---|",
+    ]
+    for name, (count, dur) in sorted(agg.items(), key=lambda x: -x[1][1]):
+        lines.append(f"| `{name.replace('hs::', '')}` | {count} | {dur / 1e6:.2f} | {dur / count / 1e3:.2f} | "
+                     f"{dur / 1e6 / args.steps:.3f} |")
+    out = TRACE_SUMMARIES[args.workload]
+    with open(out, "w") as fh:
+        fh.write("\n".join(lines) + "\n")
+    print("\n".join(lines))
+
+
 def pmc_traffic(kernels=ROOFLINE_KERNELS, path=PMC_SUMMARY):
     """HBM bytes per launch of `kernels` (sum) from the committed counter summary, or None."""
     if not os.path.exists(path):
@@ -913,6 +981,9 @@ def run_model_workload(args, torch, device):
 
 def main():
     args = parse_args()
+    if args.summarize_trace:
+        summarize_trace(args.summarize_trace, args)
+        return
     if args.summarize_pmc:
         if args.workload not in PMC_SUMMARIES:
             raise SystemExit(f"counter summaries are kept for {sorted(PMC_SUMMARIES)}")
