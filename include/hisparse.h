@@ -175,6 +175,20 @@ int hs_resolve_rows(const hs_resolve_desc* desc, void* workspace, int64_t worksp
 int hs_resolve_rows_batched(const hs_resolve_desc* descs, int32_t count, void* workspace,
                             int64_t workspace_bytes, hs_stream_t stream);
 
+/*
+ * hs_resolve_rows_batched without a workspace argument: no counterpart in the
+ * reference.  For callers that cannot allocate device memory (code under graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  The scratch
+ * is a fixed device array inside the library, one per GPU, held until the
+ * process ends; a batch whose hs_resolve_workspace_bytes sum exceeds
+ * hs_resolve_noalloc_max_bytes() (32 MiB: 16 descriptors of the Qwen2.5-7B
+ * shape at 128k tokens) is rejected with HS_EINVAL.  Nothing is allocated and
+ * the outputs are those of hs_resolve_rows_batched.  Calls that overlap on one
+ * GPU (other streams or threads) share the array and race: serialise them.
+ */
+int64_t hs_resolve_noalloc_max_bytes(void);
+int hs_resolve_rows_noalloc(const hs_resolve_desc* descs, int32_t count, hs_stream_t stream);
+
 /* --------------------------------------------------------------- (3) gather */
 
 /*

@@ -76,6 +76,8 @@ SIGNATURES = {
     "hs_resolve_workspace_bytes": (c_int64, [c_int64, c_int64, c_int64, c_int64]),
     "hs_resolve_rows": (c_int, [POINTER(ResolveDesc), c_void_p, c_int64, c_void_p]),
     "hs_resolve_rows_batched": (c_int, [POINTER(ResolveDesc), c_int32, c_void_p, c_int64, c_void_p]),
+    "hs_resolve_noalloc_max_bytes": (c_int64, []),
+    "hs_resolve_rows_noalloc": (c_int, [POINTER(ResolveDesc), c_int32, c_void_p]),
     "hs_gather_rows": (
         c_int,
         [c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_void_p, c_int64, c_int64, c_int64, c_int64,

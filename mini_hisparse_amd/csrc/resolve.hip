@@ -34,6 +34,8 @@
 //
 // Preconditions, as in the reference: unique non-negative tags, an injective
 // source table, and length <= n_pages * page_size (checked on the host).
+#include <mutex>
+
 #include "hs_common.h"
 
 namespace hs {
@@ -588,8 +590,8 @@ extern "C" int64_t hs_resolve_workspace_bytes(int64_t n, int64_t length, int64_t
   return ws_layout(length, n_pages, hot_rows, nullptr, nullptr);
 }
 
-extern "C" int hs_resolve_rows_batched(const hs_resolve_desc* descs, int32_t count, void* workspace,
-                                       int64_t workspace_bytes, hipStream_t stream) {
+// Validates every descriptor and returns the workspace bytes the batch needs (< 0: error).
+static int64_t batch_workspace(const hs_resolve_desc* descs, int32_t count) {
   HS_CHECK_ARG(descs != nullptr && count >= 1, "resolver batch must be nonempty");
   int64_t need = 0;
   for (int32_t i = 0; i < count; ++i) {
@@ -597,8 +599,22 @@ extern "C" int hs_resolve_rows_batched(const hs_resolve_desc* descs, int32_t cou
     if (rc) return rc;
     need += hs_resolve_workspace_bytes(descs[i].n, descs[i].length, descs[i].n_pages, descs[i].hot_rows);
   }
+  return need;
+}
+
+// The four launches over validated descriptors; `workspace` holds the batch's need.
+static int resolve_launch(const hs_resolve_desc* descs, int32_t count, char* workspace, hipStream_t stream);
+
+extern "C" int hs_resolve_rows_batched(const hs_resolve_desc* descs, int32_t count, void* workspace,
+                                       int64_t workspace_bytes, hipStream_t stream) {
+  const int64_t need = batch_workspace(descs, count);
+  if (need < 0) return static_cast<int>(need);
   HS_CHECK_ARG(workspace != nullptr && workspace_bytes >= need,
                "resolver workspace too small: need %lld bytes", static_cast<long long>(need));
+  return resolve_launch(descs, count, static_cast<char*>(workspace), stream);
+}
+
+static int resolve_launch(const hs_resolve_desc* descs, int32_t count, char* workspace, hipStream_t stream) {
   static bool attr_set = false;
   if (!attr_set) {
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(resolve_mark_kernel),
@@ -606,7 +622,7 @@ extern "C" int hs_resolve_rows_batched(const hs_resolve_desc* descs, int32_t cou
     (void)hipGetLastError();
     attr_set = true;
   }
-  char* ws = static_cast<char*>(workspace);
+  char* ws = workspace;
   for (int32_t start = 0; start < count; start += RMAXB) {
     ResolveBatch batch{};
     batch.count = count - start < RMAXB ? count - start : RMAXB;
@@ -640,4 +656,57 @@ extern "C" int hs_resolve_rows_batched(const hs_resolve_desc* descs, int32_t cou
 extern "C" int hs_resolve_rows(const hs_resolve_desc* desc, void* workspace, int64_t workspace_bytes,
                                hipStream_t stream) {
   return hs_resolve_rows_batched(desc, 1, workspace, workspace_bytes, stream);
+}
+
+// ---- the resolver without a caller workspace ----------------------------------
+// For callers that cannot allocate (code under graph capture, serving loops,
+// harnesses that forbid hipMalloc): the workspace is this file-scope device
+// array, one copy per GPU, held until the process ends.  The resolver's kernels
+// clear every part of the workspace they read before reading it (the mark
+// launch resets the bitmaps, the protection bits and the host-block hash), so
+// nothing is left over from an earlier call; calls that overlap on one GPU
+// (two streams, or two host threads) share the array and race.
+namespace hs {
+constexpr int64_t kNoAllocScratchBytes = static_cast<int64_t>(32) << 20;
+constexpr int kMaxDevices = 64;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+}  // namespace hs
+
+extern "C" int64_t hs_resolve_noalloc_max_bytes(void) { return kNoAllocScratchBytes; }
+
+extern "C" int hs_resolve_rows_noalloc(const hs_resolve_desc* descs, int32_t count, hipStream_t stream) {
+  // Device address of this GPU's copy of `scratch`: in host code the array's name
+  // stands for a host-side shadow, never a device address, so it is looked up once
+  // per device (with that device current) and only the looked-up pointer is used.
+  static void* device_scratch[kMaxDevices] = {};
+  static std::mutex lock;
+  int device = -1;
+  hipError_t e = hipGetDevice(&device);
+  if (e != hipSuccess || device < 0 || device >= kMaxDevices) {
+    (void)hipGetLastError();
+    hs::set_error("hs_resolve_rows_noalloc: no current device (%s)", hipGetErrorString(e));
+    return HS_ERUNTIME;
+  }
+  void* ptr = nullptr;
+  {
+    std::lock_guard<std::mutex> guard(lock);
+    ptr = device_scratch[device];
+    if (ptr == nullptr) {
+      e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+      if (e != hipSuccess || ptr == nullptr) {
+        (void)hipGetLastError();
+        hs::set_error("hs_resolve_rows_noalloc: cannot resolve the scratch array on device %d: %s", device,
+                      hipGetErrorString(e));
+        return HS_ERUNTIME;
+      }
+      device_scratch[device] = ptr;
+    }
+  }
+  const int64_t need = batch_workspace(descs, count);
+  if (need < 0) return static_cast<int>(need);
+  HS_CHECK_ARG(need <= kNoAllocScratchBytes,
+               "hs_resolve_rows_noalloc: the batch needs %lld bytes of scratch, above the fixed %lld; "
+               "split it or call hs_resolve_rows_batched with a workspace",
+               static_cast<long long>(need), static_cast<long long>(kNoAllocScratchBytes));
+  return resolve_launch(descs, count, static_cast<char*>(ptr), stream);
 }

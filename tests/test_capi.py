@@ -60,6 +60,7 @@ def test_host_queries_and_argument_errors_without_a_gpu():
     assert lib.hs_resolve_workspace_bytes(1000, 4096, 256, 512) > 0
     assert lib.hs_quest_workspace_bytes(2, 8, 100) >= 2 * 8 * 100 * 4
     assert lib.hs_attend_workspace_bytes(2, 1, 8, 2, 64, 100) > 0
+    assert lib.hs_resolve_noalloc_max_bytes() == 32 << 20
     desc = _lib.ResolveDesc()  # all null: rejected on the host, before any launch
     assert lib.hs_resolve_rows(desc, None, 0, None) == -1
     assert b"nonempty" in lib.hs_last_error()
