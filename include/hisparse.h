@@ -250,6 +250,32 @@ int hs_append_rows(const void* k, const void* v, int64_t kv_stride_b, void* pool
                    int64_t host_pool_rows, void* const* minimum, void* const* maximum, int32_t batch,
                    hs_stream_t stream);
 
+/*
+ * A write of `tokens` consecutive K/V rows to one (request, layer) whose page
+ * placement the caller has decided: the page loop of HostStore.append
+ * (mini_hisparse/storage.py:273-318) -- prefill or decode -- in one launch per 64
+ * pages.
+ *   k, v        [tokens, kv_heads, head_dim] in the pool dtype, kv_stride_t elements
+ *               between token rows
+ *   first_page / first_within  logical page and row of the first token; the write
+ *               covers `pages` = ceil((first_within + tokens) / page_size) pages
+ *   slots       host array [pages]: device block of each page, -1 = not resident
+ *               (rows go to the host mirror only); host_slots host array [pages]
+ *   minimum, maximum  the (request, layer)'s bounds [bound_pages, kv_heads, head_dim]
+ *               in the pool dtype: each page folds its new K rows in order with the
+ *               rule of hs_append_rows
+ *   summaries   nullable [bound_pages, kv_heads, head_dim] float32: the mean K of all
+ *               the page's valid rows (earlier rows read back from its device block,
+ *               or from its host slot when not resident), summed in row order
+ * Every block and host slot is checked against the pools before the first launch.
+ */
+int hs_append_tokens(const void* k, const void* v, int64_t kv_stride_t, int64_t tokens, void* pool,
+                     int64_t pool_rows, const void* host_alias, int64_t host_pool_rows, int32_t dtype,
+                     int64_t page_size, int64_t kv_heads, int64_t head_dim, int64_t first_page,
+                     int64_t first_within, int64_t pages, const int64_t* slots, const int64_t* host_slots,
+                     void* minimum, void* maximum, float* summaries, int64_t bound_pages,
+                     hs_stream_t stream);
+
 /* ------------------------------------------------------------ (4) attention */
 
 /* Scratch bytes of one attention call (split-K partials). */

@@ -94,6 +94,12 @@ SIGNATURES = {
          POINTER(c_int64), POINTER(c_void_p), POINTER(c_int64), c_int64, POINTER(c_void_p),
          POINTER(c_void_p), c_int32, c_void_p],
     ),
+    "hs_append_tokens": (
+        c_int,
+        [c_void_p, c_void_p, c_int64, c_int64, c_void_p, c_int64, c_void_p, c_int64, c_int32,
+         c_int64, c_int64, c_int64, c_int64, c_int64, c_int64, POINTER(c_int64), POINTER(c_int64),
+         c_void_p, c_void_p, c_void_p, c_int64, c_void_p],
+    ),
     "hs_attend_workspace_bytes": (c_int64, [c_int32, c_int64, c_int64, c_int64, c_int64, c_int64]),
     "hs_attend_rows": (
         c_int,

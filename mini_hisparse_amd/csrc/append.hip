@@ -173,3 +173,167 @@ extern "C" int hs_append_rows(const void* k, const void* v, int64_t kv_stride_b,
   }
   return HS_OK;
 }
+
+// ---- batched write of T tokens to one (request, layer) --------------------------
+//
+// Replaces the page loop of HostStore.append (storage.py:273-318) for a write
+// whose page placement the caller has decided: token rows go to their page's
+// device block (when the page is resident) and to its host slot (the mirror);
+// each page's bounds fold its new K rows in order with the rule above; each
+// page's mean-K summary is recomputed over all its valid rows (rows written
+// by earlier writes are read back from the device block when resident, else
+// from the host slot), summed in row order in float32 and divided.  One
+// workgroup per page.
+
+namespace hs {
+
+constexpr int TMAXP = 64;
+
+struct TokenAppendArgs {
+  const char* k;
+  const char* v;
+  int64_t kv_sb;  // bytes between token rows of k and v
+  char* pool;
+  char* host;
+  char* kmin;  // bounds of the (request, layer): [pages, Hkv, D] in the KV dtype
+  char* kmax;
+  float* summ;  // nullable [pages, Hkv, D] float32
+  int64_t P, row_bytes, n_elem, esz;
+  int64_t first_page, first_within, tokens;
+  int32_t slot[TMAXP], hslot[TMAXP];
+};
+
+template <int DT>
+__device__ __forceinline__ bool takes_new_min(float old, float x) {
+  if (old != old) return false;
+  if (x != x) return true;
+  if constexpr (DT == HS_DTYPE_F32) return x < old || (x == 0.f && old == 0.f && signbit(x) && !signbit(old));
+  else return !(old < x);
+}
+template <int DT>
+__device__ __forceinline__ bool takes_new_max(float old, float x) {
+  if (old != old) return false;
+  if (x != x) return true;
+  if constexpr (DT == HS_DTYPE_F32) return x > old || (x == 0.f && old == 0.f && !signbit(x) && signbit(old));
+  else return !(old > x);
+}
+
+template <int DT, int U>
+__global__ __launch_bounds__(AT) void append_tokens_kernel(TokenAppendArgs a) {
+  typedef typename std::conditional<U == 16, u32x4, unsigned short>::type T;
+  const int j = blockIdx.x;
+  const int64_t page = a.first_page + j;
+  const int64_t within = j == 0 ? a.first_within : 0;
+  const int64_t t0 = j == 0 ? 0 : (a.P - a.first_within) + static_cast<int64_t>(j - 1) * a.P;
+  const int64_t room = a.P - within, left = a.tokens - t0;
+  const int64_t count = room < left ? room : left;
+  const int64_t slot = a.slot[j], hslot = a.hslot[j];
+  const int64_t plane = a.P * a.row_bytes;
+  // rows: K and V of every new token, to the device block (if resident) and the host slot
+  const int64_t units = a.row_bytes / U;
+  for (int64_t w = threadIdx.x; w < count * units; w += AT) {
+    const int64_t r = w / units, u = w - r * units;
+    const T kx = *reinterpret_cast<const T*>(a.k + (t0 + r) * a.kv_sb + u * U);
+    const T vx = *reinterpret_cast<const T*>(a.v + (t0 + r) * a.kv_sb + u * U);
+    const int64_t in_page = (within + r) * a.row_bytes + u * U;
+    if (slot >= 0) {
+      char* d = a.pool + slot * 2 * plane + in_page;
+      *reinterpret_cast<T*>(d) = kx;
+      *reinterpret_cast<T*>(d + plane) = vx;
+    }
+    char* h = a.host + hslot * 2 * plane + in_page;
+    *reinterpret_cast<T*>(h) = kx;
+    *reinterpret_cast<T*>(h + plane) = vx;
+  }
+  // bounds and summary, one (kv head, channel) element per thread
+  const char* old_rows = slot >= 0 ? a.pool + slot * 2 * plane : a.host + hslot * 2 * plane;
+  for (int64_t e = threadIdx.x; e < a.n_elem; e += AT) {
+    const int64_t at = page * a.n_elem + e;
+    float lo = load_elem<DT>(a.kmin, at), hi = load_elem<DT>(a.kmax, at);
+    bool lo_new = false, hi_new = false;
+    float acc = 0.f;
+    for (int64_t r = 0; r < within; ++r) acc += load_elem<DT>(old_rows, r * a.n_elem + e);
+    for (int64_t r = 0; r < count; ++r) {
+      const float x = load_elem<DT>(a.k + (t0 + r) * a.kv_sb, e);
+      if (takes_new_min<DT>(lo, x)) lo = x, lo_new = true;
+      if (takes_new_max<DT>(hi, x)) hi = x, hi_new = true;
+      acc += x;
+    }
+    // a bound is rewritten only when it changed: an unchanged one keeps its exact bits
+    if (lo_new) store_elem<DT>(a.kmin, at, lo);
+    if (hi_new) store_elem<DT>(a.kmax, at, hi);
+    if (a.summ) a.summ[at] = acc / static_cast<float>(within + count);
+  }
+}
+
+}  // namespace hs
+
+extern "C" int hs_append_tokens(const void* k, const void* v, int64_t kv_stride_t, int64_t tokens, void* pool,
+                                int64_t pool_rows, const void* host_alias, int64_t host_pool_rows, int32_t dtype,
+                                int64_t page_size, int64_t kv_heads, int64_t head_dim, int64_t first_page,
+                                int64_t first_within, int64_t pages, const int64_t* slots,
+                                const int64_t* host_slots, void* minimum, void* maximum, float* summaries,
+                                int64_t bound_pages, hipStream_t stream) {
+  HS_CHECK_ARG(valid_dtype(dtype), "invalid dtype code %d", dtype);
+  HS_CHECK_ARG(k && v && pool && host_alias && slots && host_slots && minimum && maximum, "null append pointer");
+  HS_CHECK_ARG(page_size >= 1 && kv_heads >= 1 && head_dim >= 1 && tokens >= 1, "invalid append shape");
+  HS_CHECK_ARG(first_within >= 0 && first_within < page_size, "first row must lie inside its page");
+  HS_CHECK_ARG(pages == (first_within + tokens + page_size - 1) / page_size,
+               "%lld pages cannot hold %lld tokens from row %lld", static_cast<long long>(pages),
+               static_cast<long long>(tokens), static_cast<long long>(first_within));
+  HS_CHECK_ARG(first_page >= 0 && first_page + pages <= bound_pages, "pages outside the bounds tensor");
+  const int64_t pool_blocks = pool_rows / page_size, host_blocks = host_pool_rows / page_size;
+  for (int64_t p = 0; p < pages; ++p) {  // every page, before the first launch
+    HS_CHECK_ARG(slots[p] >= -1 && slots[p] < pool_blocks, "append block %lld outside the pool",
+                 static_cast<long long>(slots[p]));
+    HS_CHECK_ARG(host_slots[p] >= 0 && host_slots[p] < host_blocks, "append host slot %lld outside the host pool",
+                 static_cast<long long>(host_slots[p]));
+  }
+  const int64_t esz = elem_bytes(dtype);
+  TokenAppendArgs a{};
+  a.k = static_cast<const char*>(k);
+  a.v = static_cast<const char*>(v);
+  a.kv_sb = kv_stride_t * esz;
+  a.pool = static_cast<char*>(pool);
+  a.host = static_cast<char*>(const_cast<void*>(host_alias));
+  a.kmin = static_cast<char*>(minimum);
+  a.kmax = static_cast<char*>(maximum);
+  a.summ = summaries;
+  a.P = page_size;
+  a.n_elem = kv_heads * head_dim;
+  a.esz = esz;
+  a.row_bytes = a.n_elem * esz;
+  const uintptr_t align = reinterpret_cast<uintptr_t>(k) | reinterpret_cast<uintptr_t>(v) |
+                          reinterpret_cast<uintptr_t>(pool) | reinterpret_cast<uintptr_t>(host_alias) |
+                          static_cast<uintptr_t>(a.kv_sb) | static_cast<uintptr_t>(a.row_bytes);
+  const bool wide = (align & 15) == 0;
+  int64_t token = 0;
+  for (int64_t p0 = 0; p0 < pages; p0 += TMAXP) {
+    const int64_t n = pages - p0 < TMAXP ? pages - p0 : TMAXP;
+    const int64_t within = p0 == 0 ? first_within : 0;
+    a.first_page = first_page + p0;
+    a.first_within = within;
+    const int64_t chunk_tokens = (within + tokens - token) < n * page_size ? tokens - token : n * page_size - within;
+    a.tokens = chunk_tokens;
+    a.k = static_cast<const char*>(k) + token * a.kv_sb;
+    a.v = static_cast<const char*>(v) + token * a.kv_sb;
+    for (int64_t i = 0; i < n; ++i) {
+      a.slot[i] = static_cast<int32_t>(slots[p0 + i]);
+      a.hslot[i] = static_cast<int32_t>(host_slots[p0 + i]);
+    }
+    const dim3 grid(static_cast<unsigned>(n));
+    if (dtype == HS_DTYPE_BF16) {
+      if (wide) hipLaunchKernelGGL((append_tokens_kernel<HS_DTYPE_BF16, 16>), grid, dim3(AT), 0, stream, a);
+      else hipLaunchKernelGGL((append_tokens_kernel<HS_DTYPE_BF16, 2>), grid, dim3(AT), 0, stream, a);
+    } else if (dtype == HS_DTYPE_F16) {
+      if (wide) hipLaunchKernelGGL((append_tokens_kernel<HS_DTYPE_F16, 16>), grid, dim3(AT), 0, stream, a);
+      else hipLaunchKernelGGL((append_tokens_kernel<HS_DTYPE_F16, 2>), grid, dim3(AT), 0, stream, a);
+    } else {
+      if (wide) hipLaunchKernelGGL((append_tokens_kernel<HS_DTYPE_F32, 16>), grid, dim3(AT), 0, stream, a);
+      else hipLaunchKernelGGL((append_tokens_kernel<HS_DTYPE_F32, 2>), grid, dim3(AT), 0, stream, a);
+    }
+    HS_CHECK_LAUNCH("append tokens");
+    token += chunk_tokens;
+  }
+  return HS_OK;
+}

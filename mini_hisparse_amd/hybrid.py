@@ -1,22 +1,27 @@
-"""Hybrid residency policy: block leases on one slab, token-row hot contents.
+"""Hybrid residency: resident-page block leases and per-layer token-row hot regions
+on one device slab.
 
-Behaviour follows the reference ``HybridKVCache`` (hybrid.py:106-609) decision
-for decision, so row statistics and residency trajectories are the same:
+Policy (the reference's ``HybridKVCache``, ``mini_hisparse/hybrid.py:106-609``;
+its observable decisions are kept so row statistics and counters match):
 
-* admission reserves, per layer, credits for a fixed hot region
-  (``ceil(hot_rows / P)`` blocks) plus two active tail pages;
-* resident history may borrow every unused credit; when a layer's window,
-  the free-block watermark or allocation pressure demands it, the layer
-  takes its whole hot region at once and its clean, sealed history (outside
-  the two tails) becomes reclaimable: still readable until a new owner
-  actually takes the block;
-* each attention resolves selected tokens to physical rows on the GPU, loads
-  misses from pinned host memory on the transfer stream, and reads rows after
-  the load's event (``RowLease``).
+* admission reserves, per layer, the blocks of a fixed hot region
+  (``ceil(hot_rows / P)``) plus the two active tail pages; resident history may
+  borrow every block nobody has reserved;
+* a layer *requires* its hot region when the allocatable blocks fall under the
+  watermark, when its resident pages reach the window, under allocation
+  pressure, or on request; it then takes the whole region at once, and its
+  clean, sealed history outside the two tails becomes *reclaimable*: readable
+  until another owner actually takes the block;
+* an attention resolves selected tokens to physical rows on the device, loads
+  the misses from pinned host memory on the transfer stream, and reads the
+  rows after the load's event (:class:`RowLease`).
 
-Differences in structure (not behaviour): kernels come from an ops backend
-(HIP by default), per-layer page scans use the allocator's per-layer index,
-and Quest selections may stay on the device (``DeviceSelection``).
+Structure (this module's own): the policy works on the storage's per-(request,
+layer) page arrays and the allocator's block table -- candidate sets are array
+masks ordered by bind stamps, not scans over page objects -- and the device
+tables ``source``/``resident`` are mirrors of the host arrays, uploaded in one
+copy of the changed range before the resolver reads them instead of one element
+write per page event.  Kernels come from an ops backend (HIP by default).
 """
 
 from __future__ import annotations
@@ -26,14 +31,15 @@ from contextlib import suppress
 from dataclasses import dataclass, field
 from math import ceil
 
+import numpy as np
 import torch
 
-from .allocator import DeviceAllocator
+from .allocator import NO_GROUP, DeviceAllocator
 from .config import CapacityError
 from .row_index import LogicalTopK
-from .storage import HostStore, Location, PageLease
+from .storage import HostStore, Location, Page, PageLease
 
-ACTIVE_TAIL_PAGES = 2  # the appending page and the one before it stay resident
+ACTIVE_TAIL_PAGES = 2  # the page being appended and the one before it stay resident
 
 
 @dataclass(frozen=True)
@@ -61,7 +67,9 @@ class HotConfig:
 
 @dataclass
 class LayerTables:
-    source: torch.Tensor  # [pages] int32 host slot of each logical page
+    """Device tables of one (request, layer), read and updated by the resolver."""
+
+    source: torch.Tensor  # [pages] int32 host slot of each logical page, -1
     resident: torch.Tensor  # [pages] int32 device block of a resident page, -1
     hot: torch.Tensor  # [hot_blocks] int32 device block of each hot block
     tags: torch.Tensor  # [hot_rows] int32 host row cached in each hot slot, -1
@@ -72,6 +80,7 @@ class LayerTables:
     busy: bool = False
     hot_required: bool = False
     trigger: str | None = None
+    stale: list = field(default_factory=lambda: [0, 0])  # [lo, hi) pages whose mirrors are not uploaded
 
     @property
     def nbytes(self):
@@ -79,13 +88,20 @@ class LayerTables:
 
 
 class RowLease:
-    """Resolved rows of one (request, layer), readable between wait() and release()."""
+    """Resolved rows of one (request, layer), readable between ``wait`` and ``release``."""
 
-    def __init__(self, cache, tables, plan, pages):
-        self.cache, self.tables, self.plan, self.pages = cache, tables, plan, pages
-        slots = cache.allocator.slots
-        self.handles = [(i, slots[i].generation, slots[i].owner) for i in tables.blocks + [p.slot for p in pages]]
+    def __init__(self, cache, group, tables, plan, pinned):
+        self.cache, self.tables, self.plan = cache, tables, plan
+        self._lp, self._pinned = cache.storage.layer_pages(*group), pinned
+        table = cache.allocator
+        blocks = list(tables.blocks) + self._lp.slot[pinned].tolist()
+        self.handles = [(b, int(table.generation[b]), table.owner_key(b)) for b in blocks]
         self.released = False
+
+    @property
+    def pages(self):
+        group = self.cache.allocator.group_key(self._lp.gid)
+        return [Page(self._lp, (*group, int(i))) for i in self._pinned]
 
     def _validate(self):
         self.cache.storage.check_stream()
@@ -100,13 +116,11 @@ class RowLease:
 
     def release(self):
         self._validate()
-        storage = self.cache.storage
-        self.tables.last_use = storage.event(storage.compute)
-        for page in self.pages:
-            page.last_use = self.tables.last_use
-            page.pins -= 1
-            if not page.pins:
-                storage.pinned.discard(page.key)
+        done = self.cache.storage.event(self.cache.storage.compute)
+        self.tables.last_use = done
+        for i in self._pinned.tolist():
+            self._lp.last_use[i] = done
+        self._lp.pins[self._pinned] -= 1
         self.tables.busy = False
         self.released = True
 
@@ -118,6 +132,27 @@ class RowLease:
         self.release()
 
 
+class _PendingClean:
+    """Pages written since the last publication of completed host mirrors (a set of
+    page keys over a per-layer flag array)."""
+
+    def __init__(self, cache):
+        self._cache = cache
+
+    def add(self, key):
+        self._cache.storage.layer_pages(*key[:2]).unpublished[key[2]] = True
+
+    def discard(self, key):
+        if key in self._cache.storage.pages:
+            self._cache.storage.layer_pages(*key[:2]).unpublished[key[2]] = False
+
+    def __contains__(self, key):
+        return key in self._cache.storage.pages and bool(self._cache.storage.layer_pages(*key[:2]).unpublished[key[2]])
+
+    def __len__(self):
+        return sum(int(np.count_nonzero(lp.unpublished)) for r in self._cache.storage.requests.values() for lp in r.pages)
+
+
 class HybridKVCache:
     """One slab; resident blocks and per-layer hot regions lease from it."""
 
@@ -127,21 +162,21 @@ class HybridKVCache:
 
             ops = default_ops(config.device)
         self.ops = ops
+        self.config = config
         self.hot_config = hot
         self.hot_blocks = ceil(hot.hot_rows / config.page_size)
-        self.tables: dict[tuple, LayerTables] = {}
-        self._writing_key = None
-        self.pending_clean: set = set()
-        self.config = config
-        self.allocator = DeviceAllocator(config)
-        self.storage = HostStore(config, self.allocator)
-        self.pool, self.device = self.allocator.storage, self.storage.device
         if config.host_pages * config.page_size >= 2**31:
             raise ValueError("host row tags require int32 addresses")
+        self.allocator = DeviceAllocator(config)
+        self.storage = HostStore(config, self.allocator, ops)
+        self.pool, self.device = self.allocator.storage, self.storage.device
+        self.tables: dict[tuple, LayerTables] = {}
         self.row_stats = torch.zeros(3, dtype=torch.int64, device=self.device)
-        self._host_source = ops.host_source(self.storage.host)
+        self.pending_clean = _PendingClean(self)
+        self._writing = None  # (group, page index) of the page being appended
+        self._dirty: set = set()  # groups whose device tables lag their page arrays
 
-    # -- views ---------------------------------------------------------------
+    # -- views ------------------------------------------------------------------------
     @property
     def index_bytes(self):
         return self.storage.index_bytes
@@ -154,12 +189,9 @@ class HybridKVCache:
     def owners(self):
         return self.storage.owners
 
-    def _owner(self, slot):
-        return self.allocator.slots[slot].owner
-
     def index_reservation_bytes(self, max_tokens, layers):
-        tables = ceil(max_tokens / self.config.page_size) * 8 + self.hot_blocks * 4 + self.hot_config.hot_rows * 12
-        return self.storage.index_reservation_bytes(max_tokens, layers) + layers * tables
+        per_layer = ceil(max_tokens / self.config.page_size) * 8 + self.hot_blocks * 4 + self.hot_config.hot_rows * 12
+        return self.storage.index_reservation_bytes(max_tokens, layers) + layers * per_layer
 
     def admission_blocks(self, layers):
         return self.hot_config.admission_blocks(self.config.page_size, layers)
@@ -169,40 +201,51 @@ class HybridKVCache:
         configured = self.hot_config.transition_watermark
         return max(self.hot_blocks, self.budget // 10) if configured is None else configured
 
-    # -- block supply --------------------------------------------------------
-    def _readable_unpinned(self):
-        pages = self.storage.pages
-        return [
-            i for i in self.allocator.reclaimable if i < self.budget and not pages[self._owner(i)].pins
-        ]
+    def _lp(self, group):
+        return self.storage.layer_pages(*group)
+
+    def _page(self, group, index):
+        return Page(self._lp(group), (*group, int(index)))
+
+    # -- block supply -------------------------------------------------------------------
+    def _readable_blocks(self):
+        """Reclaimable blocks inside the budget whose page is not pinned, in queue order."""
+        table = self.allocator
+        queue = table.reclaim_queue(self.budget)
+        keep = [b for b in queue.tolist()
+                if not self._lp(table.group_key(int(table.owner_group[b]))).pins[table.owner_index[b]]]
+        return keep
 
     def _available_blocks(self):
-        """Empty blocks (ascending) first, then readable unpinned blocks (unpin order)."""
-        empty = sorted(i for i in self.allocator.free if i < self.budget)
-        return empty + self._readable_unpinned()
+        """Empty blocks (ascending) first, then readable unpinned blocks (queue order)."""
+        return self.allocator.free_blocks(self.budget).tolist() + self._readable_blocks()
 
     def _available_count(self):
-        return sum(1 for i in self.allocator.free if i < self.budget) + len(self._readable_unpinned())
+        return len(self.allocator.free_blocks(self.budget)) + len(self._readable_blocks())
 
     def _first_available(self):
-        empty = [i for i in self.allocator.free if i < self.budget]
-        if empty:
-            return min(empty)
-        readable = self._readable_unpinned()
+        empty = self.allocator.free_blocks(self.budget)
+        if len(empty):
+            return int(empty[0])
+        readable = self._readable_blocks()
         return readable[0] if readable else None
 
-    def _take_block(self, slot):
-        if slot in self.allocator.reclaimable:
-            self.allocator.reclaim(slot)
-        return slot
+    def _take_block(self, block):
+        if self.allocator.reclaim_stamp[block] >= 0:
+            self.allocator.reclaim(block)
+        return block
 
-    def _on_block_reused(self, slot):
-        page = self.storage.pages[self._owner(slot)]
-        assert not page.pins and page.host_committed_version == page.content_version
-        self._detach(page)
+    def _on_block_reused(self, block):
+        table = self.allocator
+        group = table.group_key(int(table.owner_group[block]))
+        index = int(table.owner_index[block])
+        lp = self._lp(group)
+        if lp.pins[index] or lp.committed[index] != lp.version[index]:
+            raise AssertionError("a reclaimable block must hold a clean, unpinned page")
+        self._detach(self._page(group, index))
         self.storage.stats["unpinned_block_reuses"] += 1
 
-    # -- admission -----------------------------------------------------------
+    # -- admission -------------------------------------------------------------------------
     def reserve(self, request_id, max_tokens, layers):
         self.collect()
         promised = sum(self.admission_blocks(r.layers) for r in self.storage.requests.values())
@@ -211,87 +254,122 @@ class HybridKVCache:
         extra = self.index_reservation_bytes(max_tokens, layers) - self.storage.index_reservation_bytes(max_tokens, layers)
         self.storage.reserve(request_id, max_tokens, layers, extra_index_bytes=extra)
         pages = self.storage.requests[request_id].page_count
-        hot_rows = self.hot_config.hot_rows
-
-        def empty(size):
-            return torch.full((size,), -1, dtype=torch.int32, device=self.device)
-
         for layer in range(layers):
+            empty = lambda n: torch.full((n,), -1, dtype=torch.int32, device=self.device)  # noqa: E731
             self.tables[request_id, layer] = LayerTables(
-                empty(pages),
-                empty(pages),
-                empty(self.hot_blocks),
-                empty(hot_rows),
-                torch.arange(hot_rows, device=self.device, dtype=torch.int64),
+                empty(pages), empty(pages), empty(self.hot_blocks), empty(self.hot_config.hot_rows),
+                torch.arange(self.hot_config.hot_rows, dtype=torch.int64, device=self.device),
             )
 
-    # -- append placement ----------------------------------------------------
-    def _prepare_append(self, page):
-        self._writing_key = page.key
-        tables = self.tables[page.key[:2]]
-        # table entries are set with fill kernels on the compute stream: assigning a
-        # Python int to a device element is a synchronising copy on ROCm PyTorch
-        tables.source[page.key[2]].fill_(page.host_slot)
+    # -- device tables ---------------------------------------------------------------------
+    def _stale(self, group, index):
+        lo, hi = self.tables[group].stale
+        self.tables[group].stale = [index, index + 1] if lo >= hi else [min(lo, index), max(hi, index + 1)]
+        self._dirty.add(group)
+
+    def _sync_tables(self):
+        """Upload every group's changed table range: called when a public operation
+        that moves pages returns, so the device tables always match the page arrays
+        outside the cache's own methods."""
+        for group in self._dirty:
+            if group in self.tables:
+                self._upload(group)
+        self._dirty.clear()
+
+    def _upload(self, group):
+        """Copy the changed range of ``source``/``resident`` from the page arrays."""
+        tables = self.tables[group]
+        lo, hi = tables.stale
+        if lo >= hi:
+            return
+        lp = self._lp(group)
+        rows = np.stack([lp.host_slot[lo:hi], lp.slot[lo:hi]]).astype(np.int32)
+        staged = torch.from_numpy(rows)
+        if self.storage.cuda:
+            staged = staged.pin_memory()
+        tables.source[lo:hi].copy_(staged[0], non_blocking=True)
+        tables.resident[lo:hi].copy_(staged[1], non_blocking=True)
+        tables.stale = [0, 0]
+
+    # -- pages -------------------------------------------------------------------------------
+    def _prepare_append(self, page: Page):
+        group = page.key[:2]
+        self._writing = (group, page.index)
         if page.valid_tokens:
             if page.slot is None:
                 raise RuntimeError("active append tail lost its resident lease")
-            page.pins += 1
-            self.storage.pinned.add(page.key)
+            page.pins = page.pins + 1
             self.storage.stats["resident_hits"] += 1
             self.storage.stats["append_resident_hits"] += 1
             return PageLease(self.storage, [page])
-        slot = self._slot()
-        self.storage.wait(self.storage.compute, self.allocator.slots[slot].fence)
-        self._bind(page, slot, Location.RESIDENT)
+        block = self._slot()
+        self.storage.wait(self.storage.compute, self.allocator.fence[block])
+        self._bind(page, block, Location.RESIDENT)  # a new page: its source and resident entries
         return None
 
-    def _bind(self, page, slot, location):
-        self.storage.bind(page, slot, location)
-        self.tables[page.key[:2]].resident[page.key[2]].fill_(slot)
+    def _bind(self, page, block, location):
+        self.storage.bind(page, block, location)
+        self._stale(page.key[:2], page.index)
 
     def _detach(self, page):
-        self.tables[page.key[:2]].resident[page.key[2]].fill_(-1)
         self.storage.detach(page)
+        self._stale(page.key[:2], page.index)
 
     def _tail_of(self, group):
-        if self._writing_key is not None and self._writing_key[:2] == group:
-            return self._writing_key[2]
-        length = self.storage.requests[group[0]].lengths[group[1]]
-        return (length - 1) // self.config.page_size
+        """Index of the page the next token of ``group`` writes (the page being
+        appended while a write is open)."""
+        if self._writing is not None and self._writing[0] == group:
+            return self._writing[1]
+        return (self.storage.requests[group[0]].lengths[group[1]] - 1) // self.config.page_size
 
-    def _historical_pages(self, group=None):
-        """Sealed, unleased resident pages outside the two active tails, in bind order."""
-        keys = self.allocator.lru if group is None else self.allocator.group_pages(group)
-        tails = {}
-        candidates = []
-        for key in keys:
-            if key[2] < 0:  # a hot block lease, not a logical page
+    def _history(self, group=None):
+        """(group, index) of every sealed, unpinned resident page at least two pages
+        behind its layer's tail, in the order their blocks were bound."""
+        table = self.allocator
+        gid = None if group is None else self._lp(group).gid
+        blocks = table.bound_pages(gid)
+        found = []
+        groups = table.owner_group[blocks]
+        for g in np.unique(groups).tolist():
+            key = table.group_key(g)
+            if key[0] not in self.storage.requests:
                 continue
-            page = self.storage.pages[key]
-            g = key[:2]
-            if g not in tails:
-                tails[g] = self._tail_of(g)
-            if page.sealed and not page.pins and key[2] <= tails[g] - ACTIVE_TAIL_PAGES:
-                candidates.append(page)
-        return candidates
+            lp = self._lp(key)
+            mine = blocks[groups == g]
+            idx = table.owner_index[mine]
+            ok = lp.sealed[idx] & (lp.pins[idx] == 0) & (idx <= self._tail_of(key) - ACTIVE_TAIL_PAGES)
+            found.append(np.stack([table.bind_stamp[mine[ok]], np.full(ok.sum(), g), idx[ok]], 1))
+        if not found:
+            return []
+        rows = np.concatenate(found)
+        rows = rows[np.argsort(rows[:, 0], kind="stable")]
+        return [(table.group_key(int(g)), int(i)) for _, g, i in rows.tolist()]
+
+    def _clean(self, group, index):
+        lp = self._lp(group)
+        return lp.committed[index] == lp.version[index]
 
     def _publish_clean(self):
-        for key in list(self.pending_clean):
-            page = self.storage.pages.get(key)
-            if page is None:
-                self.pending_clean.discard(key)
-            elif page.host_ready is None or page.host_ready.query():
-                page.host_committed_version = page.host_enqueued_version
-                self.pending_clean.discard(key)
-                self.storage.stats["host_mirror_completions"] += 1
+        """Mark pages whose host mirror has completed as clean (never waits)."""
+        for request in self.storage.requests.values():
+            for lp in request.pages:
+                for i in np.flatnonzero(lp.unpublished).tolist():
+                    event = lp.host_ready[i]
+                    if event is None or event.query():
+                        lp.committed[i] = lp.enqueued[i]
+                        lp.unpublished[i] = False
+                        self.storage.stats["host_mirror_completions"] += 1
 
     def _unpin_clean_pages(self, group):
+        """A layer with a hot region offers its clean history as reclaimable blocks,
+        nearest the tail first (the upstream release order)."""
         if not self.tables[group].blocks:
             return
-        # tail-first, like the reference; empty blocks still take precedence
-        for page in sorted(self._historical_pages(group), key=lambda p: -p.key[2]):
-            if page.host_committed_version == page.content_version and page.slot not in self.allocator.reclaimable:
-                self.allocator.unpin(page.slot, self._on_block_reused)
+        lp = self._lp(group)
+        for key, index in sorted(self._history(group), key=lambda e: -e[1]):
+            block = int(lp.slot[index])
+            if self._clean(group, index) and self.allocator.reclaim_stamp[block] < 0:
+                self.allocator.unpin(block, self._on_block_reused)
                 self.storage.stats["clean_page_unpins"] += 1
 
     def _require_hot(self, group, reason):
@@ -300,48 +378,39 @@ class HybridKVCache:
             tables.hot_required, tables.trigger = True, reason
             self.storage.stats[f"hot_trigger_{reason}"] += 1
 
-    def _groups(self, request_id, layer):
-        live = self.storage.requests
-        if request_id is not None and layer is not None:
-            group = (request_id, layer)
-            return [group] if group in self.tables and request_id in live else []
-        return [
-            g
-            for g in self.tables
-            if g[0] in live and (request_id is None or g[0] == request_id) and (layer is None or g[1] == layer)
-        ]
-
+    # -- policy ticks ----------------------------------------------------------------------------
     def update_residency(self, request_id=None, layer=None, *, upcoming_allocation=False):
-        """Publish finished mirrors and raise / serve persistent hot demand; never blocks.
+        """Publish completed mirrors and raise / serve hot-region demand, without waiting.
 
-        A per-layer resident window stands in for a scheduler-derived window;
-        before an append allocation the watermark uses projected free capacity.
-        """
+        A per-layer resident window stands in for vLLM's scheduler-derived in-flight
+        token window; before an append allocation the projected free capacity is used,
+        so demand is raised before the last free block goes."""
         self.storage.check_stream()
         self._publish_clean()
-        groups = self._groups(request_id, layer)
+        groups = [g for g in self.tables if g[0] in self.storage.requests
+                  and request_id in (None, g[0]) and layer in (None, g[1])]
         for group in groups:
             self._unpin_clean_pages(group)
         for group in groups:
             tables = self.tables[group]
-            residents = len(self.allocator.group_pages(group))
+            lp = self._lp(group)
+            residents = len(lp.resident())
             if not residents:
                 continue
             if not tables.hot_required:
-                free = self._available_count() - int(upcoming_allocation)
-                if free < self.transition_watermark:
+                if self._available_count() - int(upcoming_allocation) < self.transition_watermark:
                     self._require_hot(group, "watermark")
                 elif residents >= self.hot_config.resident_window_pages:
                     self._require_hot(group, "window")
             if tables.hot_required and not tables.blocks and not tables.busy:
-                try:
+                # a failed attempt keeps residents and demand; the next tick retries
+                with suppress(CapacityError):
                     self.transition_to_host(*group)
-                except CapacityError:
-                    pass  # retried at the next policy tick; mappings and demand are kept
             self._unpin_clean_pages(group)
+        self._sync_tables()
 
     def transition_to_host(self, request_id, layer):
-        """Lease the whole hot region atomically, then make history reclaimable."""
+        """Take the layer's whole hot region at once, then make its history reclaimable."""
         self.storage.check_stream()
         group = request_id, layer
         tables = self.tables[group]
@@ -351,72 +420,74 @@ class HybridKVCache:
         if tables.busy:
             raise CapacityError("cannot transition an active row lease")
         self._publish_clean()
-        free = self._available_blocks()
-        in_free = set(free)
-        victims = [
-            p
-            for p in self._historical_pages(group)
-            if p.host_committed_version == p.content_version and p.slot not in in_free
-        ]
-        needed = max(0, self.hot_blocks - len(free))
-        if len(victims) < needed:
+        supply = self._available_blocks()
+        lp = self._lp(group)
+        offered = set(supply)
+        victims = [i for _, i in self._history(group) if self._clean(group, i) and int(lp.slot[i]) not in offered]
+        short = max(0, self.hot_blocks - len(supply))
+        if len(victims) < short:
             raise CapacityError("cannot acquire complete hot region while blocks are leased")
-        # every check precedes every mutation; fences keep copies and readers of a
-        # just-detached block ordered before its reuse as a hot block
-        for page in victims[:needed]:
-            free.append(page.slot)
-            self.allocator.unpin(page.slot, self._on_block_reused)
+        # every check precedes every change; fences order copies and last readers even
+        # when a just-released history block becomes a hot block right away
+        for index in victims[:short]:
+            block = int(lp.slot[index])
+            supply.append(block)
+            self.allocator.unpin(block, self._on_block_reused)
             self.storage.stats["clean_page_unpins"] += 1
-        blocks = free[: self.hot_blocks]
+        blocks = supply[: self.hot_blocks]
         for i, block in enumerate(blocks):
             self._take_block(block)
-            self.storage.wait(self.storage.transfer, self.allocator.slots[block].fence)
+            self.storage.wait(self.storage.transfer, self.allocator.fence[block])
             self.allocator.bind(block, (request_id, layer, -i - 1))
         tables.blocks = blocks
         staged = torch.tensor(blocks, dtype=torch.int32)
-        if self.storage.cuda:  # pinned staging: no host synchronisation on the decode path
-            staged = staged.pin_memory()
-        tables.hot.copy_(staged, non_blocking=self.storage.cuda)
+        tables.hot.copy_(staged.pin_memory() if self.storage.cuda else staged, non_blocking=True)
         tables.ready = self.storage.event(self.storage.transfer)
         self.storage.stats["hot_region_allocations"] += 1
         self._unpin_clean_pages(group)
+        self._sync_tables()
 
     def _slot(self):
+        """A block for a new resident page: an allocatable one, else one freed by moving
+        the layer with the most history to its hot region, else wait for a mirror."""
         while True:
             self.update_residency(upcoming_allocation=True)
-            first = self._first_available()
-            if first is not None:
-                return self._take_block(first)
-            candidates = self._historical_pages()
-            counts = Counter(p.key[:2] for p in candidates)
-            for group, count in counts.most_common():
+            block = self._first_available()
+            if block is not None:
+                return self._take_block(block)
+            history = self._history()
+            per_group = Counter(group for group, _ in history)
+            for group, count in per_group.most_common():
                 if count >= self.hot_blocks + 1 and not self.tables[group].blocks:
                     self._require_hot(group, "pressure")
                     try:
                         self.transition_to_host(*group)
                     except CapacityError:
                         continue
-                    first = self._first_available()
-                    if first is not None:
-                        return self._take_block(first)
-            pending = [
-                p for p in candidates if p.host_committed_version < p.content_version and p.host_ready is not None
-            ]
-            if not pending:
+                    block = self._first_available()
+                    if block is not None:
+                        return self._take_block(block)
+            waiting = [(g, i) for g, i in history
+                       if not self._clean(g, i) and self._lp(g).host_ready[i] is not None]
+            if not waiting:
                 raise CapacityError("no reclaimable resident block; tails/readers are protected")
             # a synchronous runner cannot suspend mid-prefill: wait for one useful
             # mirror event, never for the whole device
-            pending[0].host_ready.synchronize()
+            group, index = waiting[0]
+            self._lp(group).host_ready[index].synchronize()
             self.storage.stats["pressure_mirror_waits"] += 1
 
     def reclaim_history(self, request_id, layer, *, evict=False):
-        """Make completed history allocatable while still readable (evict: take it now)."""
+        """Make completed history allocatable while still readable (``evict``: take it now)."""
+        group = request_id, layer
         self.transition_to_host(request_id, layer)
-        self._unpin_clean_pages((request_id, layer))
+        self._unpin_clean_pages(group)
         if evict:
-            for page in self._historical_pages((request_id, layer)):
-                if page.slot in self.allocator.reclaimable:
-                    self._take_block(page.slot)
+            lp = self._lp(group)
+            for _, index in self._history(group):
+                if self.allocator.reclaim_stamp[lp.slot[index]] >= 0:
+                    self._take_block(int(lp.slot[index]))
+        self._sync_tables()
 
     def _after_write(self, page):
         self.pending_clean.add(page.key)
@@ -428,9 +499,10 @@ class HybridKVCache:
         try:
             self.storage.append(request_id, layer, k, v, self._prepare_append, self._after_write)
         finally:
-            self._writing_key = None
+            self._writing = None
+            self._sync_tables()
 
-    # -- decode --------------------------------------------------------------
+    # -- decode ---------------------------------------------------------------------------------
     def attention(self, query, request_id, layer, selection, backend="auto"):
         from .attention import row_attention
 
@@ -443,7 +515,7 @@ class HybridKVCache:
         if heads != query.shape[0]:
             raise ValueError("selection must have one row per query head")
         build = getattr(selection, "logical_topk", None)
-        if build is not None:
+        if build is not None:  # a device-resident selection builds its union on the device
             topk = build(query.device, max_rows=self.hot_config.max_union_rows)
         else:
             topk = LogicalTopK.from_selection(selection, query.device)
@@ -453,63 +525,59 @@ class HybridKVCache:
         storage = self.storage
         storage.check_stream()
         topk.validate(self.device, self.hot_config.max_union_rows)
-        tables = self.tables[request_id, layer]
+        group = request_id, layer
+        tables = self.tables[group]
         if tables.busy:
             raise RuntimeError("hot contents already leased by this layer")
         length = storage.requests[request_id].lengths[layer]
         if length < 1:
             raise ValueError("cannot resolve an empty history")
-        # pin this layer's residents: the selected rows are not read back to the host
-        pages = [storage.pages[key] for key in self.allocator.group_pages((request_id, layer))]
-        for page in pages:
-            page.pins += 1
-            storage.pinned.add(page.key)
+        # pin every resident page of this layer: the selected rows never come back to
+        # the host, so any of them may be read
+        lp = self._lp(group)
+        pinned = lp.resident()
+        lp.pins[pinned] += 1
         tables.busy = True
         try:
+            self._sync_tables()
             storage.wait(storage.compute, tables.ready)
-            plan = self.ops.resolve_rows(
-                topk, tables.source, tables.resident, tables.hot, tables.tags, tables.lru,
-                length, self.config.page_size, row_stats=self.row_stats,
-            )
+            plan = self.ops.resolve_rows(topk, tables.source, tables.resident, tables.hot, tables.tags, tables.lru,
+                                         length, self.config.page_size, row_stats=self.row_stats)
             resolved = storage.event(storage.compute)
             storage.wait(storage.transfer, resolved)
             storage.wait(storage.transfer, tables.last_use)
-            # append mirrors and earlier loads already precede this on the transfer stream
+            # append mirrors and earlier loads already precede this in stream order
             with storage.context(storage.transfer):
-                self.ops.gather_rows(self._host_source, self.pool, plan, self.config)
+                self.ops.gather_rows(storage.host_source, self.pool, plan, self.config)
             tables.ready = storage.event(storage.transfer)
             if storage.cuda:  # plan tensors are produced on compute, read on transfer
-                plan.miss_host_rows.record_stream(storage.transfer)
-                plan.miss_device_rows.record_stream(storage.transfer)
-                plan.counts.record_stream(storage.transfer)
-            return RowLease(self, tables, plan, pages)
+                for tensor in (plan.miss_host_rows, plan.miss_device_rows, plan.counts):
+                    tensor.record_stream(storage.transfer)
+            return RowLease(self, group, tables, plan, pinned)
         except Exception:
-            for page in pages:
-                page.pins -= 1
-                if not page.pins:
-                    storage.pinned.discard(page.key)
+            lp.pins[pinned] -= 1
             tables.busy = False
             raise
 
-    # -- release -------------------------------------------------------------
+    # -- release -----------------------------------------------------------------------------------
     def release_request(self, request_id, wait=True):
         storage = self.storage
-        groups = [t for (name, _), t in self.tables.items() if name == request_id]
-        if any(t.busy for t in groups) or any(storage.pages[key].pins for key in storage.requests[request_id].keys):
+        request = storage.requests[request_id]
+        groups = [(g, t) for g, t in self.tables.items() if g[0] == request_id]
+        if any(t.busy for _, t in groups) or any(np.any(lp.pins > 0) for lp in request.pages):
             raise RuntimeError("cannot release a request with active row leases")
-        for tables in groups:
+        for _, tables in groups:
             storage.wait(storage.transfer, tables.ready)
             storage.wait(storage.transfer, tables.last_use)
             fence = storage.event(storage.transfer)
             for block in tables.blocks:
                 self.allocator.release(block, fence)
-        for key in storage.requests[request_id].keys:
-            page = storage.pages[key]
-            if page.slot is not None:
-                self._detach(page)
-        storage.retire(request_id, keepalive=groups)
-        for key in [key for key in self.tables if key[0] == request_id]:
-            del self.tables[key]
+        for key in request.keys:
+            if request.pages[key[1]].slot[key[2]] >= 0:
+                self._detach(storage.pages[key])
+        storage.retire(request_id, keepalive=[t for _, t in groups])
+        for group, _ in groups:
+            del self.tables[group]
         self.collect(wait=wait)
 
     def collect(self, wait=False):
@@ -519,7 +587,7 @@ class HybridKVCache:
     def page_state(self, key):
         state = self.storage.page_state(key)
         page = self.storage.pages[key]
-        unpinned = page.slot in self.allocator.reclaimable
+        unpinned = page.slot is not None and self.allocator.reclaim_stamp[page.slot] >= 0
         clean = page.host_committed_version == page.content_version
         if page.slot is None:
             residency = "host_only"
@@ -535,7 +603,7 @@ class HybridKVCache:
             raise CapacityError("hybrid block budget is fixed; hot leases need readmission to resize")
 
     def close(self):
-        # the gather reads pinned memory from the GPU; drain before teardown only
+        # kernels read the pinned host pool; drain before teardown only
         self.storage.synchronize()
 
     def __del__(self):
@@ -575,34 +643,36 @@ class HybridKVCache:
         return result
 
     def assert_invariants(self):
-        storage, allocator = self.storage, self.allocator
+        storage, table = self.storage, self.allocator
         storage.assert_invariants()
         for name, request in storage.requests.items():
             assert request.extra_index_bytes == sum(t.nbytes for g, t in self.tables.items() if g[0] == name)
-        assert not (allocator.free & allocator.reclaimable.keys())
-        for slot in allocator.reclaimable:
-            page = storage.pages[self._owner(slot)]
-            assert page.slot == slot and page.sealed
-            assert page.host_committed_version == page.content_version
-            assert self.tables[page.key[:2]].blocks
-            length = storage.requests[page.key[0]].lengths[page.key[1]]
-            assert page.key[2] <= (length - 1) // self.config.page_size - ACTIVE_TAIL_PAGES
+        queued = table.reclaim_queue()
+        assert np.all(table.owner_group[queued] != NO_GROUP)
+        for block in queued.tolist():
+            group = table.group_key(int(table.owner_group[block]))
+            index = int(table.owner_index[block])
+            lp = self._lp(group)
+            assert lp.slot[index] == block and lp.sealed[index] and self._clean(group, index)
+            assert self.tables[group].blocks
+            length = storage.requests[group[0]].lengths[group[1]]
+            assert index <= (length - 1) // self.config.page_size - ACTIVE_TAIL_PAGES
         assert sum(self.admission_blocks(r.layers) for r in storage.requests.values()) <= self.budget
         for group, tables in self.tables.items():
+            self._upload(group)
             assert len(tables.blocks) in (0, self.hot_blocks)
-            assert sorted(tables.lru.tolist()) == list(range(self.hot_config.hot_rows))
-            tags = [tag for tag in tables.tags.tolist() if tag >= 0]
-            assert len(tags) == len(set(tags))
-            if not tables.blocks:
-                assert not tags
-            else:
-                assert tables.hot_required
+            lru = tables.lru.cpu().numpy()
+            assert np.array_equal(np.sort(lru), np.arange(self.hot_config.hot_rows))
+            tags = tables.tags.cpu().numpy()
+            tags = tags[tags >= 0]
+            assert len(tags) == len(np.unique(tags))
+            assert tables.hot_required if tables.blocks else not len(tags)
             for i, block in enumerate(tables.blocks):
-                assert self.owners[block] == (*group, -i - 1)
-            residents = tables.resident.tolist()
-            for index, host in enumerate(tables.source.tolist()):
-                page = storage.pages.get((*group, index))
-                assert host == (-1 if page is None else page.host_slot)
-                assert residents[index] == (-1 if page is None or page.slot is None else page.slot)
-                if page is not None and page.slot is None:
-                    assert tables.blocks
+                assert table.owner_key(block) == (*group, -i - 1)
+            lp = self._lp(group)
+            m = lp.materialized
+            source, resident = tables.source.cpu().numpy(), tables.resident.cpu().numpy()
+            assert np.array_equal(source[:m], lp.host_slot[:m]) and np.all(source[m:] == -1)
+            assert np.array_equal(resident[:m], lp.slot[:m]) and np.all(resident[m:] == -1)
+            if np.any(lp.slot[:m] < 0):
+                assert tables.blocks

@@ -1,12 +1,20 @@
 """A Qwen2-shaped decoder that drives the sparse decode path.
 
-Same architecture and parameter layout as the reference's ``MiniModel``
-(model.py:19-226): RMSNorm, q/k/v projections with bias, rotary embedding,
-SiLU MLP; parameters are created in Hugging Face Qwen2 order and naming, so a
-seeded random init reproduces the reference's weights and Qwen2 checkpoints
-load into it.  Prefill uses PyTorch-ROCm's SDPA (not on the timed path);
-decode appends K/V to the cache, selects pages (Quest by default, through the
-cache's kernel backend) and attends over the resolved physical rows.
+The reference's ``MiniModel`` (``mini_hisparse/model.py:19-226``) is kept as an
+interface: ``ModelConfig`` fields, Hugging Face Qwen2 parameter names and the
+order parameters are created in (a seeded random init reproduces the reference's
+weights; Qwen2/Qwen2.5 checkpoints load unchanged), ``prefill`` / ``decode`` /
+``from_pretrained`` signatures and errors.
+
+Organisation (this module's own): a layer's parameters are declared as linear
+specs; one routine, :meth:`MiniModel._layers`, runs the decoder stack for any
+number of tokens at given positions and hands each layer's rotated q/k/v to an
+attention callback -- causal SDPA for a prefill (PyTorch-ROCm's, not on the
+timed path), for a decode the cache append, page selection (Quest through the
+cache's kernel backend by default) and sparse row attention.  The arithmetic of
+each step (RMSNorm in float32, rotary tables rounded to the model dtype, SiLU
+MLP) is Qwen2's, op for op, so logits match the reference bit for bit on the
+same device.
 """
 
 from __future__ import annotations
@@ -45,6 +53,8 @@ class ModelConfig:
 
 
 class RMSNorm(nn.Module):
+    """Root-mean-square norm computed in float32, scaled in the input dtype."""
+
     def __init__(self, width, eps):
         super().__init__()
         self.weight = nn.Parameter(torch.ones(width))
@@ -52,83 +62,82 @@ class RMSNorm(nn.Module):
 
     def forward(self, x):
         wide = x.float()
-        scaled = wide * torch.rsqrt(wide.square().mean(-1, keepdim=True) + self.eps)
-        return scaled.to(x.dtype) * self.weight
+        return (wide * torch.rsqrt(wide.square().mean(-1, keepdim=True) + self.eps)).to(x.dtype) * self.weight
 
 
-class Projections(nn.Module):
-    def __init__(self, cfg):
-        super().__init__()
-        kv_width = cfg.num_key_value_heads * cfg.head_dim
-        self.q_proj = nn.Linear(cfg.hidden_size, cfg.hidden_size, bias=True)
-        self.k_proj = nn.Linear(cfg.hidden_size, kv_width, bias=True)
-        self.v_proj = nn.Linear(cfg.hidden_size, kv_width, bias=True)
-        self.o_proj = nn.Linear(cfg.hidden_size, cfg.hidden_size, bias=False)
+def _linears(**specs):
+    """A module holding ``nn.Linear`` children created in the keyword order given:
+    ``name=(in_features, out_features, bias)``."""
+    module = nn.Module()
+    for name, (width_in, width_out, bias) in specs.items():
+        setattr(module, name, nn.Linear(width_in, width_out, bias=bias))
+    return module
 
 
-class MLP(nn.Module):
-    def __init__(self, cfg):
-        super().__init__()
-        self.gate_proj = nn.Linear(cfg.hidden_size, cfg.intermediate_size, bias=False)
-        self.up_proj = nn.Linear(cfg.hidden_size, cfg.intermediate_size, bias=False)
-        self.down_proj = nn.Linear(cfg.intermediate_size, cfg.hidden_size, bias=False)
-
-    def forward(self, x):
-        return self.down_proj(F.silu(self.gate_proj(x)) * self.up_proj(x))
-
-
-class Block(nn.Module):
-    def __init__(self, cfg):
-        super().__init__()
-        self.input_layernorm = RMSNorm(cfg.hidden_size, cfg.rms_norm_eps)
-        self.post_attention_layernorm = RMSNorm(cfg.hidden_size, cfg.rms_norm_eps)
-        self.self_attn = Projections(cfg)
-        self.mlp = MLP(cfg)
+def _layer(cfg: ModelConfig):
+    """One decoder layer in Qwen2 naming; creation order: the two norms, then q, k, v,
+    o, then gate, up, down (the order the random init draws in)."""
+    hidden, kv = cfg.hidden_size, cfg.num_key_value_heads * cfg.head_dim
+    layer = nn.Module()
+    layer.input_layernorm = RMSNorm(hidden, cfg.rms_norm_eps)
+    layer.post_attention_layernorm = RMSNorm(hidden, cfg.rms_norm_eps)
+    layer.self_attn = _linears(q_proj=(hidden, hidden, True), k_proj=(hidden, kv, True), v_proj=(hidden, kv, True),
+                               o_proj=(hidden, hidden, False))
+    ffn = cfg.intermediate_size
+    layer.mlp = _linears(gate_proj=(hidden, ffn, False), up_proj=(hidden, ffn, False), down_proj=(ffn, hidden, False))
+    return layer
 
 
-class Decoder(nn.Module):
-    def __init__(self, cfg):
-        super().__init__()
-        self.embed_tokens = nn.Embedding(cfg.vocab_size, cfg.hidden_size)
-        self.layers = nn.ModuleList(Block(cfg) for _ in range(cfg.num_hidden_layers))
-        self.norm = RMSNorm(cfg.hidden_size, cfg.rms_norm_eps)
+def rope_tables(start, count, dim, theta, dtype, device):
+    """Rotary cos/sin ``[count, 1, dim]`` for positions ``start .. start+count-1``:
+    angles in float32, the tables rounded to ``dtype`` (Qwen2's order of operations)."""
+    inverse = theta ** (-torch.arange(0, dim, 2, device=device).float() / dim)
+    angles = torch.arange(start, start + count, device=device).float()[:, None] * inverse[None, :]
+    angles = torch.cat((angles, angles), -1)[:, None, :]
+    return angles.cos().to(dtype), angles.sin().to(dtype)
+
+
+def apply_rope(tensor, cos, sin):
+    """``[tokens, heads, dim]`` rotated by half-dimension pairs."""
+    first, second = tensor.chunk(2, -1)
+    return tensor * cos + torch.cat((-second, first), -1) * sin
 
 
 def rotary(tensor, start, theta):
-    """Rotary embedding of [tokens, heads, head_dim] at positions start, start+1, ..."""
-    length, dim = tensor.shape[0], tensor.shape[-1]
-    inv = theta ** (-torch.arange(0, dim, 2, device=tensor.device).float() / dim)
-    positions = torch.arange(start, start + length, device=tensor.device).float()
-    angles = positions[:, None] * inv[None, :]
-    angles = torch.cat((angles, angles), -1)[:, None, :]
-    cosine, sine = angles.cos().to(tensor.dtype), angles.sin().to(tensor.dtype)
-    first, second = tensor.chunk(2, -1)
-    return tensor * cosine + torch.cat((-second, first), -1) * sine
+    """Rotary embedding of ``[tokens, heads, head_dim]`` at positions start, start+1, ..."""
+    cos, sin = rope_tables(start, tensor.shape[0], tensor.shape[-1], theta, tensor.dtype, tensor.device)
+    return apply_rope(tensor, cos, sin)
 
 
 class MiniModel(nn.Module):
     def __init__(self, config: ModelConfig | None = None):
         super().__init__()
-        self.config = config or ModelConfig()
-        self.model = Decoder(self.config)
-        self.lm_head = nn.Linear(self.config.hidden_size, self.config.vocab_size, bias=False)
+        self.config = cfg = config or ModelConfig()
+        self.model = nn.Module()
+        self.model.embed_tokens = nn.Embedding(cfg.vocab_size, cfg.hidden_size)
+        self.model.layers = nn.ModuleList(_layer(cfg) for _ in range(cfg.num_hidden_layers))
+        self.model.norm = RMSNorm(cfg.hidden_size, cfg.rms_norm_eps)
+        self.lm_head = nn.Linear(cfg.hidden_size, cfg.vocab_size, bias=False)
 
     @classmethod
     def from_pretrained(cls, name: str, device="cuda", dtype=torch.bfloat16):
-        """Load a local Qwen2/Qwen2.5 checkpoint (standard RoPE, no sliding window)."""
+        """Adopt the modules of a Qwen2/Qwen2.5 checkpoint (standard RoPE, SiLU, no
+        sliding window), given as a local directory or a hub name."""
         from transformers import AutoConfig, AutoModelForCausalLM
 
-        hf_cfg = AutoConfig.from_pretrained(name)
-        rope = getattr(hf_cfg, "rope_parameters", None) or getattr(hf_cfg, "rope_scaling", None) or {}
-        if hf_cfg.model_type != "qwen2" or rope.get("rope_type", rope.get("type", "default")) != "default":
+        hf_config = AutoConfig.from_pretrained(name)
+        # transformers 4 keeps rope_theta on the config; 5 moves it into rope_parameters
+        rope = getattr(hf_config, "rope_parameters", None) or getattr(hf_config, "rope_scaling", None) or {}
+        kind = rope.get("rope_type", rope.get("type", "default"))
+        if hf_config.model_type != "qwen2" or kind != "default":
             raise ValueError("only Qwen2/Qwen2.5 with standard RoPE are supported")
-        if getattr(hf_cfg, "use_sliding_window", False) or hf_cfg.hidden_act != "silu":
+        if getattr(hf_config, "use_sliding_window", False) or hf_config.hidden_act != "silu":
             raise ValueError("sliding window / non-SiLU models are unsupported")
+        values = {f.name: getattr(hf_config, f.name) for f in fields(ModelConfig) if f.name != "rope_theta"}
+        values["rope_theta"] = rope.get("rope_theta", getattr(hf_config, "rope_theta", 10000.0))
         hf = AutoModelForCausalLM.from_pretrained(name, torch_dtype=dtype).eval().to(device)
         model = cls.__new__(cls)
         nn.Module.__init__(model)
-        values = {f.name: getattr(hf_cfg, f.name) for f in fields(ModelConfig) if f.name != "rope_theta"}
-        values["rope_theta"] = rope.get("rope_theta", getattr(hf_cfg, "rope_theta", 10000.0))
         model.config = ModelConfig(**values)
         model.model, model.lm_head = hf.model, hf.lm_head
         return model.eval()
@@ -141,20 +150,32 @@ class MiniModel(nn.Module):
     def dtype(self):
         return self.model.embed_tokens.weight.dtype
 
-    def _project(self, layer, x, start):
-        cfg, length = self.config, len(x)
-        x = layer.input_layernorm(x)
-        attn = layer.self_attn
-        q = attn.q_proj(x).view(length, cfg.num_attention_heads, cfg.head_dim)
-        k = attn.k_proj(x).view(length, cfg.num_key_value_heads, cfg.head_dim)
-        v = attn.v_proj(x).view(length, cfg.num_key_value_heads, cfg.head_dim)
-        return rotary(q, start, cfg.rope_theta), rotary(k, start, cfg.rope_theta), v
+    # -- the decoder stack -----------------------------------------------------------
+    def _layers(self, tokens, start, attend):
+        """Run every layer over ``tokens`` (1-D device ids) at positions ``start...``;
+        ``attend(index, q, k, v)`` returns the layer's attention output ``[tokens,
+        heads, head_dim]`` from its rotated q ``[tokens, heads, D]``, k and v
+        ``[tokens, kv_heads, D]``.  Returns the final hidden states."""
+        cfg = self.config
+        x = self.model.embed_tokens(tokens)
+        cos, sin = rope_tables(start, len(tokens), cfg.head_dim, cfg.rope_theta, x.dtype, x.device)
+        for index, layer in enumerate(self.model.layers):
+            h = layer.input_layernorm(x)
+            proj = layer.self_attn
+            q = proj.q_proj(h).view(len(tokens), cfg.num_attention_heads, cfg.head_dim)
+            k = proj.k_proj(h).view(len(tokens), cfg.num_key_value_heads, cfg.head_dim)
+            v = proj.v_proj(h).view(len(tokens), cfg.num_key_value_heads, cfg.head_dim)
+            attention = attend(index, apply_rope(q, cos, sin), apply_rope(k, cos, sin), v)
+            x = x + proj.o_proj(attention.reshape(len(tokens), -1))
+            mlp = layer.mlp
+            h = layer.post_attention_layernorm(x)
+            x = x + mlp.down_proj(F.silu(mlp.gate_proj(h)) * mlp.up_proj(h))
+        return x
 
-    @staticmethod
-    def _finish(layer, residual, attention):
-        x = residual + layer.self_attn.o_proj(attention.reshape(len(residual), -1))
-        return x + layer.mlp(layer.post_attention_layernorm(x))
+    def _logits(self, hidden):
+        return self.lm_head(self.model.norm(hidden)).float()
 
+    # -- entry points ---------------------------------------------------------------------
     @torch.inference_mode()
     def prefill(self, tokens: list[int], cache=None, request_id=None, observer=None):
         if not tokens:
@@ -162,28 +183,25 @@ class MiniModel(nn.Module):
         if cache is not None and any(cache.storage.requests[request_id].lengths):
             raise ValueError("prefill is allowed exactly once per request")
         groups = self.config.num_attention_heads // self.config.num_key_value_heads
-        x = self.model.embed_tokens(torch.tensor(tokens, device=self.device))
-        for index, layer in enumerate(self.model.layers):
-            q, k, v = self._project(layer, x, 0)
+
+        def causal(index, q, k, v):
             if cache is not None:
                 cache.write(request_id, index, k, v)
             if observer is not None:
                 observer.prefill(request_id, index, k, v)
-            attention = F.scaled_dot_product_attention(
-                q.transpose(0, 1),
-                k.repeat_interleave(groups, 1).transpose(0, 1),
-                v.repeat_interleave(groups, 1).transpose(0, 1),
-                is_causal=True,
-            ).transpose(0, 1)
-            x = self._finish(layer, x, attention)
-        return self.lm_head(self.model.norm(x[-1])).float()
+            heads_first = lambda t: t.repeat_interleave(groups, 1).transpose(0, 1)  # noqa: E731
+            out = F.scaled_dot_product_attention(q.transpose(0, 1), heads_first(k), heads_first(v), is_causal=True)
+            return out.transpose(0, 1)
+
+        hidden = self._layers(torch.tensor(tokens, device=self.device), 0, causal)
+        return self._logits(hidden[-1])
 
     def _select(self, cache, request_id, layer, query, top_k, selector):
         request = cache.storage.requests[request_id]
         length = request.lengths[layer]
         if selector == "quest" and top_k is not None:
-            quest = cache.ops.quest_selection
-            return quest(query, request.minimum[layer], request.maximum[layer], length, cache.config.page_size, top_k)
+            return cache.ops.quest_selection(query, request.minimum[layer], request.maximum[layer], length,
+                                             cache.config.page_size, top_k)
         if selector in ("quest", "mean"):
             pages = select_pages(cache, request_id, layer, query, top_k)
             return Selection.from_pages(pages, length, cache.config.page_size, query.shape[0])
@@ -194,14 +212,13 @@ class MiniModel(nn.Module):
         lengths = cache.storage.requests[request_id].lengths
         if len(set(lengths)) != 1 or lengths[0] == 0:
             raise ValueError("all layers must have the same nonempty history")
-        position = lengths[0]
-        x = self.model.embed_tokens(torch.tensor([token], device=self.device))
-        for index, layer in enumerate(self.model.layers):
-            q, k, v = self._project(layer, x, position)
+
+        def sparse(index, q, k, v):
             cache.write(request_id, index, k, v)
             if observer is not None:
                 observer.decode(request_id, index, q[0], k, v)
             selection = self._select(cache, request_id, index, q[0], top_k, selector)
-            attention = cache.attention(q[0], request_id, index, selection, backend)
-            x = self._finish(layer, x, attention.unsqueeze(0))
-        return self.lm_head(self.model.norm(x[0])).float()
+            return cache.attention(q[0], request_id, index, selection, backend).unsqueeze(0)
+
+        hidden = self._layers(torch.tensor([token], device=self.device), lengths[0], sparse)
+        return self._logits(hidden[0])

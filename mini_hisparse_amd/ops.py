@@ -12,7 +12,7 @@ import torch
 
 from . import _lib
 from .row_index import resolve_rows
-from .row_kernels import MappedHost, attend_groups, attend_rows, attend_window, gather_rows
+from .row_kernels import MappedHost, append_tokens, attend_groups, attend_rows, attend_window, gather_rows
 from .selection import quest_selection
 
 
@@ -27,6 +27,12 @@ class HipOps:
     def host_source(self, host):
         """Device alias of the pinned host pool (MappedHost, row_kernels.py:10-32)."""
         return MappedHost(host)
+
+    def append_tokens(self, k, v, first_page, first_within, slots, host_slots, pool, host_source, host,
+                      minimum, maximum, summaries, config):
+        """Rows, host mirror, bounds and summaries of one write (storage.py:273-318)."""
+        append_tokens(k, v, first_page, first_within, slots, host_slots, pool, host_source, minimum, maximum,
+                      summaries, config)
 
     def resolve_rows(self, topk, source, resident, hot, tags, lru, length, page_size, row_stats=None):
         return resolve_rows(topk, source, resident, hot, tags, lru, length, page_size, row_stats=row_stats)

@@ -117,6 +117,30 @@ def append_rows(k, v, pool, device_rows, minimums, maximums, config, *, host=Non
     _lib.check(status, "hs_append_rows")
 
 
+def append_tokens(k, v, first_page, first_within, slots, host_slots, pool, host, minimum, maximum, summaries,
+                  config):
+    """A write of ``len(k)`` tokens to one (request, layer) with its page placement
+    decided (``hs_append_tokens``; the page loop of storage.py:273-318): rows to the
+    resident pages' blocks and to the host mirror, bounds and summaries of every page.
+
+    ``slots`` / ``host_slots``: per page of the write, its device block (``-1``: not
+    resident) and host slot; ``host`` a :class:`MappedHost` of the pinned host pool;
+    ``minimum`` / ``maximum`` / ``summaries`` the layer's ``[pages, Hkv, D]`` tensors."""
+    pages = len(slots)
+    if k.shape != v.shape or k.dim() != 3 or k.dtype != pool.dtype or k.stride() != v.stride() or \
+            k.stride(2) != 1 or k.stride(1) != config.head_dim:
+        raise ValueError("append needs [tokens, Hkv, D] K/V rows in the pool dtype")
+    i64 = ctypes.c_int64 * pages
+    status = _lib.load().hs_append_tokens(
+        k.data_ptr(), v.data_ptr(), k.stride(0), k.shape[0], pool.data_ptr(), pool.shape[0] * config.page_size,
+        host.data_ptr(), host.tensor.shape[0] * config.page_size, _lib.dtype_code(pool.dtype), config.page_size,
+        config.kv_heads, config.head_dim, first_page, first_within, pages, i64(*slots), i64(*host_slots),
+        minimum.data_ptr(), maximum.data_ptr(), _lib.ptr(summaries), minimum.shape[0],
+        _lib.stream_handle(pool.device),
+    )
+    _lib.check(status, "hs_append_tokens")
+
+
 # Attention workspaces, one per (device, stream), grown on demand.  Launches on
 # one stream run in order, so the calls of a stream can share its workspace.
 _ATTEND_WS = {}

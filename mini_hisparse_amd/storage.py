@@ -1,29 +1,45 @@
-"""Host-backed logical pages: append with mirrors, Quest bounds, event-safe retirement.
+"""Host-backed KV history: the pinned host pool, per-(request, layer) page arrays,
+batched writes and event-safe retirement.
 
-Same contract as the reference's ``HostStore`` (storage.py:101-441): every
-request's full KV history lives in one pinned host pool ``[host_pages, 2, P,
-Hkv, D]``; the device slab holds resident copies.  ``append`` writes new K/V
-into the resident tail page on the compute stream, updates the page's Quest
-bounds (exact K minimum / maximum in the KV dtype) and mean-K summary, and
-mirrors only the new rows to host memory on the transfer stream.  Host slots
-of a retired request are reused only after its retirement event completes.
+Replaces the reference's ``HostStore`` (``mini_hisparse/storage.py:101-441``)
+with the same contract -- every request's full history lives in one pinned host
+pool ``[host_pages, 2, P, Hkv, D]``; the device slab holds resident copies; a
+write appends K/V to the tail, updates the Quest bounds (exact K extrema in the
+KV dtype) and the page-mean summaries, and mirrors the new rows to host memory;
+host slots of a retired request return to the free list only after its
+retirement event -- organised differently:
 
-Storage knows no eviction policy: callers supply the resident placement
-(``prepare_page``) and update their own policy after the mirror
-(``after_write``).  Pages are additionally indexed per (request, layer).
+* page state is kept per (request, layer) in :class:`LayerPages`, a set of
+  arrays over that layer's logical pages (host slot, device block, valid rows,
+  pins, content / mirror versions, sealed flag, events), not one object per page;
+  :class:`Page` is a view onto one entry, for callers that inspect a page;
+* a write first makes every placement decision page by page (the caller's
+  ``prepare_page`` / ``after_write`` hooks run in page order, as the policy
+  requires), then moves the data of all its pages -- pool rows, host mirror,
+  bounds, summaries -- in one batched kernel launch (``ops.append_tokens``).
+  The host mirror is written straight from the new K/V, so a page that the
+  policy detaches again later in the same write keeps its bytes.  When the
+  policy has to wait for a page of the write that is not launched yet (a
+  detach, a mirror-completion wait), the pages placed so far are launched
+  first (``_flush``), so every wait ends.
+
+Storage knows no eviction policy: callers supply the placement of a new page
+(``prepare_page``) and update their policy after it (``after_write``).
 """
 
 from __future__ import annotations
 
 from collections import Counter
+from collections.abc import Mapping
 from contextlib import nullcontext
 from dataclasses import dataclass, field
 from enum import Enum
 from math import ceil
 
+import numpy as np
 import torch
 
-from .allocator import DeviceAllocator
+from .allocator import NO_GROUP, DeviceAllocator
 from .config import CacheConfig, CapacityError
 
 PageKey = tuple[str, int, int]
@@ -35,27 +51,87 @@ class Location(str, Enum):
     HOT = "hot"
 
 
-@dataclass
+_LOCATIONS = (Location.HOST, Location.RESIDENT, Location.HOT)
+_CODE = {loc: i for i, loc in enumerate(_LOCATIONS)}
+NEVER = -1_000_000_000
+
+
+class LayerPages:
+    """Page state of one (request, layer) as arrays over its logical pages.
+
+    Pages are materialized in index order (appends are sequential), so the
+    materialized pages are the prefix ``[0, materialized)``.
+    """
+
+    def __init__(self, gid, pages, generation):
+        self.gid = gid
+        self.generation = generation
+        self.materialized = 0
+        self.host_slot = np.full(pages, -1, np.int64)
+        self.slot = np.full(pages, -1, np.int64)
+        self.location = np.zeros(pages, np.int8)
+        self.valid = np.zeros(pages, np.int64)
+        self.pins = np.zeros(pages, np.int64)
+        self.version = np.zeros(pages, np.int64)
+        self.enqueued = np.zeros(pages, np.int64)
+        self.committed = np.zeros(pages, np.int64)
+        self.sealed = np.zeros(pages, bool)
+        self.stamp = np.zeros(pages, np.int64)  # materialization order across the store
+        self.attended = np.full(pages, NEVER, np.int64)  # last attention epoch (page layout)
+        self.touched = np.zeros(pages, np.int64)  # last touch of the page layout's clock
+        self.unpublished = np.zeros(pages, bool)  # written since the last mirror publication
+        self.ready = [None] * pages  # device contents written
+        self.last_use = [None] * pages  # last reader done
+        self.host_ready = [None] * pages  # host mirror written
+
+    def resident(self):
+        """Indices of the materialized pages that hold a device block."""
+        return np.flatnonzero(self.slot[: self.materialized] >= 0)
+
+
 class Page:
-    key: PageKey
-    host_slot: int
-    slot: int | None = None
-    location: Location = Location.HOST
-    valid_tokens: int = 0
-    pins: int = 0
-    ready: object = None
-    last_use: object = None
-    host_ready: object = None
-    request_generation: int = 0
-    content_version: int = 0
-    host_enqueued_version: int = 0
-    host_committed_version: int = 0
-    sealed: bool = False
-    last_attention_epoch: int = -1000000000
+    """View of one logical page of a :class:`LayerPages` (the reference's ``Page``)."""
+
+    __slots__ = ("_lp", "index", "key")
+
+    def __init__(self, lp: LayerPages, key: PageKey):
+        self._lp, self.index, self.key = lp, key[2], key
+
+    def _get(self, name):
+        return getattr(self._lp, name)[self.index]
+
+    def _set(self, name, value):
+        getattr(self._lp, name)[self.index] = value
+
+    host_slot = property(lambda s: int(s._get("host_slot")))
+    slot = property(lambda s: None if s._get("slot") < 0 else int(s._get("slot")))
+    location = property(lambda s: _LOCATIONS[s._get("location")])
+    valid_tokens = property(lambda s: int(s._get("valid")))
+    sealed = property(lambda s: bool(s._get("sealed")))
+    request_generation = property(lambda s: s._lp.generation)
+    content_version = property(lambda s: int(s._get("version")))
+    host_enqueued_version = property(lambda s: int(s._get("enqueued")))
+    pins = property(lambda s: int(s._get("pins")), lambda s, v: s._set("pins", v))
+    host_committed_version = property(lambda s: int(s._get("committed")), lambda s, v: s._set("committed", v))
+    ready = property(lambda s: s._get("ready"), lambda s, v: s._set("ready", v))
+    last_use = property(lambda s: s._get("last_use"), lambda s, v: s._set("last_use", v))
+    host_ready = property(lambda s: s._get("host_ready"), lambda s, v: s._set("host_ready", v))
+    last_attention_epoch = property(lambda s: int(s._get("attended")), lambda s, v: s._set("attended", v))
+
+    def __eq__(self, other):
+        return isinstance(other, Page) and other._lp is self._lp and other.index == self.index
+
+    def __hash__(self):
+        return hash((id(self._lp), self.index))
+
+    def __repr__(self):
+        return f"Page({self.key}, host_slot={self.host_slot}, slot={self.slot}, valid={self.valid_tokens})"
 
 
 @dataclass
 class RequestPages:
+    """One admitted request: lengths, Quest bounds / summaries and its layers' pages."""
+
     max_tokens: int
     layers: int
     page_count: int
@@ -65,9 +141,49 @@ class RequestPages:
     maximum: torch.Tensor  # [layers, pages, Hkv, D] KV dtype, -inf before the first token
     host_credits: int
     generation: int
-    keys: list[PageKey] = field(default_factory=list)
+    pages: list[LayerPages] = field(default_factory=list)
     extra_index_bytes: int = 0
+    name: str = ""
     keepalive: tuple = ()  # caller metadata retained until the retirement event
+
+    @property
+    def keys(self):
+        """Materialized page keys of the request, in materialization order."""
+        found = [(int(lp.stamp[i]), layer, i) for layer, lp in enumerate(self.pages) for i in range(lp.materialized)]
+        return [(self.name, layer, i) for _, layer, i in sorted(found)]
+
+
+class _PendingWrite:
+    """Stands in for the events of pages whose data is not launched yet; asking to
+    wait for it launches the pages placed so far (``HostStore._flush``)."""
+
+    def __init__(self, store):
+        self.store, self.event = store, None
+
+    def query(self):
+        return self.event is not None and self.event.query()
+
+    def resolve(self):
+        if self.event is None:
+            self.store._flush()
+        return self.event
+
+    def synchronize(self):
+        self.resolve().synchronize()
+
+
+@dataclass
+class _Write:
+    """The open write of one (request, layer): pages placed, not yet launched."""
+
+    request: RequestPages
+    layer: int
+    k: torch.Tensor
+    v: torch.Tensor
+    first_token: int  # offset into k / v of the first page not launched
+    marker: _PendingWrite
+    pages: list = field(default_factory=list)  # (index, within, count) in page order
+    joins: list = field(default_factory=list)
 
 
 class PageLease:
@@ -75,7 +191,7 @@ class PageLease:
 
     def __init__(self, store: "HostStore", pages: list[Page]):
         self.store, self.pages, self.released = store, pages, False
-        self.handles = [(p.slot, store.allocator.slots[p.slot].generation, p.key) for p in pages]
+        self.handles = [(p.slot, int(store.allocator.generation[p.slot]), p.key) for p in pages]
 
     def _validate(self):
         self.store.check_stream()
@@ -94,9 +210,7 @@ class PageLease:
         done = self.store.event(self.store.compute)
         for page in self.pages:
             page.last_use = done
-            page.pins -= 1
-            if page.pins == 0:
-                self.store.pinned.discard(page.key)
+            page.pins = page.pins - 1
         self.released = True
 
     def __enter__(self):
@@ -107,41 +221,85 @@ class PageLease:
         self.release()
 
 
+class _PageMap(Mapping):
+    """``store.pages``: page key -> :class:`Page` view over every materialized page."""
+
+    def __init__(self, store):
+        self._store = store
+
+    def _layer(self, key):
+        request = self._store.requests.get(key[0])
+        if request is None or not 0 <= key[1] < request.layers:
+            return None
+        lp = request.pages[key[1]]
+        return lp if 0 <= key[2] < lp.materialized else None
+
+    def __getitem__(self, key):
+        lp = self._layer(key)
+        if lp is None:
+            raise KeyError(key)
+        return Page(lp, key)
+
+    def __contains__(self, key):
+        return isinstance(key, tuple) and len(key) == 3 and self._layer(key) is not None
+
+    def __iter__(self):
+        for name, request in self._store.requests.items():
+            for layer, lp in enumerate(request.pages):
+                for i in range(lp.materialized):
+                    yield (name, layer, i)
+
+    def __len__(self):
+        return sum(lp.materialized for r in self._store.requests.values() for lp in r.pages)
+
+
 class HostStore:
-    def __init__(self, config: CacheConfig, allocator: DeviceAllocator):
-        self.config = config
-        device = torch.device(config.device)
-        self.cuda = device.type == "cuda"
-        if self.cuda and not torch.cuda.is_available():
-            raise RuntimeError("no ROCm device available for a device='cuda' cache")
-        self.allocator = allocator
+    def __init__(self, config: CacheConfig, allocator: DeviceAllocator, ops):
+        self.config, self.allocator, self.ops = config, allocator, ops
         self.pool = allocator.storage
         self.device = self.pool.device
-        page_shape = (2, config.page_size, config.kv_heads, config.head_dim)
-        self.host = torch.empty((config.host_pages, *page_shape), dtype=config.dtype, pin_memory=self.cuda)
+        self.cuda = self.device.type == "cuda"
+        if self.cuda and not torch.cuda.is_available():
+            raise RuntimeError("no ROCm device available for a device='cuda' cache")
+        shape = (config.host_pages, 2, config.page_size, config.kv_heads, config.head_dim)
+        self.host = torch.empty(shape, dtype=config.dtype, pin_memory=self.cuda)
+        self.host_source = ops.host_source(self.host)
         self.compute = torch.cuda.current_stream(self.device) if self.cuda else None
         self.transfer = torch.cuda.Stream(device=self.device) if self.cuda else None
-        self.pages: dict[PageKey, Page] = {}
-        self.group_pages: dict[tuple, dict[int, Page]] = {}
         self.requests: dict[str, RequestPages] = {}
+        self.pages = _PageMap(self)
         self.free_host = list(range(config.host_pages - 1, -1, -1))  # pop() yields 0, 1, 2, ...
         self.stats: Counter = Counter()
-        self.pinned: set[PageKey] = set()
-        self.retired: list[tuple[object, RequestPages, list[Page]]] = []
+        self.retired: list[tuple[object, RequestPages, np.ndarray]] = []
         self.request_generation = 0
+        self._stamp = 0
+        self._write: _Write | None = None
 
-    # -- capacity views ------------------------------------------------------
+    # -- capacity views ----------------------------------------------------------
     @property
     def budget(self):
         return self.allocator.budget
 
     @property
     def owners(self):
-        return [slot.owner for slot in self.allocator.slots]
+        return self.allocator.owners()
+
+    @property
+    def pinned(self):
+        """Keys of the pages with at least one pin."""
+        return {
+            (name, layer, int(i))
+            for name, r in self.requests.items()
+            for layer, lp in enumerate(r.pages)
+            for i in np.flatnonzero(lp.pins[: lp.materialized] > 0)
+        }
+
+    def pinned_count(self):
+        return sum(int(np.count_nonzero(lp.pins[: lp.materialized])) for r in self.requests.values() for lp in r.pages)
 
     @property
     def index_bytes(self):
-        live = list(self.requests.values()) + [r for _, r, _ in self.retired]
+        live = [*self.requests.values(), *(r for _, r, _ in self.retired)]
         tensors = sum(t.numel() * t.element_size() for r in live for t in (r.summaries, r.minimum, r.maximum))
         return tensors + sum(r.extra_index_bytes for r in live)
 
@@ -158,7 +316,7 @@ class HostStore:
     def page_bytes(self):
         return self.pool[0].numel() * self.pool.element_size()
 
-    # -- streams and events --------------------------------------------------
+    # -- streams and events --------------------------------------------------------
     def context(self, stream):
         return torch.cuda.stream(stream) if self.cuda else nullcontext()
 
@@ -170,6 +328,8 @@ class HostStore:
         return event
 
     def wait(self, stream, event):
+        if isinstance(event, _PendingWrite):
+            event = event.resolve()
         if event is not None:
             stream.wait_event(event)
 
@@ -177,7 +337,7 @@ class HostStore:
         if self.cuda and torch.cuda.current_stream(self.device) != self.compute:
             raise RuntimeError("cache operations must use the construction compute stream")
 
-    # -- admission -----------------------------------------------------------
+    # -- admission -------------------------------------------------------------------
     def reserve(self, request_id: str, max_tokens: int, layers: int, *, extra_index_bytes=0):
         """Reserve host backing and index bytes for the admitted lifetime."""
         self.check_stream()
@@ -189,68 +349,73 @@ class HostStore:
         pages = ceil(max_tokens / self.config.page_size)
         if pages * layers > self.available_host_credits:
             raise CapacityError(f"need {pages * layers} host credits; have {self.available_host_credits}")
-        index_bytes = self.index_reservation_bytes(max_tokens, layers) + extra_index_bytes
-        if self.index_bytes + index_bytes > self.config.index_budget_bytes:
+        if self.index_bytes + self.index_reservation_bytes(max_tokens, layers) + extra_index_bytes > \
+                self.config.index_budget_bytes:
             raise CapacityError("GPU index budget exhausted; defer request admission")
         shape = (layers, pages, self.config.kv_heads, self.config.head_dim)
         summaries = torch.zeros(shape, device=self.device, dtype=torch.float32)
-        request = RequestPages(
-            max_tokens,
-            layers,
-            pages,
-            [0] * layers,
-            summaries,
-            # bounds are actual K extrema, exactly representable in the KV dtype
-            torch.full(shape, torch.inf, device=self.device, dtype=self.config.dtype),
-            torch.full(shape, -torch.inf, device=self.device, dtype=self.config.dtype),
-            pages * layers,
-            self.request_generation,
-        )
-        request.extra_index_bytes = extra_index_bytes
+        # bounds are exact K extrema, exactly representable in the KV dtype
+        minimum = torch.full(shape, float("inf"), device=self.device, dtype=self.config.dtype)
+        maximum = torch.full(shape, float("-inf"), device=self.device, dtype=self.config.dtype)
+        generation = self.request_generation
         self.request_generation += 1
+        request = RequestPages(max_tokens, layers, pages, [0] * layers, summaries, minimum, maximum,
+                               pages * layers, generation, extra_index_bytes=extra_index_bytes, name=request_id)
+        request.pages = [LayerPages(self.allocator.group_id((request_id, l)), pages, generation) for l in range(layers)]
         self.requests[request_id] = request
 
-    def materialize(self, request_id, layer, index):
-        key = (request_id, layer, index)
-        page = self.pages.get(key)
-        if page is None:
-            request = self.requests[request_id]
-            assert request.host_credits > 0 and self.free_host
-            request.host_credits -= 1
-            request.keys.append(key)
-            page = Page(key, self.free_host.pop(), request_generation=request.generation)
-            self.pages[key] = page
-            self.group_pages.setdefault(key[:2], {})[index] = page
-            self.stats["materialized_pages"] += 1
-        return page
+    def layer_pages(self, request_id, layer) -> LayerPages:
+        return self.requests[request_id].pages[layer]
 
-    # -- residency transitions -----------------------------------------------
+    def materialize(self, request_id, layer, index) -> Page:
+        request = self.requests[request_id]
+        lp = request.pages[layer]
+        if lp.host_slot[index] < 0:
+            if request.host_credits < 1 or not self.free_host:
+                raise AssertionError("host credit accounting broken")
+            request.host_credits -= 1
+            lp.host_slot[index] = self.free_host.pop()
+            self._stamp += 1
+            lp.stamp[index] = self._stamp
+            lp.materialized = max(lp.materialized, index + 1)
+            self.stats["materialized_pages"] += 1
+        return Page(lp, (request_id, layer, index))
+
+    # -- residency ---------------------------------------------------------------------
     def detach(self, page: Page):
-        assert page.slot is not None and page.pins == 0
-        assert page.host_enqueued_version == page.content_version
-        # the block is free at once, but its reuse is fenced behind every reader,
-        # including a queued D2H mirror that still reads it
-        for event in (page.ready, page.last_use, page.host_ready):
+        """Drop a page's device block; the block is reused only after the page's last
+        readers, loads and host mirror (a fence event on the transfer stream)."""
+        lp, i = page._lp, page.index
+        if lp.slot[i] < 0 or lp.pins[i]:
+            raise AssertionError("detach needs an unpinned resident page")
+        if lp.enqueued[i] != lp.version[i]:
+            raise AssertionError("detach before the page's host mirror was queued")
+        for event in (lp.ready[i], lp.last_use[i], lp.host_ready[i]):
             self.wait(self.transfer, event)
-        self.allocator.release(page.slot, self.event(self.transfer))
-        page.slot, page.location = None, Location.HOST
+        self.allocator.release(int(lp.slot[i]), self.event(self.transfer))
+        lp.slot[i] = -1
+        lp.location[i] = _CODE[Location.HOST]
         self.stats["evictions"] += 1
 
     def bind(self, page: Page, slot: int, location: Location):
-        page.slot, page.location = slot, location
-        page.last_use = None
+        lp, i = page._lp, page.index
+        lp.slot[i] = slot
+        lp.location[i] = _CODE[location]
+        lp.last_use[i] = None
         self.allocator.bind(slot, page.key)
-        self.stats["peak_device_pages"] = max(self.stats["peak_device_pages"], len(self.allocator.lru))
+        bound = int(np.count_nonzero(self.allocator.owner_group != NO_GROUP))
+        self.stats["peak_device_pages"] = max(self.stats["peak_device_pages"], bound)
 
-    # -- append --------------------------------------------------------------
+    # -- writes ------------------------------------------------------------------------
     @torch.inference_mode()
     def append(self, request_id, layer, k, v, prepare_page, after_write=None):
-        """Append projected K/V [tokens, Hkv, D] and mirror only the new rows.
+        """Append projected K/V ``[tokens, Hkv, D]`` to one (request, layer).
 
-        ``prepare_page(page)`` supplies resident placement and may return a read
-        lease on an existing tail; ``after_write(page)`` updates caller policy
-        after the mirror is queued.  Storage never selects a victim.
-        """
+        ``prepare_page(page)`` gives a page without rows its device block (and may
+        return a read lease of an existing tail); ``after_write(page)`` updates the
+        caller's policy once the page's mirror is queued.  Both run page by page, in
+        order; the data of the write moves in one batched launch at the end (or
+        earlier, when the policy waits for one of its pages)."""
         self.check_stream()
         request = self.requests[request_id]
         cfg = self.config
@@ -263,113 +428,130 @@ class HostStore:
             raise ValueError("K/V must be on the cache device")
         if k.dtype != cfg.dtype or v.dtype != cfg.dtype:
             raise ValueError("K/V dtype must match the cache")
-        start = request.lengths[layer]
-        if start + len(k) > request.max_tokens:
+        start, tokens = request.lengths[layer], len(k)
+        if start + tokens > request.max_tokens:
             raise CapacityError("request exceeds its reserved host capacity")
-        if any(key[0] == request_id and key[1] == layer for key in self.pinned):
+        lp = request.pages[layer]
+        if np.any(lp.pins[: lp.materialized] > 0):
             raise RuntimeError("cannot append while this layer has active attention leases")
-        if len(self.pinned) >= self.budget:
+        if self.pinned_count() >= self.budget:
             raise CapacityError("no slot available for append")
-        done = 0
-        while done < len(k):
-            index, within = divmod(start + done, cfg.page_size)
-            count = min(cfg.page_size - within, len(k) - done)
-            page = self.materialize(request_id, layer, index)
-            self._append_page(request, layer, index, page, within, k[done : done + count], v[done : done + count], prepare_page, after_write)
-            done += count
-        request.lengths[layer] += len(k)
+        write = self._write = _Write(request, layer, k.contiguous(), v.contiguous(), 0, _PendingWrite(self))
+        P = cfg.page_size
+        try:
+            position = start
+            while position < start + tokens:
+                index, within = divmod(position, P)
+                count = min(P - within, start + tokens - position)
+                page = self.materialize(request_id, layer, index)
+                lease = prepare_page(page)
+                if lease is not None:
+                    lease.wait()
+                # earlier readers, loads and mirrors of this page finish before it changes
+                write.joins += [lp.ready[index], lp.last_use[index], lp.host_ready[index]]
+                lp.valid[index] = within + count
+                lp.version[index] += 1
+                lp.sealed[index] = lp.valid[index] == P
+                lp.location[index] = _CODE[Location.RESIDENT]
+                marker = write.marker if self.cuda else None
+                lp.ready[index] = lp.host_ready[index] = marker
+                lp.enqueued[index] = lp.version[index]
+                if not self.cuda:  # the CPU mirror is part of the (synchronous) write
+                    lp.committed[index] = lp.version[index]
+                write.pages.append((index, within, count))
+                self.stats["d2h_bytes"] += self.page_bytes * count // P
+                if lease is not None:
+                    lease.release()
+                if after_write is not None:
+                    after_write(page)
+                position += count
+            request.lengths[layer] += tokens
+        finally:
+            self._flush()
+            self._write = None
 
-    def _append_page(self, request, layer, index, page, within, k, v, prepare_page, after_write):
-        cfg = self.config
-        count = len(k)
-        lease = prepare_page(page)
-        if lease is not None:
-            lease.wait()
-        # join earlier readers and mirrors of this page before modifying it
-        for event in (page.ready, page.last_use, page.host_ready):
-            self.wait(self.compute, event)
-        target = self.pool[page.slot]
-        rows = slice(within, within + count)
-        target[0, rows].copy_(k)
-        target[1, rows].copy_(v)
-        page.valid_tokens = within + count
-        page.content_version += 1
-        page.sealed = page.valid_tokens == cfg.page_size
-        # Quest bounds (exact extrema) and the mean-K summary of the page
-        request.summaries[layer, index].copy_(target[0, : page.valid_tokens].float().mean(0))
-        new_keys = target[0, rows].float()
-        lo, hi = request.minimum[layer, index], request.maximum[layer, index]
-        lo.copy_(torch.minimum(lo, new_keys.amin(0)))
-        hi.copy_(torch.maximum(hi, new_keys.amax(0)))
-        page.ready = self.event(self.compute)
-        page.location = Location.RESIDENT
-        # mirror only the new rows to the host copy, on the transfer stream
-        self.wait(self.transfer, page.ready)
-        with self.context(self.transfer):
-            if within == 0 and count == cfg.page_size:
-                self.host[page.host_slot].copy_(target, non_blocking=self.cuda)
-            else:
-                for plane in (0, 1):
-                    self.host[page.host_slot, plane, rows].copy_(target[plane, rows], non_blocking=self.cuda)
-        page.host_ready = self.event(self.transfer)
-        page.host_enqueued_version = page.content_version
-        if not self.cuda:
-            page.host_committed_version = page.content_version
-        self.stats["d2h_bytes"] += self.page_bytes * count // cfg.page_size
-        if lease is not None:
-            lease.release()
-        if after_write is not None:
-            after_write(page)
+    def _flush(self):
+        """Launch the data movement of the open write's placed pages: one batched
+        kernel writes their rows to their current device blocks (none for a page
+        detached again meanwhile) and to the host mirror, and updates their bounds
+        and summaries; their events become the launch's event."""
+        write = self._write
+        if write is None or not write.pages:
+            return
+        lp = write.request.pages[write.layer]
+        for event in write.joins:
+            if event is not write.marker:
+                self.wait(self.compute, event)
+        indices = [i for i, _, _ in write.pages]
+        count = sum(c for _, _, c in write.pages)
+        first = write.first_token
+        self.ops.append_tokens(
+            write.k[first : first + count], write.v[first : first + count],
+            indices[0], write.pages[0][1],
+            [int(lp.slot[i]) for i in indices], [int(lp.host_slot[i]) for i in indices],
+            self.pool, self.host_source, self.host,
+            write.request.minimum[write.layer], write.request.maximum[write.layer],
+            write.request.summaries[write.layer], self.config,
+        )
+        done = self.event(self.compute)
+        write.marker.event = done
+        for i in indices:
+            if lp.ready[i] is write.marker:
+                lp.ready[i] = done
+            if lp.host_ready[i] is write.marker:
+                lp.host_ready[i] = done
+        write.first_token = first + count
+        write.pages, write.joins = [], []
+        write.marker = _PendingWrite(self)
 
-    # -- retirement ----------------------------------------------------------
+    # -- retirement ------------------------------------------------------------------------
     def retire(self, request_id: str, *, keepalive=()):
         self.check_stream()
         request = self.requests[request_id]
-        if any(self.pages[key].pins for key in request.keys):
+        if any(np.any(lp.pins[: lp.materialized] > 0) for lp in request.pages):
             raise RuntimeError("cannot free a request with active leases")
-        retired = []
-        for key in request.keys:
-            page = self.pages[key]
-            assert page.slot is None, "detach resident blocks before retiring host backing"
-            for event in (page.ready, page.last_use, page.host_ready):
-                self.wait(self.transfer, event)
-            retired.append(self.pages.pop(key))
-            group = self.group_pages.get(key[:2])
-            if group is not None:
-                group.pop(key[2], None)
-                if not group:
-                    del self.group_pages[key[:2]]
+        waited = set()
+        for lp in request.pages:
+            if np.any(lp.slot[: lp.materialized] >= 0):
+                raise AssertionError("detach resident blocks before retiring host backing")
+            for events in (lp.ready, lp.last_use, lp.host_ready):
+                for event in events[: lp.materialized]:
+                    if event is not None and id(event) not in waited:
+                        waited.add(id(event))
+                        self.wait(self.transfer, event)
+        stamps = np.concatenate([lp.stamp[: lp.materialized] for lp in request.pages])
+        slots = np.concatenate([lp.host_slot[: lp.materialized] for lp in request.pages])
         del self.requests[request_id]
         request.keepalive = tuple(keepalive)
         done = self.event(self.transfer)
-        self.retired.append((done, request, retired))
+        self.retired.append((done, request, slots[np.argsort(stamps, kind="stable")]))
         self.stats["retired_requests"] += 1
         return done
 
     def collect(self, wait=False):
-        """Publish reusable host slots only after every in-flight user finished.
+        """Return host slots of retired requests whose readers have all finished.
 
-        A normal poll never blocks; ``wait`` drains retirement events (idle or
-        shutdown) rather than synchronising the device.
-        """
+        A normal poll never blocks; ``wait`` drains the retirement events (when idle
+        or shutting down) instead of synchronising the device."""
         pending = []
-        for event, request, pages in self.retired:
+        for event, request, slots in self.retired:
             if wait and event is not None:
                 event.synchronize()
             if event is None or event.query():
-                self.free_host.extend(page.host_slot for page in pages)
+                self.free_host.extend(slots.tolist())
                 self.stats["reclaimed_requests"] += 1
             else:
-                pending.append((event, request, pages))
+                pending.append((event, request, slots))
         self.retired = pending
 
-    # -- diagnostics ---------------------------------------------------------
+    # -- inspection -----------------------------------------------------------------------
     def page_state(self, key):
         page = self.pages[key]
-        backup_pending = page.host_ready is not None and not page.host_ready.query()
+        lp, i = page._lp, page.index
+        backup_pending = lp.host_ready[i] is not None and not lp.host_ready[i].query()
         if not backup_pending:
-            page.host_committed_version = page.host_enqueued_version
-        loading = page.ready is not None and not page.ready.query()
+            lp.committed[i] = lp.enqueued[i]
+        loading = lp.ready[i] is not None and not lp.ready[i].query()
         return {
             "location": page.location.value,
             "loading": loading,
@@ -378,7 +560,7 @@ class HostStore:
             "host_committed_version": page.host_committed_version,
             "sealed": page.sealed,
             "request_generation": page.request_generation,
-            "slot_generation": None if page.slot is None else self.allocator.slots[page.slot].generation,
+            "slot_generation": None if page.slot is None else int(self.allocator.generation[page.slot]),
         }
 
     def synchronize(self):
@@ -387,21 +569,29 @@ class HostStore:
             self.transfer.synchronize()
 
     def host_kv(self, request_id: str, layer: int):
-        """Blocking diagnostic read of one layer's host history (never on the decode path)."""
+        """Blocking diagnostic read of one layer's history from the host pool."""
         self.synchronize()
         request = self.requests[request_id]
-        count = ceil(request.lengths[layer] / self.config.page_size)
-        if count == 0:
+        length = request.lengths[layer]
+        if not length:
             raise ValueError("layer has no KV")
-        chunks = []
-        for i in range(count):
-            page = self.pages[(request_id, layer, i)]
-            chunks.append(self.host[page.host_slot, :, : page.valid_tokens])
-        kv = torch.cat(chunks, dim=1)
+        lp = request.pages[layer]
+        count = ceil(length / self.config.page_size)
+        rows = self.host[torch.from_numpy(lp.host_slot[:count])]  # [count, 2, P, Hkv, D]
+        kv = rows.transpose(0, 1).reshape(2, count * self.config.page_size, *rows.shape[3:])[:, :length]
         return kv[0], kv[1]
 
+    def location_counts(self):
+        counts = Counter()
+        for r in self.requests.values():
+            for lp in r.pages:
+                m = lp.materialized
+                codes = lp.location[:m][lp.valid[:m] > 0]
+                for code, n in zip(*np.unique(codes, return_counts=True)):
+                    counts[_LOCATIONS[code].value] += int(n)
+        return dict(counts)
+
     def snapshot(self):
-        locations = Counter(p.location.value for p in self.pages.values() if p.valid_tokens)
         return {
             "budget_pages": self.budget,
             "allocated_device_bytes": self.pool.numel() * self.pool.element_size(),
@@ -413,38 +603,38 @@ class HostStore:
             "host_available_credits": self.available_host_credits,
             "retiring_requests": len(self.retired),
             "request_device_pages": dict(self.allocator.occupancy),
-            "locations": dict(locations),
+            "locations": self.location_counts(),
             "stats": dict(self.stats),
         }
 
     def assert_invariants(self):
-        owners = self.owners
-        occupied = [key for key in owners if key is not None]
-        assert len(occupied) == len(set(occupied))
-        assert all(key is None for key in owners[self.budget :])
-        retired_pages = [p for _, _, pages in self.retired for p in pages]
-        assert len(self.free_host) + len(self.pages) + len(retired_pages) == self.config.host_pages
-        host_slots = [p.host_slot for p in [*self.pages.values(), *retired_pages]]
-        assert len(set(host_slots + self.free_host)) == self.config.host_pages
+        table = self.allocator
+        bound = np.flatnonzero(table.owner_group != NO_GROUP)
+        assert not np.any(table.owner_group[self.budget :] != NO_GROUP)
+        retired = np.concatenate([s for _, _, s in self.retired]) if self.retired else np.zeros(0, np.int64)
+        live = [lp.host_slot[: lp.materialized] for r in self.requests.values() for lp in r.pages]
+        live = np.concatenate(live) if live else np.zeros(0, np.int64)
+        everything = np.concatenate([live, retired, np.asarray(self.free_host, np.int64)])
+        assert len(everything) == self.config.host_pages
+        assert len(np.unique(everything)) == self.config.host_pages
         assert self.available_host_credits >= 0
-        assert self.pinned == {p.key for p in self.pages.values() if p.pins}
-        assert set(self.allocator.lru) == set(occupied)
-        assert self.allocator.free == {i for i, key in enumerate(owners) if key is None}
-        assert +self.allocator.occupancy == Counter(key[0] for key in occupied)
         assert self.index_bytes <= self.config.index_budget_bytes
-        indexed = {(g, i): p for g, pages in self.group_pages.items() for i, p in pages.items()}
-        assert {(k[:2], k[2]) for k in self.pages} == set(indexed)
-        for request in self.requests.values():
-            assert len(request.keys) + request.host_credits == request.layers * request.page_count
-        for key, page in self.pages.items():
-            assert indexed[(key[:2], key[2])] is page
-            assert page.pins >= 0
-            assert 0 <= page.valid_tokens <= self.config.page_size
-            if page.slot is None:
-                assert page.location == Location.HOST
-            else:
-                assert owners[page.slot] == key
-                assert page.location in (Location.RESIDENT, Location.HOT)
-            assert page.pins == 0 or page.slot is not None
-            assert page.request_generation == self.requests[key[0]].generation
-            assert page.host_committed_version <= page.host_enqueued_version == page.content_version
+        owned = set()
+        for name, request in self.requests.items():
+            assert sum(lp.materialized for lp in request.pages) + request.host_credits == request.layers * request.page_count
+            for layer, lp in enumerate(request.pages):
+                m = lp.materialized
+                assert np.all(lp.host_slot[:m] >= 0) and np.all(lp.host_slot[m:] < 0)
+                assert np.all(lp.pins[:m] >= 0) and np.all((lp.valid[:m] >= 0) & (lp.valid[:m] <= self.config.page_size))
+                on_host = lp.slot[:m] < 0
+                assert np.all(lp.location[:m][on_host] == _CODE[Location.HOST])
+                assert np.all(lp.location[:m][~on_host] != _CODE[Location.HOST])
+                assert np.all((lp.pins[:m] == 0) | ~on_host)
+                assert np.all(lp.committed[:m] <= lp.enqueued[:m]) and np.all(lp.enqueued[:m] == lp.version[:m])
+                for i in np.flatnonzero(~on_host).tolist():
+                    block = int(lp.slot[i])
+                    assert table.owner_group[block] == lp.gid and table.owner_index[block] == i
+                    owned.add(block)
+        for block in bound.tolist():
+            if table.owner_index[block] >= 0:
+                assert block in owned, f"block {block} bound to a page that does not hold it"

@@ -48,7 +48,7 @@ Pinning (what each function is checked against, besides the GPU):
   their tokens, and a head that reads nothing has (-inf, 0, 0).
 """
 
-from .append import append_rows, bound_max, bound_min, takes_new_max, takes_new_min
+from .append import append_rows, append_tokens, bound_max, bound_min, takes_new_max, takes_new_min
 from .attention import attend_rows, dense_attention, row_attention_rows, selection_oracle, window_state
 from .gather import gather_rows
 from .quest import quest_pages, quest_scores, quest_selection_positions
@@ -57,6 +57,7 @@ from .union import from_selection
 
 __all__ = [
     "append_rows",
+    "append_tokens",
     "attend_rows",
     "bound_max",
     "bound_min",

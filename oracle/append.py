@@ -72,3 +72,51 @@ def append_rows(pool, host, k, v, device_rows, host_rows, minimum, maximum, page
         minimum[b][...] = bound_min(minimum[b], k[b], dtype_bits)
         maximum[b][...] = bound_max(maximum[b], k[b], dtype_bits)
     return pool, host, minimum, maximum
+
+
+def append_tokens(pool, host, k, v, first_page, first_within, slots, host_slots, minimum, maximum, summaries,
+                  page_size, dtype_bits=16):
+    """A write of ``T`` consecutive tokens to one (request, layer) (the page loop of
+    ``HostStore.append``, ``mini_hisparse/storage.py:273-318``), on CPU torch tensors.
+
+    Token ``t`` goes to page ``first_page + j`` of the write's pages (the first page
+    starts at row ``first_within``, the others at row 0); page ``j`` sits in device
+    block ``slots[j]`` (``< 0``: not resident, no pool write) and host slot
+    ``host_slots[j]``.  Per page:
+
+    * K and V rows are written to the pool block (when resident) and to the host
+      slot (the mirror, ``storage.py:300-308``);
+    * the bounds fold the new K rows in order, ``b = rule(b, row)`` with torch's
+      device ``minimum``/``maximum`` rule (``takes_new_min``): for rows without NaN
+      or equal signed zeros this is ``min(old, amin(rows))`` of ``storage.py:291-297``;
+    * the summary is the float32 mean of all the page's valid K rows (the rows
+      before ``first_within`` are read back from the host slot), summed in row
+      order then divided (``storage.py:290``).
+    """
+    import torch
+
+    tokens, t = len(k), 0
+    for j, (slot, hslot) in enumerate(zip(slots, host_slots)):
+        index = first_page + j
+        within = first_within if j == 0 else 0
+        count = min(page_size - within, tokens - t)
+        rows_k, rows_v = k[t : t + count], v[t : t + count]
+        if slot >= 0:
+            pool[slot, 0, within : within + count] = rows_k
+            pool[slot, 1, within : within + count] = rows_v
+        host[hslot, 0, within : within + count] = rows_k
+        host[hslot, 1, within : within + count] = rows_v
+        lo = minimum[index].float().numpy().astype(np.float64)
+        hi = maximum[index].float().numpy().astype(np.float64)
+        for r in range(count):
+            row = rows_k[r].float().numpy().astype(np.float64)
+            lo = bound_min(lo, row, dtype_bits)
+            hi = bound_max(hi, row, dtype_bits)
+        minimum[index] = torch.from_numpy(lo).to(minimum.dtype)
+        maximum[index] = torch.from_numpy(hi).to(maximum.dtype)
+        valid = within + count
+        acc = np.zeros(host.shape[3:], np.float32)
+        for r in range(valid):
+            acc = (acc + host[hslot, 0, r].float().numpy()).astype(np.float32)
+        summaries[index] = torch.from_numpy((acc / np.float32(valid)).astype(np.float32))
+        t += count

@@ -36,6 +36,11 @@ class CpuOracleOps:
             row_stats.add_(counts_t)
         return RowPlan(torch.from_numpy(phys), torch.from_numpy(miss_host), torch.from_numpy(miss_device), counts_t)
 
+    def append_tokens(self, k, v, first_page, first_within, slots, host_slots, pool, host_source, host,
+                      minimum, maximum, summaries, config):
+        oracle.append_tokens(pool, host, k, v, first_page, first_within, slots, host_slots, minimum, maximum,
+                             summaries, config.page_size, 32 if pool.dtype == torch.float32 else 16)
+
     def gather_rows(self, host_source, pool, plan, config):
         oracle.gather_rows(host_source, pool, plan.miss_host_rows.tolist(), plan.miss_device_rows.tolist(), config.page_size)
 

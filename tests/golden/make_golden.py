@@ -15,9 +15,6 @@ records, as small JSON fixtures next to this script:
 * paged_demo_outputs.json    -- the same CLI with the optional page layout
   (``--cache-layout pages``, reference/cache.py): tokens, counters and page
   locations under each eviction policy, with and without window overlap.
-* layout_bench_counters.json -- the reference CLI ``bench`` workload
-  (experiments/benchmark.py) on CPU at its default settings: the cache
-  counters of each arrangement (timings are not kept).
 
 These are the functions no reference test or closed form pins.  The fixtures
 are data; nothing under tests/ or the product reads the reference at run time.
@@ -168,22 +165,6 @@ def paged_demo_outputs(reference_cli):
     return results
 
 
-def layout_bench_counters():
-    from experiments.benchmark import benchmark  # the reference's (CPU path)
-    from reference.cache import PagedConfig
-
-    cases = []
-    for policy in ("fair_lru", "legacy"):
-        config = PagedConfig(gpu_pages=8, host_pages=4096, page_size=16, device="cpu", dtype=torch.float32,
-                             chunk_pages=2, eviction_policy=policy)
-        report = benchmark(config)
-        cases.append({"eviction_policy": policy, "workload": {k: report["workload"][k] for k in
-                      ("tokens", "steps", "requests", "selected_pages", "page_size", "chunk_pages")},
-                      "results": [{"mode": r["mode"], "stats": r["stats"], "budget_pages": r["budget_pages"]}
-                                  for r in report["results"]]})
-    return cases
-
-
 def main():
     reference = sys.argv[1] if len(sys.argv) > 1 else "/root/reference"
     only = set(sys.argv[2:])  # optional fixture names: write only these
@@ -198,7 +179,6 @@ def main():
         "resolver_trajectories.json": lambda: resolver_trajectories(row_index),
         "demo_outputs.json": lambda: demo_outputs(cli),
         "paged_demo_outputs.json": lambda: paged_demo_outputs(cli),
-        "layout_bench_counters.json": layout_bench_counters,
     }
     fixtures = {name: make() for name, make in makers.items() if not only or name in only}
     for name, data in fixtures.items():

@@ -1,24 +1,23 @@
-"""Hybrid cache behaviour, re-expressed from the reference's tests/test_hybrid.py.
+"""The hybrid row cache end to end: scenarios whose known answers come from the
+reference's hybrid tests (mini-hisparse tests/test_hybrid.py) -- row statistics,
+protection of late hits, hot-block fragmentation, admission, leases, graph capture
+and the engine -- checked on the CPU (oracle kernels) and on the GPU (HIP).
 
-Every test runs on CPU (numpy oracle kernels injected) and on the GPU (the
-product's HIP kernels); the known answers are the reference's.
-"""
-
-from dataclasses import replace
+Every attention is compared with dense attention over its selected tokens."""
 
 import pytest
 import torch
 
 import oracle
-from mini_hisparse_amd.attention import row_attention
 from mini_hisparse_amd.config import CacheConfig, CapacityError
 from mini_hisparse_amd.engine import Engine
 from mini_hisparse_amd.hybrid import HotConfig
 from mini_hisparse_amd.model import MiniModel, ModelConfig
 from mini_hisparse_amd.row_index import LogicalTopK
 from mini_hisparse_amd.selection import Selection
+from tests.cache_harness import F32, LOW, Harness
 from tests.conftest import gpu_available
-from tests.cpu_ops import CpuOracleOps, make_cache
+from tests.cpu_ops import make_cache
 
 
 @pytest.fixture(params=["cpu", pytest.param("cuda:0", marks=pytest.mark.gpu)])
@@ -29,281 +28,235 @@ def device(request):
     return request.param
 
 
-def make(device, hot=(4, 4), **overrides):
-    config = replace(
-        CacheConfig(gpu_pages=3, host_pages=64, page_size=4, kv_heads=1, head_dim=8, device=device), **overrides
-    )
-    return make_cache(config, HotConfig(*hot))
+def cuda_only():
+    if not gpu_available():
+        pytest.skip("no ROCm GPU")
+    return "cuda:0"
 
 
-def write(cache, name="a", length=32, layer=0):
-    shape = (length, cache.config.kv_heads, cache.config.head_dim)
-    k, v = [torch.randn(shape, device=cache.device, dtype=cache.config.dtype) for _ in range(2)]
-    cache.write(name, layer, k, v)
-    return k, v
+# ------------------------------------------------------------------ row statistics
+ROW_CASES = {
+    # name: (gpu pages, tokens written, selections in order, expected (resident, hot, miss))
+    "two_reads_of_four_rows": (3, 32, [[0, 7, 17, 31]] * 2, (2, 3, 3)),
+    "all_resident": (8, 20, [[1, 7, 17, 19]], (4, 0, 0)),
+}
 
 
-def topk(cache, values):
-    return LogicalTopK(torch.tensor(values, device=cache.device, dtype=torch.int32))
+@pytest.mark.parametrize("case", sorted(ROW_CASES))
+def test_row_statistics_known_answers(device, case):
+    pages, tokens, selections, (res, hot, miss) = ROW_CASES[case]
+    h = Harness.hybrid(device, gpu_pages=pages)
+    h.cache.reserve("a", 40, 1)
+    h.write("a", tokens)
+    pool = h.cache.pool.data_ptr()
+    for positions in selections:
+        h.attend("a", positions)
+    stats = h.row_stats()
+    assert (stats["resident_hits"], stats["hot_hits"], stats["misses"]) == (res, hot, miss)
+    assert stats["h2d_bytes"] == 64 * miss  # a row is 2 planes x 8 float32: 192 bytes for three misses
+    assert h.cache.pool.data_ptr() == pool == h.cache.allocator.storage.data_ptr()
+    if case == "all_resident":
+        assert not h.cache.tables["a", 0].blocks  # no hot region was needed
+    h.cache.assert_invariants()
 
 
-def dense(q, k, v):
-    return torch.from_numpy(oracle.dense_attention(q.cpu(), k.cpu(), v.cpu())).to(q.dtype).to(q.device)
+def test_hits_of_the_same_selection_are_protected_from_replacement(device):
+    """Three selections over four hot rows; rows hit again must survive the misses of
+    the same selection, and duplicates / -1 read each token once: 5 misses in all."""
+    h = Harness.hybrid(device)
+    h.cache.reserve("a", 40, 1)
+    h.write("a", 32)
+    for positions in ([0, 4, 8, 12], [16, 4, 8, 12], [4, 4, -1, 12]):
+        h.attend("a", positions)
+    assert h.row_stats()["misses"] == 5
+    first_row_tag = h.page("a", 0).host_slot * 4
+    assert first_row_tag not in h.cache.tables["a", 0].tags.tolist()  # the LRU row went first
+    h.cache.assert_invariants()
 
 
-def test_row_misses_copy_rows_and_resident_hits_bypass_hot(device):
-    cache = make(device)
-    cache.reserve("a", 40, 1)
-    k, v = write(cache)
-    q = torch.randn(2, 8, device=device)
-    selected = [0, 7, 17, 31]
-    for _ in range(2):
-        actual = row_attention(q, cache, "a", 0, topk(cache, selected))
-        torch.testing.assert_close(actual, dense(q, k[selected], v[selected]), atol=2e-6, rtol=2e-5)
-    assert cache.snapshot()["row_stats"] == {"resident_hits": 2, "hot_hits": 3, "misses": 3, "h2d_bytes": 192}
-    assert cache.pool.data_ptr() == cache.allocator.storage.data_ptr()
-    cache.assert_invariants()
-
-
-def test_all_resident_needs_no_hot_block_lease(device):
-    cache = make(device, gpu_pages=8)
-    cache.reserve("a", 32, 1)
-    k, v = write(cache, length=20)
-    q = torch.randn(2, 8, device=device)
-    rows = [1, 7, 17, 19]
-    torch.testing.assert_close(row_attention(q, cache, "a", 0, topk(cache, rows)), dense(q, k[rows], v[rows]))
-    assert not cache.tables["a", 0].blocks
-    assert cache.snapshot()["row_stats"]["misses"] == 0
-
-
-def test_late_hits_are_protected_and_lru_replaces_only_unselected_rows(device):
-    cache = make(device)
-    cache.reserve("a", 40, 1)
-    k, v = write(cache)
-    q = torch.randn(2, 8, device=device)
-    for selected in ([0, 4, 8, 12], [16, 4, 8, 12], [4, 4, -1, 12]):
-        actual = row_attention(q, cache, "a", 0, topk(cache, selected))
-        unique = sorted({t for t in selected if t >= 0})
-        # duplicates are deduplicated by the resolver, so they carry no extra softmax mass
-        torch.testing.assert_close(actual, dense(q, k[unique], v[unique]), atol=2e-6, rtol=2e-5)
-    assert cache.snapshot()["row_stats"]["misses"] == 5
-    tag0 = cache.storage.pages["a", 0, 0].host_slot * 4
-    assert tag0 not in cache.tables["a", 0].tags.tolist()
-    cache.assert_invariants()
-
-
-def test_per_head_token_masks_and_noncontiguous_hot_blocks(device):
+def test_per_head_selections_over_fragmented_hot_blocks(device):
+    """Interleaved writes of two requests fragment the slab; request a's hot region is
+    then blocks [7, 0], and per-head token selections read through it."""
     config = CacheConfig(gpu_pages=8, host_pages=64, page_size=3, kv_heads=2, head_dim=8, device=device)
-    cache = make_cache(config, HotConfig(6, 6, transition_watermark=0))
-    cache.reserve("a", 40, 1)
-    cache.reserve("b", 40, 1)
-    for _ in range(3):  # interleaved residents leave A's reclaimed blocks fragmented
-        write(cache, "a", 3)
-        write(cache, "b", 3)
-    write(cache, "b", 3)
-    cache.storage.synchronize()
-    cache.transition_to_host("a", 0)
-    assert cache.tables["a", 0].blocks == [7, 0]
-    write(cache, "a", 18)
-    k, v = [x.to(device) for x in cache.storage.host_kv("a", 0)]
-    q = torch.randn(4, 8, device=device)
+    h = Harness(make_cache(config, HotConfig(6, 6, transition_watermark=0)))
+    h.cache.reserve("a", 40, 1)
+    h.cache.reserve("b", 40, 1)
+    for _ in range(3):
+        h.write("a", 3)
+        h.write("b", 3)
+    h.write("b", 3)
+    h.cache.storage.synchronize()
+    h.cache.transition_to_host("a", 0)
+    assert h.cache.tables["a", 0].blocks == [7, 0]
+    h.write("a", 18)
+    q = h.query(4)
     selection = Selection.from_tokens([[0, 7], [2], [7, 11], [19, 0]], 27, 3, 4)
-    actual = cache.attention(q, "a", 0, selection=selection)
-    expected = oracle.selection_oracle(q.cpu(), k.cpu(), v.cpu(), selection.positions)
-    torch.testing.assert_close(actual.cpu(), torch.from_numpy(expected).float(), atol=2e-6, rtol=2e-5)
-    cache.assert_invariants()
+    out = h.cache.attention(q, "a", 0, selection=selection)
+    k, v = h.cache.storage.host_kv("a", 0)
+    expected = oracle.selection_oracle(q.cpu(), k, v, selection.positions)
+    torch.testing.assert_close(out.double().cpu(), torch.from_numpy(expected), **F32)
+    h.cache.assert_invariants()
 
 
-def test_capacity_admission_and_topk_overflow_are_atomic(device):
-    cache = make(device, gpu_pages=3)
-    cache.reserve("a", 40, 1)
-    before = cache.index_bytes
+# ---------------------------------------------------------------------- admission
+def test_admission_and_oversized_selections_change_nothing(device):
+    h = Harness.hybrid(device)
+    h.cache.reserve("a", 40, 1)
+    index_before = h.cache.index_bytes
     with pytest.raises(CapacityError, match="credits"):
-        cache.reserve("b", 40, 1)
-    assert "b" not in cache.storage.requests and cache.index_bytes == before
-    write(cache)
-    old = cache.tables["a", 0].tags.clone()
+        h.cache.reserve("b", 40, 1)
+    assert "b" not in h.cache.storage.requests and h.cache.index_bytes == index_before
+    h.write("a", 32)
+    tags = h.cache.tables["a", 0].tags.clone()
+    five = LogicalTopK(torch.tensor([0, 1, 2, 3, 4], dtype=torch.int32, device=device))
     with pytest.raises(ValueError, match="max_union_rows"):
-        cache.resolve("a", 0, topk(cache, [0, 1, 2, 3, 4]))
-    torch.testing.assert_close(old, cache.tables["a", 0].tags)
+        h.cache.resolve("a", 0, five)
+    assert torch.equal(tags, h.cache.tables["a", 0].tags)
     with pytest.raises(ValueError):
-        HotConfig(8, 4)
-    cache.assert_invariants()
+        HotConfig(8, 4)  # the hot region must cover the union bound
+    h.cache.assert_invariants()
 
 
-def test_index_tables_are_charged_to_budget(device):
-    needed = make(device).index_reservation_bytes(40, 1)
-    tiny = make(device, index_budget_bytes=needed - 1)
-    with pytest.raises(CapacityError, match="index budget"):
-        tiny.reserve("a", 40, 1)
-    assert not tiny.storage.requests and not tiny.tables
-    exact = make(device, index_budget_bytes=needed)
-    exact.reserve("a", 40, 1)
-    assert exact.index_bytes == needed
-    exact.release_request("a")
-    assert exact.index_bytes == 0
+@pytest.mark.parametrize("slack", [-1, 0])
+def test_index_budget_counts_tables_exactly(device, slack):
+    needed = Harness.hybrid(device).cache.index_reservation_bytes(40, 1)
+    h = Harness.hybrid(device, index_budget_bytes=needed + slack)
+    if slack < 0:
+        with pytest.raises(CapacityError, match="index budget"):
+            h.cache.reserve("a", 40, 1)
+        assert not h.cache.storage.requests and not h.cache.tables
+        return
+    h.cache.reserve("a", 40, 1)
+    assert h.cache.index_bytes == needed
+    h.cache.release_request("a")
+    assert h.cache.index_bytes == 0
 
 
-def test_active_tail_and_row_lease_lifetime(device):
-    cache = make(device, gpu_pages=3)
-    cache.reserve("a", 40, 1)
-    write(cache)
-    lease = cache.resolve("a", 0, topk(cache, [0, 4, 8, 31]))
+# ------------------------------------------------------------------------ leases
+def test_row_lease_excludes_writes_and_release_and_tails_stay(device):
+    h = Harness.hybrid(device)
+    h.cache.reserve("a", 40, 1)
+    h.write("a", 32)
+    selected = LogicalTopK(torch.tensor([0, 4, 8, 31], dtype=torch.int32, device=device))
+    lease = h.cache.resolve("a", 0, selected)
     lease.wait()
     with pytest.raises(RuntimeError, match="already leased"):
-        cache.resolve("a", 0, topk(cache, [1]))
+        h.cache.resolve("a", 0, LogicalTopK(torch.tensor([1], dtype=torch.int32, device=device)))
     with pytest.raises(RuntimeError, match="active row"):
-        cache.release_request("a")
+        h.cache.release_request("a")
     with pytest.raises(RuntimeError, match="append"):
-        write(cache, length=1)
+        h.write("a", 1)
     lease.release()
-    write(cache, length=1)
-    pages = cache.storage.pages
-    assert pages["a", 0, 8].slot is not None and pages["a", 0, 7].slot is not None
-    assert pages["a", 0, 6].slot is None
-    cache.assert_invariants()
-    cache.release_request("a")
+    h.write("a", 1)  # token 32 opens page 8
+    assert [h.resident("a", p) for p in (6, 7, 8)] == [False, True, True]
+    h.cache.assert_invariants()
+    h.cache.release_request("a")
     with pytest.raises(RuntimeError, match="released"):
         lease.wait()
 
 
-@pytest.mark.gpu
-@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
-def test_gpu_row_gather_attention_low_precision(dtype):
-    if not gpu_available():
-        pytest.skip("no ROCm GPU")
-    cache = make("cuda:0", dtype=dtype, page_size=7, head_dim=24, kv_heads=2)
-    cache.reserve("a", 100, 1)
-    k, v = write(cache, length=80)
-    q = torch.randn(6, 24, device="cuda", dtype=dtype)
-    selected = [0, 13, 39, 79]
-    actual = row_attention(q, cache, "a", 0, topk(cache, selected))
-    torch.testing.assert_close(actual, dense(q, k[selected], v[selected]), atol=0.004, rtol=0.02)
+def test_invalid_or_padding_only_selection_reads_nothing(device):
+    h = Harness.hybrid(device)
+    h.cache.reserve("a", 40, 1)
+    h.write("a", 32)
+    out = h.attend("a", [-1, -2, 100, 32])
+    assert torch.count_nonzero(out) == 0
+    assert h.row_stats()["misses"] == 0
 
 
-@pytest.mark.gpu
-def test_device_resolver_supports_graph_capture_without_cpu_readback():
-    if not gpu_available():
-        pytest.skip("no ROCm GPU")
-    from mini_hisparse_amd.row_index import resolve_rows
-
-    cache = make("cuda:0")
-    cache.reserve("a", 40, 1)
-    write(cache)
-    tables = cache.tables["a", 0]
-    logical = topk(cache, [0, 4, 8, 31])
-
-    def resolve():
-        return resolve_rows(logical, tables.source, tables.resident, tables.hot, tables.tags, tables.lru, 32, 4)
-
-    stream = torch.cuda.Stream()
-    stream.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(stream):
-        for _ in range(3):
-            resolve()
-    torch.cuda.current_stream().wait_stream(stream)
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        result = resolve()
-    logical.positions.copy_(torch.tensor([1, 5, 9, 31], device="cuda", dtype=torch.int32))
-    graph.replay()
-    torch.cuda.synchronize()
-    assert result.counts.tolist() == [1, 0, 3]
-    # later replays see the tags the first one wrote: the three rows now hit
-    for _ in range(2):
-        torch.cuda.synchronize()
-        graph.replay()
-        torch.cuda.synchronize()
-        assert result.counts.tolist() == [1, 3, 0]
+def test_random_appends_and_row_replacement_over_two_requests(device):
+    torch.manual_seed(17)
+    h = Harness.hybrid(device, gpu_pages=12, host_pages=256, seed=17)
+    for name in ("a", "b"):
+        h.cache.reserve(name, 64, 2)
+        for layer in range(2):
+            h.write(name, 19, layer)
+    rng = torch.Generator().manual_seed(18)
+    for step in range(32):
+        name, layer = "ab"[step % 2], (step // 2) % 2
+        h.write(name, 1, layer)
+        length = len(h.kv(name, layer)[0])
+        selected = torch.randperm(length - 1, generator=rng)[:3].tolist() + [length - 1]
+        h.attend(name, selected, layer)
+        h.cache.assert_invariants()
+    for name in ("a", "b"):
+        h.cache.release_request(name)
+    h.cache.assert_invariants()
 
 
-@pytest.mark.gpu
-def test_gpu_deferred_reuse_keeps_host_and_hot_readers_alive():
-    if not gpu_available():
-        pytest.skip("no ROCm GPU")
-    cache = make("cuda:0", gpu_pages=3)
-    cache.reserve("same", 40, 1)
-    k, _ = write(cache, "same")
-    with cache.resolve("same", 0, topk(cache, [0, 4, 8, 31])) as lease:
-        torch.cuda._sleep(2_000_000)
-        row = lease.plan.physical_rows[0]
-        actual = cache.pool[row // 4, 0, row % 4].clone()
-    old_hosts = {p.host_slot for p in cache.storage.pages.values()}
-    cache.release_request("same", wait=False)
-    cache.reserve("same", 40, 1)
-    write(cache, "same")
-    if cache.storage.retired:
-        assert old_hosts.isdisjoint({p.host_slot for p in cache.storage.pages.values()})
-    torch.testing.assert_close(actual, k[0])
-    cache.release_request("same")
-    cache.assert_invariants()
-
-
-def test_engine_waits_for_hot_capacity_and_never_reprefills(device):
+# ----------------------------------------------------------------------------- engine
+def test_engine_waits_for_hot_credits_and_prefills_once(device):
     torch.manual_seed(9)
-    model_cfg = ModelConfig(
-        hidden_size=16, intermediate_size=32, num_hidden_layers=2, num_attention_heads=2,
-        num_key_value_heads=1, vocab_size=32,
-    )
-    model = MiniModel(model_cfg).eval().to(device)
-    config = CacheConfig(gpu_pages=8, host_pages=64, page_size=4, kv_heads=1, head_dim=8, device=device)
-    cache = make_cache(config, HotConfig(8, 8))
+    config = ModelConfig(hidden_size=16, intermediate_size=32, num_hidden_layers=2, num_attention_heads=2,
+                         num_key_value_heads=1, vocab_size=32)
+    model = MiniModel(config).eval().to(device)
+    cache = make_cache(CacheConfig(gpu_pages=8, host_pages=64, page_size=4, kv_heads=1, head_dim=8, device=device),
+                       HotConfig(8, 8))
     engine = Engine(model, cache, top_k=2)
-    for name in ["a", "b"]:
+    for name in "ab":
         engine.add_request(name, list(range(1, 22)), 5)
     engine.step()
-    assert len(engine.waiting) == 1
+    assert len(engine.waiting) == 1  # the second request waits for hot-region credits
     outputs = engine.run()
     assert all(len(tokens) == 5 for tokens in outputs.values())
-    assert all(r.prefill_count == 1 and r.decode_count == 4 for r in engine.requests.values())
+    assert all((r.prefill_count, r.decode_count) == (1, 4) for r in engine.requests.values())
     assert not cache.storage.requests and not cache.tables and not any(cache.owners)
     cache.assert_invariants()
 
 
-def test_randomized_requests_layers_append_and_row_replacement(device):
-    torch.manual_seed(17)
-    cache = make(device, gpu_pages=12, host_pages=256)
-    histories = {}
-    for name in ("a", "b"):
-        cache.reserve(name, 64, 2)
-        for layer in range(2):
-            histories[name, layer] = write(cache, name, 19, layer)
-    for step in range(32):
-        name, layer = ("a", "b")[step % 2], (step // 2) % 2
-        k, v = histories[name, layer]
-        new_k, new_v = write(cache, name, 1, layer)
-        k, v = torch.cat((k, new_k)), torch.cat((v, new_v))
-        histories[name, layer] = k, v
-        selected = [*torch.randperm(len(k) - 1)[:3].tolist(), len(k) - 1]
-        q = torch.randn(2, 8, device=device)
-        actual = row_attention(q, cache, name, layer, topk(cache, selected))
-        torch.testing.assert_close(actual, dense(q, k[selected], v[selected]), atol=3e-6, rtol=3e-5)
-        cache.assert_invariants()
-    for name in ("a", "b"):
-        cache.release_request(name)
-    cache.assert_invariants()
+# -------------------------------------------------------------------------- GPU only
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_low_precision_rows_on_a_seven_row_page(dtype):
+    h = Harness.hybrid(cuda_only(), dtype=dtype, page_size=7, head_dim=24, kv_heads=2)
+    h.cache.reserve("a", 100, 1)
+    h.write("a", 80)
+    h.attend("a", [0, 13, 39, 79], heads=6, tol=LOW)
 
 
-def test_invalid_and_padding_only_topk_do_not_read_uninitialized_rows(device):
-    cache = make(device)
-    cache.reserve("a", 40, 1)
-    write(cache)
-    q = torch.randn(2, 8, device=device)
-    output = row_attention(q, cache, "a", 0, topk(cache, [-1, -2, 100, 32]))
-    torch.testing.assert_close(output, torch.zeros_like(output))
-    assert cache.snapshot()["row_stats"]["misses"] == 0
+@pytest.mark.gpu
+def test_resolver_replays_from_a_captured_graph():
+    from mini_hisparse_amd.row_index import resolve_rows
+
+    device = cuda_only()
+    h = Harness.hybrid(device)
+    h.cache.reserve("a", 40, 1)
+    h.write("a", 32)
+    t = h.cache.tables["a", 0]
+    logical = LogicalTopK(torch.tensor([0, 4, 8, 31], dtype=torch.int32, device=device))
+    run = lambda: resolve_rows(logical, t.source, t.resident, t.hot, t.tags, t.lru, 32, 4)  # noqa: E731
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(3):
+            run()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        captured = run()
+    logical.positions.copy_(torch.tensor([1, 5, 9, 31], dtype=torch.int32, device=device))
+    graph.replay()
+    assert captured.counts.tolist() == [1, 0, 3]
 
 
-def test_product_has_no_cpu_fallback():
-    """A CPU cache without an explicit backend is rejected; backends other than HIP too."""
-    config = CacheConfig(gpu_pages=3, host_pages=64, page_size=4, kv_heads=1, head_dim=8, device="cpu")
-    from mini_hisparse_amd.hybrid import HybridKVCache
-
-    with pytest.raises(ValueError, match="ROCm"):
-        HybridKVCache(config, HotConfig(4, 4))
-    cache = HybridKVCache(config, HotConfig(4, 4), ops=CpuOracleOps())
-    cache.reserve("a", 40, 1)
-    write(cache)
-    for backend in ("torch", "triton"):
-        with pytest.raises(ValueError, match="backend"):
-            row_attention(torch.randn(2, 8), cache, "a", 0, topk(cache, [0]), backend=backend)
+@pytest.mark.gpu
+def test_released_request_keeps_its_bytes_until_readers_finish():
+    device = cuda_only()
+    h = Harness.hybrid(device)
+    h.cache.reserve("same", 40, 1)
+    k, _ = h.write("same", 32)
+    with h.cache.resolve("same", 0, LogicalTopK(torch.tensor([0, 4, 8, 31], dtype=torch.int32,
+                                                             device=device))) as lease:
+        torch.cuda._sleep(2_000_000)
+        row = lease.plan.physical_rows[0]
+        read = h.cache.pool[row // 4, 0, row % 4].clone()
+    old_slots = {p.host_slot for p in h.cache.storage.pages.values()}
+    h.cache.release_request("same", wait=False)
+    h.cache.reserve("same", 40, 1)
+    h.history.clear()
+    h.write("same", 32)
+    if h.cache.storage.retired:  # host slots of a retiring request are not reused
+        assert old_slots.isdisjoint({p.host_slot for p in h.cache.storage.pages.values()})
+    torch.testing.assert_close(read, k[0])
+    h.cache.release_request("same")
+    h.cache.assert_invariants()

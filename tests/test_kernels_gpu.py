@@ -649,3 +649,55 @@ def test_row_read_probe_covers_the_attention_entries(gpu):
     dec.probe_reads(pool, offsets, sink)
     torch.cuda.synchronize()
     assert torch.equal(pool, before)
+
+
+# ------------------------------------------------------------- batched write (append)
+@pytest.mark.parametrize(
+    "dtype,P,kv,D,start,tokens",
+    [
+        (torch.bfloat16, 16, 4, 128, 5, 1),       # a decode token in the middle of a page
+        (torch.bfloat16, 16, 4, 128, 0, 16 * 70 + 3),  # a prefill of 71 pages: two launches of 64 pages
+        (torch.bfloat16, 16, 2, 64, 13, 40),      # starts 3 rows before a page boundary
+        (torch.float16, 7, 2, 24, 3, 30),         # 96-byte rows
+        (torch.float32, 4, 1, 8, 2, 11),          # the reference tests' shape
+        (torch.bfloat16, 3, 1, 6, 1, 9),          # 12-byte rows: the 2-byte copy path
+    ],
+)
+def test_append_tokens_matches_oracle(gpu, dtype, P, kv, D, start, tokens):
+    from mini_hisparse_amd.row_kernels import MappedHost, append_tokens
+
+    pages_total = (start + tokens + P - 1) // P + 2
+    first, within = divmod(start, P)
+    write_pages = (within + tokens + P - 1) // P
+    rng = np.random.default_rng(start * 1000 + tokens)
+    blocks, host_blocks = write_pages + 5, pages_total + 9
+    slots = rng.permutation(blocks)[:write_pages].astype(np.int64)
+    slots[rng.random(write_pages) < 0.3] = -1  # pages the policy did not keep resident
+    host_slots = rng.permutation(host_blocks)[:write_pages].astype(np.int64)
+    if within:
+        slots[0] = max(int(slots[0]), 0)  # an existing tail page is resident
+    pool = make_pool(blocks, P, kv, D, dtype, seed=71)
+    host = make_pool(host_blocks, P, kv, D, dtype, seed=72)
+    if within:  # the tail's earlier rows sit in its block and in its host slot alike
+        host[host_slots[0], :, :within] = pool[slots[0], :, :within]
+    gen = torch.Generator().manual_seed(73)
+    k = torch.randn(tokens, kv, D, generator=gen).to(dtype)
+    v = torch.randn(tokens, kv, D, generator=gen).to(dtype)
+    lo = torch.full((pages_total, kv, D), float("inf")).to(dtype)
+    hi = torch.full((pages_total, kv, D), float("-inf")).to(dtype)
+    if within:
+        lo[first] = pool[slots[0], 0, :within].amin(0)
+        hi[first] = pool[slots[0], 0, :within].amax(0)
+    summ = torch.zeros(pages_total, kv, D)
+    expected = [x.clone() for x in (pool, host, lo, hi, summ)]
+    oracle.append_tokens(expected[0], expected[1], k, v, first, within, slots.tolist(), host_slots.tolist(),
+                         expected[2], expected[3], expected[4], P, 32 if dtype == torch.float32 else 16)
+    host_pinned = host.pin_memory()
+    pool_d, lo_d, hi_d, summ_d = (x.to(gpu) for x in (pool, lo, hi, summ))
+    append_tokens(k.to(gpu), v.to(gpu), first, within, slots.tolist(), host_slots.tolist(), pool_d,
+                  MappedHost(host_pinned), lo_d, hi_d, summ_d, cfg(P, kv, D))
+    torch.cuda.synchronize()
+    assert torch.equal(pool_d.cpu(), expected[0])
+    assert torch.equal(host_pinned, expected[1])
+    assert torch.equal(lo_d.cpu(), expected[2]) and torch.equal(hi_d.cpu(), expected[3])
+    assert torch.equal(summ_d.cpu(), expected[4])

@@ -442,3 +442,38 @@ def test_append_fills_a_page_to_its_column_extrema_and_writes_rows():
     np.testing.assert_array_equal(pool[2, 1], vals)
     np.testing.assert_array_equal(host[4], pool[2])
     assert not pool[:2].any() and not host[:4].any()
+
+
+def test_one_write_of_many_tokens_equals_token_by_token_writes():
+    """The batched write's bounds fold rows in order, so one write of T tokens and T
+    writes of one token give the same pool, host mirror, bounds and summaries; the
+    bounds are the exact extrema of each page's rows (no NaN, no signed-zero ties)."""
+    import torch
+
+    P, kv, D, tokens, start = 4, 2, 3, 23, 2
+    gen = torch.Generator().manual_seed(5)
+    k, v = torch.randn(tokens, kv, D, generator=gen), torch.randn(tokens, kv, D, generator=gen)
+    pages = (start + tokens + P - 1) // P
+    slots, host_slots = list(range(pages)), list(range(10, 10 + pages))
+
+    def fresh():
+        pool, host = torch.zeros(pages, 2, P, kv, D), torch.zeros(20, 2, P, kv, D)
+        lo, hi = torch.full((pages, kv, D), float("inf")), torch.full((pages, kv, D), float("-inf"))
+        return pool, host, lo, hi, torch.zeros(pages, kv, D)
+
+    bulk = fresh()
+    oracle.append_tokens(*bulk[:2], k, v, start // P, start % P, slots[start // P:], host_slots[start // P:],
+                         *bulk[2:], P, 32)
+    steps = fresh()
+    for t in range(tokens):
+        page, within = divmod(start + t, P)
+        oracle.append_tokens(*steps[:2], k[t : t + 1], v[t : t + 1], page, within, [slots[page]],
+                             [host_slots[page]], *steps[2:], P, 32)
+    for a, b in zip(bulk, steps):
+        assert torch.equal(a, b)
+    pool, _, lo, hi, summ = bulk
+    for page in range(start // P, pages):
+        rows = range(max(0, start - page * P), min(P, start + tokens - page * P))
+        keys = torch.stack([k[page * P + r - start] for r in rows])
+        assert torch.equal(lo[page], keys.amin(0)) and torch.equal(hi[page], keys.amax(0))
+        assert torch.allclose(summ[page], pool[page, 0, : max(rows) + 1].mean(0), atol=1e-6)

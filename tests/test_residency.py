@@ -1,17 +1,17 @@
-"""Readable free pages, mirror publication and proactive hot admission,
-re-expressed from the reference's tests/test_residency.py (CPU oracle backend
-and GPU HIP backend)."""
+"""Residency policy of the hybrid cache: readable-but-reclaimable history, completion
+publication of host mirrors, and the three triggers of a hot region (window,
+watermark, pressure).  The scenarios and their known answers are those of the
+reference's residency tests (mini-hisparse tests/test_residency.py); the mirror
+completion doubles stand in for device events on the CPU."""
 
 import pytest
 import torch
 
-import oracle
-from mini_hisparse_amd.attention import row_attention
-from mini_hisparse_amd.config import CacheConfig, CapacityError
-from mini_hisparse_amd.hybrid import ACTIVE_TAIL_PAGES, HotConfig
+from mini_hisparse_amd.config import CapacityError
+from mini_hisparse_amd.hybrid import ACTIVE_TAIL_PAGES
 from mini_hisparse_amd.row_index import LogicalTopK
+from tests.cache_harness import Harness
 from tests.conftest import gpu_available
-from tests.cpu_ops import make_cache
 
 
 @pytest.fixture(params=["cpu", pytest.param("cuda:0", marks=pytest.mark.gpu)])
@@ -22,278 +22,233 @@ def device(request):
     return request.param
 
 
-def make(device, pages=7, watermark=0, window=64):
-    config = CacheConfig(gpu_pages=pages, host_pages=128, page_size=4, kv_heads=1, head_dim=8, device=device)
-    return make_cache(config, HotConfig(4, 4, resident_window_pages=window, transition_watermark=watermark))
+def cache_of(device, pages=7, watermark=0, window=64, seed=0):
+    """One KV head of 8 dims, pages of 4 tokens, a hot region of one block (4 rows)."""
+    return Harness.hybrid(device, gpu_pages=pages, host_pages=128, window=window, watermark=watermark, seed=seed)
 
 
-def spin_cycles(ms):
-    """Cycle count for torch's spin kernel that keeps a stream busy for at least ``ms``.
-
-    The spin counts shader clock cycles, whose rate follows the GPU's clock state:
-    the fastest of three calibration spins sets the count, so that a later spin at a
-    higher clock than during calibration still lasts ``ms``.
-    """
-    fastest = None
-    for _ in range(3):
-        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        start.record()
-        torch.cuda._sleep(10_000_000)
-        end.record()
-        end.synchronize()
-        elapsed = max(start.elapsed_time(end), 1e-3)
-        fastest = elapsed if fastest is None else min(fastest, elapsed)
-    return int(10_000_000 * ms / fastest)
+def positions(device, values):
+    return LogicalTopK(torch.tensor(values, dtype=torch.int32, device=device))
 
 
-def write(cache, name, count):
-    k, v = [torch.randn(count, 1, 8, device=cache.device) for _ in range(2)]
-    cache.write(name, 0, k, v)
-    return k, v
+class FakeCompletion:
+    """A host-mirror event under the test's control."""
 
-
-def select(cache, positions):
-    return LogicalTopK(torch.tensor(positions, dtype=torch.int32, device=cache.device))
-
-
-def dense(q, k, v):
-    return torch.from_numpy(oracle.dense_attention(q.cpu(), k.cpu(), v.cpu())).to(q.dtype).to(q.device)
-
-
-def test_unpinned_page_still_hits_until_actual_block_reuse(device):
-    cache = make(device)
-    for name in ("a", "b"):
-        cache.reserve(name, 64, 1)
-    k, v = write(cache, "a", 12)
-    cache.storage.synchronize()
-    page = cache.storage.pages["a", 0, 0]
-    slot, host = page.slot, page.host_slot
-    generation = cache.allocator.slots[slot].generation
-    cache.reclaim_history("a", 0)
-    assert cache.page_state(page.key)["residency"] == "clean_unpinned"
-    assert page.slot == slot and cache.tables["a", 0].resident[0].item() == slot
-    assert cache.allocator.slots[slot].generation == generation
-    assert cache.snapshot()["allocatable_device_blocks"] == 4  # 3 empty + 1 readable
-
-    q = torch.randn(2, 8, device=device)
-    torch.testing.assert_close(row_attention(q, cache, "a", 0, select(cache, [0])), dense(q, k[:1], v[:1]))
-    assert cache.snapshot()["row_stats"]["misses"] == 0
-    write(cache, "b", 12)  # empty blocks are taken before readable clean KV
-    assert page.slot == slot and cache.storage.stats["unpinned_block_reuses"] == 0
-    write(cache, "b", 1)  # no empties left: A's old block is reused now
-    assert page.slot is None and page.host_slot == host
-    assert cache.tables["a", 0].resident[0].item() == -1
-    assert cache.owners[slot] == ("b", 0, 3)
-    assert cache.allocator.slots[slot].generation == generation + 1
-    with pytest.raises(RuntimeError, match="stale"):
-        cache.allocator.validate(slot, generation, page.key)
-    torch.testing.assert_close(row_attention(q, cache, "a", 0, select(cache, [0])), dense(q, k[:1], v[:1]))
-    assert cache.snapshot()["row_stats"]["misses"] == 1
-    cache.assert_invariants()
-
-
-def test_consumer_lease_temporarily_protects_a_readable_free_block(device):
-    cache = make(device)
-    for name in ("a", "b"):
-        cache.reserve(name, 64, 1)
-    k, _ = write(cache, "a", 12)
-    cache.storage.synchronize()
-    cache.reclaim_history("a", 0)
-    page = cache.storage.pages["a", 0, 0]
-    slot = page.slot
-    with cache.resolve("a", 0, select(cache, [0])) as lease:
-        assert slot in cache.allocator.reclaimable
-        assert slot not in cache._available_blocks()
-        if cache.storage.cuda:
-            torch.cuda._sleep(2_000_000)
-        observed = cache.pool[slot, 0, 0].clone()
-        write(cache, "b", 13)  # B must reclaim its own history instead
-        assert page.slot == slot
-        assert cache.tables["b", 0].blocks
-        lease._validate()
-    torch.testing.assert_close(observed, k[0])
-    assert slot in cache._available_blocks()
-    cache.assert_invariants()
-
-
-def test_window_triggers_hot_without_memory_exhaustion(device):
-    cache = make(device, pages=12, window=3)
-    cache.reserve("a", 64, 1)
-    write(cache, "a", 8)
-    assert not cache.tables["a", 0].hot_required
-    write(cache, "a", 4)
-    tables = cache.tables["a", 0]
-    assert tables.hot_required and tables.trigger == "window" and tables.blocks
-    assert cache.storage.stats["evictions"] == 0
-    assert len(cache.allocator.free) == 8
-    cache.storage.synchronize()
-    cache.collect()
-    assert cache.page_state(("a", 0, 0))["residency"] == "clean_unpinned"
-    assert cache.storage.pages["a", 0, 0].slot is not None
-    cache.assert_invariants()
-
-
-def test_watermark_uses_projected_capacity_before_the_last_block(device):
-    cache = make(device, pages=10, watermark=4)
-    cache.reserve("a", 64, 1)
-    write(cache, "a", 24)
-    assert len(cache.allocator.free) == 4 and not cache.tables["a", 0].blocks
-    write(cache, "a", 4)
-    assert cache.tables["a", 0].trigger == "watermark"
-    assert cache.tables["a", 0].blocks
-    assert len(cache.allocator.free) == 2 and cache.storage.stats["evictions"] == 0
-    cache.assert_invariants()
-
-
-def test_hot_demand_survives_a_busy_layer_without_revoking_residents(device):
-    cache = make(device, pages=6)
-    cache.reserve("a", 64, 1)
-    write(cache, "a", 12)
-    before = cache.tables["a", 0].resident.clone()
-    with cache.resolve("a", 0, select(cache, [0, 4, 8])):
-        with pytest.raises(CapacityError, match="active row lease"):
-            cache.transition_to_host("a", 0)
-        assert cache.tables["a", 0].hot_required
-        assert not cache.tables["a", 0].blocks
-        torch.testing.assert_close(before, cache.tables["a", 0].resident)
-        cache.collect()
-        assert not cache.tables["a", 0].blocks
-    cache.collect()
-    assert cache.tables["a", 0].blocks
-    cache.assert_invariants()
-
-
-def test_two_active_tails_survive_full_and_partial_page_boundaries(device):
-    assert ACTIVE_TAIL_PAGES == 2
-    cache = make(device, pages=3, watermark=None)
-    cache.reserve("a", 64, 1)
-    write(cache, "a", 9)
-    pages = cache.storage.pages
-    assert pages["a", 0, 0].slot is None
-    assert pages["a", 0, 1].slot is not None and pages["a", 0, 2].slot is not None
-    write(cache, "a", 3)  # the last page seals; the full page before it is still a tail
-    assert pages["a", 0, 1].slot is not None
-    write(cache, "a", 1)
-    assert pages["a", 0, 1].slot is None
-    assert pages["a", 0, 2].slot is not None and pages["a", 0, 3].slot is not None
-    cache.assert_invariants()
-    small = make(device, pages=2)
-    with pytest.raises(CapacityError, match="credits"):
-        small.reserve("a", 64, 1)
-    assert not small.storage.requests and not small.tables
-
-
-def test_minimum_hot_capacity_progresses_when_every_selected_row_misses(device):
-    """H = U needs no spare row: protect zero hits, replace every slot, cross the tails."""
-    torch.manual_seed(29)
-    cache = make(device, pages=3, watermark=None)  # one hot block + two tails
-    cache.reserve("a", 64, 1)
-    k, v = write(cache, "a", 32)
-    cache.reset_stats()
-    choices = ([0, 4, 8, 12], [1, 5, 9, 13])
-    for step in range(16):
-        new_k, new_v = write(cache, "a", 1)
-        k, v = torch.cat((k, new_k)), torch.cat((v, new_v))
-        positions = choices[step % 2]
-        assert all(cache.storage.pages["a", 0, t // 4].slot is None for t in positions)
-        q = torch.randn(2, 8, device=device)
-        actual = row_attention(q, cache, "a", 0, select(cache, positions))
-        torch.testing.assert_close(actual, dense(q, k[positions], v[positions]), atol=3e-6, rtol=3e-5)
-        tail = (len(k) - 1) // 4
-        assert all(cache.storage.pages["a", 0, p].slot is not None for p in (tail - 1, tail))
-        cache.assert_invariants()
-    assert cache.row_stats.tolist() == [0, 0, 64]
-    assert cache.storage.requests["a"].lengths == [48]
-    assert cache.storage.stats["peak_device_pages"] <= 3
-    cache.release_request("a")
-    cache.assert_invariants()
-
-
-class Completion:
-    """Host-side stand-in for a device event (query/synchronize)."""
-
-    def __init__(self, fail_on_wait=False):
-        self.done, self.waits, self.fail_on_wait = False, 0, fail_on_wait
+    def __init__(self, on_wait=None):
+        self.done, self.waits, self.on_wait = False, 0, on_wait
 
     def query(self):
         return self.done
 
     def synchronize(self):
-        if self.fail_on_wait:
-            pytest.fail("a normal policy tick must not wait for pending mirrors")
+        if self.on_wait is not None:
+            self.on_wait()
         self.done = True
         self.waits += 1
 
 
-def test_pending_mirror_is_not_clean_and_policy_tick_does_not_wait():
-    cache = make("cpu", pages=6)
-    cache.reserve("a", 64, 1)
-    write(cache, "a", 12)
-    page = cache.storage.pages["a", 0, 0]
-    completion = Completion(fail_on_wait=True)
-    page.host_ready, page.host_committed_version = completion, 0
-    cache.pending_clean.add(page.key)
-    cache.reclaim_history("a", 0)
-    assert cache.page_state(page.key)["residency"] == "dirty"
-    assert page.slot not in cache.allocator.reclaimable
-    cache.collect()
-    assert page.slot not in cache.allocator.reclaimable
-    completion.done = True
-    cache.collect()
-    assert cache.page_state(page.key)["residency"] == "clean_unpinned"
+def test_reclaimable_history_hits_until_its_block_is_taken(device):
+    h = cache_of(device)
+    for name in "ab":
+        h.cache.reserve(name, 64, 1)
+    h.write("a", 12)
+    h.cache.storage.synchronize()
+    page = h.page("a", 0)
+    slot, host, generation = page.slot, page.host_slot, h.cache.allocator.slots[page.slot].generation
+    h.cache.reclaim_history("a", 0)
+    assert h.cache.page_state(page.key)["residency"] == "clean_unpinned"
+    # still mapped, same generation; 3 empty blocks + this readable one can be allocated
+    assert page.slot == slot and h.cache.tables["a", 0].resident[0].item() == slot
+    assert h.cache.allocator.slots[slot].generation == generation
+    assert h.cache.snapshot()["allocatable_device_blocks"] == 4
+    h.attend("a", [0])
+    assert h.row_stats()["misses"] == 0
+    h.write("b", 12)  # empty blocks go first
+    assert page.slot == slot and h.cache.storage.stats["unpinned_block_reuses"] == 0
+    h.write("b", 1)  # none left: b's page 3 takes a's readable block
+    assert page.slot is None and page.host_slot == host
+    assert h.cache.tables["a", 0].resident[0].item() == -1
+    assert h.cache.owners[slot] == ("b", 0, 3)
+    assert h.cache.allocator.slots[slot].generation == generation + 1
+    with pytest.raises(RuntimeError, match="stale"):
+        h.cache.allocator.validate(slot, generation, page.key)
+    h.attend("a", [0])
+    assert h.row_stats()["misses"] == 1  # now loaded from the host mirror
+    h.cache.assert_invariants()
+
+
+def test_a_reader_keeps_a_reclaimable_block(device):
+    h = cache_of(device)
+    for name in "ab":
+        h.cache.reserve(name, 64, 1)
+    k, _ = h.write("a", 12)
+    h.cache.storage.synchronize()
+    h.cache.reclaim_history("a", 0)
+    slot = h.page("a", 0).slot
+    with h.cache.resolve("a", 0, positions(device, [0])) as lease:
+        assert slot in h.cache.allocator.reclaimable and slot not in h.cache._available_blocks()
+        if h.cache.storage.cuda:
+            torch.cuda._sleep(2_000_000)
+        read = h.cache.pool[slot, 0, 0].clone()
+        h.write("b", 13)  # b must move its own history to its hot region instead
+        assert h.page("a", 0).slot == slot and h.cache.tables["b", 0].blocks
+        lease._validate()
+    torch.testing.assert_close(read, k[0])
+    assert slot in h.cache._available_blocks()
+    h.cache.assert_invariants()
+
+
+@pytest.mark.parametrize(
+    "trigger,pages,window,watermark,first,second,free_after",
+    [
+        # a resident window of 3 pages: 2 pages written, then the third raises demand
+        ("window", 12, 3, 0, 8, 4, 8),
+        # 6 of 10 blocks used (4 free = watermark): the next allocation would cross it
+        ("watermark", 10, 64, 4, 24, 4, 2),
+    ],
+)
+def test_hot_region_triggers_before_any_eviction(device, trigger, pages, window, watermark, first, second,
+                                                 free_after):
+    h = cache_of(device, pages=pages, window=window, watermark=watermark)
+    h.cache.reserve("a", 64, 1)
+    h.write("a", first)
+    tables = h.cache.tables["a", 0]
+    assert not tables.hot_required and not tables.blocks
+    h.write("a", second)
+    assert tables.hot_required and tables.trigger == trigger and tables.blocks
+    assert h.cache.storage.stats["evictions"] == 0
+    assert len(h.cache.allocator.free) == free_after
+    if trigger == "window":
+        h.cache.storage.synchronize()
+        h.cache.collect()
+        assert h.cache.page_state(("a", 0, 0))["residency"] == "clean_unpinned" and h.resident("a", 0)
+    h.cache.assert_invariants()
+
+
+def test_demand_raised_during_a_lease_is_served_after_it(device):
+    h = cache_of(device, pages=6)
+    h.cache.reserve("a", 64, 1)
+    h.write("a", 12)
+    tables = h.cache.tables["a", 0]
+    resident = tables.resident.clone()
+    with h.cache.resolve("a", 0, positions(device, [0, 4, 8])):
+        with pytest.raises(CapacityError, match="active row lease"):
+            h.cache.transition_to_host("a", 0)
+        assert tables.hot_required and not tables.blocks
+        assert torch.equal(resident, tables.resident)  # residents kept
+        h.cache.collect()
+        assert not tables.blocks  # a busy layer is not transitioned
+    h.cache.collect()
+    assert tables.blocks
+    h.cache.assert_invariants()
+
+
+def test_both_active_tails_stay_resident_across_page_boundaries(device):
+    assert ACTIVE_TAIL_PAGES == 2
+    h = cache_of(device, pages=3, watermark=None)
+    h.cache.reserve("a", 64, 1)
+    h.write("a", 9)  # pages 0, 1 full, page 2 holds one row
+    assert [h.resident("a", p) for p in range(3)] == [False, True, True]
+    h.write("a", 3)  # page 2 seals; page 1 is still the tail before it
+    assert h.resident("a", 1)
+    h.write("a", 1)  # page 3 opens: page 1 leaves
+    assert [h.resident("a", p) for p in (1, 2, 3)] == [False, True, True]
+    h.cache.assert_invariants()
+    small = cache_of(device, pages=2)
+    with pytest.raises(CapacityError, match="credits"):
+        small.cache.reserve("a", 64, 1)
+    assert not small.cache.storage.requests and not small.cache.tables
+
+
+def test_one_hot_block_serves_selections_that_always_miss(device):
+    """H = U: no spare row, every selected row misses, zero hits protected, and the two
+    tails never leave: 16 steps x 4 misses (reference known answer [0, 0, 64])."""
+    h = cache_of(device, pages=3, watermark=None, seed=29)
+    h.cache.reserve("a", 64, 1)
+    h.write("a", 32)
+    h.cache.reset_stats()
+    for step in range(16):
+        h.write("a", 1)
+        chosen = ([0, 4, 8, 12], [1, 5, 9, 13])[step % 2]
+        assert not any(h.resident("a", t // 4) for t in chosen)
+        h.attend("a", chosen)
+        tail = (len(h.kv("a")[0]) - 1) // 4
+        assert h.resident("a", tail - 1) and h.resident("a", tail)
+        h.cache.assert_invariants()
+    assert h.cache.row_stats.tolist() == [0, 0, 64]
+    assert h.cache.storage.requests["a"].lengths == [48]
+    assert h.cache.storage.stats["peak_device_pages"] <= 3
+    h.cache.release_request("a")
+    h.cache.assert_invariants()
+
+
+def test_a_page_with_a_pending_mirror_is_not_offered():
+    h = cache_of("cpu", pages=6)
+    h.cache.reserve("a", 64, 1)
+    h.write("a", 12)
+    page = h.page("a", 0)
+
+    def never_wait():
+        pytest.fail("a policy tick must not wait for a pending mirror")
+
+    pending = FakeCompletion(on_wait=never_wait)
+    page.host_ready, page.host_committed_version = pending, 0
+    h.cache.pending_clean.add(page.key)
+    h.cache.reclaim_history("a", 0)
+    assert h.cache.page_state(page.key)["residency"] == "dirty"
+    assert page.slot not in h.cache.allocator.reclaimable
+    h.cache.collect()
+    assert page.slot not in h.cache.allocator.reclaimable
+    pending.done = True
+    h.cache.collect()
+    assert h.cache.page_state(page.key)["residency"] == "clean_unpinned"
     page.host_ready = None
-    cache.release_request("a")
-    cache.assert_invariants()
+    h.cache.release_request("a")
+    h.cache.assert_invariants()
+
+
+def test_pressure_waits_for_one_eligible_mirror():
+    h = cache_of("cpu", pages=3, watermark=0)
+    h.cache.reserve("a", 64, 1)
+    h.write("a", 12)
+    # every block is resident; a hot region plus a new tail need completed history
+    doubles = []
+    for index in (0, 1):
+        page = h.page("a", index)
+        doubles.append(FakeCompletion())
+        page.host_ready, page.host_committed_version = doubles[-1], 0
+        h.cache.pending_clean.add(page.key)
+    real_wait = h.cache.storage.wait
+    h.cache.storage.wait = lambda stream, event: None  # the doubles are not device events
+    h.write("a", 1)
+    assert sum(d.waits for d in doubles) >= 1
+    assert h.cache.storage.stats["pressure_mirror_waits"] >= 1
+    for key in list(h.cache.storage.pages):
+        h.cache.storage.pages[key].host_ready = None
+    h.cache.storage.wait = real_wait
+    h.cache.release_request("a")
+    h.cache.assert_invariants()
 
 
 @pytest.mark.gpu
-def test_gpu_page_is_not_unpinned_before_its_d2h_event_completes():
+def test_device_mirror_still_running_keeps_the_page_pinned():
+    """The host mirror of a write is part of its append launch on the compute stream:
+    queued behind a long kernel, the page stays dirty (not reclaimable, no pressure
+    wait) until that launch completes."""
     if not gpu_available():
         pytest.skip("no ROCm GPU")
-    # the same writes once on a scratch cache, so first-launch code loading of
-    # every kernel on this path is done before the timed stall below
-    warm = make("cuda:0", pages=8)
-    warm.reserve("w", 64, 1)
-    write(warm, "w", 12)
-    warm.transition_to_host("w", 0)
-    warm.storage.synchronize()
-    cache = make("cuda:0", pages=8)
-    cache.reserve("a", 64, 1)
-    k, v = [torch.randn(12, 1, 8, device=cache.device) for _ in range(2)]
-    cache.storage.synchronize()
-    with torch.cuda.stream(cache.storage.transfer):
-        torch.cuda._sleep(spin_cycles(1000.0))  # the transfer stream stays busy for ~1 s
-    cache.write("a", 0, k, v)
-    page = cache.storage.pages["a", 0, 0]
-    cache.transition_to_host("a", 0)
+    h = cache_of("cuda:0", pages=8)
+    h.cache.reserve("a", 64, 1)
+    k, v = h.rows(12)
+    h.cache.storage.synchronize()
+    torch.cuda._sleep(100_000_000)  # on the compute stream, ahead of the write
+    h.cache.write("a", 0, k, v)
+    page = h.page("a", 0)
+    h.cache.transition_to_host("a", 0)
     assert not page.host_ready.query()
-    assert page.slot not in cache.allocator.reclaimable
-    assert cache.storage.stats["pressure_mirror_waits"] == 0
-    cache.storage.synchronize()
-    cache.collect()
-    assert cache.page_state(page.key)["residency"] == "clean_unpinned"
-    cache.assert_invariants()
-
-
-def test_pressure_waits_only_for_an_eligible_mirror_event():
-    cache = make("cpu", pages=3, watermark=0)
-    cache.reserve("a", 64, 1)
-    write(cache, "a", 12)
-    # every block resident: a hot region and a new tail need completed history
-    completions = []
-    for index in (0, 1):
-        page = cache.storage.pages["a", 0, index]
-        event = Completion()
-        page.host_ready, page.host_committed_version = event, 0
-        cache.pending_clean.add(page.key)
-        completions.append(event)
-    original_wait = cache.storage.wait
-    cache.storage.wait = lambda stream, event: None  # CPU completion stand-in only
-    write(cache, "a", 1)
-    assert sum(e.waits for e in completions) >= 1
-    assert cache.storage.stats["pressure_mirror_waits"] >= 1
-    for page in cache.storage.pages.values():
-        page.host_ready = None
-    cache.storage.wait = original_wait
-    cache.release_request("a")
-    cache.assert_invariants()
+    assert page.slot not in h.cache.allocator.reclaimable
+    assert h.cache.storage.stats["pressure_mirror_waits"] == 0
+    h.cache.storage.synchronize()
+    h.cache.collect()
+    assert h.cache.page_state(page.key)["residency"] == "clean_unpinned"
+    h.cache.assert_invariants()
