@@ -44,6 +44,12 @@ from math import ceil
 import numpy as np
 
 METRIC = "decode tokens/s at 1 MI355X; sparse-attn HBM GB/s as % of peak"
+# request groups pipelined across layers by default, per model workload
+DEFAULT_REQUEST_GROUPS = {"qwen2.5-7b": 2}
+# gather workgroups per request with request groups: enough host reads in flight for the
+# link while leaving the fabric to the compute stream (7B, batch 8, two groups: 8 -> 68.8
+# ms per step, 16 -> 57.4, 24 -> 56.4, 32 -> 61.3, the library default 128 -> 74.1)
+DEFAULT_GROUP_GATHER_WORKGROUPS = {"qwen2.5-7b": 24}
 HBM_PEAK_GBS = 8000.0
 
 
@@ -78,6 +84,12 @@ def parse_args():
                         "transfer stream (overlapping the dense layers)")
     p.add_argument("--graphs", action="store_true",
                    help="model workloads: replay each dense layer boundary as a captured HIP graph")
+    p.add_argument("--request-groups", type=int, default=None,
+                   help="Quest model workloads: request groups pipelined across layers (one group's gather "
+                        "overlaps the others' compute); default 2 for qwen2.5-7b, else 1")
+    p.add_argument("--group-gather-workgroups", type=int, default=None,
+                   help="gather workgroups per request with request groups (0 = the library's default; "
+                        "default 24 for qwen2.5-7b)")
     p.add_argument("--no-cpu-baseline", action="store_true", help="skip the CPU oracle leg")
     p.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU sample work")
     p.add_argument("--attention-sweep", action="store_true",
@@ -608,8 +620,9 @@ PMC_SUMMARIES = {
     "qwen2.5-7b-layer": (os.path.join(PROFILES, "qwen2.5-7b_layer_pmc.txt"),
                          "one layer of the north_star step (Qwen2.5-7B heads, 128k histories), batch 16, bf16"),
 }
-# the batch each counter summary was taken at (the traffic applies to that batch only)
-PMC_BATCH = {"microbench": 8, "qwen2.5-7b": 8, "qwen2.5-7b-layer": 16}
+# (batch, request groups) each counter summary was taken at: its per-launch traffic applies
+# to that configuration only
+PMC_CONFIG = {"microbench": (8, 1), "qwen2.5-7b": (8, 2), "qwen2.5-7b-layer": (16, 1)}
 ROOFLINE_KERNELS = ("attend_mfma_kernel", "attend_merge_kernel")
 CALIBRATION_BYTES = 1 << 30  # hbm_copy_gbs: a plain device-to-device copy of 1 GiB
 
@@ -692,9 +705,10 @@ def summarize_trace(trace_dir, args):
         raise SystemExit(f"trace holds {len(ends)} decode steps, warmup + steps need {args.warmup + args.steps}")
     start = ends[args.warmup - 1] + 1 if args.warmup else 0
     window = rows[start : ends[args.warmup + args.steps - 1] + 1]
+    groups = args.request_groups if args.request_groups is not None else DEFAULT_REQUEST_GROUPS.get(args.workload, 1)
     launches = sum("attend_mfma_kernel" in r["Kernel_Name"] for r in window)
-    if launches != L * args.steps:
-        raise SystemExit(f"the timed region holds {launches} attention launches, expected {L * args.steps}")
+    if launches != L * args.steps * groups:
+        raise SystemExit(f"the timed region holds {launches} attention launches, expected {L * args.steps * groups}")
     agg = defaultdict(lambda: [0, 0])
     for r in window:
         name = r["Kernel_Name"].split("(")[0].replace("void ", "")
@@ -714,7 +728,8 @@ def summarize_trace(trace_dir, args):
         f"Summarised by: `python bench.py --workload {args.workload} --steps {args.steps} --warmup {args.warmup} "
         "--summarize-trace <dir>`",
         "",
-        f"Timed region: {args.steps} steps x {L} layers, {len(window)} dispatches over {span_ms:.1f} ms "
+        f"Timed region: {args.steps} steps x {L} layers x {groups} request group(s), {len(window)} dispatches "
+        f"over {span_ms:.1f} ms "
         f"({span_ms / args.steps:.2f} ms per step under the profiler).",
         f"Attention (`hs_attend_groups`) per launch: attend_mfma_kernel {att_us:.2f} us + attend_merge_kernel "
         f"{mrg_us:.2f} us = {att_us + mrg_us:.2f} us (the bench line's HIP events around the call also hold the "
@@ -834,21 +849,27 @@ class AttendProbe:
         self.i = 0
 
     def before_attend(self, layer, stream, dec):
+        # HIP stamps an event with the end of the stream's previous command; the engine
+        # queues a wait for the gather right before the attention, so a start event
+        # recorded there could carry a time from before that wait.  A 1-cycle kernel
+        # placed after the wait gives the start event a time after it.
+        self.torch.cuda._sleep(1)
         self.start[self.i].record(stream)
 
     def after_attend(self, layer, stream, dec):
         self.end[self.i].record(stream)
-        self.counts[self.i].copy_(dec.entry_counts.view(-1))
-        self.widths.append(dec.width)
+        counts = dec.entry_counts.view(-1)  # the launch's requests (a request group's, when pipelined)
+        self.counts[self.i, : counts.numel()].copy_(counts)
+        self.widths.append((dec.width, dec.batch))
         self.i += 1
 
     def totals(self, bytes_of):
-        """(total ms, total algorithmic bytes, launches); ``bytes_of(entries, width)`` gives
-        one launch's bytes."""
+        """(total ms, total algorithmic bytes, launches); ``bytes_of(entries, width, batch)``
+        gives one launch's bytes."""
         n = self.i
         ms = sum(self.start[i].elapsed_time(self.end[i]) for i in range(n))
         entries = self.counts[:n].sum(1).tolist()
-        nbytes = sum(bytes_of(e, w) for e, w in zip(entries, self.widths))
+        nbytes = sum(bytes_of(e, w, b) for e, (w, b) in zip(entries, self.widths))
         return ms, nbytes, n
 
 
@@ -878,8 +899,15 @@ def run_model_workload(args, torch, device):
     print(f"[bench] {wl.name}: model + synthetic history (batch {wl.batch}, {wl.context} tokens)", file=sys.stderr, flush=True)
     model = random_model(wl, device, seed=args.seed)
     state = build_state(wl, device, seed=args.seed)
+    groups = args.request_groups
+    if groups is None:
+        groups = DEFAULT_REQUEST_GROUPS.get(args.workload, 1)
     engine = BatchedDecodeEngine(model, state, wl.top_pages, selector=wl.selector, seed=args.seed, graphs=args.graphs,
-                                 prefetch=not args.no_prefetch and wl.selector == "uniform")
+                                 prefetch=not args.no_prefetch and wl.selector == "uniform",
+                                 request_groups=groups if wl.selector == "quest" else 1,
+                                 group_gather_workgroups=args.group_gather_workgroups
+                                 if args.group_gather_workgroups is not None
+                                 else DEFAULT_GROUP_GATHER_WORKGROUPS.get(args.workload, 0))
     setup_s = time.perf_counter() - t0
     gen = torch.Generator(device=device).manual_seed(args.seed)
     tokens = torch.randint(0, wl.vocab, (wl.batch,), generator=gen, device=device)
@@ -888,7 +916,8 @@ def run_model_workload(args, torch, device):
     torch.cuda.synchronize()
     print("[bench] timing", file=sys.stderr, flush=True)
     stats0 = state.row_stats.clone()
-    probe = AttendProbe(torch, device, args.steps * wl.layers, wl.batch, wl.kv_heads)
+    launches = args.steps * wl.layers * (len(engine.groups) if engine.groups else 1)
+    probe = AttendProbe(torch, device, launches, wl.batch, wl.kv_heads)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
@@ -897,6 +926,17 @@ def run_model_workload(args, torch, device):
     elapsed = time.perf_counter() - t0
     ms_per_step = elapsed * 1e3 / args.steps
     rows = ((state.row_stats - stats0).double() / args.steps).tolist()
+    in_order = None
+    if engine.groups:
+        # the same attention with the batch in one group and no gather running beside it:
+        # two extra steps in layer order, outside the timed region
+        groups_saved, engine.groups = engine.groups, None
+        solo = AttendProbe(torch, device, 2 * wl.layers, wl.batch, wl.kv_heads)
+        for _ in range(2):
+            tokens = engine.step(tokens, probe=solo)
+        torch.cuda.synchronize()
+        engine.groups = groups_saved
+        in_order = solo
     timer = []
     engine.step(tokens, timer=timer)  # profiled step, outside the timed region
     torch.cuda.synchronize()
@@ -907,14 +947,24 @@ def run_model_workload(args, torch, device):
     misses = sum(int(m) for _, _, _, m in timer)
     e, D, Hq, B, L = 2, wl.head_dim, wl.heads, wl.batch, wl.layers
 
-    def launch_bytes(entries, width):
+    def launch_bytes(entries, width, batch):
         # union-deduplicated K/V rows + the per-head row lists + queries and outputs
-        return entries * 2 * D * e + 8 * Hq * width * B + 2 * Hq * D * e * B
+        return entries * 2 * D * e + 8 * Hq * width * batch + 2 * Hq * D * e * batch
 
     att_ms, att_bytes, launches = probe.totals(launch_bytes)
     att_gbs = att_bytes / (att_ms * 1e-3) / 1e9
+    solo_line = None
+    if in_order is not None:
+        solo_ms, solo_bytes, solo_n = in_order.totals(launch_bytes)
+        solo_gbs = solo_bytes / (solo_ms * 1e-3) / 1e9
+        solo_line = {"achieved": solo_gbs, "frac": solo_gbs / HBM_PEAK_GBS, "launches": solo_n,
+                     "bytes_per_launch": solo_bytes / solo_n, "us_per_launch": solo_ms * 1e3 / solo_n,
+                     "how": "two extra steps after the timed region with the whole batch in one group, "
+                            "in layer order (no gather running beside the attention)"}
     pmc_path = PMC_SUMMARIES.get(args.workload, (None,))[0]
-    traffic = pmc_traffic(ROOFLINE_KERNELS, pmc_path) if pmc_path and wl.batch == PMC_BATCH.get(args.workload) else None
+    profiled = PMC_CONFIG.get(args.workload)
+    traffic = pmc_traffic(ROOFLINE_KERNELS, pmc_path) if pmc_path and profiled == (
+        wl.batch, len(engine.groups) if engine.groups else 1) else None
     row_bytes = 2 * wl.kv_heads * D * e
     gather_bytes = misses * row_bytes
     link = host_link_gbs(torch, device)
@@ -941,6 +991,8 @@ def run_model_workload(args, torch, device):
                f"{wl.top_pages} pages resampled uniformly each step (tail page forced), shared by every head, ")
             + f"{wl.resident_fraction:.0%} of pages resident, hot_rows {wl.hot_rows}"
             + ("; dense layer boundaries replayed as HIP graphs" if engine.use_graphs else "")
+            + (f"; {len(engine.groups)} request groups pipelined across layers (a group's gather on a transfer "
+               "stream overlaps the other groups' compute)" if engine.groups else "")
             + ("; every layer's select/resolve/gather prefetched on a transfer stream at step start "
                "(stage times of those overlap the dense layers)" if engine.prefetch else "")
             + (f"; batch cut from {configured}: {configured} histories need "
@@ -957,10 +1009,12 @@ def run_model_workload(args, torch, device):
             "unit": "GB/s",
             "frac": att_gbs / HBM_PEAK_GBS,
             "traffic": traffic,
-            "kernel": "attend_mfma_kernel + attend_merge_kernel (hs_attend_groups), every layer of the timed steps",
+            "kernel": "attend_mfma_kernel + attend_merge_kernel (hs_attend_groups), every layer of the timed steps"
+            + (" (one launch per request group, beside the other group's gather)" if engine.groups else ""),
             "launches": launches,
             "bytes_per_launch": att_bytes / launches,
             "us_per_launch": att_ms * 1e3 / launches,
+            "in_order": solo_line,
         },
         "stages_ms_per_step": stage_ms,
         "projections_on_hs_skinny_gemm": engine.projection_kernel,

@@ -247,23 +247,26 @@ class SparseKVState:
         rows = torch.tensor([ls, bs, ps, blocks], dtype=torch.int64, pin_memory=True).to(self.device, non_blocking=True)
         self.resident[rows[0], rows[1], rows[2]] = rows[3].to(torch.int32)
 
-    def append_args(self, layer, positions):
-        """ctypes arrays of one layer's hs_append_rows call."""
+    def append_args(self, layer, positions, rows=None):
+        """ctypes arrays of one layer's hs_append_rows call for the requests in ``rows``
+        (a range; default every request)."""
         P, B, C = self.config.page_size, self.batch, self.pages
         Hkv, D = self.config.kv_heads, self.config.head_dim
         esz = self.minimum.element_size()
         page_elems = Hkv * D
-        dev_rows = (ctypes.c_int64 * B)()
-        host_rows = (ctypes.c_int64 * B)()
-        lo = (ctypes.c_void_p * B)()
-        hi = (ctypes.c_void_p * B)()
+        rows = range(B) if rows is None else rows
+        n = len(rows)
+        dev_rows = (ctypes.c_int64 * n)()
+        host_rows = (ctypes.c_int64 * n)()
+        lo = (ctypes.c_void_p * n)()
+        hi = (ctypes.c_void_p * n)()
         base_lo, base_hi = self.minimum.data_ptr(), self.maximum.data_ptr()
-        for b, pos in enumerate(positions):
-            page, off = divmod(pos, P)
-            dev_rows[b] = self.tail_block[layer][b] * P + off
-            host_rows[b] = (b * C + page) * P + off
+        for i, b in enumerate(rows):
+            page, off = divmod(positions[b], P)
+            dev_rows[i] = self.tail_block[layer][b] * P + off
+            host_rows[i] = (b * C + page) * P + off
             at = ((layer * B + b) * C + page) * page_elems * esz
-            lo[b], hi[b] = base_lo + at, base_hi + at
+            lo[i], hi[i] = base_lo + at, base_hi + at
         return dev_rows, host_rows, lo, hi
 
 
@@ -279,7 +282,7 @@ class BatchedDecodeEngine:
 
     def __init__(self, model: MiniModel, state: SparseKVState, top_pages, *, max_tokens=None, keep_sink=True,
                  selector="quest", seed=0, graphs=False, projections="auto", transfer_stream=False,
-                 prefetch=None):
+                 prefetch=None, request_groups=1, group_gather_workgroups=0):
         """``selector``: "quest" (per-head Quest pages over the bounds) or "uniform"
         (:func:`uniform_pages`, shared by every head, resampled each step).  ``graphs``:
         replay the dense part of each layer boundary as a HIP graph (when every per-layer
@@ -294,7 +297,13 @@ class BatchedDecodeEngine:
         gather every layer at the start of the step on a transfer stream, one decoder
         (buffer set) per layer, so that the host reads overlap the dense layers; layer
         l's attention waits for layer l's gather only, and the step's first transfer
-        waits for the previous step's last attention (the last reader of the hot rows)."""
+        waits for the previous step's last attention (the last reader of the hot rows).
+        ``request_groups`` (Quest selector): split the batch into that many request groups
+        and pipeline them across the layers -- while one group's gather reads host memory
+        on the transfer stream, the compute stream runs the other groups' attention, dense
+        layers, append, selection and resolve (each request's own sequence of stages is
+        unchanged, so every output is the same); ``group_gather_workgroups`` sets the
+        gather's workgroups per request there (0: the library's default)."""
         if prefetch is None:
             prefetch = selector == "uniform"
         if prefetch and selector != "uniform":
@@ -328,7 +337,25 @@ class BatchedDecodeEngine:
                 f"hot_rows {state.hot_rows} below the union bound {self.dec.capacity} of "
                 f"{cfg.num_attention_heads} heads x {top_pages} pages"
             )
-        self.transfer = torch.cuda.Stream(self.device) if transfer_stream or prefetch else None
+        self.groups = None
+        if request_groups > 1:
+            if selector != "quest" or prefetch or graphs:
+                raise ValueError("request groups pipeline the Quest path (no prefetch, no graphs)")
+            count = min(request_groups, state.batch)
+            edges = [round(i * state.batch / count) for i in range(count + 1)]
+            self.groups = []
+            for a, b in zip(edges, edges[1:]):
+                group = BatchedSparseDecode(
+                    state.config, cfg.num_attention_heads, top_pages, [max(1, l) for l in state.lengths[a:b]],
+                    keep_sink=keep_sink, device=self.device, capacity_lengths=caps[a:b],
+                )
+                self.groups.append((range(a, b), group))
+            # per (layer, group): resolved (compute -> transfer) and gathered (transfer -> compute)
+            self._group_events = [[(torch.cuda.Event(), torch.cuda.Event()) for _ in self.groups]
+                                  for _ in range(state.layers)]
+            self.group_gather_workgroups = group_gather_workgroups
+            self.current_group = None
+        self.transfer = torch.cuda.Stream(self.device) if transfer_stream or prefetch or self.groups else None
         self._pack_projections()
         self._choose_projections(projections)
         self._host_alias = [(ctypes.c_void_p * state.batch)(*([a.data_ptr()] * state.batch)) for a in state.alias]
@@ -377,30 +404,34 @@ class BatchedDecodeEngine:
         self._act = new(B, cfg.intermediate_size)
 
     # -- dense stages (the same launches eagerly and inside the graphs) ---------
-    def _dense_in(self, index, first):
-        """Residual add of the previous MLP + input RMSNorm, q|k|v, rotary + split."""
+    def _dense_in(self, index, first, rows=slice(None)):
+        """Residual add of the previous MLP + input RMSNorm, q|k|v, rotary + split, for the
+        requests in ``rows`` (a slice of the batch)."""
         cfg = self.model.config
         layer = self.model.model.layers[index]
         qkv_w, qkv_b, _ = self._packed[index]
-        h = add_rms_norm(self._x, None if first else self._delta, layer.input_layernorm.weight, cfg.rms_norm_eps,
-                         out=self._h)
-        rotary_split(self._project("qkv", h, qkv_w, qkv_b, out=self._qkv), self.positions,
+        h = add_rms_norm(self._x[rows], None if first else self._delta[rows], layer.input_layernorm.weight,
+                         cfg.rms_norm_eps, out=self._h[rows])
+        rotary_split(self._project("qkv", h, qkv_w, qkv_b, out=self._qkv[rows]), self.positions[rows],
                      cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim, cfg.rope_theta,
-                     out=(self._q, self._k, self._v))
+                     out=(self._q[rows], self._k[rows], self._v[rows]))
 
-    def _dense_out(self, index):
-        """o_proj + residual + post-attention RMSNorm, gate|up, SiLU gate, down (-> delta)."""
+    def _dense_out(self, index, rows=slice(None)):
+        """o_proj + residual + post-attention RMSNorm, gate|up, SiLU gate, down (-> delta),
+        for the requests in ``rows``."""
         cfg = self.model.config
         layer = self.model.model.layers[index]
-        B = self.state.batch
         _, _, gate_up_w = self._packed[index]
-        o = self._project("o_proj", self._attn_out.view(B, -1), layer.self_attn.o_proj.weight, out=self._o)
-        h = add_rms_norm(self._x, o, layer.post_attention_layernorm.weight, cfg.rms_norm_eps, out=self._h)
+        attn = self._attn_out[rows]
+        o = self._project("o_proj", attn.view(attn.shape[0], -1), layer.self_attn.o_proj.weight, out=self._o[rows])
+        h = add_rms_norm(self._x[rows], o, layer.post_attention_layernorm.weight, cfg.rms_norm_eps,
+                         out=self._h[rows])
         if self.projection_kernel["gate_up"]:  # gate|up and the SiLU gate in one launch
-            act = linear_swiglu_tiled(h, self._tiles[gate_up_w.data_ptr()], cfg.intermediate_size, out=self._act)
+            act = linear_swiglu_tiled(h, self._tiles[gate_up_w.data_ptr()], cfg.intermediate_size,
+                                      out=self._act[rows])
         else:
-            act = silu_mul(self._project("gate_up", h, gate_up_w, out=self._gate_up), out=self._act)
-        self._project("down", act, layer.mlp.down_proj.weight, out=self._delta)
+            act = silu_mul(self._project("gate_up", h, gate_up_w, out=self._gate_up[rows]), out=self._act[rows])
+        self._project("down", act, layer.mlp.down_proj.weight, out=self._delta[rows])
 
     def _boundary(self, index):
         """Dense launches between the sparse stages of layer index - 1 and index
@@ -515,15 +546,17 @@ class BatchedDecodeEngine:
         out.copy_(y)
         return out
 
-    def _append(self, layer, k, v, positions):
+    def _append(self, layer, k, v, positions, rows=None):
+        """Each request's new K/V row (``rows``: a range of requests, default all)."""
         st, cfg = self.state, self.state.config
-        dev_rows, host_rows, lo, hi = st.append_args(layer, positions)
+        rows = range(st.batch) if rows is None else rows
+        dev_rows, host_rows, lo, hi = st.append_args(layer, positions, rows)
         _lib.check(
             _lib.load().hs_append_rows(
-                k.data_ptr(), v.data_ptr(), k.stride(0), st.pool.data_ptr(), st.blocks * cfg.page_size,
-                _lib.dtype_code(cfg.dtype), cfg.page_size, cfg.kv_heads, cfg.head_dim,
+                k[rows.start].data_ptr(), v[rows.start].data_ptr(), k.stride(0), st.pool.data_ptr(),
+                st.blocks * cfg.page_size, _lib.dtype_code(cfg.dtype), cfg.page_size, cfg.kv_heads, cfg.head_dim,
                 dev_rows, self._host_alias[layer], host_rows, st.host[layer].shape[0] * cfg.page_size, lo, hi,
-                st.batch, _lib.stream_handle(self.device),
+                len(rows), _lib.stream_handle(self.device),
             ),
             "hs_append_rows",
         )
@@ -540,6 +573,8 @@ class BatchedDecodeEngine:
         launch on the stream it runs on (light enough for timed runs: events and a copy of
         the decoder's entry counts).
         """
+        if self.groups is not None:
+            return self._step_groups(tokens, observer, timer, probe)
         model, st, dec = self.model, self.state, self.dec
         cfg = model.config
         positions = list(st.lengths)
@@ -637,6 +672,93 @@ class BatchedDecodeEngine:
         self.positions += 1
         if self.use_graphs and self._graphs is None:
             self._capture()
+        return tokens
+
+    def _step_groups(self, tokens, observer=None, timer=None, probe=None):
+        """A decode step with the batch split into request groups pipelined over layers.
+
+        Compute-stream order: for each layer and group, the group's pending attention of
+        the previous layer (after its gather's event) and its dense output, then the
+        layer's dense input, append, Quest selection and resolve; the group's gather is
+        queued on the transfer stream behind its resolve.  While group A's gather reads
+        host memory, the compute stream serves group B, and the other way round.  Hot rows
+        are rewritten by a gather only after the same group's attention of the previous
+        step (the gather waits for a resolve queued after that attention)."""
+        model, st = self.model, self.state
+        cfg = model.config
+        positions = list(st.lengths)
+        st.open_tail_pages(positions)
+        for rows, dec in self.groups:
+            dec.set_lengths([positions[b] + 1 for b in rows])
+        compute, transfer = torch.cuda.current_stream(self.device), self.transfer
+        L = st.layers
+
+        def mark(stream):
+            if timer is None:
+                return None
+            event = torch.cuda.Event(enable_timing=True)
+            event.record(stream)
+            return event
+
+        marks = [[{} for _ in self.groups] for _ in range(L)]
+
+        def attend(index, g):
+            rows, dec = self.groups[g]
+            sl = slice(rows.start, rows.stop)
+            compute.wait_event(self._group_events[index][g][1])
+            m = marks[index][g]
+            m["attend"] = [mark(compute)]
+            if probe is not None:
+                probe.before_attend(index, compute, dec)
+            out = dec.attend(self._q[sl], st.pool, out=self._attn_out[sl])
+            if probe is not None:
+                probe.after_attend(index, compute, dec)
+            m["attend"].append(mark(compute))
+            if observer is not None:
+                self.current_group = (rows, dec)
+                observer(index, self._q[sl], self._k[sl], self._v[sl], out)
+            m["dense_out"] = [mark(compute)]
+            self._dense_out(index, sl)
+            m["dense_out"].append(mark(compute))
+            if timer is not None:
+                timer.append((index, m, dec.entry_counts.sum(), dec.row_counts[:, 2].sum()))
+
+        self._x.copy_(model.model.embed_tokens(tokens))
+        for index in range(L):
+            lo, hi = st.bounds[index]
+            for g, (rows, dec) in enumerate(self.groups):
+                sl = slice(rows.start, rows.stop)
+                if index > 0:
+                    attend(index - 1, g)
+                m = marks[index][g]
+                m["dense"] = [mark(compute)]
+                self._dense_in(index, index == 0, sl)
+                m["dense"].append(mark(compute))
+                m["append"] = [m["dense"][1]]
+                self._append(index, self._k, self._v, positions, rows)
+                m["append"].append(mark(compute))
+                m["select"] = [m["append"][1]]
+                dec.select(self._q[sl], lo[sl], hi[sl])
+                m["select"].append(mark(compute))
+                m["resolve"] = [m["select"][1]]
+                dec.resolve(st.tables[index][sl], row_stats=st.row_stats)
+                m["resolve"].append(mark(compute))
+                resolved, gathered = self._group_events[index][g]
+                resolved.record(compute)
+                transfer.wait_event(resolved)
+                m["gather"] = [mark(transfer)]
+                dec.gather(st.alias[index], st.pool, transfer, grid_x=self.group_gather_workgroups)
+                m["gather"].append(mark(transfer))
+                gathered.record(transfer)
+        for g in range(len(self.groups)):
+            attend(L - 1, g)
+        logits = self._project(
+            "lm_head", add_rms_norm(self._x, self._delta, model.model.norm.weight, cfg.rms_norm_eps),
+            model.lm_head.weight,
+        )
+        tokens = logits.argmax(-1)
+        st.lengths = [p + 1 for p in positions]
+        self.positions += 1
         return tokens
 
 

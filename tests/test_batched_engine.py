@@ -30,37 +30,39 @@ def tiny(**overrides):
     return DecodeWorkload(**values)
 
 
-def _engine_layers_match_oracle(gpu, wl, transfer_stream=False, steps=3):
+def _engine_layers_match_oracle(gpu, wl, transfer_stream=False, steps=3, **engine_options):
     """Run `steps` decode steps and check every layer of every request against the oracle:
     the state's bounds are the exact extrema of the history read back from the host pool,
     the Quest pages equal the oracle's over those bounds, and the attention output is the
-    oracle's sparse attention over the selected tokens."""
+    oracle's sparse attention over the selected tokens.  With request groups the observer
+    sees one group at a time (``engine.current_group``: its requests and decoder)."""
     from mini_hisparse_amd.batched_engine import BatchedDecodeEngine, build_state, random_model
 
     print(f"[case] {wl.name}: L={wl.layers} hidden={wl.hidden} heads={wl.heads}/{wl.kv_heads} "
-          f"D={wl.head_dim} ffn={wl.ffn} batch={wl.batch} context={wl.context}", flush=True)
+          f"D={wl.head_dim} ffn={wl.ffn} batch={wl.batch} context={wl.context} {engine_options}", flush=True)
     model = random_model(wl, gpu, seed=1)
     state = build_state(wl, gpu, seed=2)
-    engine = BatchedDecodeEngine(model, state, wl.top_pages, transfer_stream=transfer_stream)
+    engine = BatchedDecodeEngine(model, state, wl.top_pages, transfer_stream=transfer_stream, **engine_options)
     L, B, C, P = wl.layers, wl.batch, state.pages, wl.page_size
     Hkv, D = wl.kv_heads, wl.head_dim
     records = []
     tokens = torch.arange(1, B + 1, device=gpu)
     unions = 0
+
+    def observe(l, q, k, v, out):
+        rows, dec = engine.current_group if engine.groups else (range(B), engine.decoder(l))
+        records.append((l, rows, q.clone(), out.clone(), dec.pages.clone(), dec.union_count.clone()))
+
     for step in range(steps):
         records.clear()
-        tokens = engine.step(
-            tokens,
-            lambda l, q, k, v, out: records.append(
-                (l, q.clone(), out.clone(), engine.decoder(l).pages.clone(), engine.decoder(l).union_count.clone())
-            ),
-        )
+        tokens = engine.step(tokens, observe)
         torch.cuda.synchronize()
         length = state.lengths[0]
         count = ceil(length / P)
-        assert len(records) == L
-        for l, q, out, layer_pages, union_count in records:
-            for b in range(B):
+        assert sorted((r[0], r[1].start) for r in records) == sorted(
+            (l, g.start) for l in range(L) for g in ([range(B)] if not engine.groups else [r for r, _ in engine.groups]))
+        for l, rows, q, out, layer_pages, union_count in records:
+            for i, b in enumerate(rows):
                 kv = state.host[l].view(B, C, 2, P, Hkv, D)[b, :count].float()  # [count, 2, P, Hkv, D]
                 keys = kv[:, 0].reshape(count * P, Hkv, D)[:length]
                 vals = kv[:, 1].reshape(count * P, Hkv, D)[:length]
@@ -69,13 +71,13 @@ def _engine_layers_match_oracle(gpu, wl, transfer_stream=False, steps=3):
                 hi = torch.stack([keys[p * P : (p + 1) * P].amax(0) for p in range(count)])
                 torch.testing.assert_close(state.minimum[l, b, :count].float().cpu(), lo, rtol=0, atol=0)
                 torch.testing.assert_close(state.maximum[l, b, :count].float().cpu(), hi, rtol=0, atol=0)
-                pages = oracle.quest_pages(q[b].cpu(), lo, hi, length, P, wl.top_pages)
-                np.testing.assert_array_equal(layer_pages[b, :, : pages.shape[1]].cpu().numpy(), pages)
+                pages = oracle.quest_pages(q[i].cpu(), lo, hi, length, P, wl.top_pages)
+                np.testing.assert_array_equal(layer_pages[i, :, : pages.shape[1]].cpu().numpy(), pages)
                 positions = pages_to_positions(pages, length, P)
-                expected = oracle.selection_oracle(q[b].cpu(), keys, vals, positions)
-                got = out[b].float().cpu().double().numpy()
+                expected = oracle.selection_oracle(q[i].cpu(), keys, vals, positions)
+                got = out[i].float().cpu().double().numpy()
                 assert np.all(np.abs(got - expected) <= 2e-2 + 1e-2 * np.abs(expected)), np.abs(got - expected).max()
-                unions += int(union_count[b])
+                unions += int(union_count[i])
     stats = state.row_stats.tolist()
     assert sum(stats) == unions  # every selected row was a resident hit, a hot hit or a miss
     return stats
@@ -98,19 +100,15 @@ def test_batched_engine_layers_match_oracle(gpu, overrides, transfer_stream):
     assert stats[2] > 0 and stats[0] > 0 and stats[1] > 0
 
 
-def geometry(name, **overrides):
-    """The real layer geometry of a BASELINE model workload (hidden, heads, head_dim,
-    FFN, vocab, page budget, residency, hot rows) with two layers and the given batch
-    and context, for oracle checks of whole engine steps."""
-    from dataclasses import replace
-
-    from mini_hisparse_amd.batched_engine import WORKLOADS
-    from mini_hisparse_amd.selection import union_bound
-
-    wl = replace(WORKLOADS[name], layers=2, steps=8, **overrides)
-    bound = union_bound(wl.context + wl.steps, wl.page_size, wl.top_pages,
-                        1 if wl.selector == "uniform" else wl.heads)
-    return replace(wl, hot_rows=min(wl.hot_rows, 32768, max(2 * bound, bound)))
+@pytest.mark.gpu
+@pytest.mark.parametrize("groups,gather_workgroups", [(2, 0), (3, 24)])
+def test_pipelined_request_groups_match_oracle(gpu, groups, gather_workgroups):
+    """Request groups pipelined across layers (one group's gather on the transfer stream
+    while the compute stream serves the others): every layer of every request still
+    equals the oracle, with uneven groups (5 requests in 3 groups) included."""
+    stats = _engine_layers_match_oracle(gpu, tiny(batch=5), request_groups=groups,
+                                        group_gather_workgroups=gather_workgroups)
+    assert stats[2] > 0 and stats[0] > 0 and stats[1] > 0
 
 
 @pytest.mark.gpu
