@@ -3,9 +3,11 @@
 
 Default workload ("qwen2.5-7b", BASELINE configs[3], the north_star shape): greedy
 decode of a random-init Qwen2.5-7B-shape model (28 layers, hidden 3584, 28 q / 4 kv
-heads, head_dim 128, FFN 18944, bf16) with the layer-major batched engine over
-131,072-token K/V histories, Quest top-64 pages per query head, 15% of pages
-resident, hot_rows 32768.  A step is one decode step of every request through all
+heads, head_dim 128, FFN 18944, bf16) with the layer-major batched engine after a
+prefill of 131,072-token uniformly random prompts through the same model (causal
+SDPA, untimed; every layer's K/V, Quest bounds and resident pages written by
+hs_append_tokens), Quest top-64 pages per query head, 15% of pages resident,
+hot_rows 32768.  A step is one decode step of every request through all
 28 layers: dense layers, append (rows, Quest bounds, host mirror), Quest scorer +
 top-k, device union, resolver, pinned-host -> hot-row gather, group attention.
 `value` = decode tokens/s = batch x steps / wall time of the timed steps.  The
@@ -90,6 +92,9 @@ def parse_args():
     p.add_argument("--group-gather-workgroups", type=int, default=None,
                    help="gather workgroups per request with request groups (0 = the library's default; "
                         "default 24 for qwen2.5-7b)")
+    p.add_argument("--synthetic-history", action="store_true",
+                   help="model workloads: write synthetic K/V histories (N(0,1), 2%% of channels x8) directly "
+                        "instead of prefilling random prompts through the model")
     p.add_argument("--no-cpu-baseline", action="store_true", help="skip the CPU oracle leg")
     p.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU sample work")
     p.add_argument("--attention-sweep", action="store_true",
@@ -688,8 +693,8 @@ TRACE_SUMMARIES = {
 def summarize_trace(trace_dir, args):
     """Per-kernel dispatches and durations over the timed steps of a model workload's
     kernel trace.  Every decode step ends with the greedy argmax over the logits, so the
-    timed region runs from the kernel after the warmup-th argmax to the (warmup +
-    steps)-th argmax; it must hold layers x steps attention launches."""
+    timed region runs from the kernel after the warmup-th decode argmax to the (warmup +
+    steps)-th; it must hold layers x steps x groups attention launches."""
     import csv
     import glob
     from collections import defaultdict
@@ -699,7 +704,9 @@ def summarize_trace(trace_dir, args):
     wl = WORKLOADS[args.workload]
     (path,) = glob.glob(os.path.join(trace_dir, "*kernel_trace.csv"))
     rows = sorted(csv.DictReader(open(path)), key=lambda r: int(r["Start_Timestamp"]))
-    ends = [i for i, r in enumerate(rows) if "ArgMaxOps" in r["Kernel_Name"]]
+    # the prefill's argmaxes (one per prompt) come before the first decode attention
+    first = next(i for i, r in enumerate(rows) if "attend_mfma_kernel" in r["Kernel_Name"])
+    ends = [i for i, r in enumerate(rows) if i > first and "ArgMaxOps" in r["Kernel_Name"]]
     L = wl.layers
     if len(ends) < args.warmup + args.steps:
         raise SystemExit(f"trace holds {len(ends)} decode steps, warmup + steps need {args.warmup + args.steps}")
@@ -878,7 +885,8 @@ def run_model_workload(args, torch, device):
     from dataclasses import replace
 
     from mini_hisparse_amd.batched_engine import (
-        WORKLOADS, BatchedDecodeEngine, build_state, host_bytes_per_request, random_model,
+        WORKLOADS, BatchedDecodeEngine, build_state, empty_state, host_bytes_per_request, random_model,
+        random_prompts,
     )
 
     wl = WORKLOADS[args.workload]
@@ -896,9 +904,19 @@ def run_model_workload(args, torch, device):
     if args.warmup + args.steps + 1 > wl.steps:
         raise SystemExit(f"warmup + steps + 1 profiled step must fit the workload's {wl.steps} decode steps")
     t0 = time.perf_counter()
-    print(f"[bench] {wl.name}: model + synthetic history (batch {wl.batch}, {wl.context} tokens)", file=sys.stderr, flush=True)
+    print(f"[bench] {wl.name}: model + {'synthetic history' if args.synthetic_history else 'prefill'} "
+          f"(batch {wl.batch}, {wl.context} tokens)", file=sys.stderr, flush=True)
     model = random_model(wl, device, seed=args.seed)
-    state = build_state(wl, device, seed=args.seed)
+    first_tokens = None
+    if not args.synthetic_history:
+        state = empty_state(wl, device)
+        print(f"[bench] prefill of {wl.batch} random prompts", file=sys.stderr, flush=True)
+        t_prefill = time.perf_counter()
+        first_tokens = state.prefill(model, random_prompts(wl, device, seed=args.seed), wl.resident_fraction,
+                                     seed=args.seed)
+        prefill_s = time.perf_counter() - t_prefill
+    else:
+        state = build_state(wl, device, seed=args.seed)
     groups = args.request_groups
     if groups is None:
         groups = DEFAULT_REQUEST_GROUPS.get(args.workload, 1)
@@ -911,6 +929,8 @@ def run_model_workload(args, torch, device):
     setup_s = time.perf_counter() - t0
     gen = torch.Generator(device=device).manual_seed(args.seed)
     tokens = torch.randint(0, wl.vocab, (wl.batch,), generator=gen, device=device)
+    if first_tokens is not None:
+        tokens = first_tokens
     for _ in range(args.warmup):
         tokens = engine.step(tokens)
     torch.cuda.synchronize()
@@ -981,8 +1001,11 @@ def run_model_workload(args, torch, device):
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
-        "data": f"synthetic: random-init {wl.name} weights; {wl.context}-token K/V histories (N(0,1), 2% "
-        "channels x8) written directly instead of a prefill; greedy decode from random tokens",
+        "data": (f"synthetic: random-init {wl.name} weights; {wl.context}-token uniformly random prompts "
+                 "prefilled through the model (causal SDPA; K/V, bounds and resident pages written by "
+                 "hs_append_tokens); greedy decode from the prefill's tokens" if not args.synthetic_history else
+                 f"synthetic: random-init {wl.name} weights; {wl.context}-token K/V histories (N(0,1), 2% "
+                 "channels x8) written directly instead of a prefill; greedy decode from random tokens"),
         "config": {
             "workload": f"{wl.name} end to end (layer-major batched engine): {wl.layers} layers, hidden "
             f"{wl.hidden}, {wl.heads} q / {wl.kv_heads} kv heads, head_dim {wl.head_dim}, FFN {wl.ffn}, "
@@ -1023,6 +1046,7 @@ def run_model_workload(args, torch, device):
                    "host_link_memcpy_GBps": link,
                    "frac_host_link": gather_bytes / (stage_ms["gather"] * 1e-3) / 1e9 / link},
         "setup_s": setup_s,
+        "prefill_s": None if args.synthetic_history else prefill_s,
         "hbm_copy_GBps": copy,
     }
     if not args.no_cpu_baseline:

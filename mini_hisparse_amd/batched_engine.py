@@ -36,6 +36,7 @@ import ctypes
 from dataclasses import dataclass
 from math import ceil
 
+import numpy as np
 import torch
 from torch.nn import functional as F
 
@@ -212,20 +213,83 @@ class SparseKVState:
             self.minimum[l, :, used - 1] = keys[:, -1, :tail_valid].amin(1)
             self.maximum[l, :, used - 1] = keys[:, -1, :tail_valid].amax(1)
             host[:, :used].copy_(kv_pages)
-            rng = torch.Generator().manual_seed(seed * 1000003 + l)
             for b in range(B):
-                chosen = torch.randperm(used - 1, generator=rng)[: round(resident_fraction * used)]
-                pages = torch.cat((chosen, torch.tensor([used - 1]))).unique()
-                if self.next_resident + len(pages) > self.first_hot:
-                    raise ValueError("resident pages exceed the reserved resident blocks")
-                blocks = torch.arange(self.next_resident, self.next_resident + len(pages), dtype=torch.int32)
-                self.next_resident += len(pages)
-                self.resident[l, b, pages.to(dev)] = blocks.to(dev)
-                self.pool[blocks.long().to(dev)] = kv_pages[b, pages.to(dev)]
-                self.tail_block[l][b] = int(blocks[-1])
+                pages, blocks = self._place_residents(l, b, used, resident_fraction, seed)
+                self.pool[torch.from_numpy(blocks).to(dev)] = kv_pages[b, torch.from_numpy(pages).to(dev)]
             del kv_pages, keys
         torch.cuda.synchronize(dev)
         self.lengths = [length] * B
+
+    def _place_residents(self, layer, b, used, resident_fraction, seed):
+        """A seeded ``resident_fraction`` of the ``used`` pages of (layer, b), plus its tail
+        page, get resident blocks; returns (pages, blocks) as int64 arrays."""
+        rng = torch.Generator().manual_seed(seed * 1000003 + layer * 65537 + b)
+        chosen = torch.randperm(max(used - 1, 0), generator=rng)[: round(resident_fraction * used)]
+        pages = torch.cat((chosen, torch.tensor([used - 1]))).unique().numpy().astype(np.int64)
+        if self.next_resident + len(pages) > self.first_hot:
+            raise ValueError("resident pages exceed the reserved resident blocks")
+        blocks = np.arange(self.next_resident, self.next_resident + len(pages), dtype=np.int64)
+        self.next_resident += len(pages)
+        self.resident[layer, b, torch.from_numpy(pages).to(self.device)] = torch.from_numpy(blocks).to(
+            self.device, torch.int32)
+        self.tail_block[layer][b] = int(blocks[-1])
+        return pages, blocks
+
+    def write_prompt(self, layer, b, k, v, slots):
+        """The K/V rows ``[T, Hkv, D]`` of request b's prompt at layer ``layer``: every row
+        to its host page, the rows of resident pages (``slots[p] >= 0``) to their blocks,
+        and the exact Quest bounds of every page (``hs_append_tokens``)."""
+        from .row_kernels import append_tokens
+
+        C = self.pages
+        used = len(slots)
+        append_tokens(k, v, 0, 0, [int(x) for x in slots], [b * C + p for p in range(used)], self.pool,
+                      self.alias[layer], self.minimum[layer, b], self.maximum[layer, b], None, self.config)
+
+    @torch.inference_mode()
+    def prefill(self, model, prompts, resident_fraction, seed=0, observer=None):
+        """Run the model over each request's prompt (PyTorch-ROCm causal SDPA, one request
+        at a time) and write every layer's K/V into the state: host pool, a seeded
+        ``resident_fraction`` of the pages plus the tail page in resident blocks, exact
+        Quest bounds.  Returns the greedy first tokens [B] (the prefill's logits).
+        ``observer(layer, b, k, v)`` sees each layer's prompt K/V."""
+        from torch.nn.attention import SDPBackend, sdpa_kernel
+
+        cfg = model.config
+        if len(prompts) != self.batch:
+            raise ValueError(f"expected {self.batch} prompts")
+        groups = cfg.num_attention_heads // cfg.num_key_value_heads
+        P = self.config.page_size
+        firsts, lengths = [], []
+        for b, prompt in enumerate(prompts):
+            tokens = torch.as_tensor(prompt, device=self.device)
+            used = ceil(len(tokens) / P)
+            if len(tokens) > self.pages * P:
+                raise ValueError("prompt longer than the state's capacity")
+            slots = []
+            for l in range(self.layers):
+                pages, blocks = self._place_residents(l, b, used, resident_fraction, seed)
+                row = np.full(used, -1, np.int64)
+                row[pages] = blocks
+                slots.append(row)
+
+            def attend(index, q, k, v):
+                self.write_prompt(index, b, k, v, slots[index])
+                if observer is not None:
+                    observer(index, b, k, v)
+                # [1, heads, tokens, dim]: the fused kernels take 4-D operands only
+                heads_first = lambda t: t.transpose(0, 1).unsqueeze(0).contiguous()  # noqa: E731
+                grouped = lambda t: heads_first(t.repeat_interleave(groups, 1))  # noqa: E731
+                with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
+                    out = F.scaled_dot_product_attention(heads_first(q), grouped(k), grouped(v), is_causal=True)
+                return out[0].transpose(0, 1)
+
+            hidden = model._layers(tokens, 0, attend)
+            firsts.append(model._logits(hidden[-1]).argmax())
+            lengths.append(len(tokens))
+        torch.cuda.synchronize(self.device)
+        self.lengths = lengths
+        return torch.stack(firsts)
 
     # -- decode-step bookkeeping ---------------------------------------------------
     def open_tail_pages(self, positions):
@@ -782,6 +846,28 @@ def host_bytes_per_request(workload: DecodeWorkload, context=None, steps=None):
     pages = ceil((context + steps) / workload.page_size)
     element = torch.empty((), dtype=workload.dtype).element_size()
     return workload.layers * pages * 2 * workload.page_size * workload.kv_heads * workload.head_dim * element
+
+
+def empty_state(workload: DecodeWorkload, device, context=None, steps=None):
+    """A state sized for `context` history tokens plus `steps` decoded ones, no history yet."""
+    context = workload.context if context is None else context
+    steps = workload.steps if steps is None else steps
+    P = workload.page_size
+    cfg = CacheConfig(
+        gpu_pages=1, host_pages=1, page_size=P, kv_heads=workload.kv_heads, head_dim=workload.head_dim,
+        device=str(device), dtype=workload.dtype,
+    )
+    used = ceil(context / P)
+    resident = workload.layers * workload.batch * (round(workload.resident_fraction * used) + 1)
+    spare = workload.layers * workload.batch * (ceil(steps / P) + 1)
+    return SparseKVState(workload.layers, workload.batch, context + steps, cfg, workload.hot_rows, resident, spare)
+
+
+def random_prompts(workload: DecodeWorkload, device, seed=0, context=None):
+    """Uniformly random token ids: [batch, context] (the configs' random prompts)."""
+    context = workload.context if context is None else context
+    gen = torch.Generator(device=device).manual_seed(seed)
+    return torch.randint(0, workload.vocab, (workload.batch, context), generator=gen, device=device)
 
 
 def build_state(workload: DecodeWorkload, device, seed=0, context=None, steps=None):

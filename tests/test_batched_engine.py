@@ -30,7 +30,7 @@ def tiny(**overrides):
     return DecodeWorkload(**values)
 
 
-def _engine_layers_match_oracle(gpu, wl, transfer_stream=False, steps=3, **engine_options):
+def _engine_layers_match_oracle(gpu, wl, transfer_stream=False, steps=3, built=None, **engine_options):
     """Run `steps` decode steps and check every layer of every request against the oracle:
     the state's bounds are the exact extrema of the history read back from the host pool,
     the Quest pages equal the oracle's over those bounds, and the attention output is the
@@ -40,13 +40,16 @@ def _engine_layers_match_oracle(gpu, wl, transfer_stream=False, steps=3, **engin
 
     print(f"[case] {wl.name}: L={wl.layers} hidden={wl.hidden} heads={wl.heads}/{wl.kv_heads} "
           f"D={wl.head_dim} ffn={wl.ffn} batch={wl.batch} context={wl.context} {engine_options}", flush=True)
-    model = random_model(wl, gpu, seed=1)
-    state = build_state(wl, gpu, seed=2)
+    if built is None:
+        model, state, tokens = random_model(wl, gpu, seed=1), build_state(wl, gpu, seed=2), None
+    else:
+        model, state, tokens = built
     engine = BatchedDecodeEngine(model, state, wl.top_pages, transfer_stream=transfer_stream, **engine_options)
     L, B, C, P = wl.layers, wl.batch, state.pages, wl.page_size
     Hkv, D = wl.kv_heads, wl.head_dim
     records = []
-    tokens = torch.arange(1, B + 1, device=gpu)
+    if tokens is None:
+        tokens = torch.arange(1, B + 1, device=gpu)
     unions = 0
 
     def observe(l, q, k, v, out):
@@ -109,6 +112,63 @@ def test_pipelined_request_groups_match_oracle(gpu, groups, gather_workgroups):
     stats = _engine_layers_match_oracle(gpu, tiny(batch=5), request_groups=groups,
                                         group_gather_workgroups=gather_workgroups)
     assert stats[2] > 0 and stats[0] > 0 and stats[1] > 0
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("resident_fraction", [0.3, 0.0])
+def test_prefill_writes_history_bounds_and_residents_then_decodes(gpu, resident_fraction):
+    """The engine's prefill runs the model over random prompts and writes every layer's
+    K/V with the batched write kernel: the host pool holds exactly the model's K/V, the
+    bounds are the exact extrema of each page (bit for bit), resident pages hold their
+    host rows, the first tokens are the model's own prefill tokens; decoding then matches
+    the oracle layer by layer."""
+    from mini_hisparse_amd.batched_engine import empty_state, random_model, random_prompts
+
+    wl = tiny(resident_fraction=resident_fraction, context=9 * 16 + 5)
+    model = random_model(wl, gpu, seed=1)
+    state = empty_state(wl, gpu)
+    prompts = random_prompts(wl, gpu, seed=3)
+    written = {}
+    firsts = state.prefill(model, prompts, wl.resident_fraction, seed=4,
+                           observer=lambda l, b, k, v: written.__setitem__((l, b), (k.clone(), v.clone())))
+    torch.cuda.synchronize()
+    B, C, P, Hkv, D = wl.batch, state.pages, wl.page_size, wl.kv_heads, wl.head_dim
+    length = wl.context
+    count = ceil(length / P)
+    assert state.lengths == [length] * B
+    for b in range(B):
+        assert int(firsts[b]) == int(model.prefill(prompts[b].tolist()).argmax())
+        for l in range(wl.layers):
+            k, v = written[l, b]
+            host = state.host[l].view(B, C, 2, P, Hkv, D)[b, :count]
+            keys = host[:, 0].reshape(count * P, Hkv, D)[:length]
+            vals = host[:, 1].reshape(count * P, Hkv, D)[:length]
+            assert torch.equal(keys, k.cpu()) and torch.equal(vals, v.cpu())
+            lo = torch.stack([keys[p * P : (p + 1) * P].amin(0) for p in range(count)])
+            hi = torch.stack([keys[p * P : (p + 1) * P].amax(0) for p in range(count)])
+            assert torch.equal(state.minimum[l, b, :count].cpu(), lo)
+            assert torch.equal(state.maximum[l, b, :count].cpu(), hi)
+            resident = state.resident[l, b, :count].cpu()
+            assert resident[count - 1] >= 0  # the tail page is resident
+            for p in torch.nonzero(resident >= 0).flatten().tolist():
+                rows = min(P, length - p * P)
+                assert torch.equal(state.pool[int(resident[p]), :, :rows].cpu(), host[p, :, :rows])
+    _engine_layers_match_oracle(gpu, wl, built=(model, state, firsts))
+
+
+def geometry(name, **overrides):
+    """The real layer geometry of a BASELINE model workload (hidden, heads, head_dim,
+    FFN, vocab, page budget, residency, hot rows) with two layers and the given batch
+    and context, for oracle checks of whole engine steps."""
+    from dataclasses import replace
+
+    from mini_hisparse_amd.batched_engine import WORKLOADS
+    from mini_hisparse_amd.selection import union_bound
+
+    wl = replace(WORKLOADS[name], layers=2, steps=8, **overrides)
+    bound = union_bound(wl.context + wl.steps, wl.page_size, wl.top_pages,
+                        1 if wl.selector == "uniform" else wl.heads)
+    return replace(wl, hot_rows=min(wl.hot_rows, 32768, max(2 * bound, bound)))
 
 
 @pytest.mark.gpu
