@@ -649,12 +649,14 @@ def summarize_pmc(fetch_dir, write_dir, workload="microbench"):
 
     fetch, write = load(fetch_dir, "FETCH_SIZE"), load(write_dir, "WRITE_SIZE")
     kib = CALIBRATION_BYTES / 1024
-    calib = [i for i, (name, v) in write.items() if "copyBuffer" in name and abs(v - kib) < 0.01 * kib
-             and i in fetch and abs(fetch[i][1] - kib) < 0.6 * kib]
-    if not calib:
+    # the two runs need not number their dispatches alike: find the copy in each on its own
+    calib_write = [v for name, v in write.values() if "copyBuffer" in name and abs(v - kib) < 0.01 * kib]
+    calib_fetch = [v for name, v in fetch.values() if "copyBuffer" in name and abs(v - kib) < 0.6 * kib]
+    if not calib_write or not calib_fetch:
         raise SystemExit("no 1 GiB device copy found in the counter runs")
-    fetch_scale = kib / float(np.mean([fetch[i][1] for i in calib]))
-    write_scale = kib / float(np.mean([write[i][1] for i in calib]))
+    calib = calib_write
+    fetch_scale = kib / float(np.mean(calib_fetch))
+    write_scale = kib / float(np.mean(calib_write))
     per = defaultdict(lambda: [[], []])
     for i, (name, v) in fetch.items():
         if "hs::" in name:
