@@ -404,8 +404,11 @@ int hs_skinny_gemm_tiled(const void* x, int64_t x_stride, const void* weight_til
  * The MLP's gate and up projections with the SiLU gate applied on the way out:
  * out[rows, ffn] = silu(x . Wg^T) * (x . Wu^T), each projection rounded to the
  * dtype, then SiLU rounded, then the product -- the arithmetic of
- * hs_skinny_gemm_tiled on the packed gate|up weight followed by hs_silu_mul,
- * with the same bits.  gate_up_tiles: 2 * ceil(ffn/16) blocks-of-tiles in
+ * hs_skinny_gemm_tiled on the packed gate|up weight followed by hs_silu_mul.
+ * The bits are the same whenever that GEMM's plan for (rows, 2 * ffn, k) is one
+ * K slice (hs_skinny_gemm_workspace_bytes at its minimum, 256) with rounds of 8
+ * k-steps (HS_GEMM_GU unset); where it plans split-K the sums differ only in
+ * fp32 summation order.  gate_up_tiles: 2 * ceil(ffn/16) blocks-of-tiles in
  * hs_skinny_gemm_tiled's format, the gate's tile i at position 2i and the up
  * projection's tile i at 2i + 1 (rows past ffn zero).  No workspace (one K
  * slice).  No reference counterpart (replaces two launches of the batched

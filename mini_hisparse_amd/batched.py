@@ -164,11 +164,21 @@ class BatchedSparseDecode:
         )
         self._build_union(s)
 
-    def select_pages(self, pages, stream=None):
+    def select_pages(self, pages, stream=None, validate=True):
         """A selection given as pages: ``pages`` [B, top] int32 on the device, ascending
-        and distinct, min(top, count) of them per request, read by every head."""
+        and distinct, min(top, count) of them per request with the tail page last,
+        read by every head.  ``validate`` checks that on the host (a device-to-host
+        copy); a caller that builds its pages that way itself may skip it."""
         if pages.shape != (self.batch, self.top) or pages.dtype != torch.int32:
             raise ValueError(f"pages must be int32 [{self.batch}, {self.top}]")
+        if validate:
+            host = pages.cpu()
+            for b, count in enumerate(self.counts):
+                k = min(self.top, count)
+                row = host[b, :k]
+                if ((row < 0) | (row >= count)).any() or (row[1:] <= row[:-1]).any() or row[-1] != count - 1:
+                    raise ValueError(f"request {b}: pages must be {k} ascending distinct pages below {count}, "
+                                     f"the tail page {count - 1} last")
         s = stream.cuda_stream if stream is not None else _lib.stream_handle(self.device)
         self.pages.copy_(pages[:, None, :].expand(self.batch, self.heads, self.top))
         self._build_union(s)
@@ -185,6 +195,15 @@ class BatchedSparseDecode:
             ),
             "hs_build_union",
         )
+
+    def check_status(self):
+        """Raise if a union of any step so far overflowed its buffers (the union builder's
+        status bits: 1 = union positions, 2 = group entries; both are truncated then).
+        Reads the flag back to the host."""
+        bits = int(self.status.item())
+        if bits:
+            what = [name for bit, name in ((1, "union positions"), (2, "group entries")) if bits & bit]
+            raise RuntimeError(f"union overflow ({' and '.join(what)} over capacity): the selection was truncated")
 
     def _resolve_descs(self, tables):
         """Resolver descriptors of one set of B tables, built once: the workspace is sized

@@ -43,8 +43,8 @@ from torch.nn import functional as F
 from . import _lib
 from .batched import BatchedSparseDecode, LayerTablesView
 from .dense import (
-    add_rms_norm, linear_supported, linear_swiglu_tiled, linear_tiled, rotary_split, silu_mul, tile_gate_up,
-    tile_weight,
+    add_rms_norm, gemm_workspace_bytes, linear_supported, linear_swiglu_tiled, linear_tiled, rotary_split, silu_mul,
+    tile_gate_up, tile_weight,
 )
 from .config import CacheConfig
 from .model import MiniModel, ModelConfig
@@ -444,7 +444,7 @@ class BatchedDecodeEngine:
         st, dec = self.state, self.decs[index]
         with torch.cuda.stream(transfer):
             m = {"select": [mark(transfer)]}
-            dec.select_pages(sampled[index])
+            dec.select_pages(sampled[index], validate=False)  # uniform_pages: ascending, tail last
             m["select"].append(mark(transfer))
             m["resolve"] = [m["select"][1]]
             dec.resolve(st.tables[index], row_stats=st.row_stats)
@@ -493,7 +493,7 @@ class BatchedDecodeEngine:
         if self.projection_kernel["gate_up"]:  # gate|up and the SiLU gate in one launch
             act = linear_swiglu_tiled(h, self._tiles[gate_up_w.data_ptr()], cfg.intermediate_size,
                                       out=self._act[rows])
-        else:
+        else:  # PyTorch's GEMM, then the SiLU gate
             act = silu_mul(self._project("gate_up", h, gate_up_w, out=self._gate_up[rows]), out=self._act[rows])
         self._project("down", act, layer.mlp.down_proj.weight, out=self._delta[rows])
 
@@ -556,8 +556,13 @@ class BatchedDecodeEngine:
         """Per projection, the faster of the skinny-GEMM kernel on tile-major weights
         (hs_skinny_gemm_tiled) and PyTorch's GEMM at this batch, timed over the layers'
         own weights (each call reads another layer's weight from HBM, as in a step).
-        Each projection the kernel serves keeps a tile-major copy of its weights
-        (the model's row-major parameters stay as they are)."""
+        For gate|up the kernel is the fused launch with the SiLU gate
+        (hs_skinny_gemm_swiglu_tiled) and PyTorch's side is its GEMM followed by
+        hs_silu_mul: the two ways the step can run.  Each projection the kernel serves
+        keeps a tile-major copy of its weights (the model's row-major parameters stay as
+        they are).  The split-K partials of every kernel call go to one workspace owned
+        by the engine, sized for the largest plan, so captured graphs keep a buffer
+        that lives as long as they do."""
         B, dev, dt = self.state.batch, self.device, self.model.dtype
         layers = self.model.model.layers
         groups = {
@@ -569,6 +574,11 @@ class BatchedDecodeEngine:
         }
         self.projection_kernel = {}
         self._tiles = {}  # data_ptr of a row-major weight -> its tile-major copy
+        ffn = self.model.config.intermediate_size
+        row_counts = {B} | ({len(rows) for rows, _ in self.groups} if self.groups else set())
+        ws_bytes = max(gemm_workspace_bytes(r, w.shape[0], w.shape[1]) for r in row_counts
+                       for weights in groups.values() for w, _ in weights[:1])
+        self._gemm_ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
         for name, weights in groups.items():
             x = torch.full((B, weights[0][0].shape[1]), 0.01, dtype=dt, device=dev)
             if not linear_supported(x, weights[0][0]):
@@ -576,13 +586,19 @@ class BatchedDecodeEngine:
                 continue
             for w, _ in weights:
                 if w.data_ptr() not in self._tiles:
-                    self._tiles[w.data_ptr()] = tile_weight(w)
+                    self._tiles[w.data_ptr()] = tile_gate_up(w, ffn) if name == "gate_up" else tile_weight(w)
             if mode != "auto":
                 chosen = mode == "kernel"
             else:
-                kernel = lambda x, w, b: linear_tiled(x, self._tiles[w.data_ptr()], w.shape[0], b)
+                if name == "gate_up":
+                    kernel = lambda x, w, b: linear_swiglu_tiled(x, self._tiles[w.data_ptr()], ffn)  # noqa: E731
+                    reference = lambda x, w, b: silu_mul(F.linear(x, w, b))  # noqa: E731
+                else:
+                    kernel = lambda x, w, b: linear_tiled(  # noqa: E731
+                        x, self._tiles[w.data_ptr()], w.shape[0], b, workspace=self._gemm_ws)
+                    reference = F.linear
                 elapsed = {}
-                for label, fn in (("kernel", kernel), ("torch", F.linear)):
+                for label, fn in (("kernel", kernel), ("torch", reference)):
                     fn(x, *weights[0])
                     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
                     start.record()
@@ -596,14 +612,11 @@ class BatchedDecodeEngine:
             if not chosen:
                 for w, _ in weights:
                     self._tiles.pop(w.data_ptr(), None)
-            elif name == "gate_up":  # the fused SiLU launch reads gate and up tiles interleaved
-                ffn = self.model.config.intermediate_size
-                for w, _ in weights:
-                    self._tiles[w.data_ptr()] = tile_gate_up(w, ffn)
 
     def _project(self, name, x, weight, bias=None, out=None):
         if self.projection_kernel[name]:
-            return linear_tiled(x, self._tiles[weight.data_ptr()], weight.shape[0], bias, out=out)
+            return linear_tiled(x, self._tiles[weight.data_ptr()], weight.shape[0], bias, out=out,
+                                workspace=self._gemm_ws)
         y = F.linear(x, weight, bias)
         if out is None:
             return y
@@ -624,6 +637,13 @@ class BatchedDecodeEngine:
             ),
             "hs_append_rows",
         )
+
+    def check_status(self):
+        """Raise if any layer's union overflowed its buffers in a step so far (reads the
+        decoders' status flags back to the host: for tests and debugging, not timed runs)."""
+        decoders = [self.dec] + (self.decs or []) + [group for _, group in (self.groups or [])]
+        for dec in {id(d): d for d in decoders}.values():
+            dec.check_status()
 
     @torch.inference_mode()
     def step(self, tokens, observer=None, timer=None, probe=None):
@@ -696,7 +716,7 @@ class BatchedDecodeEngine:
                 if sampled is None:
                     dec.select(q, lo, hi)
                 else:
-                    dec.select_pages(sampled[index])
+                    dec.select_pages(sampled[index], validate=False)  # uniform_pages: ascending, tail last
                 marks["select"].append(mark(compute))
                 marks["resolve"] = [marks["select"][1]]
                 dec.resolve(st.tables[index], row_stats=st.row_stats)

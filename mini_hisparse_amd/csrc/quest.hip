@@ -781,11 +781,24 @@ extern "C" int hs_quest_topk(const void* query, int64_t q_stride_b, int64_t q_st
                              int64_t workspace_bytes, hipStream_t stream) {
   HS_CHECK_ARG(batch >= 1, "quest batch must be positive");
   HS_CHECK_ARG(valid_dtype(query_dtype), "invalid query dtype code %d", query_dtype);
+  HS_CHECK_ARG(valid_dtype(kv_dtype), "invalid dtype code %d", kv_dtype);
+  HS_CHECK_ARG(top >= 1 && heads >= 1 && kv_heads >= 1 && heads % kv_heads == 0,
+               "invalid page budget or GQA shape");
+  HS_CHECK_ARG(head_dim >= 1 && head_dim <= 1024, "invalid head_dim");
   HS_CHECK_ARG(query && minimum && maximum && page_counts && out_pages, "null quest pointer");
-  // every request is checked before the first launch, so an invalid one launches nothing
+  // every request and every chunk's workspace need are checked before the first
+  // launch, so an invalid call launches nothing
   for (int64_t i = 0; i < batch; ++i) {
     HS_CHECK_ARG(page_counts[i] >= 1, "cannot select pages of an empty history");
     HS_CHECK_ARG(minimum[i] && maximum[i], "null bounds pointer");
+  }
+  for (int64_t s0 = 0; s0 < batch; s0 += QMAXB) {
+    const int64_t n = batch - s0 < QMAXB ? batch - s0 : QMAXB;
+    int64_t cmax = 1;
+    for (int64_t i = s0; i < s0 + n; ++i) cmax = page_counts[i] > cmax ? page_counts[i] : cmax;
+    const int64_t need = hs_quest_workspace_bytes(n, heads, cmax);
+    HS_CHECK_ARG(workspace && workspace_bytes >= need, "quest workspace too small: need %lld bytes",
+                 static_cast<long long>(need));
   }
   const int64_t qbytes = query_dtype == HS_DTYPE_F32 ? 4 : 2;
   // chunks run in stream order and each reuses the workspace, which holds the
@@ -811,6 +824,7 @@ extern "C" int hs_build_union(const int32_t* pages, int64_t p_stride_b, int64_t 
                               int32_t* entry_counts, int32_t* status, hipStream_t stream) {
   HS_CHECK_ARG(batch >= 1, "union batch must be positive");
   HS_CHECK_ARG(top >= 1 && page_size >= 1 && lengths, "invalid union shape");
+  HS_CHECK_ARG(heads >= 1 && kv_heads >= 1 && heads % kv_heads == 0, "invalid GQA shape");
   for (int64_t i = 0; i < batch; ++i) {  // every request, before the first launch
     HS_CHECK_ARG(lengths[i] >= 1, "cannot build a union over an empty history");
     HS_CHECK_ARG(ceil_div(lengths[i], page_size) <= UMAXPAGES, "too many pages for the union builder");

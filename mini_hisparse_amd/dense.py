@@ -26,7 +26,22 @@ _WORKSPACE = {}
 _GEMM_WS_BYTES = {}
 
 
-def _workspace(device, stream, nbytes):
+def gemm_workspace_bytes(rows, n, k):
+    """Bytes of split-K partials ``linear``/``linear_tiled`` need for [rows, k] x [n, k]."""
+    nbytes = _GEMM_WS_BYTES.get((rows, n, k))
+    if nbytes is None:
+        nbytes = _GEMM_WS_BYTES[(rows, n, k)] = _lib.load().hs_skinny_gemm_workspace_bytes(rows, n, k)
+    return nbytes
+
+
+def _workspace(device, stream, nbytes, given):
+    """``given`` when the caller owns the workspace (it must hold ``nbytes``); else a
+    module buffer per (device, stream), for eager calls only: a captured graph keeps
+    the address of the buffer it saw, which a later, larger call would replace."""
+    if given is not None:
+        if given.dtype != torch.uint8 or given.device != torch.device(device) or given.numel() < nbytes:
+            raise ValueError(f"GEMM workspace must be uint8 on {device} with at least {nbytes} bytes")
+        return given
     key = (device, stream)
     ws = _WORKSPACE.get(key)
     if ws is None or ws.numel() < nbytes:
@@ -58,8 +73,10 @@ def linear_supported(x, weight):
     )
 
 
-def linear(x, weight, bias=None, out=None):
-    """``x @ weight.T + bias`` for ``x`` [rows <= 16, K] (F.linear's arguments)."""
+def linear(x, weight, bias=None, out=None, workspace=None):
+    """``x @ weight.T + bias`` for ``x`` [rows <= 16, K] (F.linear's arguments).
+    ``workspace`` (uint8, :func:`gemm_workspace_bytes`) holds the split-K partials; a
+    caller that captures the call in a graph passes its own."""
     if not linear_supported(x, weight):
         raise ValueError("linear takes 1-16 rows of a bf16/f16 x with K a multiple of 32 and a contiguous weight")
     if bias is not None and (bias.shape != (weight.shape[0],) or bias.dtype != x.dtype or not bias.is_contiguous()):
@@ -70,10 +87,7 @@ def linear(x, weight, bias=None, out=None):
     y = torch.empty((rows, n), dtype=x.dtype, device=x.device) if out is None else out
     lib = _lib.load()
     stream = _stream(x)
-    nbytes = _GEMM_WS_BYTES.get((rows, n, k))
-    if nbytes is None:
-        nbytes = _GEMM_WS_BYTES[(rows, n, k)] = lib.hs_skinny_gemm_workspace_bytes(rows, n, k)
-    ws = _workspace(x.device, stream, nbytes)
+    ws = _workspace(x.device, stream, gemm_workspace_bytes(rows, n, k), workspace)
     _lib.check(
         lib.hs_skinny_gemm(
             x.data_ptr(), x.stride(0), weight.data_ptr(), n, k, _lib.ptr(bias), y.data_ptr(), y.stride(0), rows,
@@ -95,7 +109,7 @@ def tile_weight(weight):
     return padded.reshape(rows // 16, 16, k // 32, 32).transpose(1, 2).contiguous()
 
 
-def linear_tiled(x, tiles, n, bias=None, out=None):
+def linear_tiled(x, tiles, n, bias=None, out=None, workspace=None):
     """:func:`linear` with the weight as :func:`tile_weight` packed it (``n`` its rows):
     the same arithmetic in the same order, so the same bits."""
     k = x.shape[1] if x.dim() == 2 else -1
@@ -113,10 +127,7 @@ def linear_tiled(x, tiles, n, bias=None, out=None):
     y = torch.empty((rows, n), dtype=x.dtype, device=x.device) if out is None else out
     lib = _lib.load()
     stream = _stream(x)
-    nbytes = _GEMM_WS_BYTES.get((rows, n, k))
-    if nbytes is None:
-        nbytes = _GEMM_WS_BYTES[(rows, n, k)] = lib.hs_skinny_gemm_workspace_bytes(rows, n, k)
-    ws = _workspace(x.device, stream, nbytes)
+    ws = _workspace(x.device, stream, gemm_workspace_bytes(rows, n, k), workspace)
     _lib.check(
         lib.hs_skinny_gemm_tiled(
             x.data_ptr(), x.stride(0), tiles.data_ptr(), n, k, _lib.ptr(bias), y.data_ptr(), y.stride(0), rows,
@@ -137,8 +148,12 @@ def tile_gate_up(gate_up, ffn):
 
 
 def linear_swiglu_tiled(x, tiles, ffn, out=None):
-    """``silu(x @ gate.T) * (x @ up.T)`` from :func:`tile_gate_up`'s packing: the bits of
-    :func:`linear_tiled` on the packed weight followed by :func:`silu_mul`, in one launch."""
+    """``silu(x @ gate.T) * (x @ up.T)`` from :func:`tile_gate_up`'s packing, in one launch
+    with one K slice.  It has the bits of :func:`linear_tiled` on the packed weight
+    followed by :func:`silu_mul` whenever that GEMM also runs in one K slice
+    (``gemm_workspace_bytes(rows, 2 * ffn, K)`` at its minimum of 256, with the default
+    rounds of 8 k-steps); where the GEMM plans split-K (few output rows, long K) the
+    sums are the same up to fp32 summation order."""
     k = x.shape[1] if x.dim() == 2 else -1
     if not (
         x.dim() == 2 and 1 <= x.shape[0] <= 16 and k % 32 == 0 and k > 0 and ffn >= 1

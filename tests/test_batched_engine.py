@@ -81,6 +81,7 @@ def _engine_layers_match_oracle(gpu, wl, transfer_stream=False, steps=3, built=N
                 got = out[i].float().cpu().double().numpy()
                 assert np.all(np.abs(got - expected) <= 2e-2 + 1e-2 * np.abs(expected)), np.abs(got - expected).max()
                 unions += int(union_count[i])
+    engine.check_status()  # no union or entry list was truncated
     stats = state.row_stats.tolist()
     assert sum(stats) == unions  # every selected row was a resident hit, a hot hit or a miss
     return stats

@@ -103,7 +103,7 @@ def _run_layer(gpu, *, B, Hkv, g, D, pages, length, top, hot_rows, resident_frac
         dec.gather(alias, pool, torch.cuda.current_stream(dev))
         out = dec.attend(q.to(dev), pool)
         torch.cuda.synchronize()
-        assert int(dec.status.item()) == 0, "union or entry capacity overflow"
+        dec.check_status()  # no union or entry capacity overflow
         for b in range(B):
             t = tables_np[b]
             if selector == "quest":

@@ -125,20 +125,28 @@ def test_linear_matches_an_fp32_reference(gpu, dtype, rows, n, k, bias):
 @pytest.mark.gpu
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("rows", [1, 3, 16])
-@pytest.mark.parametrize("ffn,k", [(4864, 896), (18944, 3584), (37, 64), (1000, 256)])
+@pytest.mark.parametrize("ffn,k", [(4864, 896), (18944, 3584), (37, 64), (1000, 256), (1000, 4096)])
 def test_swiglu_gemm_equals_gemm_then_silu_mul(gpu, dtype, rows, ffn, k):
     """One launch of gate|up with the SiLU gate gives the bits of the tiled GEMM on the packed
-    weight followed by hs_silu_mul (ffn not a multiple of 16 included)."""
-    from mini_hisparse_amd.dense import linear_swiglu_tiled, linear_tiled, silu_mul, tile_gate_up, tile_weight
+    weight followed by hs_silu_mul (ffn not a multiple of 16 included) whenever that GEMM
+    runs in one K slice; (1000, 4096) makes it plan split-K, and there both stay within the
+    fp32 reference's tolerance."""
+    from mini_hisparse_amd.dense import (
+        gemm_workspace_bytes, linear_swiglu_tiled, linear_tiled, silu_mul, tile_gate_up, tile_weight,
+    )
 
     gen = torch.Generator(device=gpu).manual_seed(rows + ffn + k)
     x = torch.randn(rows, k, generator=gen, device=gpu).to(dtype)
     w = (torch.randn(2 * ffn, k, generator=gen, device=gpu) / k**0.5).to(dtype)
     want = silu_mul(linear_tiled(x, tile_weight(w), 2 * ffn))
     got = linear_swiglu_tiled(x, tile_gate_up(w, ffn), ffn)
-    assert torch.equal(got, want)
+    split_k = gemm_workspace_bytes(rows, 2 * ffn, k) > 256
+    assert split_k == (k == 4096)
+    if not split_k:
+        assert torch.equal(got, want)
     ref = torch.nn.functional.silu(x.float() @ w[:ffn].float().T) * (x.float() @ w[ffn:].float().T)
     assert ((got.float() - ref).abs() <= 0.02 + 0.02 * ref.abs()).all()
+    assert ((want.float() - ref).abs() <= 0.02 + 0.02 * ref.abs()).all()
 
 
 def test_tile_gate_up_interleaves_the_two_projections():
@@ -182,3 +190,22 @@ def test_linear_reads_strided_rows_and_rejects_unsupported_shapes(gpu):
         linear(torch.zeros(17, 256, dtype=torch.bfloat16, device=gpu), w)
     with pytest.raises(ValueError):
         linear(torch.zeros(2, 100, dtype=torch.bfloat16, device=gpu), torch.zeros(8, 100, dtype=torch.bfloat16, device=gpu))
+
+
+@pytest.mark.gpu
+def test_split_k_partials_in_a_caller_workspace(gpu):
+    """A split-K plan (1000 outputs, K 4096) writes its partials to the caller's workspace
+    when given one: the same bits as the module buffer, and a short workspace is refused
+    before anything is launched."""
+    from mini_hisparse_amd.dense import gemm_workspace_bytes, linear_tiled, tile_weight
+
+    gen = torch.Generator(device=gpu).manual_seed(5)
+    x = torch.randn(2, 4096, generator=gen, device=gpu).to(torch.bfloat16)
+    w = (torch.randn(1000, 4096, generator=gen, device=gpu) / 64).to(torch.bfloat16)
+    tiles = tile_weight(w)
+    need = gemm_workspace_bytes(2, 1000, 4096)
+    assert need > 256  # split-K
+    own = torch.empty(need, dtype=torch.uint8, device=gpu)
+    assert torch.equal(linear_tiled(x, tiles, 1000, workspace=own), linear_tiled(x, tiles, 1000))
+    with pytest.raises(ValueError, match="workspace"):
+        linear_tiled(x, tiles, 1000, workspace=own[: need - 1])
