@@ -278,7 +278,13 @@ int hs_append_tokens(const void* k, const void* v, int64_t kv_stride_t, int64_t 
 
 /* ------------------------------------------------------------ (4) attention */
 
-/* Scratch bytes of one attention call (split-K partials). */
+/*
+ * Scratch bytes of one attention call: split-K partials and, for the MFMA kernel's
+ * in-kernel merge, one arrival counter per (request, KV head, head chunk).  The
+ * workspace may hold anything before a call (counters carry a per-launch tag; a
+ * value with another tag counts as empty) and calls that share it must run in
+ * order (one stream).
+ */
 int64_t hs_attend_workspace_bytes(int32_t dtype, int64_t batch, int64_t heads, int64_t kv_heads,
                                   int64_t head_dim, int64_t max_entries);
 

@@ -22,12 +22,20 @@
 //
 // bf16 / fp16 pools use MFMA (v_mfma_f32_16x16x32_{bf16,f16}): S^T = K Q^T
 // with the group's query heads as the N dimension (padded to 16), then
-// O^T += V^T P^T with V staged through LDS.  fp32 pools (and head dims not a
-// multiple of 8) use a VALU kernel with the same entry sources.  Both write
-// split-K partials (m, l, acc) that `attend_merge_kernel` combines.
+// O^T += V^T P^T with V staged through LDS.  fp32 pools (and head dims other
+// than 32, 64, 128 and 256) use a VALU kernel with the same entry sources.  Both write
+// split-K partials (m, l, acc).  The MFMA kernel combines them itself: the
+// workgroup that finishes a (request, KV head, head chunk) last -- found with an
+// arrival counter per group -- merges the group's partials and writes the
+// output, so the launch needs no second kernel.  The VALU kernel and the
+// window attention (which returns the unnormalised state) use
+// `attend_merge_kernel`; both merges run the same arithmetic.
 #include <float.h>
 #include <stdlib.h>
 #include <math.h>
+
+#include <atomic>
+#include <chrono>
 
 #include "hs_common.h"
 
@@ -59,6 +67,13 @@ struct AttendArgs {
   float* part_l;  // like part_m
   float* part_o;  // [B, Hq, splits, D], or [slots, 16, D] when scheduled
   int32_t* sched; // T(0 .. B * Hkv) of the scheduled group kernel
+  // in-kernel merge (fuse != 0): one arrival counter per (request, KV head, head
+  // chunk), [B * Hkv * head_chunks]; `epoch` tags this launch's arrivals
+  unsigned long long* arrivals;
+  unsigned long long epoch;
+  int fuse;
+  void* out;
+  int64_t o_sb, o_sh;
   const int32_t* wslots;       // WINDOW: device slot of each page [wn]
   const int32_t* wlens;        // WINDOW: valid tokens of each page [wn]
   const unsigned char* wmask;  // WINDOW: [Hq, wn, P] token mask, or null (every token)
@@ -147,6 +162,81 @@ template <int DT>
 __device__ __forceinline__ float from_bits(unsigned short v) {
   if constexpr (DT == HS_DTYPE_BF16) return bf16_bits_to_f32(v);
   else return f16_bits_to_f32(v);
+}
+
+// Combine n split-K partials (m, l, acc[d]) of one head, partial u at
+// base + u * stride.  Partials are read MS at a time, every load issued before
+// any is used (one round of loads per MS partials); chunks after the first
+// rescale the running sums, so for n <= MS the arithmetic is a plain max, then
+// sums in partial order.  Returns the unnormalised (M, L, O).
+// COHERENT reads at device scope (partials other workgroups of the running
+// launch wrote, possibly on another XCD, whose L2 is not this one's).
+template <bool COHERENT>
+__device__ __forceinline__ float partial_at(const float* p) {
+  if constexpr (COHERENT) return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  else return *p;
+}
+
+template <bool COHERENT>
+__device__ __forceinline__ void merge_partials(const float* part_m, const float* part_l, const float* part_o,
+                                               int64_t base, int64_t stride, int64_t n, int64_t d, int64_t D,
+                                               float& M, float& L, float& O) {
+  constexpr int MS = 16;
+  M = -INFINITY;
+  L = 0.f;
+  O = 0.f;
+  for (int64_t s0 = 0; s0 < n; s0 += MS) {
+    float ms[MS], ls[MS], os[MS];
+#pragma unroll
+    for (int u = 0; u < MS; ++u) {
+      const bool ok = s0 + u < n;
+      const int64_t pi = base + (ok ? s0 + u : s0) * stride;  // s0 < n: in bounds
+      const float mv = partial_at<COHERENT>(part_m + pi), lv = partial_at<COHERENT>(part_l + pi),
+                  ov = partial_at<COHERENT>(part_o + pi * D + d);
+      ms[u] = ok ? mv : -INFINITY;
+      ls[u] = lv;
+      os[u] = ov;
+    }
+    float Mc = M;
+#pragma unroll
+    for (int u = 0; u < MS; ++u) Mc = fmaxf(Mc, ms[u]);
+    if (Mc == -INFINITY) continue;
+    if (M != -INFINITY && M != Mc) {
+      const float r = __expf(M - Mc);
+      L *= r;
+      O *= r;
+    }
+#pragma unroll
+    for (int u = 0; u < MS; ++u) {
+      if (ms[u] == -INFINITY) continue;
+      const float f = __expf(ms[u] - Mc);
+      L += f * ls[u];
+      O += f * os[u];
+    }
+    M = Mc;
+  }
+}
+
+// Arrival of one workgroup at its group's counter; true for the last of `total`.
+// The counter holds (epoch << 16) | arrivals.  A value with another epoch (an
+// earlier launch's, or memory never used as a counter) counts as no arrival: the
+// first workgroup of a launch installs (epoch, 1) with a compare-and-swap, every
+// later one adds 1, so a launch costs one swap and total - 1 additions (no retry
+// loop whose length grows with the arrivals).  The last workgroup clears the
+// counter, so a launch replayed with the same epoch (a captured graph) starts
+// from zero too.  A failed swap means another workgroup changed the counter, so
+// the loop ends after at most one installation and the reads that follow it.
+__device__ __forceinline__ bool arrive_last(unsigned long long* counter, unsigned long long epoch, int64_t total) {
+  unsigned long long old = __hip_atomic_load(counter, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  while (true) {
+    if ((old >> 16) == epoch) {
+      const unsigned long long prev = atomicAdd(counter, 1ull);
+      return static_cast<int64_t>((prev & 0xffffull) + 1) == total;
+    }
+    const unsigned long long seen = atomicCAS(counter, old, (epoch << 16) | 1ull);
+    if (seen == old) return total == 1;
+    old = seen;
+  }
 }
 
 // One workgroup (8 waves; 4 for head_dim 256) per (split, KV head x head chunk,
@@ -245,8 +335,10 @@ __device__ __forceinline__ int64_t entry_total(const AttendArgs& a, int64_t b, i
 // workgroups, i.e. one round on a 256-CU gfx950 (the kernel's LDS admits one
 // workgroup per CU).  Group i's workgroups are T(i) + hc * s_i + j (head chunk
 // hc, j < s_i), each with an even share of the group's entries rounded up to
-// 32.  The workgroup index is the slot of its split-K partial; T is written to
-// the workspace for the merge.
+// 32.  A group with no entries still gets one workgroup (s_i >= 1), which
+// writes the empty partial its merge turns into a zero output.  The workgroup
+// index is the slot of its split-K partial; T is written to the workspace for
+// the merge.
 constexpr int ATT_SLOTS = 256;
 constexpr int ATT_MIN_CHUNK = 128;
 constexpr int64_t ATT_MAX_GROUPS = 4096;
@@ -254,6 +346,7 @@ constexpr int64_t ATT_MAX_GROUPS = 4096;
 struct Assignment {
   int32_t group;  // b * Hkv + k, or -1: this workgroup has no work
   int32_t hc, e0, cnt;
+  int32_t parts, part;  // workgroups of (group, hc), and this one's index among them
 };
 
 __device__ __forceinline__ int32_t wave_total(int32_t v) {
@@ -273,9 +366,10 @@ __device__ Assignment balanced_assignment(const int32_t* c, int32_t ngroups, int
   int32_t e = 0;
   for (int32_t i = i0; i < i1; ++i) e += c[i];
   e = wave_total(e);
+  auto parts_of = [](int32_t ci, int32_t ch) { return ci > 0 ? (ci + ch - 1) / ch : 1; };
   auto workgroups = [&](int32_t ch) {
     int32_t s = 0;
-    for (int32_t i = i0; i < i1; ++i) s += (c[i] + ch - 1) / ch;
+    for (int32_t i = i0; i < i1; ++i) s += parts_of(c[i], ch);
     return wave_total(s) * hcs;
   };
   int32_t lo = (hcs * e + ATT_SLOTS - 1) / ATT_SLOTS;
@@ -292,13 +386,13 @@ __device__ Assignment balanced_assignment(const int32_t* c, int32_t ngroups, int
   }
   const int32_t ch = 32 * mlo;
   int32_t mine = 0;
-  for (int32_t i = i0; i < i1; ++i) mine += hcs * ((c[i] + ch - 1) / ch);
+  for (int32_t i = i0; i < i1; ++i) mine += hcs * parts_of(c[i], ch);
   const int32_t incl = wave_inclusive_sum(mine), excl = incl - mine;
   if (table) {
     int32_t t = excl;
     for (int32_t i = i0; i < i1; ++i) {
       table[i] = t;
-      t += hcs * ((c[i] + ch - 1) / ch);
+      t += hcs * parts_of(c[i], ch);
     }
     if (lane == 63) table[ngroups] = incl;
   }
@@ -311,7 +405,7 @@ __device__ Assignment balanced_assignment(const int32_t* c, int32_t ngroups, int
   if (owner) {
     int32_t t = excl;
     for (int32_t i = i0; i < i1; ++i) {
-      const int32_t n = hcs * ((c[i] + ch - 1) / ch);
+      const int32_t n = hcs * parts_of(c[i], ch);
       if (w < t + n) {
         gi = i;
         gl = w - t;
@@ -323,13 +417,15 @@ __device__ Assignment balanced_assignment(const int32_t* c, int32_t ngroups, int
   gi = __shfl(gi, src, 64);
   gl = __shfl(gl, src, 64);
   const int32_t ci = c[gi];
-  const int32_t s = (ci + ch - 1) / ch;
+  const int32_t s = parts_of(ci, ch);
   const int32_t hc = gl / s, j = gl - hc * s;
-  const int32_t chunk = ((ci + s - 1) / s + 31) / 32 * 32;  // <= ch, and (s - 1) * chunk < ci
+  const int32_t chunk = ((ci + s - 1) / s + 31) / 32 * 32;  // <= ch, and (s - 1) * chunk < ci (ci > 0)
   r.group = gi;
   r.hc = hc;
   r.e0 = j * chunk;
   r.cnt = ci - r.e0 < chunk ? ci - r.e0 : chunk;
+  r.parts = s;
+  r.part = j;
   return r;
 }
 
@@ -341,9 +437,10 @@ __global__ __launch_bounds__(64 * attend_waves(DP)) void attend_mfma_kernel(Atte
   constexpr int NT = DP / 16;   // PV M-tiles over d
   constexpr int KK = DP / 32;   // QK k-steps over d
   constexpr int RS = DP + 8;    // LDS row stride of the V tile (elements)
-  constexpr int LPR = DP / 8;   // lanes per row for 16-byte V loads
-  constexpr int RPI = 64 / LPR; // rows per V load instruction
-  constexpr int VI = 32 / RPI;  // V load instructions per 32-row tile
+  constexpr int CPR = DP / 16 < 4 ? DP / 16 : 4;  // 16-byte V chunks per lane and row
+  constexpr int LPR = DP / (8 * CPR);  // lanes per V row
+  constexpr int RPI = 64 / LPR;        // V rows per pass of the wave
+  constexpr int VI = 32 / RPI;         // V rows per lane and tile
   constexpr int VS_BYTES = AW * 32 * RS * 2;
   constexpr int MERGE_BYTES = AW * 16 * DP * 4;
   constexpr int SMEM = VS_BYTES > MERGE_BYTES ? VS_BYTES : MERGE_BYTES;
@@ -351,6 +448,7 @@ __global__ __launch_bounds__(64 * attend_waves(DP)) void attend_mfma_kernel(Atte
   __shared__ int64_t s_koff[ACH];
   __shared__ uint32_t s_mask[ACH];
   __shared__ float s_m[AW][16], s_l[AW][16];
+  __shared__ int s_last;
 
   unsigned short* vs_all = reinterpret_cast<unsigned short*>(smem);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -358,6 +456,7 @@ __global__ __launch_bounds__(64 * attend_waves(DP)) void attend_mfma_kernel(Atte
   const int64_t split = blockIdx.x;
   int64_t k, b, e0;
   int hchunk, cnt;
+  int64_t parts, first_slot;  // workgroups of this (group, head chunk); the first one's index
   if constexpr (SCHED) {
     // group entry counts in the (not yet used) V-tile buffer, then the schedule
     int32_t* s_cnt = reinterpret_cast<int32_t*>(smem);
@@ -375,12 +474,16 @@ __global__ __launch_bounds__(64 * attend_waves(DP)) void attend_mfma_kernel(Atte
     hchunk = asg.hc;
     e0 = asg.e0;
     cnt = asg.cnt;
+    parts = asg.parts;
+    first_slot = static_cast<int64_t>(blockIdx.x) - asg.part;
   } else {
     k = blockIdx.y / a.head_chunks;
     hchunk = blockIdx.y % a.head_chunks;
     b = blockIdx.z;
     e0 = split * a.chunk;
     cnt = 0;  // set below, once the group's entry count is known
+    parts = a.splits;  // the splits with entries, once the group's count is known (below)
+    first_slot = 0;
   }
   // split-K partial of head `hl` of the group (16 * hchunk <= hl < 16 * hchunk + 16)
   auto partial_index = [&](int hl) -> int64_t {
@@ -422,6 +525,7 @@ __global__ __launch_bounds__(64 * attend_waves(DP)) void attend_mfma_kernel(Atte
     }
     const int64_t E = entry_total<MODE>(a, b, k);
     cnt = E > e0 ? static_cast<int>(E - e0 < a.chunk ? E - e0 : a.chunk) : 0;
+    parts = E > 0 ? (E + a.chunk - 1) / a.chunk : 1;
     // no branch on cnt here: a conditional block would let the compiler sink the
     // column loads below the wait for the count
 #pragma unroll
@@ -435,6 +539,7 @@ __global__ __launch_bounds__(64 * attend_waves(DP)) void attend_mfma_kernel(Atte
   } else if constexpr (!SCHED) {
     const int64_t E = entry_total<MODE>(a, b, k);
     cnt = E > e0 ? static_cast<int>(E - e0 < a.chunk ? E - e0 : a.chunk) : 0;
+    parts = E > 0 ? (E + a.chunk - 1) / a.chunk : 1;
     stage_entries<MODE, NTH, SPT>(a, b, k, e0, cnt, ph, mk);
   } else {
     stage_entries<MODE, NTH, SPT>(a, b, k, e0, cnt, ph, mk);
@@ -460,41 +565,57 @@ __global__ __launch_bounds__(64 * attend_waves(DP)) void attend_mfma_kernel(Atte
 
   const int ntiles = (cnt + 31) / 32;
   // K fragments (A operand: lane holds K[row 16rt + c][d = 32kk + 8j .. +8]) and the
-  // V rows this lane stages (row vi*RPI + lane/LPR, d = 8*(lane%LPR) .. +8) of tile t.
-  // Loads are unconditional and their results are used as loaded, so that the
-  // loads of a tile stay in flight until the tile is processed: a masked lane
-  // reads its own query row instead (in bounds, finite).  That data never
-  // reaches the output: a masked entry's score is -inf (probability 0, so its
-  // V contributes 0), K columns at d >= D meet zero Q fragments, and output
-  // columns d >= D are not written.
-  auto load_tile = [&](int t, u32x4 (&kf)[2][KK], u32x4 (&vr)[VI]) {
+  // V rows this lane stages (CPR 16-byte chunks of rows vi * RPI + lane / LPR) of
+  // tile t.  Loads are unconditional and their results are used as loaded, so that
+  // the loads of a tile stay in flight until the tile is processed: a masked entry
+  // reads the lane's query row instead (in bounds, finite).  That data never reaches
+  // the output: a masked entry's score is -inf (probability 0, so its V contributes
+  // 0).  The head dim is exactly DP, so no lane reads past a row.
+  // Addresses of the K rows and V rows this lane loads for tile t (a masked entry
+  // reads its own query row instead), computed while earlier tiles' loads are in
+  // flight, so that issuing a tile's loads needs no register the loads of the tile
+  // before it may still write.
+  struct TileAddr {
+    const unsigned short* k[2];
+    const unsigned short* v[VI];
+  };
+  auto tile_addr = [&](int t) {
+    TileAddr ad;
 #pragma unroll
     for (int rt = 0; rt < 2; ++rt) {
       const int li = 32 * t + 16 * rt + c;
       const int64_t koff = s_koff[li < ACH ? li : 0];
-      const bool row_ok = li < cnt && koff >= 0;
-#pragma unroll
-      for (int kk = 0; kk < KK; ++kk) {
-        const int d0 = 32 * kk + 8 * j;
-        kf[rt][kk] = load16(row_ok && d0 < D ? pool + koff + d0 : qrow);
-      }
+      ad.k[rt] = li < cnt && koff >= 0 ? pool + koff + 8 * j : qrow;
     }
 #pragma unroll
     for (int vi = 0; vi < VI; ++vi) {
       const int li = 32 * t + vi * RPI + lane / LPR;
-      const int cc = lane % LPR;
       const int64_t koff = s_koff[li < ACH ? li : 0];
-      const bool ok = li < cnt && koff >= 0 && 8 * cc < D;
-      vr[vi] = load16(ok ? pool + koff + vplane + 8 * cc : qrow);
+      ad.v[vi] = li < cnt && koff >= 0 ? pool + koff + vplane + 8 * CPR * (lane % LPR) : qrow;
+    }
+    return ad;
+  };
+  auto load_tile = [&](const TileAddr& ad, u32x4 (&kf)[2][KK], u32x4 (&vr)[VI][CPR]) {
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) {
+#pragma unroll
+      for (int kk = 0; kk < KK; ++kk) kf[rt][kk] = load16(ad.k[rt] + 32 * kk);
+    }
+#pragma unroll
+    for (int vi = 0; vi < VI; ++vi) {
+#pragma unroll
+      for (int cc = 0; cc < CPR; ++cc) vr[vi][cc] = load16(ad.v[vi] + 8 * cc);
     }
   };
 
-  auto process = [&](int t, const u32x4 (&kf)[2][KK], const u32x4 (&vr)[VI]) {
+  auto process = [&](int t, const u32x4 (&kf)[2][KK], const u32x4 (&vr)[VI][CPR]) {
     // V rows of this tile into LDS
 #pragma unroll
     for (int vi = 0; vi < VI; ++vi) {
       const int row = vi * RPI + lane / LPR;
-      *reinterpret_cast<u32x4*>(vs + row * RS + 8 * (lane % LPR)) = vr[vi];
+#pragma unroll
+      for (int cc = 0; cc < CPR; ++cc)
+        *reinterpret_cast<u32x4*>(vs + row * RS + 8 * CPR * (lane % LPR) + 8 * cc) = vr[vi][cc];
     }
 
     // S^T[row][head] = K Q^T
@@ -515,7 +636,7 @@ __global__ __launch_bounds__(64 * attend_waves(DP)) void attend_mfma_kernel(Atte
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const uint32_t mkv = s_mask[32 * t + 16 * rt + 4 * j + i];
-        const bool valid = hh < 32 && ((mkv >> hbit_shift) & 1u);
+        const bool valid = (mkv >> hbit_shift) & 1u;  // hh < 32: at most two head chunks
         const float sc = valid ? st[rt][i] * a.scale : -INFINITY;
         sv[rt][i] = sc;
         tmax = fmaxf(tmax, sc);
@@ -568,24 +689,37 @@ __global__ __launch_bounds__(64 * attend_waves(DP)) void attend_mfma_kernel(Atte
     wave_lds_sync();  // all reads of this tile done before the next overwrites it
   };
 
-  u32x4 kA[2][KK], vA[VI], kB[2][KK], vB[VI];
+  u32x4 kA[2][KK], vA[VI][CPR], kB[2][KK], vB[VI][CPR];
   int t = wave;
   if (t < ntiles) {  // uniform per wave
-    load_tile(t, kA, vA);
-    // the scheduling barriers keep each prefetch ahead of the wait for the
-    // tile before it (the scheduler would otherwise sink the loads below it)
+    TileAddr ad = tile_addr(t);
+    load_tile(ad, kA, vA);
+    ad = tile_addr(t + AW);
+    // each half issues the next tile's loads, computes the addresses of the tile
+    // after it, then processes the current tile; the scheduling barriers keep the
+    // loads ahead of the wait for the current tile (the scheduler would otherwise
+    // sink them below it)
     while (true) {
-      load_tile(t + AW, kB, vB);  // past the end: every lane masked
+      load_tile(ad, kB, vB);  // past the end: every lane masked
+      ad = tile_addr(t + 2 * AW);
       __builtin_amdgcn_sched_barrier(0);
       process(t, kA, vA);
       t += AW;
       if (t >= ntiles) break;
-      load_tile(t + AW, kA, vA);
+      load_tile(ad, kA, vA);
+      ad = tile_addr(t + 2 * AW);
       __builtin_amdgcn_sched_barrier(0);
       process(t, kB, vB);
       t += AW;
       if (t >= ntiles) break;
     }
+  }
+
+  if constexpr (!SCHED) {
+    // with the in-kernel merge, a split past the group's entries writes no partial
+    // and does not arrive (the group waits for its `parts` splits with entries only);
+    // the same for every wave of the workgroup, so no barrier is left waiting
+    if (a.fuse && split >= parts) return;
   }
 
   // per-wave totals over the four lane groups that share a head
@@ -623,12 +757,45 @@ __global__ __launch_bounds__(64 * attend_waves(DP)) void attend_mfma_kernel(Atte
       }
     }
     const int64_t pidx = partial_index(hl);
+    // device-scope stores: written through to where every XCD's loads of the same
+    // scope see them, with no cache-wide write-back or invalidation
     if (d == 0) {
-      a.part_m[pidx] = M;
-      a.part_l[pidx] = L;
+      __hip_atomic_store(a.part_m + pidx, M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(a.part_l + pidx, L, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    a.part_o[pidx * D + d] = O;
+    __hip_atomic_store(a.part_o + pidx * D + d, O, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
+  if (!a.fuse) return;
+
+  // The group's last workgroup merges every partial of the group and writes the
+  // output.  Every wave waits for its partial stores to complete before the
+  // barrier, so they are all in place when the arrival is counted; the last
+  // workgroup reads them after its arrival with device-scope loads.
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x == 0)
+    s_last = arrive_last(a.arrivals + (b * Hkv + k) * a.head_chunks + hchunk, a.epoch, parts) ? 1 : 0;
+  __syncthreads();
+  if (!s_last) return;
+  for (int idx = threadIdx.x; idx < 16 * DP; idx += NTH) {
+    const int head = idx / DP, d = idx % DP;
+    const int hl = 16 * hchunk + head;
+    if (hl >= a.g || d >= D) continue;
+    int64_t base, stride;
+    if constexpr (SCHED) {
+      base = first_slot * 16 + head;
+      stride = 16;
+    } else {
+      base = (b * a.Hq + k * a.g + hl) * a.splits;
+      stride = 1;
+    }
+    float M, L, O;
+    merge_partials<true>(a.part_m, a.part_l, a.part_o, base, stride, parts, d, D, M, L, O);
+    store_elem<DT>(a.out, b * a.o_sb + (k * a.g + hl) * a.o_sh + d, L > 0.f ? O / L : 0.f);
+  }
+  if (threadIdx.x == 0)
+    __hip_atomic_store(a.arrivals + (b * Hkv + k) * a.head_chunks + hchunk, 0ull, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // VALU fallback: one wave per (split, query head, request); any dtype, D <= 512.
@@ -717,41 +884,9 @@ __global__ __launch_bounds__(256) void attend_merge_kernel(const float* part_m, 
     stride = 1;
     n = splits;
   }
-  // Partials are read MS at a time, every load issued before any is used (one
-  // round of loads per MS splits); chunks after the first rescale the running
-  // sums, so for n <= MS the arithmetic is a plain max, then sums in split order.
-  constexpr int MS = 16;
   for (int64_t d = threadIdx.x; d < D; d += blockDim.x) {
-    float M = -INFINITY, L = 0.f, O = 0.f;
-    for (int64_t s0 = 0; s0 < n; s0 += MS) {
-      float ms[MS], ls[MS], os[MS];
-#pragma unroll
-      for (int u = 0; u < MS; ++u) {
-        const bool ok = s0 + u < n;
-        const int64_t pi = base + (ok ? s0 + u : s0) * stride;  // s0 < n: in bounds
-        const float mv = part_m[pi], lv = part_l[pi], ov = part_o[pi * D + d];
-        ms[u] = ok ? mv : -INFINITY;
-        ls[u] = lv;
-        os[u] = ov;
-      }
-      float Mc = M;
-#pragma unroll
-      for (int u = 0; u < MS; ++u) Mc = fmaxf(Mc, ms[u]);
-      if (Mc == -INFINITY) continue;
-      if (M != -INFINITY && M != Mc) {
-        const float r = __expf(M - Mc);
-        L *= r;
-        O *= r;
-      }
-#pragma unroll
-      for (int u = 0; u < MS; ++u) {
-        if (ms[u] == -INFINITY) continue;
-        const float f = __expf(ms[u] - Mc);
-        L += f * ls[u];
-        O += f * os[u];
-      }
-      M = Mc;
-    }
+    float M, L, O;
+    merge_partials<false>(part_m, part_l, part_o, base, stride, n, d, D, M, L, O);
     if (st_m) {  // the unnormalised state (m, l, acc) of the head, fp32
       if (d == 0) {
         st_m[b * Hq + h] = M;
@@ -813,12 +948,18 @@ struct Plan {
   int64_t grid;  // its workgroups (slots)
 };
 
+// The MFMA kernel takes 16-bit pools with a head dim of exactly 32, 64, 128 or 256
+// (its tiles cover whole rows, with no per-lane bound); others run on the VALU kernel.
+static bool mfma_shape(int dtype, int64_t D) {
+  return dtype != HS_DTYPE_F32 && (D == 32 || D == 64 || D == 128 || D == 256);
+}
+
 static Plan plan_attend(int dtype, int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int64_t max_entries) {
   Plan p{};
   const int64_t g = Hq / Hkv;
-  p.mfma = dtype != HS_DTYPE_F32 && D % 8 == 0 && D <= 256;
+  p.mfma = mfma_shape(dtype, D);
   if (p.mfma) {
-    p.dp = D <= 32 ? 32 : D <= 64 ? 64 : D <= 128 ? 128 : 256;
+    p.dp = static_cast<int>(D);
     p.head_chunks = static_cast<int>(ceil_div(g, 16));
     // entries per workgroup: about one (8-wave) workgroup per CU for the
     // largest entry lists, at most ACH (the LDS entry list), at least 128
@@ -855,20 +996,39 @@ static Plan plan_attend(int dtype, int64_t B, int64_t Hq, int64_t Hkv, int64_t D
   return p;
 }
 
-// Bytes of the partials [n] m, [n] l, [n, D] o (+ the slot table when scheduled).
-static int64_t workspace_split(const Plan& p, int64_t B, int64_t Hq, int64_t D) {
-  const int64_t n = B * Hq * p.splits;
-  return (2 * n + n * D) * 4 + 256;
-}
-static int64_t workspace_sched(const Plan& p, int64_t B, int64_t Hkv, int64_t D) {
-  const int64_t n = p.grid * 16;
-  return (2 * n + n * D) * 4 + (B * Hkv + 1) * 4 + 256;
+// Workspace of one launch: the partials [n] m, [n] l, [n, D] o, the slot table
+// T(0 .. B * Hkv) when scheduled, then (8-byte aligned) the arrival counters of
+// the in-kernel merge, one per (request, KV head, head chunk).
+struct WsLayout {
+  int64_t n, table, arrivals, bytes;
+};
+static WsLayout ws_layout(const Plan& p, bool sched, int64_t B, int64_t Hq, int64_t Hkv, int64_t D) {
+  WsLayout w{};
+  w.n = sched ? p.grid * 16 : B * Hq * p.splits;
+  w.table = (2 * w.n + w.n * D) * 4;
+  const int64_t table_end = w.table + (sched ? (B * Hkv + 1) * 4 : 0);
+  w.arrivals = (table_end + 7) / 8 * 8;
+  w.bytes = w.arrivals + B * Hkv * p.head_chunks * 8 + 256;
+  return w;
 }
 // Either schedule may run on a workspace sized by hs_attend_workspace_bytes.
 static int64_t workspace_for(const Plan& p, int64_t B, int64_t Hq, int64_t Hkv, int64_t D) {
-  const int64_t split = workspace_split(p, B, Hq, D);
-  const int64_t sched = p.sched ? workspace_sched(p, B, Hkv, D) : 0;
+  const int64_t split = ws_layout(p, false, B, Hq, Hkv, D).bytes;
+  const int64_t sched = p.sched ? ws_layout(p, true, B, Hq, Hkv, D).bytes : 0;
   return split > sched ? split : sched;
+}
+
+// Tag of one launch's arrivals: 48 bits, never 0, different for every launch of
+// the process (a counter started from the clock, so that counters left in reused
+// memory by another process are unlikely to carry it either).
+static unsigned long long next_epoch() {
+  static std::atomic<unsigned long long> counter{
+      static_cast<unsigned long long>(std::chrono::steady_clock::now().time_since_epoch().count()) * 0x9e3779b97f4a7c15ull};
+  unsigned long long e;
+  do {
+    e = counter.fetch_add(1, std::memory_order_relaxed) & 0xffffffffffffull;
+  } while (e == 0);
+  return e;
 }
 
 template <int DT, int MODE, bool SCHED>
@@ -905,19 +1065,36 @@ static int run_attend(int dtype, AttendArgs a, int64_t max_entries, void* out, i
   // pays off when the entry lists are much shorter than max_entries.
   const char* sched_env = getenv("HS_ATTEND_SCHED");
   const bool sched = p.mfma && p.sched && a.mode == MODE_GROUPS && sched_env && atoi(sched_env) == 1;
-  const int64_t need = sched ? workspace_sched(p, a.B, a.Hkv, a.D) : workspace_split(p, a.B, a.Hq, a.D);
-  HS_CHECK_ARG(ws != nullptr && ws_bytes >= need, "attention workspace too small: need %lld bytes",
-               static_cast<long long>(need));
-  const int64_t n = sched ? p.grid * 16 : a.B * a.Hq * p.splits;
+  const WsLayout w = ws_layout(p, sched, a.B, a.Hq, a.Hkv, a.D);
+  HS_CHECK_ARG(ws != nullptr && ws_bytes >= w.bytes, "attention workspace too small: need %lld bytes",
+               static_cast<long long>(w.bytes));
   float* base = static_cast<float*>(ws);
   a.part_m = base;
-  a.part_l = base + n;
-  a.part_o = base + 2 * n;
-  a.sched = sched ? reinterpret_cast<int32_t*>(base + 2 * n + n * a.D) : nullptr;
+  a.part_l = base + w.n;
+  a.part_o = base + 2 * w.n;
+  a.sched = sched ? reinterpret_cast<int32_t*>(static_cast<char*>(ws) + w.table) : nullptr;
   a.splits = p.splits;
   a.chunk = p.chunk;
   a.head_chunks = p.head_chunks;
   a.scale = 1.0f / sqrtf(static_cast<float>(a.D));
+  // The MFMA kernel merges its own partials when the caller wants the normalised
+  // output and a group has at most 16 splits: the last workgroup's merge replaces
+  // the merge launch (measured on MI355X: 60.3 -> 58.6 us at the microbench, 68.6 ->
+  // 54.1 us per launch beside the end-to-end gather), but with many short splits
+  // (28 of 128 entries at the Qwen2.5-0.5B shape) the arrivals cost more than the
+  // launch (15.5 -> 19.0 us).  HS_ATTEND_FUSED_MERGE=0 / 1 forces either way.
+  const char* fused_env = getenv("HS_ATTEND_FUSED_MERGE");  // read per call, like HS_ATTEND_SCHED
+  const int fused_merge = fused_env ? atoi(fused_env) : -1;
+  const bool few_splits = sched || p.splits <= 16;
+  a.fuse = p.mfma && st_m == nullptr && (fused_merge == 1 || (fused_merge != 0 && few_splits)) ? 1 : 0;
+  // the arrival counter holds up to 0xffff arrivals; a group has at most
+  // ceil(max_entries / 128) workgroups (chunks are at least 128 entries)
+  HS_CHECK_ARG(!a.fuse || ceil_div(max_entries, 128) <= 0xffff, "too many entries per attention group");
+  a.arrivals = reinterpret_cast<unsigned long long*>(static_cast<char*>(ws) + w.arrivals);
+  a.epoch = next_epoch();
+  a.out = out;
+  a.o_sb = o_sb;
+  a.o_sh = o_sh;
   if (p.mfma) {
     if (dtype == HS_DTYPE_BF16) launch_mfma<HS_DTYPE_BF16>(p, a, stream);
     else launch_mfma<HS_DTYPE_F16>(p, a, stream);
@@ -928,6 +1105,7 @@ static int run_attend(int dtype, AttendArgs a, int64_t max_entries, void* out, i
     else hipLaunchKernelGGL((attend_valu_kernel<HS_DTYPE_F16>), grid, dim3(64), 0, stream, a);
   }
   HS_CHECK_LAUNCH("attention");
+  if (a.fuse) return HS_OK;
   dim3 mgrid(static_cast<unsigned>(a.Hq), static_cast<unsigned>(a.B));
   const unsigned mthreads = a.D <= 64 ? 64 : (a.D <= 128 ? 128 : 256);
   const int64_t hcs = a.head_chunks;
@@ -955,7 +1133,7 @@ static int check_common(int dtype, int64_t B, int64_t Hq, int64_t Hkv, int64_t D
   HS_CHECK_ARG(Hq / Hkv <= 32, "at most 32 query heads per KV head are supported");
   HS_CHECK_ARG(D <= 512, "head_dim above 512 is not supported");
   HS_CHECK_ARG(q && pool && out, "null attention pointer");
-  if (dtype != HS_DTYPE_F32 && D % 8 == 0 && D <= 256)
+  if (mfma_shape(dtype, D))
     HS_CHECK_ARG((reinterpret_cast<uintptr_t>(q) & 15) == 0 && (reinterpret_cast<uintptr_t>(pool) & 15) == 0,
                  "query and pool must be 16-byte aligned");
   return HS_OK;

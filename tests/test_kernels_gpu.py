@@ -456,12 +456,16 @@ def _group_rows_oracle(union_physical, cols, masks, counts, capacity, kv, g):
         ("many-groups", 520, 8, 1, 32, 40, None),  # > 4096 groups: always the split schedule
     ],
 )
+@pytest.mark.parametrize("merge", ["in-kernel", "launch"])
 @pytest.mark.parametrize("schedule", ["split", "balanced"])
-def test_group_attention_schedule_matches_oracle(gpu, monkeypatch, schedule, name, B, kv, g, D, capacity, counts):
+def test_group_attention_schedule_matches_oracle(gpu, monkeypatch, schedule, merge, name, B, kv, g, D, capacity,
+                                                 counts):
     """hs_attend_groups over synthetic entry lists of very different lengths, with
-    the default split schedule and the device-derived balanced one (HS_ATTEND_SCHED=1,
-    read per call), each with its merge, against the per-head oracle."""
+    the default split schedule and the device-derived balanced one (HS_ATTEND_SCHED=1),
+    each with the last workgroup's merge and with the merge launch
+    (HS_ATTEND_FUSED_MERGE=1 / 0; both read per call), against the per-head oracle."""
     monkeypatch.setenv("HS_ATTEND_SCHED", "1" if schedule == "balanced" else "0")
+    monkeypatch.setenv("HS_ATTEND_FUSED_MERGE", "1" if merge == "in-kernel" else "0")
     from mini_hisparse_amd.row_index import GroupEntries
     from mini_hisparse_amd.row_kernels import attend_groups
 
@@ -491,6 +495,71 @@ def test_group_attention_schedule_matches_oracle(gpu, monkeypatch, schedule, nam
         _close(got[b], expected, 2e-2, 1e-2)
     if name == "all-empty":
         assert not got.any()
+
+
+def _group_case(gpu, B=6, kv=4, g=7, D=128, capacity=3000, seed=11):
+    from mini_hisparse_amd.row_index import GroupEntries
+
+    P, blocks, U = 16, 96, 900
+    rng = np.random.default_rng(seed)
+    counts = rng.integers(0, capacity + 1, size=(B, kv))
+    union_physical = rng.integers(0, blocks * P, size=(B, U))
+    cols = rng.integers(0, U, size=(B, kv, capacity)).astype(np.int32)
+    masks = rng.integers(1, 1 << g, size=(B, kv, capacity)).astype(np.uint32).view(np.int32)
+    pool = make_pool(blocks, P, kv, D, torch.bfloat16, seed=seed, outliers=True).to(gpu)
+    q = torch.randn(B, kv * g, D, generator=torch.Generator().manual_seed(seed)).to(torch.bfloat16).to(gpu)
+    entries = GroupEntries(torch.from_numpy(cols).to(gpu), torch.from_numpy(masks).to(gpu),
+                           torch.from_numpy(counts.astype(np.int32)).to(gpu), capacity)
+    return q, pool, torch.from_numpy(union_physical).to(gpu), entries, cfg(P, kv, D)
+
+
+def test_in_kernel_merge_starts_from_any_workspace_contents(gpu, monkeypatch):
+    """The arrival counters live in the caller's workspace, which may hold anything
+    (uninitialised memory, another launch's counters): every launch gives the same
+    output as the merge launch, whatever the workspace held before it."""
+    from mini_hisparse_amd import row_kernels
+    from mini_hisparse_amd.row_kernels import attend_groups
+
+    case = _group_case(gpu)
+    monkeypatch.setenv("HS_ATTEND_FUSED_MERGE", "0")
+    want = attend_groups(*case)
+    monkeypatch.setenv("HS_ATTEND_FUSED_MERGE", "1")
+    gen = torch.Generator(device=gpu).manual_seed(3)
+    for fill in ("random", "ones", "zeros", "same"):
+        ws = row_kernels._ATTEND_WS[(torch.device(gpu), torch.cuda.current_stream(gpu).cuda_stream)]
+        if fill == "random":
+            ws.copy_(torch.randint(0, 256, ws.shape, generator=gen, device=gpu, dtype=torch.int32).to(torch.uint8))
+        elif fill == "ones":
+            ws.fill_(0xFF)
+        elif fill == "zeros":
+            ws.zero_()
+        got = attend_groups(*case)
+        torch.testing.assert_close(got, want, rtol=0, atol=0)
+
+
+def test_in_kernel_merge_replays_from_a_captured_graph(gpu, monkeypatch):
+    """A captured attention replays with the epoch of its capture: the last workgroup
+    clears its group's counter, so every replay (with eager launches of other epochs
+    between them) merges exactly once per group."""
+    from mini_hisparse_amd.row_kernels import attend_groups
+
+    monkeypatch.setenv("HS_ATTEND_FUSED_MERGE", "1")
+    case = _group_case(gpu)
+    eager = attend_groups(*case)
+    side = torch.cuda.Stream(gpu)
+    side.wait_stream(torch.cuda.current_stream(gpu))
+    with torch.cuda.stream(side):
+        attend_groups(*case)  # workspace of the capture stream
+    torch.cuda.current_stream(gpu).wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        captured = attend_groups(*case)
+    for _ in range(4):
+        captured.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        torch.testing.assert_close(captured, eager, rtol=0, atol=0)
+        torch.testing.assert_close(attend_groups(*case), eager, rtol=0, atol=0)  # an eager launch between
 
 
 # ------------------------------------------------------- page-window attention
