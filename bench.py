@@ -629,6 +629,8 @@ PMC_SUMMARIES = {
 # to that configuration only
 PMC_CONFIG = {"microbench": (8, 1), "qwen2.5-7b": (8, 2), "qwen2.5-7b-layer": (16, 1)}
 ROOFLINE_KERNELS = ("attend_mfma_kernel", "attend_merge_kernel")
+ATTENTION_KERNELS = ("attend_mfma_kernel, its last workgroup per (request, KV head) merging the split partials "
+                     "(attend_merge_kernel instead when a group has more than 16 splits)")
 CALIBRATION_BYTES = 1 << 30  # hbm_copy_gbs: a plain device-to-device copy of 1 GiB
 
 
@@ -689,7 +691,54 @@ def summarize_pmc(fetch_dir, write_dir, workload="microbench"):
 
 TRACE_SUMMARIES = {
     "qwen2.5-7b": os.path.join(PROFILES, "qwen2.5-7b_e2e_kernel_trace.md"),
+    "microbench": os.path.join(PROFILES, "microbench_kernel_trace.md"),
+    "qwen2.5-7b-layer": os.path.join(PROFILES, "qwen2.5-7b_layer_kernel_trace.md"),
 }
+
+
+def summarize_layer_trace(trace_dir, args):
+    """Per-kernel dispatches and durations of the library's kernels in a kernel trace of a
+    single-layer workload (microbench, qwen2.5-7b-layer): every step of the run (warmup,
+    timed, profiled) with the attention ceilings' probes beside them, avg / min / max."""
+    import csv
+    import glob
+    from collections import defaultdict
+
+    (path,) = glob.glob(os.path.join(trace_dir, "*kernel_trace.csv"))
+    per = defaultdict(list)
+    rows = sorted(csv.DictReader(open(path)), key=lambda r: int(r["Start_Timestamp"]))
+    previous = ""
+    for r in rows:
+        name = r["Kernel_Name"].split("(")[0].replace("void ", "")
+        if not name.startswith("hs::"):
+            continue
+        name = name.replace("hs::", "")
+        duration = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+        per[name].append(duration)
+        if name.startswith("attend_mfma_kernel") and previous.startswith("gather_kernel"):
+            per[name + " (in step: after the gather)"].append(duration)
+        previous = name
+    cmd = (f"rocprofv3 --kernel-trace --stats -f csv -d <dir> -o bench -- python3 bench.py --workload "
+           f"{args.workload} --steps {args.steps} --warmup {args.warmup} --no-cpu-baseline")
+    lines = [
+        f"# Kernel trace: {SHAPES[args.workload].label}, batch {SHAPES[args.workload].batch}, bf16",
+        "",
+        f"Command: `{cmd}`",
+        f"Summarised by: `python bench.py --workload {args.workload} --steps {args.steps} --warmup {args.warmup} "
+        "--summarize-trace <dir>`",
+        "",
+        "Every dispatch of the library's kernels in the run: the warmup, timed and profiled steps and the "
+        "measured ceilings' probes (`probe_row_reads_kernel`; the attention kernel's count includes the "
+        "ceilings' launches).  Microseconds.",
+        "",
+        "| kernel | dispatches | avg us | min us | max us |",
+        "|---|---|---|---|---|",
+    ]
+    for name, ds in sorted(per.items(), key=lambda x: -float(np.mean(x[1]))):
+        lines.append(f"| `{name}` | {len(ds)} | {np.mean(ds):.1f} | {min(ds):.1f} | {max(ds):.1f} |")
+    with open(TRACE_SUMMARIES[args.workload], "w") as fh:
+        fh.write("\n".join(lines) + "\n")
+    print("\n".join(lines))
 
 
 def summarize_trace(trace_dir, args):
@@ -740,9 +789,10 @@ def summarize_trace(trace_dir, args):
         f"Timed region: {args.steps} steps x {L} layers x {groups} request group(s), {len(window)} dispatches "
         f"over {span_ms:.1f} ms "
         f"({span_ms / args.steps:.2f} ms per step under the profiler).",
-        f"Attention (`hs_attend_groups`) per launch: attend_mfma_kernel {att_us:.2f} us + attend_merge_kernel "
-        f"{mrg_us:.2f} us = {att_us + mrg_us:.2f} us (the bench line's HIP events around the call also hold the "
-        "dispatch gap between the two kernels).",
+        f"Attention (`hs_attend_groups`) per launch: attend_mfma_kernel {att_us:.2f} us"
+        + (f" + attend_merge_kernel {mrg_us:.2f} us = {att_us + mrg_us:.2f} us (the bench line's HIP events around "
+           "the call also hold the dispatch gap between the two kernels)." if mrg else
+           " (the last workgroup of each group merges the partials: no merge launch)."),
         "",
         "| kernel | dispatches | total ms | avg us | ms per step |",
         "|---|---|---|---|---|",
@@ -757,7 +807,9 @@ def summarize_trace(trace_dir, args):
 
 
 def pmc_traffic(kernels=ROOFLINE_KERNELS, path=PMC_SUMMARY):
-    """HBM bytes per launch of `kernels` (sum) from the committed counter summary, or None."""
+    """HBM bytes per launch of `kernels` (sum of those the summary lists) from the committed
+    counter summary, or None when it lacks the first (the attention kernel; the merge
+    kernel runs only when the attention does not merge its own partials)."""
     if not os.path.exists(path):
         return None
     total, found = 0.0, set()
@@ -768,7 +820,7 @@ def pmc_traffic(kernels=ROOFLINE_KERNELS, path=PMC_SUMMARY):
                 if parts[1].startswith(k):
                     total += float(parts[3]) + float(parts[4])
                     found.add(k)
-    return total if found == set(kernels) else None
+    return total if kernels[0] in found else None
 
 
 def model_cpu_baseline(torch, engine, wl, budget_s):
@@ -1034,7 +1086,7 @@ def run_model_workload(args, torch, device):
             "unit": "GB/s",
             "frac": att_gbs / HBM_PEAK_GBS,
             "traffic": traffic,
-            "kernel": "attend_mfma_kernel + attend_merge_kernel (hs_attend_groups), every layer of the timed steps"
+            "kernel": f"{ATTENTION_KERNELS} (hs_attend_groups), every layer of the timed steps"
             + (" (one launch per request group, beside the other group's gather)" if engine.groups else ""),
             "launches": launches,
             "bytes_per_launch": att_bytes / launches,
@@ -1062,7 +1114,10 @@ def run_model_workload(args, torch, device):
 def main():
     args = parse_args()
     if args.summarize_trace:
-        summarize_trace(args.summarize_trace, args)
+        if args.workload in SHAPES:
+            summarize_layer_trace(args.summarize_trace, args)
+        else:
+            summarize_trace(args.summarize_trace, args)
         return
     if args.summarize_pmc:
         if args.workload not in PMC_SUMMARIES:
@@ -1188,7 +1243,7 @@ def run_microbench(args, torch, device):
             "unit": "GB/s",
             "frac": att_gbs / HBM_PEAK_GBS,
             "traffic": pmc_traffic(ROOFLINE_KERNELS, pmc_path) if counters_apply else None,
-            "kernel": "attend_mfma_kernel + attend_merge_kernel (hs_attend_groups)",
+            "kernel": f"{ATTENTION_KERNELS} (hs_attend_groups)",
             "measured_ceilings": ceilings,
         },
         "kernels": kernels,
