@@ -1126,7 +1126,7 @@ def main():
         return
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on exactly one GPU; --gpus above 1 is not supported "
-                          "(the decode path shards by request, see DESIGN.md)", "n_gpus": args.gpus}))
+                          "(the decode path would shard by request, one GPU per request set)", "n_gpus": args.gpus}))
         sys.exit(2)
     import torch
 

@@ -4,6 +4,7 @@ and the product never reaches the CPU oracle."""
 import ctypes
 import os
 import re
+import shutil
 import subprocess
 import sys
 from textwrap import dedent
@@ -36,6 +37,22 @@ def test_library_exports_every_declared_symbol():
         assert hasattr(lib, name), name
         assert name in _lib.SIGNATURES, f"{name} has no ctypes signature"
     assert lib.hs_version() == 1
+
+
+def test_dynamic_symbol_table_holds_only_the_c_api():
+    """Every global symbol the library defines is a declared hs_* entry point: kernel
+    handles, device stubs, device variables and per-file ids stay local, so two copies of
+    the library in one process cannot meet each other's names."""
+    if not shutil.which("readelf"):
+        pytest.skip("readelf is not installed")
+    out = subprocess.run(["readelf", "--dyn-syms", "-W", str(_lib.LIBRARY_PATH)], capture_output=True, text=True,
+                         check=True).stdout
+    defined = set()
+    for line in out.splitlines():
+        parts = line.split()
+        if len(parts) >= 8 and parts[4] in ("GLOBAL", "WEAK") and parts[6] != "UND":
+            defined.add(parts[7])
+    assert defined and defined == set(declared_functions())
 
 
 def test_descriptor_layout_matches_the_header(tmp_path):
