@@ -92,6 +92,10 @@ def parse_args():
     p.add_argument("--group-gather-workgroups", type=int, default=None,
                    help="gather workgroups per request with request groups (0 = the library's default; "
                         "default 24 for qwen2.5-7b)")
+    p.add_argument("--residency", choices=["policy", "fraction"], default="policy",
+                   help="model workloads with a prefill: the hybrid policy places pages and hot regions in a slab "
+                        "of resident_fraction of the history plus every layer's promised hot region and tails "
+                        "(default), or a seeded fixed fraction of each layer's pages is resident")
     p.add_argument("--synthetic-history", action="store_true",
                    help="model workloads: write synthetic K/V histories (N(0,1), 2%% of channels x8) directly "
                         "instead of prefilling random prompts through the model")
@@ -963,7 +967,7 @@ def run_model_workload(args, torch, device):
     model = random_model(wl, device, seed=args.seed)
     first_tokens = None
     if not args.synthetic_history:
-        state = empty_state(wl, device)
+        state = empty_state(wl, device, residency=args.residency)
         print(f"[bench] prefill of {wl.batch} random prompts", file=sys.stderr, flush=True)
         t_prefill = time.perf_counter()
         first_tokens = state.prefill(model, random_prompts(wl, device, seed=args.seed), wl.resident_fraction,
@@ -1066,7 +1070,10 @@ def run_model_workload(args, torch, device):
             f"batch {wl.batch}, {wl.context}-token histories, "
             + (f"Quest top-{wl.top_pages} pages, " if wl.selector == "quest" else
                f"{wl.top_pages} pages resampled uniformly each step (tail page forced), shared by every head, ")
-            + f"{wl.resident_fraction:.0%} of pages resident, hot_rows {wl.hot_rows}"
+            + (f"hybrid residency policy (window 64 pages, default watermark) over a slab of "
+               f"{state.blocks} blocks = {wl.resident_fraction:.0%} of the history + every layer's hot region "
+               f"and two tails, hot_rows {wl.hot_rows}" if state.plan is not None else
+               f"{wl.resident_fraction:.0%} of pages resident, hot_rows {wl.hot_rows}")
             + ("; dense layer boundaries replayed as HIP graphs" if engine.use_graphs else "")
             + (f"; {len(engine.groups)} request groups pipelined across layers (a group's gather on a transfer "
                "stream overlaps the other groups' compute)" if engine.groups else "")
@@ -1101,6 +1108,11 @@ def run_model_workload(args, torch, device):
                    "frac_host_link": gather_bytes / (stage_ms["gather"] * 1e-3) / 1e9 / link},
         "setup_s": setup_s,
         "prefill_s": None if args.synthetic_history else prefill_s,
+        "placement": None if state.plan is None else {
+            "resident_pages_per_request": [
+                sum(int((state.plan.group((b, l)).slot >= 0).sum()) for l in range(wl.layers))
+                for b in range(wl.batch)],
+            "policy_counters": {k: int(v) for k, v in state.plan.stats.items()}},
         "hbm_copy_GBps": copy,
     }
     if not args.no_cpu_baseline:

@@ -24,10 +24,15 @@ and the next tokens (greedy) stay on the device: a step never reads back to
 the host.  The per-(request, layer) semantics are the reference's: the new
 token is appended before selection, Quest picks pages over bounds that include
 it, the resolver is bit-exact ``resolve_rows`` and attention covers the
-selected tokens.  What differs is the residency policy: resident pages are a
-fixed subset chosen when the history is built (plus every tail page), instead
-of the reference's adaptive policy (hybrid.py:204-392); hot rows follow the
-resolver's LRU exactly.
+selected tokens; hot rows follow the resolver's LRU exactly.  Residency is
+either the reference's hybrid policy (hybrid.py:204-392: every page and hot
+region placed by :class:`PlacementPlan` as the prefill and the decode write, in
+the reference engine's request-by-request order) or a seeded fixed fraction of
+each layer's pages (plus every tail page), chosen when the history is written.
+With the policy, placements follow the reference's decisions for that write
+order; the layer-major step then reads a layer's tables after every request's
+write of the step, where the reference reads each request's before the next
+request writes.
 """
 
 from __future__ import annotations
@@ -149,13 +154,25 @@ class SparseKVState:
     minimum / maximum  [L, B, C, Hkv, D] Quest bounds (+inf / -inf when empty)
     """
 
-    def __init__(self, layers, batch, max_tokens, config: CacheConfig, hot_rows, resident_pages, spare_blocks):
+    def __init__(self, layers, batch, max_tokens, config: CacheConfig, hot_rows, resident_pages, spare_blocks,
+                 policy_blocks=None, policy_window=64, policy_watermark=None):
+        """``resident_pages`` / ``spare_blocks`` size the slab of the fixed residency
+        (resident blocks, then every hot region, then blocks for the tails the decode
+        opens).  ``policy_blocks`` instead makes the slab that many blocks, placed by
+        the hybrid policy (:class:`PlacementPlan`: pages, hot regions and reuse) with
+        the resident window and watermark of :class:`HotConfig`."""
         P, Hkv, D, dev = config.page_size, config.kv_heads, config.head_dim, torch.device(config.device)
         self.layers, self.batch, self.config, self.device = layers, batch, config, dev
         self.pages = ceil(max_tokens / P)
         self.hot_rows = hot_rows
         C, L, B = self.pages, layers, batch
         hot_blocks = ceil(hot_rows / P)
+        self.plan = None
+        if policy_blocks is not None:
+            from .residency import PlacementPlan
+
+            self.plan = PlacementPlan(policy_blocks, P, hot_rows, window=policy_window, watermark=policy_watermark)
+            resident_pages, spare_blocks = policy_blocks - L * B * hot_blocks, 0
         self.blocks = resident_pages + L * B * hot_blocks + spare_blocks
         self.pool = torch.empty((self.blocks, 2, P, Hkv, D), dtype=config.dtype, device=dev)
         self.host = [pinned_empty((B * C, 2, P, Hkv, D), config.dtype) for _ in range(L)]
@@ -267,13 +284,19 @@ class SparseKVState:
             if len(tokens) > self.pages * P:
                 raise ValueError("prompt longer than the state's capacity")
             slots = []
-            for l in range(self.layers):
-                pages, blocks = self._place_residents(l, b, used, resident_fraction, seed)
-                row = np.full(used, -1, np.int64)
-                row[pages] = blocks
-                slots.append(row)
+            if self.plan is not None:
+                self.plan.reserve(b, self.pages * P, self.layers)
+            else:
+                for l in range(self.layers):
+                    pages, blocks = self._place_residents(l, b, used, resident_fraction, seed)
+                    row = np.full(used, -1, np.int64)
+                    row[pages] = blocks
+                    slots.append(row)
 
             def attend(index, q, k, v):
+                if self.plan is not None:  # the policy places this layer's pages as it writes them
+                    self.plan.write((b, index), len(k))
+                    slots.append(self.plan.group((b, index)).slot[:used].copy())
                 self.write_prompt(index, b, k, v, slots[index])
                 if observer is not None:
                     observer(index, b, k, v)
@@ -289,11 +312,39 @@ class SparseKVState:
             lengths.append(len(tokens))
         torch.cuda.synchronize(self.device)
         self.lengths = lengths
+        if self.plan is not None:
+            self._tables_from_plan()
         return torch.stack(firsts)
+
+    def _tables_from_plan(self):
+        """Resident pages, hot regions and tail blocks of every (l, b) as the policy
+        left them (pages it detached again hold -1).  A (request, layer) whose prefill
+        raised no hot demand (fewer pages than the window, the watermark never crossed)
+        takes its region now, request by request (the policy's explicit transition): the
+        decode serves every row it selects outside the resident pages from it."""
+        L, B, C = self.layers, self.batch, self.pages
+        resident = np.full((L, B, C), -1, np.int32)
+        hot = np.empty(tuple(self.hot.shape), np.int32)
+        for b in range(B):
+            for l in range(L):
+                if not self.plan.group((b, l)).hot:
+                    self.plan.transition(self.plan.group((b, l)))
+        for b in range(B):
+            for l in range(L):
+                g = self.plan.group((b, l))
+                resident[l, b] = g.slot[:C]
+                hot[l, b] = g.hot
+                self.tail_block[l][b] = int(g.slot[(g.length - 1) // self.config.page_size])
+        self.resident.copy_(torch.from_numpy(resident))
+        self.hot.copy_(torch.from_numpy(hot))
+        self.plan.detached.clear()
 
     # -- decode-step bookkeeping ---------------------------------------------------
     def open_tail_pages(self, positions):
         """Give every (l, b) whose next token starts a page a resident tail block."""
+        if self.plan is not None:
+            self._plan_decode_writes(positions)
+            return
         P, L = self.config.page_size, self.layers
         starts = [b for b, pos in enumerate(positions) if pos % P == 0]
         if not starts:
@@ -310,6 +361,30 @@ class SparseKVState:
         # one pinned upload, queued on the current stream (no host synchronisation)
         rows = torch.tensor([ls, bs, ps, blocks], dtype=torch.int64, pin_memory=True).to(self.device, non_blocking=True)
         self.resident[rows[0], rows[1], rows[2]] = rows[3].to(torch.int32)
+
+    def _plan_decode_writes(self, positions):
+        """The step's one-token writes through the policy, request by request and layer
+        by layer (the reference engine's order, engine.py:115-128).  A write into a page
+        that has rows changes no placement for a layer whose hot region is served, so
+        such steps only count the rows; a step that opens pages places them, and every
+        page the policy detaches or binds updates the resident table (one pinned upload
+        queued on the current stream)."""
+        L, B, plan = self.layers, self.batch, self.plan
+        if plan.append_within([(b, l) for b in range(B) for l in range(L)]):
+            return
+        ls, bs, ps, blocks = [], [], [], []
+        for b in range(B):
+            for l in range(L):
+                for page, block in plan.write((b, l), 1):
+                    self.tail_block[l][b] = int(block)
+                    ls.append(l), bs.append(b), ps.append(page), blocks.append(block)
+        for (b, l), page in plan.detached:
+            ls.append(l), bs.append(b), ps.append(page), blocks.append(-1)
+        plan.detached.clear()
+        if ls:  # no entry repeats: a page opened this step is a tail, never detached in it
+            rows = torch.tensor([ls, bs, ps, blocks], dtype=torch.int64, pin_memory=True)
+            rows = rows.to(self.device, non_blocking=True)
+            self.resident[rows[0], rows[1], rows[2]] = rows[3].to(torch.int32)
 
     def append_args(self, layer, positions, rows=None):
         """ctypes arrays of one layer's hs_append_rows call for the requests in ``rows``
@@ -868,8 +943,22 @@ def host_bytes_per_request(workload: DecodeWorkload, context=None, steps=None):
     return workload.layers * pages * 2 * workload.page_size * workload.kv_heads * workload.head_dim * element
 
 
-def empty_state(workload: DecodeWorkload, device, context=None, steps=None):
-    """A state sized for `context` history tokens plus `steps` decoded ones, no history yet."""
+def policy_blocks(workload: DecodeWorkload, context=None):
+    """Slab of the policy residency: ``resident_fraction`` of every history page, plus the
+    blocks the policy's admission promises each (request, layer): its hot region and the
+    two active tail pages (hybrid.py:36-37)."""
+    context = workload.context if context is None else context
+    used = ceil(context / workload.page_size)
+    groups = workload.layers * workload.batch
+    return round(workload.resident_fraction * groups * used) + groups * (ceil(workload.hot_rows / workload.page_size) + 2)
+
+
+def empty_state(workload: DecodeWorkload, device, context=None, steps=None, residency="fraction", window=64,
+                watermark=None):
+    """A state sized for `context` history tokens plus `steps` decoded ones, no history yet.
+    ``residency``: "fraction" (a seeded fraction of each layer's pages resident, chosen
+    at prefill) or "policy" (the hybrid policy places every page and hot region in a slab
+    of :func:`policy_blocks`, with the given resident window and watermark)."""
     context = workload.context if context is None else context
     steps = workload.steps if steps is None else steps
     P = workload.page_size
@@ -877,6 +966,12 @@ def empty_state(workload: DecodeWorkload, device, context=None, steps=None):
         gpu_pages=1, host_pages=1, page_size=P, kv_heads=workload.kv_heads, head_dim=workload.head_dim,
         device=str(device), dtype=workload.dtype,
     )
+    if residency == "policy":
+        return SparseKVState(workload.layers, workload.batch, context + steps, cfg, workload.hot_rows, 0, 0,
+                             policy_blocks=policy_blocks(workload, context), policy_window=window,
+                             policy_watermark=watermark)
+    if residency != "fraction":
+        raise ValueError(f"unknown residency {residency!r}")
     used = ceil(context / P)
     resident = workload.layers * workload.batch * (round(workload.resident_fraction * used) + 1)
     spare = workload.layers * workload.batch * (ceil(steps / P) + 1)

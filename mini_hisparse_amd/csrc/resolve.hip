@@ -154,6 +154,18 @@ __device__ __forceinline__ uint32_t range_mask(int64_t word, int64_t lo, int64_t
   return upto & ~((1u << a) - 1u);
 }
 
+// Division by the page size of non-negative 32-bit values (tokens, host rows, hot
+// slots are all below 2^31): a shift for a power-of-two page, else a 32-bit
+// division -- never the 64-bit division a plain int64_t quotient compiles to.
+struct PageDiv {
+  uint32_t p;
+  int shift;  // -1: not a power of two
+  __device__ explicit PageDiv(int64_t page_size) : p(static_cast<uint32_t>(page_size)) {
+    shift = (p & (p - 1)) == 0 ? __ffs(static_cast<int>(p)) - 1 : -1;
+  }
+  __device__ __forceinline__ uint32_t div(uint32_t x) const { return shift >= 0 ? x >> shift : x / p; }
+};
+
 // ---- mark: bitmaps, duplicates, resident count, needs-hot bits, host-block hash
 // LDS: selbits[wl], needs[wl]
 __global__ __launch_bounds__(RT) void resolve_mark_kernel(ResolveBatch batch) {
@@ -320,7 +332,7 @@ __global__ __launch_bounds__(RW) void resolve_tags_kernel(ResolveBatch batch) {
   if (tag < 0) return;
   const ResolveWs w = ws_of(d);
   const int64_t P = d.page_size;
-  const int32_t hp = static_cast<int32_t>(tag / P);
+  const int32_t hp = static_cast<int32_t>(PageDiv(P).div(static_cast<uint32_t>(tag)));
   const int64_t off = tag - static_cast<int64_t>(hp) * P;
   const uint32_t hmask = static_cast<uint32_t>(w.hcap - 1);
   uint32_t h = hash32(static_cast<uint32_t>(hp)) & hmask;
@@ -480,7 +492,8 @@ __device__ __forceinline__ int64_t row_of_input(const hs_resolve_desc& d, const 
   const int64_t L = d.length, P = d.page_size, S = d.hot_rows;
   if (t < 0 || t >= L) return -1;
   if (dups && bit_of(w.dupbits, t) && w.first_in[t] != static_cast<int32_t>(i)) return -1;
-  const int64_t page = t / P;
+  const PageDiv pdiv(P);
+  const int64_t page = pdiv.div(static_cast<uint32_t>(t));
   const int64_t off = t - page * P;
   const int32_t src = d.source[page];
   if (src < 0) return -1;
@@ -499,7 +512,7 @@ __device__ __forceinline__ int64_t row_of_input(const hs_resolve_desc& d, const 
     host = -1;
     return -1;
   }
-  const int64_t hb = slot / P;
+  const int64_t hb = pdiv.div(static_cast<uint32_t>(slot));
   return static_cast<int64_t>(d.hot[hb]) * P + (slot - hb * P);
 }
 

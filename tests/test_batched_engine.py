@@ -157,6 +157,51 @@ def test_prefill_writes_history_bounds_and_residents_then_decodes(gpu, resident_
     _engine_layers_match_oracle(gpu, wl, built=(model, state, firsts))
 
 
+@pytest.mark.gpu
+def test_policy_residency_places_prefill_and_decode_pages_like_the_plan(gpu):
+    """Residency by the hybrid policy: the prefill places every page and hot region as
+    the placement plan decides (checked against HybridKVCache in
+    tests/test_residency_plan.py), the slab holds each resident page's rows, hot regions
+    and resident pages never share a block; a decode that opens pages (and takes queued
+    blocks) keeps all of that and matches the oracle layer by layer."""
+    from mini_hisparse_amd.batched_engine import empty_state, random_model, random_prompts
+
+    wl = tiny(context=9 * 16 + 14, steps=6)
+    model = random_model(wl, gpu, seed=1)
+    state = empty_state(wl, gpu, residency="policy", window=4, watermark=0)
+    firsts = state.prefill(model, random_prompts(wl, gpu, seed=3), wl.resident_fraction)
+    plan = state.plan
+    assert plan.stats["hot_trigger_window"] == wl.layers * wl.batch
+    assert plan.stats["unpinned_block_reuses"] > 0  # the slab was too small for every page
+
+    def check():
+        torch.cuda.synchronize()
+        B, C, P, Hkv, D = wl.batch, state.pages, wl.page_size, wl.kv_heads, wl.head_dim
+        owners = {}
+        for b in range(B):
+            for l in range(wl.layers):
+                g = plan.group((b, l))
+                resident = state.resident[l, b].cpu().numpy()
+                np.testing.assert_array_equal(resident, g.slot[:C])
+                assert state.hot[l, b].tolist() == g.hot
+                host = state.host[l].view(B, C, 2, P, Hkv, D)[b]
+                length = state.lengths[b]
+                for page in np.flatnonzero(resident >= 0).tolist():
+                    rows = min(P, length - page * P)
+                    assert torch.equal(state.pool[int(resident[page]), :, :rows].cpu(), host[page, :, :rows])
+                    owners.setdefault(int(resident[page]), []).append(("page", b, l, page))
+                for block in g.hot:
+                    owners.setdefault(block, []).append(("hot", b, l))
+        assert all(len(v) == 1 for v in owners.values()), "a block with two owners"
+
+    check()
+    opened = plan.stats["evictions"]
+    _engine_layers_match_oracle(gpu, wl, steps=4, built=(model, state, firsts))
+    assert state.lengths[0] == wl.context + 4  # crossed a page boundary: pages opened
+    assert plan.stats["evictions"] > opened  # ... on queued blocks
+    check()
+
+
 def geometry(name, **overrides):
     """The real layer geometry of a BASELINE model workload (hidden, heads, head_dim,
     FFN, vocab, page budget, residency, hot rows) with two layers and the given batch
