@@ -1217,7 +1217,7 @@ def run_microbench(args, torch, device):
         "attention": hbm_line("attention", bytes_["attention"], ROOFLINE_KERNELS,
                               per_head_bytes=bytes_["attention_per_head"]),
         "quest_and_union": hbm_line("quest_and_union", bytes_["quest"],
-                                    ("quest_score_tile_kernel", "quest_topk_kernel", "build_union_kernel")),
+                                    ("quest_score", "quest_topk_kernel", "build_union_kernel")),
         "resolve": hbm_line("resolve", bytes_["resolver"], ("resolve_mark_kernel", "resolve_tags_kernel",
                                                             "resolve_order_kernel", "resolve_outputs_kernel")),
         "gather": {"ms": stages["gather"], "bytes": bytes_["gather"],

@@ -17,6 +17,7 @@
 // with a bit mask of those heads (the entry lists of the group attention).
 #include <algorithm>
 #include <stdlib.h>
+#include <string.h>
 
 #include "hs_common.h"
 
@@ -239,6 +240,132 @@ __global__ __launch_bounds__(QT) void quest_score_tile_kernel(QuestArgs a) {
   const int64_t p = p0 + lane;
   a.scores[(b * a.Hq + h0 + hA) * a.cmax + p] = accA;
   if (hB < nh) a.scores[(b * a.Hq + h0 + hB) * a.cmax + p] = accB;
+}
+
+// Scorer for bf16 bounds with the bound selection taken off the vector ALU.
+// For query head h and element d, max(q*lo, q*hi) is q*hi when q >= 0 and q*lo
+// otherwise, and that choice is the same for every page a wave scores: each
+// wave scores one query head, reads its query words with uniform (scalar) loads
+// and turns each sign into a byte selector.  One v_perm_b32 per (page, element)
+// then picks the bf16 half of the chosen bound and widens it to fp32 (the bf16
+// bits become the high half of the word, the low half zero), leaving one fused
+// multiply-add per element for bf16 queries (their product with a bf16 bound is
+// exact) and a multiply and an add for fp32 queries.  A query of -0 picks the
+// lower bound here and the upper one in quest_score_kernel; both products are
+// zeros, and a sum started at +0 is never -0, so adding either zero leaves it
+// unchanged.  One workgroup scores QP_PAGES pages of one KV head for a chunk of
+// up to QHEADS query heads (wave w: head w, lane l: pages l and l + 64), the
+// bound rows staged in LDS as in quest_score_tile_kernel; two workgroups per
+// CU (4 waves per SIMD).  The KV head is the fastest grid dimension, so the
+// workgroups running together read whole page rows.  Measured at the microbench
+// shape: 37.6 us per launch, against 30.3 us for the loads and LDS stores alone
+// and 26.0 us for the arithmetic alone (LDS reads, VALU and SALU each near
+// their rate: every wave reads the whole tile); tile-fastest or per-XCD grid
+// orders, several tiles per workgroup with the next tile's loads in flight,
+// and a persistent form with two heads per wave and 256-page tiles (2 waves
+// per SIMD) were all slower.  Same arithmetic and order as quest_score_kernel.
+constexpr int QP_PAGES = 128;                // pages per workgroup: two per lane
+constexpr int QP_T = 64 * QHEADS;            // one wave per query head of the chunk
+constexpr int QP_UNITS = 4;                  // 16-byte units per thread, bound and staging round
+constexpr int64_t QP_MAX_ROW_BYTES = 256;    // D <= 128: 69.6 KB of LDS, one staging round per tile
+
+__host__ __device__ constexpr int64_t qp_lds_bytes(int64_t row_bytes) { return 2 * QP_PAGES * (row_bytes + 16); }
+
+template <bool QF32, int DK>
+__global__ __launch_bounds__(QP_T, 4) void quest_score_perm_kernel(QuestArgs a) {  // 4 waves per SIMD: two workgroups per CU
+#pragma clang fp contract(off)
+  extern __shared__ __attribute__((aligned(16))) unsigned char qp_smem[];
+  const int64_t b = blockIdx.z;
+  const int64_t hchunks = (a.g + QHEADS - 1) / QHEADS;
+  const int64_t kv = blockIdx.x / hchunks, hc = blockIdx.x - kv * hchunks;
+  const int64_t count = a.count[b];
+  const int64_t p0 = static_cast<int64_t>(blockIdx.y) * QP_PAGES;
+  if (a.top >= count || p0 >= count) return;
+  const int64_t Hkv = a.Hkv;
+  const uint32_t D = DK ? static_cast<uint32_t>(DK) : static_cast<uint32_t>(a.D);
+  const uint32_t rb = D * 2u, rs = rb + 16u, upr = rb / 16u;
+  unsigned char* tlo = qp_smem;
+  unsigned char* thi = qp_smem + QP_PAGES * rs;
+  int64_t npg = count - p0;
+  if (npg > QP_PAGES) npg = QP_PAGES;
+  const uint32_t units = static_cast<uint32_t>(npg) * upr;
+  const char* lo_t = static_cast<const char*>(a.kmin[b]) + (p0 * Hkv + kv) * rb;
+  const char* hi_t = static_cast<const char*>(a.kmax[b]) + (p0 * Hkv + kv) * rb;
+  const uint32_t gstride = static_cast<uint32_t>(Hkv) * rb;  // bytes between consecutive pages
+  {
+    // one staging round (row_bytes <= 256: at most QP_UNITS * QP_T units): every
+    // thread issues its loads before its LDS stores; a unit past the tile reloads
+    // unit 0 (in bounds) and is not stored
+    u32x4 L[QP_UNITS], U[QP_UNITS];
+#pragma unroll
+    for (int k = 0; k < QP_UNITS; ++k) {
+      uint32_t u = threadIdx.x + static_cast<uint32_t>(k) * QP_T;
+      if (u >= units) u = 0;
+      const uint32_t r = u / upr, c = u - r * upr;
+      const uint64_t off = static_cast<uint64_t>(r) * gstride + c * 16u;
+      L[k] = *reinterpret_cast<const u32x4*>(lo_t + off);
+      U[k] = *reinterpret_cast<const u32x4*>(hi_t + off);
+    }
+#pragma unroll
+    for (int k = 0; k < QP_UNITS; ++k) {
+      const uint32_t u = threadIdx.x + static_cast<uint32_t>(k) * QP_T;
+      const uint32_t r = u / upr, c = u - r * upr;
+      if (u < units) {
+        *reinterpret_cast<u32x4*>(tlo + r * rs + c * 16u) = L[k];
+        *reinterpret_cast<u32x4*>(thi + r * rs + c * 16u) = U[k];
+      }
+    }
+  }
+  __syncthreads();
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: scalar query loads
+  int64_t nh = a.g - hc * QHEADS;
+  if (nh > QHEADS) nh = QHEADS;
+  if (wave >= nh) return;  // no barrier follows
+  const int64_t h = kv * a.g + hc * QHEADS + wave;
+  constexpr int QESZ = QF32 ? 4 : 2;
+  constexpr int WPU = QF32 ? 8 : 4;  // query words per 16-byte unit of the bounds (8 elements)
+  const uint32_t* qw = reinterpret_cast<const uint32_t*>(static_cast<const char*>(a.q) + (b * a.q_sb + h * a.q_sh) * QESZ);
+  const unsigned char* l0 = tlo + lane * rs;
+  const unsigned char* l1 = tlo + (lane + 64) * rs;
+  const unsigned char* u0 = thi + lane * rs;
+  const unsigned char* u1 = thi + (lane + 64) * rs;
+  float acc0 = 0.f, acc1 = 0.f;  // pages l and l + 64
+  // selector of bound element e (half e & 1 of word e >> 1): bytes 0-3 come from
+  // the lower bound's word, 4-7 from the upper's, 0x0c is a zero byte
+  auto selector = [](uint32_t qbits, int half) -> uint32_t {
+    const bool neg = static_cast<int32_t>(qbits) < 0;
+    return half ? (neg ? 0x03020c0cu : 0x07060c0cu) : (neg ? 0x01000c0cu : 0x05040c0cu);
+  };
+#pragma unroll 2
+  for (uint32_t c = 0; c < upr; ++c) {
+    const u32x4 L0 = *reinterpret_cast<const u32x4*>(l0 + c * 16u);
+    const u32x4 L1 = *reinterpret_cast<const u32x4*>(l1 + c * 16u);
+    const u32x4 U0 = *reinterpret_cast<const u32x4*>(u0 + c * 16u);
+    const u32x4 U1 = *reinterpret_cast<const u32x4*>(u1 + c * 16u);
+    uint32_t wq[WPU];
+#pragma unroll
+    for (int i = 0; i < WPU; ++i) wq[i] = qw[c * WPU + i];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const uint32_t qbits = QF32 ? wq[e] : ((e & 1) ? (wq[e >> 1] & 0xffff0000u) : (wq[e >> 1] << 16));
+      const float qf = __uint_as_float(qbits);
+      const uint32_t sel = selector(qbits, e & 1);
+      const float b0 = __uint_as_float(__builtin_amdgcn_perm(U0[e >> 1], L0[e >> 1], sel));
+      const float b1 = __uint_as_float(__builtin_amdgcn_perm(U1[e >> 1], L1[e >> 1], sel));
+      if constexpr (QF32) {
+        const float p0v = qf * b0, p1v = qf * b1;
+        acc0 = acc0 + p0v;
+        acc1 = acc1 + p1v;
+      } else {
+        acc0 = __builtin_fmaf(qf, b0, acc0);
+        acc1 = __builtin_fmaf(qf, b1, acc1);
+      }
+    }
+  }
+  float* out = a.scores + (b * a.Hq + h) * a.cmax + p0;
+  if (lane < npg) out[lane] = acc0;
+  if (lane + 64 < npg) out[lane + 64] = acc1;
 }
 
 __device__ __forceinline__ uint32_t score_key(float s) {
@@ -656,7 +783,31 @@ static int quest_topk_chunk(const void* query, int64_t q_stride_b, int64_t q_str
     bool aligned = true;
     for (int64_t i = 0; i < batch; ++i)
       aligned &= ((reinterpret_cast<uintptr_t>(minimum[i]) | reinterpret_cast<uintptr_t>(maximum[i])) & 15) == 0;
-    if (head_dim % epv == 0 && aligned && row_bytes <= QS_MAX_ROW_BYTES) {
+    // HS_QUEST_SCORER=tile keeps bf16 bounds on quest_score_tile_kernel (for comparisons)
+    static const bool perm_off = [] {
+      const char* env = getenv("HS_QUEST_SCORER");
+      return env && strcmp(env, "tile") == 0;
+    }();
+    const bool query_words = (reinterpret_cast<uintptr_t>(query) & 3) == 0 &&
+                             (query_dtype == HS_DTYPE_F32 || (q_stride_b % 2 == 0 && q_stride_h % 2 == 0));
+    if (!perm_off && kv_dtype == HS_DTYPE_BF16 && (query_dtype == HS_DTYPE_BF16 || query_dtype == HS_DTYPE_F32) &&
+        query_words && head_dim % 8 == 0 && aligned && row_bytes <= QP_MAX_ROW_BYTES) {
+      dim3 grid(static_cast<unsigned>(kv_heads * hchunks), static_cast<unsigned>(ceil_div(cmax, QP_PAGES)),
+                static_cast<unsigned>(batch));
+      const size_t lds = static_cast<size_t>(qp_lds_bytes(row_bytes));
+      const bool f32q = query_dtype == HS_DTYPE_F32;
+      if (head_dim == 128) {
+        if (f32q) hipLaunchKernelGGL((quest_score_perm_kernel<true, 128>), grid, dim3(QP_T), lds, stream, a);
+        else hipLaunchKernelGGL((quest_score_perm_kernel<false, 128>), grid, dim3(QP_T), lds, stream, a);
+      } else if (head_dim == 64) {
+        if (f32q) hipLaunchKernelGGL((quest_score_perm_kernel<true, 64>), grid, dim3(QP_T), lds, stream, a);
+        else hipLaunchKernelGGL((quest_score_perm_kernel<false, 64>), grid, dim3(QP_T), lds, stream, a);
+      } else {
+        if (f32q) hipLaunchKernelGGL((quest_score_perm_kernel<true, 0>), grid, dim3(QP_T), lds, stream, a);
+        else hipLaunchKernelGGL((quest_score_perm_kernel<false, 0>), grid, dim3(QP_T), lds, stream, a);
+      }
+      HS_CHECK_LAUNCH("quest scorer");
+    } else if (head_dim % epv == 0 && aligned && row_bytes <= QS_MAX_ROW_BYTES) {
       dim3 grid(static_cast<unsigned>(ceil_div(cmax, QS_PAGES)), static_cast<unsigned>(kv_heads * hchunks),
                 static_cast<unsigned>(batch));
       const size_t lds = static_cast<size_t>(qs_lds_bytes(row_bytes, head_dim));

@@ -9,6 +9,7 @@ tests/test_hybrid.py:59, :187-189).
 
 from __future__ import annotations
 
+import ctypes
 import json
 import os
 
@@ -276,6 +277,47 @@ def test_quest_pages_match_oracle(gpu, dtype, pages, P, kv, g, D, top, sink, len
     k = expected.shape[1]
     np.testing.assert_array_equal(sel.device_pages[:, :k].cpu().numpy(), expected)
     assert sel.positions == pages_to_positions(expected, length, P)
+
+
+@pytest.mark.parametrize(
+    "q_dtype,counts,kv,g,D",
+    [
+        (torch.bfloat16, [4096, 4000], 8, 8, 128),  # microbench geometry, a ragged second request
+        (torch.bfloat16, [8193], 4, 7, 128),  # 7B geometry: 28 q heads, 4 KV heads
+        (torch.float32, [1000, 129], 4, 7, 128),  # fp32 queries: multiply, then add
+        (torch.bfloat16, [2048, 300, 77], 2, 7, 64),  # 0.5B geometry
+        (torch.float32, [300], 1, 12, 64),  # two head chunks per KV head
+        (torch.bfloat16, [130], 3, 5, 40),  # D = 40: five 16-byte units per row
+    ],
+)
+def test_quest_scores_bit_exact(gpu, q_dtype, counts, kv, g, D):
+    """Every page score in the scorer's workspace equals the oracle's float32 sum bit for bit
+    (bf16 bounds), with exact zeros and -0 among the query values."""
+    from mini_hisparse_amd import _lib
+
+    lib = _lib.load()
+    P, B, heads = 16, len(counts), kv * g
+    bounds = [quest_bounds(11 + i, c, P, kv, D, torch.bfloat16) for i, c in enumerate(counts)]
+    q = torch.randn(B, heads, D, generator=torch.Generator().manual_seed(12)).to(q_dtype)
+    q[:, :, 3] = 0.0
+    q[:, :, 5] = -0.0
+    lo = [b[0].to(gpu) for b in bounds]
+    hi = [b[1].to(gpu) for b in bounds]
+    qg = q.to(gpu)
+    ws_bytes = lib.hs_quest_workspace_bytes(B, heads, max(counts))
+    ws = torch.full((ws_bytes // 4,), float("nan"), dtype=torch.float32, device=gpu)
+    pages = torch.empty((B, heads, 1), dtype=torch.int32, device=gpu)
+    ptrs = ctypes.c_void_p * B
+    status = lib.hs_quest_topk(
+        qg.data_ptr(), qg.stride(0), qg.stride(1), _lib.dtype_code(q_dtype),
+        ptrs(*[t.data_ptr() for t in lo]), ptrs(*[t.data_ptr() for t in hi]), _lib.dtype_code(torch.bfloat16),
+        (ctypes.c_int64 * B)(*counts), B, heads, kv, D, 1, 1, pages.data_ptr(), pages.stride(0),
+        ws.data_ptr(), ws_bytes, _lib.stream_handle(gpu))
+    _lib.check(status, "hs_quest_topk")
+    scores = ws[: B * heads * max(counts)].view(B, heads, max(counts)).cpu().numpy()
+    for i, c in enumerate(counts):
+        expected = oracle.quest_scores(q[i], bounds[i][0], bounds[i][1], c)
+        np.testing.assert_array_equal(scores[i, :, :c].view(np.uint32), expected.view(np.uint32))
 
 
 def test_quest_reference_known_answer(gpu):
