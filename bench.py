@@ -467,15 +467,19 @@ def algorithmic_bytes(w, torch):
     S, dec = w["shape"], w["dec"]
     B, e, D = dec.batch, 2, S.head_dim
     entries = int(w["dec"].entry_counts.sum().item())
-    per_head = int((w["dec"].physical >= 0).sum().item())
+    per_head = int((w["dec"].head_physical() >= 0).sum().item())
     misses = int(w["dec"].row_counts[:, 2].sum().item())
     n_union = int(w["dec"].union_count.sum().item())
     W = dec.width
     attention = entries * 2 * D * e + 8 * S.heads * W * B + 2 * S.heads * D * e * B
     attention_per_head = per_head * 2 * D * e + 8 * S.heads * W * B + 2 * S.heads * D * e * B
     quest = B * (2 * S.pages * S.kv_heads * D * e + S.heads * D * e + S.heads * S.top * 4)
+    # per request: positions (4n), source + resident of each position's page (8n), tags
+    # read and written (8S), LRU read and written (16S), miss plan (16n), union rows (8n),
+    # counts; with per-head rows also the head columns read and the rows written (16 H W)
+    head_rows = 16 * S.heads * W if dec.head_rows else 0
     resolver = sum(
-        4 * n + 8 * n + 8 * S.hot_rows + 16 * S.hot_rows + 16 * n + 8 * S.heads * W + 24
+        4 * n + 8 * n + 8 * S.hot_rows + 16 * S.hot_rows + 16 * n + 8 * n + head_rows + 24
         for n in w["dec"].union_count.tolist()
     )
     gather = misses * 2 * S.kv_heads * D * e
@@ -498,7 +502,7 @@ def cpu_baseline(torch, w, budget_s):
     host = w["host"]
     tags0, lru0 = w["tags0"].cpu().numpy(), w["lru0"].cpu().numpy()
     gpu_pages = dec.pages.cpu().numpy()
-    gpu_phys = dec.physical.cpu().numpy()
+    gpu_phys = dec.head_physical().cpu().numpy()
     gpu_out = w["out"].float().cpu()
     done = 0
     parity = {"pages_equal": True, "physical_equal": True, "max_abs_err": 0.0,

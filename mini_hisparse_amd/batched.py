@@ -44,15 +44,20 @@ class BatchedSparseDecode:
     """Quest -> union -> resolve -> gather -> attention for B requests of one layer."""
 
     def __init__(self, config, heads, top_pages, lengths, *, keep_sink=True, device="cuda", capacity_lengths=None,
-                 shared_selection=False, workspaces_from=None):
+                 shared_selection=False, workspaces_from=None, head_rows=False):
         """``capacity_lengths`` (default ``lengths``) sizes every buffer, so that later
         ``set_lengths`` calls up to those lengths (a decode run) allocate nothing.
         ``shared_selection``: every head of a request selects the same pages
         (:meth:`select_pages`), so the union is one head's selection.
         ``workspaces_from``: a decoder of the same shape whose scorer and attention
         workspaces this one reuses (decoders whose ``select`` and ``attend`` calls run
-        one after another on one stream, e.g. one decoder per layer)."""
+        one after another on one stream, e.g. one decoder per layer).
+        ``head_rows``: the resolver also writes each head's physical rows
+        (``physical``, [B, heads, width]: row_index.py:127-131).  The group attention
+        reads the union rows and the per-KV-head entry lists only, so the decode path
+        leaves them out unless asked."""
         self._workspaces_from = workspaces_from
+        self.head_rows = head_rows
         self.config = config
         self.heads = heads
         self.kv_heads = config.kv_heads
@@ -85,8 +90,8 @@ class BatchedSparseDecode:
         self.entry_masks = torch.empty((B, self.kv_heads, self.entry_capacity), dtype=i32, device=dev)
         self.entry_counts = torch.empty((B, self.kv_heads), dtype=i32, device=dev)
         self.status = torch.zeros(1, dtype=i32, device=dev)
-        self.physical = torch.empty((B, self.heads, self.width), dtype=i64, device=dev)
         self.union_physical = torch.empty((B, self.capacity), dtype=i64, device=dev)
+        self.physical = torch.empty((B, self.heads, self.width), dtype=i64, device=dev) if self.head_rows else None
         self.miss_host = torch.empty((B, self.capacity), dtype=i64, device=dev)
         self.miss_device = torch.empty((B, self.capacity), dtype=i64, device=dev)
         self.row_counts = torch.empty((B, 3), dtype=i64, device=dev)
@@ -221,16 +226,17 @@ class BatchedSparseDecode:
             d.positions = self.positions[b].data_ptr()
             d.n = self.capacity
             d.positions_i64 = 0
-            d.head_columns = self.head_columns[b].data_ptr()
-            d.heads, d.width = self.heads, self.width
-            d.hc_stride_h, d.hc_stride_w = self.head_columns.stride(1), 1
+            if self.head_rows:
+                d.head_columns = self.head_columns[b].data_ptr()
+                d.heads, d.width = self.heads, self.width
+                d.hc_stride_h, d.hc_stride_w = self.head_columns.stride(1), 1
             d.source, d.resident = t.source.data_ptr(), t.resident.data_ptr()
             d.n_pages = t.source.numel()
             d.hot, d.hot_blocks = t.hot.data_ptr(), t.hot.numel()
             d.tags, d.lru, d.hot_rows = t.tags.data_ptr(), t.lru.data_ptr(), t.tags.numel()
             d.length, d.page_size = self.lengths[b], P
-            d.physical = self.physical[b].data_ptr()
             d.union_physical = self.union_physical[b].data_ptr()
+            d.physical = self.physical[b].data_ptr() if self.head_rows else d.union_physical
             d.miss_host_rows = self.miss_host[b].data_ptr()
             d.miss_device_rows = self.miss_device[b].data_ptr()
             d.counts = self.row_counts[b].data_ptr()
@@ -298,6 +304,16 @@ class BatchedSparseDecode:
             "hs_attend_groups",
         )
         return out
+
+    def head_physical(self):
+        """[B, heads, width] physical rows of each head's columns (row_index.py:127-131):
+        the union row a column names, -1 for padding.  What ``physical`` holds with
+        ``head_rows``; torch ops on the device, for checks and byte counts."""
+        cols = self.head_columns
+        B = cols.shape[0]
+        flat = cols.clamp(min=0).reshape(B, -1)
+        rows = torch.gather(self.union_physical, 1, flat).view_as(cols)
+        return torch.where(cols >= 0, rows, torch.full_like(rows, -1))
 
     def entry_offsets(self, pool):
         """Byte offsets of the K segments `attend` reads (one per valid entry; host-side

@@ -4,29 +4,37 @@
 // The reference sorts the selected tokens and the hot tags and uses
 // searchsorted/argsort to find hits, protect them, pick least-recent victims
 // and reorder the LRU.  Nothing is sorted here.  A batch of (request, layer)
-// descriptors is resolved by four launches; the two whose work is per element
-// spread every descriptor over many workgroups, the two that need one
-// block-wide order use one workgroup per descriptor but read only bitmaps and
-// the LRU (no per-token table lookups):
+// descriptors is resolved by two launches:
 //
-//   mark    (1 WG / desc)  selected tokens become a bitmap over [0, length) in
-//                          LDS: ascending order is bit order, a duplicate input
-//                          is the atomicOr that finds its bit set (the first
-//                          input index of a duplicated token by atomicMin).
-//                          Per page with selected tokens: resident hits are
-//                          counted, host-backed non-resident tokens get a
-//                          needs-hot bit, and the page's host block is hashed to
-//                          the logical page (host row = source[page] * P + off).
-//   tags    (S/256 WGs)    each hot tag finds its logical token through the
-//                          hash; a tag whose token needs a hot row is a hit:
-//                          hit bit, the token's slot, the slot's protection bit.
-//   order   (1 WG / desc)  miss bits = needs-hot and not hit, with their
-//                          per-word prefix (miss ranks in token order) and the
-//                          counts; victims = the stable partition "unprotected,
-//                          then protected" of the LRU order; the new LRU = the
-//                          stable partition by category (untouched, filled,
-//                          hit), a slot being filled iff its victim rank is
-//                          below the miss count.  Two block-wide prefix sums.
+//   front   (1 WG / desc)  Everything that needs one order over the request, with
+//                          the token bitmaps in LDS:
+//                          - selected tokens become a bitmap over [0, length):
+//                            ascending order is bit order, a duplicate input is the
+//                            atomicOr that finds its bit set (the first input index
+//                            of a duplicated token by atomicMin);
+//                          - per page with selected tokens: resident hits are
+//                            counted and host-backed non-resident tokens get a
+//                            needs-hot bit;
+//                          - each hot tag (host row = source[page] * P + off) finds
+//                            its logical page: by subtraction when the source table
+//                            is affine (host block = base + page over every
+//                            host-backed page, the layout of a request's contiguous
+//                            host slots; detected here), else through a hash of the
+//                            needs-hot pages' host blocks.  A tag whose token needs
+//                            a hot row is a hit: hit bit, the token's slot, the
+//                            slot's protection bit;
+//                          - miss bits = needs-hot and not hit, their per-word
+//                            prefix (miss ranks in token order) and the counts;
+//                          - victims = the stable partition "unprotected, then
+//                            protected" of the LRU order, and the new LRU = the
+//                            stable partition by category (untouched, filled, hit,
+//                            hit and filled), a slot being filled iff its victim
+//                            rank is below the miss count.  The filled unprotected
+//                            slots are the first min(U, misses) unprotected ones and
+//                            the filled protected slots the first max(0, misses - U)
+//                            protected ones (U unprotected slots in all), so every
+//                            new position follows from one prefix: the unprotected
+//                            slots before the entry.
 //   outputs (n/256 + H*W/256 WGs)  per input: its physical row (the first
 //                          occurrence of a token wins), and for a miss its plan
 //                          entry and the new tag of its victim slot; per head
@@ -40,13 +48,19 @@
 
 namespace hs {
 
-constexpr int RT = 1024;      // threads of the single-workgroup phases
-constexpr int RW = 256;       // threads of the wide phases
-constexpr int RMAXB = 16;     // descriptors per launch (passed by value: 16 x 200 bytes)
-constexpr int LRU_CHUNK = 32; // hot_rows <= 32768 = RT * LRU_CHUNK
-constexpr int MARK_BATCH = 8; // pages loaded per thread before use
+constexpr int RT = 1024;       // threads of the front launch
+constexpr int RW = 256;        // threads of the outputs launch
+constexpr int NWAVES = RT / 64;
+constexpr int RMAXB = 16;      // descriptors per launch (passed by value: 16 x 200 bytes)
+constexpr int LRU_CHUNK = 32;  // hot_rows <= 32768 = RT * LRU_CHUNK
+constexpr int TAG_BATCH = 4;   // hash probes in flight per thread
+constexpr int MATCH_BATCH = 8; // tags matched per batch (needs-bit reads in flight together)
+constexpr int MARK_BATCH = 8;  // pages loaded per thread before use (long tables)
+constexpr int PAGE_REGS = 9;  // pages per thread loaded before the token walk (n_pages <= RT * PAGE_REGS)
+constexpr int ORDER_WORDS = 8; // token-bitmap words per thread held in registers
 constexpr int MARK_TILE = 512;                // inputs per wave and tile (8 per lane)
 constexpr int MARK_TILE_PAD = MARK_TILE / 8 * 9;
+constexpr uint64_t HASH_EMPTY = ~static_cast<uint64_t>(0);
 
 struct ResolveBatch {
   hs_resolve_desc d[RMAXB];
@@ -55,16 +69,13 @@ struct ResolveBatch {
 static_assert(sizeof(ResolveBatch) <= 4096, "resolver descriptors must fit the 4 KB kernel-argument block");
 
 struct ResolveWs {
-  uint32_t* needbits;  // [wl] selected, host-backed, not resident
   uint32_t* hitbits;   // [wl] needs-hot tokens with a hot tag
   uint32_t* missbits;  // [wl] needs-hot tokens without one
   uint32_t* dupbits;   // [wl] tokens given more than once
   int32_t* mprefix;    // [wl] misses in the words before this one
-  uint32_t* protbits;  // [wsw] slots holding a wanted tag
   int32_t* first_in;   // [length] first input index of a duplicated token
   int32_t* tslot;      // [length] hot slot of a hit token
-  int32_t* hkeys;      // [hcap] host block (-1 = empty)
-  int32_t* hvals;      // [hcap] logical page of that host block
+  uint64_t* hash;      // [hcap] (page << 32) | host block of needs-hot pages; all ones = empty
   int32_t* victims;    // [hot_rows] slots in victim order
   int64_t* totals;     // [4] resident hits, hot hits, misses, any duplicate
   int64_t hcap;
@@ -82,7 +93,6 @@ __host__ __device__ inline int64_t words_for(int64_t length) { return (length + 
 __host__ __device__ inline int64_t ws_layout(int64_t length, int64_t n_pages, int64_t hot_rows, ResolveWs* w,
                                              char* base) {
   const int64_t wl = words_for(length);
-  const int64_t wsw = (hot_rows + 31) / 32;
   const int64_t hcap = pow2_at_least(2 * (n_pages < 1 ? 1 : n_pages));
   int64_t off = 0;
   auto take = [&](int64_t bytes) {
@@ -94,27 +104,21 @@ __host__ __device__ inline int64_t ws_layout(int64_t length, int64_t n_pages, in
   char* p1 = take(wl * 4);
   char* p2 = take(wl * 4);
   char* p3 = take(wl * 4);
-  char* p4 = take(wl * 4);
-  char* p5 = take(wsw * 4);
-  char* p6 = take(length * 4);
-  char* p7 = take(length * 4);
-  char* p8 = take(hcap * 4);
-  char* p9 = take(hcap * 4);
-  char* p10 = take(hot_rows * 4);
-  char* p11 = take(4 * 8);
+  char* p4 = take(length * 4);
+  char* p5 = take(length * 4);
+  char* p6 = take(hcap * 8);
+  char* p7 = take(hot_rows * 4);
+  char* p8 = take(4 * 8);
   if (w) {
-    w->needbits = reinterpret_cast<uint32_t*>(p0);
-    w->hitbits = reinterpret_cast<uint32_t*>(p1);
-    w->missbits = reinterpret_cast<uint32_t*>(p2);
-    w->dupbits = reinterpret_cast<uint32_t*>(p3);
-    w->mprefix = reinterpret_cast<int32_t*>(p4);
-    w->protbits = reinterpret_cast<uint32_t*>(p5);
-    w->first_in = reinterpret_cast<int32_t*>(p6);
-    w->tslot = reinterpret_cast<int32_t*>(p7);
-    w->hkeys = reinterpret_cast<int32_t*>(p8);
-    w->hvals = reinterpret_cast<int32_t*>(p9);
-    w->victims = reinterpret_cast<int32_t*>(p10);
-    w->totals = reinterpret_cast<int64_t*>(p11);
+    w->hitbits = reinterpret_cast<uint32_t*>(p0);
+    w->missbits = reinterpret_cast<uint32_t*>(p1);
+    w->dupbits = reinterpret_cast<uint32_t*>(p2);
+    w->mprefix = reinterpret_cast<int32_t*>(p3);
+    w->first_in = reinterpret_cast<int32_t*>(p4);
+    w->tslot = reinterpret_cast<int32_t*>(p5);
+    w->hash = reinterpret_cast<uint64_t*>(p6);
+    w->victims = reinterpret_cast<int32_t*>(p7);
+    w->totals = reinterpret_cast<int64_t*>(p8);
     w->hcap = hcap;
   }
   return off;
@@ -166,29 +170,71 @@ struct PageDiv {
   __device__ __forceinline__ uint32_t div(uint32_t x) const { return shift >= 0 ? x >> shift : x / p; }
 };
 
-// ---- mark: bitmaps, duplicates, resident count, needs-hot bits, host-block hash
-// LDS: selbits[wl], needs[wl]
-__global__ __launch_bounds__(RT) void resolve_mark_kernel(ResolveBatch batch) {
+__device__ __forceinline__ int32_t wave_min_i32(int32_t v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    const int32_t o = __shfl_xor(v, off, 64);
+    v = o < v ? o : v;
+  }
+  return v;
+}
+__device__ __forceinline__ int32_t wave_max_i32(int32_t v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    const int32_t o = __shfl_xor(v, off, 64);
+    v = o > v ? o : v;
+  }
+  return v;
+}
+
+__device__ __forceinline__ int32_t lanes_below(uint64_t m) {
+  return static_cast<int32_t>(__builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m >> 32),
+                                                        __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m), 0u)));
+}
+
+// ---- front: bitmaps, hits and protection, miss ranks, victims, LRU reorder
+// (row_index.py:67-113).  LDS: bits[wl] (selected tokens, then hit tokens),
+// needs[wl], prot[wsw].
+template <bool POW2>  // page size a power of two (shifts), else 32-bit divisions
+__global__ __launch_bounds__(RT) void resolve_front_kernel(ResolveBatch batch) {
   extern __shared__ uint32_t lds[];
   __shared__ int64_t scan64[16];
+  __shared__ int32_t scan32[16];
   __shared__ int any_dup;
-  __shared__ int32_t mark_tile[(RT / 64) * MARK_TILE_PAD];
+  __shared__ int32_t base_lo, base_hi;
+  __shared__ int32_t mark_tile[NWAVES * MARK_TILE_PAD];
+  __shared__ int32_t ucnt[LRU_CHUNK * NWAVES];  // unprotected LRU entries per (row, wave), then their prefix
   const hs_resolve_desc& d = batch.d[blockIdx.x];
   const ResolveWs w = ws_of(d);
-  const int T = threadIdx.x;
-  const int64_t n = d.n, L = d.length, P = d.page_size, NP = d.n_pages, S = d.hot_rows;
+  const int T = threadIdx.x, lane = T & 63, wave = T >> 6;
+  const int64_t n = d.n, L = d.length, P = d.page_size, NP = d.n_pages;
+  const int32_t S = static_cast<int32_t>(d.hot_rows);
   const int64_t wl = words_for(L), wsw = (S + 31) / 32;
-  uint32_t* selbits = lds;
+  uint32_t* bits = lds;
   uint32_t* needs = lds + wl;
+  uint32_t* prot = lds + 2 * wl;
+  const uint32_t pshift = static_cast<uint32_t>(__ffsll(static_cast<unsigned long long>(P)) - 1);
+  auto page_of = [&](uint32_t x) -> uint32_t { return POW2 ? x >> pshift : x / static_cast<uint32_t>(P); };
 
-  for (int64_t i = T; i < 2 * wl; i += RT) lds[i] = 0u;
-  for (int64_t i = T; i < wl; i += RT) {
-    w.dupbits[i] = 0u;
-    w.hitbits[i] = 0u;
+  // the page tables of short histories are loaded now and used after the token walk
+  const bool pages_early = NP <= static_cast<int64_t>(RT) * PAGE_REGS;
+  int32_t src_e[PAGE_REGS], res_e[PAGE_REGS];  // res_e: only its sign is used
+  if (pages_early) {
+#pragma unroll
+    for (int k = 0; k < PAGE_REGS; ++k) {
+      const int64_t p = T + static_cast<int64_t>(k) * RT;
+      const int64_t pc = p < NP ? p : 0;  // unconditional loads, masked when used
+      src_e[k] = d.source[pc];
+      res_e[k] = d.resident[pc];
+    }
   }
-  for (int64_t i = T; i < wsw; i += RT) w.protbits[i] = 0u;
-  for (int64_t i = T; i < w.hcap; i += RT) w.hkeys[i] = -1;
-  if (T == 0) any_dup = 0;
+  for (int64_t i = T; i < 2 * wl + wsw; i += RT) lds[i] = 0u;
+  for (int64_t i = T; i < wl; i += RT) w.dupbits[i] = 0u;
+  if (T == 0) {
+    any_dup = 0;
+    base_lo = INT32_MAX;
+    base_hi = INT32_MIN;
+  }
   __syncthreads();
 
   // selected tokens; a bit already set means a duplicate input.  Each wave
@@ -200,13 +246,12 @@ __global__ __launch_bounds__(RT) void resolve_mark_kernel(ResolveBatch batch) {
   // it is published, is a duplicate; any input order gives the same bitmap
   // and duplicate set.
   {
-    const int lane = T & 63, wave = T >> 6;
     int32_t* tile = mark_tile + wave * MARK_TILE_PAD;
     int64_t cur = -1;
     uint32_t acc = 0u, accdup = 0u;
     auto flush = [&]() {
       if (cur < 0) return;
-      const uint32_t old = atomicOr(&selbits[cur], acc);
+      const uint32_t old = atomicOr(&bits[cur], acc);
       const uint32_t dm = accdup | (old & acc);
       if (dm) {
         atomicOr(&w.dupbits[cur], dm);
@@ -214,7 +259,7 @@ __global__ __launch_bounds__(RT) void resolve_mark_kernel(ResolveBatch batch) {
       }
     };
     constexpr int KT = MARK_TILE / 64;
-    constexpr int64_t STEP = static_cast<int64_t>(RT / 64) * MARK_TILE;
+    constexpr int64_t STEP = static_cast<int64_t>(NWAVES) * MARK_TILE;
     // one loop per position type: a per-load type branch would serialise the loads
     auto walk = [&](const auto* pos) {
       int64_t nxt[KT];  // the next tile's inputs, loaded while this one is walked
@@ -273,211 +318,292 @@ __global__ __launch_bounds__(RT) void resolve_mark_kernel(ResolveBatch batch) {
     }
   }
 
-  // per page with selected tokens: resident hits, needs-hot bits, hash host block -> page
-  const uint32_t hmask = static_cast<uint32_t>(w.hcap - 1);
+  // per page with selected tokens: resident hits and needs-hot bits; over every
+  // host-backed page of the history, the range of (host block - page)
   int64_t c_res = 0;
-  for (int64_t base = T; base < NP; base += static_cast<int64_t>(RT) * MARK_BATCH) {
-    int32_t src[MARK_BATCH], res[MARK_BATCH];
-#pragma unroll
-    for (int k = 0; k < MARK_BATCH; ++k) {
-      const int64_t p = base + static_cast<int64_t>(k) * RT;
-      const bool in = p < NP && p * P < L;
-      const int64_t pc = in ? p : 0;  // unconditional loads, masked afterwards
-      const int32_t sv = d.source[pc], rv = d.resident[pc];
-      src[k] = in ? sv : -1;
-      res[k] = in ? rv : -1;
+  int32_t my_lo = INT32_MAX, my_hi = INT32_MIN;
+  // a page size dividing 32 puts every page inside one bitmap word
+  const bool in_word = POW2 && P <= 32;
+  const uint32_t page_bits = P >= 32 ? 0xffffffffu : (1u << (P & 31)) - 1u;
+  auto page_work = [&](int64_t p, int32_t sv, int32_t rv) {
+    if (sv < 0) return;  // also pages past the history
+    const int32_t shift = sv - static_cast<int32_t>(p);  // both in [0, 2^31): no overflow
+    my_lo = shift < my_lo ? shift : my_lo;
+    my_hi = shift > my_hi ? shift : my_hi;
+    if (in_word) {
+      const uint32_t lo = static_cast<uint32_t>(p) << pshift;  // < length < 2^31
+      const uint32_t wd = lo >> 5;
+      uint32_t m = page_bits << (lo & 31);
+      if (lo + static_cast<uint32_t>(P) > static_cast<uint32_t>(L))  // the history's last page, cut at the length
+        m &= ((1u << (static_cast<uint32_t>(L) - lo)) - 1u) << (lo & 31);
+      m &= bits[wd];
+      if (!m) return;
+      if (rv >= 0) c_res += __popc(m);
+      else atomicOr(&needs[wd], m);
+      return;
     }
+    const int64_t lo = p * P;
+    const int64_t hi = lo + P < L ? lo + P : L;
+    for (int64_t wd = lo >> 5; wd <= (hi - 1) >> 5; ++wd) {
+      const uint32_t m = bits[wd] & range_mask(wd, lo, hi);
+      if (!m) continue;
+      if (rv >= 0) c_res += __popc(m);
+      else atomicOr(&needs[wd], m);
+    }
+  };
+  if (pages_early) {
 #pragma unroll
-    for (int k = 0; k < MARK_BATCH; ++k) {
-      const int64_t p = base + static_cast<int64_t>(k) * RT;
-      if (src[k] < 0) continue;  // also pages past the history
+    for (int k = 0; k < PAGE_REGS; ++k) {
+      const int64_t p = T + static_cast<int64_t>(k) * RT;
+      const bool in = p < NP && p * P < L;
+      page_work(p, in ? src_e[k] : -1, res_e[k]);
+    }
+  } else {
+    for (int64_t base = T; base < NP; base += static_cast<int64_t>(RT) * MARK_BATCH) {
+      int32_t src[MARK_BATCH], res[MARK_BATCH];
+#pragma unroll
+      for (int k = 0; k < MARK_BATCH; ++k) {
+        const int64_t p = base + static_cast<int64_t>(k) * RT;
+        const bool in = p < NP && p * P < L;
+        const int64_t pc = in ? p : 0;  // unconditional loads, masked afterwards
+        const int32_t sv = d.source[pc], rv = d.resident[pc];
+        src[k] = in ? sv : -1;
+        res[k] = in ? rv : -1;
+      }
+#pragma unroll
+      for (int k = 0; k < MARK_BATCH; ++k) page_work(base + static_cast<int64_t>(k) * RT, src[k], res[k]);
+    }
+  }
+  my_lo = wave_min_i32(my_lo);
+  my_hi = wave_max_i32(my_hi);
+  if (lane == 0) {
+    atomicMin(&base_lo, my_lo);
+    atomicMax(&base_hi, my_hi);
+  }
+  int64_t tot_res;
+  block_exclusive_sum<int64_t>(c_res, scan64, &tot_res);  // synchronises the block
+  // the hot tags (one round)
+  int32_t tg[LRU_CHUNK];
+#pragma unroll
+  for (int k = 0; k < LRU_CHUNK; ++k) {
+    const int32_t s = k * RT + T;
+    const int32_t v = d.tags[s < S ? s : 0];  // unconditional load, masked afterwards
+    tg[k] = s < S ? v : -1;
+  }
+
+  const bool affine = base_lo >= base_hi;  // one shift, or no host-backed page
+  const int64_t shift = base_hi;
+  for (int64_t i = T; i < wl; i += RT) bits[i] = 0u;  // from here on: hit tokens
+  if (!affine) {
+    // host block -> page for the pages with needs-hot tokens
+    for (int64_t i = T; i < w.hcap; i += RT) w.hash[i] = HASH_EMPTY;
+    __syncthreads();
+    const uint32_t hmask = static_cast<uint32_t>(w.hcap - 1);
+    for (int64_t p = T; p < NP; p += RT) {
+      if (p * P >= L) break;
       const int64_t lo = p * P;
       const int64_t hi = lo + P < L ? lo + P : L;
-      bool any = false;
-      for (int64_t wd = lo >> 5; wd <= (hi - 1) >> 5; ++wd) {
-        const uint32_t m = selbits[wd] & range_mask(wd, lo, hi);
-        if (!m) continue;
-        any = true;
-        if (res[k] >= 0) c_res += __popc(m);
-        else atomicOr(&needs[wd], m);
-      }
-      if (!any || res[k] >= 0) continue;
-      uint32_t h = hash32(static_cast<uint32_t>(src[k])) & hmask;
+      bool want = false;
+      for (int64_t wd = lo >> 5; wd <= (hi - 1) >> 5; ++wd) want |= (needs[wd] & range_mask(wd, lo, hi)) != 0u;
+      if (!want) continue;
+      const uint32_t sv = static_cast<uint32_t>(d.source[p]);
+      const uint64_t entry = (static_cast<uint64_t>(p) << 32) | sv;
+      uint32_t h = hash32(sv) & hmask;
       while (true) {
-        const int32_t prev = atomicCAS(&w.hkeys[h], -1, src[k]);
-        if (prev == -1) {
-          w.hvals[h] = static_cast<int32_t>(p);
-          break;
-        }
-        if (prev == src[k]) break;  // non-injective source table: first page wins
+        const uint64_t prev = atomicCAS(reinterpret_cast<unsigned long long*>(&w.hash[h]),
+                                        static_cast<unsigned long long>(HASH_EMPTY),
+                                        static_cast<unsigned long long>(entry));
+        if (prev == HASH_EMPTY || static_cast<uint32_t>(prev) == sv) break;  // inserted, or first page wins
         h = (h + 1) & hmask;
       }
     }
   }
-  int64_t tot_res;
-  block_exclusive_sum<int64_t>(c_res, scan64, &tot_res);  // synchronises the block
-  for (int64_t i = T; i < wl; i += RT) w.needbits[i] = needs[i];
-  if (T == 0) {
-    w.totals[0] = tot_res;
-    w.totals[3] = dups ? 1 : 0;
-  }
-}
+  __syncthreads();
 
-// ---- tags: hot tag lookup and protection (row_index.py:84-90)
-__global__ __launch_bounds__(RW) void resolve_tags_kernel(ResolveBatch batch) {
-  const hs_resolve_desc& d = batch.d[blockIdx.y];
-  const int64_t s = static_cast<int64_t>(blockIdx.x) * RW + threadIdx.x;
-  if (s >= d.hot_rows) return;
-  const int32_t tag = d.tags[s];
-  if (tag < 0) return;
-  const ResolveWs w = ws_of(d);
-  const int64_t P = d.page_size;
-  const int32_t hp = static_cast<int32_t>(PageDiv(P).div(static_cast<uint32_t>(tag)));
-  const int64_t off = tag - static_cast<int64_t>(hp) * P;
-  const uint32_t hmask = static_cast<uint32_t>(w.hcap - 1);
-  uint32_t h = hash32(static_cast<uint32_t>(hp)) & hmask;
-  int32_t page = -1;
-  while (true) {
-    const int32_t key = w.hkeys[h];
-    if (key == -1) break;
-    if (key == hp) {
-      page = w.hvals[h];
-      break;
+  // hot tags -> logical pages (row_index.py:84-86).  Affine source: page = host
+  // block - base.  Otherwise each tag is looked up in the hash and rewritten as
+  // the host row its page would have under base 0 (page * P + offset), or -1,
+  // so that one matching loop serves both.  32-bit token arithmetic: a page
+  // below the history's page count times the page size stays below length +
+  // page size < 2^32.
+  const uint32_t Lu = static_cast<uint32_t>(L), Pu = static_cast<uint32_t>(P);
+  const uint32_t hist_pages = static_cast<uint32_t>((L + P - 1) / P < NP ? (L + P - 1) / P : NP);
+  const uint32_t ushift = affine ? static_cast<uint32_t>(static_cast<int32_t>(shift)) : 0u;
+  if (!affine) {
+    const uint32_t hmask = static_cast<uint32_t>(w.hcap - 1);
+#pragma unroll
+    for (int k0 = 0; k0 < LRU_CHUNK; k0 += TAG_BATCH) {
+      uint64_t e[TAG_BATCH];
+      uint32_t h[TAG_BATCH], hp[TAG_BATCH];
+#pragma unroll
+      for (int j = 0; j < TAG_BATCH; ++j) {  // first probes in flight together
+        hp[j] = page_of(static_cast<uint32_t>(tg[k0 + j]));
+        h[j] = hash32(hp[j]) & hmask;
+        e[j] = tg[k0 + j] >= 0 ? w.hash[h[j]] : HASH_EMPTY;
+      }
+#pragma unroll
+      for (int j = 0; j < TAG_BATCH; ++j) {
+        while (e[j] != HASH_EMPTY && static_cast<uint32_t>(e[j]) != hp[j]) {
+          h[j] = (h[j] + 1) & hmask;
+          e[j] = w.hash[h[j]];
+        }
+        const uint32_t off = static_cast<uint32_t>(tg[k0 + j]) - hp[j] * Pu;
+        tg[k0 + j] = e[j] == HASH_EMPTY || tg[k0 + j] < 0 ? -1
+                                                          : static_cast<int32_t>(static_cast<uint32_t>(e[j] >> 32) * Pu + off);
+      }
     }
-    h = (h + 1) & hmask;
-  }
-  if (page < 0) return;
-  const int64_t t = static_cast<int64_t>(page) * P + off;
-  if (t >= d.length || !bit_of(w.needbits, t)) return;
-  atomicOr(&w.hitbits[t >> 5], 1u << (t & 31));
-  w.tslot[t] = static_cast<int32_t>(s);
-  atomicOr(&w.protbits[s >> 5], 1u << (s & 31));
-}
-
-// ---- order: miss ranks, counts, victims, LRU reorder (row_index.py:94-96, 112-113)
-// LDS: protbits[wsw]
-__global__ __launch_bounds__(RT) void resolve_order_kernel(ResolveBatch batch) {
-  extern __shared__ uint32_t prot[];
-  __shared__ int64_t scan64[16];
-  __shared__ int32_t scan32[16];
-  __shared__ int32_t rcnt[LRU_CHUNK * (RT / 64)], rbase[LRU_CHUNK * (RT / 64)];
-  __shared__ uint64_t ccnt[LRU_CHUNK * (RT / 64)];
-  const hs_resolve_desc& d = batch.d[blockIdx.x];
-  const ResolveWs w = ws_of(d);
-  const int T = threadIdx.x;
-  const int64_t L = d.length, S = d.hot_rows;
-  const int64_t wl = words_for(L), wsw = (S + 31) / 32;
-  for (int64_t i = T; i < wsw; i += RT) prot[i] = w.protbits[i];
-
-  // miss bits in token order and their per-word exclusive prefix
-  const int64_t wpt = (wl + RT - 1) / RT;
-  const int64_t w0 = static_cast<int64_t>(T) * wpt;
-  int64_t w1 = w0 + wpt;
-  if (w1 > wl) w1 = wl;
-  int64_t c_hit = 0, c_miss = 0;
-  for (int64_t wd = w0; wd < w1; ++wd) {
-    const uint32_t need = w.needbits[wd], hit = w.hitbits[wd];
-    const uint32_t miss = need & ~hit;
-    w.missbits[wd] = miss;
-    c_hit += __popc(hit);
-    c_miss += __popc(miss);
-  }
-  int64_t tot_hit, tot_miss;
-  block_exclusive_sum<int64_t>(c_hit, scan64, &tot_hit);
-  int64_t r = block_exclusive_sum<int64_t>(c_miss, scan64, &tot_miss);
-  for (int64_t wd = w0; wd < w1; ++wd) {
-    w.mprefix[wd] = static_cast<int32_t>(r);
-    r += __popc(w.needbits[wd] & ~w.hitbits[wd]);
   }
 
-  // victims: unprotected slots in LRU order, then protected ones; a slot is
-  // filled iff its victim rank is below the miss count.  LRU entry
-  // jj = q * RT + T (row q, thread T): loads and stores of a row are
-  // coalesced.  Ranks inside a wave come from ballots (mbcnt); the counts of
-  // every (row, wave) are scanned in row-major order, which is LRU order.
-  const int lane = T & 63, wave = T >> 6;
-  constexpr int NW = RT / 64;
-  const int32_t S32 = static_cast<int32_t>(S);
-  const int32_t tm = static_cast<int32_t>(tot_miss);
-  // slots are < 32768: the low 32-bit word of each int64 LRU entry holds it
+  // a tag whose token needs a hot row is a hit (row_index.py:84-90).  Batches of
+  // MATCH_BATCH tags with their needs-bit reads in flight together; the slots of
+  // a wave's 64 tags form two whole protection words, which lanes 2k and 2k + 1
+  // of the wave keep (row k) and store once at the end.
+  uint32_t myprot = 0u;
+#pragma unroll
+  for (int k0 = 0; k0 < LRU_CHUNK; k0 += MATCH_BATCH) {
+    uint32_t t[MATCH_BATCH], nw[MATCH_BATCH];
+    bool ok[MATCH_BATCH];
+#pragma unroll
+    for (int j = 0; j < MATCH_BATCH; ++j) {
+      const uint32_t tag = static_cast<uint32_t>(tg[k0 + j]);
+      const uint32_t hp = page_of(tag);
+      const uint32_t page = hp - ushift;  // a block outside the range wraps to >= 2^31
+      t[j] = POW2 ? (page << pshift) | (tag & (Pu - 1u)) : page * Pu + (tag - hp * Pu);
+      ok[j] = tg[k0 + j] >= 0 && page < hist_pages && t[j] < Lu;
+      nw[j] = needs[ok[j] ? t[j] >> 5 : 0];
+    }
+#pragma unroll
+    for (int j = 0; j < MATCH_BATCH; ++j) {
+      const int k = k0 + j;
+      const bool hit = ok[j] && ((nw[j] >> (t[j] & 31)) & 1u);
+      if (hit) {
+        atomicOr(&bits[t[j] >> 5], 1u << (t[j] & 31));
+        w.tslot[t[j]] = k * RT + T;
+      }
+      const uint64_t m = __ballot(hit);
+      myprot = (lane >> 1) == k ? ((lane & 1) ? static_cast<uint32_t>(m >> 32) : static_cast<uint32_t>(m)) : myprot;
+    }
+  }
+  {
+    const int32_t wi = (lane >> 1) * 32 + wave * 2 + (lane & 1);  // ((k * RT + wave * 64) >> 5) + half
+    if (wi < wsw) prot[wi] = myprot;
+  }
+
+  // the LRU (slots < 32768: the low word of each int64 entry), read before any
+  // is rewritten; the loads run while the miss words are counted
   const int32_t* lru_lo = reinterpret_cast<const int32_t*>(d.lru);
   int32_t slot[LRU_CHUNK];
 #pragma unroll
   for (int q = 0; q < LRU_CHUNK; ++q) {
     const int32_t jj = q * RT + T;
-    const int32_t v = lru_lo[2 * (jj < S32 ? jj : 0)];  // unconditional load, masked afterwards
-    slot[q] = jj < S32 ? v : -1;
+    const int32_t v = lru_lo[2 * (jj < S ? jj : 0)];  // unconditional load, masked afterwards
+    slot[q] = jj < S ? v : -1;
   }
-  __syncthreads();  // protection bits in LDS
-  auto below = [&](uint64_t m) -> int32_t {
-    return static_cast<int32_t>(__builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m >> 32),
-                                                          __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m), 0u)));
-  };
+
+  __syncthreads();
+
+  // miss bits in token order, their per-word exclusive prefix, the hit and miss counts
+  const int64_t wpt = (wl + RT - 1) / RT;
+  const int64_t w0 = static_cast<int64_t>(T) * wpt;
+  const int64_t w1 = w0 + wpt < wl ? w0 + wpt : wl;
+  int64_t c_hit = 0, c_miss = 0;
+  int64_t tot_hit, tot_miss;
+  if (wpt <= ORDER_WORDS) {
+    uint32_t miss[ORDER_WORDS];
+#pragma unroll
+    for (int k = 0; k < ORDER_WORDS; ++k) {
+      const int64_t wd = w0 + k;
+      const bool in = wd < w1;
+      const uint32_t hit = in ? bits[wd] : 0u;
+      miss[k] = in ? needs[wd] & ~hit : 0u;
+      c_hit += __popc(hit);
+      c_miss += __popc(miss[k]);
+      if (in) {
+        w.hitbits[wd] = hit;
+        w.missbits[wd] = miss[k];
+      }
+    }
+    block_exclusive_sum<int64_t>(c_hit, scan64, &tot_hit);
+    int64_t r = block_exclusive_sum<int64_t>(c_miss, scan64, &tot_miss);
+#pragma unroll
+    for (int k = 0; k < ORDER_WORDS; ++k) {
+      if (w0 + k < w1) w.mprefix[w0 + k] = static_cast<int32_t>(r);
+      r += __popc(miss[k]);
+    }
+  } else {
+    for (int64_t wd = w0; wd < w1; ++wd) {
+      const uint32_t hit = bits[wd], miss = needs[wd] & ~hit;
+      w.hitbits[wd] = hit;
+      w.missbits[wd] = miss;
+      c_hit += __popc(hit);
+      c_miss += __popc(miss);
+    }
+    block_exclusive_sum<int64_t>(c_hit, scan64, &tot_hit);
+    int64_t r = block_exclusive_sum<int64_t>(c_miss, scan64, &tot_miss);
+    for (int64_t wd = w0; wd < w1; ++wd) {
+      w.mprefix[wd] = static_cast<int32_t>(r);
+      r += __popc(needs[wd] & ~bits[wd]);
+    }
+  }
+
+  // victims and the new LRU (row_index.py:94-96, 112-113).  LRU entry
+  // jj = q * RT + T (row q, thread T): ranks inside a wave come from ballots,
+  // the counts of every (row, wave) are scanned in row-major order (LRU order).
   uint32_t protmask = 0u;  // bit q: entry of row q is protected
 #pragma unroll
-  for (int q = 0; q < LRU_CHUNK; ++q) {
-    const int32_t jj = q * RT + T;
-    const bool pr = jj < S32 && bit_of(prot, slot[q]);
-    protmask |= static_cast<uint32_t>(pr) << q;
-    const uint64_t up = __ballot(jj < S32 && !pr);
-    if (lane == 0) rcnt[q * NW + wave] = static_cast<int32_t>(__popcll(up));
+  for (int q0 = 0; q0 < LRU_CHUNK; q0 += MATCH_BATCH) {
+    uint32_t pw[MATCH_BATCH];
+#pragma unroll
+    for (int j = 0; j < MATCH_BATCH; ++j) pw[j] = prot[static_cast<uint32_t>(slot[q0 + j] < 0 ? 0 : slot[q0 + j]) >> 5];
+#pragma unroll
+    for (int j = 0; j < MATCH_BATCH; ++j) {
+      const int q = q0 + j;
+      const int32_t jj = q * RT + T;
+      const bool pr = jj < S && ((pw[j] >> (slot[q] & 31)) & 1u);
+      protmask |= static_cast<uint32_t>(pr) << q;
+      const uint64_t up = __ballot(jj < S && !pr);
+      if (lane == 0) ucnt[q * NWAVES + wave] = static_cast<int32_t>(__popcll(up));
+    }
   }
   __syncthreads();
-  int32_t total_unprot;
+  int32_t U;  // unprotected slots
   {
-    const int32_t v = T < LRU_CHUNK * NW ? rcnt[T] : 0;
-    const int32_t ex = block_exclusive_sum<int32_t>(v, scan32, &total_unprot);
-    if (T < LRU_CHUNK * NW) rbase[T] = ex;
+    const int32_t v = T < LRU_CHUNK * NWAVES ? ucnt[T] : 0;
+    const int32_t ex = block_exclusive_sum<int32_t>(v, scan32, &U);
+    if (T < LRU_CHUNK * NWAVES) ucnt[T] = ex;
   }
   __syncthreads();
-  uint64_t catbits = 0u;  // two bits per row: filled, protected
+  const int32_t tm = tot_miss < S ? static_cast<int32_t>(tot_miss) : S;  // only rank < tm matters
+  const int32_t Pn = S - U;
+  const int32_t fillU = U < tm ? U : tm;
+  const int32_t fillP = tm - U > 0 ? (tm - U < Pn ? tm - U : Pn) : 0;
+  const int32_t start1 = U - fillU, start2 = U, start3 = S - fillP;
 #pragma unroll
   for (int q = 0; q < LRU_CHUNK; ++q) {
     const int32_t jj = q * RT + T;
-    const bool in = jj < S32;
+    const bool in = jj < S;
     const bool pr = (protmask >> q) & 1u;
     const uint64_t up = __ballot(in && !pr);
-    const int32_t ubefore = rbase[q * NW + wave] + below(up);  // unprotected entries before jj
-    const int32_t rank = pr ? total_unprot + (jj - ubefore) : ubefore;
-    const int cat = static_cast<int>(rank < tm) + 2 * static_cast<int>(pr);
-    if (in) w.victims[rank] = slot[q];
-    catbits |= static_cast<uint64_t>(cat) << (2 * q);
-    uint64_t packed = 0;
-#pragma unroll
-    for (int c = 0; c < 4; ++c)
-      packed |= static_cast<uint64_t>(__popcll(__ballot(in && cat == c))) << (16 * c);
-    if (lane == 0) ccnt[q * NW + wave] = packed;
-  }
-  __syncthreads();
-  uint64_t ctotal;
-  {
-    const uint64_t v = T < LRU_CHUNK * NW ? ccnt[T] : 0;
-    const uint64_t ex = block_exclusive_sum<uint64_t>(v, reinterpret_cast<uint64_t*>(scan64), &ctotal);
-    if (T < LRU_CHUNK * NW) ccnt[T] = ex;
-  }
-  __syncthreads();
-  const auto field = [](uint64_t v, int c) { return static_cast<int32_t>((v >> (16 * c)) & 0xffffu); };
-  const int32_t start1 = field(ctotal, 0);
-  const int32_t start2 = start1 + field(ctotal, 1);
-  const int32_t start3 = start2 + field(ctotal, 2);
-  // every thread has read its LRU entries (the barriers above)
-#pragma unroll
-  for (int q = 0; q < LRU_CHUNK; ++q) {
-    const int32_t jj = q * RT + T;
-    const bool in = jj < S32;
-    const int cat = static_cast<int>((catbits >> (2 * q)) & 3u);
-    const uint64_t base = ccnt[q * NW + wave];
-    int32_t at = 0;
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const uint64_t m = __ballot(in && cat == c);
-      if (cat == c) at = (c == 0 ? 0 : c == 1 ? start1 : c == 2 ? start2 : start3) + field(base, c) + below(m);
+    const int32_t r = ucnt[q * NWAVES + wave] + lanes_below(up);  // unprotected entries before jj
+    if (in) {
+      int32_t rank, at;
+      if (!pr) {
+        rank = r;
+        at = r < fillU ? start1 + r : r - fillU;
+      } else {
+        const int32_t pj = jj - r;  // protected entries before jj
+        rank = U + pj;
+        at = pj < fillP ? start3 + pj : start2 + (pj - fillP);
+      }
+      w.victims[rank] = slot[q];
+      d.lru[at] = slot[q];
     }
-    if (in) d.lru[at] = slot[q];
   }
   if (T == 0) {
+    w.totals[0] = tot_res;
     w.totals[1] = tot_hit;
     w.totals[2] = tot_miss;
+    w.totals[3] = dups ? 1 : 0;
   }
 }
 
@@ -567,10 +693,11 @@ __global__ __launch_bounds__(RW) void resolve_outputs_kernel(ResolveBatch batch)
   d.physical[k] = r;
 }
 
-static int64_t mark_lds_bytes(int64_t length) { return 2 * words_for(length) * 4; }
-static int64_t order_lds_bytes(int64_t hot_rows) { return (hot_rows + 31) / 32 * 4; }
+static int64_t front_lds_bytes(int64_t length, int64_t hot_rows) {
+  return (2 * words_for(length) + (hot_rows + 31) / 32) * 4;
+}
 
-constexpr int64_t kMaxResolverLds = 150 * 1024;
+constexpr int64_t kMaxResolverLds = 112 * 1024;  // dynamic LDS of the front launch (its tiles use ~39 KB more)
 
 static int validate_desc(const hs_resolve_desc& d) {
   HS_CHECK_ARG(d.positions && d.n >= 1, "logical top-k must be a nonempty device integer vector");
@@ -583,7 +710,8 @@ static int validate_desc(const hs_resolve_desc& d) {
   HS_CHECK_ARG(d.hot_rows >= 1 && d.hot_rows <= RT * LRU_CHUNK, "hot_rows must be in [1, 32768]");
   HS_CHECK_ARG(d.hot_blocks * d.page_size >= d.hot_rows, "hot block table does not cover hot_rows");
   HS_CHECK_ARG(d.length < (static_cast<int64_t>(1) << 31), "length too large");
-  HS_CHECK_ARG(mark_lds_bytes(d.length) <= kMaxResolverLds,
+  HS_CHECK_ARG(d.n_pages < (static_cast<int64_t>(1) << 31), "too many pages");
+  HS_CHECK_ARG(front_lds_bytes(d.length, d.hot_rows) <= kMaxResolverLds,
                "length %lld too large for the LDS token bitmaps", static_cast<long long>(d.length));
   if (d.head_columns) HS_CHECK_ARG(d.heads >= 1 && d.width >= 1, "head columns must be a nonempty matrix");
   return HS_OK;
@@ -615,7 +743,7 @@ static int64_t batch_workspace(const hs_resolve_desc* descs, int32_t count) {
   return need;
 }
 
-// The four launches over validated descriptors; `workspace` holds the batch's need.
+// The two launches over validated descriptors; `workspace` holds the batch's need.
 static int resolve_launch(const hs_resolve_desc* descs, int32_t count, char* workspace, hipStream_t stream);
 
 extern "C" int hs_resolve_rows_batched(const hs_resolve_desc* descs, int32_t count, void* workspace,
@@ -630,7 +758,9 @@ extern "C" int hs_resolve_rows_batched(const hs_resolve_desc* descs, int32_t cou
 static int resolve_launch(const hs_resolve_desc* descs, int32_t count, char* workspace, hipStream_t stream) {
   static bool attr_set = false;
   if (!attr_set) {
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(resolve_mark_kernel),
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(resolve_front_kernel<true>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kMaxResolverLds));
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(resolve_front_kernel<false>),
                               hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kMaxResolverLds));
     (void)hipGetLastError();
     attr_set = true;
@@ -639,26 +769,22 @@ static int resolve_launch(const hs_resolve_desc* descs, int32_t count, char* wor
   for (int32_t start = 0; start < count; start += RMAXB) {
     ResolveBatch batch{};
     batch.count = count - start < RMAXB ? count - start : RMAXB;
-    int64_t mark_lds = 0, order_lds = 0, max_s = 0, max_out = 0;
+    int64_t front_lds = 0, max_out = 0;
+    bool pow2 = true;  // every descriptor's page size a power of two
     for (int i = 0; i < batch.count; ++i) {
       hs_resolve_desc& d = batch.d[i];
       d = descs[start + i];
       d.workspace = ws;
       ws += hs_resolve_workspace_bytes(d.n, d.length, d.n_pages, d.hot_rows);
-      if (mark_lds_bytes(d.length) > mark_lds) mark_lds = mark_lds_bytes(d.length);
-      if (order_lds_bytes(d.hot_rows) > order_lds) order_lds = order_lds_bytes(d.hot_rows);
-      if (d.hot_rows > max_s) max_s = d.hot_rows;
+      if (front_lds_bytes(d.length, d.hot_rows) > front_lds) front_lds = front_lds_bytes(d.length, d.hot_rows);
+      pow2 &= (d.page_size & (d.page_size - 1)) == 0;
       const int64_t outs = d.n + (d.head_columns ? d.heads * d.width : 0);
       if (outs > max_out) max_out = outs;
     }
     const unsigned nb = static_cast<unsigned>(batch.count);
-    hipLaunchKernelGGL(resolve_mark_kernel, dim3(nb), dim3(RT), static_cast<size_t>(mark_lds), stream, batch);
-    HS_CHECK_LAUNCH("resolver mark");
-    hipLaunchKernelGGL(resolve_tags_kernel, dim3(static_cast<unsigned>(ceil_div(max_s, RW)), nb), dim3(RW), 0,
-                       stream, batch);
-    HS_CHECK_LAUNCH("resolver tags");
-    hipLaunchKernelGGL(resolve_order_kernel, dim3(nb), dim3(RT), static_cast<size_t>(order_lds), stream, batch);
-    HS_CHECK_LAUNCH("resolver order");
+    if (pow2) hipLaunchKernelGGL(resolve_front_kernel<true>, dim3(nb), dim3(RT), static_cast<size_t>(front_lds), stream, batch);
+    else hipLaunchKernelGGL(resolve_front_kernel<false>, dim3(nb), dim3(RT), static_cast<size_t>(front_lds), stream, batch);
+    HS_CHECK_LAUNCH("resolver front");
     hipLaunchKernelGGL(resolve_outputs_kernel, dim3(static_cast<unsigned>(ceil_div(max_out, RW)), nb), dim3(RW),
                        0, stream, batch);
     HS_CHECK_LAUNCH("resolver outputs");
@@ -675,8 +801,9 @@ extern "C" int hs_resolve_rows(const hs_resolve_desc* desc, void* workspace, int
 // For callers that cannot allocate (code under graph capture, serving loops,
 // harnesses that forbid hipMalloc): the workspace is this file-scope device
 // array, one copy per GPU, held until the process ends.  The resolver's kernels
-// clear every part of the workspace they read before reading it (the mark
-// launch resets the bitmaps, the protection bits and the host-block hash), so
+// clear every part of the workspace they read before reading it (the front
+// launch resets the duplicate bits and, when it builds one, the host-block hash;
+// every other part is written before it is read), so
 // nothing is left over from an earlier call; calls that overlap on one GPU
 // (two streams, or two host threads) share the array and race.
 namespace hs {

@@ -32,14 +32,24 @@ def random_rows(heads, width, max_row, seed, invalid=0.1):
 
 
 def resolver_tables(seed, length, page_size, hot_rows, resident_frac=0.5, tag_frac=0.6,
-                    host_pages=None):
+                    host_pages=None, affine_base=None, foreign_tags=0):
     """Consistent per-(request, layer) tables: injective source, fragmented hot
-    blocks, unique tags that cache host rows of non-resident pages."""
+    blocks, unique tags that cache host rows of non-resident pages.
+
+    ``affine_base``: the source table is ``base + page`` (a request's contiguous host
+    slots) with a few host-less pages; ``foreign_tags``: that many empty tag slots
+    then hold host rows of blocks outside the request's range (other requests' rows)."""
     rng = np.random.default_rng(seed)
     n_pages = ceil(length / page_size) + int(rng.integers(0, 3))
     host_pages = host_pages or (n_pages * 3 + 7)
-    source = rng.permutation(host_pages)[:n_pages].astype(np.int32)
     materialized = ceil(length / page_size)
+    if affine_base is None:
+        source = rng.permutation(host_pages)[:n_pages].astype(np.int32)
+    else:
+        source = (affine_base + np.arange(n_pages)).astype(np.int32)
+        holes = rng.random(n_pages) < 0.03
+        holes[0] = False
+        source[holes] = -1
     source[materialized:] = -1
     blocks_total = n_pages + ceil(hot_rows / page_size) + 5
     block_perm = rng.permutation(blocks_total)
@@ -63,6 +73,15 @@ def resolver_tables(seed, length, page_size, hot_rows, resident_frac=0.5, tag_fr
         chosen = rng.choice(len(candidates), size=k, replace=False)
         slots = rng.choice(hot_rows, size=k, replace=False)
         tags[slots] = np.asarray(candidates, dtype=np.int64)[chosen]
+    if foreign_tags:
+        free = np.flatnonzero(tags < 0)[:foreign_tags]
+        lo_block = int(source[source >= 0].min()) if (source >= 0).any() else 0
+        hi_block = int(source.max()) + 1
+        for j, slot in enumerate(free):  # blocks just below and just above the request's range
+            step = j // page_size
+            below = j % 2 == 0 and lo_block - 1 - step >= 0
+            block = lo_block - 1 - step if below else hi_block + step
+            tags[slot] = block * page_size + j % page_size
     lru = rng.permutation(hot_rows).astype(np.int64)
     return dict(source=source, resident=resident, hot=hot, tags=tags, lru=lru)
 

@@ -80,7 +80,8 @@ def _run_layer(gpu, *, B, Hkv, g, D, pages, length, top, hot_rows, resident_frac
     bounds = [_bounds(host[b * pages : (b + 1) * pages], length, P) for b in range(B)]
     cfg = CacheConfig(gpu_pages=blocks, host_pages=B * pages, page_size=P, kv_heads=Hkv, head_dim=D,
                       device=gpu, dtype=dtype)
-    dec = BatchedSparseDecode(cfg, heads, top, [length] * B, device=dev, shared_selection=selector == "uniform")
+    dec = BatchedSparseDecode(cfg, heads, top, [length] * B, device=dev, shared_selection=selector == "uniform",
+                              head_rows=True)
     assert hot_rows >= dec.capacity, "the hot region must cover the union bound"
     tables = [LayerTablesView(*[torch.from_numpy(t[k]).to(dev) for k in ("source", "resident", "hot", "tags", "lru")])
               for t in tables_np]

@@ -170,6 +170,25 @@ def test_resolver_random_matches_oracle(gpu, seed, length, P, S, n, res_frac):
     _assert_plan(plan32, tags32, lru32, expected)
 
 
+@pytest.mark.parametrize(
+    "seed,length,P,S,n,res_frac,base",
+    [
+        (30, 97, 4, 64, 40, 0.5, 0),
+        (31, 4096, 16, 2048, 1500, 0.5, 1000),
+        (32, 131072, 16, 32768, 27808, 0.15, 3 * 8193),  # 7B shape: the fourth request's host slots
+        (33, 300, 7, 128, 100, 0.0, 5),
+    ],
+)
+def test_resolver_affine_source_matches_oracle(gpu, seed, length, P, S, n, res_frac, base):
+    """Source tables of contiguous host slots (host block = base + page, a few host-less
+    pages) take the resolver's subtraction path; tags of other requests' host rows never hit."""
+    tables = resolver_tables(seed, length, P, S, resident_frac=res_frac, affine_base=base, foreign_tags=40)
+    positions = random_positions(seed + 100, n, length)
+    expected = oracle.resolve_rows(positions, *[tables[k] for k in ("source", "resident", "hot", "tags", "lru")], length, P)
+    plan, tags, lru = _resolve_gpu(gpu, tables, positions, length, P)
+    _assert_plan(plan, tags, lru, expected)
+
+
 def test_resolver_batched_descriptors_match_oracle(gpu):
     """hs_resolve_rows_batched over 17 (request, layer) descriptors of different sizes: one
     launch of 16 descriptors and one of 1; every output of every request equals the oracle."""
