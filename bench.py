@@ -474,12 +474,16 @@ def algorithmic_bytes(w, torch):
     attention = entries * 2 * D * e + 8 * S.heads * W * B + 2 * S.heads * D * e * B
     attention_per_head = per_head * 2 * D * e + 8 * S.heads * W * B + 2 * S.heads * D * e * B
     quest = B * (2 * S.pages * S.kv_heads * D * e + S.heads * D * e + S.heads * S.top * 4)
-    # per request: positions (4n), source + resident of each position's page (8n), tags
-    # read and written (8S), LRU read and written (16S), miss plan (16n), union rows (8n),
-    # counts; with per-head rows also the head columns read and the rows written (16 H W)
+    # per request, over the n selected tokens and the C-entry position array (the union,
+    # padded with -1 to the batch's capacity): positions read (4C), source + resident of
+    # each selected token's page (8n), tags read and written (8S), LRU read and written
+    # (16S), the miss plan (16C: the misses, then -1, as the reference's fixed-width plan)
+    # and the union rows (8C) written, counts; with per-head rows also the head columns
+    # read and the rows written (16 H W)
     head_rows = 16 * S.heads * W if dec.head_rows else 0
+    C = dec.capacity
     resolver = sum(
-        4 * n + 8 * n + 8 * S.hot_rows + 16 * S.hot_rows + 16 * n + 8 * n + head_rows + 24
+        4 * C + 8 * n + 8 * S.hot_rows + 16 * S.hot_rows + 16 * C + 8 * C + head_rows + 24
         for n in w["dec"].union_count.tolist()
     )
     gather = misses * 2 * S.kv_heads * D * e
@@ -1222,8 +1226,7 @@ def run_microbench(args, torch, device):
                               per_head_bytes=bytes_["attention_per_head"]),
         "quest_and_union": hbm_line("quest_and_union", bytes_["quest"],
                                     ("quest_score", "quest_topk_kernel", "build_union_kernel")),
-        "resolve": hbm_line("resolve", bytes_["resolver"], ("resolve_mark_kernel", "resolve_tags_kernel",
-                                                            "resolve_order_kernel", "resolve_outputs_kernel")),
+        "resolve": hbm_line("resolve", bytes_["resolver"], ("resolve_front_kernel", "resolve_outputs_kernel")),
         "gather": {"ms": stages["gather"], "bytes": bytes_["gather"],
                    "GBps": bytes_["gather"] / (stages["gather"] * 1e-3) / 1e9,
                    "host_link_memcpy_GBps": link,
