@@ -193,6 +193,17 @@ def ptr(tensor) -> int:
 
 
 def stream_handle(device=None) -> int:
+    """Handle of the current stream of ``device`` (default: the current device): the stream
+    torch's own work on that device is queued on.  Read without building a Stream object
+    (which costs more than a kernel launch)."""
     import torch
 
-    return torch.cuda.current_stream(device).cuda_stream
+    if isinstance(device, torch.device):
+        index = device.index
+    elif device is None or isinstance(device, int):
+        index = device
+    else:
+        index = torch.device(device).index
+    if index is None:
+        index = torch.cuda.current_device()
+    return torch._C._cuda_getCurrentRawStream(index)

@@ -40,6 +40,14 @@ class LayerTablesView:
     lru: torch.Tensor  # [hot_rows] int64 (updated)
 
 
+def _handle(stream, device):
+    """Stream handle of ``stream``: a torch Stream, a raw handle (int), or None for the
+    current stream of ``device``."""
+    if stream is None:
+        return _lib.stream_handle(device)
+    return stream if isinstance(stream, int) else stream.cuda_stream
+
+
 class BatchedSparseDecode:
     """Quest -> union -> resolve -> gather -> attention for B requests of one layer."""
 
@@ -150,7 +158,7 @@ class BatchedSparseDecode:
         if q.stride(-1) != 1:  # read by the kernel in its dtype
             q = q.contiguous()
         lib = _lib.load()
-        s = stream.cuda_stream if stream is not None else _lib.stream_handle(self.device)
+        s = _handle(stream, self.device)
         key = tuple(map(id, minimums)) + tuple(map(id, maximums))
         hit = self._bounds.get(key)
         if hit is None or not all(a is b for a, b in zip(hit[0], (*minimums, *maximums))):
@@ -184,7 +192,7 @@ class BatchedSparseDecode:
                 if ((row < 0) | (row >= count)).any() or (row[1:] <= row[:-1]).any() or row[-1] != count - 1:
                     raise ValueError(f"request {b}: pages must be {k} ascending distinct pages below {count}, "
                                      f"the tail page {count - 1} last")
-        s = stream.cuda_stream if stream is not None else _lib.stream_handle(self.device)
+        s = _handle(stream, self.device)
         self.pages.copy_(pages[:, None, :].expand(self.batch, self.heads, self.top))
         self._build_union(s)
 
@@ -256,7 +264,7 @@ class BatchedSparseDecode:
         for b in range(self.batch):
             descs[b].length = self.lengths[b]
             descs[b].row_stats = stats
-        s = stream.cuda_stream if stream is not None else _lib.stream_handle(self.device)
+        s = _handle(stream, self.device)
         _lib.check(
             _lib.load().hs_resolve_rows_batched(descs, self.batch, self.resolve_ws.data_ptr(), self.resolve_ws_bytes, s),
             "hs_resolve_rows_batched",
@@ -278,7 +286,7 @@ class BatchedSparseDecode:
         _lib.check(
             lib.hs_gather_rows_batched(hosts[0], pool.data_ptr(), mh, md, mc, ns, hosts[1],
                                        pool.shape[0] * cfg.page_size, B, cfg.page_size, row_bytes, grid_x,
-                                       stream.cuda_stream),
+                                       _handle(stream, self.device)),
             "hs_gather_rows_batched",
         )
 
@@ -290,7 +298,7 @@ class BatchedSparseDecode:
         if out is None:
             out = torch.empty_like(q)
         lib = _lib.load()
-        s = stream.cuda_stream if stream is not None else _lib.stream_handle(self.device)
+        s = _handle(stream, self.device)
         _lib.check(
             lib.hs_attend_groups(
                 q.data_ptr(), q.stride(0), q.stride(1), pool.data_ptr(), _lib.dtype_code(pool.dtype),
@@ -334,7 +342,7 @@ class BatchedSparseDecode:
         """Read-only pass over the K and V segments at `offsets` (diagnostic ceiling)."""
         cfg = self.config
         esz = pool.element_size()
-        s = stream.cuda_stream if stream is not None else _lib.stream_handle(self.device)
+        s = _handle(stream, self.device)
         _lib.check(
             _lib.load().hs_probe_row_reads(
                 pool.data_ptr(), pool.numel() * esz, offsets.data_ptr(), offsets.numel(), cfg.head_dim * esz,

@@ -48,7 +48,8 @@ from torch.nn import functional as F
 from . import _lib
 from .batched import BatchedSparseDecode, LayerTablesView
 from .dense import (
-    add_rms_norm, gemm_workspace_bytes, linear_supported, linear_swiglu_tiled, linear_tiled, rotary_split, silu_mul,
+    add_rms_norm, gemm_workspace_bytes, linear_supported, linear_swiglu_tiled, linear_tiled, prepare_add_rms_norm,
+    prepare_linear_swiglu_tiled, prepare_linear_tiled, prepare_rotary_split, prepare_silu_mul, rotary_split, silu_mul,
     tile_gate_up, tile_weight,
 )
 from .config import CacheConfig
@@ -189,6 +190,7 @@ class SparseKVState:
         self.next_spare = resident_pages + L * B * hot_blocks
         self.lengths = [0] * B
         self.tail_block = [[-1] * B for _ in range(L)]  # device block of each (l, b) tail page
+        self._append_arrays = {}  # layer -> the ctypes arrays of its whole-batch hs_append_rows call
         self.tables = [
             [LayerTablesView(self.source[l, b], self.resident[l, b], self.hot[l, b], self.tags[l, b], self.lru[l, b])
              for b in range(B)]
@@ -388,17 +390,26 @@ class SparseKVState:
 
     def append_args(self, layer, positions, rows=None):
         """ctypes arrays of one layer's hs_append_rows call for the requests in ``rows``
-        (a range; default every request)."""
+        (a range; default every request).  Every request's call reuses one set of arrays
+        per layer, filled in place (the previous call's launch has read them: ctypes
+        passes them to the library, which copies them into the launch's arguments)."""
         P, B, C = self.config.page_size, self.batch, self.pages
         Hkv, D = self.config.kv_heads, self.config.head_dim
         esz = self.minimum.element_size()
         page_elems = Hkv * D
         rows = range(B) if rows is None else rows
         n = len(rows)
-        dev_rows = (ctypes.c_int64 * n)()
-        host_rows = (ctypes.c_int64 * n)()
-        lo = (ctypes.c_void_p * n)()
-        hi = (ctypes.c_void_p * n)()
+        if n == B:
+            arrays = self._append_arrays.get(layer)
+            if arrays is None:
+                arrays = self._append_arrays[layer] = (
+                    (ctypes.c_int64 * B)(), (ctypes.c_int64 * B)(), (ctypes.c_void_p * B)(), (ctypes.c_void_p * B)())
+            dev_rows, host_rows, lo, hi = arrays
+        else:
+            dev_rows = (ctypes.c_int64 * n)()
+            host_rows = (ctypes.c_int64 * n)()
+            lo = (ctypes.c_void_p * n)()
+            hi = (ctypes.c_void_p * n)()
         base_lo, base_hi = self.minimum.data_ptr(), self.maximum.data_ptr()
         for i, b in enumerate(rows):
             page, off = divmod(positions[b], P)
@@ -505,6 +516,7 @@ class BatchedDecodeEngine:
         self._static_buffers()
         self.use_graphs = graphs and all(self.projection_kernel[n] for n in ("qkv", "o_proj", "gate_up", "down"))
         self._graphs = None
+        self._prepared = None  # per layer boundary, its bound dense launches (built on first use)
 
     def decoder(self, layer):
         """The decoder (selection, resolver and attention buffers) that serves `layer`."""
@@ -580,6 +592,50 @@ class BatchedDecodeEngine:
             self._dense_out(index - 1)
         if index < L:
             self._dense_in(index, first=index == 0)
+
+    def _projection_launch(self, name, x, weight, out, bias=None):
+        """A bound launch of ``_project`` into ``out`` (the kernel's, or PyTorch's GEMM, which
+        runs on torch's current stream: the stream the step's launches take)."""
+        if self.projection_kernel[name]:
+            return prepare_linear_tiled(x, self._tiles[weight.data_ptr()], weight.shape[0], bias, out, self._gemm_ws)
+        return lambda stream: out.copy_(F.linear(x, weight, bias))
+
+    def _prepare_boundaries(self):
+        """Per layer boundary, the dense launches of ``_boundary`` for the whole batch with
+        every argument bound: the same launches, without re-validating and re-packing
+        their arguments on every step (the host's time per launch is what paces a step of a
+        small model)."""
+        cfg = self.model.config
+        layers = self.model.model.layers
+        L = len(layers)
+        eps = cfg.rms_norm_eps
+        boundaries = []
+        for index in range(L + 1):
+            calls = []
+            if index > 0:
+                layer = layers[index - 1]
+                _, _, gate_up_w = self._packed[index - 1]
+                attn = self._attn_out.view(self._attn_out.shape[0], -1)
+                calls.append(self._projection_launch("o_proj", attn, layer.self_attn.o_proj.weight, self._o))
+                calls.append(prepare_add_rms_norm(self._x, self._o, layer.post_attention_layernorm.weight, eps, self._h))
+                if self.projection_kernel["gate_up"]:
+                    calls.append(prepare_linear_swiglu_tiled(self._h, self._tiles[gate_up_w.data_ptr()],
+                                                             cfg.intermediate_size, self._act))
+                else:
+                    calls.append(self._projection_launch("gate_up", self._h, gate_up_w, self._gate_up))
+                    calls.append(prepare_silu_mul(self._gate_up, self._act))
+                calls.append(self._projection_launch("down", self._act, layer.mlp.down_proj.weight, self._delta))
+            if index < L:
+                layer = layers[index]
+                qkv_w, qkv_b, _ = self._packed[index]
+                calls.append(prepare_add_rms_norm(self._x, None if index == 0 else self._delta,
+                                                  layer.input_layernorm.weight, eps, self._h))
+                calls.append(self._projection_launch("qkv", self._h, qkv_w, self._qkv, qkv_b))
+                calls.append(prepare_rotary_split(self._qkv, self.positions, cfg.num_attention_heads,
+                                                  cfg.num_key_value_heads, cfg.head_dim, cfg.rope_theta,
+                                                  (self._q, self._k, self._v)))
+            boundaries.append(calls)
+        return boundaries
 
     @torch.no_grad()
     def _capture(self):
@@ -698,8 +754,9 @@ class BatchedDecodeEngine:
         out.copy_(y)
         return out
 
-    def _append(self, layer, k, v, positions, rows=None):
-        """Each request's new K/V row (``rows``: a range of requests, default all)."""
+    def _append(self, layer, k, v, positions, rows=None, handle=None):
+        """Each request's new K/V row (``rows``: a range of requests, default all), on the
+        stream ``handle`` (default: the current stream)."""
         st, cfg = self.state, self.state.config
         rows = range(st.batch) if rows is None else rows
         dev_rows, host_rows, lo, hi = st.append_args(layer, positions, rows)
@@ -708,7 +765,7 @@ class BatchedDecodeEngine:
                 k[rows.start].data_ptr(), v[rows.start].data_ptr(), k.stride(0), st.pool.data_ptr(),
                 st.blocks * cfg.page_size, _lib.dtype_code(cfg.dtype), cfg.page_size, cfg.kv_heads, cfg.head_dim,
                 dev_rows, self._host_alias[layer], host_rows, st.host[layer].shape[0] * cfg.page_size, lo, hi,
-                len(rows), _lib.stream_handle(self.device),
+                len(rows), handle if handle is not None else _lib.stream_handle(self.device),
             ),
             "hs_append_rows",
         )
@@ -764,10 +821,19 @@ class BatchedDecodeEngine:
             prefetched = [self._prefetch(i, sampled, self.transfer, mark) for i in range(min(L, self.PREFETCH_AHEAD))]
         self._x.copy_(model.model.embed_tokens(tokens))
         graphs = self._graphs
+        handle = _lib.stream_handle(self.device)  # the compute stream, looked up once per step
+        prepared = None
+        if graphs is None:
+            if self._prepared is None:
+                self._prepared = self._prepare_boundaries()
+            prepared = self._prepared
 
         def boundary(index):
             if graphs is not None:
                 graphs[index].replay()
+            elif prepared is not None:
+                for launch in prepared[index]:
+                    launch(handle)
             else:
                 self._boundary(index)
 
@@ -779,7 +845,7 @@ class BatchedDecodeEngine:
             boundary(index)
             marks["dense"].append(mark(compute))
             marks["append"] = [marks["dense"][1]]
-            self._append(index, k, v, positions)
+            self._append(index, k, v, positions, handle=handle)
             lo, hi = st.bounds[index]
             marks["append"].append(mark(compute))
             if prefetched is not None:
@@ -789,12 +855,12 @@ class BatchedDecodeEngine:
             else:
                 marks["select"] = [marks["append"][1]]
                 if sampled is None:
-                    dec.select(q, lo, hi)
+                    dec.select(q, lo, hi, stream=handle)
                 else:
-                    dec.select_pages(sampled[index], validate=False)  # uniform_pages: ascending, tail last
+                    dec.select_pages(sampled[index], stream=handle, validate=False)  # uniform_pages: ascending, tail last
                 marks["select"].append(mark(compute))
                 marks["resolve"] = [marks["select"][1]]
-                dec.resolve(st.tables[index], row_stats=st.row_stats)
+                dec.resolve(st.tables[index], row_stats=st.row_stats, stream=handle)
                 marks["resolve"].append(mark(compute))
                 transfer = self.transfer if self.transfer is not None else compute
                 if transfer is not compute:
@@ -802,7 +868,7 @@ class BatchedDecodeEngine:
                     resolved.record(compute)
                     transfer.wait_event(resolved)
                 marks["gather"] = [mark(transfer)]
-                dec.gather(st.alias[index], st.pool, transfer)
+                dec.gather(st.alias[index], st.pool, transfer if transfer is not compute else handle)
                 marks["gather"].append(mark(transfer))
                 if transfer is not compute:
                     ready.record(transfer)
@@ -810,7 +876,7 @@ class BatchedDecodeEngine:
             marks["attend"] = [mark(compute)]
             if probe is not None:
                 probe.before_attend(index, compute, dec)
-            out = dec.attend(q, st.pool, out=self._attn_out)
+            out = dec.attend(q, st.pool, out=self._attn_out, stream=handle)
             if probe is not None:
                 probe.after_attend(index, compute, dec)
             marks["attend"].append(mark(compute))

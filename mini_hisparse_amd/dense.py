@@ -22,6 +22,21 @@ def _stream(tensor):
     return _lib.stream_handle(tensor.device)
 
 
+class Launch:
+    """One library call with every argument bound but the stream (a ``prepare_*`` result):
+    ``launch(stream_handle)`` issues it.  The tensors it names must outlive it."""
+
+    __slots__ = ("fn", "args", "what")
+
+    def __init__(self, fn, args, what):
+        self.fn, self.args, self.what = fn, args, what
+
+    def __call__(self, stream):
+        status = self.fn(*self.args, stream)
+        if status:
+            _lib.check(status, self.what)
+
+
 _WORKSPACE = {}
 _GEMM_WS_BYTES = {}
 
@@ -109,9 +124,15 @@ def tile_weight(weight):
     return padded.reshape(rows // 16, 16, k // 32, 32).transpose(1, 2).contiguous()
 
 
-def linear_tiled(x, tiles, n, bias=None, out=None, workspace=None):
-    """:func:`linear` with the weight as :func:`tile_weight` packed it (``n`` its rows):
-    the same arithmetic in the same order, so the same bits."""
+def _linear_tiled_launch(x, tiles, n, bias, y, ws):
+    k = x.shape[1]
+    return Launch(_lib.load().hs_skinny_gemm_tiled,
+                  (x.data_ptr(), x.stride(0), tiles.data_ptr(), n, k, _lib.ptr(bias), y.data_ptr(), y.stride(0),
+                   x.shape[0], _lib.dtype_code(x.dtype), ws.data_ptr(), ws.numel()),
+                  "hs_skinny_gemm_tiled")
+
+
+def _linear_tiled_check(x, tiles, n, bias, out):
     k = x.shape[1] if x.dim() == 2 else -1
     if not (
         x.dim() == 2 and 1 <= x.shape[0] <= 16 and k % 32 == 0 and k > 0 and n >= 1
@@ -122,20 +143,28 @@ def linear_tiled(x, tiles, n, bias=None, out=None, workspace=None):
         raise ValueError("linear_tiled takes 1-16 rows of a bf16/f16 x (K a multiple of 32) and tile_weight's packing")
     if bias is not None and (bias.shape != (n,) or bias.dtype != x.dtype or not bias.is_contiguous()):
         raise ValueError("bias must be [N] contiguous in the dtype of x")
-    rows = x.shape[0]
-    _check_out(out, (rows, n), x, "linear_tiled")
+    _check_out(out, (x.shape[0], n), x, "linear_tiled")
+
+
+def linear_tiled(x, tiles, n, bias=None, out=None, workspace=None):
+    """:func:`linear` with the weight as :func:`tile_weight` packed it (``n`` its rows):
+    the same arithmetic in the same order, so the same bits."""
+    _linear_tiled_check(x, tiles, n, bias, out)
+    rows, k = x.shape
     y = torch.empty((rows, n), dtype=x.dtype, device=x.device) if out is None else out
-    lib = _lib.load()
     stream = _stream(x)
     ws = _workspace(x.device, stream, gemm_workspace_bytes(rows, n, k), workspace)
-    _lib.check(
-        lib.hs_skinny_gemm_tiled(
-            x.data_ptr(), x.stride(0), tiles.data_ptr(), n, k, _lib.ptr(bias), y.data_ptr(), y.stride(0), rows,
-            _lib.dtype_code(x.dtype), ws.data_ptr(), ws.numel(), stream,
-        ),
-        "hs_skinny_gemm_tiled",
-    )
+    _linear_tiled_launch(x, tiles, n, bias, y, ws)(stream)
     return y
+
+
+def prepare_linear_tiled(x, tiles, n, bias, out, workspace):
+    """:func:`linear_tiled` into ``out`` with the caller's ``workspace``, bound once."""
+    _linear_tiled_check(x, tiles, n, bias, out)
+    if out is None:
+        raise ValueError("prepare_linear_tiled writes into a given out")
+    ws = _workspace(x.device, None, gemm_workspace_bytes(x.shape[0], n, x.shape[1]), workspace)
+    return _linear_tiled_launch(x, tiles, n, bias, out, ws)
 
 
 def tile_gate_up(gate_up, ffn):
@@ -147,13 +176,7 @@ def tile_gate_up(gate_up, ffn):
     return torch.stack((gate, up), 1).reshape(2 * gate.shape[0], *gate.shape[1:]).contiguous()
 
 
-def linear_swiglu_tiled(x, tiles, ffn, out=None):
-    """``silu(x @ gate.T) * (x @ up.T)`` from :func:`tile_gate_up`'s packing, in one launch
-    with one K slice.  It has the bits of :func:`linear_tiled` on the packed weight
-    followed by :func:`silu_mul` whenever that GEMM also runs in one K slice
-    (``gemm_workspace_bytes(rows, 2 * ffn, K)`` at its minimum of 256, with the default
-    rounds of 8 k-steps); where the GEMM plans split-K (few output rows, long K) the
-    sums are the same up to fp32 summation order."""
+def _swiglu_check(x, tiles, ffn, out):
     k = x.shape[1] if x.dim() == 2 else -1
     if not (
         x.dim() == 2 and 1 <= x.shape[0] <= 16 and k % 32 == 0 and k > 0 and ffn >= 1
@@ -163,22 +186,38 @@ def linear_swiglu_tiled(x, tiles, ffn, out=None):
     ):
         raise ValueError("linear_swiglu_tiled takes 1-16 rows of a bf16/f16 x (K a multiple of 32) and "
                          "tile_gate_up's packing")
-    rows = x.shape[0]
-    _check_out(out, (rows, ffn), x, "linear_swiglu_tiled")
-    y = torch.empty((rows, ffn), dtype=x.dtype, device=x.device) if out is None else out
-    _lib.check(
-        _lib.load().hs_skinny_gemm_swiglu_tiled(
-            x.data_ptr(), x.stride(0), tiles.data_ptr(), ffn, k, y.data_ptr(), y.stride(0), rows,
-            _lib.dtype_code(x.dtype), _stream(x),
-        ),
-        "hs_skinny_gemm_swiglu_tiled",
-    )
+    _check_out(out, (x.shape[0], ffn), x, "linear_swiglu_tiled")
+
+
+def _swiglu_launch(x, tiles, ffn, y):
+    return Launch(_lib.load().hs_skinny_gemm_swiglu_tiled,
+                  (x.data_ptr(), x.stride(0), tiles.data_ptr(), ffn, x.shape[1], y.data_ptr(), y.stride(0),
+                   x.shape[0], _lib.dtype_code(x.dtype)),
+                  "hs_skinny_gemm_swiglu_tiled")
+
+
+def linear_swiglu_tiled(x, tiles, ffn, out=None):
+    """``silu(x @ gate.T) * (x @ up.T)`` from :func:`tile_gate_up`'s packing, in one launch
+    with one K slice.  It has the bits of :func:`linear_tiled` on the packed weight
+    followed by :func:`silu_mul` whenever that GEMM also runs in one K slice
+    (``gemm_workspace_bytes(rows, 2 * ffn, K)`` at its minimum of 256, with the default
+    rounds of 8 k-steps); where the GEMM plans split-K (few output rows, long K) the
+    sums are the same up to fp32 summation order."""
+    _swiglu_check(x, tiles, ffn, out)
+    y = torch.empty((x.shape[0], ffn), dtype=x.dtype, device=x.device) if out is None else out
+    _swiglu_launch(x, tiles, ffn, y)(_stream(x))
     return y
 
 
-def add_rms_norm(x, delta, weight, eps, out=None):
-    """RMSNorm of ``x`` [rows, width] (of ``x + delta`` when ``delta`` is given, and then
-    ``x`` is updated in place to the sum).  Returns the normalised rows."""
+def prepare_linear_swiglu_tiled(x, tiles, ffn, out):
+    """:func:`linear_swiglu_tiled` into ``out``, bound once."""
+    _swiglu_check(x, tiles, ffn, out)
+    if out is None:
+        raise ValueError("prepare_linear_swiglu_tiled writes into a given out")
+    return _swiglu_launch(x, tiles, ffn, out)
+
+
+def _rms_check(x, delta, weight, out):
     if x.dim() != 2 or x.stride(1) != 1:
         raise ValueError("x must be [rows, width] with unit inner stride")
     if delta is not None and (delta.shape != x.shape or delta.stride() != x.stride() or delta.dtype != x.dtype):
@@ -186,58 +225,103 @@ def add_rms_norm(x, delta, weight, eps, out=None):
     if weight.shape != (x.shape[1],) or weight.dtype != x.dtype:
         raise ValueError("weight must be [width] in the dtype of x")
     _check_out(out, x.shape, x, "add_rms_norm")
+
+
+def _rms_launch(x, delta, weight, eps, y):
+    return Launch(_lib.load().hs_add_rms_norm,
+                  (x.data_ptr(), _lib.ptr(delta), x.data_ptr() if delta is not None else None, y.data_ptr(),
+                   weight.data_ptr(), x.shape[0], x.shape[1], x.stride(0), y.stride(0), float(eps),
+                   _lib.dtype_code(x.dtype)),
+                  "hs_add_rms_norm")
+
+
+def add_rms_norm(x, delta, weight, eps, out=None):
+    """RMSNorm of ``x`` [rows, width] (of ``x + delta`` when ``delta`` is given, and then
+    ``x`` is updated in place to the sum).  Returns the normalised rows."""
+    _rms_check(x, delta, weight, out)
     y = torch.empty_like(x) if out is None else out
-    _lib.check(
-        _lib.load().hs_add_rms_norm(
-            x.data_ptr(), _lib.ptr(delta), x.data_ptr() if delta is not None else None, y.data_ptr(),
-            weight.data_ptr(), x.shape[0], x.shape[1], x.stride(0), y.stride(0), float(eps),
-            _lib.dtype_code(x.dtype), _stream(x),
-        ),
-        "hs_add_rms_norm",
-    )
+    _rms_launch(x, delta, weight, eps, y)(_stream(x))
     return y
+
+
+def prepare_add_rms_norm(x, delta, weight, eps, out):
+    """:func:`add_rms_norm` into ``out``, bound once."""
+    _rms_check(x, delta, weight, out)
+    if out is None:
+        raise ValueError("prepare_add_rms_norm writes into a given out")
+    return _rms_launch(x, delta, weight, eps, out)
+
+
+def _rotary_check(qkv, positions, heads, kv_heads, head_dim, out):
+    rows = qkv.shape[0]
+    if qkv.dim() != 2 or qkv.stride(1) != 1 or qkv.shape[1] != (heads + 2 * kv_heads) * head_dim:
+        raise ValueError("qkv must be [rows, (heads + 2 kv_heads) head_dim] with unit inner stride")
+    if positions.dtype != torch.int64 or positions.shape != (rows,) or positions.device != qkv.device:
+        raise ValueError("positions must be int64 [rows] on the device of qkv")
+    if out is not None:
+        q, k, v = out
+        _check_out(q, (rows, heads, head_dim), qkv, "rotary_split q")
+        _check_out(k, (rows, kv_heads, head_dim), qkv, "rotary_split k")
+        _check_out(v, (rows, kv_heads, head_dim), qkv, "rotary_split v")
+
+
+def _rotary_launch(qkv, positions, heads, kv_heads, head_dim, theta, q, k, v):
+    return Launch(_lib.load().hs_rotary_split,
+                  (qkv.data_ptr(), qkv.stride(0), q.data_ptr(), k.data_ptr(), v.data_ptr(), positions.data_ptr(),
+                   qkv.shape[0], heads, kv_heads, head_dim, float(theta), _lib.dtype_code(qkv.dtype)),
+                  "hs_rotary_split")
 
 
 def rotary_split(qkv, positions, heads, kv_heads, head_dim, theta, out=None):
     """Split a packed projection ``qkv`` [rows, (heads + 2 kv_heads) head_dim] into q
     [rows, heads, head_dim], k and v [rows, kv_heads, head_dim], with q and k rotated
     at ``positions`` [rows] (int64, device)."""
+    _rotary_check(qkv, positions, heads, kv_heads, head_dim, out)
     rows = qkv.shape[0]
-    if qkv.dim() != 2 or qkv.stride(1) != 1 or qkv.shape[1] != (heads + 2 * kv_heads) * head_dim:
-        raise ValueError("qkv must be [rows, (heads + 2 kv_heads) head_dim] with unit inner stride")
-    if positions.dtype != torch.int64 or positions.shape != (rows,) or positions.device != qkv.device:
-        raise ValueError("positions must be int64 [rows] on the device of qkv")
     if out is None:
         q = torch.empty((rows, heads, head_dim), dtype=qkv.dtype, device=qkv.device)
         k = torch.empty((rows, kv_heads, head_dim), dtype=qkv.dtype, device=qkv.device)
         v = torch.empty_like(k)
     else:
         q, k, v = out
-        _check_out(q, (rows, heads, head_dim), qkv, "rotary_split q")
-        _check_out(k, (rows, kv_heads, head_dim), qkv, "rotary_split k")
-        _check_out(v, (rows, kv_heads, head_dim), qkv, "rotary_split v")
-    _lib.check(
-        _lib.load().hs_rotary_split(
-            qkv.data_ptr(), qkv.stride(0), q.data_ptr(), k.data_ptr(), v.data_ptr(), positions.data_ptr(), rows,
-            heads, kv_heads, head_dim, float(theta), _lib.dtype_code(qkv.dtype), _stream(qkv),
-        ),
-        "hs_rotary_split",
-    )
+    _rotary_launch(qkv, positions, heads, kv_heads, head_dim, theta, q, k, v)(_stream(qkv))
     return q, k, v
+
+
+def prepare_rotary_split(qkv, positions, heads, kv_heads, head_dim, theta, out):
+    """:func:`rotary_split` into ``out`` = (q, k, v), bound once (``positions`` is read
+    when the launch runs)."""
+    _rotary_check(qkv, positions, heads, kv_heads, head_dim, out)
+    if out is None:
+        raise ValueError("prepare_rotary_split writes into a given out")
+    return _rotary_launch(qkv, positions, heads, kv_heads, head_dim, theta, *out)
+
+
+def _silu_check(gate_up, out):
+    if gate_up.dim() != 2 or gate_up.stride(1) != 1 or gate_up.shape[1] % 2:
+        raise ValueError("gate_up must be [rows, 2 width] with unit inner stride")
+    _check_out(out, (gate_up.shape[0], gate_up.shape[1] // 2), gate_up, "silu_mul")
+
+
+def _silu_launch(gate_up, y):
+    return Launch(_lib.load().hs_silu_mul,
+                  (gate_up.data_ptr(), gate_up.stride(0), y.data_ptr(), y.stride(0), gate_up.shape[0],
+                   gate_up.shape[1] // 2, _lib.dtype_code(gate_up.dtype)),
+                  "hs_silu_mul")
 
 
 def silu_mul(gate_up, out=None):
     """silu(gate) * up of a packed ``gate_up`` [rows, 2 width] -> [rows, width]."""
-    if gate_up.dim() != 2 or gate_up.stride(1) != 1 or gate_up.shape[1] % 2:
-        raise ValueError("gate_up must be [rows, 2 width] with unit inner stride")
+    _silu_check(gate_up, out)
     rows, width = gate_up.shape[0], gate_up.shape[1] // 2
-    _check_out(out, (rows, width), gate_up, "silu_mul")
     y = torch.empty((rows, width), dtype=gate_up.dtype, device=gate_up.device) if out is None else out
-    _lib.check(
-        _lib.load().hs_silu_mul(
-            gate_up.data_ptr(), gate_up.stride(0), y.data_ptr(), y.stride(0), rows, width,
-            _lib.dtype_code(gate_up.dtype), _stream(gate_up),
-        ),
-        "hs_silu_mul",
-    )
+    _silu_launch(gate_up, y)(_stream(gate_up))
     return y
+
+
+def prepare_silu_mul(gate_up, out):
+    """:func:`silu_mul` into ``out``, bound once."""
+    _silu_check(gate_up, out)
+    if out is None:
+        raise ValueError("prepare_silu_mul writes into a given out")
+    return _silu_launch(gate_up, out)
