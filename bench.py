@@ -195,7 +195,7 @@ def build_workload(args, torch, device):
     pool = torch.empty((blocks, 2, P, Hkv, D), dtype=torch.bfloat16, device=device)
     perm = np.random.default_rng(args.seed + 1).permutation(B * HB) + n_resident_blocks
     tags_all = torch.full((B, S.hot_rows), -1, dtype=torch.int32, device=device)
-    lru_all = torch.empty((B, S.hot_rows), dtype=torch.int64, device=device)
+    lru_all = torch.empty((B, S.hot_rows), dtype=torch.int16, device=device)  # the engine's LRU dtype
     tables = []
     next_block = 0
     stats = {"union_rows": 0, "resident_rows": 0, "hot_rows": 0, "miss_rows": 0}
@@ -213,7 +213,7 @@ def build_workload(args, torch, device):
         tags = np.full(S.hot_rows, -1, np.int32)
         tags[slots] = host_rows
         tags_all[b] = torch.from_numpy(tags).to(device)
-        lru_all[b] = torch.from_numpy(rng.permutation(S.hot_rows)).to(device)
+        lru_all[b] = torch.from_numpy(rng.permutation(S.hot_rows).astype(np.int16)).to(device)
         slot_t = torch.from_numpy(slots).to(device)
         phys = hot[slot_t // P].long() * P + slot_t % P
         tok = torch.from_numpy(hot_tokens).to(device)
@@ -477,13 +477,14 @@ def algorithmic_bytes(w, torch):
     # per request, over the n selected tokens and the C-entry position array (the union,
     # padded with -1 to the batch's capacity): positions read (4C), source + resident of
     # each selected token's page (8n), tags read and written (8S), LRU read and written
-    # (16S), the miss plan (16C: the misses, then -1, as the reference's fixed-width plan)
+    # (2 x its element size x S), the miss plan (16C: the misses, then -1, as the reference's fixed-width plan)
     # and the union rows (8C) written, counts; with per-head rows also the head columns
     # read and the rows written (16 H W)
     head_rows = 16 * S.heads * W if dec.head_rows else 0
     C = dec.capacity
+    lru_bytes = 2 * w["lru_all"].element_size() * S.hot_rows
     resolver = sum(
-        4 * C + 8 * n + 8 * S.hot_rows + 16 * S.hot_rows + 16 * C + 8 * C + head_rows + 24
+        4 * C + 8 * n + 8 * S.hot_rows + lru_bytes + 16 * C + 8 * C + head_rows + 24
         for n in w["dec"].union_count.tolist()
     )
     gather = misses * 2 * S.kv_heads * D * e

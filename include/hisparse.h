@@ -139,7 +139,7 @@ typedef struct hs_resolve_desc {
   const void* positions;        /* [n] logical tokens, int32 or int64 */
   int64_t n;
   int32_t positions_i64;        /* 1 = int64 positions, 0 = int32 */
-  int32_t reserved0;
+  int32_t lru_i16;              /* 1 = lru holds int16 slots, 0 = int64 (the reference's dtype) */
   const int64_t* head_columns;  /* nullable [heads, width] union columns, -1 padded */
   int64_t heads, width, hc_stride_h, hc_stride_w;
   const int32_t* source;        /* [n_pages] host page of each logical page, -1 = none */
@@ -148,7 +148,7 @@ typedef struct hs_resolve_desc {
   const int32_t* hot;           /* [hot_blocks] device block of each hot block */
   int64_t hot_blocks;
   int32_t* tags;                /* [hot_rows] in/out: host row held by each hot slot, -1 = empty */
-  int64_t* lru;                 /* [hot_rows] in/out: slots, least recent first */
+  void* lru;                    /* [hot_rows] in/out: slots, least recent first */
   int64_t hot_rows;             /* <= 32768 (hybrid.py:34) */
   int64_t length, page_size;    /* length <= n_pages * page_size */
   int64_t* physical;            /* out [n], or [heads, width] contiguous when head_columns */

@@ -26,7 +26,7 @@ class ResolveDesc(ctypes.Structure):
         ("positions", c_void_p),
         ("n", c_int64),
         ("positions_i64", c_int32),
-        ("reserved0", c_int32),
+        ("lru_i16", c_int32),
         ("head_columns", c_void_p),
         ("heads", c_int64),
         ("width", c_int64),

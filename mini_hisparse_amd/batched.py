@@ -37,7 +37,7 @@ class LayerTablesView:
     resident: torch.Tensor  # [pages] int32
     hot: torch.Tensor  # [hot_blocks] int32
     tags: torch.Tensor  # [hot_rows] int32 (updated)
-    lru: torch.Tensor  # [hot_rows] int64 (updated)
+    lru: torch.Tensor  # [hot_rows] int64, or int16 (a quarter of the resolver's LRU bytes) (updated)
 
 
 def _handle(stream, device):
@@ -241,7 +241,10 @@ class BatchedSparseDecode:
             d.source, d.resident = t.source.data_ptr(), t.resident.data_ptr()
             d.n_pages = t.source.numel()
             d.hot, d.hot_blocks = t.hot.data_ptr(), t.hot.numel()
+            if t.lru.dtype not in (torch.int16, torch.int64):
+                raise TypeError(f"lru must be int16 or int64, got {t.lru.dtype}")
             d.tags, d.lru, d.hot_rows = t.tags.data_ptr(), t.lru.data_ptr(), t.tags.numel()
+            d.lru_i16 = int(t.lru.dtype == torch.int16)
             d.length, d.page_size = self.lengths[b], P
             d.union_physical = self.union_physical[b].data_ptr()
             d.physical = self.physical[b].data_ptr() if self.head_rows else d.union_physical

@@ -151,7 +151,7 @@ class SparseKVState:
     pool      device [blocks, 2, P, Hkv, D]: resident pages, hot regions, spare
               blocks for the tail pages the decode opens
     source    int32 [L, B, C]    resident int32 [L, B, C] (-1 = host only)
-    hot       int32 [L, B, S/P]  tags int32 [L, B, S]  lru int64 [L, B, S]
+    hot       int32 [L, B, S/P]  tags int32 [L, B, S]  lru int16 [L, B, S]
     minimum / maximum  [L, B, C, Hkv, D] Quest bounds (+inf / -inf when empty)
     """
 
@@ -183,7 +183,7 @@ class SparseKVState:
         self.first_hot = resident_pages  # resident blocks are [0, first_hot)
         self.hot = (torch.arange(L * B * hot_blocks, dtype=torch.int32, device=dev) + self.first_hot).view(L, B, hot_blocks)
         self.tags = torch.full((L, B, hot_rows), -1, dtype=torch.int32, device=dev)
-        self.lru = torch.arange(hot_rows, dtype=torch.int64, device=dev).repeat(L * B).view(L, B, hot_rows)
+        self.lru = torch.arange(hot_rows, dtype=torch.int16, device=dev).repeat(L * B).view(L, B, hot_rows)
         self.minimum = torch.full((L, B, C, Hkv, D), float("inf"), dtype=config.dtype, device=dev)
         self.maximum = torch.full((L, B, C, Hkv, D), float("-inf"), dtype=config.dtype, device=dev)
         self.next_resident = 0

@@ -565,8 +565,9 @@ __global__ __launch_bounds__(64 * attend_waves(DP)) void attend_mfma_kernel(Atte
 
   const int ntiles = (cnt + 31) / 32;
   // K fragments (A operand: lane holds K[row 16rt + c][d = 32kk + 8j .. +8]) and the
-  // V rows this lane stages (CPR 16-byte chunks of rows vi * RPI + lane / LPR) of
-  // tile t.  Loads are unconditional and their results are used as loaded, so that
+  // V rows this lane stages (CPR 16-byte chunks of rows vi * RPI + lane / LPR: chunk
+  // cc * LPR + lane % LPR, so that the LPR lanes of a row read 16 * LPR contiguous bytes
+  // per instruction, one L1 access instead of LPR) of tile t.  Loads are unconditional and their results are used as loaded, so that
   // the loads of a tile stay in flight until the tile is processed: a masked entry
   // reads the lane's query row instead (in bounds, finite).  That data never reaches
   // the output: a masked entry's score is -inf (probability 0, so its V contributes
@@ -591,7 +592,7 @@ __global__ __launch_bounds__(64 * attend_waves(DP)) void attend_mfma_kernel(Atte
     for (int vi = 0; vi < VI; ++vi) {
       const int li = 32 * t + vi * RPI + lane / LPR;
       const int64_t koff = s_koff[li < ACH ? li : 0];
-      ad.v[vi] = li < cnt && koff >= 0 ? pool + koff + vplane + 8 * CPR * (lane % LPR) : qrow;
+      ad.v[vi] = li < cnt && koff >= 0 ? pool + koff + vplane + 8 * (lane % LPR) : qrow;
     }
     return ad;
   };
@@ -604,7 +605,7 @@ __global__ __launch_bounds__(64 * attend_waves(DP)) void attend_mfma_kernel(Atte
 #pragma unroll
     for (int vi = 0; vi < VI; ++vi) {
 #pragma unroll
-      for (int cc = 0; cc < CPR; ++cc) vr[vi][cc] = load16(ad.v[vi] + 8 * cc);
+      for (int cc = 0; cc < CPR; ++cc) vr[vi][cc] = load16(ad.v[vi] + 8 * LPR * cc);
     }
   };
 
@@ -615,7 +616,7 @@ __global__ __launch_bounds__(64 * attend_waves(DP)) void attend_mfma_kernel(Atte
       const int row = vi * RPI + lane / LPR;
 #pragma unroll
       for (int cc = 0; cc < CPR; ++cc)
-        *reinterpret_cast<u32x4*>(vs + row * RS + 8 * CPR * (lane % LPR) + 8 * cc) = vr[vi][cc];
+        *reinterpret_cast<u32x4*>(vs + row * RS + 8 * (lane % LPR) + 8 * LPR * cc) = vr[vi][cc];
     }
 
     // S^T[row][head] = K Q^T

@@ -143,6 +143,17 @@ __device__ __forceinline__ bool bit_of(const uint32_t* bits, int64_t t) {
   return (bits[t >> 5] >> (t & 31)) & 1u;
 }
 
+// Reads of workspace words that other threads of the same launch wrote with device
+// atomics (performed in L2): device-scope loads, which bypass the CU's L1, where a
+// line filled before those atomics could still hold the old value.
+__device__ __forceinline__ bool bit_of_l2(const uint32_t* bits, int64_t t) {
+  const uint32_t wd = __hip_atomic_load(bits + (t >> 5), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return (wd >> (t & 31)) & 1u;
+}
+__device__ __forceinline__ uint64_t load_l2(const uint64_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 __device__ __forceinline__ int64_t load_pos(const hs_resolve_desc& d, int64_t i) {
   return d.positions_i64 ? static_cast<const int64_t*>(d.positions)[i]
                          : static_cast<int64_t>(static_cast<const int32_t*>(d.positions)[i]);
@@ -195,7 +206,9 @@ __device__ __forceinline__ int32_t lanes_below(uint64_t m) {
 // ---- front: bitmaps, hits and protection, miss ranks, victims, LRU reorder
 // (row_index.py:67-113).  LDS: bits[wl] (selected tokens, then hit tokens),
 // needs[wl], prot[wsw].
-template <bool POW2>  // page size a power of two (shifts), else 32-bit divisions
+// POW2: page size a power of two (shifts), else 32-bit divisions.  L16: int16 LRU
+// tables (two entries per 32-bit load and register), else the reference's int64.
+template <bool POW2, bool L16>
 __global__ __launch_bounds__(RT) void resolve_front_kernel(ResolveBatch batch) {
   extern __shared__ uint32_t lds[];
   __shared__ int64_t scan64[16];
@@ -309,12 +322,12 @@ __global__ __launch_bounds__(RT) void resolve_front_kernel(ResolveBatch batch) {
   if (dups) {
     for (int64_t i = T; i < n; i += RT) {
       const int64_t t = load_pos(d, i);
-      if (t >= 0 && t < L && bit_of(w.dupbits, t)) w.first_in[t] = static_cast<int32_t>(n);
+      if (t >= 0 && t < L && bit_of_l2(w.dupbits, t)) w.first_in[t] = static_cast<int32_t>(n);
     }
     __syncthreads();
     for (int64_t i = T; i < n; i += RT) {
       const int64_t t = load_pos(d, i);
-      if (t >= 0 && t < L && bit_of(w.dupbits, t)) atomicMin(&w.first_in[t], static_cast<int32_t>(i));
+      if (t >= 0 && t < L && bit_of_l2(w.dupbits, t)) atomicMin(&w.first_in[t], static_cast<int32_t>(i));
     }
   }
 
@@ -439,13 +452,13 @@ __global__ __launch_bounds__(RT) void resolve_front_kernel(ResolveBatch batch) {
       for (int j = 0; j < TAG_BATCH; ++j) {  // first probes in flight together
         hp[j] = page_of(static_cast<uint32_t>(tg[k0 + j]));
         h[j] = hash32(hp[j]) & hmask;
-        e[j] = tg[k0 + j] >= 0 ? w.hash[h[j]] : HASH_EMPTY;
+        e[j] = tg[k0 + j] >= 0 ? load_l2(&w.hash[h[j]]) : HASH_EMPTY;
       }
 #pragma unroll
       for (int j = 0; j < TAG_BATCH; ++j) {
         while (e[j] != HASH_EMPTY && static_cast<uint32_t>(e[j]) != hp[j]) {
           h[j] = (h[j] + 1) & hmask;
-          e[j] = w.hash[h[j]];
+          e[j] = load_l2(&w.hash[h[j]]);
         }
         const uint32_t off = static_cast<uint32_t>(tg[k0 + j]) - hp[j] * Pu;
         tg[k0 + j] = e[j] == HASH_EMPTY || tg[k0 + j] < 0 ? -1
@@ -489,16 +502,28 @@ __global__ __launch_bounds__(RT) void resolve_front_kernel(ResolveBatch batch) {
     if (wi < wsw) prot[wi] = myprot;
   }
 
-  // the LRU (slots < 32768: the low word of each int64 entry), read before any
-  // is rewritten; the loads run while the miss words are counted
-  const int32_t* lru_lo = reinterpret_cast<const int32_t*>(d.lru);
-  int32_t slot[LRU_CHUNK];
+  // the LRU (slots < 32768), read before any is rewritten; the loads run while the
+  // miss words are counted.  Row q of thread T holds LRU entry q * RT + T (int64
+  // tables: the entry's low word), or for int16 tables the entries 2 (q * RT + T) and
+  // 2 (q * RT + T) + 1 in one 32-bit word (lower entry in the low half).  Rows past
+  // hot_rows load entry 0 and are masked where used.
+  constexpr int HALVES = L16 ? 2 : 1;
+  constexpr int LROWS = LRU_CHUNK / HALVES;
+  int32_t slot[LROWS];
+  {
+    const int32_t* lru32 = static_cast<const int32_t*>(d.lru);
 #pragma unroll
-  for (int q = 0; q < LRU_CHUNK; ++q) {
-    const int32_t jj = q * RT + T;
-    const int32_t v = lru_lo[2 * (jj < S ? jj : 0)];  // unconditional load, masked afterwards
-    slot[q] = jj < S ? v : -1;
+    for (int q = 0; q < LROWS; ++q) {
+      const int32_t jp = q * RT + T;
+      slot[q] = lru32[HALVES * jp < S ? (L16 ? jp : 2 * jp) : 0];  // hot_rows even for int16 (host-checked)
+    }
   }
+  // slot of half h of row q, and its LRU entry index
+  auto slot_at = [&](int q, int h) -> int32_t {
+    if constexpr (L16) return h ? static_cast<int32_t>(static_cast<uint32_t>(slot[q]) >> 16) : (slot[q] & 0xffff);
+    else return slot[q];
+  };
+  auto entry_of = [&](int q, int h) -> int32_t { return HALVES * (q * RT + T) + h; };
 
   __syncthreads();
 
@@ -546,31 +571,40 @@ __global__ __launch_bounds__(RT) void resolve_front_kernel(ResolveBatch batch) {
     }
   }
 
-  // victims and the new LRU (row_index.py:94-96, 112-113).  LRU entry
-  // jj = q * RT + T (row q, thread T): ranks inside a wave come from ballots,
-  // the counts of every (row, wave) are scanned in row-major order (LRU order).
-  uint32_t protmask = 0u;  // bit q: entry of row q is protected
+  // victims and the new LRU (row_index.py:94-96, 112-113).  The entries are in
+  // LRU order over (row, wave, lane, half): ranks inside a wave come from ballots,
+  // the counts of every (row, wave) are scanned in row-major order.
+  uint32_t protmask = 0u;  // bit HALVES * q + h: that entry is protected
 #pragma unroll
-  for (int q0 = 0; q0 < LRU_CHUNK; q0 += MATCH_BATCH) {
-    uint32_t pw[MATCH_BATCH];
+  for (int q0 = 0; q0 < LROWS; q0 += MATCH_BATCH) {
+    uint32_t pw[MATCH_BATCH][HALVES];
 #pragma unroll
-    for (int j = 0; j < MATCH_BATCH; ++j) pw[j] = prot[static_cast<uint32_t>(slot[q0 + j] < 0 ? 0 : slot[q0 + j]) >> 5];
+    for (int j = 0; j < MATCH_BATCH; ++j) {
+#pragma unroll
+      for (int h = 0; h < HALVES; ++h) {
+        const int32_t sl = slot_at(q0 + j, h);  // a slot outside [0, S) only with an invalid LRU
+        pw[j][h] = prot[(static_cast<uint32_t>(sl) < static_cast<uint32_t>(S) ? sl : 0) >> 5];
+      }
+    }
 #pragma unroll
     for (int j = 0; j < MATCH_BATCH; ++j) {
       const int q = q0 + j;
-      const int32_t jj = q * RT + T;
-      const bool pr = jj < S && ((pw[j] >> (slot[q] & 31)) & 1u);
-      protmask |= static_cast<uint32_t>(pr) << q;
-      const uint64_t up = __ballot(jj < S && !pr);
-      if (lane == 0) ucnt[q * NWAVES + wave] = static_cast<int32_t>(__popcll(up));
+      int32_t cnt = 0;
+#pragma unroll
+      for (int h = 0; h < HALVES; ++h) {
+        const bool pr = entry_of(q, h) < S && ((pw[j][h] >> (slot_at(q, h) & 31)) & 1u);
+        protmask |= static_cast<uint32_t>(pr) << (HALVES * q + h);
+        cnt += static_cast<int32_t>(__popcll(__ballot(entry_of(q, h) < S && !pr)));
+      }
+      if (lane == 0) ucnt[q * NWAVES + wave] = cnt;
     }
   }
   __syncthreads();
   int32_t U;  // unprotected slots
   {
-    const int32_t v = T < LRU_CHUNK * NWAVES ? ucnt[T] : 0;
+    const int32_t v = T < LROWS * NWAVES ? ucnt[T] : 0;
     const int32_t ex = block_exclusive_sum<int32_t>(v, scan32, &U);
-    if (T < LRU_CHUNK * NWAVES) ucnt[T] = ex;
+    if (T < LROWS * NWAVES) ucnt[T] = ex;
   }
   __syncthreads();
   const int32_t tm = tot_miss < S ? static_cast<int32_t>(tot_miss) : S;  // only rank < tm matters
@@ -579,24 +613,35 @@ __global__ __launch_bounds__(RT) void resolve_front_kernel(ResolveBatch batch) {
   const int32_t fillP = tm - U > 0 ? (tm - U < Pn ? tm - U : Pn) : 0;
   const int32_t start1 = U - fillU, start2 = U, start3 = S - fillP;
 #pragma unroll
-  for (int q = 0; q < LRU_CHUNK; ++q) {
-    const int32_t jj = q * RT + T;
-    const bool in = jj < S;
-    const bool pr = (protmask >> q) & 1u;
-    const uint64_t up = __ballot(in && !pr);
-    const int32_t r = ucnt[q * NWAVES + wave] + lanes_below(up);  // unprotected entries before jj
-    if (in) {
-      int32_t rank, at;
-      if (!pr) {
-        rank = r;
-        at = r < fillU ? start1 + r : r - fillU;
-      } else {
-        const int32_t pj = jj - r;  // protected entries before jj
-        rank = U + pj;
-        at = pj < fillP ? start3 + pj : start2 + (pj - fillP);
+  for (int q = 0; q < LROWS; ++q) {
+    uint64_t up[HALVES];
+    int32_t r = ucnt[q * NWAVES + wave];  // unprotected entries before the row's first of this lane
+#pragma unroll
+    for (int h = 0; h < HALVES; ++h) {
+      up[h] = __ballot(entry_of(q, h) < S && !((protmask >> (HALVES * q + h)) & 1u));
+      r += lanes_below(up[h]);
+    }
+#pragma unroll
+    for (int h = 0; h < HALVES; ++h) {
+      const int32_t jj = entry_of(q, h);
+      const bool in = jj < S;
+      const bool pr = (protmask >> (HALVES * q + h)) & 1u;
+      if (in) {
+        int32_t rank, at;
+        if (!pr) {
+          rank = r;
+          at = r < fillU ? start1 + r : r - fillU;
+        } else {
+          const int32_t pj = jj - r;  // protected entries before jj
+          rank = U + pj;
+          at = pj < fillP ? start3 + pj : start2 + (pj - fillP);
+        }
+        const int32_t sl = slot_at(q, h);
+        w.victims[rank] = sl;
+        if constexpr (L16) static_cast<int16_t*>(d.lru)[at] = static_cast<int16_t>(sl);
+        else static_cast<int64_t*>(d.lru)[at] = sl;
       }
-      w.victims[rank] = slot[q];
-      d.lru[at] = slot[q];
+      r += in && !pr ? 1 : 0;  // the lower half precedes the upper one
     }
   }
   if (T == 0) {
@@ -708,6 +753,10 @@ static int validate_desc(const hs_resolve_desc& d) {
   HS_CHECK_ARG(d.n_pages >= 1, "source table must be nonempty");
   HS_CHECK_ARG(d.length <= d.n_pages * d.page_size, "length exceeds the page tables");
   HS_CHECK_ARG(d.hot_rows >= 1 && d.hot_rows <= RT * LRU_CHUNK, "hot_rows must be in [1, 32768]");
+  HS_CHECK_ARG(d.lru_i16 == 0 || d.lru_i16 == 1, "lru_i16 must be 0 or 1");
+  if (d.lru_i16)  // the front launch reads an int16 LRU as 32-bit pairs
+    HS_CHECK_ARG(d.hot_rows % 2 == 0 && (reinterpret_cast<uintptr_t>(d.lru) & 3) == 0,
+                 "an int16 LRU needs an even hot_rows and 4-byte alignment");
   HS_CHECK_ARG(d.hot_blocks * d.page_size >= d.hot_rows, "hot block table does not cover hot_rows");
   HS_CHECK_ARG(d.length < (static_cast<int64_t>(1) << 31), "length too large");
   HS_CHECK_ARG(d.n_pages < (static_cast<int64_t>(1) << 31), "too many pages");
@@ -738,6 +787,7 @@ static int64_t batch_workspace(const hs_resolve_desc* descs, int32_t count) {
   for (int32_t i = 0; i < count; ++i) {
     const int rc = validate_desc(descs[i]);
     if (rc) return rc;
+    HS_CHECK_ARG(descs[i].lru_i16 == descs[0].lru_i16, "the descriptors of one batch must share lru_i16");
     need += hs_resolve_workspace_bytes(descs[i].n, descs[i].length, descs[i].n_pages, descs[i].hot_rows);
   }
   return need;
@@ -758,10 +808,11 @@ extern "C" int hs_resolve_rows_batched(const hs_resolve_desc* descs, int32_t cou
 static int resolve_launch(const hs_resolve_desc* descs, int32_t count, char* workspace, hipStream_t stream) {
   static bool attr_set = false;
   if (!attr_set) {
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(resolve_front_kernel<true>),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kMaxResolverLds));
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(resolve_front_kernel<false>),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kMaxResolverLds));
+    for (const void* f : {reinterpret_cast<const void*>(resolve_front_kernel<true, false>),
+                          reinterpret_cast<const void*>(resolve_front_kernel<false, false>),
+                          reinterpret_cast<const void*>(resolve_front_kernel<true, true>),
+                          reinterpret_cast<const void*>(resolve_front_kernel<false, true>)})
+      (void)hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kMaxResolverLds));
     (void)hipGetLastError();
     attr_set = true;
   }
@@ -782,8 +833,14 @@ static int resolve_launch(const hs_resolve_desc* descs, int32_t count, char* wor
       if (outs > max_out) max_out = outs;
     }
     const unsigned nb = static_cast<unsigned>(batch.count);
-    if (pow2) hipLaunchKernelGGL(resolve_front_kernel<true>, dim3(nb), dim3(RT), static_cast<size_t>(front_lds), stream, batch);
-    else hipLaunchKernelGGL(resolve_front_kernel<false>, dim3(nb), dim3(RT), static_cast<size_t>(front_lds), stream, batch);
+    const size_t lds = static_cast<size_t>(front_lds);
+    if (batch.d[0].lru_i16) {  // the same for every descriptor (validated)
+      if (pow2) hipLaunchKernelGGL((resolve_front_kernel<true, true>), dim3(nb), dim3(RT), lds, stream, batch);
+      else hipLaunchKernelGGL((resolve_front_kernel<false, true>), dim3(nb), dim3(RT), lds, stream, batch);
+    } else {
+      if (pow2) hipLaunchKernelGGL((resolve_front_kernel<true, false>), dim3(nb), dim3(RT), lds, stream, batch);
+      else hipLaunchKernelGGL((resolve_front_kernel<false, false>), dim3(nb), dim3(RT), lds, stream, batch);
+    }
     HS_CHECK_LAUNCH("resolver front");
     hipLaunchKernelGGL(resolve_outputs_kernel, dim3(static_cast<unsigned>(ceil_div(max_out, RW)), nb), dim3(RW),
                        0, stream, batch);

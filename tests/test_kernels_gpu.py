@@ -189,17 +189,20 @@ def test_resolver_affine_source_matches_oracle(gpu, seed, length, P, S, n, res_f
     _assert_plan(plan, tags, lru, expected)
 
 
-def test_resolver_batched_descriptors_match_oracle(gpu):
+@pytest.mark.parametrize("lru_dtype", [torch.int64, torch.int16])
+def test_resolver_batched_descriptors_match_oracle(gpu, lru_dtype):
     """hs_resolve_rows_batched over 17 (request, layer) descriptors of different sizes: one
-    launch of 16 descriptors and one of 1; every output of every request equals the oracle."""
-    import ctypes
-
+    launch of 16 descriptors and one of 1; every output of every request equals the oracle.
+    The LRU in the reference's int64 and in int16 (the batched engine's tables), up to the
+    full 32768 hot rows (slot 32767, the largest int16)."""
     from mini_hisparse_amd import _lib
 
     lib = _lib.load()
     cases = []
+    shapes = [(1000, 16, 512, 300), (4096, 16, 2048, 1500), (97, 4, 64, 40), (300, 7, 128, 100),
+              (40000, 16, 32768, 9000)]
     for i in range(17):
-        length, P, S, n = [(1000, 16, 512, 300), (4096, 16, 2048, 1500), (97, 4, 64, 40), (300, 7, 128, 100)][i % 4]
+        length, P, S, n = shapes[i % len(shapes)]
         tables = resolver_tables(50 + i, length, P, S, resident_frac=0.1 * (i % 6))
         positions = random_positions(150 + i, n, length)
         cases.append((length, P, tables, positions))
@@ -207,6 +210,7 @@ def test_resolver_batched_descriptors_match_oracle(gpu):
     keep, total = [], 0
     for d, (length, P, tables, positions) in zip(descs, cases):
         t = {k: torch.from_numpy(np.ascontiguousarray(v)).to(gpu) for k, v in tables.items()}
+        t["lru"] = t["lru"].to(lru_dtype)
         pos = torch.from_numpy(positions).to(gpu)
         n = pos.numel()
         out = {name: torch.empty(n, dtype=torch.int64, device=gpu) for name in ("phys", "uphys", "mh", "md")}
@@ -215,6 +219,7 @@ def test_resolver_batched_descriptors_match_oracle(gpu):
         d.source, d.resident, d.n_pages = t["source"].data_ptr(), t["resident"].data_ptr(), t["source"].numel()
         d.hot, d.hot_blocks = t["hot"].data_ptr(), t["hot"].numel()
         d.tags, d.lru, d.hot_rows = t["tags"].data_ptr(), t["lru"].data_ptr(), t["tags"].numel()
+        d.lru_i16 = int(lru_dtype == torch.int16)
         d.length, d.page_size = length, P
         d.physical, d.union_physical = out["phys"].data_ptr(), out["uphys"].data_ptr()
         d.miss_host_rows, d.miss_device_rows = out["mh"].data_ptr(), out["md"].data_ptr()
@@ -225,15 +230,16 @@ def test_resolver_batched_descriptors_match_oracle(gpu):
     _lib.check(lib.hs_resolve_rows_batched(descs, len(cases), ws.data_ptr(), total,
                                            _lib.stream_handle(torch.device(gpu))), "hs_resolve_rows_batched")
     torch.cuda.synchronize()
-    for (length, P, tables, positions), (t, _, out) in zip(cases, keep):
+    for i, ((length, P, tables, positions), (t, _, out)) in enumerate(zip(cases, keep)):
         phys, mh, md, counts, tags_after, lru_after = oracle.resolve_rows(
             positions, *[tables[k] for k in ("source", "resident", "hot", "tags", "lru")], length, P)
-        np.testing.assert_array_equal(out["phys"].cpu().numpy(), phys)
-        np.testing.assert_array_equal(out["mh"].cpu().numpy(), mh)
-        np.testing.assert_array_equal(out["md"].cpu().numpy(), md)
-        np.testing.assert_array_equal(out["counts"].cpu().numpy(), counts)
-        np.testing.assert_array_equal(t["tags"].cpu().numpy(), tags_after)
-        np.testing.assert_array_equal(t["lru"].cpu().numpy(), lru_after)
+        case = f"descriptor {i}: length {length}, page {P}, hot rows {tables['tags'].size}"
+        np.testing.assert_array_equal(out["phys"].cpu().numpy(), phys, err_msg=case)
+        np.testing.assert_array_equal(out["mh"].cpu().numpy(), mh, err_msg=case)
+        np.testing.assert_array_equal(out["md"].cpu().numpy(), md, err_msg=case)
+        np.testing.assert_array_equal(out["counts"].cpu().numpy(), counts, err_msg=case)
+        np.testing.assert_array_equal(t["tags"].cpu().numpy(), tags_after, err_msg=case)
+        np.testing.assert_array_equal(t["lru"].cpu().numpy(), lru_after, err_msg=case)
 
 
 def test_resolver_head_columns_and_multistep_trajectory(gpu):
