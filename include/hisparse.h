@@ -120,6 +120,13 @@ int hs_quest_topk(const void* query, int64_t q_stride_b, int64_t q_stride_h,
  *                 [batch, kv_heads]
  *   status        int32 flag OR-ed with 1 (union over capacity) / 2 (entries
  *                 over capacity); the caller clears it.
+ *   page_bits     nullable [batch, page_bits_stride] uint32: bit p of request b
+ *                 set iff page p is in the union (page_bits_stride >= the
+ *                 words of ceil(length / page_size) bits); the positions are
+ *                 then exactly the tokens below length of the marked pages,
+ *                 unless the union overflowed (status bit 1).  No counterpart
+ *                 in the reference: it lets the resolver skip reading the
+ *                 positions (hs_resolve_desc.page_bits).
  * Any batch size: launched in chunks of at most 16 requests, in order on `stream`.
  */
 int hs_build_union(const int32_t* pages, int64_t p_stride_b, int64_t top, const int64_t* lengths,
@@ -127,7 +134,7 @@ int hs_build_union(const int32_t* pages, int64_t p_stride_b, int64_t top, const 
                    int32_t* positions, int64_t pos_capacity, int64_t* head_columns, int64_t width,
                    int32_t* union_count, int32_t* entry_columns, uint32_t* entry_masks,
                    int64_t entry_capacity, int32_t* entry_counts, int32_t* status,
-                   hs_stream_t stream);
+                   uint32_t* page_bits, int64_t page_bits_stride, hs_stream_t stream);
 
 /* ------------------------------------------------------------- (2) resolver */
 
@@ -140,6 +147,10 @@ typedef struct hs_resolve_desc {
   int64_t n;
   int32_t positions_i64;        /* 1 = int64 positions, 0 = int32 */
   int32_t lru_i16;              /* 1 = lru holds int16 slots, 0 = int64 (the reference's dtype) */
+  const uint32_t* page_bits;    /* nullable: the union page bitmap of hs_build_union that produced
+                                   `positions`; its valid entries are then exactly the tokens below
+                                   length of the marked pages, and the resolver reads the bitmap
+                                   instead of the positions to find the selected tokens */
   const int64_t* head_columns;  /* nullable [heads, width] union columns, -1 padded */
   int64_t heads, width, hc_stride_h, hc_stride_w;
   const int32_t* source;        /* [n_pages] host page of each logical page, -1 = none */

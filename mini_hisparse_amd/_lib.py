@@ -27,6 +27,7 @@ class ResolveDesc(ctypes.Structure):
         ("n", c_int64),
         ("positions_i64", c_int32),
         ("lru_i16", c_int32),
+        ("page_bits", c_void_p),
         ("head_columns", c_void_p),
         ("heads", c_int64),
         ("width", c_int64),
@@ -71,7 +72,7 @@ SIGNATURES = {
         c_int,
         [c_void_p, c_int64, c_int64, POINTER(c_int64), c_int64, c_int64, c_int64, c_int64,
          c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_void_p, c_void_p, c_int64,
-         c_void_p, c_void_p, c_void_p],
+         c_void_p, c_void_p, c_void_p, c_int64, c_void_p],
     ),
     "hs_resolve_workspace_bytes": (c_int64, [c_int64, c_int64, c_int64, c_int64]),
     "hs_resolve_rows": (c_int, [POINTER(ResolveDesc), c_void_p, c_int64, c_void_p]),

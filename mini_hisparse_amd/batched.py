@@ -98,6 +98,9 @@ class BatchedSparseDecode:
         self.entry_masks = torch.empty((B, self.kv_heads, self.entry_capacity), dtype=i32, device=dev)
         self.entry_counts = torch.empty((B, self.kv_heads), dtype=i32, device=dev)
         self.status = torch.zeros(1, dtype=i32, device=dev)
+        # the union's page bitmap, read by the resolver instead of the positions
+        self.page_bits_stride = max(ceil(ceil(l / P) / 32) for l in caps)
+        self.page_bits = torch.empty((B, self.page_bits_stride), dtype=i32, device=dev)
         self.union_physical = torch.empty((B, self.capacity), dtype=i64, device=dev)
         self.physical = torch.empty((B, self.heads, self.width), dtype=i64, device=dev) if self.head_rows else None
         self.miss_host = torch.empty((B, self.capacity), dtype=i64, device=dev)
@@ -204,7 +207,8 @@ class BatchedSparseDecode:
                 self.config.page_size, self.batch, self.heads, self.kv_heads, self.positions.data_ptr(),
                 self.capacity, self.head_columns.data_ptr(), self.width, self.union_count.data_ptr(),
                 self.entry_columns.data_ptr(), self.entry_masks.data_ptr(), self.entry_capacity,
-                self.entry_counts.data_ptr(), self.status.data_ptr(), s,
+                self.entry_counts.data_ptr(), self.status.data_ptr(), self.page_bits.data_ptr(),
+                self.page_bits_stride, s,
             ),
             "hs_build_union",
         )
@@ -234,6 +238,7 @@ class BatchedSparseDecode:
             d.positions = self.positions[b].data_ptr()
             d.n = self.capacity
             d.positions_i64 = 0
+            d.page_bits = self.page_bits[b].data_ptr()  # the positions come from _build_union
             if self.head_rows:
                 d.head_columns = self.head_columns[b].data_ptr()
                 d.heads, d.width = self.heads, self.width

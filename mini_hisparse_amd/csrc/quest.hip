@@ -524,6 +524,8 @@ struct UnionArgs {
   int64_t ecap;
   int32_t* ecount;       // [B, Hkv]
   int32_t* status;       // nonzero on overflow
+  uint32_t* page_bits;   // nullable [B, pb_stride]: the union's page bitmap
+  int64_t pb_stride;
   int64_t words;         // bitmap words of the longest history
   int64_t maxcount;      // pages of the longest history
   int use_map;           // rank -> page map in LDS (maxcount <= UMAPPAGES)
@@ -640,6 +642,8 @@ __global__ __launch_bounds__(UT) void build_union_kernel(UnionArgs a) {
       }
     }
     for (int64_t i = nw + threadIdx.x; i < a.pos_cap; i += UT) pos[i] = -1;
+    if (a.page_bits)
+      for (int64_t w = threadIdx.x; w < words; w += UT) a.page_bits[b * a.pb_stride + w] = ubits[w];
   } else if (part > a.Hkv) {
     // union columns of head h: its j-th token (its pages ascending, tail last)
     const int64_t h = part - a.Hkv - 1;
@@ -867,7 +871,8 @@ static int build_union_chunk(const int32_t* pages, int64_t p_stride_b, int64_t t
                              int64_t pos_capacity, int64_t* head_columns, int64_t width,
                              int32_t* union_count, int32_t* entry_columns,
                              uint32_t* entry_masks, int64_t entry_capacity,
-                             int32_t* entry_counts, int32_t* status, hipStream_t stream) {
+                             int32_t* entry_counts, int32_t* status, uint32_t* page_bits,
+                             int64_t pb_stride, hipStream_t stream) {
   HS_CHECK_ARG(batch >= 1 && batch <= QMAXB, "union batch must be in [1, %d]", QMAXB);
   HS_CHECK_ARG(top >= 1 && page_size >= 1 && heads >= 1 && kv_heads >= 1 && heads % kv_heads == 0,
                "invalid union shape");
@@ -896,6 +901,8 @@ static int build_union_chunk(const int32_t* pages, int64_t p_stride_b, int64_t t
   a.g = heads / kv_heads;
   a.positions = positions;
   a.pos_cap = pos_capacity;
+  a.page_bits = page_bits;
+  a.pb_stride = pb_stride;
   a.head_columns = head_columns;
   a.width = width;
   a.union_count = union_count;
@@ -972,7 +979,8 @@ extern "C" int hs_build_union(const int32_t* pages, int64_t p_stride_b, int64_t 
                               int64_t pos_capacity, int64_t* head_columns, int64_t width,
                               int32_t* union_count, int32_t* entry_columns,
                               uint32_t* entry_masks, int64_t entry_capacity,
-                              int32_t* entry_counts, int32_t* status, hipStream_t stream) {
+                              int32_t* entry_counts, int32_t* status, uint32_t* page_bits,
+                              int64_t page_bits_stride, hipStream_t stream) {
   HS_CHECK_ARG(batch >= 1, "union batch must be positive");
   HS_CHECK_ARG(top >= 1 && page_size >= 1 && lengths, "invalid union shape");
   HS_CHECK_ARG(heads >= 1 && kv_heads >= 1 && heads % kv_heads == 0, "invalid GQA shape");
@@ -984,6 +992,9 @@ extern "C" int hs_build_union(const int32_t* pages, int64_t p_stride_b, int64_t 
     const int64_t W = (k - 1) * page_size + (lengths[i] - (count - 1) * page_size);
     HS_CHECK_ARG(W <= width, "head column width %lld below the selection width %lld",
                  static_cast<long long>(width), static_cast<long long>(W));
+    HS_CHECK_ARG(!page_bits || page_bits_stride >= ceil_div(count, 32),
+                 "page bitmap stride %lld below the %lld words of a history",
+                 static_cast<long long>(page_bits_stride), static_cast<long long>(ceil_div(count, 32)));
   }
   for (int64_t s0 = 0; s0 < batch; s0 += QMAXB) {
     const int64_t n = batch - s0 < QMAXB ? batch - s0 : QMAXB;
@@ -991,7 +1002,8 @@ extern "C" int hs_build_union(const int32_t* pages, int64_t p_stride_b, int64_t 
         pages + s0 * p_stride_b, p_stride_b, top, lengths + s0, page_size, n, heads, kv_heads,
         positions + s0 * pos_capacity, pos_capacity, head_columns + s0 * heads * width, width, union_count + s0,
         entry_columns + s0 * kv_heads * entry_capacity, entry_masks + s0 * kv_heads * entry_capacity,
-        entry_capacity, entry_counts + s0 * kv_heads, status, stream);
+        entry_capacity, entry_counts + s0 * kv_heads, status,
+        page_bits ? page_bits + s0 * page_bits_stride : nullptr, page_bits_stride, stream);
     if (rc != HS_OK) return rc;
   }
   return HS_OK;

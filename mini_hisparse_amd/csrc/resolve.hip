@@ -11,7 +11,8 @@
 //                          - selected tokens become a bitmap over [0, length):
 //                            ascending order is bit order, a duplicate input is the
 //                            atomicOr that finds its bit set (the first input index
-//                            of a duplicated token by atomicMin);
+//                            of a duplicated token by atomicMin); given the union's
+//                            page bitmap, the bitmap is expanded from it instead;
 //                          - per page with selected tokens: resident hits are
 //                            counted and host-backed non-resident tokens get a
 //                            needs-hot bit;
@@ -76,7 +77,7 @@ struct ResolveWs {
   int32_t* first_in;   // [length] first input index of a duplicated token
   int32_t* tslot;      // [length] hot slot of a hit token
   uint64_t* hash;      // [hcap] (page << 32) | host block of needs-hot pages; all ones = empty
-  int32_t* victims;    // [hot_rows] slots in victim order
+  int32_t* victims;    // [hot_rows] slots in victim order (ranks below the miss count written)
   int64_t* totals;     // [4] resident hits, hot hits, misses, any duplicate
   int64_t hcap;
 };
@@ -250,7 +251,10 @@ __global__ __launch_bounds__(RT) void resolve_front_kernel(ResolveBatch batch) {
   }
   __syncthreads();
 
-  // selected tokens; a bit already set means a duplicate input.  Each wave
+  // selected tokens.  With the union's page bitmap they are the tokens below
+  // length of the marked pages (no duplicates): each token word is assembled from
+  // the bits of the pages it overlaps, and no input is read.  Otherwise a bit
+  // already set means a duplicate input.  Each wave
   // loads 512 consecutive inputs (coalesced) into an LDS tile; lane l then
   // walks inputs 8l .. 8l+7 of the tile and gathers the bits of one bitmap
   // word in a register while consecutive tokens stay in it (selected tokens
@@ -258,7 +262,22 @@ __global__ __launch_bounds__(RT) void resolve_front_kernel(ResolveBatch batch) {
   // changes.  A token already in the register, or already in the word when
   // it is published, is a duplicate; any input order gives the same bitmap
   // and duplicate set.
-  {
+  if (d.page_bits) {  // the same for every thread
+    for (int64_t wd = T; wd < wl; wd += RT) {
+      const int64_t t0 = wd << 5;
+      const int64_t t1 = t0 + 32 < L ? t0 + 32 : L;  // tokens [t0, t1) of this word
+      uint32_t m = 0u;
+      if (t0 < L) {
+        const uint32_t p_hi = page_of(static_cast<uint32_t>(t1 - 1));
+        for (uint32_t pg = page_of(static_cast<uint32_t>(t0)); pg <= p_hi; ++pg) {
+          if (!((d.page_bits[pg >> 5] >> (pg & 31)) & 1u)) continue;
+          const int64_t lo = static_cast<int64_t>(pg) * P;
+          m |= range_mask(wd, lo, lo + P < t1 ? lo + P : t1);
+        }
+      }
+      bits[wd] = m;  // each word has one writer
+    }
+  } else {
     int32_t* tile = mark_tile + wave * MARK_TILE_PAD;
     int64_t cur = -1;
     uint32_t acc = 0u, accdup = 0u;
@@ -637,7 +656,7 @@ __global__ __launch_bounds__(RT) void resolve_front_kernel(ResolveBatch batch) {
           at = pj < fillP ? start3 + pj : start2 + (pj - fillP);
         }
         const int32_t sl = slot_at(q, h);
-        w.victims[rank] = sl;
+        if (rank < tm) w.victims[rank] = sl;  // the outputs read only the ranks of misses
         if constexpr (L16) static_cast<int16_t*>(d.lru)[at] = static_cast<int16_t>(sl);
         else static_cast<int64_t*>(d.lru)[at] = sl;
       }

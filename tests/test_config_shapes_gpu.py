@@ -119,6 +119,12 @@ def _run_layer(gpu, *, B, Hkv, g, D, pages, length, top, hot_rows, resident_frac
             union, cols = oracle_union(pages_to_positions(pages_o, length, P))
             n = len(union)
             assert int(dec.union_count[b]) == n
+            marked = np.zeros(dec.page_bits_stride * 32, bool)
+            marked[np.unique(pages_o[pages_o >= 0])] = True  # the union's pages
+            words = np.packbits(marked.reshape(-1, 32)[:, ::-1], axis=1).view(">u4").reshape(-1)
+            got_bits = dec.page_bits[b].cpu().numpy().view(np.uint32)
+            nw = (count + 31) // 32
+            np.testing.assert_array_equal(got_bits[:nw], words[:nw].astype(np.uint32))
             np.testing.assert_array_equal(dec.positions[b, :n].cpu().numpy(), union)
             np.testing.assert_array_equal(dec.head_columns[b, :, : cols.shape[1]].cpu().numpy(), cols)
             phys, mh, md, counts, tags1, lru1 = oracle.resolve_rows(

@@ -242,6 +242,58 @@ def test_resolver_batched_descriptors_match_oracle(gpu, lru_dtype):
         np.testing.assert_array_equal(t["lru"].cpu().numpy(), lru_after, err_msg=case)
 
 
+@pytest.mark.parametrize("affine", [False, True])
+def test_resolver_page_bits_matches_oracle(gpu, affine):
+    """Positions that are the tokens of a page set (the union builder's output, padded with
+    -1 to a capacity) resolved from the page bitmap (hs_resolve_desc.page_bits, no position
+    read in the front) and from the positions: both equal the oracle, int16 LRU."""
+    from mini_hisparse_amd import _lib
+
+    lib = _lib.load()
+    rng = np.random.default_rng(31)
+    for length, P, S, sel in [(5000, 16, 2048, 60), (131072, 16, 32768, 1700), (999, 7, 512, 40), (64, 4, 64, 16)]:
+        count = -(-length // P)
+        tables = resolver_tables(int(rng.integers(1 << 30)), length, P, S, resident_frac=0.3,
+                                 affine_base=1000 if affine else None)
+        pages = np.unique(np.append(rng.choice(count, size=min(sel, count), replace=False), count - 1))
+        union = np.asarray(pages_to_positions(pages[None, :], length, P)[0], np.int32)
+        cap = len(union) + 37
+        positions = np.full(cap, -1, np.int32)
+        positions[: len(union)] = union
+        words = -(-count // 32)
+        marked = np.zeros(words * 32, bool)
+        marked[pages] = True
+        bits = np.packbits(marked.reshape(-1, 32)[:, ::-1], axis=1).view(">u4").reshape(-1).astype(np.uint32)
+        expected = oracle.resolve_rows(positions, *[tables[k] for k in ("source", "resident", "hot", "tags", "lru")],
+                                       length, P)
+        for use_bits in (True, False):
+            t = {k: torch.from_numpy(np.ascontiguousarray(v)).to(gpu) for k, v in tables.items()}
+            t["lru"] = t["lru"].to(torch.int16)
+            pos = torch.from_numpy(positions).to(gpu)
+            bits_d = torch.from_numpy(bits.view(np.int32)).to(gpu)
+            out = {name: torch.empty(cap, dtype=torch.int64, device=gpu) for name in ("phys", "mh", "md")}
+            out["counts"] = torch.empty(3, dtype=torch.int64, device=gpu)
+            d = _lib.ResolveDesc()
+            d.positions, d.n, d.positions_i64 = pos.data_ptr(), cap, 0
+            d.page_bits = bits_d.data_ptr() if use_bits else None
+            d.source, d.resident, d.n_pages = t["source"].data_ptr(), t["resident"].data_ptr(), t["source"].numel()
+            d.hot, d.hot_blocks = t["hot"].data_ptr(), t["hot"].numel()
+            d.tags, d.lru, d.hot_rows, d.lru_i16 = t["tags"].data_ptr(), t["lru"].data_ptr(), S, 1
+            d.length, d.page_size = length, P
+            d.physical = d.union_physical = out["phys"].data_ptr()
+            d.miss_host_rows, d.miss_device_rows = out["mh"].data_ptr(), out["md"].data_ptr()
+            d.counts = out["counts"].data_ptr()
+            need = lib.hs_resolve_workspace_bytes(cap, length, d.n_pages, S)
+            ws = torch.empty(need, dtype=torch.uint8, device=gpu)
+            _lib.check(lib.hs_resolve_rows(d, ws.data_ptr(), need, _lib.stream_handle(torch.device(gpu))),
+                       "hs_resolve_rows")
+            torch.cuda.synchronize()
+            case = f"length {length}, page {P}, hot rows {S}, page bits {use_bits}"
+            for got, want in ((out["phys"], expected[0]), (out["mh"], expected[1]), (out["md"], expected[2]),
+                              (out["counts"], expected[3]), (t["tags"], expected[4]), (t["lru"], expected[5])):
+                np.testing.assert_array_equal(got.cpu().numpy(), want, err_msg=case)
+
+
 def test_resolver_head_columns_and_multistep_trajectory(gpu):
     from mini_hisparse_amd.row_index import LogicalTopK, resolve_rows
 
