@@ -59,10 +59,12 @@ def parse_args():
     p = argparse.ArgumentParser(description=__doc__)
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--workload", default="qwen2.5-7b",
-                   choices=["microbench", "qwen2.5-7b-layer", "qwen2.5-0.5b", "qwen2.5-7b", "qwen2.5-32b-stress"],
+                   choices=["microbench", "qwen2.5-7b-layer", "qwen2.5-0.5b-layer", "qwen2.5-0.5b", "qwen2.5-7b",
+                            "qwen2.5-32b-stress"],
                    help="qwen2.5-7b = BASELINE configs[3] end to end (default, the north_star shape); "
                         "microbench = configs[1]; qwen2.5-7b-layer = the microbench step at the north_star "
-                        "layer shape (7B heads, 128k histories, batch 16); qwen2.5-0.5b and qwen2.5-32b-stress "
+                        "layer shape (7B heads, 128k histories, batch 16); qwen2.5-0.5b-layer = the same at "
+                        "the configs[2] layer shape; qwen2.5-0.5b and qwen2.5-32b-stress "
                         "run configs[2] and configs[4] end to end")
     p.add_argument("--no-microbench", action="store_true",
                    help="default workload: skip the configs[1] microbench figures carried as extra keys")
@@ -138,6 +140,11 @@ SHAPES = {
     "qwen2.5-7b-layer": Shape("one layer of the Qwen2.5-7B shape (BASELINE configs[3] / north_star): 28 q / 4 kv "
                               "heads, head_dim 128, page 16, 8192 pages/request (131,072 tokens)",
                               batch=16, kv_heads=4, heads=28, pages=8192),
+    # one layer of the Qwen2.5-0.5B shape: 32k-token histories, batch 4,
+    # the end-to-end workload's top 32 pages and 13,504 hot rows
+    "qwen2.5-0.5b-layer": Shape("one layer of the Qwen2.5-0.5B shape (BASELINE configs[2]): 14 q / 2 kv heads, "
+                                "head_dim 64, page 16, 2048 pages/request (32,768 tokens), top 32",
+                                batch=4, kv_heads=2, heads=14, pages=2048, head_dim=64, top=32, hot_rows=13504),
 }
 
 

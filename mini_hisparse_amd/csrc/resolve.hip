@@ -59,6 +59,7 @@ constexpr int MATCH_BATCH = 8; // tags matched per batch (needs-bit reads in fli
 constexpr int MARK_BATCH = 8;  // pages loaded per thread before use (long tables)
 constexpr int PAGE_REGS = 9;  // pages per thread loaded before the token walk (n_pages <= RT * PAGE_REGS)
 constexpr int ORDER_WORDS = 8; // token-bitmap words per thread held in registers
+constexpr int WALK_PRE = 5;    // page-bitmap words per thread loaded first (lengths below RT * 5 * 32)
 constexpr int MARK_TILE = 512;                // inputs per wave and tile (8 per lane)
 constexpr int MARK_TILE_PAD = MARK_TILE / 8 * 9;
 constexpr uint64_t HASH_EMPTY = ~static_cast<uint64_t>(0);
@@ -209,7 +210,9 @@ __device__ __forceinline__ int32_t lanes_below(uint64_t m) {
 // needs[wl], prot[wsw].
 // POW2: page size a power of two (shifts), else 32-bit divisions.  L16: int16 LRU
 // tables (two entries per 32-bit load and register), else the reference's int64.
-template <bool POW2, bool L16>
+// SR: hot slots per thread (hot_rows <= RT * SR for every descriptor): 16 or 32, so
+// that the per-slot phases of smaller hot regions run no masked-off rows.
+template <bool POW2, bool L16, int SR>
 __global__ __launch_bounds__(RT) void resolve_front_kernel(ResolveBatch batch) {
   extern __shared__ uint32_t lds[];
   __shared__ int64_t scan64[16];
@@ -217,7 +220,7 @@ __global__ __launch_bounds__(RT) void resolve_front_kernel(ResolveBatch batch) {
   __shared__ int any_dup;
   __shared__ int32_t base_lo, base_hi;
   __shared__ int32_t mark_tile[NWAVES * MARK_TILE_PAD];
-  __shared__ int32_t ucnt[LRU_CHUNK * NWAVES];  // unprotected LRU entries per (row, wave), then their prefix
+  __shared__ int32_t ucnt[SR * NWAVES];  // unprotected LRU entries per (row, wave), then their prefix
   const hs_resolve_desc& d = batch.d[blockIdx.x];
   const ResolveWs w = ws_of(d);
   const int T = threadIdx.x, lane = T & 63, wave = T >> 6;
@@ -230,20 +233,70 @@ __global__ __launch_bounds__(RT) void resolve_front_kernel(ResolveBatch batch) {
   const uint32_t pshift = static_cast<uint32_t>(__ffsll(static_cast<unsigned long long>(P)) - 1);
   auto page_of = [&](uint32_t x) -> uint32_t { return POW2 ? x >> pshift : x / static_cast<uint32_t>(P); };
 
+  // Loads complete in issue order, so they are issued in the order of their use:
+  // the page-bitmap words of the walk, the page tables of short histories (used after
+  // the walk), then with at most 16 slots per thread and an int16 LRU (registers to
+  // spare) the hot tags and the LRU, whose loads then run under the walk and the page pass.
+  constexpr bool EARLY = SR <= 16 && L16;
+  // page-bitmap word of token words T + k * RT (one word each: a power-of-two page
+  // of at most 32 tokens puts a token word's pages in one bitmap word)
+  const bool pb_pre = d.page_bits && POW2 && P <= 32 && wl <= static_cast<int64_t>(RT) * WALK_PRE;
+  uint32_t pbw[WALK_PRE];
+  if (pb_pre) {
+#pragma unroll
+    for (int k = 0; k < WALK_PRE; ++k) {
+      const int64_t wd = T + static_cast<int64_t>(k) * RT;
+      const bool in = wd < wl && (wd << 5) < L;  // the bitmap has ceil(pages / 32) words
+      const uint32_t v = d.page_bits[in ? (wd >> pshift) : 0];
+      pbw[k] = in ? v : 0u;
+    }
+  }
   // the page tables of short histories are loaded now and used after the token walk
-  const bool pages_early = NP <= static_cast<int64_t>(RT) * PAGE_REGS;
-  int32_t src_e[PAGE_REGS], res_e[PAGE_REGS];  // res_e: only its sign is used
+  // (fewer pages per thread with the early tags and LRU: registers)
+  constexpr int PR = EARLY ? 4 : PAGE_REGS;
+  const bool pages_early = NP <= static_cast<int64_t>(RT) * PR;
+  int32_t src_e[PR], res_e[PR];  // res_e: only its sign is used
   if (pages_early) {
 #pragma unroll
-    for (int k = 0; k < PAGE_REGS; ++k) {
+    for (int k = 0; k < PR; ++k) {
       const int64_t p = T + static_cast<int64_t>(k) * RT;
       const int64_t pc = p < NP ? p : 0;  // unconditional loads, masked when used
       src_e[k] = d.source[pc];
       res_e[k] = d.resident[pc];
     }
   }
+  // the hot tags (one round), and the LRU (slots < 32768, read before any is
+  // rewritten).  Row q of thread T holds LRU entry q * RT + T (int64 tables: the
+  // entry's low word), or for int16 tables the entries 2 (q * RT + T) and
+  // 2 (q * RT + T) + 1 in one 32-bit word (lower entry in the low half).  Rows past
+  // hot_rows load entry 0 and are masked where used.
+  constexpr int HALVES = L16 ? 2 : 1;
+  constexpr int LROWS = SR / HALVES;
+  int32_t tg[SR];
+  int32_t slot[LROWS];
+  auto load_tags = [&]() {
+#pragma unroll
+    for (int k = 0; k < SR; ++k) {
+      const int32_t s = k * RT + T;
+      const int32_t v = d.tags[s < S ? s : 0];  // unconditional load, masked afterwards
+      tg[k] = s < S ? v : -1;
+    }
+  };
+  auto load_lru = [&]() {
+    const int32_t* lru32 = static_cast<const int32_t*>(d.lru);
+#pragma unroll
+    for (int q = 0; q < LROWS; ++q) {
+      const int32_t jp = q * RT + T;
+      slot[q] = lru32[HALVES * jp < S ? (L16 ? jp : 2 * jp) : 0];  // hot_rows even for int16 (host-checked)
+    }
+  };
+  if constexpr (EARLY) {
+    load_tags();
+    load_lru();
+  }
   for (int64_t i = T; i < 2 * wl + wsw; i += RT) lds[i] = 0u;
-  for (int64_t i = T; i < wl; i += RT) w.dupbits[i] = 0u;
+  if (!d.page_bits)  // a page bitmap admits no duplicate input
+    for (int64_t i = T; i < wl; i += RT) w.dupbits[i] = 0u;
   if (T == 0) {
     any_dup = 0;
     base_lo = INT32_MAX;
@@ -262,7 +315,21 @@ __global__ __launch_bounds__(RT) void resolve_front_kernel(ResolveBatch batch) {
   // changes.  A token already in the register, or already in the word when
   // it is published, is a duplicate; any input order gives the same bitmap
   // and duplicate set.
-  if (d.page_bits) {  // the same for every thread
+  if (pb_pre) {  // the same for every thread
+    const uint32_t ppw = static_cast<uint32_t>(32 / P);  // pages per token word
+    const uint32_t pmask = P >= 32 ? 0xffffffffu : (1u << P) - 1u;
+#pragma unroll
+    for (int k = 0; k < WALK_PRE; ++k) {
+      const int64_t wd = T + static_cast<int64_t>(k) * RT;
+      if (wd >= wl) break;
+      const uint32_t first = static_cast<uint32_t>(wd << (5 - pshift)) & 31u;  // first page bit of the word
+      const uint32_t pb = (pbw[k] >> first) & (ppw >= 32 ? 0xffffffffu : (1u << ppw) - 1u);
+      uint32_t m = 0u;
+      for (uint32_t j = 0; j < ppw; ++j)
+        if ((pb >> j) & 1u) m |= pmask << (j * static_cast<uint32_t>(P));
+      bits[wd] = m & range_mask(wd, 0, L);  // each word has one writer
+    }
+  } else if (d.page_bits) {  // the same for every thread
     for (int64_t wd = T; wd < wl; wd += RT) {
       const int64_t t0 = wd << 5;
       const int64_t t1 = t0 + 32 < L ? t0 + 32 : L;  // tokens [t0, t1) of this word
@@ -385,7 +452,7 @@ __global__ __launch_bounds__(RT) void resolve_front_kernel(ResolveBatch batch) {
   };
   if (pages_early) {
 #pragma unroll
-    for (int k = 0; k < PAGE_REGS; ++k) {
+    for (int k = 0; k < PR; ++k) {
       const int64_t p = T + static_cast<int64_t>(k) * RT;
       const bool in = p < NP && p * P < L;
       page_work(p, in ? src_e[k] : -1, res_e[k]);
@@ -414,14 +481,7 @@ __global__ __launch_bounds__(RT) void resolve_front_kernel(ResolveBatch batch) {
   }
   int64_t tot_res;
   block_exclusive_sum<int64_t>(c_res, scan64, &tot_res);  // synchronises the block
-  // the hot tags (one round)
-  int32_t tg[LRU_CHUNK];
-#pragma unroll
-  for (int k = 0; k < LRU_CHUNK; ++k) {
-    const int32_t s = k * RT + T;
-    const int32_t v = d.tags[s < S ? s : 0];  // unconditional load, masked afterwards
-    tg[k] = s < S ? v : -1;
-  }
+  if constexpr (!EARLY) load_tags();
 
   const bool affine = base_lo >= base_hi;  // one shift, or no host-backed page
   const int64_t shift = base_hi;
@@ -464,7 +524,7 @@ __global__ __launch_bounds__(RT) void resolve_front_kernel(ResolveBatch batch) {
   if (!affine) {
     const uint32_t hmask = static_cast<uint32_t>(w.hcap - 1);
 #pragma unroll
-    for (int k0 = 0; k0 < LRU_CHUNK; k0 += TAG_BATCH) {
+    for (int k0 = 0; k0 < SR; k0 += TAG_BATCH) {
       uint64_t e[TAG_BATCH];
       uint32_t h[TAG_BATCH], hp[TAG_BATCH];
 #pragma unroll
@@ -492,7 +552,7 @@ __global__ __launch_bounds__(RT) void resolve_front_kernel(ResolveBatch batch) {
   // of the wave keep (row k) and store once at the end.
   uint32_t myprot = 0u;
 #pragma unroll
-  for (int k0 = 0; k0 < LRU_CHUNK; k0 += MATCH_BATCH) {
+  for (int k0 = 0; k0 < SR; k0 += MATCH_BATCH) {
     uint32_t t[MATCH_BATCH], nw[MATCH_BATCH];
     bool ok[MATCH_BATCH];
 #pragma unroll
@@ -521,22 +581,8 @@ __global__ __launch_bounds__(RT) void resolve_front_kernel(ResolveBatch batch) {
     if (wi < wsw) prot[wi] = myprot;
   }
 
-  // the LRU (slots < 32768), read before any is rewritten; the loads run while the
-  // miss words are counted.  Row q of thread T holds LRU entry q * RT + T (int64
-  // tables: the entry's low word), or for int16 tables the entries 2 (q * RT + T) and
-  // 2 (q * RT + T) + 1 in one 32-bit word (lower entry in the low half).  Rows past
-  // hot_rows load entry 0 and are masked where used.
-  constexpr int HALVES = L16 ? 2 : 1;
-  constexpr int LROWS = LRU_CHUNK / HALVES;
-  int32_t slot[LROWS];
-  {
-    const int32_t* lru32 = static_cast<const int32_t*>(d.lru);
-#pragma unroll
-    for (int q = 0; q < LROWS; ++q) {
-      const int32_t jp = q * RT + T;
-      slot[q] = lru32[HALVES * jp < S ? (L16 ? jp : 2 * jp) : 0];  // hot_rows even for int16 (host-checked)
-    }
-  }
+  // the LRU loads of larger hot regions run while the miss words are counted
+  if constexpr (!EARLY) load_lru();
   // slot of half h of row q, and its LRU entry index
   auto slot_at = [&](int q, int h) -> int32_t {
     if constexpr (L16) return h ? static_cast<int32_t>(static_cast<uint32_t>(slot[q]) >> 16) : (slot[q] & 0xffff);
@@ -824,13 +870,28 @@ extern "C" int hs_resolve_rows_batched(const hs_resolve_desc* descs, int32_t cou
   return resolve_launch(descs, count, static_cast<char*>(workspace), stream);
 }
 
+template <int SR>
+static void launch_front(bool pow2, bool l16, unsigned nb, size_t lds, hipStream_t stream, const ResolveBatch& batch) {
+  if (l16) {
+    if (pow2) hipLaunchKernelGGL((resolve_front_kernel<true, true, SR>), dim3(nb), dim3(RT), lds, stream, batch);
+    else hipLaunchKernelGGL((resolve_front_kernel<false, true, SR>), dim3(nb), dim3(RT), lds, stream, batch);
+  } else {
+    if (pow2) hipLaunchKernelGGL((resolve_front_kernel<true, false, SR>), dim3(nb), dim3(RT), lds, stream, batch);
+    else hipLaunchKernelGGL((resolve_front_kernel<false, false, SR>), dim3(nb), dim3(RT), lds, stream, batch);
+  }
+}
+
 static int resolve_launch(const hs_resolve_desc* descs, int32_t count, char* workspace, hipStream_t stream) {
   static bool attr_set = false;
   if (!attr_set) {
-    for (const void* f : {reinterpret_cast<const void*>(resolve_front_kernel<true, false>),
-                          reinterpret_cast<const void*>(resolve_front_kernel<false, false>),
-                          reinterpret_cast<const void*>(resolve_front_kernel<true, true>),
-                          reinterpret_cast<const void*>(resolve_front_kernel<false, true>)})
+    for (const void* f : {reinterpret_cast<const void*>(resolve_front_kernel<true, false, 16>),
+                          reinterpret_cast<const void*>(resolve_front_kernel<false, false, 16>),
+                          reinterpret_cast<const void*>(resolve_front_kernel<true, true, 16>),
+                          reinterpret_cast<const void*>(resolve_front_kernel<false, true, 16>),
+                          reinterpret_cast<const void*>(resolve_front_kernel<true, false, 32>),
+                          reinterpret_cast<const void*>(resolve_front_kernel<false, false, 32>),
+                          reinterpret_cast<const void*>(resolve_front_kernel<true, true, 32>),
+                          reinterpret_cast<const void*>(resolve_front_kernel<false, true, 32>)})
       (void)hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kMaxResolverLds));
     (void)hipGetLastError();
     attr_set = true;
@@ -839,7 +900,7 @@ static int resolve_launch(const hs_resolve_desc* descs, int32_t count, char* wor
   for (int32_t start = 0; start < count; start += RMAXB) {
     ResolveBatch batch{};
     batch.count = count - start < RMAXB ? count - start : RMAXB;
-    int64_t front_lds = 0, max_out = 0;
+    int64_t front_lds = 0, max_out = 0, max_hot = 0;
     bool pow2 = true;  // every descriptor's page size a power of two
     for (int i = 0; i < batch.count; ++i) {
       hs_resolve_desc& d = batch.d[i];
@@ -848,18 +909,15 @@ static int resolve_launch(const hs_resolve_desc* descs, int32_t count, char* wor
       ws += hs_resolve_workspace_bytes(d.n, d.length, d.n_pages, d.hot_rows);
       if (front_lds_bytes(d.length, d.hot_rows) > front_lds) front_lds = front_lds_bytes(d.length, d.hot_rows);
       pow2 &= (d.page_size & (d.page_size - 1)) == 0;
+      if (d.hot_rows > max_hot) max_hot = d.hot_rows;
       const int64_t outs = d.n + (d.head_columns ? d.heads * d.width : 0);
       if (outs > max_out) max_out = outs;
     }
     const unsigned nb = static_cast<unsigned>(batch.count);
     const size_t lds = static_cast<size_t>(front_lds);
-    if (batch.d[0].lru_i16) {  // the same for every descriptor (validated)
-      if (pow2) hipLaunchKernelGGL((resolve_front_kernel<true, true>), dim3(nb), dim3(RT), lds, stream, batch);
-      else hipLaunchKernelGGL((resolve_front_kernel<false, true>), dim3(nb), dim3(RT), lds, stream, batch);
-    } else {
-      if (pow2) hipLaunchKernelGGL((resolve_front_kernel<true, false>), dim3(nb), dim3(RT), lds, stream, batch);
-      else hipLaunchKernelGGL((resolve_front_kernel<false, false>), dim3(nb), dim3(RT), lds, stream, batch);
-    }
+    const bool l16 = batch.d[0].lru_i16 != 0;  // the same for every descriptor (validated)
+    if (max_hot <= 16 * RT) launch_front<16>(pow2, l16, nb, lds, stream, batch);
+    else launch_front<32>(pow2, l16, nb, lds, stream, batch);
     HS_CHECK_LAUNCH("resolver front");
     hipLaunchKernelGGL(resolve_outputs_kernel, dim3(static_cast<unsigned>(ceil_div(max_out, RW)), nb), dim3(RW),
                        0, stream, batch);
