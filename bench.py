@@ -713,6 +713,7 @@ TRACE_SUMMARIES = {
     "qwen2.5-7b": os.path.join(PROFILES, "qwen2.5-7b_e2e_kernel_trace.md"),
     "microbench": os.path.join(PROFILES, "microbench_kernel_trace.md"),
     "qwen2.5-7b-layer": os.path.join(PROFILES, "qwen2.5-7b_layer_kernel_trace.md"),
+    "qwen2.5-0.5b-layer": os.path.join(PROFILES, "qwen2.5-0.5b_layer_kernel_trace.md"),
 }
 
 
@@ -1211,7 +1212,6 @@ def run_microbench(args, torch, device):
     copy = hbm_copy_gbs(torch, device)
     ceilings = attention_ceilings(torch, w, bytes_["attention"])
     att_gbs = bytes_["attention"] / (stages["attention"] * 1e-3) / 1e9
-    # the committed counter summary was taken on the default microbench run
     # the committed counter summary of this workload, when its shape is the one profiled
     pmc_path = PMC_SUMMARIES[args.workload][0] if args.workload in PMC_SUMMARIES else None
     counters_apply = pmc_path is not None and args.batch == shape.batch
