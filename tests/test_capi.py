@@ -85,6 +85,44 @@ def test_host_queries_and_argument_errors_without_a_gpu():
     assert status == -1 and b"dtype" in lib.hs_last_error()
 
 
+def _fake_resolve_desc(hot_rows=64, lru_i16=0):
+    """A descriptor that passes the null and shape checks (pointers are never dereferenced
+    on the host: every case below is rejected before any launch)."""
+    d = _lib.ResolveDesc()
+    for i, name in enumerate(("positions", "source", "resident", "hot", "tags", "lru", "physical",
+                              "miss_host_rows", "miss_device_rows", "counts")):
+        setattr(d, name, 0x10000 * (i + 1))
+    d.n, d.length, d.page_size, d.n_pages = 8, 64, 16, 4
+    d.hot_rows, d.hot_blocks, d.lru_i16 = hot_rows, (hot_rows + 15) // 16, lru_i16
+    return d
+
+
+def test_resolver_lru_dtype_rules_without_a_gpu():
+    """int16 LRU tables: the flag is 0 or 1, hot_rows even (pairs per 32-bit load), one
+    dtype per batch; all rejected on the host."""
+    lib = _lib.load()
+    assert lib.hs_resolve_rows(_fake_resolve_desc(lru_i16=2), None, 0, None) == -1
+    assert b"lru_i16 must be 0 or 1" in lib.hs_last_error()
+    assert lib.hs_resolve_rows(_fake_resolve_desc(hot_rows=63, lru_i16=1), None, 0, None) == -1
+    assert b"even hot_rows" in lib.hs_last_error()
+    pair = (_lib.ResolveDesc * 2)(_fake_resolve_desc(lru_i16=1), _fake_resolve_desc(lru_i16=0))
+    assert lib.hs_resolve_rows_batched(pair, 2, None, 0, None) == -1
+    assert b"share lru_i16" in lib.hs_last_error()
+    # a valid batch gets as far as the workspace check
+    same = (_lib.ResolveDesc * 2)(_fake_resolve_desc(lru_i16=1), _fake_resolve_desc(lru_i16=1))
+    assert lib.hs_resolve_rows_batched(same, 2, None, 0, None) == -1
+    assert b"workspace too small" in lib.hs_last_error()
+
+
+def test_union_page_bitmap_stride_checked_without_a_gpu():
+    lib = _lib.load()
+    lengths = (ctypes.c_int64 * 1)(4096)  # 256 pages: 8 bitmap words
+    args = [0x1000, 64, 8, lengths, 16, 1, 8, 2, 0x2000, 4096, 0x3000, 128, 0x4000, 0x5000, 0x6000, 4096,
+            0x7000, 0x8000]
+    assert lib.hs_build_union(*args, 0x9000, 7, None) == -1
+    assert b"page bitmap stride" in lib.hs_last_error()
+
+
 def test_missing_library_fails_loudly(tmp_path):
     with pytest.raises(_lib.HipLibraryError, match="missing"):
         _lib.load(tmp_path / "libhisparse_hip.so")
