@@ -216,6 +216,7 @@ template <bool POW2, bool L16, int SR>
 __global__ __launch_bounds__(RT) void resolve_front_kernel(ResolveBatch batch) {
   extern __shared__ uint32_t lds[];
   __shared__ int64_t scan64[16];
+  __shared__ unsigned long long s_res;  // resident hits of the request
   __shared__ int32_t scan32[16];
   __shared__ int any_dup;
   __shared__ int32_t base_lo, base_hi;
@@ -234,10 +235,8 @@ __global__ __launch_bounds__(RT) void resolve_front_kernel(ResolveBatch batch) {
   auto page_of = [&](uint32_t x) -> uint32_t { return POW2 ? x >> pshift : x / static_cast<uint32_t>(P); };
 
   // Loads complete in issue order, so they are issued in the order of their use:
-  // the page-bitmap words of the walk, the page tables of short histories (used after
-  // the walk), then with at most 16 slots per thread and an int16 LRU (registers to
-  // spare) the hot tags and the LRU, whose loads then run under the walk and the page pass.
-  constexpr bool EARLY = SR <= 16 && L16;
+  // the page-bitmap words of the walk first, then the page tables of short histories
+  // (used after the walk).
   // page-bitmap word of token words T + k * RT (one word each: a power-of-two page
   // of at most 32 tokens puts a token word's pages in one bitmap word)
   const bool pb_pre = d.page_bits && POW2 && P <= 32 && wl <= static_cast<int64_t>(RT) * WALK_PRE;
@@ -252,8 +251,7 @@ __global__ __launch_bounds__(RT) void resolve_front_kernel(ResolveBatch batch) {
     }
   }
   // the page tables of short histories are loaded now and used after the token walk
-  // (fewer pages per thread with the early tags and LRU: registers)
-  constexpr int PR = EARLY ? 4 : PAGE_REGS;
+  constexpr int PR = PAGE_REGS;
   const bool pages_early = NP <= static_cast<int64_t>(RT) * PR;
   int32_t src_e[PR], res_e[PR];  // res_e: only its sign is used
   if (pages_early) {
@@ -265,21 +263,25 @@ __global__ __launch_bounds__(RT) void resolve_front_kernel(ResolveBatch batch) {
       res_e[k] = d.resident[pc];
     }
   }
-  // the hot tags (one round), and the LRU (slots < 32768, read before any is
-  // rewritten).  Row q of thread T holds LRU entry q * RT + T (int64 tables: the
-  // entry's low word), or for int16 tables the entries 2 (q * RT + T) and
-  // 2 (q * RT + T) + 1 in one 32-bit word (lower entry in the low half).  Rows past
-  // hot_rows load entry 0 and are masked where used.
-  constexpr int HALVES = L16 ? 2 : 1;
+  // The hot tags, TR rows of RT slots per round (row k of thread T: slot k * RT + T),
+  // and the LRU (slots < 32768, read before any is rewritten): row q of thread T
+  // holds the entries 2 (q * RT + T) and 2 (q * RT + T) + 1 as two 16-bit halves of one
+  // register (lower entry in the low half): one 32-bit load for int16 tables, the low
+  // words of two entries for int64 ones.  Rows past hot_rows load entry 0 and are
+  // masked where used.  (Holding every tag and every LRU entry of 32 rows in registers
+  // at once made the compiler spill; a build of that form returned wrong tags in one
+  // row at the 32768-slot shape, so the per-thread state is kept to 16 + 16 registers.)
+  constexpr int TR = 16;
+  constexpr int HALVES = 2;
   constexpr int LROWS = SR / HALVES;
-  int32_t tg[SR];
+  int32_t tg[TR];
   int32_t slot[LROWS];
-  auto load_tags = [&]() {
+  auto load_tags = [&](int r) {
 #pragma unroll
-    for (int k = 0; k < SR; ++k) {
-      const int32_t s = k * RT + T;
+    for (int kk = 0; kk < TR; ++kk) {
+      const int32_t s = (r * TR + kk) * RT + T;
       const int32_t v = d.tags[s < S ? s : 0];  // unconditional load, masked afterwards
-      tg[k] = s < S ? v : -1;
+      tg[kk] = s < S ? v : -1;
     }
   };
   auto load_lru = [&]() {
@@ -287,18 +289,21 @@ __global__ __launch_bounds__(RT) void resolve_front_kernel(ResolveBatch batch) {
 #pragma unroll
     for (int q = 0; q < LROWS; ++q) {
       const int32_t jp = q * RT + T;
-      slot[q] = lru32[HALVES * jp < S ? (L16 ? jp : 2 * jp) : 0];  // hot_rows even for int16 (host-checked)
+      if constexpr (L16) {
+        slot[q] = lru32[2 * jp < S ? jp : 0];  // hot_rows even for int16 (host-checked)
+      } else {
+        const int32_t lo = lru32[2 * (2 * jp < S ? 2 * jp : 0)];
+        const int32_t hi = lru32[2 * (2 * jp + 1 < S ? 2 * jp + 1 : 0)];
+        slot[q] = (lo & 0xffff) | (hi << 16);
+      }
     }
   };
-  if constexpr (EARLY) {
-    load_tags();
-    load_lru();
-  }
   for (int64_t i = T; i < 2 * wl + wsw; i += RT) lds[i] = 0u;
   if (!d.page_bits)  // a page bitmap admits no duplicate input
     for (int64_t i = T; i < wl; i += RT) w.dupbits[i] = 0u;
   if (T == 0) {
     any_dup = 0;
+    s_res = 0ull;
     base_lo = INT32_MAX;
     base_hi = INT32_MIN;
   }
@@ -479,9 +484,11 @@ __global__ __launch_bounds__(RT) void resolve_front_kernel(ResolveBatch batch) {
     atomicMin(&base_lo, my_lo);
     atomicMax(&base_hi, my_hi);
   }
-  int64_t tot_res;
-  block_exclusive_sum<int64_t>(c_res, scan64, &tot_res);  // synchronises the block
-  if constexpr (!EARLY) load_tags();
+  // resident hits: only the request's total is needed (one LDS add per wave)
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) c_res += __shfl_xor(c_res, off, 64);
+  if (lane == 0) atomicAdd(&s_res, static_cast<unsigned long long>(c_res));
+  __syncthreads();  // the page pass and the block-range atomics are complete
 
   const bool affine = base_lo >= base_hi;  // one shift, or no host-backed page
   const int64_t shift = base_hi;
@@ -521,59 +528,63 @@ __global__ __launch_bounds__(RT) void resolve_front_kernel(ResolveBatch batch) {
   const uint32_t Lu = static_cast<uint32_t>(L), Pu = static_cast<uint32_t>(P);
   const uint32_t hist_pages = static_cast<uint32_t>((L + P - 1) / P < NP ? (L + P - 1) / P : NP);
   const uint32_t ushift = affine ? static_cast<uint32_t>(static_cast<int32_t>(shift)) : 0u;
-  if (!affine) {
-    const uint32_t hmask = static_cast<uint32_t>(w.hcap - 1);
-#pragma unroll
-    for (int k0 = 0; k0 < SR; k0 += TAG_BATCH) {
-      uint64_t e[TAG_BATCH];
-      uint32_t h[TAG_BATCH], hp[TAG_BATCH];
-#pragma unroll
-      for (int j = 0; j < TAG_BATCH; ++j) {  // first probes in flight together
-        hp[j] = page_of(static_cast<uint32_t>(tg[k0 + j]));
-        h[j] = hash32(hp[j]) & hmask;
-        e[j] = tg[k0 + j] >= 0 ? load_l2(&w.hash[h[j]]) : HASH_EMPTY;
-      }
-#pragma unroll
-      for (int j = 0; j < TAG_BATCH; ++j) {
-        while (e[j] != HASH_EMPTY && static_cast<uint32_t>(e[j]) != hp[j]) {
-          h[j] = (h[j] + 1) & hmask;
-          e[j] = load_l2(&w.hash[h[j]]);
-        }
-        const uint32_t off = static_cast<uint32_t>(tg[k0 + j]) - hp[j] * Pu;
-        tg[k0 + j] = e[j] == HASH_EMPTY || tg[k0 + j] < 0 ? -1
-                                                          : static_cast<int32_t>(static_cast<uint32_t>(e[j] >> 32) * Pu + off);
-      }
-    }
-  }
-
-  // a tag whose token needs a hot row is a hit (row_index.py:84-90).  Batches of
-  // MATCH_BATCH tags with their needs-bit reads in flight together; the slots of
-  // a wave's 64 tags form two whole protection words, which lanes 2k and 2k + 1
-  // of the wave keep (row k) and store once at the end.
+  // a tag whose token needs a hot row is a hit (row_index.py:84-90), TR rows per
+  // round.  Batches of MATCH_BATCH tags with their needs-bit reads in flight
+  // together; the slots of a wave's 64 tags form two whole protection words, which
+  // lanes 2k and 2k + 1 of the wave keep (row k) and store once at the end.
   uint32_t myprot = 0u;
+#pragma unroll 1
+  for (int r = 0; r < SR / TR; ++r) {
+    load_tags(r);
+    if (!affine) {
+      const uint32_t hmask = static_cast<uint32_t>(w.hcap - 1);
 #pragma unroll
-  for (int k0 = 0; k0 < SR; k0 += MATCH_BATCH) {
-    uint32_t t[MATCH_BATCH], nw[MATCH_BATCH];
-    bool ok[MATCH_BATCH];
+      for (int k0 = 0; k0 < TR; k0 += TAG_BATCH) {
+        uint64_t e[TAG_BATCH];
+        uint32_t h[TAG_BATCH], hp[TAG_BATCH];
 #pragma unroll
-    for (int j = 0; j < MATCH_BATCH; ++j) {
-      const uint32_t tag = static_cast<uint32_t>(tg[k0 + j]);
-      const uint32_t hp = page_of(tag);
-      const uint32_t page = hp - ushift;  // a block outside the range wraps to >= 2^31
-      t[j] = POW2 ? (page << pshift) | (tag & (Pu - 1u)) : page * Pu + (tag - hp * Pu);
-      ok[j] = tg[k0 + j] >= 0 && page < hist_pages && t[j] < Lu;
-      nw[j] = needs[ok[j] ? t[j] >> 5 : 0];
-    }
+        for (int j = 0; j < TAG_BATCH; ++j) {  // first probes in flight together
+          hp[j] = page_of(static_cast<uint32_t>(tg[k0 + j]));
+          h[j] = hash32(hp[j]) & hmask;
+          e[j] = tg[k0 + j] >= 0 ? load_l2(&w.hash[h[j]]) : HASH_EMPTY;
+        }
 #pragma unroll
-    for (int j = 0; j < MATCH_BATCH; ++j) {
-      const int k = k0 + j;
-      const bool hit = ok[j] && ((nw[j] >> (t[j] & 31)) & 1u);
-      if (hit) {
-        atomicOr(&bits[t[j] >> 5], 1u << (t[j] & 31));
-        w.tslot[t[j]] = k * RT + T;
+        for (int j = 0; j < TAG_BATCH; ++j) {
+          while (e[j] != HASH_EMPTY && static_cast<uint32_t>(e[j]) != hp[j]) {
+            h[j] = (h[j] + 1) & hmask;
+            e[j] = load_l2(&w.hash[h[j]]);
+          }
+          const uint32_t off = static_cast<uint32_t>(tg[k0 + j]) - hp[j] * Pu;
+          tg[k0 + j] = e[j] == HASH_EMPTY || tg[k0 + j] < 0 ? -1
+                                                            : static_cast<int32_t>(static_cast<uint32_t>(e[j] >> 32) * Pu + off);
+        }
       }
-      const uint64_t m = __ballot(hit);
-      myprot = (lane >> 1) == k ? ((lane & 1) ? static_cast<uint32_t>(m >> 32) : static_cast<uint32_t>(m)) : myprot;
+    }
+
+#pragma unroll
+    for (int k0 = 0; k0 < TR; k0 += MATCH_BATCH) {
+      uint32_t t[MATCH_BATCH], nw[MATCH_BATCH];
+      bool ok[MATCH_BATCH];
+#pragma unroll
+      for (int j = 0; j < MATCH_BATCH; ++j) {
+        const uint32_t tag = static_cast<uint32_t>(tg[k0 + j]);
+        const uint32_t hp = page_of(tag);
+        const uint32_t page = hp - ushift;  // a block outside the range wraps to >= 2^31
+        t[j] = POW2 ? (page << pshift) | (tag & (Pu - 1u)) : page * Pu + (tag - hp * Pu);
+        ok[j] = tg[k0 + j] >= 0 && page < hist_pages && t[j] < Lu;
+        nw[j] = needs[ok[j] ? t[j] >> 5 : 0];
+      }
+#pragma unroll
+      for (int j = 0; j < MATCH_BATCH; ++j) {
+        const int k = r * TR + k0 + j;
+        const bool hit = ok[j] && ((nw[j] >> (t[j] & 31)) & 1u);
+        if (hit) {
+          atomicOr(&bits[t[j] >> 5], 1u << (t[j] & 31));
+          w.tslot[t[j]] = k * RT + T;
+        }
+        const uint64_t m = __ballot(hit);
+        myprot = (lane >> 1) == k ? ((lane & 1) ? static_cast<uint32_t>(m >> 32) : static_cast<uint32_t>(m)) : myprot;
+      }
     }
   }
   {
@@ -581,12 +592,11 @@ __global__ __launch_bounds__(RT) void resolve_front_kernel(ResolveBatch batch) {
     if (wi < wsw) prot[wi] = myprot;
   }
 
-  // the LRU loads of larger hot regions run while the miss words are counted
-  if constexpr (!EARLY) load_lru();
+  // the LRU loads run while the miss words are counted
+  load_lru();
   // slot of half h of row q, and its LRU entry index
   auto slot_at = [&](int q, int h) -> int32_t {
-    if constexpr (L16) return h ? static_cast<int32_t>(static_cast<uint32_t>(slot[q]) >> 16) : (slot[q] & 0xffff);
-    else return slot[q];
+    return h ? static_cast<int32_t>(static_cast<uint32_t>(slot[q]) >> 16) : (slot[q] & 0xffff);
   };
   auto entry_of = [&](int q, int h) -> int32_t { return HALVES * (q * RT + T) + h; };
 
@@ -598,6 +608,16 @@ __global__ __launch_bounds__(RT) void resolve_front_kernel(ResolveBatch batch) {
   const int64_t w1 = w0 + wpt < wl ? w0 + wpt : wl;
   int64_t c_hit = 0, c_miss = 0;
   int64_t tot_hit, tot_miss;
+  // one block scan of the (hits, misses) pair packed in 64 bits (each count is below
+  // 2^31, so the halves never carry into each other): the miss prefix and both totals
+  auto hit_miss_scan = [&](int64_t h, int64_t m, int64_t& th, int64_t& tm_) -> int64_t {
+    uint64_t tot;
+    const uint64_t ex = block_exclusive_sum<uint64_t>((static_cast<uint64_t>(h) << 32) | static_cast<uint64_t>(m),
+                                                      reinterpret_cast<uint64_t*>(scan64), &tot);
+    th = static_cast<int64_t>(tot >> 32);
+    tm_ = static_cast<int64_t>(tot & 0xffffffffull);
+    return static_cast<int64_t>(ex & 0xffffffffull);
+  };
   if (wpt <= ORDER_WORDS) {
     uint32_t miss[ORDER_WORDS];
 #pragma unroll
@@ -613,8 +633,7 @@ __global__ __launch_bounds__(RT) void resolve_front_kernel(ResolveBatch batch) {
         w.missbits[wd] = miss[k];
       }
     }
-    block_exclusive_sum<int64_t>(c_hit, scan64, &tot_hit);
-    int64_t r = block_exclusive_sum<int64_t>(c_miss, scan64, &tot_miss);
+    int64_t r = hit_miss_scan(c_hit, c_miss, tot_hit, tot_miss);
 #pragma unroll
     for (int k = 0; k < ORDER_WORDS; ++k) {
       if (w0 + k < w1) w.mprefix[w0 + k] = static_cast<int32_t>(r);
@@ -628,8 +647,7 @@ __global__ __launch_bounds__(RT) void resolve_front_kernel(ResolveBatch batch) {
       c_hit += __popc(hit);
       c_miss += __popc(miss);
     }
-    block_exclusive_sum<int64_t>(c_hit, scan64, &tot_hit);
-    int64_t r = block_exclusive_sum<int64_t>(c_miss, scan64, &tot_miss);
+    int64_t r = hit_miss_scan(c_hit, c_miss, tot_hit, tot_miss);
     for (int64_t wd = w0; wd < w1; ++wd) {
       w.mprefix[wd] = static_cast<int32_t>(r);
       r += __popc(needs[wd] & ~bits[wd]);
@@ -710,7 +728,7 @@ __global__ __launch_bounds__(RT) void resolve_front_kernel(ResolveBatch batch) {
     }
   }
   if (T == 0) {
-    w.totals[0] = tot_res;
+    w.totals[0] = static_cast<int64_t>(s_res);
     w.totals[1] = tot_hit;
     w.totals[2] = tot_miss;
     w.totals[3] = dups ? 1 : 0;
