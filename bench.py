@@ -712,6 +712,7 @@ def summarize_pmc(fetch_dir, write_dir, workload="microbench"):
 TRACE_SUMMARIES = {
     "qwen2.5-7b": os.path.join(PROFILES, "qwen2.5-7b_e2e_kernel_trace.md"),
     "qwen2.5-0.5b": os.path.join(PROFILES, "qwen2.5-0.5b_e2e_kernel_trace.md"),
+    "qwen2.5-32b-stress": os.path.join(PROFILES, "qwen2.5-32b-stress_e2e_kernel_trace.md"),
     "microbench": os.path.join(PROFILES, "microbench_kernel_trace.md"),
     "qwen2.5-7b-layer": os.path.join(PROFILES, "qwen2.5-7b_layer_kernel_trace.md"),
     "qwen2.5-0.5b-layer": os.path.join(PROFILES, "qwen2.5-0.5b_layer_kernel_trace.md"),

@@ -34,7 +34,25 @@ __device__ __forceinline__ float round_to(float v) {
 }
 
 // One workgroup per row.  `delta` may be null (no residual add); `x_out` may
-// alias `x`.
+// alias `x`.  A row of at most NR_REG * DN_T elements is held in registers: every
+// load of x, delta and the weight is issued before the first is used, so the row
+// costs one memory round trip (a store to x_out may alias the next load of x, so a
+// loop that stores as it goes would wait out a round trip per element).  Longer
+// rows go in rounds of NR_CH elements per thread, loads of a round issued together.
+constexpr int NR_REG = 24;
+constexpr int NR_CH = 8;
+
+__device__ __forceinline__ float block_sum_dn(float v, float* partial) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  if ((threadIdx.x & 63) == 0) partial[threadIdx.x >> 6] = v;
+  __syncthreads();
+  float total = 0.f;
+#pragma unroll
+  for (int w = 0; w < DN_T / 64; ++w) total += partial[w];
+  return total;
+}
+
 template <int DT>
 __global__ __launch_bounds__(DN_T) void add_rms_norm_kernel(const void* x, const void* delta, void* x_out, void* y,
                                                             const void* weight, int64_t width, int64_t x_stride,
@@ -42,27 +60,74 @@ __global__ __launch_bounds__(DN_T) void add_rms_norm_kernel(const void* x, const
   __shared__ float partial[DN_T / 64];
   const int64_t row = blockIdx.x;
   const int64_t xo = row * x_stride, yo = row * y_stride;
-  float sq = 0.f;
-  for (int64_t i = threadIdx.x; i < width; i += DN_T) {
-    float s = load_elem<DT>(x, xo + i);
-    if (delta != nullptr) {
-      s = round_to<DT>(s + load_elem<DT>(delta, xo + i));
-      store_elem<DT>(x_out, xo + i, s);
+  const bool add = delta != nullptr;
+  if (width <= static_cast<int64_t>(NR_REG) * DN_T) {
+    float v[NR_REG], dl[NR_REG], wv[NR_REG];
+#pragma unroll
+    for (int k = 0; k < NR_REG; ++k) {
+      const int64_t i = threadIdx.x + static_cast<int64_t>(k) * DN_T;
+      const bool in = i < width;
+      v[k] = in ? load_elem<DT>(x, xo + i) : 0.f;
+      dl[k] = in && add ? load_elem<DT>(delta, xo + i) : 0.f;
+      wv[k] = in ? load_elem<DT>(weight, i) : 0.f;
     }
-    sq += s * s;
+    float sq = 0.f;
+#pragma unroll
+    for (int k = 0; k < NR_REG; ++k) {
+      const int64_t i = threadIdx.x + static_cast<int64_t>(k) * DN_T;
+      if (i >= width) break;
+      if (add) {
+        v[k] = round_to<DT>(v[k] + dl[k]);
+        store_elem<DT>(x_out, xo + i, v[k]);
+      }
+      sq += v[k] * v[k];
+    }
+    const float r = rsqrtf(block_sum_dn(sq, partial) / static_cast<float>(width) + eps);
+#pragma unroll
+    for (int k = 0; k < NR_REG; ++k) {
+      const int64_t i = threadIdx.x + static_cast<int64_t>(k) * DN_T;
+      if (i >= width) break;
+      store_elem<DT>(y, yo + i, round_to<DT>(v[k] * r) * wv[k]);
+    }
+    return;
   }
+  float sq = 0.f;
+  for (int64_t base = threadIdx.x; base < width; base += static_cast<int64_t>(DN_T) * NR_CH) {
+    float a[NR_CH], b[NR_CH];
 #pragma unroll
-  for (int off = 32; off > 0; off >>= 1) sq += __shfl_xor(sq, off, 64);
-  if ((threadIdx.x & 63) == 0) partial[threadIdx.x >> 6] = sq;
-  __syncthreads();
-  float total = 0.f;
+    for (int k = 0; k < NR_CH; ++k) {
+      const int64_t i = base + static_cast<int64_t>(k) * DN_T;
+      a[k] = i < width ? load_elem<DT>(x, xo + i) : 0.f;
+      b[k] = i < width && add ? load_elem<DT>(delta, xo + i) : 0.f;
+    }
 #pragma unroll
-  for (int w = 0; w < DN_T / 64; ++w) total += partial[w];
-  const float r = rsqrtf(total / static_cast<float>(width) + eps);
-  const void* src = delta != nullptr ? x_out : x;
-  for (int64_t i = threadIdx.x; i < width; i += DN_T) {
-    const float s = load_elem<DT>(src, xo + i);
-    store_elem<DT>(y, yo + i, round_to<DT>(s * r) * load_elem<DT>(weight, i));
+    for (int k = 0; k < NR_CH; ++k) {
+      const int64_t i = base + static_cast<int64_t>(k) * DN_T;
+      if (i >= width) break;
+      float s = a[k];
+      if (add) {
+        s = round_to<DT>(s + b[k]);
+        store_elem<DT>(x_out, xo + i, s);
+      }
+      sq += s * s;
+    }
+  }
+  const float r = rsqrtf(block_sum_dn(sq, partial) / static_cast<float>(width) + eps);
+  const void* src = add ? x_out : x;
+  for (int64_t base = threadIdx.x; base < width; base += static_cast<int64_t>(DN_T) * NR_CH) {
+    float a[NR_CH], b[NR_CH];
+#pragma unroll
+    for (int k = 0; k < NR_CH; ++k) {
+      const int64_t i = base + static_cast<int64_t>(k) * DN_T;
+      a[k] = i < width ? load_elem<DT>(src, xo + i) : 0.f;
+      b[k] = i < width ? load_elem<DT>(weight, i) : 0.f;
+    }
+#pragma unroll
+    for (int k = 0; k < NR_CH; ++k) {
+      const int64_t i = base + static_cast<int64_t>(k) * DN_T;
+      if (i >= width) break;
+      store_elem<DT>(y, yo + i, round_to<DT>(a[k] * r) * b[k]);
+    }
   }
 }
 

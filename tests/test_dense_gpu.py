@@ -39,7 +39,7 @@ def test_wrappers_check_shapes_without_a_gpu():
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
-@pytest.mark.parametrize("rows,width", [(1, 896), (8, 3584), (3, 5120), (5, 100)])
+@pytest.mark.parametrize("rows,width", [(1, 896), (8, 3584), (3, 5120), (5, 100), (2, 7000)])
 def test_add_rms_norm_matches_the_model_norm(gpu, dtype, rows, width):
     gen = torch.Generator(device=gpu).manual_seed(rows * 7 + width)
     x = (torch.randn(rows, width, generator=gen, device=gpu) * 3).to(dtype)
