@@ -61,15 +61,21 @@ __global__ __launch_bounds__(DN_T) void add_rms_norm_kernel(const void* x, const
   const int64_t row = blockIdx.x;
   const int64_t xo = row * x_stride, yo = row * y_stride;
   const bool add = delta != nullptr;
+  const void* dsrc = add ? delta : x;  // always a valid row: no load sits under a branch
   if (width <= static_cast<int64_t>(NR_REG) * DN_T) {
     float v[NR_REG], dl[NR_REG], wv[NR_REG];
 #pragma unroll
     for (int k = 0; k < NR_REG; ++k) {
+      // unconditional loads of in-bounds elements (a load under a branch would be
+      // waited for before the next), masked afterwards
       const int64_t i = threadIdx.x + static_cast<int64_t>(k) * DN_T;
       const bool in = i < width;
-      v[k] = in ? load_elem<DT>(x, xo + i) : 0.f;
-      dl[k] = in && add ? load_elem<DT>(delta, xo + i) : 0.f;
-      wv[k] = in ? load_elem<DT>(weight, i) : 0.f;
+      const int64_t ic = in ? i : 0;
+      const float xv = load_elem<DT>(x, xo + ic), wvv = load_elem<DT>(weight, ic);
+      const float dv = load_elem<DT>(dsrc, xo + ic);
+      v[k] = in ? xv : 0.f;
+      dl[k] = in ? dv : 0.f;
+      wv[k] = in ? wvv : 0.f;
     }
     float sq = 0.f;
 #pragma unroll
@@ -97,8 +103,11 @@ __global__ __launch_bounds__(DN_T) void add_rms_norm_kernel(const void* x, const
 #pragma unroll
     for (int k = 0; k < NR_CH; ++k) {
       const int64_t i = base + static_cast<int64_t>(k) * DN_T;
-      a[k] = i < width ? load_elem<DT>(x, xo + i) : 0.f;
-      b[k] = i < width && add ? load_elem<DT>(delta, xo + i) : 0.f;
+      const int64_t ic = i < width ? i : 0;
+      const float xv = load_elem<DT>(x, xo + ic);
+      const float dv = load_elem<DT>(dsrc, xo + ic);
+      a[k] = i < width ? xv : 0.f;
+      b[k] = i < width ? dv : 0.f;
     }
 #pragma unroll
     for (int k = 0; k < NR_CH; ++k) {
@@ -119,8 +128,10 @@ __global__ __launch_bounds__(DN_T) void add_rms_norm_kernel(const void* x, const
 #pragma unroll
     for (int k = 0; k < NR_CH; ++k) {
       const int64_t i = base + static_cast<int64_t>(k) * DN_T;
-      a[k] = i < width ? load_elem<DT>(src, xo + i) : 0.f;
-      b[k] = i < width ? load_elem<DT>(weight, i) : 0.f;
+      const int64_t ic = i < width ? i : 0;
+      const float sv = load_elem<DT>(src, xo + ic), wvv = load_elem<DT>(weight, ic);
+      a[k] = i < width ? sv : 0.f;
+      b[k] = i < width ? wvv : 0.f;
     }
 #pragma unroll
     for (int k = 0; k < NR_CH; ++k) {
