@@ -745,20 +745,27 @@ __device__ __forceinline__ int64_t row_of_input(const hs_resolve_desc& d, const 
   const int64_t t = load_pos(d, i);
   const int64_t L = d.length, P = d.page_size, S = d.hot_rows;
   if (t < 0 || t >= L) return -1;
-  if (dups && bit_of(w.dupbits, t) && w.first_in[t] != static_cast<int32_t>(i)) return -1;
   const PageDiv pdiv(P);
   const int64_t page = pdiv.div(static_cast<uint32_t>(t));
   const int64_t off = t - page * P;
-  const int32_t src = d.source[page];
-  if (src < 0) return -1;
-  const int32_t res = d.resident[page];
-  if (res >= 0) return static_cast<int64_t>(res) * P + off;
   const int64_t word = t >> 5;
   const uint32_t bit = 1u << (t & 31);
-  if (w.hitbits[word] & bit) {
-    slot = w.tslot[t];
+  // everything that depends on the token alone, in one round of loads (a hit slot
+  // or a first input is read whether or not it applies, and used only where it does)
+  const int32_t src = d.source[page], res = d.resident[page];
+  const uint32_t hw = w.hitbits[word], mw = w.missbits[word];
+  const int32_t mp = w.mprefix[word], ts = w.tslot[t];
+  if (dups) {
+    const uint32_t dw = w.dupbits[word];
+    const int32_t fi = w.first_in[t];
+    if ((dw & bit) && fi != static_cast<int32_t>(i)) return -1;
+  }
+  if (src < 0) return -1;
+  if (res >= 0) return static_cast<int64_t>(res) * P + off;
+  if (hw & bit) {
+    slot = ts;
   } else {
-    miss_rank = w.mprefix[word] + __popc(w.missbits[word] & (bit - 1u));
+    miss_rank = mp + __popc(mw & (bit - 1u));
     slot = w.victims[miss_rank < S - 1 ? miss_rank : S - 1];
     host = static_cast<int64_t>(src) * P + off;
   }
