@@ -922,10 +922,12 @@ class AttendProbe:
     """HIP events around every attention launch of the timed steps, on the compute stream
     the launch runs on, and a device copy of each launch's entry counts (the rows each
     (request, KV head) reads), from which the launch's algorithmic bytes follow.  Events
-    and the count buffer are allocated before the timed region."""
+    and the count buffer are allocated before the timed region.  ``fence``: the engine
+    hands the gather's rows over from another stream (see ``before_attend``)."""
 
-    def __init__(self, torch, device, launches, batch, kv_heads):
+    def __init__(self, torch, device, launches, batch, kv_heads, fence=True):
         self.torch = torch
+        self.fence = fence
         self.start = [torch.cuda.Event(enable_timing=True) for _ in range(launches)]
         self.end = [torch.cuda.Event(enable_timing=True) for _ in range(launches)]
         self.counts = torch.zeros((launches, batch * kv_heads), dtype=torch.int32, device=device)
@@ -936,8 +938,10 @@ class AttendProbe:
         # HIP stamps an event with the end of the stream's previous command; the engine
         # queues a wait for the gather right before the attention, so a start event
         # recorded there could carry a time from before that wait.  A 1-cycle kernel
-        # placed after the wait gives the start event a time after it.
-        self.torch.cuda._sleep(1)
+        # placed after the wait gives the start event a time after it.  With every stage
+        # on one stream there is no such wait, and the start event follows the gather.
+        if self.fence:
+            self.torch.cuda._sleep(1)
         self.start[self.i].record(stream)
 
     def after_attend(self, layer, stream, dec):
@@ -1014,7 +1018,7 @@ def run_model_workload(args, torch, device):
     print("[bench] timing", file=sys.stderr, flush=True)
     stats0 = state.row_stats.clone()
     launches = args.steps * wl.layers * (len(engine.groups) if engine.groups else 1)
-    probe = AttendProbe(torch, device, launches, wl.batch, wl.kv_heads)
+    probe = AttendProbe(torch, device, launches, wl.batch, wl.kv_heads, fence=engine.transfer is not None)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
@@ -1028,7 +1032,7 @@ def run_model_workload(args, torch, device):
         # the same attention with the batch in one group and no gather running beside it:
         # two extra steps in layer order, outside the timed region
         groups_saved, engine.groups = engine.groups, None
-        solo = AttendProbe(torch, device, 2 * wl.layers, wl.batch, wl.kv_heads)
+        solo = AttendProbe(torch, device, 2 * wl.layers, wl.batch, wl.kv_heads, fence=engine.transfer is not None)
         for _ in range(2):
             tokens = engine.step(tokens, probe=solo)
         torch.cuda.synchronize()
