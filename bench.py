@@ -86,6 +86,10 @@ def parse_args():
                    help="uniform-selector model workloads: run select, resolve and gather in layer order "
                         "on the compute stream instead of prefetching every layer's at step start on a "
                         "transfer stream (overlapping the dense layers)")
+    p.add_argument("--projections", choices=["auto", "kernel", "torch"], default="auto",
+                   help="model workloads: the decode projections on hs_skinny_gemm or PyTorch's GEMM, or the faster "
+                        "of the two timed at start (auto; a kernel trace perturbs that timing, so the traces of "
+                        "the model workloads name the choice the bench line made)")
     p.add_argument("--graphs", action="store_true",
                    help="model workloads: replay each dense layer boundary as a captured HIP graph")
     p.add_argument("--request-groups", type=int, default=None,
@@ -797,7 +801,8 @@ def summarize_trace(trace_dir, args):
         agg[name][1] += int(r["End_Timestamp"]) - int(r["Start_Timestamp"])
     span_ms = (int(window[-1]["End_Timestamp"]) - int(window[0]["Start_Timestamp"])) / 1e6
     cmd = f"rocprofv3 --kernel-trace --stats -f csv -d <dir> -o bench -- python3 bench.py --workload {args.workload} " \
-          f"--no-microbench --no-cpu-baseline --steps {args.steps} --warmup {args.warmup}"
+          f"--no-microbench --no-cpu-baseline --projections {args.projections} --steps {args.steps} " \
+          f"--warmup {args.warmup}"
     att = [agg[k] for k in agg if k.startswith("hs::attend_mfma_kernel")]
     mrg = [agg[k] for k in agg if k.startswith("hs::attend_merge_kernel")]
     att_us = sum(d for _, d in att) / max(1, sum(c for c, _ in att)) / 1e3
@@ -806,8 +811,8 @@ def summarize_trace(trace_dir, args):
         f"# Kernel trace: {wl.name} end to end, timed steps only",
         "",
         f"Command: `{cmd}`",
-        f"Summarised by: `python bench.py --workload {args.workload} --steps {args.steps} --warmup {args.warmup} "
-        "--summarize-trace <dir>`",
+        f"Summarised by: `python bench.py --workload {args.workload} --projections {args.projections} "
+        f"--steps {args.steps} --warmup {args.warmup} --summarize-trace <dir>`",
         "",
         f"Timed region: {args.steps} steps x {L} layers x {groups} request group(s), {len(window)} dispatches "
         f"over {span_ms:.1f} ms "
@@ -1002,6 +1007,7 @@ def run_model_workload(args, torch, device):
     if groups is None:
         groups = DEFAULT_REQUEST_GROUPS.get(args.workload, 1)
     engine = BatchedDecodeEngine(model, state, wl.top_pages, selector=wl.selector, seed=args.seed, graphs=args.graphs,
+                                 projections=args.projections,
                                  prefetch=not args.no_prefetch and wl.selector == "uniform",
                                  request_groups=groups if wl.selector == "quest" else 1,
                                  group_gather_workgroups=args.group_gather_workgroups
