@@ -446,7 +446,12 @@ def test_union_builder_matches_host_adapter(gpu, pages, P, kv, g, top, length):
 
 
 # --------------------------------------------------------------------- gather
-@pytest.mark.parametrize("dtype,P,kv,D", [(torch.bfloat16, 16, 8, 128), (torch.float32, 4, 1, 8), (torch.float16, 7, 2, 24), (torch.bfloat16, 16, 4, 128)])
+# rows of 2 KB and 1 KB (one row plane per wave instruction), 256, 128 and 8 bytes (a wave
+# instruction reads one plane of 4, 8 and 64 consecutive entries), 32 bytes (2 units) and 96
+# bytes (6 units, not a divisor of the wave: per-row mapping)
+@pytest.mark.parametrize("dtype,P,kv,D", [(torch.bfloat16, 16, 8, 128), (torch.float32, 4, 1, 8), (torch.float16, 7, 2, 24),
+                                          (torch.bfloat16, 16, 4, 128), (torch.bfloat16, 16, 2, 64),
+                                          (torch.bfloat16, 16, 1, 64), (torch.float16, 3, 1, 4)])
 def test_gather_copies_planned_rows(gpu, dtype, P, kv, D):
     from mini_hisparse_amd.row_index import RowPlan
     from mini_hisparse_amd.row_kernels import MappedHost, gather_rows
