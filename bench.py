@@ -257,7 +257,9 @@ def run_steps(torch, w, steps, record):
     events = []
     last = w.get("last_use")
     out = None
-    for _ in range(steps):
+    kernel = KernelTimer(torch, steps) if record else None
+    w["attention_kernel"] = kernel
+    for step in range(steps):
         ev = [torch.cuda.Event(enable_timing=record) for _ in range(8)]
         w["tags_all"].copy_(w["tags0"])
         w["lru_all"].copy_(w["lru0"])
@@ -274,6 +276,8 @@ def run_steps(torch, w, steps, record):
         ev[4].record(transfer)
         compute.wait_event(ev[4])
         ev[5].record(compute)
+        if kernel is not None:
+            kernel.arm(step)
         out = dec.attend(w["q"], w["pool"])
         ev[6].record(compute)
         last = ev[6]
@@ -301,19 +305,24 @@ def run_pipelined(torch, w, steps):
     return out
 
 
-def stage_ms(events):
+def stage_ms(events, kernel=None):
     """Per-stage milliseconds: the median over the recorded steps, so that a one-off host
     stall (the GPU idles inside one stage's event pair until the host launches) does not
-    move it."""
+    move it.  With ``kernel`` (the steps' KernelTimer), "attention" is the attention
+    launch's own kernel duration and "attention_event_window" the stream events around it."""
     def avg(i, j):
         return float(np.median([e[i].elapsed_time(e[j]) for e in events]))
 
-    return {
+    out = {
         "quest_and_union": avg(0, 1),
         "resolve": avg(1, 2),
         "gather": avg(3, 4),
         "attention": avg(5, 6),
     }
+    if kernel is not None:
+        out["attention_event_window"] = out["attention"]
+        out["attention"] = float(np.median([kernel.ms(i) for i in range(len(events))]))
+    return out
 
 
 def host_link_gbs(torch, device, nbytes=1 << 30):
@@ -851,90 +860,227 @@ def pmc_traffic(kernels=ROOFLINE_KERNELS, path=PMC_SUMMARY):
     return total if kernels[0] in found else None
 
 
-def model_cpu_baseline(torch, engine, wl, budget_s):
-    """The reference CPU path, extrapolated: one (request, layer) sparse path with the numpy
-    oracle (Quest, union, resolver, the per-row host gather loop, attention over the
-    selected tokens) and one layer of dense math plus the LM head in torch on the host
-    cores; per step = layers x batch sparse paths + layers dense layers + LM head."""
-    import oracle
-    from oracle.quest import pages_to_positions
-
+def _sparse_inputs(torch, engine, wl, request=0, layer=0):
+    """One (request, layer) of the engine's state as host arrays: the reference CPU path's
+    inputs (query drawn at random; bounds, tables and the layer's host pool as they are)."""
     st = engine.state
-    cores = os.cpu_count() or 1
-    torch.set_num_threads(cores)
-    P, Hkv, D, L, B, C = wl.page_size, wl.kv_heads, wl.head_dim, wl.layers, wl.batch, st.pages
-    length = st.lengths[0]
+    P, Hkv, D, C = wl.page_size, wl.kv_heads, wl.head_dim, st.pages
+    length = st.lengths[request]
     count = ceil(length / P)
-    gen = torch.Generator().manual_seed(5)
-    q = torch.randn(wl.heads, D, generator=gen).to(wl.dtype)
-    lo, hi = st.minimum[0, 0, :count].cpu(), st.maximum[0, 0, :count].cpu()
-    t = st.tables[0][0]
-    tables = [x.cpu().numpy() for x in (t.source, t.resident, t.hot, t.tags, t.lru)]
-    host = st.host[0].view(B, C, 2, P, Hkv, D)[0]
-    t0 = time.perf_counter()
-    if wl.selector == "uniform":  # the tail page and top - 1 uniform others, for every head
-        rng = np.random.default_rng(5)
-        drawn = np.sort(np.append(rng.choice(count - 1, size=wl.top_pages - 1, replace=False), count - 1))
-        pages = np.repeat(drawn[None, :], wl.heads, axis=0)
-        selection = f"{wl.top_pages} uniform pages of {count}"
-    else:
-        pages = oracle.quest_pages(q, lo, hi, length, P, wl.top_pages)
-        selection = f"Quest over {count} pages"
-    positions = pages_to_positions(pages, length, P)
-    union, cols = oracle.from_selection(positions)
-    phys, mh, md, counts, _, _ = oracle.resolve_rows(union, *tables, length, P, head_columns=cols)
-    staging = np.empty((max(1, int(counts[2])), 2, Hkv, D), dtype=np.float32)
-    for i, hrow in enumerate(mh[: int(counts[2])].tolist()):  # the CPU gather loop, one row at a time
-        hb, ho = divmod(hrow - int(tables[0][0]) * P, P)
-        staging[i] = host[hb, :, ho].float().numpy()
-    kv = host[:count].float()
-    keys = kv[:, 0].reshape(count * P, Hkv, D)[:length]
-    vals = kv[:, 1].reshape(count * P, Hkv, D)[:length]
-    oracle.selection_oracle(q, keys, vals, positions)
-    sparse_s = time.perf_counter() - t0
-    layer = engine.model.model.layers[0]
-    weights = {n: p.detach().float().cpu() for n, p in layer.named_parameters()}
-    x = torch.randn(B, wl.hidden, generator=gen)
-    t0 = time.perf_counter()
-    for _ in range(2):
-        hq = torch.nn.functional.linear(x, weights["self_attn.q_proj.weight"], weights["self_attn.q_proj.bias"])
-        hk = torch.nn.functional.linear(x, weights["self_attn.k_proj.weight"], weights["self_attn.k_proj.bias"])
-        hv = torch.nn.functional.linear(x, weights["self_attn.v_proj.weight"], weights["self_attn.v_proj.bias"])
-        y = x + torch.nn.functional.linear(hq, weights["self_attn.o_proj.weight"])
-        g = torch.nn.functional.linear(y, weights["mlp.gate_proj.weight"])
-        u = torch.nn.functional.linear(y, weights["mlp.up_proj.weight"])
-        y = y + torch.nn.functional.linear(torch.nn.functional.silu(g) * u, weights["mlp.down_proj.weight"])
-    dense_s = (time.perf_counter() - t0) / 2
-    head = engine.model.lm_head.weight.detach()[: wl.vocab // 8].float().cpu()
-    t0 = time.perf_counter()
-    torch.nn.functional.linear(x, head)
-    head_s = (time.perf_counter() - t0) * 8
-    step_s = L * B * sparse_s + L * dense_s + head_s
+    gen = torch.Generator().manual_seed(5 + 97 * request + layer)
+    t = st.tables[layer][request]
+    i16 = lambda x: x.detach().cpu().contiguous().view(torch.int16).numpy()
+    host = st.host[layer].view(wl.batch, C, 2, P, Hkv, D)[request]
+    source = t.source.cpu().numpy().astype(np.int64)
+    source = source - int(source[0])  # this request's host pages, numbered from 0 in `host`
     return {
-        "value": B / step_s,
-        "unit": "tokens/s",
-        "cores": cores,
-        "kind": "port",
-        "sample": f"extrapolated: one (request, layer) sparse path (numpy oracle: {selection}, "
-        f"union, resolver, {int(counts[2])}-row host gather loop, attention; {sparse_s:.2f} s, 1 thread) "
-        f"x {L * B} + one dense layer for {B} tokens ({dense_s:.2f} s, torch fp32, {cores} threads) x {L} "
-        f"+ LM head ({head_s:.2f} s) = {step_s:.1f} s per step",
-        "host_cpus": cores,
+        "q": i16(torch.randn(wl.heads, D, generator=gen).to(wl.dtype)),
+        "lo": i16(st.minimum[layer, request, :count]), "hi": i16(st.maximum[layer, request, :count]),
+        "source": source, "resident": t.resident.cpu().numpy(),
+        "tags": (t.tags.cpu().numpy().astype(np.int64) - int(t.source[0].item()) * P).clip(min=-1),
+        "lru": t.lru.cpu().numpy().astype(np.int64), "host": i16(host),
+        "meta": np.array([length, P, wl.top_pages, Hkv, D, wl.heads, 1 if wl.selector == "uniform" else 0,
+                          t.hot.numel(), 5 + 97 * request + layer], dtype=np.int64),
     }
 
 
+def _sparse_path(x):
+    """The reference CPU path of one (request, layer) on host arrays (``_sparse_inputs``):
+    Quest (or the uniform draw), union, resolver, the per-row gather loop into a CPU hot
+    region, row attention over the selected rows.  Returns (seconds per stage, misses)."""
+    import torch
+
+    from oracle import cpu_path
+
+    bf = lambda a: torch.from_numpy(np.ascontiguousarray(a)).view(torch.bfloat16)
+    length, P, top, Hkv, D, heads, uniform, hot_blocks, seed = (int(v) for v in x["meta"])
+    q, lo, hi, host = bf(x["q"]), bf(x["lo"]), bf(x["hi"]), bf(x["host"])
+    hot_pool = torch.empty((hot_blocks, 2, P, Hkv, D), dtype=torch.bfloat16)
+    hot = np.arange(hot_blocks, dtype=np.int64)  # the layer's hot blocks, numbered in hot_pool
+    tags, lru = np.array(x["tags"]), np.array(x["lru"])
+    count = ceil(length / P)
+    t = [time.perf_counter()]
+    if uniform:  # the tail page and top - 1 uniform others, shared by every head
+        rng = np.random.default_rng(seed)
+        drawn = np.sort(np.append(rng.choice(count - 1, size=top - 1, replace=False), count - 1))
+        tokens = tuple(int(tok) for pg in drawn for tok in range(pg * P, min((pg + 1) * P, length)))
+        positions = [tokens] * heads
+    else:
+        positions = cpu_path.quest_select(q, lo, hi, length, P, top)
+    t.append(time.perf_counter())
+    union, cols = cpu_path.union_columns(positions)
+    t.append(time.perf_counter())
+    _, mh, md, counts = cpu_path.resolve(union, cols, x["source"], x["resident"], hot, tags, lru, length, P)
+    t.append(time.perf_counter())
+    misses = cpu_path.gather_loop(host, hot_pool, mh, md, P)
+    t.append(time.perf_counter())
+    # the K/V of every selected row, read where its values live in the host pool's layout
+    rows = torch.from_numpy(cpu_path.host_rows(positions, x["source"], P))
+    t.append(time.perf_counter())
+    cpu_path.row_attention(q, host, rows, P, Hkv, D)
+    t.append(time.perf_counter())
+    stages = {"select": t[1] - t[0], "union": t[2] - t[1], "resolve": t[3] - t[2], "gather_loop": t[4] - t[3],
+              "attention": t[6] - t[5]}
+    return stages, misses
+
+
+def _sparse_worker(job):
+    """A worker process of the all-cores leg: map the inputs, wait for the start, run."""
+    import torch
+
+    torch.set_num_threads(1)
+    d, start_at = job
+    x = {f[:-4]: np.load(os.path.join(d, f), mmap_mode="r") for f in os.listdir(d) if f.endswith(".npy")}
+    while time.time() < start_at:
+        time.sleep(0.001)
+    t0 = time.perf_counter()
+    stages, misses = _sparse_path(x)
+    return time.perf_counter() - t0, stages, misses
+
+
+def _dense_seconds(torch, engine, wl, threads):
+    """One dense layer for the batch's tokens plus the LM head, torch fp32 on the host cores
+    (q/k/v, o_proj and the SwiGLU MLP; norms and rotary are a few vector ops and left out)."""
+    torch.set_num_threads(threads)
+    gen = torch.Generator().manual_seed(6)
+    layer = engine.model.model.layers[0]
+    w = {n: p.detach().float().cpu() for n, p in layer.named_parameters()}
+    x = torch.randn(wl.batch, wl.hidden, generator=gen)
+    lin = torch.nn.functional.linear
+    t0 = time.perf_counter()
+    for _ in range(2):
+        hq = lin(x, w["self_attn.q_proj.weight"], w["self_attn.q_proj.bias"])
+        lin(x, w["self_attn.k_proj.weight"], w["self_attn.k_proj.bias"])
+        lin(x, w["self_attn.v_proj.weight"], w["self_attn.v_proj.bias"])
+        y = x + lin(hq, w["self_attn.o_proj.weight"])
+        g, u = lin(y, w["mlp.gate_proj.weight"]), lin(y, w["mlp.up_proj.weight"])
+        y = y + lin(torch.nn.functional.silu(g) * u, w["mlp.down_proj.weight"])
+    dense_s = (time.perf_counter() - t0) / 2
+    head = engine.model.lm_head.weight.detach()[: wl.vocab // 8].float().cpu()
+    t0 = time.perf_counter()
+    lin(x, head)
+    head_s = (time.perf_counter() - t0) * 8
+    return dense_s, head_s
+
+
+def model_cpu_baseline(torch, engine, wl, budget_s, max_workers=16):
+    """The reference CPU path (BASELINE.md's plan), extrapolated to one decode step of the
+    workload: per (request, layer) the sparse path of ``oracle.cpu_path`` -- the Quest
+    scorer as the reference's torch expression over every page and channel, the Python
+    union, the resolver, the per-row gather loop (hybrid.py:466-472) and row attention
+    over the selected rows (attention.py:26-35) -- and per layer one dense layer, plus the
+    LM head.  Two legs, each labelled with the threads it used:
+
+    * one thread: sparse paths of sampled (request, layer) pairs one after another,
+      dense math with ``torch.set_num_threads(1)`` (the reference CLI's setting);
+    * all cores: ``workers`` processes (the host's CPU share, at most ``max_workers``)
+      each run one sparse path at the same moment, so paths/s = workers / wall time;
+      dense math with that many torch threads.
+
+    Per step = layers x batch sparse paths + layers dense layers + LM head."""
+    import shutil
+    import tempfile
+    from concurrent.futures import ProcessPoolExecutor
+    from multiprocessing import get_context
+
+    L, B = wl.layers, wl.batch
+    workers = max(1, min(max_workers, os.cpu_count() or 1))
+    pairs = [(b, l) for l in (0, L // 2, L - 1) for b in (0, B - 1)]
+    # leg 1: one thread, sampled (request, layer) pairs within half the budget
+    torch.set_num_threads(1)
+    samples, stages_sum, misses_sum = [], {}, 0
+    t_leg = time.perf_counter()
+    for b, l in pairs:
+        x = _sparse_inputs(torch, engine, wl, b, l)
+        stages, misses = _sparse_path(x)
+        samples.append(sum(stages.values()))
+        misses_sum += misses
+        for k, v in stages.items():
+            stages_sum[k] = stages_sum.get(k, 0.0) + v
+        if time.perf_counter() - t_leg > budget_s / 2:
+            break
+    n = len(samples)
+    path_s = float(np.mean(samples))
+    dense_s, head_s = _dense_seconds(torch, engine, wl, 1)
+    step_1 = L * B * path_s + L * dense_s + head_s
+    stage_txt = ", ".join(f"{k} {v / n * 1e3:.0f} ms" for k, v in stages_sum.items())
+    single = {
+        "value": B / step_1, "unit": "tokens/s", "cores": 1, "kind": "port",
+        "sample": f"extrapolated from {n} (request, layer) sparse paths run one after another on 1 thread "
+                  f"(mean {path_s:.2f} s: {stage_txt}; {misses_sum / n:.0f} rows copied by the gather loop "
+                  f"per path) x {L * B} + one dense layer for {B} tokens ({dense_s:.2f} s, torch fp32, 1 thread) "
+                  f"x {L} + LM head ({head_s:.2f} s) = {step_1:.1f} s per step",
+    }
+    # leg 2: all cores, one sparse path per worker process at the same moment
+    d = tempfile.mkdtemp(prefix="hs_cpu_path_")
+    try:
+        for k, v in _sparse_inputs(torch, engine, wl, 0, 0).items():
+            np.save(os.path.join(d, k + ".npy"), v)
+        with ProcessPoolExecutor(workers, mp_context=get_context("spawn")) as pool:
+            list(pool.map(_cpu_worker_ready, range(workers)))
+            start_at = time.time() + 2.0
+            results = list(pool.map(_sparse_worker, [(d, start_at)] * workers))
+    finally:
+        shutil.rmtree(d, ignore_errors=True)
+    slowest = max(r[0] for r in results)
+    paths_per_s = workers / slowest
+    dense_all, head_all = _dense_seconds(torch, engine, wl, workers)
+    step_all = L * B / paths_per_s + L * dense_all + head_all
+    torch.set_num_threads(1)
+    return {
+        "value": B / step_all, "unit": "tokens/s", "cores": workers, "kind": "port",
+        "sample": f"extrapolated: {workers} worker processes (1 thread each) ran the sparse path of (request 0, "
+                  f"layer 0) at the same moment, the slowest in {slowest:.2f} s ({paths_per_s:.2f} paths/s: Quest "
+                  "scores as the reference's torch expression, Python union, resolver, per-row gather loop, row "
+                  f"attention over the selected rows) x {L * B} + one dense layer for {B} tokens ({dense_all:.2f} s, "
+                  f"torch fp32, {workers} threads) x {L} + LM head ({head_all:.2f} s) = {step_all:.1f} s per step",
+        "single_thread": single,
+        "host": platform.processor() or platform.machine(),
+        "host_cpus": os.cpu_count(),
+    }
+
+
+class KernelTimer:
+    """Durations of attention launches from their own kernel dispatches: before a launch,
+    ``arm(i)`` hands event pair i to ``hs_attend_time_next``, so the library launches the
+    attention kernel with ``hipExtLaunchKernel`` and the pair is stamped by the dispatch
+    itself (start of the attention kernel, end of the launch's last kernel).  That is the
+    duration a kernel trace reports, without the queueing and dispatch gaps that events
+    recorded on the stream include.  Events are created (by one record each) before the
+    timed region."""
+
+    def __init__(self, torch, launches):
+        from mini_hisparse_amd import _lib
+
+        self.lib = _lib.load()
+        self.start = [torch.cuda.Event(enable_timing=True) for _ in range(launches)]
+        self.stop = [torch.cuda.Event(enable_timing=True) for _ in range(launches)]
+        for ev in self.start + self.stop:
+            ev.record()  # creates the HIP event
+        torch.cuda.synchronize()
+
+    def arm(self, i):
+        self.lib.hs_attend_time_next(self.start[i], self.stop[i])
+
+    def ms(self, i):
+        return self.start[i].elapsed_time(self.stop[i])
+
+
 class AttendProbe:
-    """HIP events around every attention launch of the timed steps, on the compute stream
-    the launch runs on, and a device copy of each launch's entry counts (the rows each
-    (request, KV head) reads), from which the launch's algorithmic bytes follow.  Events
-    and the count buffer are allocated before the timed region.  ``fence``: the engine
-    hands the gather's rows over from another stream (see ``before_attend``)."""
+    """Timing of every attention launch of the timed steps: its kernels' own duration
+    (``KernelTimer``, the figure the roofline uses) and, as a secondary figure, HIP events
+    recorded on the compute stream around the launch; plus a device copy of each launch's
+    entry counts (the rows each (request, KV head) reads), from which the launch's
+    algorithmic bytes follow.  Events and the count buffer are allocated before the timed
+    region.  ``fence``: the engine hands the gather's rows over from another stream (see
+    ``before_attend``)."""
 
     def __init__(self, torch, device, launches, batch, kv_heads, fence=True):
         self.torch = torch
         self.fence = fence
         self.start = [torch.cuda.Event(enable_timing=True) for _ in range(launches)]
         self.end = [torch.cuda.Event(enable_timing=True) for _ in range(launches)]
+        self.kernel = KernelTimer(torch, launches)
         self.counts = torch.zeros((launches, batch * kv_heads), dtype=torch.int32, device=device)
         self.widths = []
         self.i = 0
@@ -948,6 +1094,7 @@ class AttendProbe:
         if self.fence:
             self.torch.cuda._sleep(1)
         self.start[self.i].record(stream)
+        self.kernel.arm(self.i)
 
     def after_attend(self, layer, stream, dec):
         self.end[self.i].record(stream)
@@ -957,13 +1104,14 @@ class AttendProbe:
         self.i += 1
 
     def totals(self, bytes_of):
-        """(total ms, total algorithmic bytes, launches); ``bytes_of(entries, width, batch)``
-        gives one launch's bytes."""
+        """(kernel ms, event-window ms, algorithmic bytes, launches), totals over the
+        launches; ``bytes_of(entries, width, batch)`` gives one launch's bytes."""
         n = self.i
-        ms = sum(self.start[i].elapsed_time(self.end[i]) for i in range(n))
+        kernel_ms = sum(self.kernel.ms(i) for i in range(n))
+        window_ms = sum(self.start[i].elapsed_time(self.end[i]) for i in range(n))
         entries = self.counts[:n].sum(1).tolist()
         nbytes = sum(bytes_of(e, w, b) for e, (w, b) in zip(entries, self.widths))
-        return ms, nbytes, n
+        return kernel_ms, window_ms, nbytes, n
 
 
 def run_model_workload(args, torch, device):
@@ -1058,16 +1206,18 @@ def run_model_workload(args, torch, device):
         # union-deduplicated K/V rows + the per-head row lists + queries and outputs
         return entries * 2 * D * e + 8 * Hq * width * batch + 2 * Hq * D * e * batch
 
-    att_ms, att_bytes, launches = probe.totals(launch_bytes)
+    att_ms, att_window_ms, att_bytes, launches = probe.totals(launch_bytes)
     att_gbs = att_bytes / (att_ms * 1e-3) / 1e9
     solo_line = None
     if in_order is not None:
-        solo_ms, solo_bytes, solo_n = in_order.totals(launch_bytes)
+        solo_ms, solo_window_ms, solo_bytes, solo_n = in_order.totals(launch_bytes)
         solo_gbs = solo_bytes / (solo_ms * 1e-3) / 1e9
         solo_line = {"achieved": solo_gbs, "frac": solo_gbs / HBM_PEAK_GBS, "launches": solo_n,
                      "bytes_per_launch": solo_bytes / solo_n, "us_per_launch": solo_ms * 1e3 / solo_n,
+                     "event_window_us_per_launch": solo_window_ms * 1e3 / solo_n,
                      "how": "two extra steps after the timed region with the whole batch in one group, "
-                            "in layer order (no gather running beside the attention)"}
+                            "in layer order (no gather running beside the attention); kernel duration "
+                            "from dispatch-stamped events"}
     pmc_path = PMC_SUMMARIES.get(args.workload, (None,))[0]
     profiled = PMC_CONFIG.get(args.workload)
     traffic = pmc_traffic(ROOFLINE_KERNELS, pmc_path) if pmc_path and profiled == (
@@ -1124,9 +1274,12 @@ def run_model_workload(args, torch, device):
             "traffic": traffic,
             "kernel": f"{ATTENTION_KERNELS} (hs_attend_groups), every layer of the timed steps"
             + (" (one launch per request group, beside the other group's gather)" if engine.groups else ""),
+            "timing": "each launch's own kernel duration: HIP events stamped by the dispatch "
+                      "(hipExtLaunchKernel via hs_attend_time_next), the figure a kernel trace reports",
             "launches": launches,
             "bytes_per_launch": att_bytes / launches,
             "us_per_launch": att_ms * 1e3 / launches,
+            "event_window_us_per_launch": att_window_ms * 1e3 / launches,
             "in_order": solo_line,
         },
         "stages_ms_per_step": stage_ms,
@@ -1216,7 +1369,7 @@ def run_microbench(args, torch, device):
     run_steps(torch, w, 2, record=False)
     events = run_steps(torch, w, args.steps, record=True)
     torch.cuda.synchronize()
-    stages = stage_ms(events)
+    stages = stage_ms(events, w["attention_kernel"])
     sequential_ms = float(np.mean([e[0].elapsed_time(e[6]) for e in events]))
     diff = (w["pipe_out"].float() - w["out"].float()).abs().max().item()
     bytes_ = algorithmic_bytes(w, torch)
@@ -1243,7 +1396,10 @@ def run_microbench(args, torch, device):
 
     kernels = {
         "attention": hbm_line("attention", bytes_["attention"], ROOFLINE_KERNELS,
-                              per_head_bytes=bytes_["attention_per_head"]),
+                              per_head_bytes=bytes_["attention_per_head"],
+                              timing="the launch's own kernel duration (dispatch-stamped HIP events, "
+                                     "hs_attend_time_next); median over the recorded steps",
+                              event_window_ms=stages["attention_event_window"]),
         "quest_and_union": hbm_line("quest_and_union", bytes_["quest"],
                                     ("quest_score", "quest_topk_kernel", "build_union_kernel")),
         "resolve": hbm_line("resolve", bytes_["resolver"], ("resolve_front_kernel", "resolve_outputs_kernel")),

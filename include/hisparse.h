@@ -196,6 +196,9 @@ int hs_resolve_rows_batched(const hs_resolve_desc* descs, int32_t count, void* w
  * shape at 128k tokens) is rejected with HS_EINVAL.  Nothing is allocated and
  * the outputs are those of hs_resolve_rows_batched.  Calls that overlap on one
  * GPU (other streams or threads) share the array and race: serialise them.
+ * The first call on a device looks the array's address up (hipGetSymbolAddress),
+ * so a caller that captures the call into a HIP graph makes one uncaptured call
+ * on that device first; captured replays then run the same kernels.
  */
 int64_t hs_resolve_noalloc_max_bytes(void);
 int hs_resolve_rows_noalloc(const hs_resolve_desc* descs, int32_t count, hs_stream_t stream);
@@ -363,6 +366,19 @@ int hs_attend_window(const void* query, int64_t q_stride_h, const void* pool, in
  */
 int hs_probe_row_reads(const void* base, int64_t region_bytes, const int64_t* offsets, int64_t n,
                        int64_t segment_bytes, int64_t plane_bytes, void* sink, hs_stream_t stream);
+
+/*
+ * Diagnostic (no reference counterpart): time the next attention launch of the
+ * calling host thread (hs_attend_rows, hs_attend_groups or hs_attend_window)
+ * with two HIP events taken from the kernel dispatches themselves
+ * (hipExtLaunchKernel): `start` is stamped when the attention kernel begins and
+ * `stop` when the launch's last kernel (the attention, or its merge kernel)
+ * ends, so their elapsed time is the kernels' own duration, without the
+ * queueing and dispatch gaps that events recorded on the stream include.  Both
+ * are events created with timing enabled (hipEvent_t); either may be null.
+ * The pair is used by one launch only.
+ */
+int hs_attend_time_next(void* start_event, void* stop_event);
 
 /*
  * Dense-layer helpers of the batched decode engine.  They replace the

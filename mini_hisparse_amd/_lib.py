@@ -111,6 +111,7 @@ SIGNATURES = {
     "hs_probe_row_reads": (
         c_int, [c_void_p, c_int64, c_void_p, c_int64, c_int64, c_int64, c_void_p, c_void_p],
     ),
+    "hs_attend_time_next": (c_int, [c_void_p, c_void_p]),
     "hs_add_rms_norm": (
         c_int,
         [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int64, c_float,
@@ -151,26 +152,32 @@ SIGNATURES = {
 }
 
 _LIB = None
+_LIB_PATH = None
 
 
 def load(path: Path | str | None = None):
-    """Load (once) and return the library; raises if it is absent."""
-    global _LIB
-    if _LIB is not None and path is None:
+    """Load (once per process) and return the library; raises if it is absent.
+
+    ``path`` names another build of the library; the process holds one copy at most,
+    so a path other than the one already loaded is refused (two copies would register
+    the same kernels twice with the HIP runtime)."""
+    global _LIB, _LIB_PATH
+    target = (Path(path) if path is not None else LIBRARY_PATH).resolve()
+    if _LIB is not None and target == _LIB_PATH:
         return _LIB
-    target = Path(path) if path is not None else LIBRARY_PATH
     if not target.exists():
         raise HipLibraryError(
             f"{target} is missing: build it with `python -m mini_hisparse_amd.build` "
             "(the HIP kernels have no fallback)"
         )
+    if _LIB is not None:
+        raise HipLibraryError(f"{_LIB_PATH} is already loaded; a second copy ({target}) is refused")
     lib = ctypes.CDLL(str(target))
     for name, (restype, argtypes) in SIGNATURES.items():
         fn = getattr(lib, name)
         fn.restype = restype
         fn.argtypes = argtypes
-    if path is None:
-        _LIB = lib
+    _LIB, _LIB_PATH = lib, target
     return lib
 
 

@@ -23,7 +23,7 @@
 // bf16 / fp16 pools use MFMA (v_mfma_f32_16x16x32_{bf16,f16}): S^T = K Q^T
 // with the group's query heads as the N dimension (padded to 16), then
 // O^T += V^T P^T with V staged through LDS.  fp32 pools (and head dims other
-// than 32, 64, 128 and 256) use a VALU kernel with the same entry sources.  Both write
+// than 32, 64 and 128) use a VALU kernel with the same entry sources.  Both write
 // split-K partials (m, l, acc).  The MFMA kernel combines them itself: the
 // workgroup that finishes a (request, KV head, head chunk) last -- found with an
 // arrival counter per group -- merges the group's partials and writes the
@@ -32,10 +32,13 @@
 // `attend_merge_kernel`; both merges run the same arithmetic.
 #include <float.h>
 #include <stdlib.h>
+#include <string.h>
 #include <math.h>
 
 #include <atomic>
 #include <chrono>
+
+#include <hip/hip_ext.h>
 
 #include "hs_common.h"
 
@@ -72,6 +75,8 @@ struct AttendArgs {
   unsigned long long* arrivals;
   unsigned long long epoch;
   int fuse;
+  int relaxed_merge;  // arrivals without release/acquire (measurement only)
+  int contiguous;     // group splits as contiguous chunks, not dealt by tile (measurement only)
   void* out;
   int64_t o_sb, o_sh;
   const int32_t* wslots;       // WINDOW: device slot of each page [wn]
@@ -226,7 +231,26 @@ __device__ __forceinline__ void merge_partials(const float* part_m, const float*
 // counter, so a launch replayed with the same epoch (a captured graph) starts
 // from zero too.  A failed swap means another workgroup changed the counter, so
 // the loop ends after at most one installation and the reads that follow it.
+// Both read-modify-writes are agent-scope releases: every partial this workgroup
+// stored before the arrival (ordered before it by the workgroup barrier) is
+// visible to the workgroup that arrives last, which acquires (merge_group).
 __device__ __forceinline__ bool arrive_last(unsigned long long* counter, unsigned long long epoch, int64_t total) {
+  unsigned long long old = __hip_atomic_load(counter, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  while (true) {
+    if ((old >> 16) == epoch) {
+      const unsigned long long prev = __hip_atomic_fetch_add(counter, 1ull, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+      return static_cast<int64_t>((prev & 0xffffull) + 1) == total;
+    }
+    unsigned long long expected = old;
+    if (__hip_atomic_compare_exchange_strong(counter, &expected, (epoch << 16) | 1ull, __ATOMIC_RELEASE,
+                                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
+      return total == 1;
+    old = expected;
+  }
+}
+// Relaxed arrival, for measuring what the release costs (HS_ATTEND_MERGE_ORDER=relaxed).
+__device__ __forceinline__ bool arrive_last_relaxed(unsigned long long* counter, unsigned long long epoch,
+                                                    int64_t total) {
   unsigned long long old = __hip_atomic_load(counter, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   while (true) {
     if ((old >> 16) == epoch) {
@@ -239,19 +263,43 @@ __device__ __forceinline__ bool arrive_last(unsigned long long* counter, unsigne
   }
 }
 
-// One workgroup (8 waves; 4 for head_dim 256) per (split, KV head x head chunk,
-// request), or per slot of the balanced schedule below.  The split's entries
+// One workgroup (8 waves) per (split, KV head x head chunk, request), or per slot
+// of the balanced schedule below.  The split's entries
 // (K element offset, head mask) are staged in LDS once with two batched rounds
 // of loads (entry columns with the group's count and the query, then physical
 // rows); each wave then walks tiles w, w+8, ... of 32 entries with two register
 // buffers used in turn: the loads of tile t+8 are in flight while tile t
 // computes, and no buffer is copied (a copy would make the compiler wait for
 // the loads).
+//
+// Group entry lists (split schedule) are dealt to the splits a tile of 32 entries
+// at a time: split s takes the group's tiles s, s + splits, s + 2 splits, ...  The
+// splits of a group therefore differ by at most one tile whatever the group's
+// entry count, with no extra round of loads: a split's entry indices do not depend
+// on the count, so its entry columns load together with the count.  (Contiguous
+// chunks sized for the capacity left the last split of a typical group nearly
+// empty: three of four splits full at the benched shapes.)
+constexpr int ATILE = 32;  // entries per tile
+
+// Entries of split s among `splits` when a group's E entries are dealt a tile at a
+// time: the splits' tiles are s, s + splits, ..., and only the group's last tile
+// may be partial.
+__host__ __device__ __forceinline__ int64_t dealt_count(int64_t E, int64_t s, int64_t splits) {
+  const int64_t tiles = (E + ATILE - 1) / ATILE;
+  if (tiles <= s) return 0;
+  const int64_t mine = (tiles - s + splits - 1) / splits;
+  const int64_t short_by = ((tiles - 1) % splits == s) ? tiles * ATILE - E : 0;
+  return mine * ATILE - short_by;
+}
+
+// Group entry index of local entry i of split s (tile-dealt).
+__host__ __device__ __forceinline__ int64_t dealt_entry(int64_t i, int64_t s, int64_t splits) {
+  return ATILE * (s + splits * (i / ATILE)) + i % ATILE;
+}
 constexpr int ACH = 2048;        // entries per workgroup (chunk) of the MFMA kernel
 
-// Waves per workgroup of the MFMA kernel: 8 (4 for head_dim 256, whose V tiles
-// and wave-merge buffer would not fit in LDS).
-__host__ __device__ constexpr int attend_waves(int DP) { return DP <= 128 ? 8 : 4; }
+// Waves per workgroup of the MFMA kernel.
+__host__ __device__ constexpr int attend_waves(int DP) { return 8; }
 
 // Physical row and head mask of entries e0 + i, i = threadIdx.x + s * NTH < cnt
 // (rows outside the pool are masked); every load is issued before any use.
@@ -511,21 +559,29 @@ __global__ __launch_bounds__(64 * attend_waves(DP)) void attend_mfma_kernel(Atte
   uint32_t mk[SPT];
   if constexpr (MODE == MODE_GROUPS && !SCHED) {
     // The split's entry columns and masks are loaded together with the group's
-    // entry count (one round of loads instead of two): every split starts below
-    // emax, so entries e0 .. e0 + min(chunk, emax - e0) - 1 are in bounds.
+    // entry count (one round of loads instead of two): the split's entries are
+    // dealt a tile at a time, so their indices do not depend on the count; an
+    // index at or past emax loads entry 0 instead (in bounds, masked below).
     int32_t col[SPT];
-    const int64_t lim = a.emax - e0 < a.chunk ? a.emax - e0 : a.chunk;
-    const int64_t base = b * a.e_sb + k * a.e_sk + e0;
+    const int64_t base = b * a.e_sb + k * a.e_sk;
 #pragma unroll
     for (int s = 0; s < SPT; ++s) {
       const int i = threadIdx.x + s * NTH;
-      const int64_t ic = i < lim ? i : 0;
+      const int64_t e = a.contiguous ? e0 + i : dealt_entry(i, split, a.splits);
+      const int64_t ic = e < a.emax ? e : 0;
       col[s] = a.ecol[base + ic];
       mk[s] = a.emask[base + ic];
     }
     const int64_t E = entry_total<MODE>(a, b, k);
-    cnt = E > e0 ? static_cast<int>(E - e0 < a.chunk ? E - e0 : a.chunk) : 0;
-    parts = E > 0 ? (E + a.chunk - 1) / a.chunk : 1;
+    if (a.contiguous) {
+      cnt = E > e0 ? static_cast<int>(E - e0 < a.chunk ? E - e0 : a.chunk) : 0;
+      parts = E > 0 ? (E + a.chunk - 1) / a.chunk : 1;
+    } else {
+      cnt = static_cast<int>(dealt_count(E, split, a.splits));
+      // splits that hold entries: the first min(splits, tiles) (one when the list is empty)
+      const int64_t tiles = (E + ATILE - 1) / ATILE;
+      parts = E > 0 ? (tiles < a.splits ? tiles : a.splits) : 1;
+    }
     // no branch on cnt here: a conditional block would let the compiler sink the
     // column loads below the wait for the count
 #pragma unroll
@@ -774,8 +830,18 @@ __global__ __launch_bounds__(64 * attend_waves(DP)) void attend_mfma_kernel(Atte
   // workgroup reads them after its arrival with device-scope loads.
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  if (threadIdx.x == 0)
-    s_last = arrive_last(a.arrivals + (b * Hkv + k) * a.head_chunks + hchunk, a.epoch, parts) ? 1 : 0;
+  if (threadIdx.x == 0) {
+    unsigned long long* counter = a.arrivals + (b * Hkv + k) * a.head_chunks + hchunk;
+    if (a.relaxed_merge) {
+      s_last = arrive_last_relaxed(counter, a.epoch, parts) ? 1 : 0;
+    } else {
+      const bool last = arrive_last(counter, a.epoch, parts);
+      // the last arrival acquires every other workgroup's release before the merge
+      // reads their partials (the barrier below orders the other waves after it)
+      if (last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+      s_last = last ? 1 : 0;
+    }
+  }
   __syncthreads();
   if (!s_last) return;
   for (int idx = threadIdx.x; idx < 16 * DP; idx += NTH) {
@@ -949,10 +1015,12 @@ struct Plan {
   int64_t grid;  // its workgroups (slots)
 };
 
-// The MFMA kernel takes 16-bit pools with a head dim of exactly 32, 64, 128 or 256
-// (its tiles cover whole rows, with no per-lane bound); others run on the VALU kernel.
+// The MFMA kernel takes 16-bit pools with a head dim of exactly 32, 64 or 128 (its
+// tiles cover whole rows, with no per-lane bound); others run on the VALU kernel.
+// (A head dim of 256 would need more than 256 VGPRs for the two tile buffers, the
+// query fragments and the accumulators, and the build rejects kernels that spill.)
 static bool mfma_shape(int dtype, int64_t D) {
-  return dtype != HS_DTYPE_F32 && (D == 32 || D == 64 || D == 128 || D == 256);
+  return dtype != HS_DTYPE_F32 && (D == 32 || D == 64 || D == 128);
 }
 
 static Plan plan_attend(int dtype, int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int64_t max_entries) {
@@ -1032,26 +1100,38 @@ static unsigned long long next_epoch() {
   return e;
 }
 
+// Events of the next attention launch of this host thread (hs_attend_time_next).
+struct LaunchEvents {
+  hipEvent_t start = nullptr, stop = nullptr;
+};
+static thread_local LaunchEvents next_events;
+
+// Launch `kernel`, stamping `ev` from the dispatch itself when either event is set.
+template <typename K, typename... Args>
+static void launch_timed(K kernel, dim3 grid, dim3 block, hipStream_t s, const LaunchEvents& ev, Args... args) {
+  if (ev.start || ev.stop) hipExtLaunchKernelGGL(kernel, grid, block, 0, s, ev.start, ev.stop, 0, args...);
+  else hipLaunchKernelGGL(kernel, grid, block, 0, s, args...);
+}
+
 template <int DT, int MODE, bool SCHED>
-static void launch_mfma_mode(const Plan& p, const AttendArgs& a, hipStream_t s) {
+static void launch_mfma_mode(const Plan& p, const AttendArgs& a, hipStream_t s, const LaunchEvents& ev) {
   dim3 grid(static_cast<unsigned>(p.splits), static_cast<unsigned>(a.Hkv * p.head_chunks),
             static_cast<unsigned>(a.B));
   if (SCHED) grid = dim3(static_cast<unsigned>(p.grid));
   switch (p.dp) {
-    case 32: hipLaunchKernelGGL((attend_mfma_kernel<DT, 32, MODE, SCHED>), grid, dim3(64 * attend_waves(32)), 0, s, a); break;
-    case 64: hipLaunchKernelGGL((attend_mfma_kernel<DT, 64, MODE, SCHED>), grid, dim3(64 * attend_waves(64)), 0, s, a); break;
-    case 128: hipLaunchKernelGGL((attend_mfma_kernel<DT, 128, MODE, SCHED>), grid, dim3(64 * attend_waves(128)), 0, s, a); break;
-    default: hipLaunchKernelGGL((attend_mfma_kernel<DT, 256, MODE, SCHED>), grid, dim3(64 * attend_waves(256)), 0, s, a); break;
+    case 32: launch_timed(attend_mfma_kernel<DT, 32, MODE, SCHED>, grid, dim3(64 * attend_waves(32)), s, ev, a); break;
+    case 64: launch_timed(attend_mfma_kernel<DT, 64, MODE, SCHED>, grid, dim3(64 * attend_waves(64)), s, ev, a); break;
+    default: launch_timed(attend_mfma_kernel<DT, 128, MODE, SCHED>, grid, dim3(64 * attend_waves(128)), s, ev, a); break;
   }
 }
 
 template <int DT>
-static void launch_mfma(const Plan& p, const AttendArgs& a, hipStream_t s) {
-  if (a.mode == MODE_GROUPS && a.sched) launch_mfma_mode<DT, MODE_GROUPS, true>(p, a, s);
-  else if (a.mode == MODE_GROUPS) launch_mfma_mode<DT, MODE_GROUPS, false>(p, a, s);
-  else if (a.mode == MODE_SHARED) launch_mfma_mode<DT, MODE_SHARED, false>(p, a, s);
-  else if (a.mode == MODE_WINDOW) launch_mfma_mode<DT, MODE_WINDOW, false>(p, a, s);
-  else launch_mfma_mode<DT, MODE_ROWS, false>(p, a, s);
+static void launch_mfma(const Plan& p, const AttendArgs& a, hipStream_t s, const LaunchEvents& ev) {
+  if (a.mode == MODE_GROUPS && a.sched) launch_mfma_mode<DT, MODE_GROUPS, true>(p, a, s, ev);
+  else if (a.mode == MODE_GROUPS) launch_mfma_mode<DT, MODE_GROUPS, false>(p, a, s, ev);
+  else if (a.mode == MODE_SHARED) launch_mfma_mode<DT, MODE_SHARED, false>(p, a, s, ev);
+  else if (a.mode == MODE_WINDOW) launch_mfma_mode<DT, MODE_WINDOW, false>(p, a, s, ev);
+  else launch_mfma_mode<DT, MODE_ROWS, false>(p, a, s, ev);
 }
 
 // out (o_sb, o_sh) receives the normalised output in the pool dtype; when st_m is
@@ -1059,6 +1139,8 @@ static void launch_mfma(const Plan& p, const AttendArgs& a, hipStream_t s) {
 static int run_attend(int dtype, AttendArgs a, int64_t max_entries, void* out, int64_t o_sb,
                       int64_t o_sh, void* ws, int64_t ws_bytes, hipStream_t stream,
                       float* st_m = nullptr, float* st_l = nullptr, float* st_o = nullptr) {
+  const LaunchEvents ev = next_events;  // this launch's, also when it is rejected
+  next_events = LaunchEvents{};
   Plan p = plan_attend(dtype, a.B, a.Hq, a.Hkv, a.D, max_entries);
   // The split schedule is the default: its first loads (entry count, columns,
   // query) go out in one round, which the balanced schedule cannot do (it needs
@@ -1093,35 +1175,45 @@ static int run_attend(int dtype, AttendArgs a, int64_t max_entries, void* out, i
   HS_CHECK_ARG(!a.fuse || ceil_div(max_entries, 128) <= 0xffff, "too many entries per attention group");
   a.arrivals = reinterpret_cast<unsigned long long*>(static_cast<char*>(ws) + w.arrivals);
   a.epoch = next_epoch();
+  const char* order_env = getenv("HS_ATTEND_MERGE_ORDER");
+  a.relaxed_merge = order_env && strcmp(order_env, "relaxed") == 0 ? 1 : 0;
+  const char* deal_env = getenv("HS_ATTEND_DEAL");
+  a.contiguous = deal_env && atoi(deal_env) == 0 ? 1 : 0;
   a.out = out;
   a.o_sb = o_sb;
   a.o_sh = o_sh;
+  // the timing events of hs_attend_time_next: start on the attention kernel, stop on
+  // the launch's last kernel
+  const LaunchEvents first{ev.start, a.fuse ? ev.stop : nullptr};
+  const LaunchEvents last{nullptr, ev.stop};
   if (p.mfma) {
-    if (dtype == HS_DTYPE_BF16) launch_mfma<HS_DTYPE_BF16>(p, a, stream);
-    else launch_mfma<HS_DTYPE_F16>(p, a, stream);
+    if (dtype == HS_DTYPE_BF16) launch_mfma<HS_DTYPE_BF16>(p, a, stream, first);
+    else launch_mfma<HS_DTYPE_F16>(p, a, stream, first);
   } else {
     dim3 grid(static_cast<unsigned>(p.splits), static_cast<unsigned>(a.Hq), static_cast<unsigned>(a.B));
-    if (dtype == HS_DTYPE_F32) hipLaunchKernelGGL((attend_valu_kernel<HS_DTYPE_F32>), grid, dim3(64), 0, stream, a);
-    else if (dtype == HS_DTYPE_BF16) hipLaunchKernelGGL((attend_valu_kernel<HS_DTYPE_BF16>), grid, dim3(64), 0, stream, a);
-    else hipLaunchKernelGGL((attend_valu_kernel<HS_DTYPE_F16>), grid, dim3(64), 0, stream, a);
+    if (dtype == HS_DTYPE_F32) launch_timed(attend_valu_kernel<HS_DTYPE_F32>, grid, dim3(64), stream, first, a);
+    else if (dtype == HS_DTYPE_BF16) launch_timed(attend_valu_kernel<HS_DTYPE_BF16>, grid, dim3(64), stream, first, a);
+    else launch_timed(attend_valu_kernel<HS_DTYPE_F16>, grid, dim3(64), stream, first, a);
   }
   HS_CHECK_LAUNCH("attention");
   if (a.fuse) return HS_OK;
   dim3 mgrid(static_cast<unsigned>(a.Hq), static_cast<unsigned>(a.B));
   const unsigned mthreads = a.D <= 64 ? 64 : (a.D <= 128 ? 128 : 256);
   const int64_t hcs = a.head_chunks;
+  const float* pm = a.part_m;
+  const float* pl = a.part_l;
+  const float* po = a.part_o;
+  const int32_t* table = a.sched;
+  const int64_t splits = p.splits, Hkv = a.Hkv, g = a.g, Hq = a.Hq, D = a.D;
   if (dtype == HS_DTYPE_F32)
-    hipLaunchKernelGGL((attend_merge_kernel<HS_DTYPE_F32>), mgrid, dim3(mthreads), 0, stream, a.part_m, a.part_l,
-                       a.part_o, p.splits, a.sched, a.Hkv, a.g, hcs, a.Hq, a.D, out, o_sb, o_sh,
-                       st_m, st_l, st_o);
+    launch_timed(attend_merge_kernel<HS_DTYPE_F32>, mgrid, dim3(mthreads), stream, last, pm, pl, po, splits, table,
+                 Hkv, g, hcs, Hq, D, out, o_sb, o_sh, st_m, st_l, st_o);
   else if (dtype == HS_DTYPE_BF16)
-    hipLaunchKernelGGL((attend_merge_kernel<HS_DTYPE_BF16>), mgrid, dim3(mthreads), 0, stream, a.part_m, a.part_l,
-                       a.part_o, p.splits, a.sched, a.Hkv, a.g, hcs, a.Hq, a.D, out, o_sb, o_sh,
-                       st_m, st_l, st_o);
+    launch_timed(attend_merge_kernel<HS_DTYPE_BF16>, mgrid, dim3(mthreads), stream, last, pm, pl, po, splits, table,
+                 Hkv, g, hcs, Hq, D, out, o_sb, o_sh, st_m, st_l, st_o);
   else
-    hipLaunchKernelGGL((attend_merge_kernel<HS_DTYPE_F16>), mgrid, dim3(mthreads), 0, stream, a.part_m, a.part_l,
-                       a.part_o, p.splits, a.sched, a.Hkv, a.g, hcs, a.Hq, a.D, out, o_sb, o_sh,
-                       st_m, st_l, st_o);
+    launch_timed(attend_merge_kernel<HS_DTYPE_F16>, mgrid, dim3(mthreads), stream, last, pm, pl, po, splits, table,
+                 Hkv, g, hcs, Hq, D, out, o_sb, o_sh, st_m, st_l, st_o);
   HS_CHECK_LAUNCH("attention merge");
   return HS_OK;
 }
@@ -1251,6 +1343,12 @@ extern "C" int hs_attend_window(const void* query, int64_t q_stride_h, const voi
   a.mode = MODE_WINDOW;
   return run_attend(dtype, a, n_pages * page_size, nullptr, 0, 0, workspace, workspace_bytes, stream, out_m,
                     out_l, out_acc);
+}
+
+extern "C" int hs_attend_time_next(void* start_event, void* stop_event) {
+  next_events.start = static_cast<hipEvent_t>(start_event);
+  next_events.stop = static_cast<hipEvent_t>(stop_event);
+  return HS_OK;
 }
 
 extern "C" int hs_probe_row_reads(const void* base, int64_t region_bytes, const int64_t* offsets, int64_t n,

@@ -907,8 +907,9 @@ static void launch_front(bool pow2, bool l16, unsigned nb, size_t lds, hipStream
 }
 
 static int resolve_launch(const hs_resolve_desc* descs, int32_t count, char* workspace, hipStream_t stream) {
-  static bool attr_set = false;
-  if (!attr_set) {
+  // once per process, from whichever host thread launches first (the others wait)
+  static std::once_flag attr_once;
+  std::call_once(attr_once, [] {
     for (const void* f : {reinterpret_cast<const void*>(resolve_front_kernel<true, false, 16>),
                           reinterpret_cast<const void*>(resolve_front_kernel<false, false, 16>),
                           reinterpret_cast<const void*>(resolve_front_kernel<true, true, 16>),
@@ -919,8 +920,7 @@ static int resolve_launch(const hs_resolve_desc* descs, int32_t count, char* wor
                           reinterpret_cast<const void*>(resolve_front_kernel<false, true, 32>)})
       (void)hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kMaxResolverLds));
     (void)hipGetLastError();
-    attr_set = true;
-  }
+  });
   char* ws = workspace;
   for (int32_t start = 0; start < count; start += RMAXB) {
     ResolveBatch batch{};
@@ -964,7 +964,10 @@ extern "C" int hs_resolve_rows(const hs_resolve_desc* desc, void* workspace, int
 // launch resets the duplicate bits and, when it builds one, the host-block hash;
 // every other part is written before it is read), so
 // nothing is left over from an earlier call; calls that overlap on one GPU
-// (two streams, or two host threads) share the array and race.
+// (two streams, or two host threads) share the array and race.  The first call
+// on a device looks up the array's address (and the first resolver call of the
+// process sets the front kernels' LDS limit), so a caller that captures the
+// call into a graph makes one uncaptured call on that device first.
 namespace hs {
 constexpr int64_t kNoAllocScratchBytes = static_cast<int64_t>(32) << 20;
 constexpr int kMaxDevices = 64;

@@ -403,7 +403,6 @@ class HybridKVCache:
                 elif residents >= self.hot_config.resident_window_pages:
                     self._require_hot(group, "window")
             if tables.hot_required and not tables.blocks and not tables.busy:
-                # a failed attempt keeps residents and demand; the next tick retries
                 with suppress(CapacityError):
                     self.transition_to_host(*group)
             self._unpin_clean_pages(group)
@@ -427,8 +426,6 @@ class HybridKVCache:
         short = max(0, self.hot_blocks - len(supply))
         if len(victims) < short:
             raise CapacityError("cannot acquire complete hot region while blocks are leased")
-        # every check precedes every change; fences order copies and last readers even
-        # when a just-released history block becomes a hot block right away
         for index in victims[:short]:
             block = int(lp.slot[index])
             supply.append(block)
@@ -471,8 +468,6 @@ class HybridKVCache:
                        if not self._clean(g, i) and self._lp(g).host_ready[i] is not None]
             if not waiting:
                 raise CapacityError("no reclaimable resident block; tails/readers are protected")
-            # a synchronous runner cannot suspend mid-prefill: wait for one useful
-            # mirror event, never for the whole device
             group, index = waiting[0]
             self._lp(group).host_ready[index].synchronize()
             self.storage.stats["pressure_mirror_waits"] += 1
@@ -532,8 +527,6 @@ class HybridKVCache:
         length = storage.requests[request_id].lengths[layer]
         if length < 1:
             raise ValueError("cannot resolve an empty history")
-        # pin every resident page of this layer: the selected rows never come back to
-        # the host, so any of them may be read
         lp = self._lp(group)
         pinned = lp.resident()
         lp.pins[pinned] += 1
@@ -546,11 +539,10 @@ class HybridKVCache:
             resolved = storage.event(storage.compute)
             storage.wait(storage.transfer, resolved)
             storage.wait(storage.transfer, tables.last_use)
-            # append mirrors and earlier loads already precede this in stream order
             with storage.context(storage.transfer):
                 self.ops.gather_rows(storage.host_source, self.pool, plan, self.config)
             tables.ready = storage.event(storage.transfer)
-            if storage.cuda:  # plan tensors are produced on compute, read on transfer
+            if storage.cuda:
                 for tensor in (plan.miss_host_rows, plan.miss_device_rows, plan.counts):
                     tensor.record_stream(storage.transfer)
             return RowLease(self, group, tables, plan, pinned)
@@ -603,7 +595,6 @@ class HybridKVCache:
             raise CapacityError("hybrid block budget is fixed; hot leases need readmission to resize")
 
     def close(self):
-        # kernels read the pinned host pool; drain before teardown only
         self.storage.synchronize()
 
     def __del__(self):

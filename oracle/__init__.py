@@ -22,9 +22,10 @@ checkout):
                    ``dense_attention`` (``selection.py:158-163``),
                    ``selection_oracle`` (``selection.py:104-126``) and the
                    paged layout's window state (``reference/kernels.py:12-68``)
-* ``ops``       -- a CPU kernel backend with the same call signatures as the
-                   product's HIP backend, used by CPU tests of the host
-                   control plane (and by nothing else).
+* ``cpu_path``  -- the reference's CPU decode path of one (request, layer) as
+                   torch CPU ops (Quest, union, resolver, per-row gather loop,
+                   row attention): what ``bench.py``'s ``cpu_baseline`` leg
+                   times, not a checker.
 
 Pinning (what each function is checked against, besides the GPU):
 

@@ -59,3 +59,36 @@ def test_all_cores_cpu_baseline_matches_sequential_oracle():
     result = bench.cpu_baseline_all_cores(torch, w, max_workers=2)
     assert result["cores"] == 2 and result["value"] > 0
     assert result["sample"].endswith("True")
+
+
+def test_reference_cpu_path_of_one_request_layer():
+    """The model workloads' CPU leg (oracle.cpu_path via bench._sparse_path): its Quest
+    selection equals the numpy oracle's, its gather loop copies exactly the planned misses,
+    and its row attention over the selected rows equals the float64 oracle's."""
+    from oracle import cpu_path
+
+    C, P, Hkv, g, D, top, hot_rows = 64, 16, 2, 4, 32, 8, 512
+    L = C * P - 3
+    gen = torch.Generator().manual_seed(3)
+    host = torch.randn(C, 2, P, Hkv, D, generator=gen).to(torch.bfloat16)
+    host[-1, :, L - (C - 1) * P:] = 0
+    lo, hi = host[:, 0].amin(1), host[:, 0].amax(1)
+    lo[-1], hi[-1] = host[-1, 0, : L - (C - 1) * P].amin(0), host[-1, 0, : L - (C - 1) * P].amax(0)
+    q = torch.randn(Hkv * g, D, generator=gen).to(torch.bfloat16)
+    positions = cpu_path.quest_select(q, lo, hi, L, P, top)
+    assert list(positions) == list(pages_to_positions(oracle.quest_pages(q, lo, hi, L, P, top), L, P))
+    resident = np.full(C, -1, np.int32)
+    resident[::3] = np.arange(len(resident[::3]))
+    i16 = lambda t: t.contiguous().view(torch.int16).numpy()
+    x = {"q": i16(q), "lo": i16(lo), "hi": i16(hi), "source": np.arange(C, dtype=np.int64), "resident": resident,
+         "tags": np.full(hot_rows, -1, np.int64), "lru": np.arange(hot_rows, dtype=np.int64), "host": i16(host),
+         "meta": np.array([L, P, top, Hkv, D, Hkv * g, 0, hot_rows // P, 1], dtype=np.int64)}
+    stages, misses = bench._sparse_path(x)
+    assert set(stages) == {"select", "union", "resolve", "gather_loop", "attention"}
+    union, _ = oracle.from_selection(positions)
+    expected_misses = int((resident[union // P] < 0).sum())
+    assert misses == expected_misses > 0
+    rows = cpu_path.host_rows(positions, x["source"], P)
+    out = cpu_path.row_attention(q, host, torch.from_numpy(rows), P, Hkv, D).double().numpy()
+    ref = oracle.row_attention_rows(q, host, rows, P)
+    np.testing.assert_allclose(out, ref, atol=2e-2, rtol=1e-2)

@@ -128,6 +128,17 @@ def test_missing_library_fails_loudly(tmp_path):
         _lib.load(tmp_path / "libhisparse_hip.so")
 
 
+def test_a_second_copy_of_the_library_is_refused(tmp_path):
+    import shutil
+
+    _lib.load()
+    copy = tmp_path / "libhisparse_hip.so"
+    shutil.copy(_lib.LIBRARY_PATH, copy)
+    with pytest.raises(_lib.HipLibraryError, match="second copy"):
+        _lib.load(copy)
+    assert _lib.load(_lib.LIBRARY_PATH) is _lib.load()
+
+
 def test_product_runs_without_the_oracle_or_tests_packages():
     program = dedent("""
         import importlib.abc, sys

@@ -260,3 +260,31 @@ def test_released_request_keeps_its_bytes_until_readers_finish():
     torch.testing.assert_close(read, k[0])
     h.cache.release_request("same")
     h.cache.assert_invariants()
+
+
+# ------------------------------------------------------------------ no CPU fallback
+def test_a_cache_off_rocm_needs_explicit_ops():
+    """The product has no CPU kernels: a cache on the CPU without an ops object fails at
+    construction instead of falling back to anything."""
+    from mini_hisparse_amd.hybrid import HybridKVCache
+    from mini_hisparse_amd.paged import PagedKVCache
+
+    config = CacheConfig(gpu_pages=4, host_pages=4, page_size=4, kv_heads=1, head_dim=8, device="cpu",
+                         dtype=torch.float32)
+    with pytest.raises(ValueError, match="ROCm"):
+        HybridKVCache(config, HotConfig(max_union_rows=8))
+    with pytest.raises(ValueError, match="ROCm"):
+        PagedKVCache(config)
+
+
+@pytest.mark.parametrize("backend", ["torch", "triton", "cpu"])
+def test_row_attention_rejects_the_reference_backends(backend):
+    """The reference's torch and Triton attention paths do not exist here (attention.py:7-9)."""
+    from mini_hisparse_amd.attention import row_attention
+
+    config = CacheConfig(gpu_pages=4, host_pages=4, page_size=4, kv_heads=1, head_dim=8, device="cpu",
+                         dtype=torch.float32)
+    cache = make_cache(config, HotConfig(max_union_rows=8))
+    topk = LogicalTopK(torch.tensor([0], dtype=torch.int32))
+    with pytest.raises(ValueError, match="invalid attention backend"):
+        row_attention(torch.zeros(2, 8), cache, "r", 0, topk, backend=backend)

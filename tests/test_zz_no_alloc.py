@@ -98,3 +98,35 @@ def test_noalloc_resolver_rejects_a_batch_above_its_scratch(gpu):
     torch.cuda.synchronize()
     assert torch.equal(keep[0][0]["tags"], tags_before)  # nothing ran
     assert int(keep[0][2]["counts"][0]) == -7
+
+
+def test_noalloc_resolver_replays_from_a_captured_graph(gpu):
+    """After one uncaptured call (the scratch address lookup), the call is captured into a
+    HIP graph; each replay must equal a fresh eager hs_resolve_rows_batched on tables that
+    went through the same steps (the in-place tags and LRU carry hits between steps)."""
+    from mini_hisparse_amd import _lib
+
+    print("[case] noalloc under graph capture: 3 descriptors, 3 replays", flush=True)
+    lib = _lib.load()
+    cases = _cases(600, [(4096, 16, 2048, 1500), (97, 4, 64, 40), (65536, 16, 32768, 20000)])
+    warm, _ = _batch(gpu, cases)
+    _lib.check(lib.hs_resolve_rows_noalloc(warm, len(cases), _lib.stream_handle(torch.device(gpu))), "warm-up")
+    torch.cuda.synchronize()
+    ref_descs, ref = _batch(gpu, cases)
+    need = sum(lib.hs_resolve_workspace_bytes(d.n, d.length, d.n_pages, d.hot_rows) for d in ref_descs)
+    ws = torch.empty(need, dtype=torch.uint8, device=gpu)
+    g_descs, cap = _batch(gpu, cases)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        status = lib.hs_resolve_rows_noalloc(g_descs, len(cases), torch.cuda.current_stream().cuda_stream)
+    assert status == 0, lib.hs_last_error()
+    for step in range(3):
+        _lib.check(lib.hs_resolve_rows_batched(ref_descs, len(cases), ws.data_ptr(), need,
+                                               _lib.stream_handle(torch.device(gpu))), "hs_resolve_rows_batched")
+        graph.replay()
+        torch.cuda.synchronize()
+        for (t0, _, o0), (t1, _, o1) in zip(ref, cap):
+            for name in ("phys", "uphys", "mh", "md", "counts"):
+                assert torch.equal(o0[name], o1[name]), (step, name)
+            assert torch.equal(t0["tags"], t1["tags"]) and torch.equal(t0["lru"], t1["lru"]), step
+    assert int(cap[0][2]["counts"][1]) > 0  # later steps hit the rows the first one loaded
