@@ -66,16 +66,17 @@ struct AttendArgs {
   int64_t B, Hq, g;
   int64_t splits, chunk;
   float scale;
-  float* part_m;  // [B, Hq, splits], or [slots, 16] when scheduled
-  float* part_l;  // like part_m
-  float* part_o;  // [B, Hq, splits, D], or [slots, 16, D] when scheduled
+  // split-K partials as tagged words (partial_word): [B, Hq, splits], or [slots, 16]
+  // when scheduled; part_o [B, Hq, splits, D], or [slots, 16, D]
+  unsigned long long* part_m;
+  unsigned long long* part_l;
+  unsigned long long* part_o;
   int32_t* sched; // T(0 .. B * Hkv) of the scheduled group kernel
   // in-kernel merge (fuse != 0): one arrival counter per (request, KV head, head
   // chunk), [B * Hkv * head_chunks]; `epoch` tags this launch's arrivals
   unsigned long long* arrivals;
   unsigned long long epoch;
   int fuse;
-  int relaxed_merge;  // arrivals without release/acquire (measurement only)
   int contiguous;     // group splits as contiguous chunks, not dealt by tile (measurement only)
   void* out;
   int64_t o_sb, o_sh;
@@ -169,38 +170,87 @@ __device__ __forceinline__ float from_bits(unsigned short v) {
   else return f16_bits_to_f32(v);
 }
 
+// A split-K partial value is one 64-bit word: the fp32 bits in the low half and,
+// when the launch merges its own partials, a tag in the high half that names the
+// launch and, for a launch replayed from a captured graph (same epoch), the replay
+// (group_tag).  The workgroup that merges a group reads every partial word with
+// relaxed device-scope atomic loads and takes a word only once it carries the tag:
+// by coherence of each word, a read that returns the tag returns the value this
+// launch's producer stored, so the merge needs no release/acquire fence (on this
+// multi-XCD part those write back and invalidate the L2: ~6 us per launch,
+// measured).  The producers' stores complete before their arrival is counted, so
+// the first read finds the tag; a word read early is read again (at most
+// kSpinReads times; stores become visible in finite time).
+constexpr int kSpinReads = 1 << 22;
+
+__device__ __forceinline__ unsigned long long partial_word(float v, uint32_t tag) {
+  return (static_cast<unsigned long long>(tag) << 32) | __float_as_uint(v);
+}
+__device__ __forceinline__ float partial_value(unsigned long long w) {
+  return __uint_as_float(static_cast<uint32_t>(w));
+}
+__device__ __forceinline__ void store_partial(unsigned long long* p, float v, uint32_t tag) {
+  __hip_atomic_store(p, partial_word(v, tag), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Tagged read (TAGGED) of a partial word another workgroup of the running launch
+// stores, possibly on another XCD; a plain read of one a finished launch stored.
+template <bool TAGGED>
+__device__ __forceinline__ unsigned long long partial_load(const unsigned long long* p) {
+  if constexpr (TAGGED) return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  else return *p;
+}
+__device__ __noinline__ unsigned long long partial_reread(const unsigned long long* p, uint32_t tag) {
+  unsigned long long w = 0;
+  for (int i = 0; i < kSpinReads; ++i) {
+    w = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (static_cast<uint32_t>(w >> 32) == tag) break;
+    __builtin_amdgcn_s_sleep(1);
+  }
+  return w;
+}
+
 // Combine n split-K partials (m, l, acc[d]) of one head, partial u at
 // base + u * stride.  Partials are read MS at a time, every load issued before
 // any is used (one round of loads per MS partials); chunks after the first
 // rescale the running sums, so for n <= MS the arithmetic is a plain max, then
-// sums in partial order.  Returns the unnormalised (M, L, O).
-// COHERENT reads at device scope (partials other workgroups of the running
-// launch wrote, possibly on another XCD, whose L2 is not this one's).
-template <bool COHERENT>
-__device__ __forceinline__ float partial_at(const float* p) {
-  if constexpr (COHERENT) return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  else return *p;
-}
-
-template <bool COHERENT>
-__device__ __forceinline__ void merge_partials(const float* part_m, const float* part_l, const float* part_o,
-                                               int64_t base, int64_t stride, int64_t n, int64_t d, int64_t D,
-                                               float& M, float& L, float& O) {
-  constexpr int MS = 16;
+// sums in partial order.  Returns the unnormalised (M, L, O).  TAGGED: the
+// partials of the running launch, each taken once it carries `tag`.
+template <bool TAGGED, int MS>
+__device__ __forceinline__ void merge_partials_by(const unsigned long long* part_m, const unsigned long long* part_l,
+                                                  const unsigned long long* part_o, int64_t base, int64_t stride,
+                                                  int64_t n, int64_t d, int64_t D, uint32_t tag,
+                                                  float& M, float& L, float& O) {
   M = -INFINITY;
   L = 0.f;
   O = 0.f;
   for (int64_t s0 = 0; s0 < n; s0 += MS) {
     float ms[MS], ls[MS], os[MS];
+    unsigned long long wm[MS], wl[MS], wo[MS];
 #pragma unroll
     for (int u = 0; u < MS; ++u) {
       const bool ok = s0 + u < n;
       const int64_t pi = base + (ok ? s0 + u : s0) * stride;  // s0 < n: in bounds
-      const float mv = partial_at<COHERENT>(part_m + pi), lv = partial_at<COHERENT>(part_l + pi),
-                  ov = partial_at<COHERENT>(part_o + pi * D + d);
-      ms[u] = ok ? mv : -INFINITY;
-      ls[u] = lv;
-      os[u] = ov;
+      wm[u] = partial_load<TAGGED>(part_m + pi);
+      wl[u] = partial_load<TAGGED>(part_l + pi);
+      wo[u] = partial_load<TAGGED>(part_o + pi * D + d);
+    }
+    if constexpr (TAGGED) {
+#pragma unroll
+      for (int u = 0; u < MS; ++u) {
+        if (s0 + u >= n) continue;
+        const int64_t pi = base + (s0 + u) * stride;
+        if (static_cast<uint32_t>(wm[u] >> 32) != tag) wm[u] = partial_reread(part_m + pi, tag);
+        if (static_cast<uint32_t>(wl[u] >> 32) != tag) wl[u] = partial_reread(part_l + pi, tag);
+        if (static_cast<uint32_t>(wo[u] >> 32) != tag) wo[u] = partial_reread(part_o + pi * D + d, tag);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < MS; ++u) {
+      const bool ok = s0 + u < n;
+      ms[u] = ok ? partial_value(wm[u]) : -INFINITY;
+      ls[u] = partial_value(wl[u]);
+      os[u] = partial_value(wo[u]);
     }
     float Mc = M;
 #pragma unroll
@@ -222,42 +272,61 @@ __device__ __forceinline__ void merge_partials(const float* part_m, const float*
   }
 }
 
-// Arrival of one workgroup at its group's counter; true for the last of `total`.
-// The counter holds (epoch << 16) | arrivals.  A value with another epoch (an
-// earlier launch's, or memory never used as a counter) counts as no arrival: the
-// first workgroup of a launch installs (epoch, 1) with a compare-and-swap, every
-// later one adds 1, so a launch costs one swap and total - 1 additions (no retry
-// loop whose length grows with the arrivals).  The last workgroup clears the
-// counter, so a launch replayed with the same epoch (a captured graph) starts
-// from zero too.  A failed swap means another workgroup changed the counter, so
-// the loop ends after at most one installation and the reads that follow it.
-// Both read-modify-writes are agent-scope releases: every partial this workgroup
-// stored before the arrival (ordered before it by the workgroup barrier) is
-// visible to the workgroup that arrives last, which acquires (merge_group).
-__device__ __forceinline__ bool arrive_last(unsigned long long* counter, unsigned long long epoch, int64_t total) {
-  unsigned long long old = __hip_atomic_load(counter, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  while (true) {
-    if ((old >> 16) == epoch) {
-      const unsigned long long prev = __hip_atomic_fetch_add(counter, 1ull, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
-      return static_cast<int64_t>((prev & 0xffffull) + 1) == total;
-    }
-    unsigned long long expected = old;
-    if (__hip_atomic_compare_exchange_strong(counter, &expected, (epoch << 16) | 1ull, __ATOMIC_RELEASE,
-                                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
-      return total == 1;
-    old = expected;
-  }
+// merge_partials_by with the batch sized to n (4, 8 or 16 partials per round), so
+// that the usual few splits issue no redundant loads (the merging workgroup's loads
+// sit at the end of the launch, on its critical path).  The sums are the same: a
+// batch covers every partial of n <= 16 in order.
+template <bool TAGGED>
+__device__ __forceinline__ void merge_partials(const unsigned long long* part_m, const unsigned long long* part_l,
+                                               const unsigned long long* part_o, int64_t base, int64_t stride,
+                                               int64_t n, int64_t d, int64_t D, uint32_t tag,
+                                               float& M, float& L, float& O) {
+  if (n <= 4) merge_partials_by<TAGGED, 4>(part_m, part_l, part_o, base, stride, n, d, D, tag, M, L, O);
+  else if (n <= 8) merge_partials_by<TAGGED, 8>(part_m, part_l, part_o, base, stride, n, d, D, tag, M, L, O);
+  else merge_partials_by<TAGGED, 16>(part_m, part_l, part_o, base, stride, n, d, D, tag, M, L, O);
 }
-// Relaxed arrival, for measuring what the release costs (HS_ATTEND_MERGE_ORDER=relaxed).
-__device__ __forceinline__ bool arrive_last_relaxed(unsigned long long* counter, unsigned long long epoch,
-                                                    int64_t total) {
+
+// Arrival counter of a (request, KV head, head chunk) group: bits 63-32 the
+// identity of the launch that last used it (counter_id: the low 31 bits of its
+// epoch with bit 31 set), bits 31-16 the replay round, bits 15-0 the arrivals of
+// the running launch.  A counter of another launch (an earlier launch's, or memory
+// never used as a counter) is round 0 with no arrival.  The merging workgroup
+// leaves (id, round + 1, 0): a replay of the same launch from a captured graph then
+// counts from zero again and tags its partials with the next round, so no word of
+// the previous replay carries its tag.  The workspace is shared by launches of
+// other shapes, so the counter of one launch may sit where another left a partial
+// word: partial-word tags have bit 31 clear and counter identities have it set, so
+// a partial word never reads as a counter of the running launch.
+__device__ __forceinline__ uint32_t counter_id(unsigned long long epoch) {
+  return static_cast<uint32_t>(epoch) | 0x80000000u;
+}
+__device__ __forceinline__ uint32_t counter_round(unsigned long long c, unsigned long long epoch) {
+  return static_cast<uint32_t>(c >> 32) == counter_id(epoch) ? static_cast<uint32_t>(c >> 16) & 0xffffu : 0u;
+}
+// Partial-word tag of a group's launch in replay round `round`: odd (never 0, which
+// marks a word of a launch that does not merge its own partials), bit 31 clear,
+// and different for consecutive epochs and for the rounds of one epoch.
+__device__ __forceinline__ uint32_t group_tag(unsigned long long epoch, uint32_t round) {
+  return (2u * static_cast<uint32_t>(epoch) + 1u + 2u * 0x9e3779b9u * round) & 0x7fffffffu;
+}
+
+// Arrival of one workgroup; true for the last of `total`.  The first workgroup of a
+// launch that finds another epoch installs (epoch, 0, 1) with a compare-and-swap,
+// every later one adds 1 (a launch costs one swap and total - 1 additions, no retry
+// loop whose length grows with the arrivals).  A failed swap means another
+// workgroup changed the counter, so the loop ends after at most one installation
+// and the reads that follow it.  The counter only elects the merging workgroup and
+// tells it that every split has stored its partials; the partial words carry their
+// own tag (partial_word).
+__device__ __forceinline__ bool arrive_last(unsigned long long* counter, unsigned long long epoch, int64_t total) {
+  const unsigned long long mine = static_cast<unsigned long long>(counter_id(epoch)) << 32;
   unsigned long long old = __hip_atomic_load(counter, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   while (true) {
-    if ((old >> 16) == epoch) {
+    if ((old >> 32) == (mine >> 32)) {
       const unsigned long long prev = atomicAdd(counter, 1ull);
       return static_cast<int64_t>((prev & 0xffffull) + 1) == total;
     }
-    const unsigned long long seen = atomicCAS(counter, old, (epoch << 16) | 1ull);
+    const unsigned long long seen = atomicCAS(counter, old, mine | 1ull);
     if (seen == old) return total == 1;
     old = seen;
   }
@@ -543,6 +612,10 @@ __global__ __launch_bounds__(64 * attend_waves(DP)) void attend_mfma_kernel(Atte
   const unsigned short* pool = static_cast<const unsigned short*>(a.pool);
   unsigned short* vs = vs_all + wave * 32 * RS;
 
+  // replay round of the group's arrival counter (the in-kernel merge tags its
+  // partial words with it): loaded with the first loads, used after the tiles
+  const unsigned long long counter0 = __hip_atomic_load(a.arrivals + (b * a.Hkv + k) * a.head_chunks + hchunk,
+                                                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   // Q^T fragments (lane holds Q[head hh][d = 32kk + 8j .. +8]): they depend only
   // on (b, k, hchunk), so their loads go out with the first entry loads.
   u32x4 qf[KK];
@@ -779,6 +852,7 @@ __global__ __launch_bounds__(64 * attend_waves(DP)) void attend_mfma_kernel(Atte
     if (a.fuse && split >= parts) return;
   }
 
+  const uint32_t round = counter_round(counter0, a.epoch);
   // per-wave totals over the four lane groups that share a head
   l_run += __shfl_xor(l_run, 16, 64);
   l_run += __shfl_xor(l_run, 32, 64);
@@ -814,41 +888,28 @@ __global__ __launch_bounds__(64 * attend_waves(DP)) void attend_mfma_kernel(Atte
       }
     }
     const int64_t pidx = partial_index(hl);
-    // device-scope stores: written through to where every XCD's loads of the same
-    // scope see them, with no cache-wide write-back or invalidation
+    // device-scope stores of tagged words (partial_word): written through to where
+    // every XCD's loads of the same scope see them
+    const uint32_t tag = a.fuse ? group_tag(a.epoch, round) : 0u;
     if (d == 0) {
-      __hip_atomic_store(a.part_m + pidx, M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(a.part_l + pidx, L, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      store_partial(a.part_m + pidx, M, tag);
+      store_partial(a.part_l + pidx, L, tag);
     }
-    __hip_atomic_store(a.part_o + pidx * D + d, O, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    store_partial(a.part_o + pidx * D + d, O, tag);
   }
   if (!a.fuse) return;
 
   // The group's last workgroup merges every partial of the group and writes the
   // output.  Every wave waits for its partial stores to complete before the
-  // barrier, so they are all in place when the arrival is counted; the last
-  // workgroup reads them after its arrival with device-scope loads.
+  // barrier, so they are in place when the arrival is counted; the last workgroup
+  // reads them as tagged words (merge_partials).
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  if (threadIdx.x == 0) {
-    unsigned long long* counter = a.arrivals + (b * Hkv + k) * a.head_chunks + hchunk;
-    if (a.relaxed_merge) {
-      s_last = arrive_last_relaxed(counter, a.epoch, parts) ? 1 : 0;
-    } else {
-      const bool last = arrive_last(counter, a.epoch, parts);
-      // the last arrival acquires every other workgroup's release before the merge
-      // reads their partials (the barrier below orders the other waves after it)
-      if (last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-      s_last = last ? 1 : 0;
-    }
-  }
+  unsigned long long* counter = a.arrivals + (b * Hkv + k) * a.head_chunks + hchunk;
+  if (threadIdx.x == 0) s_last = arrive_last(counter, a.epoch, parts) ? 1 : 0;
   __syncthreads();
   if (!s_last) return;
-  for (int idx = threadIdx.x; idx < 16 * DP; idx += NTH) {
-    const int head = idx / DP, d = idx % DP;
-    const int hl = 16 * hchunk + head;
-    if (hl >= a.g || d >= D) continue;
-    int64_t base, stride;
+  auto head_base = [&](int head, int hl, int64_t& base, int64_t& stride) {
     if constexpr (SCHED) {
       base = first_slot * 16 + head;
       stride = 16;
@@ -856,13 +917,23 @@ __global__ __launch_bounds__(64 * attend_waves(DP)) void attend_mfma_kernel(Atte
       base = (b * a.Hq + k * a.g + hl) * a.splits;
       stride = 1;
     }
+  };
+  for (int idx = threadIdx.x; idx < 16 * DP; idx += NTH) {
+    const int head = idx / DP, d = idx % DP;
+    const int hl = 16 * hchunk + head;
+    if (hl >= a.g || d >= D) continue;
+    int64_t base, stride;
+    head_base(head, hl, base, stride);
     float M, L, O;
-    merge_partials<true>(a.part_m, a.part_l, a.part_o, base, stride, parts, d, D, M, L, O);
+    merge_partials<true>(a.part_m, a.part_l, a.part_o, base, stride, parts, d, D, group_tag(a.epoch, round), M, L,
+                         O);
     store_elem<DT>(a.out, b * a.o_sb + (k * a.g + hl) * a.o_sh + d, L > 0.f ? O / L : 0.f);
   }
-  if (threadIdx.x == 0)
-    __hip_atomic_store(a.arrivals + (b * Hkv + k) * a.head_chunks + hchunk, 0ull, __ATOMIC_RELAXED,
-                       __HIP_MEMORY_SCOPE_AGENT);
+  if (threadIdx.x == 0)  // the next replay of this launch counts from zero in the next round
+    __hip_atomic_store(counter,
+                       (static_cast<unsigned long long>(counter_id(a.epoch)) << 32) |
+                           (static_cast<unsigned long long>((round + 1) & 0xffffu) << 16),
+                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // VALU fallback: one wave per (split, query head, request); any dtype, D <= 512.
@@ -916,13 +987,13 @@ __global__ __launch_bounds__(64) void attend_valu_kernel(AttendArgs a) {
   }
   const int64_t pidx = (b * a.Hq + h) * a.splits + split;
   if (lane == 0) {
-    a.part_m[pidx] = m_run;
-    a.part_l[pidx] = l_run;
+    a.part_m[pidx] = partial_word(m_run, 0u);
+    a.part_l[pidx] = partial_word(l_run, 0u);
   }
 #pragma unroll
   for (int t = 0; t < ND; ++t) {
     const int64_t d = lane + 64 * t;
-    if (d < D) a.part_o[pidx * D + d] = acc[t];
+    if (d < D) a.part_o[pidx * D + d] = partial_word(acc[t], 0u);
   }
 }
 
@@ -932,8 +1003,9 @@ __global__ __launch_bounds__(64) void attend_valu_kernel(AttendArgs a) {
 // T(i) + (hl / 16) * n + s, s < n = (T(i + 1) - T(i)) / head_chunks, i = b * Hkv + k,
 // and its partial in slot t is t * 16 + hl % 16.
 template <int DT>
-__global__ __launch_bounds__(256) void attend_merge_kernel(const float* part_m, const float* part_l,
-                                                            const float* part_o, int64_t splits,
+__global__ __launch_bounds__(256) void attend_merge_kernel(const unsigned long long* part_m,
+                                                            const unsigned long long* part_l,
+                                                            const unsigned long long* part_o, int64_t splits,
                                                             const int32_t* table, int64_t Hkv, int64_t g,
                                                             int64_t head_chunks, int64_t Hq, int64_t D,
                                                             void* out, int64_t o_sb, int64_t o_sh,
@@ -953,7 +1025,7 @@ __global__ __launch_bounds__(256) void attend_merge_kernel(const float* part_m, 
   }
   for (int64_t d = threadIdx.x; d < D; d += blockDim.x) {
     float M, L, O;
-    merge_partials<false>(part_m, part_l, part_o, base, stride, n, d, D, M, L, O);
+    merge_partials<false>(part_m, part_l, part_o, base, stride, n, d, D, 0u, M, L, O);
     if (st_m) {  // the unnormalised state (m, l, acc) of the head, fp32
       if (d == 0) {
         st_m[b * Hq + h] = M;
@@ -1074,7 +1146,7 @@ struct WsLayout {
 static WsLayout ws_layout(const Plan& p, bool sched, int64_t B, int64_t Hq, int64_t Hkv, int64_t D) {
   WsLayout w{};
   w.n = sched ? p.grid * 16 : B * Hq * p.splits;
-  w.table = (2 * w.n + w.n * D) * 4;
+  w.table = (2 * w.n + w.n * D) * 8;  // tagged 64-bit partial words
   const int64_t table_end = w.table + (sched ? (B * Hkv + 1) * 4 : 0);
   w.arrivals = (table_end + 7) / 8 * 8;
   w.bytes = w.arrivals + B * Hkv * p.head_chunks * 8 + 256;
@@ -1087,9 +1159,11 @@ static int64_t workspace_for(const Plan& p, int64_t B, int64_t Hq, int64_t Hkv, 
   return split > sched ? split : sched;
 }
 
-// Tag of one launch's arrivals: 48 bits, never 0, different for every launch of
-// the process (a counter started from the clock, so that counters left in reused
-// memory by another process are unlikely to carry it either).
+// Epoch of one launch: 48 bits, never 0, different for every launch of the process
+// (a counter started from the clock, so that counters left in reused memory by
+// another process are unlikely to carry it either); its low 31 bits name the
+// launch in the arrival counters (counter_id) and in the partial-word tags
+// (group_tag).
 static unsigned long long next_epoch() {
   static std::atomic<unsigned long long> counter{
       static_cast<unsigned long long>(std::chrono::steady_clock::now().time_since_epoch().count()) * 0x9e3779b97f4a7c15ull};
@@ -1151,7 +1225,7 @@ static int run_attend(int dtype, AttendArgs a, int64_t max_entries, void* out, i
   const WsLayout w = ws_layout(p, sched, a.B, a.Hq, a.Hkv, a.D);
   HS_CHECK_ARG(ws != nullptr && ws_bytes >= w.bytes, "attention workspace too small: need %lld bytes",
                static_cast<long long>(w.bytes));
-  float* base = static_cast<float*>(ws);
+  unsigned long long* base = static_cast<unsigned long long*>(ws);
   a.part_m = base;
   a.part_l = base + w.n;
   a.part_o = base + 2 * w.n;
@@ -1175,8 +1249,6 @@ static int run_attend(int dtype, AttendArgs a, int64_t max_entries, void* out, i
   HS_CHECK_ARG(!a.fuse || ceil_div(max_entries, 128) <= 0xffff, "too many entries per attention group");
   a.arrivals = reinterpret_cast<unsigned long long*>(static_cast<char*>(ws) + w.arrivals);
   a.epoch = next_epoch();
-  const char* order_env = getenv("HS_ATTEND_MERGE_ORDER");
-  a.relaxed_merge = order_env && strcmp(order_env, "relaxed") == 0 ? 1 : 0;
   const char* deal_env = getenv("HS_ATTEND_DEAL");
   a.contiguous = deal_env && atoi(deal_env) == 0 ? 1 : 0;
   a.out = out;
@@ -1200,9 +1272,9 @@ static int run_attend(int dtype, AttendArgs a, int64_t max_entries, void* out, i
   dim3 mgrid(static_cast<unsigned>(a.Hq), static_cast<unsigned>(a.B));
   const unsigned mthreads = a.D <= 64 ? 64 : (a.D <= 128 ? 128 : 256);
   const int64_t hcs = a.head_chunks;
-  const float* pm = a.part_m;
-  const float* pl = a.part_l;
-  const float* po = a.part_o;
+  const unsigned long long* pm = a.part_m;
+  const unsigned long long* pl = a.part_l;
+  const unsigned long long* po = a.part_o;
   const int32_t* table = a.sched;
   const int64_t splits = p.splits, Hkv = a.Hkv, g = a.g, Hq = a.Hq, D = a.D;
   if (dtype == HS_DTYPE_F32)

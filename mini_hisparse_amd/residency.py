@@ -17,8 +17,9 @@ write (the CPU semantics of the policy: every written page is clean at the next
 tick) and with no row leases open (nothing is read while the plan is built).
 What it exploits:
 
-* the empty blocks are always a suffix ``[next_free, blocks)`` -- blocks are
-  taken lowest first and never returned (no request is released);
+* the empty blocks are a suffix ``[next_free, blocks)`` plus the blocks released
+  requests returned (a min-heap below ``next_free``) -- blocks are taken lowest
+  first, like the allocator's ascending free list;
 * every queued block is readable (the only pinned page is an append tail, which
   is never history);
 * a page is bound once, when it is written, so a group's history in bind order
@@ -28,12 +29,16 @@ What it exploits:
   region is still owed, and the groups with residents and no demand yet (the
   watermark or the window may raise it); the others are skipped.
 
-``tests/test_residency_plan.py`` checks every decision, queue and counter against
-``HybridKVCache`` itself on random write sequences.
+``release`` is ``HybridKVCache.release_request``: a finished request's hot blocks
+and resident pages become empty blocks (queued ones leave the reclaim queue) and
+its groups leave the plan.  ``tests/test_residency_plan.py`` checks every
+decision, queue and counter against ``HybridKVCache`` itself on random write
+sequences, with requests released and new ones admitted between them.
 """
 
 from __future__ import annotations
 
+import heapq
 from collections import Counter, deque
 from math import ceil
 
@@ -45,7 +50,8 @@ ACTIVE_TAIL_PAGES = 2
 
 
 class _Group:
-    __slots__ = ("gid", "key", "slot", "valid", "length", "residents", "hot", "required", "trigger", "offered")
+    __slots__ = ("gid", "key", "slot", "valid", "length", "residents", "hot", "required", "trigger", "offered",
+                 "released")
 
     def __init__(self, gid, key, pages):
         self.gid, self.key = gid, key
@@ -57,6 +63,7 @@ class _Group:
         self.required = False
         self.trigger = None
         self.offered = 0  # pages [0, offered) have been offered to the reclaim queue
+        self.released = False
 
 
 class PlacementPlan:
@@ -72,8 +79,14 @@ class PlacementPlan:
         self.window = window
         self.watermark = max(self.hot_blocks, blocks // 10) if watermark is None else watermark
         self.next_free = 0
-        self.queue: deque[int] = deque()  # reclaimable blocks, queue order
+        self.free: list[int] = []  # empty blocks below next_free (released), a min-heap
+        # reclaimable blocks in queue order as (block, ticket); an entry is live while the
+        # block is queued under that ticket (a released block leaves the queue at once,
+        # its entry is dropped when it reaches the head)
+        self._queue: deque[tuple[int, int]] = deque()
         self.queued = np.zeros(blocks, bool)
+        self.ticket = np.zeros(blocks, np.int64)
+        self.n_queued = 0
         self.owner = np.full(blocks, -1, np.int64)  # group id of a page's block, -1 (free or hot)
         self.owner_page = np.zeros(blocks, np.int64)
         self.bind_order = np.zeros(blocks, np.int64)  # clock of the block's page bind
@@ -92,7 +105,20 @@ class PlacementPlan:
         return self.groups[self._by_key[key]]
 
     def available(self):
-        return self.blocks - self.next_free + len(self.queue)
+        return self.blocks - self.next_free + len(self.free) + self.n_queued
+
+    @property
+    def queue(self):
+        """The reclaimable blocks, in queue order."""
+        return [b for b, t in self._queue if self.queued[b] and self.ticket[b] == t]
+
+    def _queue_head(self):
+        while self._queue:
+            block, ticket = self._queue[0]
+            if self.queued[block] and self.ticket[block] == ticket:
+                return block
+            self._queue.popleft()
+        return None
 
     def _tail(self, g: _Group):
         if self._writing is not None and self._writing[0] == g.gid:
@@ -128,16 +154,19 @@ class PlacementPlan:
     def _enqueue(self, block):
         if not self.queued[block]:
             self.queued[block] = True
-            self.queue.append(block)
             self._clock += 1
+            self.ticket[block] = self._clock
+            self._queue.append((block, self._clock))
+            self.n_queued += 1
 
     def _take(self, block):
         """Hand an available block to a new owner; a queued one detaches its page."""
         if self.queued[block]:
-            if self.queue[0] != block:
+            if self._queue_head() != block:
                 raise AssertionError("blocks leave the reclaim queue from its head")
-            self.queue.popleft()
+            self._queue.popleft()
             self.queued[block] = False
+            self.n_queued -= 1
             g = self.groups[int(self.owner[block])]
             page = int(self.owner_page[block])
             g.slot[page] = -1
@@ -148,16 +177,20 @@ class PlacementPlan:
             self.stats["unpinned_block_reuses"] += 1
             self.stats["evictions"] += 1
             self.detached.append((g.key, page))
-        elif block == self.next_free:
+        elif self.free and block == self.free[0]:
+            heapq.heappop(self.free)
+        elif block == self.next_free and not (self.free and self.free[0] < block):
             self.next_free += 1
         else:
             raise AssertionError("empty blocks are taken lowest first")
         return block
 
     def _first_available(self):
+        if self.free:
+            return self.free[0]  # below next_free
         if self.next_free < self.blocks:
             return self.next_free
-        return self.queue[0] if self.queue else None
+        return self._queue_head()
 
     # -- policy --------------------------------------------------------------------------
     def _offer(self, g: _Group):
@@ -320,6 +353,37 @@ class PlacementPlan:
         self.stats["resident_hits"] += len(groups)
         self.stats["append_resident_hits"] += len(groups)
         return True
+
+    # -- release ------------------------------------------------------------------------
+    def release(self, request):
+        """``HybridKVCache.release_request`` and its collect: every hot block and resident
+        page of the request's groups becomes an empty block (a queued one leaves the
+        reclaim queue), the groups leave the plan, then a tick over every group.
+        Returns the groups' keys."""
+        layers = self.requests.pop(request)
+        groups = [self.groups[self._by_key.pop((request, layer))] for layer in range(layers)]
+        for g in groups:
+            for block in g.hot:
+                heapq.heappush(self.free, int(block))
+            g.hot = []
+        for g in groups:
+            for page in np.flatnonzero(g.slot >= 0).tolist():
+                block = int(g.slot[page])
+                if self.queued[block]:
+                    self.queued[block] = False
+                    self.n_queued -= 1
+                self.owner[block] = -1
+                heapq.heappush(self.free, block)
+                g.slot[page] = -1
+                self.stats["evictions"] += 1
+            g.residents = 0
+            g.released = True
+            self._open.discard(g.gid)
+            self._owed.discard(g.gid)
+        self.detached = [(key, page) for key, page in self.detached if key[0] != request]
+        self.stats["retired_requests"] += 1
+        self._tick(None)
+        return [g.key for g in groups]
 
     def resident_pages(self, key):
         """(pages, blocks) of the group's resident pages."""

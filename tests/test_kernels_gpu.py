@@ -662,14 +662,15 @@ def test_in_kernel_merge_starts_from_any_workspace_contents(gpu, monkeypatch):
 
 
 def test_in_kernel_merge_replays_from_a_captured_graph(gpu, monkeypatch):
-    """A captured attention replays with the epoch of its capture: the last workgroup
-    clears its group's counter, so every replay (with eager launches of other epochs
-    between them) merges exactly once per group."""
+    """A captured attention replays with the epoch (and partial-word tag) of its
+    capture: the last workgroup clears its group's counter and the partial words it
+    merged, so every replay (with eager launches of other epochs between them, and a
+    new query each time) merges this replay's partials exactly once per group."""
     from mini_hisparse_amd.row_kernels import attend_groups
 
     monkeypatch.setenv("HS_ATTEND_FUSED_MERGE", "1")
     case = _group_case(gpu)
-    eager = attend_groups(*case)
+    q = case[0]
     side = torch.cuda.Stream(gpu)
     side.wait_stream(torch.cuda.current_stream(gpu))
     with torch.cuda.stream(side):
@@ -678,12 +679,14 @@ def test_in_kernel_merge_replays_from_a_captured_graph(gpu, monkeypatch):
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph, stream=side):
         captured = attend_groups(*case)
+    gen = torch.Generator().manual_seed(99)
     for _ in range(4):
+        q.copy_(torch.randn(q.shape, generator=gen).to(q.dtype))  # the graph reads q in place
+        eager = attend_groups(*case)  # another workspace, another epoch
         captured.zero_()
         graph.replay()
         torch.cuda.synchronize()
         torch.testing.assert_close(captured, eager, rtol=0, atol=0)
-        torch.testing.assert_close(attend_groups(*case), eager, rtol=0, atol=0)  # an eager launch between
 
 
 # ------------------------------------------------------- page-window attention

@@ -119,3 +119,94 @@ def test_a_long_prefill_takes_the_window_route_and_queues_history_tail_first():
     pages, held = plan.resident_pages(("a", 0))
     assert held.size == blocks - 2  # every other block ends up holding a page
     assert pages[-1] == 39 and pages[-2] == 38
+
+
+def run_churn_case(seed):
+    """Requests admitted, decoded, released and replaced: after every release the freed
+    hot blocks and resident pages are empty blocks again (queued ones leave the reclaim
+    queue), and later admissions and writes take them lowest first -- the same blocks,
+    regions, queue and counters as ``HybridKVCache.release_request``."""
+    rng = np.random.default_rng(seed)
+    P = int(rng.choice([2, 4]))
+    layers = int(rng.integers(1, 4))
+    hot_rows = P * int(rng.integers(1, 4))
+    window = int(rng.integers(2, 9))
+    watermark = [None, 0, int(rng.integers(1, 6))][int(rng.integers(0, 3))]
+    max_len, decode = 10 * P, 2 * P
+    per_request = layers * (-(-(max_len + decode) // P))
+    blocks = max(layers * (hot_rows // P + 2) * 2, int(rng.integers(per_request // 2 + 1, 2 * per_request + 2)))
+    config = CacheConfig(gpu_pages=blocks, host_pages=8 * per_request, page_size=P, kv_heads=1, head_dim=8,
+                         device="cpu")
+    cache = make_cache(config, HotConfig(hot_rows, hot_rows, resident_window_pages=window,
+                                         transition_watermark=watermark))
+    plan = PlacementPlan(blocks, P, hot_rows, window=window, watermark=watermark)
+    gen = torch.Generator().manual_seed(seed)
+    live, next_id, budget = [], 0, {}
+    for _ in range(6):
+        # admit up to two requests (a refused one is dropped, as the engine would defer it)
+        for _ in range(int(rng.integers(1, 3))):
+            r, n = next_id, int(rng.integers(1, max_len))
+            next_id += 1
+            try:
+                cache.reserve(r, n + decode, layers)
+            except CapacityError as error:
+                with pytest.raises(CapacityError, match=re.escape(str(error)[:20])):
+                    plan.reserve(r, n + decode, layers)
+                continue
+            plan.reserve(r, n + decode, layers)
+            for layer in range(layers):
+                k = torch.randn(n, 1, 8, generator=gen)
+                try:
+                    cache.write(r, layer, k, k)
+                except CapacityError:
+                    with pytest.raises(CapacityError):
+                        plan.write((r, layer), n)
+                    return
+                plan.write((r, layer), n)
+                compare(cache, plan)
+            live.append(r)
+            budget[r] = decode
+        # a few decode steps, request by request, within each request's reservation
+        for _ in range(int(rng.integers(0, decode // 2 + 1))):
+            for r in live:
+                if budget[r] == 0:
+                    continue
+                budget[r] -= 1
+                for layer in range(layers):
+                    k = torch.randn(1, 1, 8, generator=gen)
+                    try:
+                        cache.write(r, layer, k, k)
+                    except CapacityError:
+                        with pytest.raises(CapacityError):
+                            plan.write((r, layer), 1)
+                        return
+                    plan.write((r, layer), 1)
+            compare(cache, plan)
+        # release one or two requests
+        for _ in range(min(len(live), int(rng.integers(1, 3)))):
+            r = live.pop(int(rng.integers(0, len(live))))
+            cache.release_request(r)
+            plan.release(r)
+            compare(cache, plan)
+    return next_id
+
+
+@pytest.mark.parametrize("seed", range(30))
+def test_placement_plan_releases_like_the_policy(seed):
+    run_churn_case(2000 + seed)
+
+
+def test_release_returns_every_block():
+    """One request fills the slab (hot region, history queued); after its release every
+    block is empty again and the next request's pages take them from the lowest."""
+    P, blocks = 4, 24
+    plan = PlacementPlan(blocks, P, hot_rows=8, window=4, watermark=0)
+    plan.reserve("a", 40 * P, 1)
+    plan.write(("a", 0), 40 * P)
+    assert plan.available() < blocks
+    plan.release("a")
+    assert plan.available() == blocks and plan.queue == []
+    plan.reserve("b", 3 * P, 1)
+    assert [block for _, block in plan.write(("b", 0), 3 * P)] == [0, 1, 2]
+    with pytest.raises(KeyError):
+        plan.release("a")
