@@ -102,6 +102,9 @@ def parse_args():
                    help="model workloads with a prefill: the hybrid policy places pages and hot regions in a slab "
                         "of resident_fraction of the history plus every layer's promised hot region and tails "
                         "(default), or a seeded fixed fraction of each layer's pages is resident")
+    p.add_argument("--direct", action="store_true",
+                   help="model workloads: prefill every prompt first and time the engine's device-resident "
+                        "token loop only, instead of admitting and decoding through the Engine API")
     p.add_argument("--synthetic-history", action="store_true",
                    help="model workloads: write synthetic K/V histories (N(0,1), 2%% of channels x8) directly "
                         "instead of prefilling random prompts through the model")
@@ -1068,59 +1071,64 @@ class KernelTimer:
 
 class AttendProbe:
     """Timing of every attention launch of the timed steps: its kernels' own duration
-    (``KernelTimer``, the figure the roofline uses) and, as a secondary figure, HIP events
-    recorded on the compute stream around the launch; plus a device copy of each launch's
-    entry counts (the rows each (request, KV head) reads), from which the launch's
-    algorithmic bytes follow.  Events and the count buffer are allocated before the timed
-    region.  ``fence``: the engine hands the gather's rows over from another stream (see
-    ``before_attend``)."""
+    (``KernelTimer``), plus a device copy of each launch's entry counts (the rows each
+    (request, KV head) reads), from which the launch's algorithmic bytes follow.  Events
+    and the count buffer are allocated before the timed region; per launch the probe
+    adds one 32-byte device copy to the step."""
 
-    def __init__(self, torch, device, launches, batch, kv_heads, fence=True):
+    def __init__(self, torch, device, launches, batch, kv_heads):
         self.torch = torch
-        self.fence = fence
-        self.start = [torch.cuda.Event(enable_timing=True) for _ in range(launches)]
-        self.end = [torch.cuda.Event(enable_timing=True) for _ in range(launches)]
         self.kernel = KernelTimer(torch, launches)
         self.counts = torch.zeros((launches, batch * kv_heads), dtype=torch.int32, device=device)
         self.widths = []
         self.i = 0
 
     def before_attend(self, layer, stream, dec):
-        # HIP stamps an event with the end of the stream's previous command; the engine
-        # queues a wait for the gather right before the attention, so a start event
-        # recorded there could carry a time from before that wait.  A 1-cycle kernel
-        # placed after the wait gives the start event a time after it.  With every stage
-        # on one stream there is no such wait, and the start event follows the gather.
-        if self.fence:
-            self.torch.cuda._sleep(1)
-        self.start[self.i].record(stream)
         self.kernel.arm(self.i)
 
     def after_attend(self, layer, stream, dec):
-        self.end[self.i].record(stream)
         counts = dec.entry_counts.view(-1)  # the launch's requests (a request group's, when pipelined)
         self.counts[self.i, : counts.numel()].copy_(counts)
         self.widths.append((dec.width, dec.batch))
         self.i += 1
 
     def totals(self, bytes_of):
-        """(kernel ms, event-window ms, algorithmic bytes, launches), totals over the
-        launches; ``bytes_of(entries, width, batch)`` gives one launch's bytes."""
+        """(kernel ms, algorithmic bytes, launches), totals over the launches;
+        ``bytes_of(entries, width, batch)`` gives one launch's bytes."""
         n = self.i
         kernel_ms = sum(self.kernel.ms(i) for i in range(n))
-        window_ms = sum(self.start[i].elapsed_time(self.end[i]) for i in range(n))
         entries = self.counts[:n].sum(1).tolist()
         nbytes = sum(bytes_of(e, w, b) for e, (w, b) in zip(entries, self.widths))
-        return kernel_ms, window_ms, nbytes, n
+        return kernel_ms, nbytes, n
+
+
+def _time_steps(torch, run, steps):
+    """Wall time of ``steps`` calls of ``run`` between two device synchronisations."""
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        run()
+    torch.cuda.synchronize()
+    return time.perf_counter() - t0
 
 
 def run_model_workload(args, torch, device):
-    """End-to-end decode of a Qwen-shape random-init model with the layer-major engine."""
+    """End-to-end decode of a Qwen-shape random-init model with the layer-major engine.
+
+    Default (the drop-in path): through the reference's Engine API (``LayerMajorEngine``).
+    The batch's random prompts are added as requests and admitted one per step between
+    decode turns (each prefilled through the model, its K/V written by hs_append_tokens and
+    its pages placed by the hybrid policy); once all run, the timed steps are
+    ``Engine.step()`` calls, each returning the step's (request, token) pairs (one read of
+    the tokens per step).  The same state then runs as many steps on the engine's
+    device-resident token loop (``BatchedDecodeEngine.step``, no read-back per step):
+    ``device_loop``.  ``--direct``, ``--synthetic-history`` or ``--residency fraction``:
+    every prompt prefilled (or the history written) first, then the device loop only."""
     from dataclasses import replace
 
     from mini_hisparse_amd.batched_engine import (
-        WORKLOADS, BatchedDecodeEngine, build_state, empty_state, host_bytes_per_request, random_model,
-        random_prompts,
+        WORKLOADS, BatchedDecodeEngine, build_state, empty_state, host_bytes_per_request, policy_blocks,
+        random_model, random_prompts,
     )
 
     wl = WORKLOADS[args.workload]
@@ -1135,50 +1143,82 @@ def run_model_workload(args, torch, device):
         print(f"[bench] batch {wl.batch} needs {wl.batch * per_request / 2**30:.0f} GiB pinned; "
               f"running batch {fits}", file=sys.stderr, flush=True)
         wl = replace(wl, batch=fits)
-    if args.warmup + args.steps + 1 > wl.steps:
-        raise SystemExit(f"warmup + steps + 1 profiled step must fit the workload's {wl.steps} decode steps")
-    t0 = time.perf_counter()
-    print(f"[bench] {wl.name}: model + {'synthetic history' if args.synthetic_history else 'prefill'} "
-          f"(batch {wl.batch}, {wl.context} tokens)", file=sys.stderr, flush=True)
-    model = random_model(wl, device, seed=args.seed)
-    first_tokens = None
-    if not args.synthetic_history:
-        state = empty_state(wl, device, residency=args.residency)
-        print(f"[bench] prefill of {wl.batch} random prompts", file=sys.stderr, flush=True)
-        t_prefill = time.perf_counter()
-        first_tokens = state.prefill(model, random_prompts(wl, device, seed=args.seed), wl.resident_fraction,
-                                     seed=args.seed)
-        prefill_s = time.perf_counter() - t_prefill
-    else:
-        state = build_state(wl, device, seed=args.seed)
+    api = not (args.direct or args.synthetic_history or args.residency == "fraction")
+    # decode steps a request takes in the run: admission turns, warmup, timed steps, two
+    # in-order steps, the profiled step and the device-loop steps
+    needed = wl.batch + args.warmup + 2 * args.steps + 4
+    if needed > wl.steps:
+        raise SystemExit(f"the run needs {needed} decode steps per request, above the workload's {wl.steps}")
     groups = args.request_groups
     if groups is None:
         groups = DEFAULT_REQUEST_GROUPS.get(args.workload, 1)
-    engine = BatchedDecodeEngine(model, state, wl.top_pages, selector=wl.selector, seed=args.seed, graphs=args.graphs,
-                                 projections=args.projections,
-                                 prefetch=not args.no_prefetch and wl.selector == "uniform",
-                                 request_groups=groups if wl.selector == "quest" else 1,
-                                 group_gather_workgroups=args.group_gather_workgroups
-                                 if args.group_gather_workgroups is not None
-                                 else DEFAULT_GROUP_GATHER_WORKGROUPS.get(args.workload, 0))
+    options = dict(seed=args.seed, graphs=args.graphs, projections=args.projections,
+                   prefetch=not args.no_prefetch and wl.selector == "uniform",
+                   request_groups=groups if wl.selector == "quest" else 1,
+                   group_gather_workgroups=args.group_gather_workgroups if args.group_gather_workgroups is not None
+                   else DEFAULT_GROUP_GATHER_WORKGROUPS.get(args.workload, 0))
+    t0 = time.perf_counter()
+    print(f"[bench] {wl.name}: model + {'synthetic history' if args.synthetic_history else 'prefill'} "
+          f"(batch {wl.batch}, {wl.context} tokens, {'Engine API' if api else 'direct'})", file=sys.stderr,
+          flush=True)
+    model = random_model(wl, device, seed=args.seed)
+    prefill_s, admission = None, None
+    if api:
+        from mini_hisparse_amd.config import CacheConfig
+        from mini_hisparse_amd.hybrid import HotConfig
+        from mini_hisparse_amd.selection import union_bound
+        from mini_hisparse_amd.serving import LayerMajorCache, LayerMajorEngine
+
+        P = wl.page_size
+        max_tokens = wl.context + wl.steps
+        config = CacheConfig(gpu_pages=policy_blocks(wl), host_pages=wl.batch * wl.layers * ceil(max_tokens / P),
+                             page_size=P, kv_heads=wl.kv_heads, head_dim=wl.head_dim, device=str(device),
+                             dtype=wl.dtype, index_budget_bytes=1 << 40)
+        heads = 1 if wl.selector == "uniform" else wl.heads
+        hot = HotConfig(union_bound(max_tokens, P, wl.top_pages, heads), wl.hot_rows)
+        cache = LayerMajorCache(config, hot, wl.layers, max_requests=wl.batch, max_tokens=max_tokens)
+        api_engine = LayerMajorEngine(model, cache, wl.top_pages, selector=wl.selector, **options)
+        engine, state = api_engine.batched, cache.state
+        prompts = random_prompts(wl, device, seed=args.seed).cpu()
+        for b in range(wl.batch):
+            api_engine.add_request(str(b), prompts[b].tolist(), wl.steps)
+        del prompts
+        print(f"[bench] admitting {wl.batch} requests through Engine.step (one prefill per step)", file=sys.stderr,
+              flush=True)
+        t_prefill = time.perf_counter()
+        admission = 0
+        while api_engine.waiting:
+            api_engine.step()
+            admission += 1
+        torch.cuda.synchronize()
+        prefill_s = time.perf_counter() - t_prefill
+        step = lambda **kw: api_engine.step(**kw)  # noqa: E731
+    else:
+        if not args.synthetic_history:
+            state = empty_state(wl, device, residency=args.residency)
+            print(f"[bench] prefill of {wl.batch} random prompts", file=sys.stderr, flush=True)
+            t_prefill = time.perf_counter()
+            tokens = state.prefill(model, random_prompts(wl, device, seed=args.seed), wl.resident_fraction,
+                                   seed=args.seed)
+            prefill_s = time.perf_counter() - t_prefill
+        else:
+            state = build_state(wl, device, seed=args.seed)
+            gen = torch.Generator(device=device).manual_seed(args.seed)
+            tokens = torch.randint(0, wl.vocab, (wl.batch,), generator=gen, device=device)
+        engine = BatchedDecodeEngine(model, state, wl.top_pages, selector=wl.selector, **options)
+        loop = {"tokens": tokens}
+
+        def step(**kw):
+            loop["tokens"] = engine.step(loop["tokens"], **kw)
+
     setup_s = time.perf_counter() - t0
-    gen = torch.Generator(device=device).manual_seed(args.seed)
-    tokens = torch.randint(0, wl.vocab, (wl.batch,), generator=gen, device=device)
-    if first_tokens is not None:
-        tokens = first_tokens
     for _ in range(args.warmup):
-        tokens = engine.step(tokens)
-    torch.cuda.synchronize()
+        step()
     print("[bench] timing", file=sys.stderr, flush=True)
     stats0 = state.row_stats.clone()
     launches = args.steps * wl.layers * (len(engine.groups) if engine.groups else 1)
-    probe = AttendProbe(torch, device, launches, wl.batch, wl.kv_heads, fence=engine.transfer is not None)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        tokens = engine.step(tokens, probe=probe)
-    torch.cuda.synchronize()
-    elapsed = time.perf_counter() - t0
+    probe = AttendProbe(torch, device, launches, wl.batch, wl.kv_heads)
+    elapsed = _time_steps(torch, lambda: step(probe=probe), args.steps)
     ms_per_step = elapsed * 1e3 / args.steps
     rows = ((state.row_stats - stats0).double() / args.steps).tolist()
     in_order = None
@@ -1186,15 +1226,29 @@ def run_model_workload(args, torch, device):
         # the same attention with the batch in one group and no gather running beside it:
         # two extra steps in layer order, outside the timed region
         groups_saved, engine.groups = engine.groups, None
-        solo = AttendProbe(torch, device, 2 * wl.layers, wl.batch, wl.kv_heads, fence=engine.transfer is not None)
+        in_order = AttendProbe(torch, device, 2 * wl.layers, wl.batch, wl.kv_heads)
         for _ in range(2):
-            tokens = engine.step(tokens, probe=solo)
+            step(probe=in_order)
         torch.cuda.synchronize()
         engine.groups = groups_saved
-        in_order = solo
     timer = []
-    engine.step(tokens, timer=timer)  # profiled step, outside the timed region
+    step(timer=timer)  # profiled step, outside the timed region
     torch.cuda.synchronize()
+    device_loop = None
+    if api:
+        # the same state on the engine's device-resident token loop (no read-back per step)
+        loop_tokens = torch.zeros(wl.batch, dtype=torch.int64, device=device)
+        for request in api_engine.running:
+            loop_tokens[cache.slot_of[request.request_id]] = request.generated[-1]
+        loop = {"tokens": loop_tokens}
+
+        def device_step():
+            loop["tokens"] = engine.step(loop["tokens"])
+
+        loop_s = _time_steps(torch, device_step, args.steps)
+        device_loop = {"value": wl.batch * args.steps / loop_s, "ms_per_step": loop_s * 1e3 / args.steps,
+                       "how": "BatchedDecodeEngine.step on the same state after the timed Engine.step calls: "
+                              "the tokens stay on the device (no per-step read-back or host-side scheduling)"}
     stage_ms = {}
     for _, marks, _, _ in timer:
         for stage, (start, end) in marks.items():
@@ -1206,15 +1260,14 @@ def run_model_workload(args, torch, device):
         # union-deduplicated K/V rows + the per-head row lists + queries and outputs
         return entries * 2 * D * e + 8 * Hq * width * batch + 2 * Hq * D * e * batch
 
-    att_ms, att_window_ms, att_bytes, launches = probe.totals(launch_bytes)
+    att_ms, att_bytes, launches = probe.totals(launch_bytes)
     att_gbs = att_bytes / (att_ms * 1e-3) / 1e9
     solo_line = None
     if in_order is not None:
-        solo_ms, solo_window_ms, solo_bytes, solo_n = in_order.totals(launch_bytes)
+        solo_ms, solo_bytes, solo_n = in_order.totals(launch_bytes)
         solo_gbs = solo_bytes / (solo_ms * 1e-3) / 1e9
         solo_line = {"achieved": solo_gbs, "frac": solo_gbs / HBM_PEAK_GBS, "launches": solo_n,
                      "bytes_per_launch": solo_bytes / solo_n, "us_per_launch": solo_ms * 1e3 / solo_n,
-                     "event_window_us_per_launch": solo_window_ms * 1e3 / solo_n,
                      "how": "two extra steps after the timed region with the whole batch in one group, "
                             "in layer order (no gather running beside the attention); kernel duration "
                             "from dispatch-stamped events"}
@@ -1244,7 +1297,9 @@ def run_model_workload(args, torch, device):
                  f"synthetic: random-init {wl.name} weights; {wl.context}-token K/V histories (N(0,1), 2% "
                  "channels x8) written directly instead of a prefill; greedy decode from random tokens"),
         "config": {
-            "workload": f"{wl.name} end to end (layer-major batched engine): {wl.layers} layers, hidden "
+            "workload": f"{wl.name} end to end (layer-major batched engine"
+            + (", through the Engine API: requests admitted one per step, timed Engine.step() calls" if api else "")
+            + f"): {wl.layers} layers, hidden "
             f"{wl.hidden}, {wl.heads} q / {wl.kv_heads} kv heads, head_dim {wl.head_dim}, FFN {wl.ffn}, "
             f"batch {wl.batch}, {wl.context}-token histories, "
             + (f"Quest top-{wl.top_pages} pages, " if wl.selector == "quest" else
@@ -1279,9 +1334,9 @@ def run_model_workload(args, torch, device):
             "launches": launches,
             "bytes_per_launch": att_bytes / launches,
             "us_per_launch": att_ms * 1e3 / launches,
-            "event_window_us_per_launch": att_window_ms * 1e3 / launches,
             "in_order": solo_line,
         },
+        "device_loop": device_loop,
         "stages_ms_per_step": stage_ms,
         "projections_on_hs_skinny_gemm": engine.projection_kernel,
         "rows_per_step": {"resident_hits": rows[0], "hot_hits": rows[1], "misses": rows[2]},
@@ -1289,7 +1344,8 @@ def run_model_workload(args, torch, device):
                    "host_link_memcpy_GBps": link,
                    "frac_host_link": gather_bytes / (stage_ms["gather"] * 1e-3) / 1e9 / link},
         "setup_s": setup_s,
-        "prefill_s": None if args.synthetic_history else prefill_s,
+        "prefill_s": prefill_s,
+        "admission_steps": admission,
         "placement": None if state.plan is None else {
             "resident_pages_per_request": [
                 sum(int((state.plan.group((b, l)).slot >= 0).sum()) for l in range(wl.layers))

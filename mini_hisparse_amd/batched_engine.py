@@ -272,83 +272,122 @@ class SparseKVState:
         ``resident_fraction`` of the pages plus the tail page in resident blocks, exact
         Quest bounds.  Returns the greedy first tokens [B] (the prefill's logits).
         ``observer(layer, b, k, v)`` sees each layer's prompt K/V."""
-        from torch.nn.attention import SDPBackend, sdpa_kernel
-
-        cfg = model.config
         if len(prompts) != self.batch:
             raise ValueError(f"expected {self.batch} prompts")
-        groups = cfg.num_attention_heads // cfg.num_key_value_heads
-        P = self.config.page_size
-        firsts, lengths = [], []
+        firsts = []
         for b, prompt in enumerate(prompts):
-            tokens = torch.as_tensor(prompt, device=self.device)
-            used = ceil(len(tokens) / P)
-            if len(tokens) > self.pages * P:
-                raise ValueError("prompt longer than the state's capacity")
-            slots = []
             if self.plan is not None:
-                self.plan.reserve(b, self.pages * P, self.layers)
-            else:
-                for l in range(self.layers):
-                    pages, blocks = self._place_residents(l, b, used, resident_fraction, seed)
-                    row = np.full(used, -1, np.int64)
-                    row[pages] = blocks
-                    slots.append(row)
-
-            def attend(index, q, k, v):
-                if self.plan is not None:  # the policy places this layer's pages as it writes them
-                    self.plan.write((b, index), len(k))
-                    slots.append(self.plan.group((b, index)).slot[:used].copy())
-                self.write_prompt(index, b, k, v, slots[index])
-                if observer is not None:
-                    observer(index, b, k, v)
-                # [1, heads, tokens, dim]: the fused kernels take 4-D operands only
-                heads_first = lambda t: t.transpose(0, 1).unsqueeze(0).contiguous()  # noqa: E731
-                grouped = lambda t: heads_first(t.repeat_interleave(groups, 1))  # noqa: E731
-                with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
-                    out = F.scaled_dot_product_attention(heads_first(q), grouped(k), grouped(v), is_causal=True)
-                return out[0].transpose(0, 1)
-
-            hidden = model._layers(tokens, 0, attend)
-            firsts.append(model._logits(hidden[-1]).argmax())
-            lengths.append(len(tokens))
+                self.plan.reserve(b, self.pages * self.config.page_size, self.layers)
+            firsts.append(self._prefill_request(model, b, prompt, resident_fraction, seed, observer))
         torch.cuda.synchronize(self.device)
-        self.lengths = lengths
         if self.plan is not None:
             self._tables_from_plan()
         return torch.stack(firsts)
 
-    def _tables_from_plan(self):
-        """Resident pages, hot regions and tail blocks of every (l, b) as the policy
-        left them (pages it detached again hold -1).  A (request, layer) whose prefill
-        raised no hot demand (fewer pages than the window, the watermark never crossed)
-        takes its region now, request by request (the policy's explicit transition): the
-        decode serves every row it selects outside the resident pages from it."""
-        L, B, C = self.layers, self.batch, self.pages
-        resident = np.full((L, B, C), -1, np.int32)
-        hot = np.empty(tuple(self.hot.shape), np.int32)
-        for b in range(B):
+    @torch.inference_mode()
+    def prefill_slot(self, model, b, prompt, observer=None):
+        """Admit one prompt into the empty slot ``b`` (its policy groups already reserved,
+        the engine's admission): the prefill of ``prefill`` for that request, its pages
+        placed by the policy, then its tables from the plan (and the resident entries of
+        other slots whose blocks this prefill reclaimed).  Returns the first token
+        (device scalar)."""
+        if self.plan is None:
+            raise ValueError("slot admission needs the policy residency")
+        first = self._prefill_request(model, b, prompt, 0.0, 0, observer)
+        self._tables_from_plan(slots=[b])
+        return first
+
+    def _prefill_request(self, model, b, prompt, resident_fraction, seed, observer):
+        from torch.nn.attention import SDPBackend, sdpa_kernel
+
+        cfg = model.config
+        groups = cfg.num_attention_heads // cfg.num_key_value_heads
+        P = self.config.page_size
+        tokens = torch.as_tensor(prompt, device=self.device)
+        used = ceil(len(tokens) / P)
+        if len(tokens) > self.pages * P:
+            raise ValueError("prompt longer than the state's capacity")
+        slots = []
+        if self.plan is None:
+            for l in range(self.layers):
+                pages, blocks = self._place_residents(l, b, used, resident_fraction, seed)
+                row = np.full(used, -1, np.int64)
+                row[pages] = blocks
+                slots.append(row)
+
+        def attend(index, q, k, v):
+            if self.plan is not None:  # the policy places this layer's pages as it writes them
+                self.plan.write((b, index), len(k))
+                slots.append(self.plan.group((b, index)).slot[:used].copy())
+            self.write_prompt(index, b, k, v, slots[index])
+            if observer is not None:
+                observer(index, b, k, v)
+            # [1, heads, tokens, dim]: the fused kernels take 4-D operands only
+            heads_first = lambda t: t.transpose(0, 1).unsqueeze(0).contiguous()  # noqa: E731
+            grouped = lambda t: heads_first(t.repeat_interleave(groups, 1))  # noqa: E731
+            with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
+                out = F.scaled_dot_product_attention(heads_first(q), grouped(k), grouped(v), is_causal=True)
+            return out[0].transpose(0, 1)
+
+        hidden = model._layers(tokens, 0, attend)
+        self.lengths[b] = len(tokens)
+        return model._logits(hidden[-1]).argmax()
+
+    def reset_slot(self, b):
+        """Slot ``b`` empty again (a released request's): no resident page, no hot tag,
+        the LRU in slot order, empty Quest bounds, no history."""
+        self.resident[:, b] = -1
+        self.tags[:, b] = -1
+        self.lru[:, b] = torch.arange(self.hot_rows, dtype=self.lru.dtype, device=self.device)
+        self.minimum[:, b] = float("inf")
+        self.maximum[:, b] = float("-inf")
+        self.lengths[b] = 0
+        for l in range(self.layers):
+            self.tail_block[l][b] = -1
+
+    def _tables_from_plan(self, slots=None):
+        """Resident pages, hot regions and tail blocks of every (l, b) of ``slots``
+        (default: every slot) as the policy left them (pages it detached again hold -1),
+        and the resident entries of other slots' pages it detached meanwhile.  A
+        (request, layer) whose prefill raised no hot demand (fewer pages than the window,
+        the watermark never crossed) takes its region now, request by request (the
+        policy's explicit transition): the decode serves every row it selects outside the
+        resident pages from it."""
+        L, C = self.layers, self.pages
+        slots = list(range(self.batch)) if slots is None else list(slots)
+        for b in slots:
             for l in range(L):
                 if not self.plan.group((b, l)).hot:
                     self.plan.transition(self.plan.group((b, l)))
-        for b in range(B):
+        resident = np.full((L, len(slots), C), -1, np.int32)
+        hot = np.empty((L, len(slots), self.hot.shape[2]), np.int32)
+        for i, b in enumerate(slots):
             for l in range(L):
                 g = self.plan.group((b, l))
-                resident[l, b] = g.slot[:C]
-                hot[l, b] = g.hot
+                held = min(C, len(g.slot))  # the group spans the request's own reservation
+                resident[l, i, :held] = g.slot[:held]
+                hot[l, i] = g.hot
                 self.tail_block[l][b] = int(g.slot[(g.length - 1) // self.config.page_size])
-        self.resident.copy_(torch.from_numpy(resident))
-        self.hot.copy_(torch.from_numpy(hot))
+        index = torch.tensor(slots, device=self.device)
+        self.resident.index_copy_(1, index, torch.from_numpy(resident).to(self.device))
+        self.hot.index_copy_(1, index, torch.from_numpy(hot).to(self.device))
+        others = [(key, page) for key, page in self.plan.detached if key[0] not in slots]
+        if others:
+            rows = torch.tensor([(l, b, page) for (b, l), page in others], dtype=torch.int64).T.to(self.device)
+            self.resident[rows[0], rows[1], rows[2]] = -1
         self.plan.detached.clear()
 
     # -- decode-step bookkeeping ---------------------------------------------------
-    def open_tail_pages(self, positions):
-        """Give every (l, b) whose next token starts a page a resident tail block."""
+    def open_tail_pages(self, positions, order=None):
+        """Give every (l, b) whose next token starts a page a resident tail block, for the
+        requests in ``order`` (default: every slot, in slot order; the policy places the
+        writes in that order)."""
+        rows = list(range(self.batch)) if order is None else list(order)
         if self.plan is not None:
-            self._plan_decode_writes(positions)
+            self._plan_decode_writes(positions, rows)
             return
         P, L = self.config.page_size, self.layers
-        starts = [b for b, pos in enumerate(positions) if pos % P == 0]
+        starts = [b for b in rows if positions[b] % P == 0]
         if not starts:
             return
         if self.next_spare + L * len(starts) > self.blocks:
@@ -364,18 +403,18 @@ class SparseKVState:
         rows = torch.tensor([ls, bs, ps, blocks], dtype=torch.int64, pin_memory=True).to(self.device, non_blocking=True)
         self.resident[rows[0], rows[1], rows[2]] = rows[3].to(torch.int32)
 
-    def _plan_decode_writes(self, positions):
-        """The step's one-token writes through the policy, request by request and layer
-        by layer (the reference engine's order, engine.py:115-128).  A write into a page
-        that has rows changes no placement for a layer whose hot region is served, so
-        such steps only count the rows; a step that opens pages places them, and every
-        page the policy detaches or binds updates the resident table (one pinned upload
-        queued on the current stream)."""
-        L, B, plan = self.layers, self.batch, self.plan
-        if plan.append_within([(b, l) for b in range(B) for l in range(L)]):
+    def _plan_decode_writes(self, positions, rows):
+        """The step's one-token writes through the policy, request by request (``rows``,
+        in the engine's turn order) and layer by layer (the reference engine's order,
+        engine.py:115-128).  A write into a page that has rows changes no placement for a
+        layer whose hot region is served, so such steps only count the rows; a step that
+        opens pages places them, and every page the policy detaches or binds updates the
+        resident table (one pinned upload queued on the current stream)."""
+        L, plan = self.layers, self.plan
+        if plan.append_within([(b, l) for b in rows for l in range(L)]):
             return
         ls, bs, ps, blocks = [], [], [], []
-        for b in range(B):
+        for b in rows:
             for l in range(L):
                 for page, block in plan.write((b, l), 1):
                     self.tail_block[l][b] = int(block)
@@ -504,7 +543,6 @@ class BatchedDecodeEngine:
             self._group_events = [[(torch.cuda.Event(), torch.cuda.Event()) for _ in self.groups]
                                   for _ in range(state.layers)]
             self.group_gather_workgroups = group_gather_workgroups
-            self.current_group = None
         self.transfer = torch.cuda.Stream(self.device) if transfer_stream or prefetch or self.groups else None
         self._pack_projections()
         self._choose_projections(projections)
@@ -513,6 +551,9 @@ class BatchedDecodeEngine:
         # per layer: resolved (compute -> transfer) and gathered (transfer -> compute)
         self._handoff = [(torch.cuda.Event(), torch.cuda.Event()) for _ in range(state.layers)]
         self._step_start = torch.cuda.Event()
+        self._subsets = {}  # sorted slots of a partial batch -> its decoder and buffers
+        self._keep_sink, self._top_pages, self._caps = keep_sink, top_pages, caps
+        self.current_group = None  # (requests, decoder) the observer's arguments belong to
         self._static_buffers()
         self.use_graphs = graphs and all(self.projection_kernel[n] for n in ("qkv", "o_proj", "gate_up", "down"))
         self._graphs = None
@@ -755,14 +796,16 @@ class BatchedDecodeEngine:
         return out
 
     def _append(self, layer, k, v, positions, rows=None, handle=None):
-        """Each request's new K/V row (``rows``: a range of requests, default all), on the
-        stream ``handle`` (default: the current stream)."""
+        """Each request's new K/V row (``rows``: a range of requests, default all, whose rows
+        are those of ``k``/``v``; or a list of slots whose rows are ``k``/``v`` in that
+        order), on the stream ``handle`` (default: the current stream)."""
         st, cfg = self.state, self.state.config
         rows = range(st.batch) if rows is None else rows
+        first = rows.start if isinstance(rows, range) else 0
         dev_rows, host_rows, lo, hi = st.append_args(layer, positions, rows)
         _lib.check(
             _lib.load().hs_append_rows(
-                k[rows.start].data_ptr(), v[rows.start].data_ptr(), k.stride(0), st.pool.data_ptr(),
+                k[first].data_ptr(), v[first].data_ptr(), k.stride(0), st.pool.data_ptr(),
                 st.blocks * cfg.page_size, _lib.dtype_code(cfg.dtype), cfg.page_size, cfg.kv_heads, cfg.head_dim,
                 dev_rows, self._host_alias[layer], host_rows, st.host[layer].shape[0] * cfg.page_size, lo, hi,
                 len(rows), handle if handle is not None else _lib.stream_handle(self.device),
@@ -773,14 +816,20 @@ class BatchedDecodeEngine:
     def check_status(self):
         """Raise if any layer's union overflowed its buffers in a step so far (reads the
         decoders' status flags back to the host: for tests and debugging, not timed runs)."""
-        decoders = [self.dec] + (self.decs or []) + [group for _, group in (self.groups or [])]
+        decoders = [self.dec] + (self.decs or []) + [group for _, group in (self.groups or [])] + [
+            sub[0] for sub in self._subsets.values()]
         for dec in {id(d): d for d in decoders}.values():
             dec.check_status()
 
     @torch.inference_mode()
-    def step(self, tokens, observer=None, timer=None, probe=None):
+    def step(self, tokens, observer=None, timer=None, probe=None, active=None):
         """One decode step for all B requests: `tokens` [B] int64 (device) -> next tokens.
 
+        ``active`` (optional): the slots that decode this step, in the order their writes
+        go through the residency policy (the engine's turn order); the other slots are
+        idle (no append, selection, resolve, gather or attention; their rows of the dense
+        layers and of the returned tokens are not meaningful).  Default: every slot, in
+        slot order.
         ``timer`` (optional list) receives, per layer, the stage events
         ``(layer, {stage: (start, end)}, entries)`` with ``entries`` the layer's
         attention entry total (device tensor) -- for profiling, not for timed runs.
@@ -789,12 +838,17 @@ class BatchedDecodeEngine:
         launch on the stream it runs on (light enough for timed runs: events and a copy of
         the decoder's entry counts).
         """
+        order = None
+        if active is not None:
+            order = [int(b) for b in active]
+            if sorted(order) != list(range(self.state.batch)):
+                return self._step_subset(tokens, order, observer, timer, probe)
         if self.groups is not None:
-            return self._step_groups(tokens, observer, timer, probe)
+            return self._step_groups(tokens, observer, timer, probe, order)
         model, st, dec = self.model, self.state, self.dec
         cfg = model.config
         positions = list(st.lengths)
-        st.open_tail_pages(positions)
+        st.open_tail_pages(positions, order)
         for d in self.decs or (dec,):
             d.set_lengths([p + 1 for p in positions])
         sampled = None
@@ -881,6 +935,7 @@ class BatchedDecodeEngine:
                 probe.after_attend(index, compute, dec)
             marks["attend"].append(mark(compute))
             if observer is not None:
+                self.current_group = (range(st.batch), dec)
                 observer(index, q, k, v, out)
             if index == L - 1:  # the last layer's o_proj and MLP
                 marks["dense_last"] = [marks["attend"][1]]
@@ -899,7 +954,115 @@ class BatchedDecodeEngine:
             self._capture()
         return tokens
 
-    def _step_groups(self, tokens, observer=None, timer=None, probe=None):
+    def _subset(self, slots):
+        """Decoder and compact buffers of the partial batch ``slots`` (sorted), built on
+        first use (a few per run: admissions and finishes change the running set)."""
+        key = tuple(slots)
+        sub = self._subsets.get(key)
+        if sub is None:
+            st, cfg = self.state, self.model.config
+            if len(self._subsets) >= 8:  # keep the latest few
+                self._subsets.pop(next(iter(self._subsets)))
+            dec = BatchedSparseDecode(
+                st.config, cfg.num_attention_heads, self._top_pages, [max(1, st.lengths[b]) for b in slots],
+                keep_sink=self._keep_sink, device=self.device, capacity_lengths=[self._caps[b] for b in slots],
+                shared_selection=self.selector == "uniform", workspaces_from=self.dec,
+            )
+            index = torch.tensor(slots, dtype=torch.int64, device=self.device)
+            n, dt, dev = len(slots), self.model.dtype, self.device
+            Hq, Hkv, D = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
+            buffers = tuple(torch.empty(shape, dtype=dt, device=dev)
+                            for shape in ((n, Hq, D), (n, Hkv, D), (n, Hkv, D), (n, Hq, D)))
+            sub = self._subsets[key] = (dec, index, buffers)
+        return sub
+
+    def _step_subset(self, tokens, order, observer=None, timer=None, probe=None):
+        """A decode step of the slots in ``order`` only (the others idle): the dense
+        layers run for the whole batch (their cost is the weights, read once either way),
+        the sparse stages for the decoding slots, gathered into compact buffers, in layer
+        order on the compute stream."""
+        model, st = self.model, self.state
+        cfg = model.config
+        slots = sorted(order)
+        dec, index, (q, k, v, out) = self._subset(slots)
+        positions = list(st.lengths)
+        st.open_tail_pages(positions, order)
+        dec.set_lengths([positions[b] + 1 for b in slots])
+        sampled = None
+        if self.selector == "uniform":
+            sampled = uniform_pages([positions[b] + 1 for b in slots], st.config.page_size, dec.top, st.layers,
+                                    self._sampler, self.device)
+        compute = torch.cuda.current_stream(self.device)
+        handle = _lib.stream_handle(self.device)
+        if self._prepared is None:
+            self._prepared = self._prepare_boundaries()
+        L = st.layers
+
+        def mark(stream):
+            if timer is None:
+                return None
+            event = torch.cuda.Event(enable_timing=True)
+            event.record(stream)
+            return event
+
+        self._x.copy_(model.model.embed_tokens(tokens))
+        for layer in range(L):
+            marks = {"dense": [mark(compute)]}
+            for launch in self._prepared[layer]:
+                launch(handle)
+            torch.index_select(self._q, 0, index, out=q)
+            torch.index_select(self._k, 0, index, out=k)
+            torch.index_select(self._v, 0, index, out=v)
+            marks["dense"].append(mark(compute))
+            marks["append"] = [marks["dense"][1]]
+            self._append(layer, k, v, positions, slots, handle=handle)
+            marks["append"].append(mark(compute))
+            marks["select"] = [marks["append"][1]]
+            if sampled is None:
+                lo, hi = st.bounds[layer]
+                dec.select(q, [lo[b] for b in slots], [hi[b] for b in slots], stream=handle)
+            else:
+                dec.select_pages(sampled[layer], stream=handle, validate=False)
+            marks["select"].append(mark(compute))
+            marks["resolve"] = [marks["select"][1]]
+            dec.resolve([st.tables[layer][b] for b in slots], row_stats=st.row_stats, stream=handle)
+            marks["resolve"].append(mark(compute))
+            marks["gather"] = [marks["resolve"][1]]
+            dec.gather(st.alias[layer], st.pool, handle)
+            marks["gather"].append(mark(compute))
+            marks["attend"] = [marks["gather"][1]]
+            if probe is not None:
+                probe.before_attend(layer, compute, dec)
+            dec.attend(q, st.pool, out=out, stream=handle)
+            if probe is not None:
+                probe.after_attend(layer, compute, dec)
+            marks["attend"].append(mark(compute))
+            self._attn_out.index_copy_(0, index, out)
+            if observer is not None:
+                self.current_group = (slots, dec)
+                observer(layer, q, k, v, out)
+            if layer == L - 1:
+                marks["dense_last"] = [marks["attend"][1]]
+                for launch in self._prepared[L]:
+                    launch(handle)
+                marks["dense_last"].append(mark(compute))
+            if timer is not None:
+                timer.append((layer, marks, dec.entry_counts.sum(), dec.row_counts[:, 2].sum()))
+        logits = self._project(
+            "lm_head", add_rms_norm(self._x, self._delta, model.model.norm.weight, cfg.rms_norm_eps),
+            model.lm_head.weight,
+        )
+        tokens = logits.argmax(-1)
+        for b in slots:
+            st.lengths[b] = positions[b] + 1
+        self.positions.index_add_(0, index, torch.ones_like(index))
+        return tokens
+
+    def reset_slot(self, b, length):
+        """Slot ``b`` holds a new request with a ``length``-token history (its prefill)."""
+        self.positions[b] = length
+
+    def _step_groups(self, tokens, observer=None, timer=None, probe=None, order=None):
         """A decode step with the batch split into request groups pipelined over layers.
 
         Compute-stream order: for each layer and group, the group's pending attention of
@@ -912,7 +1075,7 @@ class BatchedDecodeEngine:
         model, st = self.model, self.state
         cfg = model.config
         positions = list(st.lengths)
-        st.open_tail_pages(positions)
+        st.open_tail_pages(positions, order)
         for rows, dec in self.groups:
             dec.set_lengths([positions[b] + 1 for b in rows])
         compute, transfer = torch.cuda.current_stream(self.device), self.transfer

@@ -210,6 +210,30 @@ __device__ __noinline__ unsigned long long partial_reread(const unsigned long lo
   return w;
 }
 
+// Fold a batch of partials (m = -inf: none) into the running (M, L, O): the batch's
+// maximum, the running sums rescaled to it, then the batch's terms in order.
+template <int MS>
+__device__ __forceinline__ void fold_partials(const float (&ms)[MS], const float (&ls)[MS], const float (&os)[MS],
+                                              float& M, float& L, float& O) {
+  float Mc = M;
+#pragma unroll
+  for (int u = 0; u < MS; ++u) Mc = fmaxf(Mc, ms[u]);
+  if (Mc == -INFINITY) return;
+  if (M != -INFINITY && M != Mc) {
+    const float r = __expf(M - Mc);
+    L *= r;
+    O *= r;
+  }
+#pragma unroll
+  for (int u = 0; u < MS; ++u) {
+    if (ms[u] == -INFINITY) continue;
+    const float f = __expf(ms[u] - Mc);
+    L += f * ls[u];
+    O += f * os[u];
+  }
+  M = Mc;
+}
+
 // Combine n split-K partials (m, l, acc[d]) of one head, partial u at
 // base + u * stride.  Partials are read MS at a time, every load issued before
 // any is used (one round of loads per MS partials); chunks after the first
@@ -252,23 +276,7 @@ __device__ __forceinline__ void merge_partials_by(const unsigned long long* part
       ls[u] = partial_value(wl[u]);
       os[u] = partial_value(wo[u]);
     }
-    float Mc = M;
-#pragma unroll
-    for (int u = 0; u < MS; ++u) Mc = fmaxf(Mc, ms[u]);
-    if (Mc == -INFINITY) continue;
-    if (M != -INFINITY && M != Mc) {
-      const float r = __expf(M - Mc);
-      L *= r;
-      O *= r;
-    }
-#pragma unroll
-    for (int u = 0; u < MS; ++u) {
-      if (ms[u] == -INFINITY) continue;
-      const float f = __expf(ms[u] - Mc);
-      L += f * ls[u];
-      O += f * os[u];
-    }
-    M = Mc;
+    fold_partials<MS>(ms, ls, os, M, L, O);
   }
 }
 
@@ -284,6 +292,88 @@ __device__ __forceinline__ void merge_partials(const unsigned long long* part_m,
   if (n <= 4) merge_partials_by<TAGGED, 4>(part_m, part_l, part_o, base, stride, n, d, D, tag, M, L, O);
   else if (n <= 8) merge_partials_by<TAGGED, 8>(part_m, part_l, part_o, base, stride, n, d, D, tag, M, L, O);
   else merge_partials_by<TAGGED, 16>(part_m, part_l, part_o, base, stride, n, d, D, tag, M, L, O);
+}
+
+// The merging workgroup's merge of a group of n <= NMAX partials in one round of
+// loads: each thread loads one m or l word of the group (a (partial, head) pair,
+// passed to every thread of that head through LDS) and the o words of its (head, d)
+// pairs, PT per thread, all before the first use, then folds them exactly as
+// merge_partials_by does (one batch).  `widx(head, u)` is the word index of head
+// `head` of the chunk in partial u; `hc` heads are real; s_ml holds 2 * NMAX * 16
+// floats.
+template <int DT, int NTH, int NMAX, int PT, typename W>
+__device__ __forceinline__ void merge_group_round(const AttendArgs& a, W widx, int hc, int64_t n, uint32_t tag,
+                                                  float* s_ml, int64_t out_base) {
+  static_assert(2 * NMAX * 16 <= NTH, "one m or l word per thread");
+  const int D = static_cast<int>(a.D);
+  const int which = threadIdx.x / (NMAX * 16);
+  const int rem = threadIdx.x % (NMAX * 16);
+  const int mu = rem / 16, mhead = rem % 16;
+  const bool ml_ok = which < 2 && mu < n && mhead < hc;
+  const unsigned long long* ml_part = which == 0 ? a.part_m : a.part_l;
+  const int64_t ml_at = ml_ok ? widx(mhead, mu) : widx(0, 0);
+  unsigned long long wml = partial_load<true>(ml_part + ml_at);
+  const int pairs = hc * D;
+  // only the loads of pairs and partials that exist: both conditions are the same for
+  // every thread of the workgroup but the last pair round's, so the loads of a thread
+  // still go out together (the merge moves splits x pairs words through one CU)
+  unsigned long long wo[PT][NMAX];
+#pragma unroll
+  for (int p = 0; p < PT; ++p) {
+    if (p * NTH >= pairs) continue;
+    const int pair = threadIdx.x + p * NTH;
+    const bool ok = pair < pairs;
+    const int head = ok ? pair / D : 0, d = ok ? pair % D : 0;
+#pragma unroll
+    for (int u = 0; u < NMAX; ++u) {
+      wo[p][u] = 0;
+      if (u < n) wo[p][u] = partial_load<true>(a.part_o + widx(head, u) * D + d);
+    }
+  }
+  if (ml_ok && static_cast<uint32_t>(wml >> 32) != tag) wml = partial_reread(ml_part + ml_at, tag);
+#pragma unroll
+  for (int p = 0; p < PT; ++p) {
+    const int pair = threadIdx.x + p * NTH;
+    if (pair >= pairs) continue;
+    const int head = pair / D, d = pair % D;
+#pragma unroll
+    for (int u = 0; u < NMAX; ++u)
+      if (u < n && static_cast<uint32_t>(wo[p][u] >> 32) != tag)
+        wo[p][u] = partial_reread(a.part_o + widx(head, u) * D + d, tag);
+  }
+  if (ml_ok) s_ml[(which * NMAX + mu) * 16 + mhead] = partial_value(wml);
+  __syncthreads();
+#pragma unroll
+  for (int p = 0; p < PT; ++p) {
+    const int pair = threadIdx.x + p * NTH;
+    if (pair >= pairs) continue;
+    const int head = pair / D, d = pair % D;
+    float ms[NMAX], ls[NMAX], os[NMAX];
+#pragma unroll
+    for (int u = 0; u < NMAX; ++u) {
+      ms[u] = u < n ? s_ml[u * 16 + head] : -INFINITY;
+      ls[u] = u < n ? s_ml[(NMAX + u) * 16 + head] : 0.f;
+      os[u] = partial_value(wo[p][u]);
+    }
+    float M = -INFINITY, L = 0.f, O = 0.f;
+    fold_partials<NMAX>(ms, ls, os, M, L, O);
+    store_elem<DT>(a.out, out_base + head * a.o_sh + d, L > 0.f ? O / L : 0.f);
+  }
+}
+
+// The same merge for more than 16 partials (the balanced schedule's long lists): the
+// (head, d) pairs one after another, merge_partials batches of 16 partials each.
+template <int DT, int NTH, typename W>
+__device__ __forceinline__ void merge_group_pairs(const AttendArgs& a, W widx, int hc, int64_t n, uint32_t tag,
+                                                  int64_t out_base) {
+  const int D = static_cast<int>(a.D);
+  for (int pair = threadIdx.x; pair < hc * D; pair += NTH) {
+    const int head = pair / D, d = pair % D;
+    const int64_t base = widx(head, 0), stride = widx(head, 1) - base;
+    float M, L, O;
+    merge_partials<true>(a.part_m, a.part_l, a.part_o, base, stride, n, d, D, tag, M, L, O);
+    store_elem<DT>(a.out, out_base + head * a.o_sh + d, L > 0.f ? O / L : 0.f);
+  }
 }
 
 // Arrival counter of a (request, KV head, head chunk) group: bits 63-32 the
@@ -900,34 +990,33 @@ __global__ __launch_bounds__(64 * attend_waves(DP)) void attend_mfma_kernel(Atte
   if (!a.fuse) return;
 
   // The group's last workgroup merges every partial of the group and writes the
-  // output.  Every wave waits for its partial stores to complete before the
-  // barrier, so they are in place when the arrival is counted; the last workgroup
-  // reads them as tagged words (merge_partials).
-  __builtin_amdgcn_s_waitcnt(0);
+  // output.  It takes each partial word once the word carries the tag (partial_word),
+  // so the arrival need not wait for this workgroup's partial stores to complete: the
+  // stores and the arrival travel together (one memory round trip fewer on the
+  // launch's critical path), and a word the merger reads before its store has landed
+  // is read again.  The barrier orders every wave's stores before the arrival.
   __syncthreads();
   unsigned long long* counter = a.arrivals + (b * Hkv + k) * a.head_chunks + hchunk;
   if (threadIdx.x == 0) s_last = arrive_last(counter, a.epoch, parts) ? 1 : 0;
   __syncthreads();
   if (!s_last) return;
-  auto head_base = [&](int head, int hl, int64_t& base, int64_t& stride) {
-    if constexpr (SCHED) {
-      base = first_slot * 16 + head;
-      stride = 16;
-    } else {
-      base = (b * a.Hq + k * a.g + hl) * a.splits;
-      stride = 1;
-    }
+  const uint32_t tag = group_tag(a.epoch, round);
+  const int hc = a.g - 16 * hchunk < 16 ? static_cast<int>(a.g - 16 * hchunk) : 16;  // heads of the chunk
+  const int64_t out_base = b * a.o_sb + (k * a.g + 16 * hchunk) * a.o_sh;
+  auto widx = [&](int head, int64_t u) -> int64_t {  // word of head `head` of the chunk in partial u
+    if constexpr (SCHED) return (first_slot + u) * 16 + head;
+    else return (b * a.Hq + k * a.g + 16 * hchunk + head) * a.splits + u;
   };
-  for (int idx = threadIdx.x; idx < 16 * DP; idx += NTH) {
-    const int head = idx / DP, d = idx % DP;
-    const int hl = 16 * hchunk + head;
-    if (hl >= a.g || d >= D) continue;
-    int64_t base, stride;
-    head_base(head, hl, base, stride);
-    float M, L, O;
-    merge_partials<true>(a.part_m, a.part_l, a.part_o, base, stride, parts, d, D, group_tag(a.epoch, round), M, L,
-                         O);
-    store_elem<DT>(a.out, b * a.o_sb + (k * a.g + hl) * a.o_sh + d, L > 0.f ? O / L : 0.f);
+  constexpr int PT = (16 * DP + NTH - 1) / NTH;  // (head, d) pairs per thread
+  float* s_ml = reinterpret_cast<float*>(smem);  // free again: the partials are stored
+  if (parts <= 4) {
+    merge_group_round<DT, NTH, 4, PT>(a, widx, hc, parts, tag, s_ml, out_base);
+  } else if (parts <= 8) {
+    merge_group_round<DT, NTH, 8, PT>(a, widx, hc, parts, tag, s_ml, out_base);
+  } else if (parts <= 16) {
+    merge_group_round<DT, NTH, 16, PT>(a, widx, hc, parts, tag, s_ml, out_base);
+  } else {
+    merge_group_pairs<DT, NTH>(a, widx, hc, parts, tag, out_base);
   }
   if (threadIdx.x == 0)  // the next replay of this launch counts from zero in the next round
     __hip_atomic_store(counter,
