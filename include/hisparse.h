@@ -169,6 +169,10 @@ typedef struct hs_resolve_desc {
   int64_t* counts;              /* out [3]: resident hits, hot hits, misses */
   int64_t* row_stats;           /* nullable [3]: counts are added here (hybrid.py:454) */
   void* workspace;              /* set by the library from the call's workspace */
+  int32_t miss_prefix_only;     /* 1 = write the miss plan's compact prefix only (entries
+                                   [0, counts[2])), not its -1 tail: for a caller whose gather
+                                   stops at the miss count; 0 = the whole RowPlan */
+  int32_t reserved;             /* 0 */
 } hs_resolve_desc;
 
 /* Scratch bytes for one descriptor (sum them for a batch). */

@@ -50,6 +50,8 @@ class ResolveDesc(ctypes.Structure):
         ("counts", c_void_p),
         ("row_stats", c_void_p),
         ("workspace", c_void_p),
+        ("miss_prefix_only", c_int32),
+        ("reserved", c_int32),
     ]
 
 

@@ -255,6 +255,7 @@ class BatchedSparseDecode:
             d.physical = self.physical[b].data_ptr() if self.head_rows else d.union_physical
             d.miss_host_rows = self.miss_host[b].data_ptr()
             d.miss_device_rows = self.miss_device[b].data_ptr()
+            d.miss_prefix_only = 1  # the gather stops at the miss count: no -1 tail
             d.counts = self.row_counts[b].data_ptr()
             total += lib.hs_resolve_workspace_bytes(self.capacity, self.capacity_lengths[b], d.n_pages, d.hot_rows)
         if total > self.resolve_ws_bytes:

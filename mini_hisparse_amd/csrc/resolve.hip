@@ -796,7 +796,7 @@ __global__ __launch_bounds__(RW) void resolve_outputs_kernel(ResolveBatch batch)
       d.miss_device_rows[rank] = r;
       if (r >= 0 && (rank < S - 1 || rank == tot_miss - 1)) d.tags[slot] = static_cast<int32_t>(host);
     }
-    if (e >= tot_miss) {
+    if (e >= tot_miss && !d.miss_prefix_only) {  // the RowPlan's -1 tail
       d.miss_host_rows[e] = -1;
       d.miss_device_rows[e] = -1;
     }
@@ -844,6 +844,7 @@ static int validate_desc(const hs_resolve_desc& d) {
   HS_CHECK_ARG(d.length <= d.n_pages * d.page_size, "length exceeds the page tables");
   HS_CHECK_ARG(d.hot_rows >= 1 && d.hot_rows <= RT * LRU_CHUNK, "hot_rows must be in [1, 32768]");
   HS_CHECK_ARG(d.lru_i16 == 0 || d.lru_i16 == 1, "lru_i16 must be 0 or 1");
+  HS_CHECK_ARG(d.miss_prefix_only == 0 || d.miss_prefix_only == 1, "miss_prefix_only must be 0 or 1");
   if (d.lru_i16)  // the front launch reads an int16 LRU as 32-bit pairs
     HS_CHECK_ARG(d.hot_rows % 2 == 0 && (reinterpret_cast<uintptr_t>(d.lru) & 3) == 0,
                  "an int16 LRU needs an even hot_rows and 4-byte alignment");

@@ -213,13 +213,14 @@ def test_resolver_batched_descriptors_match_oracle(gpu, lru_dtype):
         t["lru"] = t["lru"].to(lru_dtype)
         pos = torch.from_numpy(positions).to(gpu)
         n = pos.numel()
-        out = {name: torch.empty(n, dtype=torch.int64, device=gpu) for name in ("phys", "uphys", "mh", "md")}
+        out = {name: torch.full((n,), -7, dtype=torch.int64, device=gpu) for name in ("phys", "uphys", "mh", "md")}
         out["counts"] = torch.empty(3, dtype=torch.int64, device=gpu)
         d.positions, d.n, d.positions_i64 = pos.data_ptr(), n, 1
         d.source, d.resident, d.n_pages = t["source"].data_ptr(), t["resident"].data_ptr(), t["source"].numel()
         d.hot, d.hot_blocks = t["hot"].data_ptr(), t["hot"].numel()
         d.tags, d.lru, d.hot_rows = t["tags"].data_ptr(), t["lru"].data_ptr(), t["tags"].numel()
         d.lru_i16 = int(lru_dtype == torch.int16)
+        d.miss_prefix_only = len(keep) % 2  # every other descriptor: the plan's prefix only
         d.length, d.page_size = length, P
         d.physical, d.union_physical = out["phys"].data_ptr(), out["uphys"].data_ptr()
         d.miss_host_rows, d.miss_device_rows = out["mh"].data_ptr(), out["md"].data_ptr()
@@ -235,8 +236,14 @@ def test_resolver_batched_descriptors_match_oracle(gpu, lru_dtype):
             positions, *[tables[k] for k in ("source", "resident", "hot", "tags", "lru")], length, P)
         case = f"descriptor {i}: length {length}, page {P}, hot rows {tables['tags'].size}"
         np.testing.assert_array_equal(out["phys"].cpu().numpy(), phys, err_msg=case)
-        np.testing.assert_array_equal(out["mh"].cpu().numpy(), mh, err_msg=case)
-        np.testing.assert_array_equal(out["md"].cpu().numpy(), md, err_msg=case)
+        if i % 2:  # miss_prefix_only: the compact prefix, and the -1 tail left unwritten
+            m = int(counts[2])
+            np.testing.assert_array_equal(out["mh"][:m].cpu().numpy(), mh[:m], err_msg=case)
+            np.testing.assert_array_equal(out["md"][:m].cpu().numpy(), md[:m], err_msg=case)
+            assert (out["mh"][m:] == -7).all() and (out["md"][m:] == -7).all(), case
+        else:
+            np.testing.assert_array_equal(out["mh"].cpu().numpy(), mh, err_msg=case)
+            np.testing.assert_array_equal(out["md"].cpu().numpy(), md, err_msg=case)
         np.testing.assert_array_equal(out["counts"].cpu().numpy(), counts, err_msg=case)
         np.testing.assert_array_equal(t["tags"].cpu().numpy(), tags_after, err_msg=case)
         np.testing.assert_array_equal(t["lru"].cpu().numpy(), lru_after, err_msg=case)
