@@ -782,9 +782,9 @@ def summarize_layer_trace(trace_dir, args):
 
 def summarize_trace(trace_dir, args):
     """Per-kernel dispatches and durations over the timed steps of a model workload's
-    kernel trace.  Every decode step ends with the greedy argmax over the logits, so the
-    timed region runs from the kernel after the warmup-th decode argmax to the (warmup +
-    steps)-th; it must hold layers x steps x groups attention launches."""
+    kernel trace: the kernels between the first two spin kernels (``_time_steps``'s
+    markers) after the first decode attention; they must be layers x steps x groups
+    attention launches."""
     import csv
     import glob
     from collections import defaultdict
@@ -794,14 +794,12 @@ def summarize_trace(trace_dir, args):
     wl = WORKLOADS[args.workload]
     (path,) = glob.glob(os.path.join(trace_dir, "*kernel_trace.csv"))
     rows = sorted(csv.DictReader(open(path)), key=lambda r: int(r["Start_Timestamp"]))
-    # the prefill's argmaxes (one per prompt) come before the first decode attention
     first = next(i for i, r in enumerate(rows) if "attend_mfma_kernel" in r["Kernel_Name"])
-    ends = [i for i, r in enumerate(rows) if i > first and "ArgMaxOps" in r["Kernel_Name"]]
+    marks = [i for i, r in enumerate(rows) if i > first and "spin_kernel" in r["Kernel_Name"]]
     L = wl.layers
-    if len(ends) < args.warmup + args.steps:
-        raise SystemExit(f"trace holds {len(ends)} decode steps, warmup + steps need {args.warmup + args.steps}")
-    start = ends[args.warmup - 1] + 1 if args.warmup else 0
-    window = rows[start : ends[args.warmup + args.steps - 1] + 1]
+    if len(marks) < 2:
+        raise SystemExit("the trace holds no marked timed region (spin kernels around it)")
+    window = rows[marks[0] + 1 : marks[1]]
     groups = args.request_groups if args.request_groups is not None else DEFAULT_REQUEST_GROUPS.get(args.workload, 1)
     launches = sum("attend_mfma_kernel" in r["Kernel_Name"] for r in window)
     if launches != L * args.steps * groups:
@@ -1071,45 +1069,55 @@ class KernelTimer:
 
 class AttendProbe:
     """Timing of every attention launch of the timed steps: its kernels' own duration
-    (``KernelTimer``), plus a device copy of each launch's entry counts (the rows each
-    (request, KV head) reads), from which the launch's algorithmic bytes follow.  Events
-    and the count buffer are allocated before the timed region; per launch the probe
-    adds one 32-byte device copy to the step."""
+    (``KernelTimer``), and the launch's algorithmic bytes from the union launches' own
+    entry total (``BatchedDecodeEngine.set_entry_stats``: the union builder adds its
+    entry counts to a device counter, so the probe puts no copy into the step) plus
+    the per-launch row lists, queries and outputs, known on the host."""
 
-    def __init__(self, torch, device, launches, batch, kv_heads):
+    def __init__(self, torch, device, launches, engine):
         self.torch = torch
+        self.engine = engine
         self.kernel = KernelTimer(torch, launches)
-        self.counts = torch.zeros((launches, batch * kv_heads), dtype=torch.int32, device=device)
+        self.entries = torch.zeros(1, dtype=torch.int64, device=device)
         self.widths = []
         self.i = 0
+
+    def __enter__(self):
+        self.engine.set_entry_stats(self.entries)
+        return self
+
+    def __exit__(self, *exc):
+        self.engine.set_entry_stats(None)
 
     def before_attend(self, layer, stream, dec):
         self.kernel.arm(self.i)
 
     def after_attend(self, layer, stream, dec):
-        counts = dec.entry_counts.view(-1)  # the launch's requests (a request group's, when pipelined)
-        self.counts[self.i, : counts.numel()].copy_(counts)
         self.widths.append((dec.width, dec.batch))
         self.i += 1
 
-    def totals(self, bytes_of):
-        """(kernel ms, algorithmic bytes, launches), totals over the launches;
-        ``bytes_of(entries, width, batch)`` gives one launch's bytes."""
+    def totals(self, entry_bytes, launch_bytes):
+        """(kernel ms, algorithmic bytes, launches) over the launches: ``entry_bytes`` per
+        entry read, ``launch_bytes(width, batch)`` per launch."""
         n = self.i
         kernel_ms = sum(self.kernel.ms(i) for i in range(n))
-        entries = self.counts[:n].sum(1).tolist()
-        nbytes = sum(bytes_of(e, w, b) for e, (w, b) in zip(entries, self.widths))
+        nbytes = int(self.entries.item()) * entry_bytes + sum(launch_bytes(w, b) for w, b in self.widths)
         return kernel_ms, nbytes, n
 
 
 def _time_steps(torch, run, steps):
-    """Wall time of ``steps`` calls of ``run`` between two device synchronisations."""
+    """Wall time of ``steps`` calls of ``run`` between two device synchronisations.  A
+    short spin kernel before and after the region (outside the timing) marks it in
+    kernel traces (``summarize_trace``)."""
+    torch.cuda._sleep(100)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(steps):
         run()
     torch.cuda.synchronize()
-    return time.perf_counter() - t0
+    elapsed = time.perf_counter() - t0
+    torch.cuda._sleep(100)
+    return elapsed
 
 
 def run_model_workload(args, torch, device):
@@ -1217,8 +1225,8 @@ def run_model_workload(args, torch, device):
     print("[bench] timing", file=sys.stderr, flush=True)
     stats0 = state.row_stats.clone()
     launches = args.steps * wl.layers * (len(engine.groups) if engine.groups else 1)
-    probe = AttendProbe(torch, device, launches, wl.batch, wl.kv_heads)
-    elapsed = _time_steps(torch, lambda: step(probe=probe), args.steps)
+    with AttendProbe(torch, device, launches, engine) as probe:
+        elapsed = _time_steps(torch, lambda: step(probe=probe), args.steps)
     ms_per_step = elapsed * 1e3 / args.steps
     rows = ((state.row_stats - stats0).double() / args.steps).tolist()
     in_order = None
@@ -1226,10 +1234,10 @@ def run_model_workload(args, torch, device):
         # the same attention with the batch in one group and no gather running beside it:
         # two extra steps in layer order, outside the timed region
         groups_saved, engine.groups = engine.groups, None
-        in_order = AttendProbe(torch, device, 2 * wl.layers, wl.batch, wl.kv_heads)
-        for _ in range(2):
-            step(probe=in_order)
-        torch.cuda.synchronize()
+        with AttendProbe(torch, device, 2 * wl.layers, engine) as in_order:
+            for _ in range(2):
+                step(probe=in_order)
+            torch.cuda.synchronize()
         engine.groups = groups_saved
     timer = []
     step(timer=timer)  # profiled step, outside the timed region
@@ -1256,15 +1264,16 @@ def run_model_workload(args, torch, device):
     misses = sum(int(m) for _, _, _, m in timer)
     e, D, Hq, B, L = 2, wl.head_dim, wl.heads, wl.batch, wl.layers
 
-    def launch_bytes(entries, width, batch):
-        # union-deduplicated K/V rows + the per-head row lists + queries and outputs
-        return entries * 2 * D * e + 8 * Hq * width * batch + 2 * Hq * D * e * batch
+    def launch_bytes(width, batch):
+        # beside the union-deduplicated K/V rows (2 D e per entry): the per-head row
+        # lists, the queries and the outputs
+        return 8 * Hq * width * batch + 2 * Hq * D * e * batch
 
-    att_ms, att_bytes, launches = probe.totals(launch_bytes)
+    att_ms, att_bytes, launches = probe.totals(2 * D * e, launch_bytes)
     att_gbs = att_bytes / (att_ms * 1e-3) / 1e9
     solo_line = None
     if in_order is not None:
-        solo_ms, solo_bytes, solo_n = in_order.totals(launch_bytes)
+        solo_ms, solo_bytes, solo_n = in_order.totals(2 * D * e, launch_bytes)
         solo_gbs = solo_bytes / (solo_ms * 1e-3) / 1e9
         solo_line = {"achieved": solo_gbs, "frac": solo_gbs / HBM_PEAK_GBS, "launches": solo_n,
                      "bytes_per_launch": solo_bytes / solo_n, "us_per_launch": solo_ms * 1e3 / solo_n,

@@ -127,6 +127,10 @@ int hs_quest_topk(const void* query, int64_t q_stride_b, int64_t q_stride_h,
  *                 unless the union overflowed (status bit 1).  No counterpart
  *                 in the reference: it lets the resolver skip reading the
  *                 positions (hs_resolve_desc.page_bits).
+ *   entry_stats   nullable int64 [1]: the (clamped) entry counts of the call are
+ *                 added here on the device, so a caller can total the entries its
+ *                 attention reads over many steps without a copy per call (the
+ *                 attention's algorithmic bytes).  No counterpart in the reference.
  * Any batch size: launched in chunks of at most 16 requests, in order on `stream`.
  */
 int hs_build_union(const int32_t* pages, int64_t p_stride_b, int64_t top, const int64_t* lengths,
@@ -134,7 +138,8 @@ int hs_build_union(const int32_t* pages, int64_t p_stride_b, int64_t top, const 
                    int32_t* positions, int64_t pos_capacity, int64_t* head_columns, int64_t width,
                    int32_t* union_count, int32_t* entry_columns, uint32_t* entry_masks,
                    int64_t entry_capacity, int32_t* entry_counts, int32_t* status,
-                   uint32_t* page_bits, int64_t page_bits_stride, hs_stream_t stream);
+                   uint32_t* page_bits, int64_t page_bits_stride, int64_t* entry_stats,
+                   hs_stream_t stream);
 
 /* ------------------------------------------------------------- (2) resolver */
 

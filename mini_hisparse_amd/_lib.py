@@ -74,7 +74,7 @@ SIGNATURES = {
         c_int,
         [c_void_p, c_int64, c_int64, POINTER(c_int64), c_int64, c_int64, c_int64, c_int64,
          c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_void_p, c_void_p, c_int64,
-         c_void_p, c_void_p, c_void_p, c_int64, c_void_p],
+         c_void_p, c_void_p, c_void_p, c_int64, c_void_p, c_void_p],
     ),
     "hs_resolve_workspace_bytes": (c_int64, [c_int64, c_int64, c_int64, c_int64]),
     "hs_resolve_rows": (c_int, [POINTER(ResolveDesc), c_void_p, c_int64, c_void_p]),

@@ -66,6 +66,7 @@ class BatchedSparseDecode:
         leaves them out unless asked."""
         self._workspaces_from = workspaces_from
         self.head_rows = head_rows
+        self.entry_stats = None  # optional int64 [1] device total of the unions' entry counts
         self.config = config
         self.heads = heads
         self.kv_heads = config.kv_heads
@@ -208,7 +209,7 @@ class BatchedSparseDecode:
                 self.capacity, self.head_columns.data_ptr(), self.width, self.union_count.data_ptr(),
                 self.entry_columns.data_ptr(), self.entry_masks.data_ptr(), self.entry_capacity,
                 self.entry_counts.data_ptr(), self.status.data_ptr(), self.page_bits.data_ptr(),
-                self.page_bits_stride, s,
+                self.page_bits_stride, _lib.ptr(self.entry_stats), s,
             ),
             "hs_build_union",
         )

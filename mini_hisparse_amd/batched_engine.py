@@ -813,12 +813,24 @@ class BatchedDecodeEngine:
             "hs_append_rows",
         )
 
+    def decoders(self):
+        """Every decoder the engine has built (whole batch, per layer, request groups,
+        partial batches)."""
+        found = [self.dec] + (self.decs or []) + [group for _, group in (self.groups or [])] + [
+            sub[0] for sub in self._subsets.values()]
+        return list({id(d): d for d in found}.values())
+
+    def set_entry_stats(self, stats):
+        """Total the attention's entry counts of every later step into ``stats`` (int64
+        [1] on the device; None stops), from the union launches themselves."""
+        self._entry_stats = stats
+        for dec in self.decoders():
+            dec.entry_stats = stats
+
     def check_status(self):
         """Raise if any layer's union overflowed its buffers in a step so far (reads the
         decoders' status flags back to the host: for tests and debugging, not timed runs)."""
-        decoders = [self.dec] + (self.decs or []) + [group for _, group in (self.groups or [])] + [
-            sub[0] for sub in self._subsets.values()]
-        for dec in {id(d): d for d in decoders}.values():
+        for dec in self.decoders():
             dec.check_status()
 
     @torch.inference_mode()
@@ -973,6 +985,7 @@ class BatchedDecodeEngine:
             Hq, Hkv, D = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
             buffers = tuple(torch.empty(shape, dtype=dt, device=dev)
                             for shape in ((n, Hq, D), (n, Hkv, D), (n, Hkv, D), (n, Hq, D)))
+            dec.entry_stats = getattr(self, "_entry_stats", None)
             sub = self._subsets[key] = (dec, index, buffers)
         return sub
 

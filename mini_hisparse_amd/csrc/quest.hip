@@ -523,6 +523,7 @@ struct UnionArgs {
   uint32_t* emask;
   int64_t ecap;
   int32_t* ecount;       // [B, Hkv]
+  unsigned long long* estats;  // nullable: the clamped entry counts are added here
   int32_t* status;       // nonzero on overflow
   uint32_t* page_bits;   // nullable [B, pb_stride]: the union's page bitmap
   int64_t pb_stride;
@@ -671,6 +672,7 @@ __global__ __launch_bounds__(UT) void build_union_kernel(UnionArgs a) {
     if (threadIdx.x == 0) {
       a.ecount[b * a.Hkv + kv] = static_cast<int32_t>(E < a.ecap ? E : a.ecap);
       if (E > a.ecap) atomicOr(a.status, 2);
+      if (a.estats) atomicAdd(a.estats, static_cast<unsigned long long>(E < a.ecap ? E : a.ecap));
     }
     if (masks_in_lds) {
       // head bits of each group page, indexed by the page's rank in the group
@@ -872,7 +874,7 @@ static int build_union_chunk(const int32_t* pages, int64_t p_stride_b, int64_t t
                              int32_t* union_count, int32_t* entry_columns,
                              uint32_t* entry_masks, int64_t entry_capacity,
                              int32_t* entry_counts, int32_t* status, uint32_t* page_bits,
-                             int64_t pb_stride, hipStream_t stream) {
+                             int64_t pb_stride, int64_t* entry_stats, hipStream_t stream) {
   HS_CHECK_ARG(batch >= 1 && batch <= QMAXB, "union batch must be in [1, %d]", QMAXB);
   HS_CHECK_ARG(top >= 1 && page_size >= 1 && heads >= 1 && kv_heads >= 1 && heads % kv_heads == 0,
                "invalid union shape");
@@ -910,6 +912,7 @@ static int build_union_chunk(const int32_t* pages, int64_t p_stride_b, int64_t t
   a.emask = entry_masks;
   a.ecap = entry_capacity;
   a.ecount = entry_counts;
+  a.estats = reinterpret_cast<unsigned long long*>(entry_stats);
   a.status = status;
   int64_t max_count = 1;
   for (int64_t i = 0; i < batch; ++i) max_count = std::max(max_count, ceil_div(lengths[i], page_size));
@@ -980,7 +983,7 @@ extern "C" int hs_build_union(const int32_t* pages, int64_t p_stride_b, int64_t 
                               int32_t* union_count, int32_t* entry_columns,
                               uint32_t* entry_masks, int64_t entry_capacity,
                               int32_t* entry_counts, int32_t* status, uint32_t* page_bits,
-                              int64_t page_bits_stride, hipStream_t stream) {
+                              int64_t page_bits_stride, int64_t* entry_stats, hipStream_t stream) {
   HS_CHECK_ARG(batch >= 1, "union batch must be positive");
   HS_CHECK_ARG(top >= 1 && page_size >= 1 && lengths, "invalid union shape");
   HS_CHECK_ARG(heads >= 1 && kv_heads >= 1 && heads % kv_heads == 0, "invalid GQA shape");
@@ -1003,7 +1006,7 @@ extern "C" int hs_build_union(const int32_t* pages, int64_t p_stride_b, int64_t 
         positions + s0 * pos_capacity, pos_capacity, head_columns + s0 * heads * width, width, union_count + s0,
         entry_columns + s0 * kv_heads * entry_capacity, entry_masks + s0 * kv_heads * entry_capacity,
         entry_capacity, entry_counts + s0 * kv_heads, status,
-        page_bits ? page_bits + s0 * page_bits_stride : nullptr, page_bits_stride, stream);
+        page_bits ? page_bits + s0 * page_bits_stride : nullptr, page_bits_stride, entry_stats, stream);
     if (rc != HS_OK) return rc;
   }
   return HS_OK;

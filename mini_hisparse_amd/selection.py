@@ -262,7 +262,7 @@ def build_union(pages, lengths, page_size, kv_heads, top_pages, keep_sink=True, 
     rc = _lib.load().hs_build_union(
         pages.data_ptr(), pages.stride(0), top, length_arr, page_size, batch, heads, kv_heads,
         positions.data_ptr(), capacity, columns.data_ptr(), width, union_count.data_ptr(),
-        ecol.data_ptr(), emask.data_ptr(), entry_cap, ecount.data_ptr(), status.data_ptr(), None, 0,
+        ecol.data_ptr(), emask.data_ptr(), entry_cap, ecount.data_ptr(), status.data_ptr(), None, 0, None,
         _lib.stream_handle(device),
     )
     _lib.check(rc, "hs_build_union")

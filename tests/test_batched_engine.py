@@ -52,9 +52,14 @@ def _engine_layers_match_oracle(gpu, wl, transfer_stream=False, steps=3, built=N
         tokens = torch.arange(1, B + 1, device=gpu)
     unions = 0
 
+    entry_total = torch.zeros(1, dtype=torch.int64, device=gpu)
+    engine.set_entry_stats(entry_total)  # the union launches total their entry counts here
+    entries = []
+
     def observe(l, q, k, v, out):
         rows, dec = engine.current_group if engine.groups else (range(B), engine.decoder(l))
         records.append((l, rows, q.clone(), out.clone(), dec.pages.clone(), dec.union_count.clone()))
+        entries.append(dec.entry_counts.sum())
 
     for step in range(steps):
         records.clear()
@@ -82,6 +87,8 @@ def _engine_layers_match_oracle(gpu, wl, transfer_stream=False, steps=3, built=N
                 assert np.all(np.abs(got - expected) <= 2e-2 + 1e-2 * np.abs(expected)), np.abs(got - expected).max()
                 unions += int(union_count[i])
     engine.check_status()  # no union or entry list was truncated
+    assert int(entry_total.item()) == int(sum(int(x) for x in entries))
+    engine.set_entry_stats(None)
     stats = state.row_stats.tolist()
     assert sum(stats) == unions  # every selected row was a resident hit, a hot hit or a miss
     return stats

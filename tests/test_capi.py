@@ -119,7 +119,7 @@ def test_union_page_bitmap_stride_checked_without_a_gpu():
     lengths = (ctypes.c_int64 * 1)(4096)  # 256 pages: 8 bitmap words
     args = [0x1000, 64, 8, lengths, 16, 1, 8, 2, 0x2000, 4096, 0x3000, 128, 0x4000, 0x5000, 0x6000, 4096,
             0x7000, 0x8000]
-    assert lib.hs_build_union(*args, 0x9000, 7, None) == -1
+    assert lib.hs_build_union(*args, 0x9000, 7, None, None) == -1
     assert b"page bitmap stride" in lib.hs_last_error()
 
 
