@@ -64,6 +64,33 @@ constexpr int MARK_TILE = 512;                // inputs per wave and tile (8 per
 constexpr int MARK_TILE_PAD = MARK_TILE / 8 * 9;
 constexpr uint64_t HASH_EMPTY = ~static_cast<uint64_t>(0);
 
+// Per-thread arrays of the front launch.  Every index into them comes from fully
+// unrolled loops with constant bounds, so after unrolling each one is a constant and
+// the array lives in registers (a non-constant index would put it in scratch, which
+// the build rejects).  Built with HS_REG_CHECK (a CPU-side check, never launched),
+// every access carries a trap for an index outside [0, N); the compiler folds each
+// such test away when the index is a constant inside the range, so a trap left in
+// the front kernel's machine code names an index that can leave its array
+// (tests/test_resolver_registers.py compiles the 16- and 32-slot fronts this way).
+#ifndef HS_REG_CHECK
+#define HS_REG_CHECK 0
+#endif
+__device__ __forceinline__ void reg_check(int i, int n) {
+  if (HS_REG_CHECK && static_cast<unsigned>(i) >= static_cast<unsigned>(n)) __builtin_trap();
+}
+#if HS_REG_CHECK
+template <typename T, int N>
+struct Regs {
+  T r[N];
+  __device__ __forceinline__ T& operator[](int i) {
+    reg_check(i, N);
+    return r[i];
+  }
+};
+#else
+template <typename T, int N>
+using Regs = T[N];  // the shipped build: plain arrays
+#endif
 struct ResolveBatch {
   hs_resolve_desc d[RMAXB];
   int count;
@@ -240,7 +267,7 @@ __global__ __launch_bounds__(RT) void resolve_front_kernel(ResolveBatch batch) {
   // page-bitmap word of token words T + k * RT (one word each: a power-of-two page
   // of at most 32 tokens puts a token word's pages in one bitmap word)
   const bool pb_pre = d.page_bits && POW2 && P <= 32 && wl <= static_cast<int64_t>(RT) * WALK_PRE;
-  uint32_t pbw[WALK_PRE];
+  Regs<uint32_t, WALK_PRE> pbw;
   if (pb_pre) {
 #pragma unroll
     for (int k = 0; k < WALK_PRE; ++k) {
@@ -253,7 +280,7 @@ __global__ __launch_bounds__(RT) void resolve_front_kernel(ResolveBatch batch) {
   // the page tables of short histories are loaded now and used after the token walk
   constexpr int PR = PAGE_REGS;
   const bool pages_early = NP <= static_cast<int64_t>(RT) * PR;
-  int32_t src_e[PR], res_e[PR];  // res_e: only its sign is used
+  Regs<int32_t, PR> src_e, res_e;  // res_e: only its sign is used
   if (pages_early) {
 #pragma unroll
     for (int k = 0; k < PR; ++k) {
@@ -274,8 +301,8 @@ __global__ __launch_bounds__(RT) void resolve_front_kernel(ResolveBatch batch) {
   constexpr int TR = 16;
   constexpr int HALVES = 2;
   constexpr int LROWS = SR / HALVES;
-  int32_t tg[TR];
-  int32_t slot[LROWS];
+  Regs<int32_t, TR> tg;
+  Regs<int32_t, LROWS> slot;
   auto load_tags = [&](int r) {
 #pragma unroll
     for (int kk = 0; kk < TR; ++kk) {
@@ -366,7 +393,7 @@ __global__ __launch_bounds__(RT) void resolve_front_kernel(ResolveBatch batch) {
     constexpr int64_t STEP = static_cast<int64_t>(NWAVES) * MARK_TILE;
     // one loop per position type: a per-load type branch would serialise the loads
     auto walk = [&](const auto* pos) {
-      int64_t nxt[KT];  // the next tile's inputs, loaded while this one is walked
+      Regs<int64_t, KT> nxt;  // the next tile's inputs, loaded while this one is walked
       auto load_tile = [&](int64_t base) {  // unconditional loads (clamped index), then masked
 #pragma unroll
         for (int k = 0; k < KT; ++k) {
@@ -464,7 +491,7 @@ __global__ __launch_bounds__(RT) void resolve_front_kernel(ResolveBatch batch) {
     }
   } else {
     for (int64_t base = T; base < NP; base += static_cast<int64_t>(RT) * MARK_BATCH) {
-      int32_t src[MARK_BATCH], res[MARK_BATCH];
+      Regs<int32_t, MARK_BATCH> src, res;
 #pragma unroll
       for (int k = 0; k < MARK_BATCH; ++k) {
         const int64_t p = base + static_cast<int64_t>(k) * RT;
@@ -540,8 +567,8 @@ __global__ __launch_bounds__(RT) void resolve_front_kernel(ResolveBatch batch) {
       const uint32_t hmask = static_cast<uint32_t>(w.hcap - 1);
 #pragma unroll
       for (int k0 = 0; k0 < TR; k0 += TAG_BATCH) {
-        uint64_t e[TAG_BATCH];
-        uint32_t h[TAG_BATCH], hp[TAG_BATCH];
+        Regs<uint64_t, TAG_BATCH> e;
+        Regs<uint32_t, TAG_BATCH> h, hp;
 #pragma unroll
         for (int j = 0; j < TAG_BATCH; ++j) {  // first probes in flight together
           hp[j] = page_of(static_cast<uint32_t>(tg[k0 + j]));
@@ -563,8 +590,8 @@ __global__ __launch_bounds__(RT) void resolve_front_kernel(ResolveBatch batch) {
 
 #pragma unroll
     for (int k0 = 0; k0 < TR; k0 += MATCH_BATCH) {
-      uint32_t t[MATCH_BATCH], nw[MATCH_BATCH];
-      bool ok[MATCH_BATCH];
+      Regs<uint32_t, MATCH_BATCH> t, nw;
+      Regs<bool, MATCH_BATCH> ok;
 #pragma unroll
       for (int j = 0; j < MATCH_BATCH; ++j) {
         const uint32_t tag = static_cast<uint32_t>(tg[k0 + j]);
@@ -619,7 +646,7 @@ __global__ __launch_bounds__(RT) void resolve_front_kernel(ResolveBatch batch) {
     return static_cast<int64_t>(ex & 0xffffffffull);
   };
   if (wpt <= ORDER_WORDS) {
-    uint32_t miss[ORDER_WORDS];
+    Regs<uint32_t, ORDER_WORDS> miss;
 #pragma unroll
     for (int k = 0; k < ORDER_WORDS; ++k) {
       const int64_t wd = w0 + k;
@@ -658,9 +685,10 @@ __global__ __launch_bounds__(RT) void resolve_front_kernel(ResolveBatch batch) {
   // LRU order over (row, wave, lane, half): ranks inside a wave come from ballots,
   // the counts of every (row, wave) are scanned in row-major order.
   uint32_t protmask = 0u;  // bit HALVES * q + h: that entry is protected
+  static_assert(HALVES * LROWS <= 32, "one protection bit per LRU entry of the thread");
 #pragma unroll
   for (int q0 = 0; q0 < LROWS; q0 += MATCH_BATCH) {
-    uint32_t pw[MATCH_BATCH][HALVES];
+    Regs<Regs<uint32_t, HALVES>, MATCH_BATCH> pw;
 #pragma unroll
     for (int j = 0; j < MATCH_BATCH; ++j) {
 #pragma unroll
@@ -697,7 +725,7 @@ __global__ __launch_bounds__(RT) void resolve_front_kernel(ResolveBatch batch) {
   const int32_t start1 = U - fillU, start2 = U, start3 = S - fillP;
 #pragma unroll
   for (int q = 0; q < LROWS; ++q) {
-    uint64_t up[HALVES];
+    Regs<uint64_t, HALVES> up;
     int32_t r = ucnt[q * NWAVES + wave];  // unprotected entries before the row's first of this lane
 #pragma unroll
     for (int h = 0; h < HALVES; ++h) {
