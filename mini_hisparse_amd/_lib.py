@@ -155,6 +155,7 @@ SIGNATURES = {
 
 _LIB = None
 _LIB_PATH = None
+_LIB_DEFAULT = False  # the loaded copy is the package's own build
 
 
 def load(path: Path | str | None = None):
@@ -163,7 +164,9 @@ def load(path: Path | str | None = None):
     ``path`` names another build of the library; the process holds one copy at most,
     so a path other than the one already loaded is refused (two copies would register
     the same kernels twice with the HIP runtime)."""
-    global _LIB, _LIB_PATH
+    global _LIB, _LIB_PATH, _LIB_DEFAULT
+    if path is None and _LIB_DEFAULT:  # every wrapper call: no filesystem lookup
+        return _LIB
     target = (Path(path) if path is not None else LIBRARY_PATH).resolve()
     if _LIB is not None and target == _LIB_PATH:
         return _LIB
@@ -180,6 +183,7 @@ def load(path: Path | str | None = None):
         fn.restype = restype
         fn.argtypes = argtypes
     _LIB, _LIB_PATH = lib, target
+    _LIB_DEFAULT = target == LIBRARY_PATH.resolve()
     return lib
 
 

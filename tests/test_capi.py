@@ -139,6 +139,19 @@ def test_a_second_copy_of_the_library_is_refused(tmp_path):
     assert _lib.load(_lib.LIBRARY_PATH) is _lib.load()
 
 
+def test_loaded_library_is_returned_without_a_filesystem_lookup(monkeypatch):
+    """Every kernel wrapper calls ``load()`` once per launch: once the package's build is
+    loaded, the call must not resolve paths (a path lookup per launch made a decode step
+    of ~400 launches host-bound)."""
+    lib = _lib.load()
+
+    def no_lookup(self, *args, **kwargs):
+        raise AssertionError("load() looked the library path up again")
+
+    monkeypatch.setattr(_lib.Path, "resolve", no_lookup)
+    assert _lib.load() is lib
+
+
 def test_product_runs_without_the_oracle_or_tests_packages():
     program = dedent("""
         import importlib.abc, sys
