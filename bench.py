@@ -810,8 +810,9 @@ def summarize_trace(trace_dir, args):
         agg[name][0] += 1
         agg[name][1] += int(r["End_Timestamp"]) - int(r["Start_Timestamp"])
     span_ms = (int(window[-1]["End_Timestamp"]) - int(window[0]["Start_Timestamp"])) / 1e6
-    cmd = f"rocprofv3 --kernel-trace --stats -f csv -d <dir> -o bench -- python3 bench.py --workload {args.workload} " \
-          f"--no-microbench --no-cpu-baseline --projections {args.projections} --steps {args.steps} " \
+    path = " --direct" if args.direct else ""  # the engine driven directly, not through the Engine API
+    cmd = f"rocprofv3 --kernel-trace --stats -f csv -d <dir> -o bench -- python3 bench.py --workload {args.workload}" \
+          f"{path} --no-microbench --no-cpu-baseline --projections {args.projections} --steps {args.steps} " \
           f"--warmup {args.warmup}"
     att = [agg[k] for k in agg if k.startswith("hs::attend_mfma_kernel")]
     mrg = [agg[k] for k in agg if k.startswith("hs::attend_merge_kernel")]
@@ -821,7 +822,7 @@ def summarize_trace(trace_dir, args):
         f"# Kernel trace: {wl.name} end to end, timed steps only",
         "",
         f"Command: `{cmd}`",
-        f"Summarised by: `python bench.py --workload {args.workload} --projections {args.projections} "
+        f"Summarised by: `python bench.py --workload {args.workload}{path} --projections {args.projections} "
         f"--steps {args.steps} --warmup {args.warmup} --summarize-trace <dir>`",
         "",
         f"Timed region: {args.steps} steps x {L} layers x {groups} request group(s), {len(window)} dispatches "
