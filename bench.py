@@ -102,6 +102,9 @@ def parse_args():
                    help="model workloads with a prefill: the hybrid policy places pages and hot regions in a slab "
                         "of resident_fraction of the history plus every layer's promised hot region and tails "
                         "(default), or a seeded fixed fraction of each layer's pages is resident")
+    p.add_argument("--resolver-front", choices=("split", "single"), default="split",
+                   help="the resolver's front over several workgroups per request (split, the default) or one "
+                        "(single)")
     p.add_argument("--direct", action="store_true",
                    help="model workloads: prefill every prompt first and time the engine's device-resident "
                         "token loop only, instead of admitting and decoding through the Engine API")
@@ -242,7 +245,8 @@ def build_workload(args, torch, device):
     del kv_pages
     torch.cuda.synchronize()
     cfg = CacheConfig(gpu_pages=blocks, host_pages=B * C, page_size=P, kv_heads=Hkv, head_dim=D, device=device, dtype=torch.bfloat16)
-    dec = BatchedSparseDecode(cfg, S.heads, S.top, [L] * B, device=device)
+    dec = BatchedSparseDecode(cfg, S.heads, S.top, [L] * B, device=device,
+                              split_front=args.resolver_front == "split")  # request b's host pages: b C + page
     pipe = PipelinedSparseDecode(cfg, S.heads, S.top, [L] * B, parts=args.parts, device=device)
     return dict(
         cfg=cfg, dec=dec, pipe=pipe, q=q, kmin=kmin, kmax=kmax, host=host, alias=MappedHost(host), pool=pool,
@@ -1162,6 +1166,7 @@ def run_model_workload(args, torch, device):
     if groups is None:
         groups = DEFAULT_REQUEST_GROUPS.get(args.workload, 1)
     options = dict(seed=args.seed, graphs=args.graphs, projections=args.projections,
+                   resolver_split=args.resolver_front == "split",
                    prefetch=not args.no_prefetch and wl.selector == "uniform",
                    request_groups=groups if wl.selector == "quest" else 1,
                    group_gather_workgroups=args.group_gather_workgroups if args.group_gather_workgroups is not None

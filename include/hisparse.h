@@ -177,7 +177,15 @@ typedef struct hs_resolve_desc {
   int32_t miss_prefix_only;     /* 1 = write the miss plan's compact prefix only (entries
                                    [0, counts[2])), not its -1 tail: for a caller whose gather
                                    stops at the miss count; 0 = the whole RowPlan */
-  int32_t reserved;             /* 0 */
+  int32_t split_front;          /* 1 = the front's work may go over several workgroups per request
+                                   (three launches instead of one; taken for hot regions above 16384
+                                   rows, where it is faster; HS_RESOLVE_SPLIT=0/1 forces it off/on):
+                                   needs page_bits, a power-of-two page_size <= 32 and a source table
+                                   affine with base source[0] (host block = source[0] + page for every
+                                   host-backed page, as a request's contiguous host slots are); a
+                                   table that is not is refused on the device: no row (-1), counts 0.
+                                   Every descriptor of a call shares it.  0 = one workgroup per
+                                   request */
 } hs_resolve_desc;
 
 /* Scratch bytes for one descriptor (sum them for a batch). */

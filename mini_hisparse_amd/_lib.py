@@ -51,7 +51,7 @@ class ResolveDesc(ctypes.Structure):
         ("row_stats", c_void_p),
         ("workspace", c_void_p),
         ("miss_prefix_only", c_int32),
-        ("reserved", c_int32),
+        ("split_front", c_int32),
     ]
 
 

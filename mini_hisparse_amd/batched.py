@@ -52,7 +52,7 @@ class BatchedSparseDecode:
     """Quest -> union -> resolve -> gather -> attention for B requests of one layer."""
 
     def __init__(self, config, heads, top_pages, lengths, *, keep_sink=True, device="cuda", capacity_lengths=None,
-                 shared_selection=False, workspaces_from=None, head_rows=False):
+                 shared_selection=False, workspaces_from=None, head_rows=False, split_front=False):
         """``capacity_lengths`` (default ``lengths``) sizes every buffer, so that later
         ``set_lengths`` calls up to those lengths (a decode run) allocate nothing.
         ``shared_selection``: every head of a request selects the same pages
@@ -63,7 +63,12 @@ class BatchedSparseDecode:
         ``head_rows``: the resolver also writes each head's physical rows
         (``physical``, [B, heads, width]: row_index.py:127-131).  The group attention
         reads the union rows and the per-KV-head entry lists only, so the decode path
-        leaves them out unless asked."""
+        leaves them out unless asked.
+        ``split_front``: the tables given to :meth:`resolve` are affine with base
+        ``source[0]`` (host block = source[0] + page, a request's contiguous host slots),
+        so the resolver may spread its front over several workgroups per request
+        (``hs_resolve_desc.split_front``; power-of-two pages of at most 32 tokens)."""
+        self.split_front = split_front
         self._workspaces_from = workspaces_from
         self.head_rows = head_rows
         self.entry_stats = None  # optional int64 [1] device total of the unions' entry counts
@@ -257,6 +262,7 @@ class BatchedSparseDecode:
             d.miss_host_rows = self.miss_host[b].data_ptr()
             d.miss_device_rows = self.miss_device[b].data_ptr()
             d.miss_prefix_only = 1  # the gather stops at the miss count: no -1 tail
+            d.split_front = int(self.split_front and P <= 32 and (P & (P - 1)) == 0)
             d.counts = self.row_counts[b].data_ptr()
             total += lib.hs_resolve_workspace_bytes(self.capacity, self.capacity_lengths[b], d.n_pages, d.hot_rows)
         if total > self.resolve_ws_bytes:

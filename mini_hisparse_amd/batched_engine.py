@@ -471,7 +471,7 @@ class BatchedDecodeEngine:
 
     def __init__(self, model: MiniModel, state: SparseKVState, top_pages, *, max_tokens=None, keep_sink=True,
                  selector="quest", seed=0, graphs=False, projections="auto", transfer_stream=False,
-                 prefetch=None, request_groups=1, group_gather_workgroups=0):
+                 prefetch=None, request_groups=1, group_gather_workgroups=0, resolver_split=True):
         """``selector``: "quest" (per-head Quest pages over the bounds) or "uniform"
         (:func:`uniform_pages`, shared by every head, resampled each step).  ``graphs``:
         replay the dense part of each layer boundary as a HIP graph (when every per-layer
@@ -492,7 +492,10 @@ class BatchedDecodeEngine:
         on the transfer stream, the compute stream runs the other groups' attention, dense
         layers, append, selection and resolve (each request's own sequence of stages is
         unchanged, so every output is the same); ``group_gather_workgroups`` sets the
-        gather's workgroups per request there (0: the library's default)."""
+        gather's workgroups per request there (0: the library's default).
+        ``resolver_split``: the resolver's front over several workgroups per request
+        (``hs_resolve_desc.split_front``; the state's source tables are affine by
+        construction), else one workgroup per request."""
         if prefetch is None:
             prefetch = selector == "uniform"
         if prefetch and selector != "uniform":
@@ -512,7 +515,7 @@ class BatchedDecodeEngine:
         decoder = lambda donor=None: BatchedSparseDecode(
             state.config, cfg.num_attention_heads, top_pages, [max(1, l) for l in state.lengths],
             keep_sink=keep_sink, device=self.device, capacity_lengths=caps,
-            shared_selection=selector == "uniform", workspaces_from=donor,
+            shared_selection=selector == "uniform", workspaces_from=donor, split_front=resolver_split,
         )
         self.dec = decoder()
         self.prefetch = prefetch
@@ -537,6 +540,7 @@ class BatchedDecodeEngine:
                 group = BatchedSparseDecode(
                     state.config, cfg.num_attention_heads, top_pages, [max(1, l) for l in state.lengths[a:b]],
                     keep_sink=keep_sink, device=self.device, capacity_lengths=caps[a:b],
+                    split_front=resolver_split,
                 )
                 self.groups.append((range(a, b), group))
             # per (layer, group): resolved (compute -> transfer) and gathered (transfer -> compute)
@@ -553,6 +557,7 @@ class BatchedDecodeEngine:
         self._step_start = torch.cuda.Event()
         self._subsets = {}  # sorted slots of a partial batch -> its decoder and buffers
         self._keep_sink, self._top_pages, self._caps = keep_sink, top_pages, caps
+        self._resolver_split = resolver_split
         self.current_group = None  # (requests, decoder) the observer's arguments belong to
         self._static_buffers()
         self.use_graphs = graphs and all(self.projection_kernel[n] for n in ("qkv", "o_proj", "gate_up", "down"))
@@ -979,6 +984,7 @@ class BatchedDecodeEngine:
                 st.config, cfg.num_attention_heads, self._top_pages, [max(1, st.lengths[b]) for b in slots],
                 keep_sink=self._keep_sink, device=self.device, capacity_lengths=[self._caps[b] for b in slots],
                 shared_selection=self.selector == "uniform", workspaces_from=self.dec,
+                split_front=self._resolver_split,
             )
             index = torch.tensor(slots, dtype=torch.int64, device=self.device)
             n, dt, dev = len(slots), self.model.dtype, self.device

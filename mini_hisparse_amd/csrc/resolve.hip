@@ -60,6 +60,8 @@ constexpr int MARK_BATCH = 8;  // pages loaded per thread before use (long table
 constexpr int PAGE_REGS = 9;  // pages per thread loaded before the token walk (n_pages <= RT * PAGE_REGS)
 constexpr int ORDER_WORDS = 8; // token-bitmap words per thread held in registers
 constexpr int WALK_PRE = 5;    // page-bitmap words per thread loaded first (lengths below RT * 5 * 32)
+constexpr int ST = 512;        // threads of the split front's launches
+constexpr int SPLIT_MAX = 64;  // workgroups per request of the split front
 constexpr int MARK_TILE = 512;                // inputs per wave and tile (8 per lane)
 constexpr int MARK_TILE_PAD = MARK_TILE / 8 * 9;
 constexpr uint64_t HASH_EMPTY = ~static_cast<uint64_t>(0);
@@ -106,8 +108,17 @@ struct ResolveWs {
   int32_t* tslot;      // [length] hot slot of a hit token
   uint64_t* hash;      // [hcap] (page << 32) | host block of needs-hot pages; all ones = empty
   int32_t* victims;    // [hot_rows] slots in victim order (ranks below the miss count written)
-  int64_t* totals;     // [4] resident hits, hot hits, misses, any duplicate
+  int64_t* totals;     // [4] resident hits, hot hits, misses, any duplicate (2: see the split front)
   int64_t hcap;
+};
+
+// The split front's own workspace (after the regions above; a separate struct, so
+// that the single-workgroup front carries none of its pointers).
+struct SplitWs {
+  uint32_t* prot;      // [ceil(hot_rows / 32)] protected slots
+  uint16_t* lru_snap;  // [hot_rows] the LRU as read before its rewrite
+  int64_t* part;       // [6 * SPLIT_MAX] per-workgroup partials
+  uint32_t* needpg;    // [2 * ceil(n_pages / 64)] pages with needs-hot tokens
 };
 
 __host__ __device__ inline int64_t align256(int64_t x) { return (x + 255) & ~static_cast<int64_t>(255); }
@@ -120,7 +131,7 @@ __host__ __device__ inline int64_t pow2_at_least(int64_t x) {
 __host__ __device__ inline int64_t words_for(int64_t length) { return (length + 32) / 32; }
 
 __host__ __device__ inline int64_t ws_layout(int64_t length, int64_t n_pages, int64_t hot_rows, ResolveWs* w,
-                                             char* base) {
+                                             char* base, SplitWs* sw = nullptr) {
   const int64_t wl = words_for(length);
   const int64_t hcap = pow2_at_least(2 * (n_pages < 1 ? 1 : n_pages));
   int64_t off = 0;
@@ -138,6 +149,10 @@ __host__ __device__ inline int64_t ws_layout(int64_t length, int64_t n_pages, in
   char* p6 = take(hcap * 8);
   char* p7 = take(hot_rows * 4);
   char* p8 = take(4 * 8);
+  char* p9 = take((hot_rows + 31) / 32 * 4);
+  char* p10 = take(hot_rows * 2);
+  char* p11 = take(6 * SPLIT_MAX * 8);
+  char* p12 = take((n_pages + 63) / 64 * 8);
   if (w) {
     w->hitbits = reinterpret_cast<uint32_t*>(p0);
     w->missbits = reinterpret_cast<uint32_t*>(p1);
@@ -150,6 +165,12 @@ __host__ __device__ inline int64_t ws_layout(int64_t length, int64_t n_pages, in
     w->totals = reinterpret_cast<int64_t*>(p8);
     w->hcap = hcap;
   }
+  if (sw) {
+    sw->prot = reinterpret_cast<uint32_t*>(p9);
+    sw->lru_snap = reinterpret_cast<uint16_t*>(p10);
+    sw->part = reinterpret_cast<int64_t*>(p11);
+    sw->needpg = reinterpret_cast<uint32_t*>(p12);
+  }
   return off;
 }
 
@@ -157,6 +178,12 @@ __device__ __forceinline__ ResolveWs ws_of(const hs_resolve_desc& d) {
   ResolveWs w;
   ws_layout(d.length, d.n_pages, d.hot_rows, &w, static_cast<char*>(d.workspace));
   return w;
+}
+__device__ __forceinline__ SplitWs split_ws_of(const hs_resolve_desc& d) {
+  ResolveWs w;
+  SplitWs sw;
+  ws_layout(d.length, d.n_pages, d.hot_rows, &w, static_cast<char*>(d.workspace), &sw);
+  return sw;
 }
 
 __device__ __forceinline__ uint32_t hash32(uint32_t x) {
@@ -763,6 +790,386 @@ __global__ __launch_bounds__(RT) void resolve_front_kernel(ResolveBatch batch) {
   }
 }
 
+// ---- split front: the front's work spread over SW workgroups per request, in
+// three launches, for the batched decode's descriptors (hs_resolve_desc.split_front):
+// a union page bitmap, a power-of-two page of at most 32 tokens, and an affine source
+// table whose base is source[0] (host block = source[0] + page for every host-backed
+// page, the layout of a request's contiguous host slots).  The single-workgroup
+// front keeps the bitmaps of a request in one CU's LDS; here every phase that needs
+// the whole request waits for the launch before it instead:
+//
+//   match  (SW WGs / desc)  pages: resident hits, the range of (host block - page);
+//                           hot slots: a slot whose tag's token needs a hot row is a
+//                           hit (row_index.py:84-90): the token's slot, the slot's
+//                           protection bit;
+//   order  (SW WGs / desc)  token words: needs-hot bits, hits among them (a token
+//                           whose slot, written by the match launch, holds its tag:
+//                           slots left by earlier calls hold other tags), misses;
+//                           LRU entries: protected or not, a copy of the LRU;
+//   place  (SW WGs / desc)  from every workgroup's counts: the miss prefix per word,
+//                           the victims and the new LRU (the same partitions as the
+//                           front's, row_index.py:94-96, 112-113), the totals.
+//
+// Per-workgroup counts go to part[k * SPLIT_MAX + wi].  A table that is not affine
+// with base source[0] (other than one with no host-backed page) is refused by the
+// place launch: totals[3] = 2, and the outputs launch writes no row.
+enum { PART_RES = 0, PART_LO, PART_HI, PART_HIT, PART_MISS, PART_FREE };
+constexpr int SPLIT_SLOTS = 4;  // hot slots / LRU entries per thread and launch (hot_rows <= SW * ST * 4)
+
+struct SplitGeom {
+  int64_t L, P, NPh, wl;
+  int32_t S;
+  uint32_t pshift, base;
+  __device__ explicit SplitGeom(const hs_resolve_desc& d)
+      : L(d.length), P(d.page_size), NPh((d.length + d.page_size - 1) / d.page_size), wl(words_for(d.length)),
+        S(static_cast<int32_t>(d.hot_rows)),
+        pshift(static_cast<uint32_t>(__ffsll(static_cast<unsigned long long>(d.page_size)) - 1)),
+        base(static_cast<uint32_t>(d.source[0])) {}
+  // token of the host row `tag` under the affine table (-1: none of the history)
+  __device__ __forceinline__ int64_t token_of(int32_t tag) const {
+    if (tag < 0) return -1;
+    const uint32_t page = (static_cast<uint32_t>(tag) >> pshift) - base;  // outside the range: >= 2^31
+    if (page >= static_cast<uint64_t>(NPh)) return -1;
+    const int64_t t = (static_cast<int64_t>(page) << pshift) | (static_cast<uint32_t>(tag) & static_cast<uint32_t>(P - 1));
+    return t < L ? t : -1;
+  }
+};
+
+__device__ __forceinline__ bool page_bit(const uint32_t* bits, int64_t p) { return (bits[p >> 5] >> (p & 31)) & 1u; }
+
+// sums (and min / max) of one value per thread, published by thread 0
+__device__ __forceinline__ int64_t block_sum64(int64_t v, int64_t* red) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+  __syncthreads();
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  int64_t s = 0;
+  for (int u = 0; u < static_cast<int>(blockDim.x >> 6); ++u) s += red[u];
+  return s;
+}
+
+__global__ __launch_bounds__(ST) void resolve_split_match_kernel(ResolveBatch batch) {
+  __shared__ int64_t red[ST / 64];
+  __shared__ int32_t red_lo[ST / 64], red_hi[ST / 64];
+  const hs_resolve_desc& d = batch.d[blockIdx.y];
+  const ResolveWs w = ws_of(d);
+  const SplitWs x = split_ws_of(d);
+  const SplitGeom g(d);
+  const int SW = gridDim.x, wi = blockIdx.x, T = threadIdx.x, lane = T & 63, wave = T >> 6;
+  // the workgroup's hot slots, 64-aligned (a wave's 64 slots form two protection
+  // words, which lanes 0 and 32 store); their tags load first, with the pages' tables
+  const int64_t spad = (static_cast<int64_t>(g.S) + 63) / 64 * 64;
+  const int64_t sp = ((g.S + SW - 1) / SW + 63) / 64 * 64;
+  const int64_t s0 = wi * sp, s1 = s0 + sp < spad ? s0 + sp : spad;
+  Regs<int32_t, SPLIT_SLOTS> tag;
+#pragma unroll
+  for (int k = 0; k < SPLIT_SLOTS; ++k) {
+    const int64_t s = s0 + T + static_cast<int64_t>(k) * ST;
+    tag[k] = d.tags[s < g.S ? s : 0];  // unconditional load, masked below
+  }
+  // the workgroup's pages, 64-aligned (a wave's 64 pages form two needs-page words):
+  // resident hits of the selected pages, the range of (host block - page), and the
+  // pages whose selected tokens need a hot row
+  const int64_t ppad = (g.NPh + 63) / 64 * 64;
+  const int64_t pp = ((g.NPh + SW - 1) / SW + 63) / 64 * 64;
+  const int64_t p0 = wi * pp, p1 = p0 + pp < ppad ? p0 + pp : ppad;
+  int64_t c_res = 0;
+  int32_t lo = INT32_MAX, hi = INT32_MIN;
+  for (int64_t pb = p0; pb < p1; pb += static_cast<int64_t>(ST) * SPLIT_SLOTS) {
+    Regs<int32_t, SPLIT_SLOTS> sv, rv;
+    Regs<uint32_t, SPLIT_SLOTS> bw;
+#pragma unroll
+    for (int k = 0; k < SPLIT_SLOTS; ++k) {
+      const int64_t p = pb + T + static_cast<int64_t>(k) * ST;
+      const int64_t pc = p < g.NPh ? p : 0;  // unconditional loads, masked below
+      sv[k] = d.source[pc];
+      rv[k] = d.resident[pc];
+      bw[k] = d.page_bits[pc >> 5];
+    }
+#pragma unroll
+    for (int k = 0; k < SPLIT_SLOTS; ++k) {
+      const int64_t p = pb + T + static_cast<int64_t>(k) * ST;
+      if (p >= p1) break;  // the same for the whole wave (pb, p1 and ST are multiples of 64)
+      const bool host = p < g.NPh && sv[k] >= 0;
+      const bool sel = (bw[k] >> (p & 31)) & 1u;
+      if (host) {
+        const int32_t shift = sv[k] - static_cast<int32_t>(p);  // both in [0, 2^31): no overflow
+        lo = shift < lo ? shift : lo;
+        hi = shift > hi ? shift : hi;
+        if (rv[k] >= 0 && sel) c_res += g.L - p * g.P < g.P ? g.L - p * g.P : g.P;
+      }
+      const uint64_t m = __ballot(host && sel && rv[k] < 0);
+      if ((lane & 31) == 0) x.needpg[p >> 5] = lane ? static_cast<uint32_t>(m >> 32) : static_cast<uint32_t>(m);
+    }
+  }
+  // hot slots: a slot whose tag's token needs a hot row is a hit
+  Regs<int64_t, SPLIT_SLOTS> tok;
+  Regs<bool, SPLIT_SLOTS> hit;
+#pragma unroll
+  for (int k = 0; k < SPLIT_SLOTS; ++k) {
+    const int64_t s = s0 + T + static_cast<int64_t>(k) * ST;
+    tok[k] = s < s1 && s < g.S ? g.token_of(tag[k]) : -1;
+  }
+#pragma unroll
+  for (int k = 0; k < SPLIT_SLOTS; ++k) {
+    const int64_t pg = tok[k] >= 0 ? tok[k] >> g.pshift : 0;
+    const bool sel = page_bit(d.page_bits, pg);
+    const int32_t sv = d.source[pg], rv = d.resident[pg];
+    hit[k] = tok[k] >= 0 && sel && sv >= 0 && rv < 0;
+  }
+#pragma unroll
+  for (int k = 0; k < SPLIT_SLOTS; ++k) {
+    const int64_t s = s0 + T + static_cast<int64_t>(k) * ST;
+    if (s >= s1) break;  // the same for the whole wave (s0, s1 and ST are multiples of 64)
+    if (hit[k]) w.tslot[tok[k]] = static_cast<int32_t>(s);
+    const uint64_t m = __ballot(hit[k]);
+    if ((lane & 31) == 0 && (s >> 5) < (g.S + 31) / 32)
+      x.prot[s >> 5] = lane ? static_cast<uint32_t>(m >> 32) : static_cast<uint32_t>(m);
+  }
+  lo = wave_min_i32(lo);
+  hi = wave_max_i32(hi);
+  if (lane == 0) {
+    red_lo[wave] = lo;
+    red_hi[wave] = hi;
+  }
+  const int64_t res = block_sum64(c_res, red);  // its barriers order red_lo / red_hi too
+  if (T == 0) {
+    for (int u = 0; u < ST / 64; ++u) {
+      lo = red_lo[u] < lo ? red_lo[u] : lo;
+      hi = red_hi[u] > hi ? red_hi[u] : hi;
+    }
+    x.part[PART_RES * SPLIT_MAX + wi] = res;
+    x.part[PART_LO * SPLIT_MAX + wi] = lo;
+    x.part[PART_HI * SPLIT_MAX + wi] = hi;
+  }
+}
+
+template <bool L16>
+__global__ __launch_bounds__(ST) void resolve_split_order_kernel(ResolveBatch batch) {
+  __shared__ int64_t red[ST / 64];
+  const hs_resolve_desc& d = batch.d[blockIdx.y];
+  const ResolveWs w = ws_of(d);
+  const SplitWs x = split_ws_of(d);
+  const SplitGeom g(d);
+  const int SW = gridDim.x, wi = blockIdx.x, T = threadIdx.x;
+  // LRU entries (their loads go out with the token words' first loads)
+  const int64_t ep = (g.S + SW - 1) / SW, e0 = wi * ep, e1 = e0 + ep < g.S ? e0 + ep : g.S;
+  Regs<uint32_t, SPLIT_SLOTS> sl;
+#pragma unroll
+  for (int k = 0; k < SPLIT_SLOTS; ++k) {
+    const int64_t j = e0 + T + static_cast<int64_t>(k) * ST;
+    const int64_t jc = j < e1 ? j : 0;
+    // the front's reading of an LRU entry: its low 16 bits (slots < 32768)
+    sl[k] = L16 ? static_cast<uint32_t>(static_cast<uint16_t>(static_cast<const int16_t*>(d.lru)[jc]))
+                : static_cast<uint32_t>(static_cast<const int64_t*>(d.lru)[jc]) & 0xffffu;
+  }
+  // token words: needs-hot bits from the match launch's page bitmap, hits among them
+  // (a token whose slot still holds its tag), misses
+  const int64_t wp = (g.wl + SW - 1) / SW, w0 = wi * wp, w1 = w0 + wp < g.wl ? w0 + wp : g.wl;
+  const uint32_t ppw = 32u >> g.pshift;  // pages per token word
+  const uint32_t pmask = g.P >= 32 ? 0xffffffffu : (1u << g.P) - 1u;
+  int64_t c_hit = 0, c_miss = 0;
+  int64_t c_free = 0;
+  bool lru_done = false;
+  for (int64_t wb = w0; wb < w1 || !lru_done; wb += ST) {
+    const int64_t wd = wb + T;
+    const int64_t t0 = wd << 5;
+    const bool word = wd < w1 && t0 < g.L;
+    // a multiple of ppw: the word's pages share one bitmap word
+    const int64_t pf = word ? t0 >> g.pshift : 0;
+    const uint32_t np = x.needpg[pf >> 5] >> (pf & 31);
+    if (!lru_done) {  // the LRU's protection words, loaded beside the first needs words
+#pragma unroll
+      for (int k = 0; k < SPLIT_SLOTS; ++k) {
+        const int64_t j = e0 + T + static_cast<int64_t>(k) * ST;
+        const uint32_t pw = x.prot[(sl[k] < static_cast<uint32_t>(g.S) ? sl[k] : 0u) >> 5];
+        if (j < e1) {
+          x.lru_snap[j] = static_cast<uint16_t>(sl[k]);
+          c_free += ((pw >> (sl[k] & 31)) & 1u) ? 0 : 1;
+        }
+      }
+      lru_done = true;
+    }
+    if (wd >= w1) continue;
+    uint32_t needs = 0u;
+    if (word) {
+      for (uint32_t j = 0; j < ppw; ++j)
+        if ((np >> j) & 1u) needs |= pmask << (j * static_cast<uint32_t>(g.P));
+      needs &= range_mask(wd, 0, g.L);
+    }
+    uint32_t hitw = 0u;
+    if (needs) {
+      // the word's slots (tslot has room up to the next 64 tokens), then their tags
+      Regs<int32_t, 32> ts;
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const int4 v = *reinterpret_cast<const int4*>(w.tslot + t0 + 4 * q);
+        ts[4 * q] = v.x;
+        ts[4 * q + 1] = v.y;
+        ts[4 * q + 2] = v.z;
+        ts[4 * q + 3] = v.w;
+      }
+      Regs<int32_t, 32> tg;
+#pragma unroll
+      for (int j = 0; j < 32; ++j) {
+        const bool ok = ((needs >> j) & 1u) && ts[j] >= 0 && ts[j] < g.S;
+        const int32_t v = d.tags[ok ? ts[j] : 0];  // unconditional load, masked afterwards
+        tg[j] = ok ? v : -1;
+      }
+#pragma unroll
+      for (int j = 0; j < 32; ++j)
+        if (g.token_of(tg[j]) == t0 + j) hitw |= 1u << j;
+    }
+    const uint32_t missw = needs & ~hitw;
+    w.hitbits[wd] = hitw;
+    w.missbits[wd] = missw;
+    c_hit += __popc(hitw);
+    c_miss += __popc(missw);
+  }
+  const int64_t hits = block_sum64(c_hit, red);
+  const int64_t misses = block_sum64(c_miss, red);
+  const int64_t freed = block_sum64(c_free, red);
+  if (T == 0) {
+    x.part[PART_HIT * SPLIT_MAX + wi] = hits;
+    x.part[PART_MISS * SPLIT_MAX + wi] = misses;
+    x.part[PART_FREE * SPLIT_MAX + wi] = freed;
+  }
+}
+
+template <bool L16>
+__global__ __launch_bounds__(ST) void resolve_split_place_kernel(ResolveBatch batch) {
+  __shared__ int64_t s_tot[8];  // resident, hits, misses, unprotected; miss and unprotected offsets; lo; hi
+  __shared__ int32_t scan32[ST / 64];
+  __shared__ int32_t wcnt[ST / 64];
+  const hs_resolve_desc& d = batch.d[blockIdx.y];
+  const ResolveWs w = ws_of(d);
+  const SplitWs x = split_ws_of(d);
+  const SplitGeom g(d);
+  const int SW = gridDim.x, wi = blockIdx.x, T = threadIdx.x, lane = T & 63, wave = T >> 6;
+  // one round of loads: the workgroup's miss words (contiguous runs per thread, in word
+  // order; the first word of each run here), its LRU entries, every workgroup's counts
+  const int64_t wp = (g.wl + SW - 1) / SW, w0 = wi * wp, w1 = w0 + wp < g.wl ? w0 + wp : g.wl;
+  const int64_t run = (w1 - w0 + ST - 1) / ST;
+  const int64_t a0 = w0 + T * run < w1 ? w0 + T * run : w1;
+  const int64_t a1 = a0 + run < w1 ? a0 + run : w1;
+  const uint32_t first_miss = w.missbits[a0 < w1 ? a0 : 0];
+  const int64_t ep = (g.S + SW - 1) / SW, e0 = wi * ep, e1 = e0 + ep < g.S ? e0 + ep : g.S;
+  Regs<uint32_t, SPLIT_SLOTS> sl;
+#pragma unroll
+  for (int k = 0; k < SPLIT_SLOTS; ++k) {
+    const int64_t j = e0 + T + static_cast<int64_t>(k) * ST;
+    sl[k] = x.lru_snap[j < e1 ? j : 0];
+  }
+  if (wave == 0) {  // every workgroup's counts: totals and this workgroup's offsets
+    const bool in = lane < SW;
+    int64_t res = in ? x.part[PART_RES * SPLIT_MAX + lane] : 0;
+    int32_t lo = in ? static_cast<int32_t>(x.part[PART_LO * SPLIT_MAX + lane]) : INT32_MAX;
+    int32_t hi = in ? static_cast<int32_t>(x.part[PART_HI * SPLIT_MAX + lane]) : INT32_MIN;
+    int64_t hit = in ? x.part[PART_HIT * SPLIT_MAX + lane] : 0;
+    const int64_t miss = in ? x.part[PART_MISS * SPLIT_MAX + lane] : 0;
+    const int64_t fr = in ? x.part[PART_FREE * SPLIT_MAX + lane] : 0;
+    const int64_t miss_inc = wave_inclusive_sum(miss), free_inc = wave_inclusive_sum(fr);
+    lo = wave_min_i32(lo);
+    hi = wave_max_i32(hi);
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+      res += __shfl_xor(res, off, 64);
+      hit += __shfl_xor(hit, off, 64);
+    }
+    if (lane == wi) {
+      s_tot[4] = miss_inc - miss;
+      s_tot[5] = free_inc - fr;
+    }
+    if (lane == 63) {
+      s_tot[0] = res;
+      s_tot[1] = hit;
+      s_tot[2] = miss_inc;
+      s_tot[3] = free_inc;
+      s_tot[6] = lo;
+      s_tot[7] = hi;
+    }
+  }
+  __syncthreads();
+  const int64_t tot_miss = s_tot[2];
+  const int32_t lo = static_cast<int32_t>(s_tot[6]), hi = static_cast<int32_t>(s_tot[7]);
+  // a table with host-backed pages must be affine with base source[0]
+  const bool affine = lo > hi || (lo == hi && lo == d.source[0]);
+  if (!affine) {
+    if (wi == 0 && T == 0) {
+      w.totals[0] = 0;
+      w.totals[1] = 0;
+      w.totals[2] = 0;
+      w.totals[3] = 2;
+    }
+    return;
+  }
+  if (wi == 0 && T == 0) {
+    w.totals[0] = s_tot[0];
+    w.totals[1] = s_tot[1];
+    w.totals[2] = tot_miss;
+    w.totals[3] = 0;  // a page bitmap admits no duplicate input
+  }
+  // miss prefix of the workgroup's words
+  {
+    int32_t cnt = a0 < a1 ? __popc(first_miss) : 0;
+    for (int64_t wd = a0 + 1; wd < a1; ++wd) cnt += __popc(w.missbits[wd]);
+    int32_t all;
+    int64_t r = s_tot[4] + block_exclusive_sum<int32_t>(cnt, scan32, &all);
+    for (int64_t wd = a0; wd < a1; ++wd) {
+      w.mprefix[wd] = static_cast<int32_t>(r);
+      r += __popc(wd == a0 ? first_miss : w.missbits[wd]);
+    }
+  }
+  // victims and the new LRU over the workgroup's LRU entries, in LRU order
+  const int32_t S = g.S;
+  const int32_t U = static_cast<int32_t>(s_tot[3]);
+  const int32_t tm = tot_miss < S ? static_cast<int32_t>(tot_miss) : S;  // only rank < tm matters
+  const int32_t Pn = S - U;
+  const int32_t fillU = U < tm ? U : tm;
+  const int32_t fillP = tm - U > 0 ? (tm - U < Pn ? tm - U : Pn) : 0;
+  const int32_t start1 = U - fillU, start2 = U, start3 = S - fillP;
+  Regs<bool, SPLIT_SLOTS> fr;
+#pragma unroll
+  for (int k = 0; k < SPLIT_SLOTS; ++k) {
+    const int64_t j = e0 + T + static_cast<int64_t>(k) * ST;
+    const uint32_t pw = x.prot[(sl[k] < static_cast<uint32_t>(S) ? sl[k] : 0u) >> 5];
+    fr[k] = j < e1 && !((pw >> (sl[k] & 31)) & 1u);
+  }
+  int32_t r = static_cast<int32_t>(s_tot[5]);  // unprotected entries before the chunk
+#pragma unroll
+  for (int k = 0; k < SPLIT_SLOTS; ++k) {
+    const int64_t j = e0 + T + static_cast<int64_t>(k) * ST;
+    const uint64_t m = __ballot(fr[k]);
+    if (lane == 0) wcnt[wave] = static_cast<int32_t>(__popcll(m));
+    __syncthreads();
+    int32_t before = 0, chunk = 0;
+    for (int u = 0; u < ST / 64; ++u) {
+      const int32_t c = wcnt[u];
+      before += u < wave ? c : 0;
+      chunk += c;
+    }
+    __syncthreads();
+    if (j < e1) {
+      const int32_t rr = r + before + lanes_below(m);  // unprotected entries before entry j
+      int32_t rank, at;
+      if (fr[k]) {
+        rank = rr;
+        at = rr < fillU ? start1 + rr : rr - fillU;
+      } else {
+        const int32_t pj = static_cast<int32_t>(j) - rr;  // protected entries before entry j
+        rank = U + pj;
+        at = pj < fillP ? start3 + pj : start2 + (pj - fillP);
+      }
+      if (rank < tm) w.victims[rank] = static_cast<int32_t>(sl[k]);
+      if constexpr (L16) static_cast<int16_t*>(d.lru)[at] = static_cast<int16_t>(sl[k]);
+      else static_cast<int64_t*>(d.lru)[at] = static_cast<int64_t>(sl[k]);
+    }
+    r += chunk;
+  }
+}
+
 // Physical row of input i (-1 when invalid, a later duplicate, or host-less).
 // For a miss, `miss_rank` gets its rank, `slot` its victim slot and `host` its
 // host row; otherwise miss_rank = -1.
@@ -812,6 +1219,20 @@ __global__ __launch_bounds__(RW) void resolve_outputs_kernel(ResolveBatch batch)
   const int64_t n = d.n, S = d.hot_rows;
   const int64_t e = static_cast<int64_t>(blockIdx.x) * RW + threadIdx.x;
   const int64_t tot_miss = w.totals[2];
+  if (w.totals[3] == 2) {  // the split front refused the source table: no row, no miss, no count
+    if (e < n) {
+      if (d.union_physical) d.union_physical[e] = -1;
+      if (!d.head_columns && d.physical != d.union_physical) d.physical[e] = -1;
+      if (!d.miss_prefix_only) {
+        d.miss_host_rows[e] = -1;
+        d.miss_device_rows[e] = -1;
+      }
+      if (e == 0) d.counts[0] = d.counts[1] = d.counts[2] = 0;
+    } else if (d.head_columns && e - n < d.heads * d.width) {
+      d.physical[e - n] = -1;
+    }
+    return;
+  }
   const bool dups = w.totals[3] != 0;
   if (e < n) {
     int64_t rank, host = -1;
@@ -873,6 +1294,10 @@ static int validate_desc(const hs_resolve_desc& d) {
   HS_CHECK_ARG(d.hot_rows >= 1 && d.hot_rows <= RT * LRU_CHUNK, "hot_rows must be in [1, 32768]");
   HS_CHECK_ARG(d.lru_i16 == 0 || d.lru_i16 == 1, "lru_i16 must be 0 or 1");
   HS_CHECK_ARG(d.miss_prefix_only == 0 || d.miss_prefix_only == 1, "miss_prefix_only must be 0 or 1");
+  HS_CHECK_ARG(d.split_front == 0 || d.split_front == 1, "split_front must be 0 or 1");
+  if (d.split_front)
+    HS_CHECK_ARG(d.page_bits != nullptr && d.page_size <= 32 && (d.page_size & (d.page_size - 1)) == 0,
+                 "split_front needs a union page bitmap and a power-of-two page size of at most 32");
   if (d.lru_i16)  // the front launch reads an int16 LRU as 32-bit pairs
     HS_CHECK_ARG(d.hot_rows % 2 == 0 && (reinterpret_cast<uintptr_t>(d.lru) & 3) == 0,
                  "an int16 LRU needs an even hot_rows and 4-byte alignment");
@@ -907,6 +1332,8 @@ static int64_t batch_workspace(const hs_resolve_desc* descs, int32_t count) {
     const int rc = validate_desc(descs[i]);
     if (rc) return rc;
     HS_CHECK_ARG(descs[i].lru_i16 == descs[0].lru_i16, "the descriptors of one batch must share lru_i16");
+    HS_CHECK_ARG(descs[i].split_front == descs[0].split_front,
+                 "the descriptors of one batch must share split_front");
     need += hs_resolve_workspace_bytes(descs[i].n, descs[i].length, descs[i].n_pages, descs[i].hot_rows);
   }
   return need;
@@ -970,8 +1397,34 @@ static int resolve_launch(const hs_resolve_desc* descs, int32_t count, char* wor
     const unsigned nb = static_cast<unsigned>(batch.count);
     const size_t lds = static_cast<size_t>(front_lds);
     const bool l16 = batch.d[0].lru_i16 != 0;  // the same for every descriptor (validated)
-    if (max_hot <= 16 * RT) launch_front<16>(pow2, l16, nb, lds, stream, batch);
-    else launch_front<32>(pow2, l16, nb, lds, stream, batch);
+    // The split front where it measured faster: hot regions above 16384 rows (the 7B
+    // layer shape: 30.4 us for its three launches against 37.5 us for the one-workgroup
+    // front; the 0.5B layer shape, 13504 rows: 21.7 against 19.3 us); HS_RESOLVE_SPLIT=0 / 1
+    // forces either way for descriptors that allow it (read per call).
+    const char* split_env = getenv("HS_RESOLVE_SPLIT");
+    const int split_force = split_env ? atoi(split_env) : -1;
+    const bool split = batch.d[0].split_front && (split_force == 1 || (split_force != 0 && max_hot > 16 * RT));
+    if (split) {
+      // workgroups per request: about one round of 256 in all, and at least enough for
+      // SPLIT_SLOTS hot slots per thread
+      int sw = static_cast<int>(256 / nb);
+      const int need = static_cast<int>(ceil_div(max_hot, static_cast<int64_t>(ST) * SPLIT_SLOTS));
+      sw = sw < need ? need : sw;
+      sw = sw < 1 ? 1 : (sw > SPLIT_MAX ? SPLIT_MAX : sw);
+      const dim3 grid(static_cast<unsigned>(sw), nb);
+      hipLaunchKernelGGL(resolve_split_match_kernel, grid, dim3(ST), 0, stream, batch);
+      if (l16) {
+        hipLaunchKernelGGL(resolve_split_order_kernel<true>, grid, dim3(ST), 0, stream, batch);
+        hipLaunchKernelGGL(resolve_split_place_kernel<true>, grid, dim3(ST), 0, stream, batch);
+      } else {
+        hipLaunchKernelGGL(resolve_split_order_kernel<false>, grid, dim3(ST), 0, stream, batch);
+        hipLaunchKernelGGL(resolve_split_place_kernel<false>, grid, dim3(ST), 0, stream, batch);
+      }
+    } else if (max_hot <= 16 * RT) {
+      launch_front<16>(pow2, l16, nb, lds, stream, batch);
+    } else {
+      launch_front<32>(pow2, l16, nb, lds, stream, batch);
+    }
     HS_CHECK_LAUNCH("resolver front");
     hipLaunchKernelGGL(resolve_outputs_kernel, dim3(static_cast<unsigned>(ceil_div(max_out, RW)), nb), dim3(RW),
                        0, stream, batch);

@@ -114,6 +114,30 @@ def test_resolver_lru_dtype_rules_without_a_gpu():
     assert b"workspace too small" in lib.hs_last_error()
 
 
+def test_resolver_split_front_rules_without_a_gpu():
+    """The split front needs a union page bitmap and a power-of-two page of at most 32
+    tokens, and one setting per batch; all rejected on the host."""
+    lib = _lib.load()
+
+    def split(page_bits=0x90000, page_size=16, flag=1):
+        d = _fake_resolve_desc(lru_i16=1)
+        d.page_bits, d.page_size, d.split_front = page_bits, page_size, flag
+        d.length = min(d.length, page_size * d.n_pages)
+        return d
+
+    assert lib.hs_resolve_rows(split(flag=2), None, 0, None) == -1
+    assert b"split_front must be 0 or 1" in lib.hs_last_error()
+    for bad in (split(page_bits=None), split(page_size=12), split(page_size=64)):
+        assert lib.hs_resolve_rows(bad, None, 0, None) == -1
+        assert b"split_front needs a union page bitmap" in lib.hs_last_error()
+    mixed = (_lib.ResolveDesc * 2)(split(), split(flag=0))
+    assert lib.hs_resolve_rows_batched(mixed, 2, None, 0, None) == -1
+    assert b"share split_front" in lib.hs_last_error()
+    same = (_lib.ResolveDesc * 2)(split(), split())
+    assert lib.hs_resolve_rows_batched(same, 2, None, 0, None) == -1
+    assert b"workspace too small" in lib.hs_last_error()
+
+
 def test_union_page_bitmap_stride_checked_without_a_gpu():
     lib = _lib.load()
     lengths = (ctypes.c_int64 * 1)(4096)  # 256 pages: 8 bitmap words

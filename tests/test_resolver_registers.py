@@ -1,4 +1,4 @@
-"""Per-thread register arrays of the resolver's front kernel stay inside their bounds.
+"""Per-thread register arrays of the resolver's front kernels stay inside their bounds.
 
 The front kernel keeps per-thread state in small arrays (tag rows, packed LRU pairs,
 page-bitmap words, early page-table entries, batches of probes and matches) indexed only
@@ -72,6 +72,11 @@ def test_front_register_indices_stay_in_range(assemblies):
     slots = sorted(int(re.search(r"ELi(\d+)EE", name).group(1)) for name in kernels)
     assert slots == [16] * 4 + [32] * 4, sorted(kernels)
     for name, body in kernels.items():
+        assert "s_trap" not in body, f"{name}: a per-thread array index can leave its array"
+    # the split front's three kernels (int16 and int64 LRU forms of the last two)
+    split = functions(front, "_ZN2hs26resolve_split_")
+    assert len(split) == 5, sorted(split)
+    for name, body in split.items():
         assert "s_trap" not in body, f"{name}: a per-thread array index can leave its array"
 
 
