@@ -418,3 +418,62 @@ def test_graph_replayed_dense_layers_match_eager_launches(gpu):
     for t0, t1 in zip(et, gt):
         assert torch.equal(t0, t1)
     assert torch.equal(es, gs)
+
+
+@pytest.mark.gpu
+def test_full_7b_step_matches_oracle_on_every_layer(gpu):
+    """The whole BASELINE configs[3] step at its full size for one request: 28 layers,
+    131,072-token history (synthetic), top-64 pages, 32,768 hot rows (the resolver's split
+    front), two decode steps.  Every layer of each step is checked against the oracle: the bounds equal the exact extrema of the history read back from the host
+    pool, the Quest pages equal the oracle's, the attention equals the oracle's sparse
+    attention over the selected tokens; every layer's rows are resident, hot or missed."""
+    from dataclasses import replace
+
+    from mini_hisparse_amd.batched_engine import WORKLOADS, BatchedDecodeEngine, build_state, random_model
+
+    wl = replace(WORKLOADS["qwen2.5-7b"], batch=1, context=131072 - 1, steps=4)
+    print(f"[case] full 7B step: L={wl.layers} context={wl.context} hot_rows={wl.hot_rows}", flush=True)
+    model, state = random_model(wl, gpu, seed=1), build_state(wl, gpu, seed=2)
+    engine = BatchedDecodeEngine(model, state, wl.top_pages)
+    P, Hkv, D, C = wl.page_size, wl.kv_heads, wl.head_dim, state.pages
+    sampled = tuple(range(wl.layers))
+    records = []
+
+    def observe(l, q, k, v, out):
+        if l in sampled:
+            dec = engine.decoder(l)
+            records.append((l, q.clone(), out.clone(), dec.pages.clone(), dec.union_count.clone()))
+
+    tokens = torch.tensor([7], device=gpu)
+    stats0 = state.row_stats.clone()
+    for step in range(2):
+        records.clear()
+        tokens = engine.step(tokens, observe)
+        torch.cuda.synchronize()
+        length = state.lengths[0]
+        count = ceil(length / P)
+        assert [r[0] for r in records] == list(sampled)
+        for l, q, out, layer_pages, union_count in records:
+            kv = state.host[l].view(1, C, 2, P, Hkv, D)[0, :count].float()
+            keys = kv[:, 0].reshape(count * P, Hkv, D)[:length]
+            vals = kv[:, 1].reshape(count * P, Hkv, D)[:length]
+            padded = torch.cat([keys, keys[-1:].expand(count * P - length, Hkv, D)]).view(count, P, Hkv, D)
+            lo, hi = padded.amin(1), padded.amax(1)  # the last page's padding repeats its last row
+            torch.testing.assert_close(state.minimum[l, 0, :count].float().cpu(), lo, rtol=0, atol=0)
+            torch.testing.assert_close(state.maximum[l, 0, :count].float().cpu(), hi, rtol=0, atol=0)
+            pages = oracle.quest_pages(q[0].cpu(), lo, hi, length, P, wl.top_pages)
+            np.testing.assert_array_equal(layer_pages[0, :, : pages.shape[1]].cpu().numpy(), pages,
+                                          err_msg=f"step {step} layer {l}")
+            positions = pages_to_positions(pages, length, P)
+            assert int(union_count[0]) == len(set().union(*map(set, positions)))
+            # each head over its selected tokens (the request's host rows are its tokens)
+            width = max(len(p) for p in positions)
+            rows = np.full((len(positions), width), -1, np.int64)
+            for h, p in enumerate(positions):
+                rows[h, : len(p)] = p
+            expected = oracle.row_attention_rows(q[0].cpu(), state.host[l].view(C, 2, P, Hkv, D), rows, P)
+            got = out[0].float().cpu().double().numpy()
+            assert np.all(np.abs(got - expected) <= 2e-2 + 1e-2 * np.abs(expected)), (step, l)
+    engine.check_status()
+    rows = (state.row_stats - stats0).tolist()
+    assert rows[0] > 0 and rows[1] + rows[2] > 0  # resident, hot and missed rows all occur
