@@ -179,7 +179,8 @@ typedef struct hs_resolve_desc {
                                    stops at the miss count; 0 = the whole RowPlan */
   int32_t split_front;          /* 1 = the front's work may go over several workgroups per request
                                    (three launches instead of one; taken for hot regions above 16384
-                                   rows, where it is faster; HS_RESOLVE_SPLIT=0/1 forces it off/on):
+                                   rows or histories above 40000 tokens, where it measured faster;
+                                   HS_RESOLVE_SPLIT=0/1 forces it off/on):
                                    needs page_bits, a power-of-two page_size <= 32 and a source table
                                    affine with base source[0] (host block = source[0] + page for every
                                    host-backed page, as a request's contiguous host slots are); a

@@ -96,7 +96,9 @@ class BatchedSparseDecode:
         self.entry_capacity = max(union_bound(l, P, self.top, group_heads, self.keep_sink) for l in caps)
         self.width = max(min(self.top * P, l) for l in caps)
         i32, i64 = torch.int32, torch.int64
-        self.pages = torch.empty((B, self.heads, self.top), dtype=i32, device=dev)
+        # the selection's pages [B, heads, top]: this buffer, or a caller's expanded pages
+        # (select_pages), read in place
+        self.pages = self._page_buf = torch.empty((B, self.heads, self.top), dtype=i32, device=dev)
         self.positions = torch.empty((B, self.capacity), dtype=i32, device=dev)
         self.head_columns = torch.empty((B, self.heads, self.width), dtype=i64, device=dev)
         self.union_count = torch.empty(B, dtype=i32, device=dev)
@@ -175,6 +177,7 @@ class BatchedSparseDecode:
                    (ctypes.c_void_p * B)(*[t.data_ptr() for t in maximums]))
             self._bounds[key] = hit
         _, lo, hi = hit
+        self.pages = self._page_buf
         _lib.check(
             lib.hs_quest_topk(
                 q.data_ptr(), q.stride(0), q.stride(1), _lib.dtype_code(q.dtype),
@@ -187,14 +190,21 @@ class BatchedSparseDecode:
         self._build_union(s)
 
     def select_pages(self, pages, stream=None, validate=True):
-        """A selection given as pages: ``pages`` [B, top] int32 on the device, ascending
-        and distinct, min(top, count) of them per request with the tail page last,
-        read by every head.  ``validate`` checks that on the host (a device-to-host
-        copy); a caller that builds its pages that way itself may skip it."""
-        if pages.shape != (self.batch, self.top) or pages.dtype != torch.int32:
-            raise ValueError(f"pages must be int32 [{self.batch}, {self.top}]")
+        """A selection given as pages, read by every head: ``pages`` int32 on the device,
+        [B, top] (copied to every head) or already [B, heads, top] with every head's row
+        the same (read in place, no copy; each request's [heads, top] block contiguous);
+        ascending and distinct, min(top, count) of them per request with the tail page
+        last.  ``validate`` checks that on the host (a device-to-host copy); a caller that
+        builds its pages that way itself may skip it."""
+        expanded = pages.dim() == 3
+        if pages.dtype != torch.int32 or pages.shape != ((self.batch, self.heads, self.top) if expanded
+                                                           else (self.batch, self.top)):
+            raise ValueError(f"pages must be int32 [{self.batch}, {self.top}] or [{self.batch}, {self.heads}, "
+                             f"{self.top}]")
+        if expanded and (pages.stride(2) != 1 or pages.stride(1) != self.top):
+            raise ValueError("each request's [heads, top] pages must be contiguous")
         if validate:
-            host = pages.cpu()
+            host = (pages[:, 0] if expanded else pages).cpu()
             for b, count in enumerate(self.counts):
                 k = min(self.top, count)
                 row = host[b, :k]
@@ -202,7 +212,11 @@ class BatchedSparseDecode:
                     raise ValueError(f"request {b}: pages must be {k} ascending distinct pages below {count}, "
                                      f"the tail page {count - 1} last")
         s = _handle(stream, self.device)
-        self.pages.copy_(pages[:, None, :].expand(self.batch, self.heads, self.top))
+        if expanded:
+            self.pages = pages
+        else:
+            self.pages = self._page_buf
+            self.pages.copy_(pages[:, None, :].expand(self.batch, self.heads, self.top))
         self._build_union(s)
 
     def _build_union(self, s):

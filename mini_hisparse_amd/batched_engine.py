@@ -557,6 +557,7 @@ class BatchedDecodeEngine:
         self._step_start = torch.cuda.Event()
         self._subsets = {}  # sorted slots of a partial batch -> its decoder and buffers
         self._keep_sink, self._top_pages, self._caps = keep_sink, top_pages, caps
+        self._pages_bufs = {}  # per running-set size: the uniform pages copied to every head
         self._resolver_split = resolver_split
         self.current_group = None  # (requests, decoder) the observer's arguments belong to
         self._static_buffers()
@@ -567,6 +568,19 @@ class BatchedDecodeEngine:
     def decoder(self, layer):
         """The decoder (selection, resolver and attention buffers) that serves `layer`."""
         return self.decs[layer] if self.decs is not None else self.dec
+
+    def _heads_pages(self, sampled):
+        """The step's uniform pages [L, n, top] copied to every head, [L, n, heads, top], in
+        one launch: each layer's union build reads its slice in place.  The buffer is
+        reused every step; the step's last attention waits for every layer's gather, so
+        every read of it precedes the next step's copy on the compute stream."""
+        L, n, top = sampled.shape
+        Hq = self.model.config.num_attention_heads
+        buf = self._pages_bufs.get(n)
+        if buf is None:
+            buf = self._pages_bufs[n] = torch.empty((L, n, Hq, top), dtype=torch.int32, device=self.device)
+        buf.copy_(sampled[:, :, None, :].expand(L, n, Hq, top))
+        return buf
 
     def _prefetch(self, index, sampled, transfer, mark):
         """Layer `index`'s select, resolve and gather on `transfer`; returns its stage
@@ -870,8 +884,8 @@ class BatchedDecodeEngine:
             d.set_lengths([p + 1 for p in positions])
         sampled = None
         if self.selector == "uniform":
-            sampled = uniform_pages([p + 1 for p in positions], st.config.page_size, dec.top, st.layers,
-                                    self._sampler, self.device)
+            sampled = self._heads_pages(uniform_pages([p + 1 for p in positions], st.config.page_size, dec.top,
+                                                      st.layers, self._sampler, self.device))
         compute = torch.cuda.current_stream(self.device)
         L = st.layers
 
@@ -1009,8 +1023,8 @@ class BatchedDecodeEngine:
         dec.set_lengths([positions[b] + 1 for b in slots])
         sampled = None
         if self.selector == "uniform":
-            sampled = uniform_pages([positions[b] + 1 for b in slots], st.config.page_size, dec.top, st.layers,
-                                    self._sampler, self.device)
+            sampled = self._heads_pages(uniform_pages([positions[b] + 1 for b in slots], st.config.page_size,
+                                                      dec.top, st.layers, self._sampler, self.device))
         compute = torch.cuda.current_stream(self.device)
         handle = _lib.stream_handle(self.device)
         if self._prepared is None:

@@ -1381,7 +1381,7 @@ static int resolve_launch(const hs_resolve_desc* descs, int32_t count, char* wor
   for (int32_t start = 0; start < count; start += RMAXB) {
     ResolveBatch batch{};
     batch.count = count - start < RMAXB ? count - start : RMAXB;
-    int64_t front_lds = 0, max_out = 0, max_hot = 0;
+    int64_t front_lds = 0, max_out = 0, max_hot = 0, max_len = 0;
     bool pow2 = true;  // every descriptor's page size a power of two
     for (int i = 0; i < batch.count; ++i) {
       hs_resolve_desc& d = batch.d[i];
@@ -1391,19 +1391,23 @@ static int resolve_launch(const hs_resolve_desc* descs, int32_t count, char* wor
       if (front_lds_bytes(d.length, d.hot_rows) > front_lds) front_lds = front_lds_bytes(d.length, d.hot_rows);
       pow2 &= (d.page_size & (d.page_size - 1)) == 0;
       if (d.hot_rows > max_hot) max_hot = d.hot_rows;
+      if (d.length > max_len) max_len = d.length;
       const int64_t outs = d.n + (d.head_columns ? d.heads * d.width : 0);
       if (outs > max_out) max_out = outs;
     }
     const unsigned nb = static_cast<unsigned>(batch.count);
     const size_t lds = static_cast<size_t>(front_lds);
     const bool l16 = batch.d[0].lru_i16 != 0;  // the same for every descriptor (validated)
-    // The split front where it measured faster: hot regions above 16384 rows (the 7B
-    // layer shape: 30.4 us for its three launches against 37.5 us for the one-workgroup
-    // front; the 0.5B layer shape, 13504 rows: 21.7 against 19.3 us); HS_RESOLVE_SPLIT=0 / 1
-    // forces either way for descriptors that allow it (read per call).
+    // The split front where it measured faster: hot regions above 16384 rows or histories
+    // above 40000 tokens (7B layer shape, 32768 rows and 131072 tokens: 30.4 us for its three
+    // launches against 37.5 us for the one-workgroup front; 32B stress shape, 2048 rows and
+    // 65536 tokens: the resolve stage 4.20 -> 3.47 ms per step; 0.5B layer shape, 13504 rows
+    // and 32768 tokens: 21.7 against 19.3 us, so it keeps the one-workgroup front).
+    // HS_RESOLVE_SPLIT=0 / 1 forces either way for descriptors that allow it (read per call).
     const char* split_env = getenv("HS_RESOLVE_SPLIT");
     const int split_force = split_env ? atoi(split_env) : -1;
-    const bool split = batch.d[0].split_front && (split_force == 1 || (split_force != 0 && max_hot > 16 * RT));
+    const bool large = max_hot > 16 * RT || max_len > 40000;
+    const bool split = batch.d[0].split_front && (split_force == 1 || (split_force != 0 && large));
     if (split) {
       // workgroups per request: about one round of 256 in all, and at least enough for
       // SPLIT_SLOTS hot slots per thread
