@@ -1293,6 +1293,23 @@ def run_model_workload(args, torch, device):
     row_bytes = 2 * wl.kv_heads * D * e
     gather_bytes = misses * row_bytes
     link = host_link_gbs(torch, device)
+    # the step's floor: the HBM bytes it must move (weights once per request group, the
+    # Quest bounds of every page, the attention's rows, the gathered rows written) at
+    # 8 TB/s, or the gathered rows at the measured host-link rate, whichever is longer
+    embed = model.model.embed_tokens.weight
+    tied = model.lm_head.weight.data_ptr() == embed.data_ptr()
+    weight_bytes = sum(t.numel() * t.element_size() for t in model.parameters()
+                       if tied or t.data_ptr() != embed.data_ptr())
+    pages_read = sum(ceil(state.lengths[b] / wl.page_size) for b in range(wl.batch)) * wl.layers
+    hbm_bytes = (weight_bytes * (len(engine.groups) if engine.groups else 1) + pages_read * 2 * wl.kv_heads * D * e
+                 + att_bytes / args.steps + gather_bytes)
+    hbm_ms, host_ms = hbm_bytes / (HBM_PEAK_GBS * 1e9) * 1e3, gather_bytes / (link * 1e9) * 1e3
+    step_roofline = {"hbm_bytes": hbm_bytes, "host_link_bytes": gather_bytes, "hbm_ms": hbm_ms,
+                     "host_link_ms": host_ms, "bound": "host link" if host_ms > hbm_ms else "hbm",
+                     "frac": max(hbm_ms, host_ms) / ms_per_step,
+                     "how": "max(HBM bytes / 8 TB/s, gathered bytes / measured pinned memcpy rate) / ms_per_step; "
+                            "HBM bytes: weights (once per request group), every page's Quest bounds, the "
+                            "attention's rows, the gathered rows written"}
     copy = hbm_copy_gbs(torch, device)  # also the counter runs' calibration kernel
     result = {
         "metric": METRIC,
@@ -1351,6 +1368,7 @@ def run_model_workload(args, torch, device):
             "us_per_launch": att_ms * 1e3 / launches,
             "in_order": solo_line,
         },
+        "step_roofline": step_roofline,
         "device_loop": device_loop,
         "stages_ms_per_step": stage_ms,
         "projections_on_hs_skinny_gemm": engine.projection_kernel,

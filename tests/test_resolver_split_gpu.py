@@ -110,7 +110,7 @@ def test_split_front_batches_match_oracle(gpu, lru_dtype, count):
     request) of mixed shapes, every other one with the prefix-only miss plan."""
     rng = np.random.default_rng(1000 + count)
     shapes = [(5000, 16, 2048, 60), (131072, 16, 32768, 900), (64, 4, 64, 16), (40000, 32, 13504, 200),
-              (2048, 1, 256, 300), (777, 8, 512, 30)]
+              (2048, 1, 256, 300), (777, 8, 330, 30), (3001, 2, 1000, 400)]
     cases = []
     for i in range(count):
         length, P, S, sel = shapes[(i + count) % len(shapes)]
