@@ -283,6 +283,23 @@ int hs_append_rows(const void* k, const void* v, int64_t kv_stride_b, void* pool
                    hs_stream_t stream);
 
 /*
+ * hs_rotary_split (below) and hs_append_rows in one launch: the decode step's
+ * rotary embedding of the q|k|v projection output and the append of the rotated
+ * K row and the V row of each of `rows` (request, layer) pairs to its pool row, its
+ * host mirror row and its tail page's bounds.  Replaces the same reference steps as
+ * the two calls it fuses (model.py:183-226's rotary; storage.py:246-319's single-token
+ * append); every output holds the bits the two calls give.  Arguments: those of
+ * hs_rotary_split, then those of hs_append_rows for the same rows (k and v are the
+ * rotary's outputs, so no k/v source is passed).
+ */
+int hs_rotary_split_append(const void* qkv, int64_t qkv_stride, void* q, void* k, void* v,
+                           const int64_t* positions, int64_t rows, int64_t heads, int64_t kv_heads,
+                           int64_t head_dim, float theta, int32_t dtype, void* pool, int64_t pool_rows,
+                           int64_t page_size, const int64_t* device_rows, const void* const* host_alias,
+                           const int64_t* host_rows, int64_t host_pool_rows, void* const* minimum,
+                           void* const* maximum, hs_stream_t stream);
+
+/*
  * A write of `tokens` consecutive K/V rows to one (request, layer) whose page
  * placement the caller has decided: the page loop of HostStore.append
  * (mini_hisparse/storage.py:273-318) -- prefill or decode -- in one launch per 64

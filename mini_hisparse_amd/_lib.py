@@ -97,6 +97,12 @@ SIGNATURES = {
          POINTER(c_int64), POINTER(c_void_p), POINTER(c_int64), c_int64, POINTER(c_void_p),
          POINTER(c_void_p), c_int32, c_void_p],
     ),
+    "hs_rotary_split_append": (
+        c_int,
+        [c_void_p, c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int64, c_float,
+         c_int32, c_void_p, c_int64, c_int64, POINTER(c_int64), POINTER(c_void_p), POINTER(c_int64), c_int64,
+         POINTER(c_void_p), POINTER(c_void_p), c_void_p],
+    ),
     "hs_append_tokens": (
         c_int,
         [c_void_p, c_void_p, c_int64, c_int64, c_void_p, c_int64, c_void_p, c_int64, c_int32,

@@ -471,7 +471,8 @@ class BatchedDecodeEngine:
 
     def __init__(self, model: MiniModel, state: SparseKVState, top_pages, *, max_tokens=None, keep_sink=True,
                  selector="quest", seed=0, graphs=False, projections="auto", transfer_stream=False,
-                 prefetch=None, request_groups=1, group_gather_workgroups=0, resolver_split=True):
+                 prefetch=None, request_groups=1, group_gather_workgroups=0, resolver_split=True,
+                 fuse_rotary_append=True):
         """``selector``: "quest" (per-head Quest pages over the bounds) or "uniform"
         (:func:`uniform_pages`, shared by every head, resampled each step).  ``graphs``:
         replay the dense part of each layer boundary as a HIP graph (when every per-layer
@@ -495,7 +496,9 @@ class BatchedDecodeEngine:
         gather's workgroups per request there (0: the library's default).
         ``resolver_split``: the resolver's front over several workgroups per request
         (``hs_resolve_desc.split_front``; the state's source tables are affine by
-        construction), else one workgroup per request."""
+        construction), else one workgroup per request.  ``fuse_rotary_append``: each
+        layer's rotary embedding and the append of its new K/V rows in one launch
+        (``hs_rotary_split_append``) where the dense launches are not graph-replayed."""
         if prefetch is None:
             prefetch = selector == "uniform"
         if prefetch and selector != "uniform":
@@ -557,6 +560,7 @@ class BatchedDecodeEngine:
         self._step_start = torch.cuda.Event()
         self._subsets = {}  # sorted slots of a partial batch -> its decoder and buffers
         self._keep_sink, self._top_pages, self._caps = keep_sink, top_pages, caps
+        self.fuse_rotary_append = fuse_rotary_append
         self._pages_bufs = {}  # per running-set size: the uniform pages copied to every head
         self._resolver_split = resolver_split
         self.current_group = None  # (requests, decoder) the observer's arguments belong to
@@ -832,6 +836,22 @@ class BatchedDecodeEngine:
             "hs_append_rows",
         )
 
+    def _rotary_append(self, layer, positions, handle):
+        """Layer ``layer``'s rotary embedding of the q|k|v projection and the append of every
+        request's new K/V row, in one launch (hs_rotary_split_append)."""
+        st, cfg, mc = self.state, self.state.config, self.model.config
+        dev_rows, host_rows, lo, hi = st.append_args(layer, positions)
+        _lib.check(
+            _lib.load().hs_rotary_split_append(
+                self._qkv.data_ptr(), self._qkv.stride(0), self._q.data_ptr(), self._k.data_ptr(),
+                self._v.data_ptr(), self.positions.data_ptr(), st.batch, mc.num_attention_heads,
+                mc.num_key_value_heads, mc.head_dim, mc.rope_theta, _lib.dtype_code(cfg.dtype), st.pool.data_ptr(),
+                st.blocks * cfg.page_size, cfg.page_size, dev_rows, self._host_alias[layer], host_rows,
+                st.host[layer].shape[0] * cfg.page_size, lo, hi, handle,
+            ),
+            "hs_rotary_split_append",
+        )
+
     def decoders(self):
         """Every decoder the engine has built (whole batch, per layer, request groups,
         partial batches)."""
@@ -913,11 +933,14 @@ class BatchedDecodeEngine:
                 self._prepared = self._prepare_boundaries()
             prepared = self._prepared
 
+        # the rotary launch (the last of a boundary before a layer) fused with the append
+        fuse = self.fuse_rotary_append and graphs is None and prepared is not None
+
         def boundary(index):
             if graphs is not None:
                 graphs[index].replay()
             elif prepared is not None:
-                for launch in prepared[index]:
+                for launch in prepared[index][:-1] if fuse and index < L else prepared[index]:
                     launch(handle)
             else:
                 self._boundary(index)
@@ -930,7 +953,10 @@ class BatchedDecodeEngine:
             boundary(index)
             marks["dense"].append(mark(compute))
             marks["append"] = [marks["dense"][1]]
-            self._append(index, k, v, positions, handle=handle)
+            if fuse:  # with the layer's rotary: the append stage holds it
+                self._rotary_append(index, positions, handle)
+            else:
+                self._append(index, k, v, positions, handle=handle)
             lo, hi = st.bounds[index]
             marks["append"].append(mark(compute))
             if prefetched is not None:

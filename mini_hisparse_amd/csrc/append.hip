@@ -40,13 +40,8 @@ __device__ __forceinline__ float from_storage(unsigned short bits) {
 template <int DT>
 __device__ __forceinline__ void bound_update(const unsigned short* newv, unsigned short* lo, unsigned short* hi,
                                              int n) {
-  for (int e = 0; e < n; ++e) {
-    const float x = from_storage<DT>(newv[e]);
-    const float a = from_storage<DT>(lo[e]);
-    const float b = from_storage<DT>(hi[e]);
-    if (!(a != a) && (x != x || !(a < x))) lo[e] = newv[e];
-    if (!(b != b) && (x != x || !(b > x))) hi[e] = newv[e];
-  }
+  for (int e = 0; e < n; ++e)
+    bound16_take(lo + e, hi + e, newv[e], from_storage<DT>(newv[e]), from_storage<DT>(lo[e]), from_storage<DT>(hi[e]));
 }
 
 template <int DT>
@@ -78,20 +73,88 @@ __global__ __launch_bounds__(AT) void append_kernel(AppendArgs a) {
       float* lo = reinterpret_cast<float*>(a.kmin[b] + u * 16);
       float* hi = reinterpret_cast<float*>(a.kmax[b] + u * 16);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float x = __uint_as_float(kx[e]);
-        const float a = lo[e], b = hi[e];
-        const bool zero_tie = x == 0.f && a == 0.f;  // both zeros: -0 is the smaller
-        if (!(a != a) && (x != x || x < a || (zero_tie && signbit(x) && !signbit(a)))) lo[e] = x;
-        const bool zero_tie_hi = x == 0.f && b == 0.f;
-        if (!(b != b) && (x != x || x > b || (zero_tie_hi && !signbit(x) && signbit(b)))) hi[e] = x;
-      }
+      for (int e = 0; e < 4; ++e) bound32_take(lo + e, hi + e, __uint_as_float(kx[e]));
     } else {
       unsigned short nv[8];
       __builtin_memcpy(nv, &kx, 16);
       bound_update<DT>(nv, reinterpret_cast<unsigned short*>(a.kmin[b] + u * 16),
                        reinterpret_cast<unsigned short*>(a.kmax[b] + u * 16), 8);
     }
+  }
+}
+
+// The rotary + split of a q|k|v projection (rotary_split_kernel's arithmetic) fused
+// with the append of the new K and V rows (append_kernel's): grid (heads + 2 kv_heads,
+// rows), one thread per rotation pair.  q heads are rotated into q; k heads are rotated
+// into k, the pool row and the host mirror, and fold into the tail page's bounds; v
+// heads are copied to v, the pool row and the host mirror.  Every element goes out
+// through the same store as the k / v buffers, so the pool, the mirror and the bounds
+// hold the bits the separate launches give.
+struct RotaryArgs {
+  const void* qkv;
+  int64_t qkv_stride;
+  void* q;
+  void* k;
+  void* v;
+  const int64_t* positions;
+  int64_t heads, kv_heads, D;
+  float theta;
+};
+
+template <int DT>
+__device__ __forceinline__ unsigned short bits_of(float v) {
+  if constexpr (DT == HS_DTYPE_BF16) return f32_to_bf16_bits(v);
+  else return f32_to_f16_bits(v);
+}
+
+template <int DT>
+__device__ __forceinline__ void append_elem(const AppendArgs& a, int row, int64_t pk, int64_t hk, int64_t bound,
+                                            float x, bool is_k) {
+  store_elem<DT>(a.pool, pk, x);
+  if (hk >= 0) store_elem<DT>(a.host[row], hk, x);
+  if (!is_k) return;
+  if constexpr (DT == HS_DTYPE_F32) {
+    bound32_take(reinterpret_cast<float*>(a.kmin[row]) + bound, reinterpret_cast<float*>(a.kmax[row]) + bound, x);
+  } else {
+    unsigned short* lo = reinterpret_cast<unsigned short*>(a.kmin[row]) + bound;
+    unsigned short* hi = reinterpret_cast<unsigned short*>(a.kmax[row]) + bound;
+    const unsigned short xb = bits_of<DT>(x);
+    bound16_take(lo, hi, xb, from_storage<DT>(xb), from_storage<DT>(*lo), from_storage<DT>(*hi));
+  }
+}
+
+template <int DT>
+__global__ __launch_bounds__(AT) void rotary_append_kernel(RotaryArgs r, AppendArgs a) {
+  const int64_t h = blockIdx.x;
+  const int row = blockIdx.y;
+  const int64_t D = r.D, half = D / 2, Hkv = r.kv_heads;
+  const int64_t src = row * r.qkv_stride + h * D;
+  const bool is_q = h < r.heads, is_k = !is_q && h < r.heads + Hkv;
+  const int64_t kvh = is_q ? 0 : (is_k ? h - r.heads : h - r.heads - Hkv);
+  void* dst = is_q ? r.q : (is_k ? r.k : r.v);
+  const int64_t doff = is_q ? (row * r.heads + h) * D : (row * Hkv + kvh) * D;
+  // the row's K (or V) segment in the pool and the host mirror ([block, 2, P, Hkv, D])
+  const int64_t P = a.P, plane = P * Hkv * D, seg = kvh * D + (is_k ? 0 : plane);
+  const int64_t dr = a.dev_row[row], hr = a.host_row[row];
+  const int64_t pk = ((dr / P) * 2 * P + dr % P) * Hkv * D + seg;
+  const int64_t hk = hr >= 0 ? ((hr / P) * 2 * P + hr % P) * Hkv * D + seg : -1;
+  if (!is_q && !is_k) {
+    for (int64_t d = threadIdx.x; d < D; d += blockDim.x) {
+      const float x = load_elem<DT>(r.qkv, src + d);
+      store_elem<DT>(dst, doff + d, x);
+      append_elem<DT>(a, row, pk + d, hk >= 0 ? hk + d : -1, 0, x, false);
+    }
+    return;
+  }
+  const float pos = static_cast<float>(r.positions[row]);
+  for (int64_t i = threadIdx.x; i < half; i += blockDim.x) {
+    float lo, hi;
+    rotary_pair<DT>(load_elem<DT>(r.qkv, src + i), load_elem<DT>(r.qkv, src + i + half), pos, i, D, r.theta, lo, hi);
+    store_elem<DT>(dst, doff + i, lo);
+    store_elem<DT>(dst, doff + i + half, hi);
+    if (!is_k) continue;
+    append_elem<DT>(a, row, pk + i, hk >= 0 ? hk + i : -1, kvh * D + i, round_to<DT>(lo), true);
+    append_elem<DT>(a, row, pk + i + half, hk >= 0 ? hk + i + half : -1, kvh * D + i + half, round_to<DT>(hi), true);
   }
 }
 
@@ -170,6 +233,62 @@ extern "C" int hs_append_rows(const void* k, const void* v, int64_t kv_stride_b,
                                 host_alias ? host_alias + s0 : nullptr, host_rows ? host_rows + s0 : nullptr,
                                 host_pool_rows, minimum + s0, maximum + s0, c, stream);
     if (rc != HS_OK) return rc;
+  }
+  return HS_OK;
+}
+
+extern "C" int hs_rotary_split_append(const void* qkv, int64_t qkv_stride, void* q, void* k, void* v,
+                                      const int64_t* positions, int64_t rows, int64_t heads, int64_t kv_heads,
+                                      int64_t head_dim, float theta, int32_t dtype, void* pool, int64_t pool_rows,
+                                      int64_t page_size, const int64_t* device_rows, const void* const* host_alias,
+                                      const int64_t* host_rows, int64_t host_pool_rows, void* const* minimum,
+                                      void* const* maximum, hipStream_t stream) {
+  HS_CHECK_ARG(valid_dtype(dtype), "invalid dtype code %d", dtype);
+  HS_CHECK_ARG(rows >= 1 && rows <= 65535 && heads >= 1 && kv_heads >= 1 && head_dim >= 2 && head_dim % 2 == 0,
+               "invalid rotary shape");
+  HS_CHECK_ARG(qkv_stride >= (heads + 2 * kv_heads) * head_dim, "q|k|v row stride below its width");
+  HS_CHECK_ARG(qkv && q && k && v && positions && pool && device_rows && minimum && maximum,
+               "null rotary/append pointer");
+  HS_CHECK_ARG(page_size >= 1, "invalid append shape");
+  for (int64_t i = 0; i < rows; ++i) {  // every row, before the first launch
+    HS_CHECK_ARG(device_rows[i] >= 0 && device_rows[i] < pool_rows, "append device row %lld outside the pool",
+                 static_cast<long long>(device_rows[i]));
+    HS_CHECK_ARG(!host_rows || host_rows[i] < host_pool_rows, "append host row %lld outside the host pool",
+                 static_cast<long long>(host_rows[i]));
+    HS_CHECK_ARG(minimum[i] && maximum[i], "null bounds pointer");
+    HS_CHECK_ARG(!host_rows || host_rows[i] < 0 || (host_alias && host_alias[i]), "a host row needs a host alias");
+  }
+  const int64_t esz = elem_bytes(dtype);
+  const unsigned threads = head_dim / 2 >= AT ? AT : static_cast<unsigned>(((head_dim / 2 + 63) / 64) * 64);
+  for (int64_t s0 = 0; s0 < rows; s0 += AMAXB) {
+    const int32_t c = rows - s0 < AMAXB ? static_cast<int32_t>(rows - s0) : AMAXB;
+    RotaryArgs r{};
+    r.qkv = static_cast<const char*>(qkv) + s0 * qkv_stride * esz;
+    r.qkv_stride = qkv_stride;
+    r.q = static_cast<char*>(q) + s0 * heads * head_dim * esz;
+    r.k = static_cast<char*>(k) + s0 * kv_heads * head_dim * esz;
+    r.v = static_cast<char*>(v) + s0 * kv_heads * head_dim * esz;
+    r.positions = positions + s0;
+    r.heads = heads;
+    r.kv_heads = kv_heads;
+    r.D = head_dim;
+    r.theta = theta;
+    AppendArgs a{};
+    a.pool = static_cast<char*>(pool);
+    a.P = page_size;
+    a.row_bytes = kv_heads * head_dim * esz;
+    for (int32_t i = 0; i < c; ++i) {
+      a.dev_row[i] = device_rows[s0 + i];
+      a.host_row[i] = host_rows ? host_rows[s0 + i] : -1;
+      a.host[i] = host_alias ? static_cast<char*>(const_cast<void*>(host_alias[s0 + i])) : nullptr;
+      a.kmin[i] = static_cast<char*>(minimum[s0 + i]);
+      a.kmax[i] = static_cast<char*>(maximum[s0 + i]);
+    }
+    const dim3 grid(static_cast<unsigned>(heads + 2 * kv_heads), static_cast<unsigned>(c));
+    if (dtype == HS_DTYPE_BF16) hipLaunchKernelGGL(rotary_append_kernel<HS_DTYPE_BF16>, grid, dim3(threads), 0, stream, r, a);
+    else if (dtype == HS_DTYPE_F16) hipLaunchKernelGGL(rotary_append_kernel<HS_DTYPE_F16>, grid, dim3(threads), 0, stream, r, a);
+    else hipLaunchKernelGGL(rotary_append_kernel<HS_DTYPE_F32>, grid, dim3(threads), 0, stream, r, a);
+    HS_CHECK_LAUNCH("rotary_split_append");
   }
   return HS_OK;
 }

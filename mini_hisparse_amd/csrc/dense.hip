@@ -26,13 +26,6 @@ namespace hs {
 
 constexpr int DN_T = 256;
 
-template <int DT>
-__device__ __forceinline__ float round_to(float v) {
-  if constexpr (DT == HS_DTYPE_F32) return v;
-  else if constexpr (DT == HS_DTYPE_BF16) return bf16_bits_to_f32(f32_to_bf16_bits(v));
-  else return f16_bits_to_f32(f32_to_f16_bits(v));
-}
-
 // One workgroup per row.  `delta` may be null (no residual add); `x_out` may
 // alias `x`.  A row of at most NR_REG * DN_T elements is held in registers: every
 // load of x, delta and the weight is issued before the first is used, so the row
@@ -170,13 +163,10 @@ __global__ __launch_bounds__(DN_T) void rotary_split_kernel(const void* qkv, int
   }
   const float pos = static_cast<float>(positions[row]);
   for (int64_t i = threadIdx.x; i < half; i += blockDim.x) {
-    // inv_freq = theta ** (-(2i) / D), angle = position * inv_freq (fp32, as model.py's rotary)
-    const float inv = powf(theta, -(static_cast<float>(2 * i) / static_cast<float>(D)));
-    const float angle = pos * inv;
-    const float c = round_to<DT>(cosf(angle)), s = round_to<DT>(sinf(angle));
-    const float a = load_elem<DT>(qkv, src + i), b = load_elem<DT>(qkv, src + i + half);
-    store_elem<DT>(dst, doff + i, round_to<DT>(a * c) + round_to<DT>(-b * s));
-    store_elem<DT>(dst, doff + i + half, round_to<DT>(b * c) + round_to<DT>(a * s));
+    float lo, hi;
+    rotary_pair<DT>(load_elem<DT>(qkv, src + i), load_elem<DT>(qkv, src + i + half), pos, i, D, theta, lo, hi);
+    store_elem<DT>(dst, doff + i, lo);
+    store_elem<DT>(dst, doff + i + half, hi);
   }
 }
 

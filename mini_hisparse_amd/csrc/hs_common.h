@@ -2,6 +2,7 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+#include <math.h>
 #include <stdint.h>
 
 #include "hisparse.h"
@@ -76,6 +77,46 @@ __device__ __forceinline__ void store_elem(void* base, int64_t i, float v) {
   } else {
     static_cast<unsigned short*>(base)[i] = f32_to_f16_bits(v);
   }
+}
+
+// v rounded to the storage dtype (float32: unchanged).
+template <int DT>
+__device__ __forceinline__ float round_to(float v) {
+  if constexpr (DT == HS_DTYPE_F32) return v;
+  else if constexpr (DT == HS_DTYPE_BF16) return bf16_bits_to_f32(f32_to_bf16_bits(v));
+  else return f16_bits_to_f32(f32_to_f16_bits(v));
+}
+
+// The rotary pair (x_i, x_{i + D/2}) of a head vector at position `pos` with base
+// `theta`, as the model's rotary computes it: inv_freq = theta ** (-(2i) / D) and the
+// angle in fp32, cos/sin rounded to the dtype, each product rounded, then the sum
+// (which the caller's store rounds).
+template <int DT>
+__device__ __forceinline__ void rotary_pair(float a, float b, float pos, int64_t i, int64_t D, float theta,
+                                            float& lo, float& hi) {
+  const float inv = powf(theta, -(static_cast<float>(2 * i) / static_cast<float>(D)));
+  const float angle = pos * inv;
+  const float c = round_to<DT>(cosf(angle)), s = round_to<DT>(sinf(angle));
+  lo = round_to<DT>(a * c) + round_to<DT>(-b * s);
+  hi = round_to<DT>(b * c) + round_to<DT>(a * s);
+}
+
+// A Quest bound element taking a new K element, as torch.minimum / torch.maximum
+// compute it on this device: a NaN operand is returned (the existing bound first);
+// 16-bit types return old < new ? old : new (so an equal compare -- +0 vs -0
+// included -- returns the new element); float32 orders -0 below +0.  `x` is the new
+// element as stored (`xbits` its 16-bit pattern).
+__device__ __forceinline__ void bound16_take(unsigned short* lo, unsigned short* hi, unsigned short xbits, float x,
+                                             float a, float b) {
+  if (!(a != a) && (x != x || !(a < x))) *lo = xbits;
+  if (!(b != b) && (x != x || !(b > x))) *hi = xbits;
+}
+__device__ __forceinline__ void bound32_take(float* lo, float* hi, float x) {
+  const float a = *lo, b = *hi;
+  const bool zero_tie = x == 0.f && a == 0.f;  // both zeros: -0 is the smaller
+  if (!(a != a) && (x != x || x < a || (zero_tie && signbit(x) && !signbit(a)))) *lo = x;
+  const bool zero_tie_hi = x == 0.f && b == 0.f;
+  if (!(b != b) && (x != x || x > b || (zero_tie_hi && !signbit(x) && signbit(b)))) *hi = x;
 }
 
 inline int elem_bytes(int dtype) { return dtype == HS_DTYPE_F32 ? 4 : 2; }

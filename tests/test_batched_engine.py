@@ -477,3 +477,46 @@ def test_full_7b_step_matches_oracle_on_every_layer(gpu):
     engine.check_status()
     rows = (state.row_stats - stats0).tolist()
     assert rows[0] > 0 and rows[1] + rows[2] > 0  # resident, hot and missed rows all occur
+
+
+@pytest.mark.gpu
+def test_fused_rotary_append_equals_the_separate_launches(gpu):
+    """hs_rotary_split_append (the engine's default) against hs_rotary_split followed by
+    hs_append_rows: over four steps (one crossing a page boundary) the tokens, the pool,
+    the host mirror and the Quest bounds are bit-identical."""
+    from mini_hisparse_amd.batched_engine import BatchedDecodeEngine, build_state, random_model
+
+    wl = tiny(context=40 * 16 - 2)
+    print(f"[case] fused rotary+append: {wl}", flush=True)
+    runs = []
+    for fused in (True, False):
+        model, state = random_model(wl, gpu, seed=1), build_state(wl, gpu, seed=2)
+        engine = BatchedDecodeEngine(model, state, wl.top_pages, fuse_rotary_append=fused)
+        tokens = torch.arange(1, wl.batch + 1, device=gpu)
+        seq = []
+        for _ in range(4):
+            tokens = engine.step(tokens)
+            seq.append(tokens.clone())
+        torch.cuda.synchronize()
+        runs.append((seq, state))
+    (seq_a, a), (seq_b, b) = runs
+    assert all(torch.equal(x, y) for x, y in zip(seq_a, seq_b))
+    # the rows the four appends wrote, in the pool (the tail blocks, placed alike) and in
+    # the host mirror; the bounds of every page
+    P, C, B = wl.page_size, a.pages, wl.batch
+    for l in range(wl.layers):
+        assert a.tail_block[l] == b.tail_block[l]
+        pool_a, pool_b = a.pool.view(-1, 2, P, wl.kv_heads, wl.head_dim), b.pool.view(-1, 2, P, wl.kv_heads, wl.head_dim)
+        host_a = a.host[l].view(-1, 2, P, wl.kv_heads, wl.head_dim)
+        host_b = b.host[l].view(-1, 2, P, wl.kv_heads, wl.head_dim)
+        for r in range(B):
+            for pos in range(wl.context, wl.context + 4):
+                page, off = divmod(pos, P)
+                hb = r * C + page
+                assert torch.equal(host_a[hb, :, off].view(torch.int16).cpu(), host_b[hb, :, off].view(torch.int16).cpu())
+            blk = a.tail_block[l][r]
+            for pos in range((wl.context + 3) // P * P, wl.context + 4):  # the current tail page's new rows
+                off = pos % P
+                assert torch.equal(pool_a[blk, :, off].view(torch.int16), pool_b[blk, :, off].view(torch.int16))
+    assert torch.equal(a.minimum.view(torch.int16), b.minimum.view(torch.int16))
+    assert torch.equal(a.maximum.view(torch.int16), b.maximum.view(torch.int16))

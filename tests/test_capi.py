@@ -114,6 +114,27 @@ def test_resolver_lru_dtype_rules_without_a_gpu():
     assert b"workspace too small" in lib.hs_last_error()
 
 
+def test_rotary_split_append_argument_errors_without_a_gpu():
+    """Rejected on the host before any launch: a bad shape, a device row outside the
+    pool, a host row without its host alias."""
+    from ctypes import c_int64, c_void_p
+
+    lib = _lib.load()
+    rows = (c_int64 * 2)(0, 5)
+    host = (c_int64 * 2)(3, 4)
+    alias = (c_void_p * 2)(0x1000, 0x2000)
+    bounds = (c_void_p * 2)(0x3000, 0x4000)
+    p = [0x10000 * i for i in range(1, 7)]
+
+    def call(head_dim=64, dev=rows, alias_=alias, pool_rows=16):
+        return lib.hs_rotary_split_append(p[0], (8 + 4) * head_dim, p[1], p[2], p[3], p[4], 2, 8, 2, head_dim, 1e6,
+                                          2, p[5], pool_rows, 16, dev, alias_, host, 64, bounds, bounds, None)
+
+    assert call(head_dim=63) == -1 and b"invalid rotary shape" in lib.hs_last_error()
+    assert call(pool_rows=4) == -1 and b"outside the pool" in lib.hs_last_error()
+    assert call(alias_=None) == -1 and b"host alias" in lib.hs_last_error()
+
+
 def test_resolver_split_front_rules_without_a_gpu():
     """The split front needs a union page bitmap and a power-of-two page of at most 32
     tokens, and one setting per batch; all rejected on the host."""
