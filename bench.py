@@ -247,7 +247,8 @@ def build_workload(args, torch, device):
     cfg = CacheConfig(gpu_pages=blocks, host_pages=B * C, page_size=P, kv_heads=Hkv, head_dim=D, device=device, dtype=torch.bfloat16)
     dec = BatchedSparseDecode(cfg, S.heads, S.top, [L] * B, device=device,
                               split_front=args.resolver_front == "split")  # request b's host pages: b C + page
-    pipe = PipelinedSparseDecode(cfg, S.heads, S.top, [L] * B, parts=args.parts, device=device)
+    pipe = PipelinedSparseDecode(cfg, S.heads, S.top, [L] * B, parts=args.parts, device=device,
+                                 split_front=args.resolver_front == "split")
     return dict(
         cfg=cfg, dec=dec, pipe=pipe, q=q, kmin=kmin, kmax=kmax, host=host, alias=MappedHost(host), pool=pool,
         tables=tables, tags_all=tags_all, lru_all=lru_all, tags0=tags_all.clone(), lru0=lru_all.clone(),
@@ -1491,7 +1492,10 @@ def run_microbench(args, torch, device):
                               event_window_ms=stages["attention_event_window"]),
         "quest_and_union": hbm_line("quest_and_union", bytes_["quest"],
                                     ("quest_score", "quest_topk_kernel", "build_union_kernel")),
-        "resolve": hbm_line("resolve", bytes_["resolver"], ("resolve_front_kernel", "resolve_outputs_kernel")),
+        # the split front's three launches at these lengths (above 40,000 tokens), else the one front launch
+        "resolve": hbm_line("resolve", bytes_["resolver"],
+                            ("resolve_split", "resolve_outputs_kernel") if args.resolver_front == "split"
+                            else ("resolve_front_kernel", "resolve_outputs_kernel")),
         "gather": {"ms": stages["gather"], "bytes": bytes_["gather"],
                    "GBps": bytes_["gather"] / (stages["gather"] * 1e-3) / 1e9,
                    "host_link_memcpy_GBps": link,

@@ -412,11 +412,12 @@ class PipelinedSparseDecode:
     the compute stream selects and resolves group g+1; group g's attention runs
     while later groups gather.  Each group is a :class:`BatchedSparseDecode`
     with its own buffers; per group the stream and event order is that of
-    ``BatchedSparseDecode.step``.
+    ``BatchedSparseDecode.step``.  ``split_front`` is passed to every group (the
+    resolver's multi-workgroup front, for affine source tables).
     """
 
     def __init__(self, config, heads, top_pages, lengths, *, parts=2, keep_sink=True, device="cuda",
-                 capacity_lengths=None):
+                 capacity_lengths=None, split_front=False):
         lengths = list(lengths)
         caps = list(capacity_lengths or lengths)
         parts = max(1, min(parts, len(lengths)))
@@ -424,7 +425,7 @@ class PipelinedSparseDecode:
         self.slices = [slice(bounds[i], bounds[i + 1]) for i in range(parts)]
         self.parts = [
             BatchedSparseDecode(config, heads, top_pages, lengths[s], keep_sink=keep_sink, device=device,
-                                capacity_lengths=caps[s])
+                                capacity_lengths=caps[s], split_front=split_front)
             for s in self.slices
         ]
         self.batch = len(lengths)

@@ -168,3 +168,68 @@ def test_qwen32b_stress_layer_shape_matches_oracle(gpu):
                         resident_frac=0.4, selector="uniform", steps=3, seed=71)
     selected = totals.sum()
     assert 0.45 < totals[2] / selected < 0.75, totals  # the miss-heavy regime
+
+
+def test_pipelined_groups_with_split_front_match_one_batch(gpu, monkeypatch):
+    """``PipelinedSparseDecode`` (two request groups, transfer stream, split resolver
+    front forced on) against one ``BatchedSparseDecode`` of the whole batch with the
+    single-workgroup front, from identical tables, pool and queries, over two steps
+    that carry the tags and LRU: the same miss plans, tags, LRU and pool bit for bit,
+    and the same attention output within the bf16 tolerance (2e-2 abs / 1e-2 rel; the
+    groups' split-K schedules may differ from the whole batch's)."""
+    from mini_hisparse_amd.batched import BatchedSparseDecode, LayerTablesView, PipelinedSparseDecode
+    from mini_hisparse_amd.config import CacheConfig
+    from mini_hisparse_amd.row_kernels import MappedHost
+
+    monkeypatch.setenv("HS_RESOLVE_SPLIT", "1")
+    B, Hkv, g, D, P, pages, length, top, hot_rows = 4, 2, 7, 64, 16, 1032, 16385, 32, 7168
+    heads, dtype, dev = Hkv * g, torch.bfloat16, torch.device(gpu)
+    print(f"[case] pipelined split front: B={B} length={length} S={hot_rows}", flush=True)
+    host = make_pool(B * pages, P, Hkv, D, dtype, seed=5, outliers=True).pin_memory()
+    rng = np.random.default_rng(5)
+    count, hot_blocks = ceil(length / P), ceil(hot_rows / P)
+    res_sets = [np.unique(np.append(rng.permutation(count - 1)[: count // 4], count - 1)) for _ in range(B)]
+    n_res = sum(len(r) for r in res_sets)
+    pool0 = torch.zeros(n_res + B * hot_blocks, 2, P, Hkv, D, dtype=dtype)
+    tables_np, nb = [], 0
+    for b in range(B):
+        resident = np.full(pages, -1, np.int32)
+        resident[res_sets[b]] = np.arange(nb, nb + len(res_sets[b]), dtype=np.int32)
+        pool0[nb : nb + len(res_sets[b])] = host[b * pages + torch.from_numpy(res_sets[b]).long()]
+        nb += len(res_sets[b])
+        tables_np.append(dict(source=np.arange(b * pages, (b + 1) * pages, dtype=np.int32), resident=resident,
+                              hot=(n_res + b * hot_blocks + rng.permutation(hot_blocks)).astype(np.int32),
+                              tags=np.full(hot_rows, -1, np.int32), lru=rng.permutation(hot_rows).astype(np.int16)))
+    bounds = [_bounds(host[b * pages : (b + 1) * pages], length, P) for b in range(B)]
+    lo = [x.to(dev) for x, _ in bounds]
+    hi = [x.to(dev) for _, x in bounds]
+    cfg = CacheConfig(gpu_pages=pool0.shape[0], host_pages=B * pages, page_size=P, kv_heads=Hkv, head_dim=D,
+                      device=gpu, dtype=dtype)
+    runs = {}
+    for name in ("pipelined", "batch"):
+        if name == "pipelined":
+            dec = PipelinedSparseDecode(cfg, heads, top, [length] * B, parts=2, device=dev, split_front=True)
+            transfer = torch.cuda.Stream(dev)
+            assert all(part.split_front for part in dec.parts)
+            assert hot_rows >= dec.parts[0].capacity, "the hot region must cover the union bound"
+        else:
+            dec = BatchedSparseDecode(cfg, heads, top, [length] * B, device=dev, split_front=False)
+            transfer = torch.cuda.current_stream(dev)
+        tables = [LayerTablesView(*[torch.from_numpy(t[k]).to(dev) for k in ("source", "resident", "hot", "tags", "lru")])
+                  for t in tables_np]
+        pool, alias, outs = pool0.to(dev), MappedHost(host), []
+        for step in range(2):
+            q = torch.randn(B, heads, D, generator=torch.Generator().manual_seed(50 + step)).to(dtype).to(dev)
+            if name == "pipelined":
+                out, _ = dec.step(q, lo, hi, tables, pool, alias, transfer)
+            else:
+                out = dec.step(q, lo, hi, tables, pool, alias, transfer)[0]
+            torch.cuda.synchronize()
+            outs.append(out.float().cpu())
+        runs[name] = (outs, [(t.tags.cpu(), t.lru.cpu()) for t in tables], pool.cpu())
+    (outs_p, tl_p, pool_p), (outs_b, tl_b, pool_b) = runs["pipelined"], runs["batch"]
+    for (tp, lp), (tb, lb) in zip(tl_p, tl_b):
+        assert torch.equal(tp, tb) and torch.equal(lp, lb)
+    assert torch.equal(pool_p, pool_b)
+    for a, b in zip(outs_p, outs_b):
+        assert ((a - b).abs() <= 2e-2 + 1e-2 * b.abs()).all()
