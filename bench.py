@@ -1373,6 +1373,7 @@ def run_model_workload(args, torch, device):
         "device_loop": device_loop,
         "stages_ms_per_step": stage_ms,
         "projections_on_hs_skinny_gemm": engine.projection_kernel,
+        "projection_choice_ms": engine.projection_times,  # each side's device ms over the layers' weights
         "rows_per_step": {"resident_hits": rows[0], "hot_hits": rows[1], "misses": rows[2]},
         "gather": {"bytes_per_step": gather_bytes, "GBps": gather_bytes / (stage_ms["gather"] * 1e-3) / 1e9,
                    "host_link_memcpy_GBps": link,

@@ -485,6 +485,21 @@ int hs_skinny_gemm_tiled(const void* x, int64_t x_stride, const void* weight_til
 int hs_skinny_gemm_swiglu_tiled(const void* x, int64_t x_stride, const void* gate_up_tiles, int64_t ffn, int64_t k,
                                 void* out, int64_t out_stride, int64_t rows, int32_t dtype, hs_stream_t stream);
 
+/*
+ * Greedy next tokens of the LM head: tokens[r] = argmax_n of the logits
+ * x[r] . W[n]^T (+ bias[n]) rounded to the dtype, the first maximal index on ties
+ * (-0 equal to +0; a NaN above every number), as torch.argmax over the logits of
+ * hs_skinny_gemm_tiled with one K slice -- without writing the logits.  W packed as
+ * for hs_skinny_gemm_tiled, n < 2^31.  Each workgroup leaves its best key per token
+ * in the workspace (hs_skinny_gemm_argmax_workspace_bytes, 8-byte aligned) and a
+ * second launch reduces them.  Replaces the logits GEMM and `argmax` of the
+ * reference's greedy decode (engine.py:71-72, _emit: logits.argmax()).
+ */
+int64_t hs_skinny_gemm_argmax_workspace_bytes(int64_t rows, int64_t n, int64_t k);
+int hs_skinny_gemm_argmax_tiled(const void* x, int64_t x_stride, const void* weight_tiles, int64_t n, int64_t k,
+                                const void* bias, int64_t* tokens, int64_t rows, int32_t dtype, void* workspace,
+                                int64_t workspace_bytes, hs_stream_t stream);
+
 #pragma GCC visibility pop
 
 #ifdef __cplusplus

@@ -145,6 +145,12 @@ SIGNATURES = {
         [c_void_p, c_int64, c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_int64, c_int64, c_int32, c_void_p,
          c_int64, c_void_p],
     ),
+    "hs_skinny_gemm_argmax_workspace_bytes": (c_int64, [c_int64, c_int64, c_int64]),
+    "hs_skinny_gemm_argmax_tiled": (
+        c_int,
+        [c_void_p, c_int64, c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_int64, c_int32, c_void_p, c_int64,
+         c_void_p],
+    ),
     "hs_attend_groups": (
         c_int,
         [c_void_p, c_int64, c_int64, c_void_p, c_int32, c_int64, c_int64, c_int64, c_int64,

@@ -48,7 +48,8 @@ from torch.nn import functional as F
 from . import _lib
 from .batched import BatchedSparseDecode, LayerTablesView
 from .dense import (
-    add_rms_norm, gemm_workspace_bytes, linear_supported, linear_swiglu_tiled, linear_tiled, prepare_add_rms_norm,
+    add_rms_norm, argmax_workspace_bytes, gemm_workspace_bytes, linear_argmax_tiled, linear_supported,
+    linear_swiglu_tiled, linear_tiled, prepare_add_rms_norm,
     prepare_linear_swiglu_tiled, prepare_linear_tiled, prepare_rotary_split, prepare_silu_mul, rotary_split, silu_mul,
     tile_gate_up, tile_weight,
 )
@@ -383,6 +384,12 @@ class SparseKVState:
         requests in ``order`` (default: every slot, in slot order; the policy places the
         writes in that order)."""
         rows = list(range(self.batch)) if order is None else list(order)
+        # every step calls this before its first launch: a token past the capacity is
+        # refused here, on the host, since its page would index past the tables that
+        # the uploads below and the step's launches write
+        full = [b for b in rows if positions[b] >= self.pages * self.config.page_size]
+        if full:
+            raise RuntimeError(f"slot(s) {full}: history full ({self.pages * self.config.page_size} tokens)")
         if self.plan is not None:
             self._plan_decode_writes(positions, rows)
             return
@@ -457,6 +464,32 @@ class SparseKVState:
             at = ((layer * B + b) * C + page) * page_elems * esz
             lo[i], hi[i] = base_lo + at, base_hi + at
         return dev_rows, host_rows, lo, hi
+
+
+def _graph_time(calls, device, replays=3):
+    """Device milliseconds of ``calls`` in order (launches on the current stream), as
+    the median of ``replays`` replays of a HIP graph captured from them after one eager
+    pass on the capture stream."""
+    stream = torch.cuda.Stream(device)
+    stream.wait_stream(torch.cuda.current_stream(device))
+    with torch.cuda.stream(stream):
+        for call in calls:
+            call()
+    stream.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        for call in calls:
+            call()
+    times = []
+    for _ in range(replays + 1):
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        graph.replay()
+        end.record()
+        end.synchronize()
+        times.append(start.elapsed_time(end))
+    del graph
+    return sorted(times[1:])[replays // 2]
 
 
 class BatchedDecodeEngine:
@@ -751,6 +784,10 @@ class BatchedDecodeEngine:
         """Per projection, the faster of the skinny-GEMM kernel on tile-major weights
         (hs_skinny_gemm_tiled) and PyTorch's GEMM at this batch, timed over the layers'
         own weights (each call reads another layer's weight from HBM, as in a step).
+        Each side runs as the step runs it, into a buffer of the step's shape (PyTorch's
+        GEMM followed by the copy into it), and is timed as a replayed HIP graph of its
+        calls: device time, which eager calls through Python would hide behind the
+        host's time per launch (~10 us, above the kernels' 3-8 us at these shapes).
         For gate|up the kernel is the fused launch with the SiLU gate
         (hs_skinny_gemm_swiglu_tiled) and PyTorch's side is its GEMM followed by
         hs_silu_mul: the two ways the step can run.  Each projection the kernel serves
@@ -765,14 +802,16 @@ class BatchedDecodeEngine:
             "o_proj": [(layer.self_attn.o_proj.weight, None) for layer in layers],
             "gate_up": [(gate_up, None) for _, _, gate_up in self._packed],
             "down": [(layer.mlp.down_proj.weight, None) for layer in layers],
-            "lm_head": [(self.model.lm_head.weight, None)] * 4,
+            "lm_head": [(self.model.lm_head.weight, self.model.lm_head.bias)] * 4,
         }
         self.projection_kernel = {}
+        self.projection_times = {}  # per projection, the timed choice's device ms of each side
         self._tiles = {}  # data_ptr of a row-major weight -> its tile-major copy
         ffn = self.model.config.intermediate_size
         row_counts = {B} | ({len(rows) for rows, _ in self.groups} if self.groups else set())
-        ws_bytes = max(gemm_workspace_bytes(r, w.shape[0], w.shape[1]) for r in row_counts
-                       for weights in groups.values() for w, _ in weights[:1])
+        vocab, hidden = self.model.lm_head.weight.shape
+        ws_bytes = max(max(gemm_workspace_bytes(r, w.shape[0], w.shape[1]), argmax_workspace_bytes(r, vocab, hidden))
+                       for r in row_counts for weights in groups.values() for w, _ in weights[:1])
         self._gemm_ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
         for name, weights in groups.items():
             x = torch.full((B, weights[0][0].shape[1]), 0.01, dtype=dt, device=dev)
@@ -785,28 +824,38 @@ class BatchedDecodeEngine:
             if mode != "auto":
                 chosen = mode == "kernel"
             else:
+                n_out = ffn if name == "gate_up" else weights[0][0].shape[0]
+                y = torch.empty(B, n_out, dtype=dt, device=dev)
                 if name == "gate_up":
-                    kernel = lambda x, w, b: linear_swiglu_tiled(x, self._tiles[w.data_ptr()], ffn)  # noqa: E731
-                    reference = lambda x, w, b: silu_mul(F.linear(x, w, b))  # noqa: E731
+                    kernel = lambda x, w, b: linear_swiglu_tiled(x, self._tiles[w.data_ptr()], ffn, out=y)  # noqa: E731
+                    reference = lambda x, w, b: silu_mul(F.linear(x, w, b), out=y)  # noqa: E731
+                elif name == "lm_head":  # the step's greedy tokens: the head and its argmax
+                    tokens = torch.empty(B, dtype=torch.int64, device=dev)
+                    kernel = lambda x, w, b: linear_argmax_tiled(  # noqa: E731
+                        x, self._tiles[w.data_ptr()], w.shape[0], b, out=tokens, workspace=self._gemm_ws)
+                    reference = lambda x, w, b: tokens.copy_(F.linear(x, w, b).argmax(-1))  # noqa: E731
                 else:
                     kernel = lambda x, w, b: linear_tiled(  # noqa: E731
-                        x, self._tiles[w.data_ptr()], w.shape[0], b, workspace=self._gemm_ws)
-                    reference = F.linear
-                elapsed = {}
-                for label, fn in (("kernel", kernel), ("torch", reference)):
-                    fn(x, *weights[0])
-                    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-                    start.record()
-                    for w, b in weights:
-                        fn(x, w, b)
-                    end.record()
-                    end.synchronize()
-                    elapsed[label] = start.elapsed_time(end)
+                        x, self._tiles[w.data_ptr()], w.shape[0], b, out=y, workspace=self._gemm_ws)
+                    reference = lambda x, w, b: y.copy_(F.linear(x, w, b))  # noqa: E731
+                elapsed = {label: _graph_time([lambda w=w, b=b, fn=fn: fn(x, w, b) for w, b in weights], dev)
+                           for label, fn in (("kernel", kernel), ("torch", reference))}
                 chosen = elapsed["kernel"] <= elapsed["torch"]
+            self.projection_times[name] = elapsed if mode == "auto" else None
             self.projection_kernel[name] = chosen
             if not chosen:
                 for w, _ in weights:
                     self._tiles.pop(w.data_ptr(), None)
+
+    def _next_tokens(self, h):
+        """Greedy tokens (int64 [rows]) of the final-normed rows ``h``: the LM head and
+        its argmax in the kernel's two launches (hs_skinny_gemm_argmax_tiled, no logits
+        written) where the LM head runs on the kernel, else PyTorch's GEMM and argmax."""
+        head = self.model.lm_head
+        if self.projection_kernel["lm_head"]:
+            return linear_argmax_tiled(h, self._tiles[head.weight.data_ptr()], head.weight.shape[0], head.bias,
+                                       workspace=self._gemm_ws)
+        return F.linear(h, head.weight, head.bias).argmax(-1)
 
     def _project(self, name, x, weight, bias=None, out=None):
         if self.projection_kernel[name]:
@@ -1000,11 +1049,7 @@ class BatchedDecodeEngine:
                 marks["dense_last"].append(mark(compute))
             if timer is not None:
                 timer.append((index, marks, dec.entry_counts.sum(), dec.row_counts[:, 2].sum()))
-        logits = self._project(
-            "lm_head", add_rms_norm(self._x, self._delta, model.model.norm.weight, cfg.rms_norm_eps),
-            model.lm_head.weight,
-        )
-        tokens = logits.argmax(-1)
+        tokens = self._next_tokens(add_rms_norm(self._x, self._delta, model.model.norm.weight, cfg.rms_norm_eps))
         st.lengths = [p + 1 for p in positions]
         self.positions += 1
         if self.use_graphs and self._graphs is None:
@@ -1107,11 +1152,7 @@ class BatchedDecodeEngine:
                 marks["dense_last"].append(mark(compute))
             if timer is not None:
                 timer.append((layer, marks, dec.entry_counts.sum(), dec.row_counts[:, 2].sum()))
-        logits = self._project(
-            "lm_head", add_rms_norm(self._x, self._delta, model.model.norm.weight, cfg.rms_norm_eps),
-            model.lm_head.weight,
-        )
-        tokens = logits.argmax(-1)
+        tokens = self._next_tokens(add_rms_norm(self._x, self._delta, model.model.norm.weight, cfg.rms_norm_eps))
         for b in slots:
             st.lengths[b] = positions[b] + 1
         self.positions.index_add_(0, index, torch.ones_like(index))
@@ -1199,11 +1240,7 @@ class BatchedDecodeEngine:
                 gathered.record(transfer)
         for g in range(len(self.groups)):
             attend(L - 1, g)
-        logits = self._project(
-            "lm_head", add_rms_norm(self._x, self._delta, model.model.norm.weight, cfg.rms_norm_eps),
-            model.lm_head.weight,
-        )
-        tokens = logits.argmax(-1)
+        tokens = self._next_tokens(add_rms_norm(self._x, self._delta, model.model.norm.weight, cfg.rms_norm_eps))
         st.lengths = [p + 1 for p in positions]
         self.positions += 1
         return tokens

@@ -15,7 +15,9 @@
 // bias and writes y; with several (split-K, for tall-K shapes that would
 // otherwise give too few workgroups) it writes fp32 partials and
 // gemm_finalize_kernel sums them in slice order (deterministic), adds the
-// bias and rounds.
+// bias and rounds.  The argmax form (the LM head of a greedy step) keeps, per
+// workgroup and token, only the best rounded logit and its index as one ordered
+// 64-bit key, and argmax_finalize_kernel takes the largest key per token.
 #include <math.h>
 #include <stdlib.h>
 
@@ -47,7 +49,20 @@ struct GemmArgs {
   float* part;  // [splits, M, N] when splits > 1
   int64_t splits, slice_steps;
   int64_t F;  // SWIGLU: output features (N = 2 * 16 * ceil(F / 16) interleaved weight rows)
+  unsigned long long* keys;  // ARGMAX: [M, gridDim.x] best key per token and workgroup
 };
+
+// Ordered key of logit v at vocabulary index n: a larger key is a larger value, or
+// the same value at a smaller index, so the largest key is torch.argmax's answer
+// (the first maximal index).  -0 counts as +0 (they compare equal); a NaN sits
+// above every number (torch's argmax returns the first NaN).  Every key is above
+// 0, the key of "no row".
+__device__ __forceinline__ unsigned long long argmax_key(float v, int64_t n) {
+  const uint32_t u = v == 0.f ? 0u : __float_as_uint(v);
+  uint32_t ord = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  if (v != v) ord = 0xffffffffu;
+  return (static_cast<unsigned long long>(ord) << 32) | (0xffffffffu - static_cast<uint32_t>(n));
+}
 
 template <int DT>
 __device__ __forceinline__ float gemm_round(float v) {
@@ -68,7 +83,9 @@ __device__ __forceinline__ float gemm_round(float v) {
 // 16i..), and the workgroup writes silu(gate) * up for its 16 features with the
 // arithmetic of the separate path: each projection rounded to the dtype, then
 // SiLU rounded, then the product (hs_silu_mul).
-template <int DT, int GM_TILES, int GU, bool TILED, bool SWIGLU = false>
+// ARGMAX (one K slice): per token the workgroup's best key over its rows, each
+// logit rounded to the dtype after the bias as the plain form stores it.
+template <int DT, int GM_TILES, int GU, bool TILED, bool SWIGLU = false, bool ARGMAX = false>
 __global__ __launch_bounds__(GM_T) void skinny_gemm_kernel(GemmArgs a) {
   constexpr int GM_ROWS = 16 * GM_TILES;  // weight rows per workgroup
   __shared__ float red[4][GM_ROWS][17];
@@ -141,6 +158,27 @@ __global__ __launch_bounds__(GM_T) void skinny_gemm_kernel(GemmArgs a) {
     }
     return;
   }
+  if constexpr (ARGMAX) {
+    __shared__ unsigned long long best[GM_ROWS][16];
+    for (int idx = threadIdx.x; idx < GM_ROWS * 16; idx += GM_T) {
+      const int r = idx >> 4, m = idx & 15;
+      const int64_t n = n0 + r;
+      unsigned long long key = 0;
+      if (n < a.N) {
+        const float b = a.bias != nullptr ? load_elem<DT>(a.bias, n) : 0.f;
+        key = argmax_key(gemm_round<DT>((red[0][r][m] + red[1][r][m] + red[2][r][m] + red[3][r][m]) + b), n);
+      }
+      best[r][m] = key;
+    }
+    __syncthreads();
+    if (threadIdx.x < a.M) {
+      const int m = threadIdx.x;
+      unsigned long long key = 0;
+      for (int r = 0; r < GM_ROWS; ++r) key = best[r][m] > key ? best[r][m] : key;
+      a.keys[static_cast<int64_t>(m) * gridDim.x + blockIdx.x] = key;
+    }
+    return;
+  }
   for (int idx = threadIdx.x; idx < GM_ROWS * 16; idx += GM_T) {
     const int r = idx >> 4, m = idx & 15;
     const int64_t n = n0 + r;
@@ -166,6 +204,30 @@ __global__ __launch_bounds__(GM_T) void gemm_finalize_kernel(const float* part, 
   for (int64_t s = 0; s < splits; ++s) v += part[(s * M + m) * N + n];
   if (bias != nullptr) v += load_elem<DT>(bias, n);
   store_elem<DT>(out, m * out_stride + n, v);
+}
+
+// One workgroup per token: the largest of its `blocks` keys, as the vocabulary index.
+__global__ __launch_bounds__(GM_T) void argmax_finalize_kernel(const unsigned long long* keys, int64_t blocks,
+                                                               int64_t* tokens) {
+  __shared__ unsigned long long wave_best[GM_T / 64];
+  const int64_t m = blockIdx.x;
+  unsigned long long key = 0;
+  for (int64_t b = threadIdx.x; b < blocks; b += GM_T) {
+    const unsigned long long v = keys[m * blocks + b];
+    key = v > key ? v : key;
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const unsigned long long o = __shfl_xor(key, off, 64);
+    key = o > key ? o : key;
+  }
+  if ((threadIdx.x & 63) == 0) wave_best[threadIdx.x >> 6] = key;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+#pragma unroll
+    for (int w = 1; w < GM_T / 64; ++w) key = wave_best[w] > key ? wave_best[w] : key;
+    tokens[m] = static_cast<int64_t>(0xffffffffu - static_cast<uint32_t>(key));
+  }
 }
 
 struct GemmPlan {
@@ -194,26 +256,35 @@ static GemmPlan plan_gemm(int64_t N, int64_t K) {
   p.gu = f_gu == 4 ? 4 : 8;
   p.blocks = gemm_ceil(N, 16 * p.tiles);
   const int64_t steps = K / 32;
-  int64_t splits = f_splits > 0 ? f_splits : gemm_ceil(512, p.blocks);
+  int64_t splits = gemm_ceil(512, p.blocks);
   const int64_t most = steps / (2 * 4 * p.gu);
   if (splits > most) splits = most;
+  if (f_splits > 0) splits = f_splits < steps ? f_splits : steps;  // forced: at least one k-step per slice
   if (splits < 1) splits = 1;
   p.slice_steps = gemm_ceil(steps, splits);
   p.splits = gemm_ceil(steps, p.slice_steps);
   return p;
 }
 
-template <int DT, int TILES, bool TILED>
+template <int DT, int TILES, bool TILED, bool ARGMAX>
 static void launch_gemm_tiles(const GemmPlan& p, dim3 grid, const GemmArgs& a, hipStream_t s) {
-  if (p.gu == 4) hipLaunchKernelGGL((skinny_gemm_kernel<DT, TILES, 4, TILED>), grid, dim3(GM_T), 0, s, a);
-  else hipLaunchKernelGGL((skinny_gemm_kernel<DT, TILES, 8, TILED>), grid, dim3(GM_T), 0, s, a);
+  if (p.gu == 4) hipLaunchKernelGGL((skinny_gemm_kernel<DT, TILES, 4, TILED, false, ARGMAX>), grid, dim3(GM_T), 0, s, a);
+  else hipLaunchKernelGGL((skinny_gemm_kernel<DT, TILES, 8, TILED, false, ARGMAX>), grid, dim3(GM_T), 0, s, a);
 }
 
-template <int DT, bool TILED>
+template <int DT, bool TILED, bool ARGMAX = false>
 static void launch_gemm(const GemmPlan& p, dim3 grid, const GemmArgs& a, hipStream_t s) {
-  if (p.tiles == 1) launch_gemm_tiles<DT, 1, TILED>(p, grid, a, s);
-  else if (p.tiles == 2) launch_gemm_tiles<DT, 2, TILED>(p, grid, a, s);
-  else launch_gemm_tiles<DT, 4, TILED>(p, grid, a, s);
+  if (p.tiles == 1) launch_gemm_tiles<DT, 1, TILED, ARGMAX>(p, grid, a, s);
+  else if (p.tiles == 2) launch_gemm_tiles<DT, 2, TILED, ARGMAX>(p, grid, a, s);
+  else launch_gemm_tiles<DT, 4, TILED, ARGMAX>(p, grid, a, s);
+}
+
+// The argmax form's plan: the plain plan's tiles and rounds, one K slice.
+static GemmPlan plan_argmax(int64_t N, int64_t K) {
+  GemmPlan p = plan_gemm(N, K);
+  p.slice_steps = K / 32;
+  p.splits = 1;
+  return p;
 }
 
 }  // namespace hs
@@ -322,5 +393,47 @@ extern "C" int hs_skinny_gemm_swiglu_tiled(const void* x, int64_t x_stride, cons
   else
     hipLaunchKernelGGL((skinny_gemm_kernel<HS_DTYPE_F16, 2, 8, true, true>), grid, dim3(GM_T), 0, stream, a);
   HS_CHECK_LAUNCH("skinny GEMM swiglu");
+  return HS_OK;
+}
+
+extern "C" int64_t hs_skinny_gemm_argmax_workspace_bytes(int64_t rows, int64_t n, int64_t k) {
+  if (rows < 1 || n < 1 || k < 32) return 256;
+  return plan_argmax(n, k).blocks * rows * 8 + 256;
+}
+
+extern "C" int hs_skinny_gemm_argmax_tiled(const void* x, int64_t x_stride, const void* weight_tiles, int64_t n,
+                                           int64_t k, const void* bias, int64_t* tokens, int64_t rows, int32_t dtype,
+                                           void* workspace, int64_t workspace_bytes, hipStream_t stream) {
+  HS_CHECK_ARG(dtype == HS_DTYPE_BF16 || dtype == HS_DTYPE_F16, "the decode GEMM takes bf16 or f16");
+  HS_CHECK_ARG(rows >= 1 && rows <= 16, "the decode GEMM takes 1 to 16 rows");
+  HS_CHECK_ARG(n >= 1 && n <= 0x7fffffff && k >= 32 && k % 32 == 0,
+               "n must be in [1, 2^31) and K a positive multiple of 32");
+  HS_CHECK_ARG(x_stride >= k && x_stride % 8 == 0, "invalid row stride");
+  HS_CHECK_ARG(x && weight_tiles && tokens, "null GEMM pointer");
+  HS_CHECK_ARG((reinterpret_cast<uintptr_t>(x) & 15) == 0 && (reinterpret_cast<uintptr_t>(weight_tiles) & 15) == 0,
+               "x and weight must be 16-byte aligned");
+  const GemmPlan p = plan_argmax(n, k);
+  HS_CHECK_ARG(p.blocks <= 0x7fffffff, "GEMM too large");
+  const int64_t need = p.blocks * rows * 8;
+  HS_CHECK_ARG(workspace != nullptr && workspace_bytes >= need && (reinterpret_cast<uintptr_t>(workspace) & 7) == 0,
+               "argmax workspace too small or misaligned: need %lld bytes", static_cast<long long>(need));
+  GemmArgs a{};
+  a.x = static_cast<const unsigned short*>(x);
+  a.x_stride = x_stride;
+  a.w = static_cast<const unsigned short*>(weight_tiles);
+  a.K = k;
+  a.N = n;
+  a.M = rows;
+  a.bias = static_cast<const unsigned short*>(bias);
+  a.splits = 1;
+  a.slice_steps = p.slice_steps;
+  a.keys = static_cast<unsigned long long*>(workspace);
+  const dim3 grid(static_cast<unsigned>(p.blocks));
+  if (dtype == HS_DTYPE_BF16) launch_gemm<HS_DTYPE_BF16, true, true>(p, grid, a, stream);
+  else launch_gemm<HS_DTYPE_F16, true, true>(p, grid, a, stream);
+  HS_CHECK_LAUNCH("skinny GEMM argmax");
+  hipLaunchKernelGGL(argmax_finalize_kernel, dim3(static_cast<unsigned>(rows)), dim3(GM_T), 0, stream, a.keys,
+                     p.blocks, tokens);
+  HS_CHECK_LAUNCH("argmax finalize");
   return HS_OK;
 }

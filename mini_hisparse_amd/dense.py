@@ -167,6 +167,33 @@ def prepare_linear_tiled(x, tiles, n, bias, out, workspace):
     return _linear_tiled_launch(x, tiles, n, bias, out, ws)
 
 
+def argmax_workspace_bytes(rows, n, k):
+    """Bytes of per-workgroup keys :func:`linear_argmax_tiled` needs for [rows, k] x [n, k]."""
+    return _lib.load().hs_skinny_gemm_argmax_workspace_bytes(rows, n, k)
+
+
+def linear_argmax_tiled(x, tiles, n, bias=None, out=None, workspace=None):
+    """Greedy tokens of the LM head: ``argmax(x @ weight.T + bias, -1)`` as int64 [rows]
+    (``hs_skinny_gemm_argmax_tiled``: the logits of :func:`linear_tiled` with one K
+    slice, never written; the first maximal index on ties, as torch.argmax)."""
+    _linear_tiled_check(x, tiles, n, bias, None)
+    rows, k = x.shape
+    if out is not None and (out.dtype != torch.int64 or out.shape != (rows,) or out.device != x.device
+                            or not out.is_contiguous()):
+        raise ValueError(f"linear_argmax_tiled: out must be int64 [{rows}] contiguous on {x.device}")
+    tokens = torch.empty(rows, dtype=torch.int64, device=x.device) if out is None else out
+    stream = _stream(x)
+    ws = _workspace(x.device, stream, argmax_workspace_bytes(rows, n, k), workspace)
+    _lib.check(
+        _lib.load().hs_skinny_gemm_argmax_tiled(
+            x.data_ptr(), x.stride(0), tiles.data_ptr(), n, k, _lib.ptr(bias), tokens.data_ptr(), rows,
+            _lib.dtype_code(x.dtype), ws.data_ptr(), ws.numel(), stream,
+        ),
+        "hs_skinny_gemm_argmax_tiled",
+    )
+    return tokens
+
+
 def tile_gate_up(gate_up, ffn):
     """The packed gate|up weight [2 * ffn, K] for :func:`linear_swiglu_tiled`: the gate's
     and the up projection's :func:`tile_weight` tiles interleaved (gate tile i at 2i)."""

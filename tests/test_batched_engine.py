@@ -520,3 +520,26 @@ def test_fused_rotary_append_equals_the_separate_launches(gpu):
                 assert torch.equal(pool_a[blk, :, off].view(torch.int16), pool_b[blk, :, off].view(torch.int16))
     assert torch.equal(a.minimum.view(torch.int16), b.minimum.view(torch.int16))
     assert torch.equal(a.maximum.view(torch.int16), b.maximum.view(torch.int16))
+
+
+@pytest.mark.gpu
+def test_a_step_past_the_history_capacity_is_refused_on_the_host(gpu):
+    """A state sized for 641 tokens (41 pages of 16: room up to token 655) decodes from
+    637 tokens until full; the next step raises before it launches anything (the new
+    page would index past the state's tables), and the state is left as it was."""
+    from mini_hisparse_amd.batched_engine import BatchedDecodeEngine, build_state, random_model
+
+    wl = tiny(context=40 * 16 - 3, steps=4)
+    model, state = random_model(wl, gpu, seed=1), build_state(wl, gpu, seed=2)
+    engine = BatchedDecodeEngine(model, state, wl.top_pages)
+    capacity = state.pages * wl.page_size
+    assert capacity == 656
+    tokens = torch.arange(1, wl.batch + 1, device=gpu)
+    while state.lengths[0] < capacity:
+        tokens = engine.step(tokens)
+    torch.cuda.synchronize()
+    lengths = list(state.lengths)
+    with pytest.raises(RuntimeError, match="history full"):
+        engine.step(tokens)
+    torch.cuda.synchronize()
+    assert state.lengths == lengths

@@ -209,3 +209,55 @@ def test_split_k_partials_in_a_caller_workspace(gpu):
     assert torch.equal(linear_tiled(x, tiles, 1000, workspace=own), linear_tiled(x, tiles, 1000))
     with pytest.raises(ValueError, match="workspace"):
         linear_tiled(x, tiles, 1000, workspace=own[: need - 1])
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("rows", [1, 4, 16])
+@pytest.mark.parametrize("n,k,bias", [(151936, 896, False), (1000, 256, True), (37, 64, False), (50001, 2048, True)])
+def test_argmax_gemm_equals_torch_argmax_of_the_logits(gpu, dtype, rows, n, k, bias):
+    """hs_skinny_gemm_argmax_tiled against torch.argmax over the logits of
+    hs_skinny_gemm_tiled (one K slice at these shapes: the same rounded logits), on
+    random rows, then with exact ties planted (the best row copied to index 0 and to
+    the last index: the first index wins), all-zero inputs (logits +0 and -0: index 0)
+    and NaN rows (the first NaN wins, as torch takes it)."""
+    from mini_hisparse_amd.dense import gemm_workspace_bytes, linear_argmax_tiled, linear_tiled, tile_weight
+
+    assert gemm_workspace_bytes(rows, n, k) == 256  # one K slice
+    gen = torch.Generator(device=gpu).manual_seed(rows + n + k)
+    x = torch.randn(rows, k, generator=gen, device=gpu).to(dtype)
+    w = (torch.randn(n, k, generator=gen, device=gpu) / k**0.5).to(dtype)
+    b = torch.randn(n, generator=gen, device=gpu).to(dtype) if bias else None
+
+    def check(x, w, what):
+        tiles = tile_weight(w)
+        expected = linear_tiled(x, tiles, n, b).argmax(-1)
+        got = linear_argmax_tiled(x, tiles, n, b)
+        assert got.dtype == torch.int64 and torch.equal(got, expected), (what, got.tolist(), expected.tolist())
+        return expected
+
+    best = check(x, w, "random")
+    if n > 2:
+        tied = w.clone()
+        r = int(best[0])
+        tied[0], tied[n - 1] = w[r], w[r]
+        assert int(check(x, tied, "ties")[0]) == 0 or (b is not None and b[0] != b[r])
+    zeros = check(torch.zeros_like(x), w, "zeros")
+    if b is None:
+        assert (zeros == 0).all()
+    if n > 8:
+        nan = w.clone()
+        nan[n // 2, 0] = float("nan")
+        nan[n // 3 + 5, 1] = float("nan")
+        assert (check(x, nan, "nan") == min(n // 2, n // 3 + 5)).all()
+
+
+@pytest.mark.gpu
+def test_argmax_gemm_rejects_a_short_workspace(gpu):
+    from mini_hisparse_amd.dense import argmax_workspace_bytes, linear_argmax_tiled, tile_weight
+
+    x = torch.ones(2, 64, dtype=torch.bfloat16, device=gpu)
+    tiles = tile_weight(torch.ones(100, 64, dtype=torch.bfloat16, device=gpu))
+    need = argmax_workspace_bytes(2, 100, 64)
+    with pytest.raises(ValueError, match="workspace"):
+        linear_argmax_tiled(x, tiles, 100, workspace=torch.empty(need - 300, dtype=torch.uint8, device=gpu))
