@@ -86,7 +86,7 @@ __global__ __launch_bounds__(DN_T) void add_rms_norm_kernel(const void* x, const
     for (int k = 0; k < NR_REG; ++k) {
       const int64_t i = threadIdx.x + static_cast<int64_t>(k) * DN_T;
       if (i >= width) break;
-      store_elem<DT>(y, yo + i, round_to<DT>(v[k] * r) * wv[k]);
+      store_elem<DT>(y, yo + i, round_to<DT>(mul_rn(v[k], r)) * wv[k]);
     }
     return;
   }
@@ -130,7 +130,7 @@ __global__ __launch_bounds__(DN_T) void add_rms_norm_kernel(const void* x, const
     for (int k = 0; k < NR_CH; ++k) {
       const int64_t i = base + static_cast<int64_t>(k) * DN_T;
       if (i >= width) break;
-      store_elem<DT>(y, yo + i, round_to<DT>(a[k] * r) * b[k]);
+      store_elem<DT>(y, yo + i, round_to<DT>(mul_rn(a[k], r)) * b[k]);
     }
   }
 }

@@ -79,6 +79,18 @@ __device__ __forceinline__ void store_elem(void* base, int64_t i, float v) {
   }
 }
 
+// x * y rounded to fp32, never contracted with a following conversion: the
+// compiler may otherwise fold fptrunc(x * y) into one mixed-precision FMA that
+// rounds the exact product to f16 once, where PyTorch's (x * y).to(float16) rounds
+// to fp32 first (and it does so for some lanes of a kernel and not others).
+// (The empty asm holds the product as an fp32 register value; it emits nothing.
+// A contract(off) pragma does not reach that fold.)
+__device__ __forceinline__ float mul_rn(float x, float y) {
+  float p = x * y;
+  asm("" : "+v"(p));
+  return p;
+}
+
 // v rounded to the storage dtype (float32: unchanged).
 template <int DT>
 __device__ __forceinline__ float round_to(float v) {

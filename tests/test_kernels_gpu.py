@@ -404,6 +404,24 @@ def test_quest_scores_bit_exact(gpu, q_dtype, counts, kv, g, D):
         np.testing.assert_array_equal(scores[i, :, :c].view(np.uint32), expected.view(np.uint32))
 
 
+@pytest.mark.parametrize("pages,top,sink", [(2049, 32, True), (4096, 64, True), (300, 300 - 1, False), (65, 64, True),
+                                             (4097, 32, True), (2048, 1, True), (1000, 7, False)])
+def test_quest_topk_with_many_ties_matches_oracle(gpu, pages, top, sink):
+    """Bounds and queries of small integers, so that many pages score exactly alike: the
+    radix select's pages equal the oracle's, ties taken from the lowest page."""
+    from mini_hisparse_amd.selection import quest_selection
+
+    P, kv, g, D = 16, 2, 7, 64
+    length = pages * P
+    gen = torch.Generator().manual_seed(pages + top)
+    lo = torch.randint(-2, 1, (pages, kv, D), generator=gen).to(torch.bfloat16)
+    hi = lo + torch.randint(0, 2, (pages, kv, D), generator=gen).to(torch.bfloat16)
+    q = torch.randint(-1, 2, (kv * g, D), generator=gen).to(torch.bfloat16)
+    expected = oracle.quest_pages(q, lo, hi, length, P, top, keep_sink=sink)
+    sel = quest_selection(q.to(gpu), lo.to(gpu), hi.to(gpu), length, P, top, keep_sink=sink)
+    np.testing.assert_array_equal(sel.device_pages[:, : expected.shape[1]].cpu().numpy(), expected)
+
+
 def test_quest_reference_known_answer(gpu):
     """tests/test_selection.py:33-47 of the reference: pages [0, 2], not the mean's page 1."""
     from mini_hisparse_amd.selection import quest_selection
