@@ -288,3 +288,18 @@ def test_row_attention_rejects_the_reference_backends(backend):
     topk = LogicalTopK(torch.tensor([0], dtype=torch.int32))
     with pytest.raises(ValueError, match="invalid attention backend"):
         row_attention(torch.zeros(2, 8), cache, "r", 0, topk, backend=backend)
+
+
+def test_product_refuses_a_non_rocm_cache_without_explicit_ops():
+    """No CPU fallback in the product: a cache on the CPU needs an explicit ops backend
+    (the tests' oracle backend), and the attention takes no backend but the HIP one."""
+    from mini_hisparse_amd.attention import row_attention
+    from mini_hisparse_amd.hybrid import HybridKVCache
+
+    cfg = CacheConfig(gpu_pages=8, host_pages=8, page_size=4, kv_heads=1, head_dim=8, device="cpu",
+                      dtype=torch.float32)
+    with pytest.raises(ValueError, match="ROCm"):
+        HybridKVCache(cfg, HotConfig(max_union_rows=4))
+    for backend in ("torch", "triton", "cpu"):
+        with pytest.raises(ValueError, match="invalid attention backend"):
+            row_attention(torch.zeros(1, 8), None, 0, 0, None, backend=backend)
