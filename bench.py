@@ -258,9 +258,13 @@ def build_workload(args, torch, device):
 
 def run_steps(torch, w, steps, record):
     """`steps` decode steps; per-stage HIP events when `record`."""
+    from mini_hisparse_amd.streams import independent_stream
+
     dec, device = w["dec"], w["pool"].device
     compute = torch.cuda.current_stream(device)
-    transfer = w.setdefault("transfer", torch.cuda.Stream(device))
+    if "transfer" not in w:
+        w["transfer"] = independent_stream(device)
+    transfer = w["transfer"]
     row_stats = w.setdefault("row_stats", torch.zeros(3, dtype=torch.int64, device=device))
     events = []
     last = w.get("last_use")
@@ -297,8 +301,12 @@ def run_steps(torch, w, steps, record):
 
 def run_pipelined(torch, w, steps):
     """`steps` decode steps of the whole batch as overlapped request groups."""
+    from mini_hisparse_amd.streams import independent_stream
+
     pipe, device = w["pipe"], w["pool"].device
-    transfer = w.setdefault("transfer", torch.cuda.Stream(device)) if w["use_transfer_stream"] else None
+    if w["use_transfer_stream"] and "transfer" not in w:
+        w["transfer"] = independent_stream(device)
+    transfer = w["transfer"] if w["use_transfer_stream"] else None
     row_stats = w.setdefault("row_stats", torch.zeros(3, dtype=torch.int64, device=device))
     out = w.get("pipe_out")
     for _ in range(steps):

@@ -104,6 +104,20 @@ int hs_quest_topk(const void* query, int64_t q_stride_b, int64_t q_stride_h,
                   int64_t workspace_bytes, hs_stream_t stream);
 
 /*
+ * Uniformly resampled page selections (BASELINE configs[4]'s miss-heavy stress
+ * selector; no counterpart in the reference, whose selections come from Quest or
+ * the caller): for each (layer, request), the tail page count - 1 and top - 1 other
+ * pages drawn uniformly without replacement from [0, count - 1) (Floyd's
+ * algorithm over a counter-based splitmix64 generator of seed, step, layer,
+ * request), written ascending to every head's row of out [layers, batch, heads,
+ * top] int32, then -1; a request of at most `top` pages selects all of them.  The
+ * same (seed, step) always draws the same pages.  page_counts host [batch], each
+ * 1 to 65536.  The rows are hs_build_union's `pages`.
+ */
+int hs_uniform_pages(uint64_t seed, uint64_t step, const int64_t* page_counts, int64_t batch, int64_t layers,
+                     int64_t top, int64_t heads, int32_t* out, hs_stream_t stream);
+
+/*
  * Device-side Selection -> LogicalTopK adapter for page selections.
  * Replaces: Selection.from_pages (selection.py:43-60) followed by
  * LogicalTopK.from_selection (row_index.py:20-31), without the host sync of

@@ -7,7 +7,7 @@ no fallback: when the library is missing every kernel call raises.
 from __future__ import annotations
 
 import ctypes
-from ctypes import POINTER, c_char_p, c_float, c_int, c_int32, c_int64, c_void_p
+from ctypes import c_uint64, POINTER, c_char_p, c_float, c_int, c_int32, c_int64, c_void_p
 from pathlib import Path
 
 LIBRARY_PATH = Path(__file__).resolve().parent / "libhisparse_hip.so"
@@ -131,6 +131,9 @@ SIGNATURES = {
          c_float, c_int32, c_void_p],
     ),
     "hs_silu_mul": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_int64, c_int64, c_int32, c_void_p]),
+    "hs_uniform_pages": (
+        c_int, [c_uint64, c_uint64, POINTER(c_int64), c_int64, c_int64, c_int64, c_int64, c_void_p, c_void_p],
+    ),
     "hs_skinny_gemm_workspace_bytes": (c_int64, [c_int64, c_int64, c_int64]),
     "hs_skinny_gemm": (
         c_int,

@@ -46,6 +46,7 @@ import torch
 from torch.nn import functional as F
 
 from . import _lib
+from .streams import independent_stream
 from .batched import BatchedSparseDecode, LayerTablesView
 from .dense import (
     add_rms_norm, argmax_workspace_bytes, gemm_workspace_bytes, linear_argmax_tiled, linear_supported,
@@ -129,6 +130,24 @@ def uniform_pages(lengths, page_size, top_pages, layers, generator, device):
         if count <= top_pages:
             pages[:, b, :count] = torch.arange(count, dtype=torch.int32, device=device)
     return pages
+
+
+def uniform_pages_device(seed, step, lengths, page_size, top_pages, layers, heads, device="cuda", out=None,
+                         stream=None):
+    """:func:`uniform_pages`'s rule drawn on the device by ``hs_uniform_pages``: per (layer,
+    request) the tail page plus ``top_pages - 1`` others uniformly without replacement,
+    ascending, for every head: int32 [layers, B, heads, top_pages] (-1 past a short
+    history's pages).  A counter-based generator: (seed, step) fixes the draw."""
+    B = len(lengths)
+    counts = (ctypes.c_int64 * B)(*[ceil(length / page_size) for length in lengths])
+    if out is None:
+        out = torch.empty((layers, B, heads, top_pages), dtype=torch.int32, device=device)
+    if out.dtype != torch.int32 or tuple(out.shape) != (layers, B, heads, top_pages) or not out.is_contiguous():
+        raise ValueError(f"out must be contiguous int32 [{layers}, {B}, {heads}, {top_pages}]")
+    handle = stream if stream is not None else _lib.stream_handle(out.device)
+    _lib.check(_lib.load().hs_uniform_pages(seed & (2**64 - 1), step & (2**64 - 1), counts, B, layers, top_pages,
+                                            heads, out.data_ptr(), handle), "hs_uniform_pages")
+    return out
 
 
 def rotary_at(tensor, positions, theta):
@@ -466,11 +485,11 @@ class SparseKVState:
         return dev_rows, host_rows, lo, hi
 
 
-def _graph_time(calls, device, replays=3):
+def _graph_time(calls, stream, replays=3):
     """Device milliseconds of ``calls`` in order (launches on the current stream), as
-    the median of ``replays`` replays of a HIP graph captured from them after one eager
-    pass on the capture stream."""
-    stream = torch.cuda.Stream(device)
+    the median of ``replays`` replays of a HIP graph captured from them on ``stream``
+    after one eager pass there."""
+    device = stream.device
     stream.wait_stream(torch.cuda.current_stream(device))
     with torch.cuda.stream(stream):
         for call in calls:
@@ -557,7 +576,7 @@ class BatchedDecodeEngine:
         self.prefetch = prefetch
         self.decs = [self.dec] + [decoder(self.dec) for _ in range(state.layers - 1)] if prefetch else None
         self.selector = selector
-        self._sampler = torch.Generator(device=self.device).manual_seed(seed)
+        self._sample_seed, self._sample_step = seed, 0  # the uniform selector's draws: (seed, step)
         if state.hot_rows < self.dec.capacity:
             # the resolver's precondition (row_index.py:41-42, hybrid.py:34): every
             # selected row must fit the hot region, or misses would share victim slots
@@ -583,7 +602,8 @@ class BatchedDecodeEngine:
             self._group_events = [[(torch.cuda.Event(), torch.cuda.Event()) for _ in self.groups]
                                   for _ in range(state.layers)]
             self.group_gather_workgroups = group_gather_workgroups
-        self.transfer = torch.cuda.Stream(self.device) if transfer_stream or prefetch or self.groups else None
+        # its own hardware queue, or the transfers would run in the compute stream's order
+        self.transfer = independent_stream(self.device) if transfer_stream or prefetch or self.groups else None
         self._pack_projections()
         self._choose_projections(projections)
         self._host_alias = [(ctypes.c_void_p * state.batch)(*([a.data_ptr()] * state.batch)) for a in state.alias]
@@ -606,17 +626,21 @@ class BatchedDecodeEngine:
         """The decoder (selection, resolver and attention buffers) that serves `layer`."""
         return self.decs[layer] if self.decs is not None else self.dec
 
-    def _heads_pages(self, sampled):
-        """The step's uniform pages [L, n, top] copied to every head, [L, n, heads, top], in
-        one launch: each layer's union build reads its slice in place.  The buffer is
-        reused every step; the step's last attention waits for every layer's gather, so
-        every read of it precedes the next step's copy on the compute stream."""
-        L, n, top = sampled.shape
+    def _draw_pages(self, lengths):
+        """The step's uniform pages, [L, n, heads, top] for the ``n`` decoding requests'
+        ``lengths``, drawn on the device (``hs_uniform_pages``, one launch) into a buffer
+        reused every step; each layer's union build reads its slice in place.  The step's
+        last attention waits for every layer's gather, so every read of the buffer precedes
+        the next step's draw on the compute stream."""
+        L, n = self.state.layers, len(lengths)
         Hq = self.model.config.num_attention_heads
         buf = self._pages_bufs.get(n)
         if buf is None:
-            buf = self._pages_bufs[n] = torch.empty((L, n, Hq, top), dtype=torch.int32, device=self.device)
-        buf.copy_(sampled[:, :, None, :].expand(L, n, Hq, top))
+            buf = self._pages_bufs[n] = torch.empty((L, n, Hq, self.dec.top), dtype=torch.int32,
+                                                    device=self.device)
+        uniform_pages_device(self._sample_seed, self._sample_step, lengths, self.state.config.page_size,
+                             self.dec.top, L, Hq, out=buf)
+        self._sample_step += 1
         return buf
 
     def _prefetch(self, index, sampled, transfer, mark):
@@ -806,6 +830,7 @@ class BatchedDecodeEngine:
         }
         self.projection_kernel = {}
         self.projection_times = {}  # per projection, the timed choice's device ms of each side
+        capture = None
         self._tiles = {}  # data_ptr of a row-major weight -> its tile-major copy
         ffn = self.model.config.intermediate_size
         row_counts = {B} | ({len(rows) for rows, _ in self.groups} if self.groups else set())
@@ -838,7 +863,9 @@ class BatchedDecodeEngine:
                     kernel = lambda x, w, b: linear_tiled(  # noqa: E731
                         x, self._tiles[w.data_ptr()], w.shape[0], b, out=y, workspace=self._gemm_ws)
                     reference = lambda x, w, b: y.copy_(F.linear(x, w, b))  # noqa: E731
-                elapsed = {label: _graph_time([lambda w=w, b=b, fn=fn: fn(x, w, b) for w, b in weights], dev)
+                if capture is None:
+                    capture = torch.cuda.Stream(dev)  # one capture stream for every timed choice
+                elapsed = {label: _graph_time([lambda w=w, b=b, fn=fn: fn(x, w, b) for w, b in weights], capture)
                            for label, fn in (("kernel", kernel), ("torch", reference))}
                 chosen = elapsed["kernel"] <= elapsed["torch"]
             self.projection_times[name] = elapsed if mode == "auto" else None
@@ -953,8 +980,7 @@ class BatchedDecodeEngine:
             d.set_lengths([p + 1 for p in positions])
         sampled = None
         if self.selector == "uniform":
-            sampled = self._heads_pages(uniform_pages([p + 1 for p in positions], st.config.page_size, dec.top,
-                                                      st.layers, self._sampler, self.device))
+            sampled = self._draw_pages([p + 1 for p in positions])
         compute = torch.cuda.current_stream(self.device)
         L = st.layers
 
@@ -1094,8 +1120,7 @@ class BatchedDecodeEngine:
         dec.set_lengths([positions[b] + 1 for b in slots])
         sampled = None
         if self.selector == "uniform":
-            sampled = self._heads_pages(uniform_pages([positions[b] + 1 for b in slots], st.config.page_size,
-                                                      dec.top, st.layers, self._sampler, self.device))
+            sampled = self._draw_pages([positions[b] + 1 for b in slots])
         compute = torch.cuda.current_stream(self.device)
         handle = _lib.stream_handle(self.device)
         if self._prepared is None:

@@ -509,6 +509,88 @@ __global__ __launch_bounds__(TT) void quest_topk_kernel(QuestArgs a) {
   }
 }
 
+// Uniform page resampling (the miss-heavy stress workload's selector): per
+// (layer, request) the tail page and top - 1 other pages drawn uniformly without
+// replacement by Floyd's algorithm -- for j = n - k .. n - 1, t uniform in
+// [0, j]; take t unless taken, else j -- over the count - 1 non-tail pages, with
+// a counter-based generator (splitmix64 of seed, step, layer, request, j), so the
+// draw depends on nothing but those.  Lane 0 draws into an LDS bitmap; the wave
+// then writes the pages in ascending order (tail last) to every head's row, and
+// -1 past min(top, count).  One wave per (layer, request).
+struct UniformArgs {
+  uint64_t seed, step;
+  int64_t count[QMAXB];  // of requests b0 .. b0 + gridDim.y - 1
+  int64_t b0, B, layers, top, heads;
+  int32_t* out;  // [layers, B, heads, top]
+};
+
+__host__ __device__ __forceinline__ uint64_t splitmix64(uint64_t x) {
+  x += 0x9e3779b97f4a7c15ull;
+  x = (x ^ (x >> 30)) * 0xbf58476d1ce4e5b9ull;
+  x = (x ^ (x >> 27)) * 0x94d049bb133111ebull;
+  return x ^ (x >> 31);
+}
+
+// Uniform in [0, bound) from a 64-bit draw: the high half of draw_hi32 * bound.
+__host__ __device__ __forceinline__ uint32_t uniform_below(uint64_t draw, uint32_t bound) {
+  return static_cast<uint32_t>(((draw >> 32) * static_cast<uint64_t>(bound)) >> 32);
+}
+
+constexpr int UNIFORM_MAX_PAGES = 1 << 16;
+
+__global__ __launch_bounds__(64) void uniform_pages_kernel(UniformArgs a) {
+  __shared__ uint32_t bits[UNIFORM_MAX_PAGES / 32];
+  const int64_t layer = blockIdx.x, b = a.b0 + blockIdx.y;
+  const int lane = threadIdx.x;
+  const int64_t count = a.count[blockIdx.y];
+  const int64_t n = count - 1;  // non-tail pages
+  const int64_t k = a.top - 1;  // of them drawn
+  const int64_t words = (count + 31) / 32;
+  for (int64_t w = lane; w < words; w += 64) bits[w] = 0u;
+  __syncthreads();
+  if (count <= a.top) {
+    for (int64_t w = lane; w < words; w += 64) {
+      const int64_t rest = count - 32 * w;
+      bits[w] = rest >= 32 ? 0xffffffffu : ((1u << rest) - 1u);
+    }
+  } else if (lane == 0) {
+    const uint64_t base = splitmix64(splitmix64(splitmix64(a.seed) ^ a.step) ^
+                                     static_cast<uint64_t>(layer * a.B + b));
+    for (int64_t j = n - k; j < n; ++j) {
+      const uint32_t t = uniform_below(splitmix64(base ^ static_cast<uint64_t>(j)), static_cast<uint32_t>(j + 1));
+      const bool taken = (bits[t >> 5] >> (t & 31)) & 1u;
+      const uint32_t pick = taken ? static_cast<uint32_t>(j) : t;
+      bits[pick >> 5] |= 1u << (pick & 31);
+    }
+    bits[n >> 5] |= 1u << (n & 31);  // the tail page
+  }
+  __syncthreads();
+  // ascending write: lane l owns words l, l + 64, ...; a running base per round
+  int32_t* row = a.out + (layer * a.B + b) * a.heads * a.top;
+  int64_t written = 0;
+  for (int64_t w0 = 0; w0 < words; w0 += 64) {
+    const int64_t w = w0 + lane;
+    uint32_t word = w < words ? bits[w] : 0u;
+    const int c = __popc(word);
+    int inc = c;  // inclusive prefix over the wave
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int o = __shfl_up(inc, off, 64);
+      if (lane >= off) inc += o;
+    }
+    int64_t at = written + inc - c;
+    while (word) {
+      const int bit = __ffs(word) - 1;
+      word &= word - 1;
+      for (int64_t h = 0; h < a.heads; ++h) row[h * a.top + at] = static_cast<int32_t>(32 * w + bit);
+      ++at;
+    }
+    written += __shfl(inc, 63, 64);
+  }
+  for (int64_t i = written + lane; i < a.top; i += 64)
+    for (int64_t h = 0; h < a.heads; ++h) row[h * a.top + i] = -1;
+}
+
 struct UnionArgs {
   const int32_t* pages;  // [B, Hq, top], first min(top, count) ascending
   int64_t p_sb, top;
@@ -1008,6 +1090,33 @@ extern "C" int hs_build_union(const int32_t* pages, int64_t p_stride_b, int64_t 
         entry_capacity, entry_counts + s0 * kv_heads, status,
         page_bits ? page_bits + s0 * page_bits_stride : nullptr, page_bits_stride, entry_stats, stream);
     if (rc != HS_OK) return rc;
+  }
+  return HS_OK;
+}
+
+extern "C" int hs_uniform_pages(uint64_t seed, uint64_t step, const int64_t* page_counts, int64_t batch,
+                                int64_t layers, int64_t top, int64_t heads, int32_t* out, hipStream_t stream) {
+  HS_CHECK_ARG(batch >= 1 && layers >= 1 && layers <= 65535 && heads >= 1 && top >= 1,
+               "invalid uniform pages shape");
+  HS_CHECK_ARG(page_counts && out, "null uniform pages pointer");
+  for (int64_t i = 0; i < batch; ++i)
+    HS_CHECK_ARG(page_counts[i] >= 1 && page_counts[i] <= UNIFORM_MAX_PAGES, "page counts must be 1 to %d",
+                 UNIFORM_MAX_PAGES);
+  for (int64_t b0 = 0; b0 < batch; b0 += QMAXB) {  // launches of at most 16 requests, in order
+    const int64_t nb = batch - b0 < QMAXB ? batch - b0 : QMAXB;
+    UniformArgs a{};
+    a.seed = seed;
+    a.step = step;
+    for (int64_t i = 0; i < nb; ++i) a.count[i] = page_counts[b0 + i];
+    a.b0 = b0;
+    a.B = batch;
+    a.layers = layers;
+    a.top = top;
+    a.heads = heads;
+    a.out = out;
+    hipLaunchKernelGGL(uniform_pages_kernel, dim3(static_cast<unsigned>(layers), static_cast<unsigned>(nb)),
+                       dim3(64), 0, stream, a);
+    HS_CHECK_LAUNCH("uniform pages");
   }
   return HS_OK;
 }

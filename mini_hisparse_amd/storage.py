@@ -41,6 +41,7 @@ import torch
 
 from .allocator import NO_GROUP, DeviceAllocator
 from .config import CacheConfig, CapacityError
+from .streams import independent_stream
 
 PageKey = tuple[str, int, int]
 
@@ -265,7 +266,7 @@ class HostStore:
         self.host = torch.empty(shape, dtype=config.dtype, pin_memory=self.cuda)
         self.host_source = ops.host_source(self.host)
         self.compute = torch.cuda.current_stream(self.device) if self.cuda else None
-        self.transfer = torch.cuda.Stream(device=self.device) if self.cuda else None
+        self.transfer = independent_stream(self.device) if self.cuda else None
         self.requests: dict[str, RequestPages] = {}
         self.pages = _PageMap(self)
         self.free_host = list(range(config.host_pages - 1, -1, -1))  # pop() yields 0, 1, 2, ...
