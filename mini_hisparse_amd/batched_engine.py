@@ -526,7 +526,7 @@ class BatchedDecodeEngine:
                  prefetch=None, request_groups=1, group_gather_workgroups=0, resolver_split=True,
                  fuse_rotary_append=True):
         """``selector``: "quest" (per-head Quest pages over the bounds) or "uniform"
-        (:func:`uniform_pages`, shared by every head, resampled each step).  ``graphs``:
+        (:func:`uniform_pages_device`, shared by every head, resampled each step).  ``graphs``:
         replay the dense part of each layer boundary as a HIP graph (when every per-layer
         projection runs on hs_skinny_gemm; captured after the first step): it cuts the host
         time of a boundary from ~80 to ~22 us, which pays only where the host, not the GPU,
