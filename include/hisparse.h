@@ -460,8 +460,11 @@ int hs_silu_mul(const void* gate_up, int64_t gu_stride, void* out, int64_t out_s
  * the PyTorch GEMMs of the decode step's projections (model.py:183-226) for
  * these skinny shapes.  k % 32 == 0, x rows 16-byte aligned (x_stride % 8 == 0),
  * W contiguous [n, k].  Tall-k shapes are split over k: the workspace
- * (hs_skinny_gemm_workspace_bytes) then holds fp32 partials that a second
- * launch sums in a fixed order, so results are deterministic.
+ * (hs_skinny_gemm_workspace_bytes, 8-byte aligned, any contents before a call)
+ * then holds the slices' partials, which the last workgroup of each row tile sums
+ * in slice order, so results are deterministic (one launch; calls sharing a
+ * workspace run in order on one stream, and a call captured in a graph may be
+ * replayed).
  */
 int64_t hs_skinny_gemm_workspace_bytes(int64_t rows, int64_t n, int64_t k);
 int hs_skinny_gemm(const void* x, int64_t x_stride, const void* weight, int64_t n, int64_t k, const void* bias,

@@ -13,14 +13,18 @@
 // weight fragments, GU token fragments) before the first MFMA.  The waves'
 // partial tiles are summed in LDS.  With one K slice the workgroup adds the
 // bias and writes y; with several (split-K, for tall-K shapes that would
-// otherwise give too few workgroups) it writes fp32 partials and
-// gemm_finalize_kernel sums them in slice order (deterministic), adds the
-// bias and rounds.  The argmax form (the LM head of a greedy step) keeps, per
+// otherwise give too few workgroups) it writes partials and
+// the last workgroup of each row tile to arrive sums them in slice order
+// (deterministic), adds the bias and rounds: tagged partial words and an arrival
+// counter per tile (arrive.h), so the launch needs no second kernel
+// (HS_GEMM_FUSED_MERGE=0: fp32 partials summed the same way by
+// gemm_finalize_kernel, a second launch).  The argmax form (the LM head of a greedy step) keeps, per
 // workgroup and token, only the best rounded logit and its index as one ordered
 // 64-bit key, and argmax_finalize_kernel takes the largest key per token.
 #include <math.h>
 #include <stdlib.h>
 
+#include "arrive.h"
 #include "hs_common.h"
 
 namespace hs {
@@ -50,6 +54,11 @@ struct GemmArgs {
   int64_t splits, slice_steps;
   int64_t F;  // SWIGLU: output features (N = 2 * 16 * ceil(F / 16) interleaved weight rows)
   unsigned long long* keys;  // ARGMAX: [M, gridDim.x] best key per token and workgroup
+  // split-K merged in-kernel (epoch != 0): tagged partial words [splits, M, N] and one
+  // arrival counter per row tile
+  unsigned long long* words;
+  unsigned long long* counters;
+  unsigned long long epoch;
 };
 
 // Ordered key of logit v at vocabulary index n: a larger key is a larger value, or
@@ -113,6 +122,11 @@ __global__ __launch_bounds__(GM_T) void skinny_gemm_kernel(GemmArgs a) {
     }
   }
   const unsigned short* xrow = a.x + (c < a.M ? c : a.M - 1) * a.x_stride + 8 * j;
+  // the tile's arrival counter, read with the first loads: its round tags the partials
+  const unsigned long long c0 = (a.splits > 1 && a.epoch != 0)
+                                    ? __hip_atomic_load(a.counters + blockIdx.x, __ATOMIC_RELAXED,
+                                                        __HIP_MEMORY_SCOPE_AGENT)
+                                    : 0ull;
   f32x4 acc[GM_TILES];
 #pragma unroll
   for (int t = 0; t < GM_TILES; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -177,6 +191,56 @@ __global__ __launch_bounds__(GM_T) void skinny_gemm_kernel(GemmArgs a) {
       for (int r = 0; r < GM_ROWS; ++r) key = best[r][m] > key ? best[r][m] : key;
       a.keys[static_cast<int64_t>(m) * gridDim.x + blockIdx.x] = key;
     }
+    return;
+  }
+  if (a.splits > 1 && a.epoch != 0) {
+    // this slice's partial words, then the arrival; the tile's last workgroup sums
+    // every slice's word in slice order (reading again a word whose tag has not
+    // landed yet), adds the bias, rounds, and leaves the counter to the next round
+    const uint32_t round = counter_round(c0, a.epoch);
+    const uint32_t tag = group_tag(a.epoch, round);
+    for (int idx = threadIdx.x; idx < GM_ROWS * 16; idx += GM_T) {
+      const int r = idx >> 4, m = idx & 15;
+      const int64_t n = n0 + r;
+      if (m >= a.M || n >= a.N) continue;
+      store_partial(a.words + (split * a.M + m) * a.N + n,
+                    red[0][r][m] + red[1][r][m] + red[2][r][m] + red[3][r][m], tag);
+    }
+    __shared__ int s_last;
+    __syncthreads();
+    if (threadIdx.x == 0) s_last = arrive_last(a.counters + blockIdx.x, a.epoch, a.splits) ? 1 : 0;
+    __syncthreads();
+    if (!s_last) return;
+    constexpr int MS = 8;  // slices whose words are loaded together
+    const int64_t sstride = a.M * a.N;
+    for (int idx = threadIdx.x; idx < GM_ROWS * 16; idx += GM_T) {
+      const int r = idx >> 4, m = idx & 15;
+      const int64_t n = n0 + r;
+      if (m >= a.M || n >= a.N) continue;
+      const unsigned long long* w0 = a.words + m * a.N + n;
+      float v = 0.f;
+      for (int64_t s0 = 0; s0 < a.splits; s0 += MS) {
+        unsigned long long w[MS];
+#pragma unroll
+        for (int u = 0; u < MS; ++u) {
+          const int64_t sl = s0 + u < a.splits ? s0 + u : s0;  // in bounds; not added
+          w[u] = __hip_atomic_load(w0 + sl * sstride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+#pragma unroll
+        for (int u = 0; u < MS; ++u) {
+          if (s0 + u >= a.splits) break;
+          if (static_cast<uint32_t>(w[u] >> 32) != tag) w[u] = partial_reread(w0 + (s0 + u) * sstride, tag);
+          v += partial_value(w[u]);
+        }
+      }
+      const float b = a.bias != nullptr ? load_elem<DT>(a.bias, n) : 0.f;
+      store_elem<DT>(a.out, m * a.out_stride + n, v + b);
+    }
+    if (threadIdx.x == 0)
+      __hip_atomic_store(a.counters + blockIdx.x,
+                         (static_cast<unsigned long long>(counter_id(a.epoch)) << 32) |
+                             (static_cast<unsigned long long>((round + 1) & 0xffffu) << 16),
+                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     return;
   }
   for (int idx = threadIdx.x; idx < GM_ROWS * 16; idx += GM_T) {
@@ -294,7 +358,9 @@ using namespace hs;
 extern "C" int64_t hs_skinny_gemm_workspace_bytes(int64_t rows, int64_t n, int64_t k) {
   if (rows < 1 || n < 1 || k < 32) return 256;
   const GemmPlan p = plan_gemm(n, k);
-  return p.splits > 1 ? p.splits * rows * n * 4 + 256 : 256;
+  // tagged 64-bit partial words and a counter per row tile (the fp32 partials of the
+  // two-launch form fit in the same bytes)
+  return p.splits > 1 ? p.splits * rows * n * 8 + p.blocks * 8 + 256 : 256;
 }
 
 static int run_gemm(const void* x, int64_t x_stride, const void* weight, int64_t n, int64_t k, const void* bias,
@@ -321,11 +387,20 @@ static int run_gemm(const void* x, int64_t x_stride, const void* weight, int64_t
   a.out_stride = out_stride;
   a.splits = p.splits;
   a.slice_steps = p.slice_steps;
+  // the split-K partials merged in-kernel unless HS_GEMM_FUSED_MERGE=0 (read per call)
+  const char* fused_env = getenv("HS_GEMM_FUSED_MERGE");
+  const bool fused = !(fused_env && atoi(fused_env) == 0);
   if (p.splits > 1) {
-    const int64_t need = p.splits * rows * n * 4;
-    HS_CHECK_ARG(workspace != nullptr && workspace_bytes >= need, "GEMM workspace too small: need %lld bytes",
-                 static_cast<long long>(need));
-    a.part = static_cast<float*>(workspace);
+    const int64_t need = fused ? p.splits * rows * n * 8 + p.blocks * 8 : p.splits * rows * n * 4;
+    HS_CHECK_ARG(workspace != nullptr && workspace_bytes >= need && (reinterpret_cast<uintptr_t>(workspace) & 7) == 0,
+                 "GEMM workspace too small or misaligned: need %lld bytes", static_cast<long long>(need));
+    if (fused) {
+      a.words = static_cast<unsigned long long*>(workspace);
+      a.counters = a.words + p.splits * rows * n;
+      a.epoch = next_epoch();
+    } else {
+      a.part = static_cast<float*>(workspace);
+    }
   }
   const dim3 grid(static_cast<unsigned>(p.blocks), static_cast<unsigned>(p.splits));
   if (dtype == HS_DTYPE_BF16) {
@@ -336,7 +411,7 @@ static int run_gemm(const void* x, int64_t x_stride, const void* weight, int64_t
     else launch_gemm<HS_DTYPE_F16, false>(p, grid, a, stream);
   }
   HS_CHECK_LAUNCH("skinny GEMM");
-  if (p.splits > 1) {
+  if (p.splits > 1 && !fused) {
     const unsigned blocks = static_cast<unsigned>(gemm_ceil(rows * n, GM_T));
     if (dtype == HS_DTYPE_BF16)
       hipLaunchKernelGGL((gemm_finalize_kernel<HS_DTYPE_BF16>), dim3(blocks), dim3(GM_T), 0, stream, a.part, p.splits,

@@ -261,3 +261,69 @@ def test_argmax_gemm_rejects_a_short_workspace(gpu):
     need = argmax_workspace_bytes(2, 100, 64)
     with pytest.raises(ValueError, match="workspace"):
         linear_argmax_tiled(x, tiles, 100, workspace=torch.empty(need - 300, dtype=torch.uint8, device=gpu))
+
+
+SPLIT_SHAPES = [(4, 1000, 4096), (4, 896, 4864), (8, 3584, 18944), (3, 64, 16384), (1, 5120, 27648), (16, 300, 8192)]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("rows,n,k", SPLIT_SHAPES)
+def test_in_kernel_split_merge_equals_the_finalize_launch(gpu, monkeypatch, rows, n, k):
+    """Split-K projections merged by each row tile's last workgroup (the default) have
+    the bits of the fp32 partials summed by gemm_finalize_kernel (HS_GEMM_FUSED_MERGE=0),
+    with and without a bias, from a workspace full of arbitrary bytes."""
+    from mini_hisparse_amd.dense import gemm_workspace_bytes, linear_tiled, tile_weight
+
+    gen = torch.Generator(device=gpu).manual_seed(rows + n + k)
+    x = torch.randn(rows, k, generator=gen, device=gpu).to(torch.bfloat16)
+    w = (torch.randn(n, k, generator=gen, device=gpu) / k**0.5).to(torch.bfloat16)
+    bias = torch.randn(n, generator=gen, device=gpu).to(torch.bfloat16)
+    tiles = tile_weight(w)
+    need = gemm_workspace_bytes(rows, n, k)
+    assert need > 256  # split over K
+    ws = torch.randint(0, 256, (need,), generator=gen, device=gpu, dtype=torch.uint8)
+    for b in (None, bias):
+        monkeypatch.setenv("HS_GEMM_FUSED_MERGE", "0")
+        expected = linear_tiled(x, tiles, n, b, workspace=torch.empty_like(ws))
+        monkeypatch.delenv("HS_GEMM_FUSED_MERGE")
+        got = linear_tiled(x, tiles, n, b, workspace=ws)
+        again = linear_tiled(x, tiles, n, b, workspace=ws)  # the counters as the first call left them
+        torch.cuda.synchronize()
+        assert torch.equal(got, expected) and torch.equal(again, expected)
+
+
+@pytest.mark.gpu
+def test_in_kernel_split_merge_replays_from_a_captured_graph(gpu):
+    """A captured split-K projection replayed four times with new rows, with eager
+    projections of other shapes sharing the workspace between the replays: every replay
+    equals the eager result (the counters count each replay in its own round)."""
+    from mini_hisparse_amd.dense import gemm_workspace_bytes, linear_tiled, tile_weight
+
+    gen = torch.Generator(device=gpu).manual_seed(3)
+    k, n, rows = 4864, 896, 4
+    w = (torch.randn(n, k, generator=gen, device=gpu) / 70).to(torch.bfloat16)
+    other = (torch.randn(1000, 4096, generator=gen, device=gpu) / 64).to(torch.bfloat16)
+    tiles, other_tiles = tile_weight(w), tile_weight(other)
+    ws = torch.zeros(max(gemm_workspace_bytes(rows, n, k), gemm_workspace_bytes(2, 1000, 4096)), dtype=torch.uint8,
+                     device=gpu)
+    x = torch.randn(rows, k, generator=gen, device=gpu).to(torch.bfloat16)
+    y = torch.empty(rows, n, dtype=torch.bfloat16, device=gpu)
+    stream = torch.cuda.Stream(gpu)
+    stream.wait_stream(torch.cuda.current_stream(gpu))
+    with torch.cuda.stream(stream):
+        linear_tiled(x, tiles, n, out=y, workspace=ws)
+    stream.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        linear_tiled(x, tiles, n, out=y, workspace=ws)
+    for replay in range(4):
+        print(f"[case] split-K graph replay {replay}", flush=True)
+        x.copy_(torch.randn(rows, k, generator=gen, device=gpu).to(torch.bfloat16))
+        graph.replay()
+        torch.cuda.synchronize()
+        got = y.clone()
+        expected = linear_tiled(x, tiles, n, workspace=torch.empty_like(ws))
+        linear_tiled(torch.randn(2, 4096, generator=gen, device=gpu).to(torch.bfloat16), other_tiles, 1000,
+                     workspace=ws)  # another launch's words and counters in the same bytes
+        torch.cuda.synchronize()
+        assert torch.equal(got, expected), replay
