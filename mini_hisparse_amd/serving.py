@@ -175,6 +175,8 @@ class LayerMajorEngine(Engine):
         slot = self.cache.slot_of[request.request_id]
         first = self.cache.state.prefill_slot(self.model, slot, request.prompt)
         self.batched.reset_slot(slot, len(request.prompt))
+        with torch.inference_mode():  # the token buffer is a step's output (an inference tensor)
+            self._tokens[slot] = first  # the slot's next input token, on the device
         request.prefill_count += 1
         token = int(first.item())
         self._record(request, token)
@@ -194,11 +196,13 @@ class LayerMajorEngine(Engine):
             return []
         turns = list(self.running)
         slots = [self.cache.slot_of[r.request_id] for r in turns]
-        index = torch.tensor(slots, dtype=torch.int64)
-        self._tokens[index.to(self._tokens.device)] = torch.tensor([r.generated[-1] for r in turns],
-                                                                   device=self._tokens.device)
+        # every running request's last token is already on the device: its prefill's in
+        # its slot (admission), or its slot of the previous step's output; the step's
+        # output is the next step's input, so no token crosses to the device per step
         out = self.batched.step(self._tokens, observer=observer, timer=timer, probe=probe, active=slots)
-        tokens = out.cpu()[index].tolist()
+        self._tokens = out
+        host = out.cpu().tolist()
+        tokens = [host[slot] for slot in slots]
         emitted = []
         for request, token in zip(turns, tokens):
             request.decode_count += 1
