@@ -111,6 +111,12 @@ def parse_args():
     p.add_argument("--synthetic-history", action="store_true",
                    help="model workloads: write synthetic K/V histories (N(0,1), 2%% of channels x8) directly "
                         "instead of prefilling random prompts through the model")
+    p.add_argument("--context", type=int, default=None,
+                   help="model workloads: prompt length (default: the workload's); the line then names it")
+    p.add_argument("--engine", choices=("layer-major", "per-request"), default="layer-major",
+                   help="model workloads: the layer-major engine (the default) or the reference-shaped "
+                        "per-request Engine over HybridKVCache (each request's layers decoded in turn); the "
+                        "latter prints its own line and no roofline")
     p.add_argument("--no-cpu-baseline", action="store_true", help="skip the CPU oracle leg")
     p.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU sample work")
     p.add_argument("--attention-sweep", action="store_true",
@@ -1157,6 +1163,8 @@ def run_model_workload(args, torch, device):
     configured = wl.batch
     if args.batch is not None:
         wl = replace(wl, batch=args.batch)
+    if args.context is not None:
+        wl = replace(wl, context=args.context)
     per_request = host_bytes_per_request(wl)
     fits = int(args.host_budget_gib * 2**30 // per_request)
     if fits < 1:
@@ -1298,7 +1306,8 @@ def run_model_workload(args, torch, device):
     pmc_path = PMC_SUMMARIES.get(args.workload, (None,))[0]
     profiled = PMC_CONFIG.get(args.workload)
     traffic = pmc_traffic(ROOFLINE_KERNELS, pmc_path) if pmc_path and profiled == (
-        wl.batch, len(engine.groups) if engine.groups else 1) else None
+        wl.batch, len(engine.groups) if engine.groups else 1) and wl.context == WORKLOADS[args.workload].context \
+        else None
     row_bytes = 2 * wl.kv_heads * D * e
     gather_bytes = misses * row_bytes
     link = host_link_gbs(torch, device)
@@ -1404,6 +1413,93 @@ def run_model_workload(args, torch, device):
     return result
 
 
+def run_per_request_engine(args, torch, device):
+    """The same model workload through the reference-shaped per-request stack:
+    ``Engine(model, HybridKVCache(...))`` (engine.py:36-146, hybrid.py), whose decode turn
+    runs one request's layers in turn (append, Quest selection, resolve, gather and
+    attention per (request, layer), each on the HIP library).  The batch's prompts are
+    admitted one per step; the timed steps are ``Engine.step()`` calls once every request
+    runs.  The slab, host pool, hot bound and hot rows are the layer-major leg's."""
+    from dataclasses import replace
+
+    from mini_hisparse_amd.batched_engine import WORKLOADS, policy_blocks, random_model, random_prompts
+    from mini_hisparse_amd.cli import union_rows_bound
+    from mini_hisparse_amd.config import CacheConfig
+    from mini_hisparse_amd.engine import Engine
+    from mini_hisparse_amd.hybrid import HotConfig, HybridKVCache
+
+    wl = WORKLOADS[args.workload]
+    if args.batch is not None:
+        wl = replace(wl, batch=args.batch)
+    if args.context is not None:
+        wl = replace(wl, context=args.context)
+    if wl.selector != "quest":
+        raise SystemExit("the per-request Engine selects with Quest or page means; this workload samples uniformly")
+    needed = wl.batch + args.warmup + args.steps
+    if needed > wl.steps:
+        raise SystemExit(f"the run needs {needed} decode steps per request, above the workload's {wl.steps}")
+    P = wl.page_size
+    model = random_model(wl, device, seed=args.seed)
+    config = CacheConfig(gpu_pages=policy_blocks(wl), host_pages=wl.batch * wl.layers * ceil((wl.context + wl.steps) / P),
+                         page_size=P, kv_heads=wl.kv_heads, head_dim=wl.head_dim, device=str(device), dtype=wl.dtype,
+                         index_budget_bytes=1 << 40)
+    hot = HotConfig(union_rows_bound(wl.context, wl.steps, wl.top_pages, wl.heads, P), wl.hot_rows)
+    cache = HybridKVCache(config, hot)
+    engine = Engine(model, cache, wl.top_pages, selector="quest")
+    prompts = random_prompts(wl, device, seed=args.seed).cpu()
+    for b in range(wl.batch):
+        engine.add_request(str(b), prompts[b].tolist(), wl.steps)
+    del prompts
+    print(f"[bench] {wl.name}: per-request Engine over HybridKVCache, admitting {wl.batch} requests",
+          file=sys.stderr, flush=True)
+    t0 = time.perf_counter()
+    admission = 0
+    while engine.waiting:
+        engine.step()
+        admission += 1
+        print(f"[bench] admission step {admission}: {time.perf_counter() - t0:.1f} s", file=sys.stderr, flush=True)
+    torch.cuda.synchronize()
+    prefill_s = time.perf_counter() - t0
+    for _ in range(args.warmup):
+        engine.step()
+    print("[bench] timing", file=sys.stderr, flush=True)
+    emitted = []
+    elapsed = _time_steps(torch, lambda: emitted.extend(engine.step()), args.steps)
+    if len(emitted) != wl.batch * args.steps:
+        raise SystemExit(f"expected {wl.batch * args.steps} tokens from the timed steps, got {len(emitted)}")
+    return {
+        "metric": METRIC,
+        "value": len(emitted) / elapsed,
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": elapsed * 1e3 / args.steps,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": (f"synthetic: random-init {wl.name} weights; {wl.context}-token uniformly random prompts "
+                 "prefilled through the model; greedy decode"),
+        "config": {
+            "workload": f"{wl.name} end to end through the per-request Engine over HybridKVCache (every "
+                        f"(request, layer) decoded in turn): {wl.layers} layers, batch {wl.batch}, "
+                        f"{wl.context}-token histories, Quest top-{wl.top_pages} pages, slab of "
+                        f"{config.gpu_pages} blocks, hot_rows {wl.hot_rows}",
+            "global_batch": wl.batch,
+            "seq_len": wl.context,
+            "parallelism": "none (1 GPU)",
+        },
+        "roofline": None,
+        "cpu_baseline": None,
+        "why_no_roofline": "a comparison leg: the layer-major line of the same workload carries the roofline "
+                           "and CPU baseline",
+        "admission_steps": admission,
+        "prefill_s": prefill_s,
+        "row_stats": [int(v) for v in cache.row_stats.tolist()],
+    }
+
+
 def main():
     args = parse_args()
     if args.summarize_trace:
@@ -1429,6 +1525,11 @@ def main():
     device = torch.device("cuda:0")
     if args.attention_sweep:
         attention_sweep(torch, device)
+        return
+    if args.engine == "per-request":
+        if args.workload in SHAPES:
+            raise SystemExit("--engine per-request runs a model workload")
+        print(json.dumps(run_per_request_engine(args, torch, device)))
         return
     if args.workload not in SHAPES:
         result = run_model_workload(args, torch, device)

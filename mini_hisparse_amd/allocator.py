@@ -98,6 +98,10 @@ class DeviceAllocator:
         self.fence = [None] * n
         self.on_reuse = [None] * n
         self._clock = 0
+        # bumped by every bind, release and unpin: a count of free or reclaimable blocks
+        # taken at one version holds until the version changes
+        self.version = 0
+        self.bound = 0  # blocks bound to a group
         # (request, layer) <-> group number
         self._group_of: dict[tuple, int] = {}
         self._group_key: list[tuple] = []
@@ -127,6 +131,8 @@ class DeviceAllocator:
     def bind(self, block, key):
         if self.owner_group[block] != NO_GROUP or block >= self.budget:
             raise AssertionError(f"block {block} is not free within the budget")
+        self.version += 1
+        self.bound += 1
         self.owner_group[block] = self.group_id(key[:2])
         self.owner_index[block] = key[2]
         self.generation[block] += 1
@@ -135,6 +141,8 @@ class DeviceAllocator:
     def release(self, block, fence):
         if self.owner_group[block] == NO_GROUP:
             raise AssertionError(f"block {block} is not bound")
+        self.version += 1
+        self.bound -= 1
         self.owner_group[block] = NO_GROUP
         self.bind_stamp[block] = -1
         self.reclaim_stamp[block] = -1
@@ -149,6 +157,7 @@ class DeviceAllocator:
         if self.owner_group[block] == NO_GROUP:
             raise AssertionError(f"block {block} is not bound")
         if self.reclaim_stamp[block] < 0:
+            self.version += 1
             self.reclaim_stamp[block] = self._stamp()
             self.on_reuse[block] = on_reuse
 
@@ -160,6 +169,20 @@ class DeviceAllocator:
 
     def validate(self, block, generation, owner):
         if self.owner_key(block) != owner or self.generation[block] != generation:
+            raise RuntimeError("stale device-slot generation (ABA)")
+
+    def snapshot(self, blocks):
+        """(blocks, generations, owner groups, owner indices) of ``blocks`` now: the
+        handles of a lease over many blocks, checked at once by ``validate_snapshot``."""
+        blocks = np.asarray(blocks, np.int64)
+        return blocks, self.generation[blocks].copy(), self.owner_group[blocks].copy(), self.owner_index[blocks].copy()
+
+    def validate_snapshot(self, snapshot):
+        """``validate`` of every block of a snapshot: same owner (or still free) and
+        same generation."""
+        blocks, generation, group, index = snapshot
+        same = (self.owner_group[blocks] == group) & ((group == NO_GROUP) | (self.owner_index[blocks] == index))
+        if not np.all(same & (self.generation[blocks] == generation)):
             raise RuntimeError("stale device-slot generation (ABA)")
 
     # -- queries for the policies -----------------------------------------------

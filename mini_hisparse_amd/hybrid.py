@@ -93,9 +93,8 @@ class RowLease:
     def __init__(self, cache, group, tables, plan, pinned):
         self.cache, self.tables, self.plan = cache, tables, plan
         self._lp, self._pinned = cache.storage.layer_pages(*group), pinned
-        table = cache.allocator
-        blocks = list(tables.blocks) + self._lp.slot[pinned].tolist()
-        self.handles = [(b, int(table.generation[b]), table.owner_key(b)) for b in blocks]
+        self.handles = cache.allocator.snapshot(np.concatenate([np.asarray(tables.blocks, np.int64),
+                                                                self._lp.slot[pinned]]))
         self.released = False
 
     @property
@@ -107,8 +106,7 @@ class RowLease:
         self.cache.storage.check_stream()
         if self.released:
             raise RuntimeError("row lease already released")
-        for handle in self.handles:
-            self.cache.allocator.validate(*handle)
+        self.cache.allocator.validate_snapshot(self.handles)
 
     def wait(self):
         self._validate()
@@ -138,9 +136,12 @@ class _PendingClean:
 
     def __init__(self, cache):
         self._cache = cache
+        self.layers = {}  # (request, layer) -> its page arrays, for layers that may hold flags
 
     def add(self, key):
-        self._cache.storage.layer_pages(*key[:2]).unpublished[key[2]] = True
+        lp = self._cache.storage.layer_pages(*key[:2])
+        lp.unpublished[key[2]] = True
+        self.layers[key[:2]] = lp
 
     def discard(self, key):
         if key in self._cache.storage.pages:
@@ -212,9 +213,14 @@ class HybridKVCache:
         """Reclaimable blocks inside the budget whose page is not pinned, in queue order."""
         table = self.allocator
         queue = table.reclaim_queue(self.budget)
-        keep = [b for b in queue.tolist()
-                if not self._lp(table.group_key(int(table.owner_group[b]))).pins[table.owner_index[b]]]
-        return keep
+        if not len(queue):
+            return []
+        groups, index = table.owner_group[queue], table.owner_index[queue]
+        pinned = np.zeros(len(queue), bool)
+        for g in np.unique(groups).tolist():
+            mine = groups == g
+            pinned[mine] = self._lp(table.group_key(g)).pins[index[mine]] != 0
+        return queue[~pinned].tolist()
 
     def _available_blocks(self):
         """Empty blocks (ascending) first, then readable unpinned blocks (queue order)."""
@@ -322,12 +328,22 @@ class HybridKVCache:
             return self._writing[1]
         return (self.storage.requests[group[0]].lengths[group[1]] - 1) // self.config.page_size
 
+    def _history_of(self, group):
+        """Page indices of one layer's sealed, unpinned resident pages at least two pages
+        behind its tail, in the order their blocks were bound (the layer's page-to-block
+        map holds exactly its bound page blocks, so no scan of the whole slab)."""
+        lp = self._lp(group)
+        idx = lp.resident()
+        idx = idx[lp.sealed[idx] & (lp.pins[idx] == 0) & (idx <= self._tail_of(group) - ACTIVE_TAIL_PAGES)]
+        return idx[np.argsort(self.allocator.bind_stamp[lp.slot[idx]], kind="stable")]
+
     def _history(self, group=None):
         """(group, index) of every sealed, unpinned resident page at least two pages
         behind its layer's tail, in the order their blocks were bound."""
+        if group is not None:
+            return [(group, i) for i in self._history_of(group).tolist()]
         table = self.allocator
-        gid = None if group is None else self._lp(group).gid
-        blocks = table.bound_pages(gid)
+        blocks = table.bound_pages()
         found = []
         groups = table.owner_group[blocks]
         for g in np.unique(groups).tolist():
@@ -350,15 +366,22 @@ class HybridKVCache:
         return lp.committed[index] == lp.version[index]
 
     def _publish_clean(self):
-        """Mark pages whose host mirror has completed as clean (never waits)."""
-        for request in self.storage.requests.values():
-            for lp in request.pages:
-                for i in np.flatnonzero(lp.unpublished).tolist():
-                    event = lp.host_ready[i]
-                    if event is None or event.query():
-                        lp.committed[i] = lp.enqueued[i]
-                        lp.unpublished[i] = False
-                        self.storage.stats["host_mirror_completions"] += 1
+        """Mark pages whose host mirror has completed as clean (never waits).  Only the
+        layers written since their last full publication are visited."""
+        layers = self.pending_clean.layers
+        for group, lp in list(layers.items()):
+            request = self.storage.requests.get(group[0])
+            if request is None or request.pages[group[1]] is not lp:
+                del layers[group]  # released: its flags went with it
+                continue
+            for i in np.flatnonzero(lp.unpublished).tolist():
+                event = lp.host_ready[i]
+                if event is None or event.query():
+                    lp.committed[i] = lp.enqueued[i]
+                    lp.unpublished[i] = False
+                    self.storage.stats["host_mirror_completions"] += 1
+            if not lp.unpublished.any():
+                del layers[group]
 
     def _unpin_clean_pages(self, group):
         """A layer with a hot region offers its clean history as reclaimable blocks,
@@ -366,11 +389,12 @@ class HybridKVCache:
         if not self.tables[group].blocks:
             return
         lp = self._lp(group)
-        for key, index in sorted(self._history(group), key=lambda e: -e[1]):
-            block = int(lp.slot[index])
-            if self._clean(group, index) and self.allocator.reclaim_stamp[block] < 0:
-                self.allocator.unpin(block, self._on_block_reused)
-                self.storage.stats["clean_page_unpins"] += 1
+        idx = np.sort(self._history_of(group))[::-1]
+        blocks = lp.slot[idx]
+        todo = (lp.committed[idx] == lp.version[idx]) & (self.allocator.reclaim_stamp[blocks] < 0)
+        for block in blocks[todo].tolist():
+            self.allocator.unpin(block, self._on_block_reused)
+            self.storage.stats["clean_page_unpins"] += 1
 
     def _require_hot(self, group, reason):
         tables = self.tables[group]
@@ -391,6 +415,9 @@ class HybridKVCache:
                   and request_id in (None, g[0]) and layer in (None, g[1])]
         for group in groups:
             self._unpin_clean_pages(group)
+        # pins and the budget hold still inside this loop, so the available count changes
+        # only with the allocator's version (a bind, release or unpin)
+        counted = None
         for group in groups:
             tables = self.tables[group]
             lp = self._lp(group)
@@ -398,7 +425,9 @@ class HybridKVCache:
             if not residents:
                 continue
             if not tables.hot_required:
-                if self._available_count() - int(upcoming_allocation) < self.transition_watermark:
+                if counted is None or counted[0] != self.allocator.version:
+                    counted = self.allocator.version, self._available_count()
+                if counted[1] - int(upcoming_allocation) < self.transition_watermark:
                     self._require_hot(group, "watermark")
                 elif residents >= self.hot_config.resident_window_pages:
                     self._require_hot(group, "window")

@@ -404,8 +404,7 @@ class HostStore:
         lp.location[i] = _CODE[location]
         lp.last_use[i] = None
         self.allocator.bind(slot, page.key)
-        bound = int(np.count_nonzero(self.allocator.owner_group != NO_GROUP))
-        self.stats["peak_device_pages"] = max(self.stats["peak_device_pages"], bound)
+        self.stats["peak_device_pages"] = max(self.stats["peak_device_pages"], self.allocator.bound)
 
     # -- writes ------------------------------------------------------------------------
     @torch.inference_mode()
@@ -612,6 +611,7 @@ class HostStore:
         table = self.allocator
         bound = np.flatnonzero(table.owner_group != NO_GROUP)
         assert not np.any(table.owner_group[self.budget :] != NO_GROUP)
+        assert table.bound == len(bound)
         retired = np.concatenate([s for _, _, s in self.retired]) if self.retired else np.zeros(0, np.int64)
         live = [lp.host_slot[: lp.materialized] for r in self.requests.values() for lp in r.pages]
         live = np.concatenate(live) if live else np.zeros(0, np.int64)

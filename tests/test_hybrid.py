@@ -155,6 +155,26 @@ def test_row_lease_excludes_writes_and_release_and_tails_stay(device):
         lease.wait()
 
 
+def test_row_lease_notices_a_block_rebound_under_it(device):
+    """A row lease holds its blocks' owners and generations: a block released and bound
+    again to the same owner (a new generation) fails the lease's next check."""
+    h = Harness.hybrid(device)
+    h.cache.reserve("a", 40, 1)
+    h.write("a", 32)
+    h.cache.transition_to_host("a", 0)
+    lease = h.cache.resolve("a", 0, LogicalTopK(torch.tensor([0, 4, 31], dtype=torch.int32, device=device)))
+    lease.wait()
+    table = h.cache.allocator
+    block = int(lease.handles[0][0])
+    owner = table.owner_key(block)
+    table.release(block, None)
+    with pytest.raises(RuntimeError, match="stale device-slot"):
+        lease.wait()
+    table.bind(block, owner)
+    with pytest.raises(RuntimeError, match="stale device-slot"):
+        lease.release()
+
+
 def test_invalid_or_padding_only_selection_reads_nothing(device):
     h = Harness.hybrid(device)
     h.cache.reserve("a", 40, 1)
