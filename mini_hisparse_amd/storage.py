@@ -434,7 +434,9 @@ class HostStore:
         lp = request.pages[layer]
         if np.any(lp.pins[: lp.materialized] > 0):
             raise RuntimeError("cannot append while this layer has active attention leases")
-        if self.pinned_count() >= self.budget:
+        # a pinned page holds a bound block, so fewer bound blocks than the budget
+        # means fewer pinned pages too (the count is a scan over every layer)
+        if self.allocator.bound >= self.budget and self.pinned_count() >= self.budget:
             raise CapacityError("no slot available for append")
         write = self._write = _Write(request, layer, k.contiguous(), v.contiguous(), 0, _PendingWrite(self))
         P = cfg.page_size
