@@ -405,10 +405,12 @@ def test_quest_scores_bit_exact(gpu, q_dtype, counts, kv, g, D):
 
 
 @pytest.mark.parametrize("pages,top,sink", [(2049, 32, True), (4096, 64, True), (300, 300 - 1, False), (65, 64, True),
-                                             (4097, 32, True), (2048, 1, True), (1000, 7, False)])
+                                             (4097, 32, True), (2048, 1, True), (1000, 7, False),
+                                             (16384, 64, True), (16385, 64, False), (3000, 65, True)])
 def test_quest_topk_with_many_ties_matches_oracle(gpu, pages, top, sink):
     """Bounds and queries of small integers, so that many pages score exactly alike: the
-    radix select's pages equal the oracle's, ties taken from the lowest page."""
+    radix select's pages equal the oracle's, ties taken from the lowest page (16384 pages
+    keep the keys in LDS; one more reads them from the scores)."""
     from mini_hisparse_amd.selection import quest_selection
 
     P, kv, g, D = 16, 2, 7, 64
